@@ -1,0 +1,167 @@
+/*
+ * vokra_hip.h — C ABI of the MI355X (gfx950) quantized-transformer hot path.
+ *
+ * A drop-in device arm for the reference's backend seams. Every entry point
+ * names the reference interface it replaces (paths relative to the
+ * ayutaz/vokra repository root). Plain pointers and sizes only.
+ *
+ * Error convention (crates/vokra-core/src/error.rs:21-104 mapped as in
+ * include/vokra.h:56-66): every fallible call returns a vokra_hip_status_t;
+ * the message of the last failure on the calling thread is available from
+ * vokra_hip_last_error(). A missing or failed device is
+ * VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, a shape mismatch
+ * VOKRA_HIP_ERROR_INVALID_ARGUMENT, an uncovered dtype
+ * VOKRA_HIP_ERROR_UNSUPPORTED_OP. Nothing ever falls back to the CPU.
+ *
+ * Buffers: the "copy mode" calls take host pointers and behave like the
+ * reference's per-op GPU methods (upload, launch, synchronize, read back;
+ * crates/vokra-backend-cuda/src/context.rs:1701-1768). The "_dev" calls take
+ * device pointers, enqueue on the context's stream and return without
+ * synchronizing; argument errors are still reported synchronously.
+ */
+#ifndef VOKRA_HIP_H
+#define VOKRA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum vokra_hip_status_t {
+    VOKRA_HIP_OK = 0,
+    VOKRA_HIP_ERROR_UNSUPPORTED_OP = 3,      /* VokraError::UnsupportedOp */
+    VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE = 4, /* VokraError::BackendUnavailable */
+    VOKRA_HIP_ERROR_INVALID_ARGUMENT = 5,    /* VokraError::InvalidArgument */
+    VOKRA_HIP_ERROR_OTHER = 9,
+    VOKRA_HIP_ERROR_KV_CACHE_EXHAUSTED = 10  /* VokraError::KvCacheExhausted */
+} vokra_hip_status_t;
+
+/* KvQuant in declaration order (crates/vokra-core/src/kv_quant/mod.rs:81-91). */
+typedef enum vokra_hip_kv_quant_t {
+    VOKRA_HIP_KV_FP32 = 0,
+    VOKRA_HIP_KV_Q4_0 = 1,
+    VOKRA_HIP_KV_Q5_0 = 2,
+    VOKRA_HIP_KV_Q8_0 = 3
+} vokra_hip_kv_quant_t;
+
+/* Weight dtypes of gemm_q_f32, numbered by ggml type tag. The reference's
+ * KQuantDtype (crates/vokra-backend-cpu/src/kernels/kquant.rs:56-63) covers
+ * the K-quants; the block formats are this arm's extension of the seam. */
+typedef enum vokra_hip_wdtype_t {
+    VOKRA_HIP_W_Q4_0 = 2,
+    VOKRA_HIP_W_Q5_0 = 6,
+    VOKRA_HIP_W_Q8_0 = 8,
+    VOKRA_HIP_W_Q4_K = 12
+} vokra_hip_wdtype_t;
+
+/* Activation quantization convention of the block-format INT8 GEMM.
+ * AMAX127: per 32-element block s = amax/127, q = clamp(round(v/s), +-127)
+ *          (the K-quant convention of kquant.rs:418-441 at group 32).
+ * POW2:    per 32-element block s = smallest power of two >= amax/127
+ *          (shared-exponent int8, as in the OCP MXINT8 format). */
+typedef enum vokra_hip_act_quant_t {
+    VOKRA_HIP_ACT_AMAX127 = 0,
+    VOKRA_HIP_ACT_POW2 = 1
+} vokra_hip_act_quant_t;
+
+typedef struct vokra_hip_ctx vokra_hip_ctx_t;
+typedef struct vokra_hip_qweight vokra_hip_qweight_t;
+typedef struct vokra_hip_event vokra_hip_event_t;
+
+/* ---- lifecycle ---------------------------------------------------------- */
+
+/* Number of visible HIP devices; BACKEND_UNAVAILABLE when the runtime has
+ * none. Replaces the CUDA device probe (crates/vokra-backend-cuda/src/probe.rs). */
+int vokra_hip_probe(int *n_devices);
+
+/* Context on one device with its own default-priority stream. Replaces
+ * CudaContext::new (crates/vokra-backend-cuda/src/context.rs:1167). */
+int vokra_hip_create(int device, vokra_hip_ctx_t **out);
+void vokra_hip_destroy(vokra_hip_ctx_t *ctx);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *vokra_hip_last_error(void);
+
+/* Blocks until the context stream drains; reports asynchronous faults. */
+int vokra_hip_synchronize(vokra_hip_ctx_t *ctx);
+
+/* ---- device memory and timing (resident mode plumbing) ------------------ */
+int vokra_hip_device_alloc(vokra_hip_ctx_t *ctx, size_t bytes, void **dptr);
+int vokra_hip_device_free(vokra_hip_ctx_t *ctx, void *dptr);
+int vokra_hip_memcpy_htod(vokra_hip_ctx_t *ctx, void *dst, const void *src, size_t bytes);
+int vokra_hip_memcpy_dtoh(vokra_hip_ctx_t *ctx, void *dst, const void *src, size_t bytes);
+int vokra_hip_event_create(vokra_hip_ctx_t *ctx, vokra_hip_event_t **ev);
+int vokra_hip_event_record(vokra_hip_ctx_t *ctx, vokra_hip_event_t *ev);
+int vokra_hip_event_elapsed_ms(vokra_hip_event_t *start, vokra_hip_event_t *stop, float *ms);
+void vokra_hip_event_destroy(vokra_hip_event_t *ev);
+
+/* ---- block dequantization and the fused dequant GEMV ---------------------- */
+
+/* Wire Q4_0/Q5_0/Q8_0 blocks -> f32, bit-exact. Replaces
+ * kv_quant::dequantize_bytes_into (crates/vokra-core/src/kv_quant/mod.rs:336-359). */
+int vokra_hip_dequantize_bytes(vokra_hip_ctx_t *ctx, int mode, const uint8_t *bytes, size_t n_bytes,
+                               float *out, size_t out_len);
+
+/* f32 -> wire Q4_0/Q5_0/Q8_0 blocks, bit-exact with the reference packers
+ * (BlockQ8_0::pack q8_0.rs:40-64, BlockQ4_0::pack q4_0.rs:44-68,
+ * BlockQ5_0::pack) as driven by pack_matrix_to_bytes
+ * (crates/vokra-core/src/kv_quant/dequant_gemm.rs:137-186): n must be a
+ * multiple of 32 and out_len must equal n/32 * block_bytes. */
+int vokra_hip_quantize_bytes(vokra_hip_ctx_t *ctx, int mode, const float *x, size_t n, uint8_t *out,
+                             size_t out_len);
+/* Same on device pointers (async on the context stream). */
+int vokra_hip_quantize_bytes_dev(vokra_hip_ctx_t *ctx, int mode, const float *d_x, size_t n, uint8_t *d_out);
+
+/* y[r] = sum_k dequant(row r)[k] * x[k], f32 semantics. Replaces
+ * KvQuantDequantGemvOps::fused_dequant_gemv (crates/vokra-core/src/kv_quant/gpu_ops.rs:70-80)
+ * as implemented by CudaContext::dequant_gemv_f32 (crates/vokra-backend-cuda/src/context.rs:1686-1768),
+ * validated exactly as validate_dequant_gemv (gpu_ops.rs:95-131). y has n_rows floats. */
+int vokra_hip_dequant_gemv_f32(vokra_hip_ctx_t *ctx, int mode, const uint8_t *blocks, size_t n_bytes,
+                               size_t n_rows, size_t n_blocks_per_row, const float *x, size_t x_len,
+                               float *y);
+
+/* ---- quantized-weight matmul ---------------------------------------------- */
+
+/* out[m, n] = sum_l a[m, l] * dequant(wq[n, l]) (+ bias[n]) through INT8
+ * activations. Replaces Compute::gemm_q_f32 (crates/vokra-models/src/compute.rs:943-963)
+ * -> kernels::gemm_q_f32 (crates/vokra-backend-cpu/src/kernels/mod.rs:341-364)
+ * -> gemm_driver::run_q (gemm_driver.rs:312-332): wq is the untransposed
+ * [n, k] payload, a is [m, k], out is [m, n], bias is added after. Block
+ * formats use the context's activation convention (default AMAX127). */
+int vokra_hip_gemm_q_f32(vokra_hip_ctx_t *ctx, int wdtype, size_t m, size_t n, size_t k, const float *a,
+                         size_t a_len, const uint8_t *wq, size_t wq_len, const float *bias, float *out,
+                         size_t out_len);
+
+/* Activation convention for the block-format INT8 path of this context. */
+int vokra_hip_set_act_quant(vokra_hip_ctx_t *ctx, int act_quant);
+
+/* Device-resident weight: uploads the [n, k] wire payload once and builds
+ * the device layouts the kernels stream (the reference keeps weights
+ * device-resident in its sessions, context.rs:5025). */
+int vokra_hip_qweight_upload(vokra_hip_ctx_t *ctx, int wdtype, size_t n, size_t k, const uint8_t *wq,
+                             size_t wq_len, vokra_hip_qweight_t **out);
+void vokra_hip_qweight_free(vokra_hip_qweight_t *w);
+
+/* gemm_q_f32 on device pointers against a resident weight (async on the
+ * context stream). d_a: [m, k] f32, d_bias: [n] or NULL, d_out: [m, n]. */
+int vokra_hip_gemm_q_f32_dev(vokra_hip_ctx_t *ctx, const vokra_hip_qweight_t *w, size_t m,
+                             const float *d_a, const float *d_bias, float *d_out, int act_quant);
+
+/* gemm_q_f32_dev split in its two launches, for callers that feed one
+ * activation matrix to several weights (the q/k/v projections of
+ * crates/vokra-models/src/whisper/nn.rs:185-197 read the same LN output):
+ * quantize once into a qact buffer, then run any number of GEMMs on it. */
+typedef struct vokra_hip_qact vokra_hip_qact_t;
+int vokra_hip_qact_create(vokra_hip_ctx_t *ctx, size_t max_m, size_t k, vokra_hip_qact_t **out);
+void vokra_hip_qact_free(vokra_hip_qact_t *qa);
+int vokra_hip_qact_quantize_dev(vokra_hip_ctx_t *ctx, vokra_hip_qact_t *qa, size_t m, const float *d_a,
+                                int act_quant);
+int vokra_hip_gemm_qact_dev(vokra_hip_ctx_t *ctx, const vokra_hip_qweight_t *w, const vokra_hip_qact_t *qa,
+                            const float *d_bias, float *d_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VOKRA_HIP_H */

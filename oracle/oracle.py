@@ -80,6 +80,9 @@ def _declare(L):
     L.vo_dequant_gemv_scalar.argtypes = [C.c_int, _u8p, _sz, _sz, _sz, _f32p, _sz, _f32p]
     L.vo_dense_gemv_f32.argtypes = [_f32p, _sz, _f32p, _sz, _f32p]
     L.vo_quantize_act_b32.argtypes = [_f32p, _sz, _i8p, _f32p, _i32p]
+    L.vo_quantize_act_b32_mode.argtypes = [_f32p, _sz, _i8p, _f32p, _i32p, C.c_int]
+    L.vo_gemm_qblock_i8_mode.argtypes = [C.c_int, _sz, _sz, _sz, _f32p, _u8p, _sz, _f32p, _f32p, C.c_int]
+    L.vo_qblock_block_dots_mode.argtypes = [C.c_int, _sz, _sz, _sz, _f32p, _u8p, _i32p, C.c_int]
     L.vo_gemm_qblock_i8.argtypes = [C.c_int, _sz, _sz, _sz, _f32p, _u8p, _sz, _f32p, _f32p]
     L.vo_qblock_block_dots.argtypes = [C.c_int, _sz, _sz, _sz, _f32p, _u8p, _i32p]
     L.vo_qblock_error_bound.restype = C.c_float
@@ -220,30 +223,32 @@ def dense_gemv_f32(a, n_rows, x):
 
 
 # ---- block INT8 --------------------------------------------------------
-def quantize_act_b32(x):
+def quantize_act_b32(x, pow2=False):
     xv = _f32(x)
     k = xv.size
     q = np.zeros(k, np.int8)
     s = np.zeros(k // 32, np.float32)
     g = np.zeros(k // 32, np.int32)
-    lib().vo_quantize_act_b32(_p(xv, _f32p), k, _p(q, _i8p), _p(s, _f32p), _p(g, _i32p))
+    lib().vo_quantize_act_b32_mode(_p(xv, _f32p), k, _p(q, _i8p), _p(s, _f32p), _p(g, _i32p),
+                                   int(pow2))
     return q, s, g
 
 
-def gemm_qblock_i8(wdtype, m, n, k, a, wq, bias=None):
+def gemm_qblock_i8(wdtype, m, n, k, a, wq, bias=None, pow2=False):
     av, wv = _f32(a), _u8(wq)
     bv = None if bias is None else _f32(bias)
     out = np.zeros(m * n, np.float32)
-    _check(lib().vo_gemm_qblock_i8(wdtype, m, n, k, _p(av, _f32p), _p(wv, _u8p), wv.size,
-                                   _p(bv, _f32p), _p(out, _f32p)), "gemm_qblock_i8")
+    _check(lib().vo_gemm_qblock_i8_mode(wdtype, m, n, k, _p(av, _f32p), _p(wv, _u8p), wv.size,
+                                        _p(bv, _f32p), _p(out, _f32p), int(pow2)),
+           "gemm_qblock_i8")
     return out.reshape(m, n)
 
 
-def qblock_block_dots(wdtype, m, n, k, a, wq):
+def qblock_block_dots(wdtype, m, n, k, a, wq, pow2=False):
     av, wv = _f32(a), _u8(wq)
     out = np.zeros(m * n * (k // 32), np.int32)
-    _check(lib().vo_qblock_block_dots(wdtype, m, n, k, _p(av, _f32p), _p(wv, _u8p),
-                                      _p(out, _i32p)), "qblock_block_dots")
+    _check(lib().vo_qblock_block_dots_mode(wdtype, m, n, k, _p(av, _f32p), _p(wv, _u8p),
+                                           _p(out, _i32p), int(pow2)), "qblock_block_dots")
     return out.reshape(m, n, k // 32)
 
 

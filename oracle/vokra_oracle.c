@@ -330,7 +330,9 @@ void vo_dense_gemv_f32(const float *a, size_t n_rows, const float *x, size_t x_l
  *                acc starting at +0.0; bias added after (gemm_driver.rs:326-330).
  * ====================================================================== */
 
-void vo_quantize_act_b32(const float *x, size_t k, int8_t *q, float *scale, int32_t *gsum) {
+/* pow2 != 0 selects the shared-exponent convention: s = the smallest power
+ * of two >= amax/127 (frexpf: amax/127 = f * 2^ex, f in [0.5, 1)). */
+void vo_quantize_act_b32_mode(const float *x, size_t k, int8_t *q, float *scale, int32_t *gsum, int pow2) {
     size_t nb = k / 32;
     for (size_t b = 0; b < nb; ++b) {
         const float *xs = x + b * 32;
@@ -343,6 +345,11 @@ void vo_quantize_act_b32(const float *x, size_t k, int8_t *q, float *scale, int3
             continue;
         }
         float s = amax / 127.0f;
+        if (pow2) {
+            int ex;
+            float f = frexpf(s, &ex);
+            s = ldexpf(1.0f, f == 0.5f ? ex - 1 : ex);
+        }
         for (int t = 0; t < 32; ++t) {
             float r = clampf_rs(roundf(xs[t] / s), -127.0f, 127.0f);
             int32_t ri = sat_i32(r);
@@ -352,6 +359,10 @@ void vo_quantize_act_b32(const float *x, size_t k, int8_t *q, float *scale, int3
         scale[b] = s;
         gsum[b] = g;
     }
+}
+
+void vo_quantize_act_b32(const float *x, size_t k, int8_t *q, float *scale, int32_t *gsum) {
+    vo_quantize_act_b32_mode(x, k, q, scale, gsum, 0);
 }
 
 static int wdtype_block_bytes(int wd) {
@@ -394,8 +405,8 @@ static int qblock_check(int wd, size_t m, size_t n, size_t k) {
     return VO_OK;
 }
 
-int vo_qblock_block_dots(int wd, size_t m, size_t n, size_t k, const float *a, const uint8_t *wq,
-                         int32_t *dots) {
+int vo_qblock_block_dots_mode(int wd, size_t m, size_t n, size_t k, const float *a, const uint8_t *wq,
+                              int32_t *dots, int pow2) {
     int st = qblock_check(wd, m, n, k);
     if (st) return st;
     size_t nb = k / 32, bb = (size_t)wdtype_block_bytes(wd);
@@ -405,7 +416,7 @@ int vo_qblock_block_dots(int wd, size_t m, size_t n, size_t k, const float *a, c
     int8_t qw[32];
     float dw;
     for (size_t i = 0; i < m; ++i) {
-        vo_quantize_act_b32(a + i * k, k, qa, sa, ga);
+        vo_quantize_act_b32_mode(a + i * k, k, qa, sa, ga, pow2);
         for (size_t j = 0; j < n; ++j)
             for (size_t b = 0; b < nb; ++b) {
                 vo_qblock_weight_ints(wd, wq + (j * nb + b) * bb, qw, &dw);
@@ -420,8 +431,13 @@ int vo_qblock_block_dots(int wd, size_t m, size_t n, size_t k, const float *a, c
     return VO_OK;
 }
 
-int vo_gemm_qblock_i8(int wd, size_t m, size_t n, size_t k, const float *a, const uint8_t *wq,
-                      size_t wq_len, const float *bias, float *out) {
+int vo_qblock_block_dots(int wd, size_t m, size_t n, size_t k, const float *a, const uint8_t *wq,
+                         int32_t *dots) {
+    return vo_qblock_block_dots_mode(wd, m, n, k, a, wq, dots, 0);
+}
+
+int vo_gemm_qblock_i8_mode(int wd, size_t m, size_t n, size_t k, const float *a, const uint8_t *wq,
+                           size_t wq_len, const float *bias, float *out, int pow2) {
     int st = qblock_check(wd, m, n, k);
     if (st) return st;
     size_t nb = k / 32, bb = (size_t)wdtype_block_bytes(wd);
@@ -440,7 +456,7 @@ int vo_gemm_qblock_i8(int wd, size_t m, size_t n, size_t k, const float *a, cons
         for (size_t b = 0; b < nb; ++b)
             vo_qblock_weight_ints(wd, wq + (j * nb + b) * bb, qw + j * k + b * 32, dw + j * nb + b);
     for (size_t i = 0; i < m; ++i) {
-        vo_quantize_act_b32(a + i * k, k, qa, sa, ga);
+        vo_quantize_act_b32_mode(a + i * k, k, qa, sa, ga, pow2);
         for (size_t j = 0; j < n; ++j) {
             const int8_t *wr = qw + j * k;
             float acc = 0.0f;
@@ -456,6 +472,11 @@ int vo_gemm_qblock_i8(int wd, size_t m, size_t n, size_t k, const float *a, cons
     }
     free(qw); free(dw); free(qa); free(sa); free(ga);
     return VO_OK;
+}
+
+int vo_gemm_qblock_i8(int wd, size_t m, size_t n, size_t k, const float *a, const uint8_t *wq,
+                      size_t wq_len, const float *bias, float *out) {
+    return vo_gemm_qblock_i8_mode(wd, m, n, k, a, wq, wq_len, bias, out, 0);
 }
 
 /* Activation-rounding bound for one output of the block INT8 GEMM, the

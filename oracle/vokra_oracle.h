@@ -63,6 +63,11 @@ void vo_dense_gemv_f32(const float *a, size_t n_rows, const float *x, size_t x_l
 
 /* ---- block-format INT8 GEMM (Q8_0 / Q4_0 / Q5_0 weights, gemm_q_f32) -- */
 void vo_quantize_act_b32(const float *x, size_t k, int8_t *q, float *scale, int32_t *gsum);
+void vo_quantize_act_b32_mode(const float *x, size_t k, int8_t *q, float *scale, int32_t *gsum, int pow2);
+int vo_gemm_qblock_i8_mode(int wdtype, size_t m, size_t n, size_t k, const float *a,
+                           const uint8_t *wq, size_t wq_len, const float *bias, float *out, int pow2);
+int vo_qblock_block_dots_mode(int wdtype, size_t m, size_t n, size_t k, const float *a,
+                              const uint8_t *wq, int32_t *dots, int pow2);
 int vo_qblock_weight_ints(int wdtype, const uint8_t *blk, int8_t *q32, float *d);
 int vo_gemm_qblock_i8(int wdtype, size_t m, size_t n, size_t k, const float *a,
                       const uint8_t *wq, size_t wq_len, const float *bias, float *out);

@@ -1,0 +1,602 @@
+// vk_capi.hip — C++ host layer behind include/vokra_hip.h.
+//
+// Mirrors the reference's device-context surface (CudaContext in
+// crates/vokra-backend-cuda/src/context.rs): a context owns one device and one
+// stream; per-op "copy mode" calls validate, upload, launch, synchronize and
+// read back; resident ("_dev") calls only enqueue. Validation follows the
+// reference's own rules and happens before any device work.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/vokra_hip.h"
+#include "vk_launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define VK_TRY(call, what)                                 \
+    do {                                                   \
+        hipError_t _e = (call);                            \
+        if (_e != hipSuccess) return hip_fail(_e, (what)); \
+    } while (0)
+
+size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+bool mul_ok(size_t a, size_t b, size_t* out) {
+    if (a != 0 && b > SIZE_MAX / a) return false;
+    *out = a * b;
+    return true;
+}
+
+int kv_block_bytes(int mode) {
+    switch (mode) {
+    case VOKRA_HIP_KV_Q4_0: return 18;
+    case VOKRA_HIP_KV_Q5_0: return 22;
+    case VOKRA_HIP_KV_Q8_0: return 34;
+    default: return 0;
+    }
+}
+
+// Block-format weight dtype -> KvQuant discriminant used by the kernels.
+int wd_kv_mode(int wd) {
+    switch (wd) {
+    case VOKRA_HIP_W_Q4_0: return VOKRA_HIP_KV_Q4_0;
+    case VOKRA_HIP_W_Q5_0: return VOKRA_HIP_KV_Q5_0;
+    case VOKRA_HIP_W_Q8_0: return VOKRA_HIP_KV_Q8_0;
+    default: return 0;
+    }
+}
+
+// A device buffer that only grows (hot calls reuse it without allocating).
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    hipError_t ensure(size_t bytes) {
+        if (bytes <= cap) return hipSuccess;
+        if (p) {
+            hipError_t e = hipFree(p);
+            if (e != hipSuccess) return e;
+            p = nullptr;
+            cap = 0;
+        }
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e == hipSuccess) cap = bytes;
+        return e;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+}  // namespace
+
+// Quantized activations in the MFMA A-fragment layout (rows padded to the
+// GEMM tile), their per-block scales and block sums.
+struct vokra_hip_qact {
+    vokra_hip_ctx* ctx = nullptr;
+    size_t max_m = 0, k = 0, m = 0, m_pad = 0;
+    bool growable = false;
+    int act_quant = VOKRA_HIP_ACT_AMAX127;
+    DevBuf frag, scale, gsum;
+};
+
+struct vokra_hip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int act_quant = VOKRA_HIP_ACT_AMAX127;
+    // Copy-mode staging and the context's own activation workspace.
+    DevBuf in0, in1, in2, out0;
+    vokra_hip_qact act;
+};
+
+struct vokra_hip_qweight {
+    vokra_hip_ctx* ctx = nullptr;
+    int wdtype = 0;
+    size_t n = 0, k = 0, n_pad = 0, nb = 0;
+    DevBuf frag, scale;
+};
+
+struct vokra_hip_event {
+    hipEvent_t ev = nullptr;
+};
+
+namespace {
+
+hipError_t set_dev(const vokra_hip_ctx* c) { return hipSetDevice(c->device); }
+
+int qact_reserve(vokra_hip_qact* qa, size_t m, size_t k) {
+    const size_t m_pad = round_up(m, vk::GEMM_TM);
+    const size_t nb = k / 32;
+    VK_TRY(qa->frag.ensure(m_pad * k * 2), "hipMalloc(activation fragments)");
+    VK_TRY(qa->scale.ensure(m_pad * nb * sizeof(float)), "hipMalloc(activation scales)");
+    VK_TRY(qa->gsum.ensure(m_pad * nb * sizeof(int)), "hipMalloc(activation sums)");
+    return VOKRA_HIP_OK;
+}
+
+// Quantize [m, k] device activations into qa (the INT8 activation pass).
+int quantize_activations(vokra_hip_ctx* c, vokra_hip_qact* qa, const float* d_a, size_t m, size_t k,
+                         int act_quant) {
+    if (qa->growable) {
+        int st = qact_reserve(qa, m, k);
+        if (st) return st;
+    }
+    const size_t m_pad = round_up(m, vk::GEMM_TM);
+    VK_TRY(vk::launch_quantize_act_b32(c->stream, act_quant == VOKRA_HIP_ACT_POW2, d_a, (int)m, (int)m_pad,
+                                       (int)k, (uint4*)qa->frag.p, (float*)qa->scale.p, (int*)qa->gsum.p),
+           "launch(vk_quantize_act_b32)");
+    qa->m = m;
+    qa->k = k;
+    qa->m_pad = m_pad;
+    qa->act_quant = act_quant;
+    return VOKRA_HIP_OK;
+}
+
+int check_block_shapes(int wdtype, size_t n, size_t k, size_t wq_len) {
+    const int mode = wd_kv_mode(wdtype);
+    if (mode == 0) {
+        if (wdtype == VOKRA_HIP_W_Q4_K)
+            return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "gemm_q_f32: Q4_K is not wired on this arm yet");
+        return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "gemm_q_f32: unsupported weight dtype %d", wdtype);
+    }
+    if (k == 0 || k % 32 != 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "gemm_q_f32 needs k to be a positive multiple of 32, got %zu", k);
+    size_t rb, want;
+    if (!mul_ok(n, k / 32, &rb) || !mul_ok(rb, (size_t)kv_block_bytes(mode), &want))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32: weight byte-length overflow");
+    if (wq_len != want)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "block weight payload is %zu bytes, want %zu (n=%zu rows x %zu blocks)", wq_len, want, n,
+                    k / 32);
+    if (n > (size_t)INT32_MAX || k > (size_t)INT32_MAX)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32: dimension exceeds int32");
+    return VOKRA_HIP_OK;
+}
+
+int upload_weight(vokra_hip_ctx* c, int wdtype, size_t n, size_t k, const uint8_t* d_wq, vokra_hip_qweight* w) {
+    w->ctx = c;
+    w->wdtype = wdtype;
+    w->n = n;
+    w->k = k;
+    w->nb = k / 32;
+    w->n_pad = round_up(n ? n : 1, vk::GEMM_TN);
+    VK_TRY(w->frag.ensure(w->n_pad * k * 2), "hipMalloc(weight fragments)");
+    VK_TRY(w->scale.ensure(w->n_pad * w->nb * sizeof(float)), "hipMalloc(weight scales)");
+    VK_TRY(vk::launch_repack_w_b32(c->stream, wd_kv_mode(wdtype), d_wq, (int)n, (int)w->n_pad, (int)w->nb,
+                                   (uint4*)w->frag.p, (float*)w->scale.p),
+           "launch(vk_repack_w_b32)");
+    return VOKRA_HIP_OK;
+}
+
+int run_gemm_qact(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_qact* qa, const float* d_bias,
+                 float* d_out) {
+    VK_TRY(vk::launch_gemm_qblock(c->stream, qa->act_quant == VOKRA_HIP_ACT_POW2, (const uint4*)qa->frag.p,
+                                  (const float*)qa->scale.p, (const uint4*)w->frag.p, (const float*)w->scale.p,
+                                  d_bias, d_out, (int)qa->m, (int)qa->m_pad, (int)w->n, (int)w->n_pad,
+                                  (int)w->nb),
+           "launch(vk_gemm_qblock)");
+    return VOKRA_HIP_OK;
+}
+
+int run_gemm(vokra_hip_ctx* c, const vokra_hip_qweight* w, size_t m, const float* d_a, const float* d_bias,
+             float* d_out, int act_quant) {
+    int st = quantize_activations(c, &c->act, d_a, m, w->k, act_quant);
+    if (st) return st;
+    return run_gemm_qact(c, w, &c->act, d_bias, d_out);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* vokra_hip_last_error(void) { return g_last_error.c_str(); }
+
+int vokra_hip_probe(int* n_devices) {
+    if (!n_devices) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "probe: n_devices is NULL");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    *n_devices = (e == hipSuccess) ? n : 0;
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (n == 0) return fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, "no HIP device visible");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_create(int device, vokra_hip_ctx_t** out) {
+    if (!out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "create: out is NULL");
+    *out = nullptr;
+    int n = 0;
+    int st = vokra_hip_probe(&n);
+    if (st) return st;
+    if (device < 0 || device >= n)
+        return fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, "device %d out of range (%d visible)", device, n);
+    hipDeviceProp_t prop;
+    VK_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, "device %d is %s; this library is built for gfx950",
+                    device, prop.gcnArchName);
+    VK_TRY(hipSetDevice(device), "hipSetDevice");
+    auto* c = new vokra_hip_ctx();
+    c->device = device;
+    c->act.ctx = c;
+    c->act.growable = true;
+    hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return hip_fail(e, "hipStreamCreate");
+    }
+    *out = c;
+    return VOKRA_HIP_OK;
+}
+
+void vokra_hip_destroy(vokra_hip_ctx_t* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    for (DevBuf* b : {&c->in0, &c->in1, &c->in2, &c->out0, &c->act.frag, &c->act.scale, &c->act.gsum})
+        b->release();
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+int vokra_hip_synchronize(vokra_hip_ctx_t* c) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "synchronize: ctx is NULL");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_device_alloc(vokra_hip_ctx_t* c, size_t bytes, void** dptr) {
+    if (!c || !dptr) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "device_alloc: NULL argument");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(hipMalloc(dptr, bytes ? bytes : 1), "hipMalloc");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_device_free(vokra_hip_ctx_t* c, void* dptr) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "device_free: ctx is NULL");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    VK_TRY(hipFree(dptr), "hipFree");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_memcpy_htod(vokra_hip_ctx_t* c, void* dst, const void* src, size_t bytes) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "memcpy_htod: ctx is NULL");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_memcpy_dtoh(vokra_hip_ctx_t* c, void* dst, const void* src, size_t bytes) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "memcpy_dtoh: ctx is NULL");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(D2H)");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_event_create(vokra_hip_ctx_t* c, vokra_hip_event_t** ev) {
+    if (!c || !ev) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "event_create: NULL argument");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    auto* e = new vokra_hip_event();
+    hipError_t r = hipEventCreate(&e->ev);
+    if (r != hipSuccess) {
+        delete e;
+        return hip_fail(r, "hipEventCreate");
+    }
+    *ev = e;
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_event_record(vokra_hip_ctx_t* c, vokra_hip_event_t* ev) {
+    if (!c || !ev) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "event_record: NULL argument");
+    VK_TRY(hipEventRecord(ev->ev, c->stream), "hipEventRecord");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_event_elapsed_ms(vokra_hip_event_t* a, vokra_hip_event_t* b, float* ms) {
+    if (!a || !b || !ms) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "event_elapsed: NULL argument");
+    VK_TRY(hipEventSynchronize(b->ev), "hipEventSynchronize");
+    VK_TRY(hipEventElapsedTime(ms, a->ev, b->ev), "hipEventElapsedTime");
+    return VOKRA_HIP_OK;
+}
+
+void vokra_hip_event_destroy(vokra_hip_event_t* ev) {
+    if (!ev) return;
+    (void)hipEventDestroy(ev->ev);
+    delete ev;
+}
+
+int vokra_hip_dequantize_bytes(vokra_hip_ctx_t* c, int mode, const uint8_t* bytes, size_t n_bytes, float* out,
+                               size_t out_len) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "dequantize_bytes: ctx is NULL");
+    const int bb = kv_block_bytes(mode);
+    if (bb == 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "kv_quant::dequantize_bytes: mode %d has no on-wire block layout", mode);
+    if (n_bytes % (size_t)bb != 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "kv_quant::dequantize_bytes: bytes.len()=%zu not a multiple of block_bytes=%d", n_bytes, bb);
+    const size_t nblk = n_bytes / (size_t)bb;
+    if (out_len != nblk * 32)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "dequantize_bytes_into: out.len()=%zu != n_blocks(%zu)*BLOCK_SIZE", out_len, nblk);
+    if (nblk == 0) return VOKRA_HIP_OK;
+    if (!bytes || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "dequantize_bytes: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(c->in0.ensure(n_bytes), "hipMalloc");
+    VK_TRY(c->out0.ensure(out_len * sizeof(float)), "hipMalloc");
+    VK_TRY(hipMemcpyAsync(c->in0.p, bytes, n_bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+    VK_TRY(vk::launch_dequantize_q0(c->stream, mode, (const uint8_t*)c->in0.p, nblk, (float*)c->out0.p),
+           "launch(vk_dequantize_q0)");
+    VK_TRY(hipMemcpyAsync(out, c->out0.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c->stream),
+           "hipMemcpyAsync(D2H)");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_dequant_gemv_f32(vokra_hip_ctx_t* c, int mode, const uint8_t* blocks, size_t n_bytes,
+                               size_t n_rows, size_t n_bpr, const float* x, size_t x_len, float* y) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "fused_dequant_gemv: ctx is NULL");
+    // validate_dequant_gemv (crates/vokra-core/src/kv_quant/gpu_ops.rs:95-131)
+    if (mode == VOKRA_HIP_KV_FP32)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "fused_dequant_gemv: mode=Fp32 has no on-wire block layout; use dense_gemv_f32 instead");
+    const int bb = kv_block_bytes(mode);
+    if (bb == 0) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "fused_dequant_gemv: unknown mode %d", mode);
+    size_t per_row = 0;
+    if (!mul_ok(n_bpr, 32, &per_row) || x_len != per_row)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "fused_dequant_gemv: x.len()=%zu != n_blocks_per_row(%zu)*32", x_len, n_bpr);
+    size_t rb, expected;
+    if (!mul_ok(n_rows, n_bpr, &rb) || !mul_ok(rb, (size_t)bb, &expected))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "fused_dequant_gemv: byte-length overflow");
+    if (n_bytes != expected)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "fused_dequant_gemv: blocks_bytes.len()=%zu != n_rows(%zu)*n_blocks_per_row(%zu)*block_bytes(%d) "
+                    "= %zu",
+                    n_bytes, n_rows, n_bpr, bb, expected);
+    if (n_rows == 0) return VOKRA_HIP_OK;  // the reference returns an empty Vec
+    if (n_bpr == 0) {
+        for (size_t i = 0; i < n_rows; ++i) y[i] = 0.0f;
+        return VOKRA_HIP_OK;
+    }
+    if (n_rows > (size_t)INT32_MAX || n_bpr > 4096)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "fused_dequant_gemv: n_rows must fit int32 and n_blocks_per_row <= 4096");
+    if (!blocks || !x || !y) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "fused_dequant_gemv: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(c->in0.ensure(n_bytes), "hipMalloc");
+    VK_TRY(c->in1.ensure(x_len * sizeof(float)), "hipMalloc");
+    VK_TRY(c->out0.ensure(n_rows * sizeof(float)), "hipMalloc");
+    VK_TRY(hipMemcpyAsync(c->in0.p, blocks, n_bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+    VK_TRY(hipMemcpyAsync(c->in1.p, x, x_len * sizeof(float), hipMemcpyHostToDevice, c->stream),
+           "hipMemcpyAsync(H2D)");
+    VK_TRY(vk::launch_dequant_gemv_f32(c->stream, mode, (const uint8_t*)c->in0.p, (int)n_rows, (int)n_bpr,
+                                       (const float*)c->in1.p, (float*)c->out0.p),
+           "launch(vk_dequant_gemv_f32)");
+    VK_TRY(hipMemcpyAsync(y, c->out0.p, n_rows * sizeof(float), hipMemcpyDeviceToHost, c->stream),
+           "hipMemcpyAsync(D2H)");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_set_act_quant(vokra_hip_ctx_t* c, int act_quant) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "set_act_quant: ctx is NULL");
+    if (act_quant != VOKRA_HIP_ACT_AMAX127 && act_quant != VOKRA_HIP_ACT_POW2)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "set_act_quant: unknown convention %d", act_quant);
+    c->act_quant = act_quant;
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_qweight_upload(vokra_hip_ctx_t* c, int wdtype, size_t n, size_t k, const uint8_t* wq, size_t wq_len,
+                             vokra_hip_qweight_t** out) {
+    if (!c || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qweight_upload: NULL argument");
+    *out = nullptr;
+    int st = check_block_shapes(wdtype, n, k, wq_len);
+    if (st) return st;
+    if (n == 0) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qweight_upload: n == 0");
+    if (!wq) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qweight_upload: NULL payload");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(c->in2.ensure(wq_len), "hipMalloc");
+    VK_TRY(hipMemcpyAsync(c->in2.p, wq, wq_len, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+    auto* w = new vokra_hip_qweight();
+    st = upload_weight(c, wdtype, n, k, (const uint8_t*)c->in2.p, w);
+    if (st == VOKRA_HIP_OK) {
+        hipError_t e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) st = hip_fail(e, "hipStreamSynchronize");
+    }
+    if (st) {
+        vokra_hip_qweight_free(w);
+        return st;
+    }
+    *out = w;
+    return VOKRA_HIP_OK;
+}
+
+void vokra_hip_qweight_free(vokra_hip_qweight_t* w) {
+    if (!w) return;
+    if (w->ctx) {
+        (void)hipSetDevice(w->ctx->device);
+        (void)hipStreamSynchronize(w->ctx->stream);
+    }
+    w->frag.release();
+    w->scale.release();
+    delete w;
+}
+
+int vokra_hip_gemm_q_f32_dev(vokra_hip_ctx_t* c, const vokra_hip_qweight_t* w, size_t m, const float* d_a,
+                             const float* d_bias, float* d_out, int act_quant) {
+    if (!c || !w) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: NULL context or weight");
+    if (w->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: weight belongs to another context");
+    if (m == 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "batched gemm_q_f32 needs at least one activation vector, got m = 0");
+    if (m > (size_t)INT32_MAX / 2) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: m too large");
+    if (act_quant != VOKRA_HIP_ACT_AMAX127 && act_quant != VOKRA_HIP_ACT_POW2)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: unknown activation convention %d", act_quant);
+    if (!d_a || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    return run_gemm(c, w, m, d_a, d_bias, d_out, act_quant);
+}
+
+int vokra_hip_gemm_q_f32(vokra_hip_ctx_t* c, int wdtype, size_t m, size_t n, size_t k, const float* a, size_t a_len,
+                         const uint8_t* wq, size_t wq_len, const float* bias, float* out, size_t out_len) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32: ctx is NULL");
+    // kernels::gemm_q_f32 argument checks (kernels/mod.rs:351-358)
+    size_t mk, mn;
+    if (!mul_ok(m, k, &mk) || a_len != mk)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q a: length %zu != m*k", a_len);
+    if (!mul_ok(m, n, &mn) || out_len != mn)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q out: length %zu != m*n", out_len);
+    int st = check_block_shapes(wdtype, n, k, wq_len);
+    if (st) return st;
+    if (m == 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "batched gemm_q_f32 needs at least one activation vector, got m = 0");
+    if (n == 0) return VOKRA_HIP_OK;
+    if (!a || !wq || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(c->in0.ensure(a_len * sizeof(float)), "hipMalloc");
+    VK_TRY(c->in1.ensure(bias ? n * sizeof(float) : 4), "hipMalloc");
+    VK_TRY(c->in2.ensure(wq_len), "hipMalloc");
+    VK_TRY(c->out0.ensure(out_len * sizeof(float)), "hipMalloc");
+    VK_TRY(hipMemcpyAsync(c->in0.p, a, a_len * sizeof(float), hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
+    VK_TRY(hipMemcpyAsync(c->in2.p, wq, wq_len, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
+    if (bias)
+        VK_TRY(hipMemcpyAsync(c->in1.p, bias, n * sizeof(float), hipMemcpyHostToDevice, c->stream),
+               "hipMemcpyAsync");
+    vokra_hip_qweight w;
+    st = upload_weight(c, wdtype, n, k, (const uint8_t*)c->in2.p, &w);
+    if (st == VOKRA_HIP_OK)
+        st = run_gemm(c, &w, m, (const float*)c->in0.p, bias ? (const float*)c->in1.p : nullptr, (float*)c->out0.p,
+                      c->act_quant);
+    if (st == VOKRA_HIP_OK) {
+        hipError_t e = hipMemcpyAsync(out, c->out0.p, out_len * sizeof(float), hipMemcpyDeviceToHost, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) st = hip_fail(e, "gemm_q_f32 readback");
+    } else {
+        (void)hipStreamSynchronize(c->stream);
+    }
+    w.frag.release();
+    w.scale.release();
+    return st;
+}
+
+int vokra_hip_quantize_bytes_dev(vokra_hip_ctx_t* c, int mode, const float* d_x, size_t n, uint8_t* d_out) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "quantize_bytes: ctx is NULL");
+    if (kv_block_bytes(mode) == 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "pack_matrix_to_bytes: mode %d has no packed layout", mode);
+    if (n % 32 != 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "kv_quant::pack_slice: input.len()=%zu not a multiple of 32", n);
+    if (n == 0) return VOKRA_HIP_OK;
+    if (!d_x || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "quantize_bytes: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_pack_q0(c->stream, mode, d_x, n / 32, d_out), "launch(vk_pack_q0)");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_quantize_bytes(vokra_hip_ctx_t* c, int mode, const float* x, size_t n, uint8_t* out, size_t out_len) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "quantize_bytes: ctx is NULL");
+    const int bb = kv_block_bytes(mode);
+    if (bb == 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "pack_matrix_to_bytes: mode %d has no packed layout", mode);
+    if (n % 32 != 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "kv_quant::pack_slice: input.len()=%zu not a multiple of 32", n);
+    if (out_len != n / 32 * (size_t)bb)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "quantize_bytes: out_len %zu != %zu blocks x %d bytes",
+                    out_len, n / 32, bb);
+    if (n == 0) return VOKRA_HIP_OK;
+    if (!x || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "quantize_bytes: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(c->in0.ensure(n * sizeof(float)), "hipMalloc");
+    VK_TRY(c->out0.ensure(out_len), "hipMalloc");
+    VK_TRY(hipMemcpyAsync(c->in0.p, x, n * sizeof(float), hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+    VK_TRY(vk::launch_pack_q0(c->stream, mode, (const float*)c->in0.p, n / 32, (uint8_t*)c->out0.p),
+           "launch(vk_pack_q0)");
+    VK_TRY(hipMemcpyAsync(out, c->out0.p, out_len, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(D2H)");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_qact_create(vokra_hip_ctx_t* c, size_t max_m, size_t k, vokra_hip_qact_t** out) {
+    if (!c || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qact_create: NULL argument");
+    *out = nullptr;
+    if (max_m == 0 || k == 0 || k % 32 != 0 || max_m > (size_t)INT32_MAX / 2 || k > (size_t)INT32_MAX)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "qact_create: need max_m > 0 and k a positive multiple of 32 (got %zu, %zu)", max_m, k);
+    VK_TRY(set_dev(c), "hipSetDevice");
+    auto* qa = new vokra_hip_qact();
+    qa->ctx = c;
+    qa->max_m = max_m;
+    qa->k = k;
+    int st = qact_reserve(qa, max_m, k);
+    if (st) {
+        vokra_hip_qact_free(qa);
+        return st;
+    }
+    *out = qa;
+    return VOKRA_HIP_OK;
+}
+
+void vokra_hip_qact_free(vokra_hip_qact_t* qa) {
+    if (!qa) return;
+    if (qa->ctx) {
+        (void)hipSetDevice(qa->ctx->device);
+        (void)hipStreamSynchronize(qa->ctx->stream);
+    }
+    qa->frag.release();
+    qa->scale.release();
+    qa->gsum.release();
+    delete qa;
+}
+
+int vokra_hip_qact_quantize_dev(vokra_hip_ctx_t* c, vokra_hip_qact_t* qa, size_t m, const float* d_a,
+                                int act_quant) {
+    if (!c || !qa || !d_a) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qact_quantize: NULL argument");
+    if (qa->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qact_quantize: qact belongs to another context");
+    if (m == 0 || m > qa->max_m)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qact_quantize: m=%zu outside 1..%zu", m, qa->max_m);
+    if (act_quant != VOKRA_HIP_ACT_AMAX127 && act_quant != VOKRA_HIP_ACT_POW2)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qact_quantize: unknown activation convention %d", act_quant);
+    VK_TRY(set_dev(c), "hipSetDevice");
+    return quantize_activations(c, qa, d_a, m, qa->k, act_quant);
+}
+
+int vokra_hip_gemm_qact_dev(vokra_hip_ctx_t* c, const vokra_hip_qweight_t* w, const vokra_hip_qact_t* qa,
+                            const float* d_bias, float* d_out) {
+    if (!c || !w || !qa || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: NULL argument");
+    if (w->ctx != c || qa->ctx != c)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: weight/activations belong to another context");
+    if (qa->m == 0) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: activations were never quantized");
+    if (qa->k != w->k)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: activation k=%zu != weight k=%zu", qa->k, w->k);
+    VK_TRY(set_dev(c), "hipSetDevice");
+    return run_gemm_qact(c, w, qa, d_bias, d_out);
+}
+
+}  // extern "C"

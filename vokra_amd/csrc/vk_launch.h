@@ -1,0 +1,23 @@
+// vk_launch.h — host launchers for the gfx950 kernels. Each launcher checks
+// nothing: the C-ABI layer validates shapes before calling it.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace vk {
+constexpr int GEMM_TM = 128;  // block GEMM workgroup tile (rows of A)
+constexpr int GEMM_TN = 128;  // block GEMM workgroup tile (rows of W)
+
+hipError_t launch_dequantize_q0(hipStream_t s, int mode, const uint8_t* bytes, size_t n_blocks, float* out);
+hipError_t launch_pack_q0(hipStream_t s, int mode, const float* x, size_t n_blocks, uint8_t* out);
+hipError_t launch_dequant_gemv_f32(hipStream_t s, int mode, const uint8_t* bytes, int n_rows, int n_bpr,
+                                   const float* x, float* y);
+hipError_t launch_quantize_act_b32(hipStream_t s, bool pow2, const float* a, int m, int m_pad, int k,
+                                   uint4* afrag, float* ascale, int* agsum);
+hipError_t launch_repack_w_b32(hipStream_t s, int mode, const uint8_t* wq, int n, int n_pad, int nb,
+                               uint4* wfrag, float* wscale);
+hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
+                              const uint4* wfrag, const float* wscale, const float* bias, float* out, int m,
+                              int m_pad, int n, int n_pad, int nb);
+}  // namespace vk

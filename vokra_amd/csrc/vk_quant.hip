@@ -1,0 +1,453 @@
+// vk_quant.hip — block-quant kernels for gfx950 (CDNA4).
+//
+//  * vk_dequantize_q0        : wire Q4_0/Q5_0/Q8_0 blocks -> f32 (bit-exact,
+//                              crates/vokra-core/src/kv_quant/mod.rs:307-359)
+//  * vk_dequant_gemv_f32     : KvQuantDequantGemvOps (f32 semantics,
+//                              crates/vokra-core/src/kv_quant/dequant_gemm.rs:49-98)
+//  * vk_quantize_act_b32     : per-32-block INT8 activation quantization into
+//                              the MFMA A-fragment layout
+//  * vk_repack_w_b32         : wire weight blocks -> exact bf16 integers in the
+//                              MFMA B-fragment layout + f32 block scales
+//  * vk_gemm_qblock          : INT8-semantics block GEMM on bf16 MFMA
+//
+// Fragment layout ("frag16"): a 16-row x 32-column (one quant block) tile is
+// stored as 64 lanes x 8 bf16, lane l holding row (l % 16), columns
+// 8*(l/16) .. 8*(l/16)+7. That is exactly the per-lane operand of
+// v_mfma_f32_16x16x32_bf16, so a wave loads a fragment with one coalesced
+// 16-byte-per-lane read. Tiles are ordered [row_tile][block][lane][8].
+#include "vk_common.h"
+
+namespace vk {
+
+// Block wire sizes of the KvQuant formats (kv_quant/mod.rs:101-110).
+__host__ __device__ constexpr int q0_block_bytes(int mode) {
+    return mode == 1 ? 18 : (mode == 2 ? 22 : (mode == 3 ? 34 : 0));
+}
+
+// Integer value of element i of a wire block (Q4_0 nib-8, Q5_0 v-16, Q8_0 q):
+// q4_0.rs:73-87, q5_0.rs unpack, q8_0.rs:69-80.
+__device__ __forceinline__ int q0_int(int mode, const uint8_t* blk, int i) {
+    if (mode == 3) return (int)(int8_t)blk[2 + i];
+    if (mode == 1) {
+        const uint8_t b = blk[2 + (i >> 1)];
+        return (int)((i & 1) ? (b >> 4) : (b & 0x0f)) - 8;
+    }
+    const uint8_t* qh = blk + 2;
+    const uint8_t b = blk[6 + (i >> 1)];
+    const uint32_t lo4 = (i & 1) ? (b >> 4) : (b & 0x0fu);
+    const uint32_t hi1 = (qh[i >> 3] >> (i & 7)) & 1u;
+    return (int)((hi1 << 4) | lo4) - 16;
+}
+
+__device__ __forceinline__ float q0_scale(const uint8_t* blk) {
+    return vk_f16_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+}
+
+// ---------------------------------------------------------------------------
+// Dequantize: 4 threads per block, 8 elements each, value = (float)q * d
+// (the reference multiplies the integer-valued f32 by the decoded scale).
+__global__ void vk_dequantize_q0(int mode, const uint8_t* __restrict__ bytes, size_t n_blocks,
+                                 float* __restrict__ out) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t blk = gid >> 2;
+    if (blk >= n_blocks) return;
+    const int c = (int)(gid & 3);
+    const int bb = q0_block_bytes(mode);
+    const uint8_t* p = bytes + blk * (size_t)bb;
+    const float d = q0_scale(p);
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (float)q0_int(mode, p, 8 * c + e) * d;
+    float4* o = reinterpret_cast<float4*>(out + blk * 32 + 8 * c);
+    o[0] = make_float4(v[0], v[1], v[2], v[3]);
+    o[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// ---------------------------------------------------------------------------
+// Pack f32 -> wire blocks, one 32-lane half-wave per block (lane i owns
+// element i). Same arithmetic as the reference packers: amax fold, d = amax/k
+// (k = 127, 7, 15), inv = 1/d, q = round(clamp(x*inv, lo, hi)), f16(d) stored
+// (q8_0.rs:40-64, q4_0.rs:44-68 + quantize_nibble :100-105, q5_0.rs pack).
+__device__ __forceinline__ int vk_sat_round(float c) {
+    // Rust `round() as i32` on an already clamped value: NaN -> 0.
+    return (c != c) ? 0 : (int)roundf(c);
+}
+
+__global__ void vk_pack_q0(int mode, const float* __restrict__ x, size_t n_blocks, uint8_t* __restrict__ out) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t blk = gid >> 5;
+    const int i = (int)(gid & 31);
+    const bool live = blk < n_blocks;
+    const float v = live ? x[blk * 32 + i] : 0.0f;
+    const float amax = vk_group_max<32>(fabsf(v));
+    if (!live) return;
+    const float div = mode == 3 ? 127.0f : (mode == 1 ? 7.0f : 15.0f);
+    const float d = amax == 0.0f ? 0.0f : amax / div;
+    const float inv = d == 0.0f ? 0.0f : 1.0f / d;
+    const float sc = v * inv;
+    uint8_t* p = out + blk * (size_t)q0_block_bytes(mode);
+    if (i == 0) {
+        const uint32_t h = vk_f32_to_f16_bits(d);
+        p[0] = (uint8_t)(h & 0xff);
+        p[1] = (uint8_t)(h >> 8);
+    }
+    // clamp-then-round; a NaN survives Rust's clamp and its cast gives 0
+    // (fminf/fmaxf would replace the NaN, so it is tested first).
+    if (mode == 3) {
+        p[2 + i] = (uint8_t)(int8_t)vk_sat_round(sc != sc ? sc : fminf(fmaxf(sc, -127.0f), 127.0f));
+        return;
+    }
+    int biased;
+    if (mode == 1) biased = min(max(vk_sat_round(sc != sc ? sc : fminf(fmaxf(sc, -8.0f), 7.0f)) + 8, 0), 15);
+    else biased = min(max(vk_sat_round(sc != sc ? sc : fminf(fmaxf(sc, -16.0f), 15.0f)) + 16, 0), 31);
+    // Gather the packed fields: nibble pairs (2i, 2i+1) share a byte.
+    const int lo4 = biased & 0x0f;
+    const int partner = __shfl_xor(lo4, 1, VK_WAVE);
+    if (mode == 1) {
+        if ((i & 1) == 0) p[2 + (i >> 1)] = (uint8_t)(lo4 | (partner << 4));
+        return;
+    }
+    if ((i & 1) == 0) p[6 + (i >> 1)] = (uint8_t)(lo4 | (partner << 4));
+    const unsigned long long hb = __ballot(((biased >> 4) & 1) != 0);
+    const uint32_t qh = (uint32_t)(hb >> (threadIdx.x & 32));
+    if (i < 4) p[2 + i] = (uint8_t)((qh >> (8 * i)) & 0xff);
+}
+
+// ---------------------------------------------------------------------------
+// f32-semantics dequant GEMV. Each work-item forms the partial dot of one
+// (row, block) pair in element order; one lane per row then sums the row's
+// block partials in block order. Rows per workgroup: floor(256 / n_bpr) (>= 1).
+__global__ void vk_dequant_gemv_f32(int mode, const uint8_t* __restrict__ bytes, int n_rows,
+                                    int n_bpr, int rows_per_wg, const float* __restrict__ x,
+                                    float* __restrict__ y) {
+    extern __shared__ float partial[];  // rows_per_wg * n_bpr
+    const int row0 = blockIdx.x * rows_per_wg;
+    const int rows_here = min(rows_per_wg, n_rows - row0);
+    const int items = rows_here * n_bpr;
+    const int bb = q0_block_bytes(mode);
+    for (int it = threadIdx.x; it < items; it += blockDim.x) {
+        const int r = it / n_bpr, b = it - r * n_bpr;
+        const uint8_t* p = bytes + ((size_t)(row0 + r) * n_bpr + b) * bb;
+        const float d = q0_scale(p);
+        const float* xb = x + (size_t)b * 32;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int i = 0; i < 32; ++i) acc = acc + ((float)q0_int(mode, p, i) * d) * xb[i];
+        partial[it] = acc;
+    }
+    __syncthreads();
+    for (int r = threadIdx.x; r < rows_here; r += blockDim.x) {
+        float acc = 0.0f;
+        for (int b = 0; b < n_bpr; ++b) acc = acc + partial[r * n_bpr + b];
+        y[row0 + r] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// INT8 activation quantization, 4 lanes per 32-element block (8 elements
+// each). Convention "amax127" (kquant.rs:418-441 at group 32): s = amax/127,
+// q = clamp(round(v / s), -127, 127); all-zero block -> s = 0, q = 0.
+// Convention "pow2": s = 2^e, the smallest power of two >= amax/127, so the
+// bf16 operand q * 2^e is exact and the MFMA folds the activation scale.
+// Output: A fragments (bf16 of q, or of q * 2^e for pow2), scales [tile][nb][16]
+// and block sums of q (same indexing). Rows >= m are written as zeros.
+template <bool POW2>
+__global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pad, int k,
+                                    uint4* __restrict__ afrag, float* __restrict__ ascale,
+                                    int* __restrict__ agsum) {
+    const int nb = k >> 5;
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)m_pad * nb * 4;
+    if (gid >= total) return;  // total is a multiple of 4: whole groups exit together
+    const int c = (int)(gid & 3);
+    const size_t rb = gid >> 2;  // row-block index
+    const int row = (int)(rb / nb), b = (int)(rb % nb);
+    float v[8];
+    if (row < m) {
+        const float4* src = reinterpret_cast<const float4*>(a + (size_t)row * k + b * 32 + 8 * c);
+        const float4 x0 = src[0], x1 = src[1];
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    amax = vk_group_max<4>(amax);
+    float s = 0.0f;
+    int q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (amax != 0.0f) {
+        s = amax / 127.0f;
+        if (POW2) {
+            int ex;
+            const float f = frexpf(s, &ex);  // s = f * 2^ex, f in [0.5, 1)
+            s = ldexpf(1.0f, f == 0.5f ? ex - 1 : ex);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            // Rust: (v / s).round().clamp(-127, 127) as i32 — a NaN survives
+            // the clamp and the saturating cast maps it to 0.
+            const float r = vk_round_half_away(v[e] / s);
+            q[e] = (r != r) ? 0 : (int)fminf(fmaxf(r, -127.0f), 127.0f);
+        }
+    }
+    int gs = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) gs += q[e];
+    gs = vk_group_sum_i<4>(gs);
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        uint32_t lo, hi;
+        if (POW2) {
+            lo = __float_as_uint((float)q[2 * e] * s) >> 16;
+            hi = __float_as_uint((float)q[2 * e + 1] * s) >> 16;
+        } else {
+            lo = vk_int_to_bf16_bits(q[2 * e]);
+            hi = vk_int_to_bf16_bits(q[2 * e + 1]);
+        }
+        w[e] = lo | (hi << 16);
+    }
+    const int mt = row >> 4, mr = row & 15;
+    const size_t frag = (size_t)mt * nb + b;
+    afrag[frag * 64 + (size_t)(mr + 16 * c)] = make_uint4(w[0], w[1], w[2], w[3]);
+    if (c == 0) {
+        ascale[frag * 16 + mr] = s;
+        agsum[frag * 16 + mr] = gs;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Weight repack (upload time): wire blocks [n][nb] -> bf16 integer fragments
+// [n_pad/16][nb][64][8] + f32 scales [n_pad/16][nb][16]. Rows >= n are zero.
+__global__ void vk_repack_w_b32(int mode, const uint8_t* __restrict__ wq, int n, int n_pad, int nb,
+                                uint4* __restrict__ wfrag, float* __restrict__ wscale) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)n_pad * nb * 4;
+    if (gid >= total) return;
+    const int c = (int)(gid & 3);
+    const size_t rb = gid >> 2;
+    const int row = (int)(rb / nb), b = (int)(rb % nb);
+    const int bb = q0_block_bytes(mode);
+    uint32_t w[4] = {0, 0, 0, 0};
+    float d = 0.0f;
+    if (row < n) {
+        const uint8_t* p = wq + ((size_t)row * nb + b) * bb;
+        d = q0_scale(p);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            w[e] = vk_int_to_bf16_bits(q0_int(mode, p, 8 * c + 2 * e)) |
+                   (vk_int_to_bf16_bits(q0_int(mode, p, 8 * c + 2 * e + 1)) << 16);
+        }
+    }
+    const int nt = row >> 4, nr = row & 15;
+    const size_t frag = (size_t)nt * nb + b;
+    wfrag[frag * 64 + (size_t)(nr + 16 * c)] = make_uint4(w[0], w[1], w[2], w[3]);
+    if (c == 0) wscale[frag * 16 + nr] = d;
+}
+
+// ---------------------------------------------------------------------------
+// Block GEMM, INT8 semantics on bf16 MFMA.
+//   out[m, n] = sum_b fmaf(sa[m,b] * dw[n,b], P_b[m,n], .)   (+ bias[n])
+// where P_b = v_mfma_f32_16x16x32_bf16 over one 32-element block of exact
+// integer-valued bf16 operands: every partial sum is an integer below 2^24,
+// so P_b equals the int32 block dot product exactly. With POW2 activations
+// the A operand already carries 2^e and the combine is fmaf(dw, P_b, .),
+// which is the same value (the power-of-two product sa * dw is exact).
+//
+// Workgroup tile 128 (m) x 128 (n), 4 waves in 2 x 2, wave tile 64 x 64 =
+// 4 x 4 MFMA tiles. One quant block per K step, double-buffered in LDS with
+// the next block's global loads in flight during the MFMAs.
+namespace gemm {
+constexpr int TM = 128, TN = 128;
+constexpr int FRAG_U4 = 64;  // uint4 per 16x32 fragment (1 KiB)
+}  // namespace gemm
+
+template <bool POW2>
+__global__ __launch_bounds__(256, 2) void vk_gemm_qblock(
+    const uint4* __restrict__ afrag, const float* __restrict__ ascale,
+    const uint4* __restrict__ wfrag, const float* __restrict__ wscale, const float* __restrict__ bias,
+    float* __restrict__ out, int m, int n, int nb, int ldo) {
+    using namespace gemm;
+    __shared__ uint4 lds_a[2][8 * FRAG_U4];
+    __shared__ uint4 lds_b[2][8 * FRAG_U4];
+    __shared__ float lds_sa[2][TM];
+    __shared__ float lds_dw[2][TN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int mt0 = blockIdx.y * (TM / 16), nt0 = blockIdx.x * (TN / 16);
+
+    // Global -> register staging: each thread moves 2 A + 2 B uint4 per block,
+    // threads 0..31 move the 128 A scales, threads 32..63 the 128 W scales.
+    uint4 ra[2], rb[2];
+    float4 rs;
+    auto gload = [&](int b) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int idx = tid + 256 * h;          // 0..511
+            const int t = idx >> 6, l = idx & 63;   // tile 0..7, lane
+            ra[h] = afrag[((size_t)(mt0 + t) * nb + b) * FRAG_U4 + l];
+            rb[h] = wfrag[((size_t)(nt0 + t) * nb + b) * FRAG_U4 + l];
+        }
+        if (tid < 32) {
+            const int t = tid >> 2, q = tid & 3;
+            rs = reinterpret_cast<const float4*>(ascale + ((size_t)(mt0 + t) * nb + b) * 16)[q];
+        } else if (tid < 64) {
+            const int t = (tid - 32) >> 2, q = tid & 3;
+            rs = reinterpret_cast<const float4*>(wscale + ((size_t)(nt0 + t) * nb + b) * 16)[q];
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            lds_a[buf][tid + 256 * h] = ra[h];
+            lds_b[buf][tid + 256 * h] = rb[h];
+        }
+        if (tid < 32) reinterpret_cast<float4*>(lds_sa[buf])[tid] = rs;
+        else if (tid < 64) reinterpret_cast<float4*>(lds_dw[buf])[tid - 32] = rs;
+    };
+
+    vk_f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = (vk_f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    const vk_f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < nb; ++b) {
+        const int buf = b & 1;
+        if (b + 1 < nb) gload(b + 1);
+        vk_bf16x8 af[4], bf[4];
+        float sa[4][4], dw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            af[i] = __builtin_bit_cast(vk_bf16x8, lds_a[buf][(wm * 4 + i) * FRAG_U4 + lane]);
+            const float4 s4 = reinterpret_cast<const float4*>(lds_sa[buf] + (wm * 4 + i) * 16)[lane >> 4];
+            sa[i][0] = s4.x; sa[i][1] = s4.y; sa[i][2] = s4.z; sa[i][3] = s4.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            bf[j] = __builtin_bit_cast(vk_bf16x8, lds_b[buf][(wn * 4 + j) * FRAG_U4 + lane]);
+            dw[j] = lds_dw[buf][(wn * 4 + j) * 16 + (lane & 15)];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const vk_f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (POW2) acc[i][j][r] = fmaf(dw[j], p[r], acc[i][j][r]);
+                    else acc[i][j][r] = fmaf(sa[i][r] * dw[j], p[r], acc[i][j][r]);
+                }
+            }
+        if (b + 1 < nb) {
+            lstore(buf ^ 1);
+        }
+        __syncthreads();
+    }
+
+    // D layout of v_mfma_f32_16x16x32_bf16: lane l holds rows 4*(l/16)+r of
+    // column l%16.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = (nt0 + wn * 4 + j) * 16 + (lane & 15);
+            if (col >= n) continue;
+            const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = (mt0 + wm * 4 + i) * 16 + 4 * (lane >> 4) + r;
+                if (row < m) out[(size_t)row * ldo + col] = bias ? acc[i][j][r] + bv : acc[i][j][r];
+            }
+        }
+}
+
+template __global__ void vk_quantize_act_b32<false>(const float*, int, int, int, uint4*, float*, int*);
+template __global__ void vk_quantize_act_b32<true>(const float*, int, int, int, uint4*, float*, int*);
+template __global__ void vk_gemm_qblock<false>(const uint4*, const float*, const uint4*, const float*,
+                                               const float*, float*, int, int, int, int);
+template __global__ void vk_gemm_qblock<true>(const uint4*, const float*, const uint4*, const float*,
+                                              const float*, float*, int, int, int, int);
+
+}  // namespace vk
+
+// ===========================================================================
+// Host-side launchers (called by the C-ABI layer in vk_capi.hip).
+// ===========================================================================
+#include "vk_launch.h"
+
+namespace vk {
+
+hipError_t launch_dequantize_q0(hipStream_t s, int mode, const uint8_t* bytes, size_t n_blocks,
+                                float* out) {
+    if (n_blocks == 0) return hipSuccess;
+    const size_t threads = n_blocks * 4;
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    hipLaunchKernelGGL(vk_dequantize_q0, dim3(grid), dim3(256), 0, s, mode, bytes, n_blocks, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_q0(hipStream_t s, int mode, const float* x, size_t n_blocks, uint8_t* out) {
+    if (n_blocks == 0) return hipSuccess;
+    const size_t threads = n_blocks * 32;
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    hipLaunchKernelGGL(vk_pack_q0, dim3(grid), dim3(256), 0, s, mode, x, n_blocks, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_gemv_f32(hipStream_t s, int mode, const uint8_t* bytes, int n_rows,
+                                   int n_bpr, const float* x, float* y) {
+    if (n_rows == 0) return hipSuccess;
+    const int rows_per_wg = n_bpr >= 256 ? 1 : 256 / n_bpr;
+    const unsigned grid = (unsigned)((n_rows + rows_per_wg - 1) / rows_per_wg);
+    const size_t lds = (size_t)rows_per_wg * n_bpr * sizeof(float);
+    hipLaunchKernelGGL(vk_dequant_gemv_f32, dim3(grid), dim3(256), lds, s, mode, bytes, n_rows, n_bpr,
+                       rows_per_wg, x, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_act_b32(hipStream_t s, bool pow2, const float* a, int m, int m_pad, int k,
+                                   uint4* afrag, float* ascale, int* agsum) {
+    const size_t threads = (size_t)m_pad * (k / 32) * 4;
+    if (threads == 0) return hipSuccess;
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    if (pow2)
+        hipLaunchKernelGGL(vk_quantize_act_b32<true>, dim3(grid), dim3(256), 0, s, a, m, m_pad, k, afrag,
+                           ascale, agsum);
+    else
+        hipLaunchKernelGGL(vk_quantize_act_b32<false>, dim3(grid), dim3(256), 0, s, a, m, m_pad, k, afrag,
+                           ascale, agsum);
+    return hipGetLastError();
+}
+
+hipError_t launch_repack_w_b32(hipStream_t s, int mode, const uint8_t* wq, int n, int n_pad, int nb,
+                               uint4* wfrag, float* wscale) {
+    const size_t threads = (size_t)n_pad * nb * 4;
+    if (threads == 0) return hipSuccess;
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    hipLaunchKernelGGL(vk_repack_w_b32, dim3(grid), dim3(256), 0, s, mode, wq, n, n_pad, nb, wfrag, wscale);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
+                              const uint4* wfrag, const float* wscale, const float* bias, float* out,
+                              int m, int m_pad, int n, int n_pad, int nb) {
+    const dim3 grid((unsigned)(n_pad / gemm::TN), (unsigned)(m_pad / gemm::TM));
+    if (pow2)
+        hipLaunchKernelGGL(vk_gemm_qblock<true>, grid, dim3(256), 0, s, afrag, ascale, wfrag, wscale, bias,
+                           out, m, n, nb, n);
+    else
+        hipLaunchKernelGGL(vk_gemm_qblock<false>, grid, dim3(256), 0, s, afrag, ascale, wfrag, wscale, bias,
+                           out, m, n, nb, n);
+    return hipGetLastError();
+}
+
+}  // namespace vk

@@ -1,0 +1,348 @@
+"""Python mirror of the reference's device-context surface over the C ABI.
+
+``HipContext`` follows ``CudaContext`` (crates/vokra-backend-cuda/src/context.rs):
+the same method names, argument meaning and error behaviour, so the parity
+tests read like the reference's ``parity_kernels_cuda.rs``. Errors map to the
+``VokraError`` variants (crates/vokra-core/src/error.rs:21-104). There is no
+CPU fallback anywhere: if the HIP library or a device is missing, calls raise
+``BackendUnavailable``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from enum import IntEnum
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libvokra_hip.so")
+
+
+class VokraError(RuntimeError):
+    code = 9
+
+
+class UnsupportedOp(VokraError):
+    code = 3
+
+
+class BackendUnavailable(VokraError):
+    code = 4
+
+
+class InvalidArgument(VokraError):
+    code = 5
+
+
+class KvCacheExhausted(VokraError):
+    code = 10
+
+
+_ERRORS = {3: UnsupportedOp, 4: BackendUnavailable, 5: InvalidArgument, 10: KvCacheExhausted}
+
+
+class KvQuant(IntEnum):
+    """crates/vokra-core/src/kv_quant/mod.rs:81-91 (declaration order)."""
+    Fp32 = 0
+    Q4_0 = 1
+    Q5_0 = 2
+    Q8_0 = 3
+
+    def block_bytes(self) -> int:
+        return {0: 128, 1: 18, 2: 22, 3: 34}[int(self)]
+
+
+class WDtype(IntEnum):
+    """Weight dtypes of gemm_q_f32 (ggml type tags)."""
+    Q4_0 = 2
+    Q5_0 = 6
+    Q8_0 = 8
+    Q4_K = 12
+
+
+class ActQuant(IntEnum):
+    AMAX127 = 0
+    POW2 = 1
+
+
+_lib = None
+
+
+def _declare(L):
+    P = C.c_void_p
+    sz = C.c_size_t
+    f32p = C.POINTER(C.c_float)
+    u8p = C.POINTER(C.c_uint8)
+    L.vokra_hip_last_error.restype = C.c_char_p
+    L.vokra_hip_probe.argtypes = [C.POINTER(C.c_int)]
+    L.vokra_hip_create.argtypes = [C.c_int, C.POINTER(P)]
+    L.vokra_hip_destroy.argtypes = [P]
+    L.vokra_hip_destroy.restype = None
+    L.vokra_hip_synchronize.argtypes = [P]
+    L.vokra_hip_device_alloc.argtypes = [P, sz, C.POINTER(P)]
+    L.vokra_hip_device_free.argtypes = [P, P]
+    L.vokra_hip_memcpy_htod.argtypes = [P, P, P, sz]
+    L.vokra_hip_memcpy_dtoh.argtypes = [P, P, P, sz]
+    L.vokra_hip_event_create.argtypes = [P, C.POINTER(P)]
+    L.vokra_hip_event_record.argtypes = [P, P]
+    L.vokra_hip_event_elapsed_ms.argtypes = [P, P, f32p]
+    L.vokra_hip_event_destroy.argtypes = [P]
+    L.vokra_hip_event_destroy.restype = None
+    L.vokra_hip_dequantize_bytes.argtypes = [P, C.c_int, u8p, sz, f32p, sz]
+    L.vokra_hip_dequant_gemv_f32.argtypes = [P, C.c_int, u8p, sz, sz, sz, f32p, sz, f32p]
+    L.vokra_hip_gemm_q_f32.argtypes = [P, C.c_int, sz, sz, sz, f32p, sz, u8p, sz, f32p, f32p, sz]
+    L.vokra_hip_set_act_quant.argtypes = [P, C.c_int]
+    L.vokra_hip_qweight_upload.argtypes = [P, C.c_int, sz, sz, u8p, sz, C.POINTER(P)]
+    L.vokra_hip_qweight_free.argtypes = [P]
+    L.vokra_hip_qweight_free.restype = None
+    L.vokra_hip_gemm_q_f32_dev.argtypes = [P, P, sz, P, P, P, C.c_int]
+    L.vokra_hip_quantize_bytes.argtypes = [P, C.c_int, f32p, sz, u8p, sz]
+    L.vokra_hip_quantize_bytes_dev.argtypes = [P, C.c_int, P, sz, P]
+    L.vokra_hip_qact_create.argtypes = [P, sz, sz, C.POINTER(P)]
+    L.vokra_hip_qact_free.argtypes = [P]
+    L.vokra_hip_qact_free.restype = None
+    L.vokra_hip_qact_quantize_dev.argtypes = [P, P, sz, P, C.c_int]
+    L.vokra_hip_gemm_qact_dev.argtypes = [P, P, P, P, P]
+
+
+def lib():
+    """Loads libvokra_hip.so; raises BackendUnavailable if it was never built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise BackendUnavailable(
+                f"{LIB_PATH} is missing: build it with `python -m vokra_amd.build` "
+                "(there is no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        _declare(L)
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    """Names the C ABI exports (for the symbol test on machines without a GPU)."""
+    return [n for n in dir(lib()) if n.startswith("vokra_hip_")]
+
+
+def _check(code: int):
+    if code != 0:
+        msg = lib().vokra_hip_last_error().decode(errors="replace")
+        raise _ERRORS.get(code, VokraError)(msg)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _u8(a):
+    return np.ascontiguousarray(np.frombuffer(a, np.uint8) if isinstance(a, (bytes, bytearray)) else a,
+                                dtype=np.uint8)
+
+
+def _ptr(a, t):
+    return None if a is None else a.ctypes.data_as(C.POINTER(t))
+
+
+def probe() -> int:
+    n = C.c_int(0)
+    _check(lib().vokra_hip_probe(C.byref(n)))
+    return n.value
+
+
+class DeviceBuffer:
+    """A device allocation owned by a context (resident-mode plumbing)."""
+
+    def __init__(self, ctx: "HipContext", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        _check(lib().vokra_hip_device_alloc(ctx._h, self.nbytes, C.byref(p)))
+        self.ptr = p
+
+    @classmethod
+    def from_array(cls, ctx, arr):
+        arr = np.ascontiguousarray(arr)
+        buf = cls(ctx, arr.nbytes)
+        buf.upload(arr)
+        return buf
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        _check(lib().vokra_hip_memcpy_htod(self.ctx._h, self.ptr, arr.ctypes.data_as(C.c_void_p), arr.nbytes))
+
+    def download(self, dtype, count):
+        out = np.empty(count, dtype)
+        assert out.nbytes <= self.nbytes
+        _check(lib().vokra_hip_memcpy_dtoh(self.ctx._h, out.ctypes.data_as(C.c_void_p), self.ptr, out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            _check(lib().vokra_hip_device_free(self.ctx._h, self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if getattr(self, "ptr", None) and self.ctx._h:
+                lib().vokra_hip_device_free(self.ctx._h, self.ptr)
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self, ctx: "HipContext"):
+        self.ctx = ctx
+        p = C.c_void_p()
+        _check(lib().vokra_hip_event_create(ctx._h, C.byref(p)))
+        self._h = p
+
+    def record(self):
+        _check(lib().vokra_hip_event_record(self.ctx._h, self._h))
+
+    def elapsed_ms(self, stop: "Event") -> float:
+        ms = C.c_float(0.0)
+        _check(lib().vokra_hip_event_elapsed_ms(self._h, stop._h, C.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None):
+                lib().vokra_hip_event_destroy(self._h)
+        except Exception:
+            pass
+
+
+class QWeight:
+    """Device-resident quantized weight ([n, k] wire payload uploaded once)."""
+
+    def __init__(self, ctx: "HipContext", wdtype: WDtype, n: int, k: int, wq):
+        self.ctx, self.wdtype, self.n, self.k = ctx, WDtype(wdtype), int(n), int(k)
+        w = _u8(wq)
+        p = C.c_void_p()
+        _check(lib().vokra_hip_qweight_upload(ctx._h, int(wdtype), n, k, _ptr(w, C.c_uint8), w.size,
+                                              C.byref(p)))
+        self._h = p
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None):
+                lib().vokra_hip_qweight_free(self._h)
+        except Exception:
+            pass
+
+
+class QAct:
+    """Device-resident INT8-quantized activations (quantize once, many GEMMs)."""
+
+    def __init__(self, ctx: "HipContext", max_m: int, k: int):
+        self.ctx, self.max_m, self.k = ctx, int(max_m), int(k)
+        p = C.c_void_p()
+        _check(lib().vokra_hip_qact_create(ctx._h, max_m, k, C.byref(p)))
+        self._h = p
+
+    def quantize(self, m: int, d_a: "DeviceBuffer", act: "ActQuant" = None):
+        act = ActQuant.AMAX127 if act is None else act
+        _check(lib().vokra_hip_qact_quantize_dev(self.ctx._h, self._h, m, d_a.ptr, int(act)))
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None):
+                lib().vokra_hip_qact_free(self._h)
+        except Exception:
+            pass
+
+
+class HipContext:
+    """One gfx950 device + stream (mirror of CudaContext::new, context.rs:1167)."""
+
+    def __init__(self, device: int = 0):
+        p = C.c_void_p()
+        _check(lib().vokra_hip_create(device, C.byref(p)))
+        self._h = p
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().vokra_hip_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synchronize(self):
+        _check(lib().vokra_hip_synchronize(self._h))
+
+    # ---- kv_quant surface ------------------------------------------------
+    def dequantize_bytes(self, mode: KvQuant, data) -> np.ndarray:
+        """kv_quant::dequantize_bytes (kv_quant/mod.rs:307-319) on the device."""
+        b = _u8(data)
+        bb = KvQuant(mode).block_bytes() if int(mode) in (0, 1, 2, 3) else 1
+        n_out = (b.size // bb) * 32 if bb else 0
+        out = np.zeros(max(n_out, 1), np.float32)
+        _check(lib().vokra_hip_dequantize_bytes(self._h, int(mode), _ptr(b, C.c_uint8), b.size,
+                                                _ptr(out, C.c_float), n_out))
+        return out[:n_out]
+
+    def quantize_bytes(self, mode: KvQuant, x) -> np.ndarray:
+        """pack_matrix_to_bytes (dequant_gemm.rs:137-186) on the device: f32 -> wire blocks."""
+        xv = _f32(x).reshape(-1)
+        bb = KvQuant(mode).block_bytes() if int(mode) in (1, 2, 3) else 0
+        n_out = xv.size // 32 * bb
+        out = np.zeros(max(n_out, 1), np.uint8)
+        _check(lib().vokra_hip_quantize_bytes(self._h, int(mode), _ptr(xv, C.c_float), xv.size,
+                                              _ptr(out, C.c_uint8), n_out))
+        return out[:n_out]
+
+    def quantize_bytes_dev(self, mode: KvQuant, d_x: "DeviceBuffer", n: int, d_out: "DeviceBuffer"):
+        _check(lib().vokra_hip_quantize_bytes_dev(self._h, int(mode), d_x.ptr, n, d_out.ptr))
+
+    def dequant_gemv_f32(self, mode: KvQuant, blocks_bytes, n_rows: int, n_blocks_per_row: int, x):
+        """CudaContext::dequant_gemv_f32 (context.rs:1686-1699)."""
+        b, xv = _u8(blocks_bytes), _f32(x)
+        y = np.zeros(max(n_rows, 1), np.float32)
+        _check(lib().vokra_hip_dequant_gemv_f32(self._h, int(mode), _ptr(b, C.c_uint8), b.size, n_rows,
+                                                n_blocks_per_row, _ptr(xv, C.c_float), xv.size,
+                                                _ptr(y, C.c_float)))
+        return y[:n_rows]
+
+    def fused_dequant_gemv(self, mode, blocks_bytes, n_rows, n_blocks_per_row, x):
+        """KvQuantDequantGemvOps::fused_dequant_gemv (kv_quant/gpu_ops.rs:70-80)."""
+        return self.dequant_gemv_f32(mode, blocks_bytes, n_rows, n_blocks_per_row, x)
+
+    # ---- quantized linear -------------------------------------------------
+    def set_act_quant(self, act: ActQuant):
+        _check(lib().vokra_hip_set_act_quant(self._h, int(act)))
+
+    def gemm_q_f32(self, m: int, n: int, k: int, a, wq, dtype: WDtype, bias=None, out=None):
+        """Compute::gemm_q_f32 (compute.rs:943-963): out[m, n] = a[m, k] . dequant(wq[n, k])^T."""
+        av, w = _f32(a), _u8(wq)
+        bv = None if bias is None else _f32(bias)
+        o = np.zeros(max(m * n, 1), np.float32)
+        _check(lib().vokra_hip_gemm_q_f32(self._h, int(dtype), m, n, k, _ptr(av, C.c_float), av.size,
+                                          _ptr(w, C.c_uint8), w.size, _ptr(bv, C.c_float),
+                                          _ptr(o, C.c_float), m * n))
+        res = o[: m * n].reshape(m, n)
+        if out is not None:
+            out[...] = res
+            return out
+        return res
+
+    def upload_qweight(self, wdtype, n, k, wq) -> QWeight:
+        return QWeight(self, wdtype, n, k, wq)
+
+    def gemm_q_f32_dev(self, w: QWeight, m: int, d_a: DeviceBuffer, d_out: DeviceBuffer, d_bias=None,
+                       act: ActQuant = ActQuant.AMAX127):
+        """Enqueue gemm_q_f32 on device buffers against a resident weight."""
+        _check(lib().vokra_hip_gemm_q_f32_dev(self._h, w._h, m, d_a.ptr,
+                                              None if d_bias is None else d_bias.ptr, d_out.ptr, int(act)))
+
+    def qact(self, max_m: int, k: int) -> QAct:
+        return QAct(self, max_m, k)
+
+    def gemm_qact_dev(self, w: QWeight, qa: QAct, d_out: DeviceBuffer, d_bias=None):
+        _check(lib().vokra_hip_gemm_qact_dev(self._h, w._h, qa._h, None if d_bias is None else d_bias.ptr,
+                                             d_out.ptr))
