@@ -72,6 +72,21 @@ def bench_q8_gemm(ctx, hip, steps, warmup, act):
             "a": a, "wq": wq}
 
 
+def bench_copy(ctx, hip, nbytes=1 << 30, reps=5):
+    """Plain streaming copy of 1 GiB (4x the 256 MB MALL): the
+    achievable-HBM reference and the rocprof byte-counter calibration kernel."""
+    src = hip.DeviceBuffer(ctx, nbytes)
+    dst = hip.DeviceBuffer(ctx, nbytes)
+    ctx.copy_dev(dst, src, nbytes)
+    e0, e1 = hip.Event(ctx), hip.Event(ctx)
+    e0.record()
+    for _ in range(reps):
+        ctx.copy_dev(dst, src, nbytes)
+    e1.record()
+    ms = e0.elapsed_ms(e1) / reps
+    return {"bytes": nbytes, "ms": round(ms, 4), "gbs": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def cpu_baseline_q8(a, wq, N, K, budget_s=10.0):
     """Oracle INT8 block GEMM on as many rows as fit the time budget."""
     from oracle import oracle as orc
@@ -117,6 +132,7 @@ def main():
     ctx = hip.HipContext(0)
     main_run = bench_q8_gemm(ctx, hip, args.steps, args.warmup, hip.ActQuant.AMAX127)
     pow2_run = bench_q8_gemm(ctx, hip, args.steps, args.warmup, hip.ActQuant.POW2)
+    copy_run = bench_copy(ctx, hip)
 
     M, N, K = main_run["M"], main_run["N"], main_run["K"]
     achieved = main_run["gemm_tops"]
@@ -144,6 +160,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "extra": {
+            "hbm_copy_reference": copy_run,
             "gemm_kernel_ms": round(main_run["gemm_ms"], 4),
             "gemm_frac_of_bf16_mfma_peak": round(achieved / PEAK["bf16_tflops"], 4),
             "pow2_act": {"tops": round(pow2_run["tops"], 2), "gemm_tops": round(pow2_run["gemm_tops"], 2),

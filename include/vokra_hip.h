@@ -96,6 +96,10 @@ int vokra_hip_event_create(vokra_hip_ctx_t *ctx, vokra_hip_event_t **ev);
 int vokra_hip_event_record(vokra_hip_ctx_t *ctx, vokra_hip_event_t *ev);
 int vokra_hip_event_elapsed_ms(vokra_hip_event_t *start, vokra_hip_event_t *stop, float *ms);
 void vokra_hip_event_destroy(vokra_hip_event_t *ev);
+/* Device-to-device copy by a plain streaming kernel (bytes % 16 == 0, both
+ * pointers 16-byte aligned); the HBM bandwidth reference. No reference
+ * counterpart: plumbing for measurement. */
+int vokra_hip_copy_dev(vokra_hip_ctx_t *ctx, void *d_dst, const void *d_src, size_t bytes);
 
 /* ---- block dequantization and the fused dequant GEMV ---------------------- */
 

@@ -505,6 +505,17 @@ int vokra_hip_gemm_q_f32(vokra_hip_ctx_t* c, int wdtype, size_t m, size_t n, siz
     return st;
 }
 
+int vokra_hip_copy_dev(vokra_hip_ctx_t* c, void* d_dst, const void* d_src, size_t bytes) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "copy_dev: ctx is NULL");
+    if (bytes % 16 != 0 || ((reinterpret_cast<uintptr_t>(d_dst) | reinterpret_cast<uintptr_t>(d_src)) & 15))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "copy_dev: needs 16-byte aligned pointers and size");
+    if (bytes == 0) return VOKRA_HIP_OK;
+    if (!d_dst || !d_src) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "copy_dev: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_copy_u4(c->stream, d_src, d_dst, bytes / 16), "launch(vk_copy_u4)");
+    return VOKRA_HIP_OK;
+}
+
 int vokra_hip_quantize_bytes_dev(vokra_hip_ctx_t* c, int mode, const float* d_x, size_t n, uint8_t* d_out) {
     if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "quantize_bytes: ctx is NULL");
     if (kv_block_bytes(mode) == 0)

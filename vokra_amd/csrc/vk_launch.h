@@ -6,11 +6,12 @@
 #include <stdint.h>
 
 namespace vk {
-constexpr int GEMM_TM = 128;  // block GEMM workgroup tile (rows of A)
+constexpr int GEMM_TM = 256;  // block GEMM workgroup tile (rows of A)
 constexpr int GEMM_TN = 128;  // block GEMM workgroup tile (rows of W)
 
 hipError_t launch_dequantize_q0(hipStream_t s, int mode, const uint8_t* bytes, size_t n_blocks, float* out);
 hipError_t launch_pack_q0(hipStream_t s, int mode, const float* x, size_t n_blocks, uint8_t* out);
+hipError_t launch_copy_u4(hipStream_t s, const void* src, void* dst, size_t n16);
 hipError_t launch_dequant_gemv_f32(hipStream_t s, int mode, const uint8_t* bytes, int n_rows, int n_bpr,
                                    const float* x, float* y);
 hipError_t launch_quantize_act_b32(hipStream_t s, bool pow2, const float* a, int m, int m_pad, int k,

@@ -64,6 +64,14 @@ __global__ void vk_dequantize_q0(int mode, const uint8_t* __restrict__ bytes, si
 }
 
 // ---------------------------------------------------------------------------
+// Plain 16-byte-per-lane copy (HBM bandwidth reference and the calibration
+// kernel for rocprof FETCH_SIZE / WRITE_SIZE).
+__global__ void vk_copy_u4(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
+// ---------------------------------------------------------------------------
 // Pack f32 -> wire blocks, one 32-lane half-wave per block (lane i owns
 // element i). Same arithmetic as the reference packers: amax fold, d = amax/k
 // (k = 127, 7, 15), inv = 1/d, q = round(clamp(x*inv, lo, hi)), f16(d) stored
@@ -213,15 +221,15 @@ __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pa
     const int mt = row >> 4, mr = row & 15;
     const size_t frag = (size_t)mt * nb + b;
     afrag[frag * 64 + (size_t)(mr + 16 * c)] = make_uint4(w[0], w[1], w[2], w[3]);
-    if (c == 0) {
-        ascale[frag * 16 + mr] = s;
-        agsum[frag * 16 + mr] = gs;
+    if (c == 0) {  // scales and sums are block-major: [nb][m_pad]
+        ascale[(size_t)b * m_pad + row] = s;
+        agsum[(size_t)b * m_pad + row] = gs;
     }
 }
 
 // ---------------------------------------------------------------------------
 // Weight repack (upload time): wire blocks [n][nb] -> bf16 integer fragments
-// [n_pad/16][nb][64][8] + f32 scales [n_pad/16][nb][16]. Rows >= n are zero.
+// [n_pad/16][nb][64][8] + f32 scales block-major [nb][n_pad]. Rows >= n are zero.
 __global__ void vk_repack_w_b32(int mode, const uint8_t* __restrict__ wq, int n, int n_pad, int nb,
                                 uint4* __restrict__ wfrag, float* __restrict__ wscale) {
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -245,7 +253,7 @@ __global__ void vk_repack_w_b32(int mode, const uint8_t* __restrict__ wq, int n,
     const int nt = row >> 4, nr = row & 15;
     const size_t frag = (size_t)nt * nb + b;
     wfrag[frag * 64 + (size_t)(nr + 16 * c)] = make_uint4(w[0], w[1], w[2], w[3]);
-    if (c == 0) wscale[frag * 16 + nr] = d;
+    if (c == 0) wscale[(size_t)b * n_pad + row] = d;
 }
 
 // ---------------------------------------------------------------------------
@@ -257,57 +265,77 @@ __global__ void vk_repack_w_b32(int mode, const uint8_t* __restrict__ wq, int n,
 // the A operand already carries 2^e and the combine is fmaf(dw, P_b, .),
 // which is the same value (the power-of-two product sa * dw is exact).
 //
-// Workgroup tile 128 (m) x 128 (n), 4 waves in 2 x 2, wave tile 64 x 64 =
-// 4 x 4 MFMA tiles. One quant block per K step, double-buffered in LDS with
-// the next block's global loads in flight during the MFMAs.
+// Workgroup tile 256 (m) x 128 (n): 8 waves in 4 x 2, wave tile 64 x 64 =
+// 4 x 4 MFMA tiles, one quant block (K = 32) per pipeline stage. Operands
+// are staged global -> registers -> LDS (double-buffered): two register sets
+// keep the loads for the next two stages in flight while a stage computes.
+// Barriers are bare s_barrier: __syncthreads() would also fence, which waits
+// for every load in flight and would serialize the pipeline.
+// Tile order is XCD-aware: workgroup i runs on XCD i % 8, so each XCD gets a
+// contiguous run of tiles, ordered n-tile-major to share W tiles in its L2.
+// The epilogue transposes each wave's 16 x 64 row strips through LDS so rows
+// leave as full 256-byte dwordx4 stores.
 namespace gemm {
-constexpr int TM = 128, TN = 128;
-constexpr int FRAG_U4 = 64;  // uint4 per 16x32 fragment (1 KiB)
+constexpr int TM = 256, TN = 128, THREADS = 512;
+constexpr int MT = TM / 16, NT = TN / 16;  // fragment tiles per workgroup tile
+constexpr int FRAG_U4 = 64;                // uint4 per 16x32 fragment (1 KiB)
+constexpr int N_XCD = 8;
 }  // namespace gemm
 
+// LDS writes of this wave are complete, then all waves meet.
+#define VK_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
+struct vk_stage_regs {
+    uint4 a0, a1, b0;
+    float s;
+};
+
 template <bool POW2>
-__global__ __launch_bounds__(256, 2) void vk_gemm_qblock(
+__global__ __launch_bounds__(512, 1) void vk_gemm_qblock(
     const uint4* __restrict__ afrag, const float* __restrict__ ascale,
     const uint4* __restrict__ wfrag, const float* __restrict__ wscale, const float* __restrict__ bias,
-    float* __restrict__ out, int m, int n, int nb, int ldo) {
+    float* __restrict__ out, int m, int n, int nb, int ldo, int m_pad, int n_pad) {
     using namespace gemm;
-    __shared__ uint4 lds_a[2][8 * FRAG_U4];
-    __shared__ uint4 lds_b[2][8 * FRAG_U4];
+    __shared__ uint4 lds_a[2][MT * FRAG_U4];  // 2 x 16 KiB; reused by the epilogue
+    __shared__ uint4 lds_b[2][NT * FRAG_U4];  // 2 x 8 KiB
     __shared__ float lds_sa[2][TM];
     __shared__ float lds_dw[2][TN];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int mt0 = blockIdx.y * (TM / 16), nt0 = blockIdx.x * (TN / 16);
 
-    // Global -> register staging: each thread moves 2 A + 2 B uint4 per block,
-    // threads 0..31 move the 128 A scales, threads 32..63 the 128 W scales.
-    uint4 ra[2], rb[2];
-    float4 rs;
-    auto gload = [&](int b) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int idx = tid + 256 * h;          // 0..511
-            const int t = idx >> 6, l = idx & 63;   // tile 0..7, lane
-            ra[h] = afrag[((size_t)(mt0 + t) * nb + b) * FRAG_U4 + l];
-            rb[h] = wfrag[((size_t)(nt0 + t) * nb + b) * FRAG_U4 + l];
-        }
-        if (tid < 32) {
-            const int t = tid >> 2, q = tid & 3;
-            rs = reinterpret_cast<const float4*>(ascale + ((size_t)(mt0 + t) * nb + b) * 16)[q];
-        } else if (tid < 64) {
-            const int t = (tid - 32) >> 2, q = tid & 3;
-            rs = reinterpret_cast<const float4*>(wscale + ((size_t)(nt0 + t) * nb + b) * 16)[q];
-        }
+    // XCD-aware tile index: workgroups L, L+8, L+16, ... share an XCD.
+    const int tiles_m = m_pad / TM, tiles_n = n_pad / TN, tiles = tiles_m * tiles_n;
+    const int L = blockIdx.x;
+    const int per_xcd = tiles / N_XCD;
+    const int t = (per_xcd * N_XCD == tiles) ? (L % N_XCD) * per_xcd + L / N_XCD : L;
+    const int ntile = t / tiles_m, mtile = t - ntile * tiles_m;
+    const int mt0 = mtile * MT, nt0 = ntile * NT;
+
+    // Per-thread slice of one stage: A fragment quads tid and tid+512, B quad
+    // tid, and one scale (threads 0..255: A, 256..383: W, the rest idle).
+    const size_t a_base0 = (size_t)(mt0 + (tid >> 6)) * nb * FRAG_U4 + lane;
+    const size_t a_base1 = (size_t)(mt0 + 8 + (tid >> 6)) * nb * FRAG_U4 + lane;
+    const size_t b_base0 = (size_t)(nt0 + (tid >> 6)) * nb * FRAG_U4 + lane;
+    const bool s_live = tid < TM + TN;
+    const float* s_src = tid < TM ? ascale + mt0 * 16 + tid : wscale + nt0 * 16 + (tid - TM);
+    const int s_stride = tid < TM ? m_pad : n_pad;
+
+    auto gload = [=](int b) -> vk_stage_regs {
+        const size_t o = (size_t)b * FRAG_U4;
+        vk_stage_regs r;
+        r.a0 = afrag[a_base0 + o];
+        r.a1 = afrag[a_base1 + o];
+        r.b0 = wfrag[b_base0 + o];
+        r.s = s_live ? s_src[(size_t)b * s_stride] : 0.0f;
+        return r;
     };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            lds_a[buf][tid + 256 * h] = ra[h];
-            lds_b[buf][tid + 256 * h] = rb[h];
-        }
-        if (tid < 32) reinterpret_cast<float4*>(lds_sa[buf])[tid] = rs;
-        else if (tid < 64) reinterpret_cast<float4*>(lds_dw[buf])[tid - 32] = rs;
+    auto lstore = [&](const vk_stage_regs r, int buf) {
+        lds_a[buf][tid] = r.a0;
+        lds_a[buf][tid + THREADS] = r.a1;
+        lds_b[buf][tid] = r.b0;
+        if (tid < TM) lds_sa[buf][tid] = r.s;
+        else if (tid < TM + TN) lds_dw[buf][tid - TM] = r.s;
     };
 
     vk_f32x4 acc[4][4];
@@ -316,13 +344,8 @@ __global__ __launch_bounds__(256, 2) void vk_gemm_qblock(
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = (vk_f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
     const vk_f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int b = 0; b < nb; ++b) {
-        const int buf = b & 1;
-        if (b + 1 < nb) gload(b + 1);
+    auto compute = [&](int buf) {
         vk_bf16x8 af[4], bf[4];
         float sa[4][4], dw[4];
 #pragma unroll
@@ -347,35 +370,74 @@ __global__ __launch_bounds__(256, 2) void vk_gemm_qblock(
                     else acc[i][j][r] = fmaf(sa[i][r] * dw[j], p[r], acc[i][j][r]);
                 }
             }
-        if (b + 1 < nb) {
-            lstore(buf ^ 1);
-        }
-        __syncthreads();
+    };
+
+    // Loads past the last block re-read block nb-1 (in bounds, never used),
+    // which keeps the loop free of conditionals around the staging registers.
+    const int last = nb - 1;
+    vk_stage_regs r0 = gload(0);
+    vk_stage_regs r1 = gload(min(1, last));
+    lstore(r0, 0);
+    r0 = gload(min(2, last));
+    VK_LDS_BARRIER();
+    for (int b = 0; b < nb; b += 2) {
+        compute(0);  // stage b
+        if (b + 1 < nb) lstore(r1, 1);
+        r1 = gload(min(b + 3, last));
+        VK_LDS_BARRIER();
+        if (b + 1 >= nb) break;
+        compute(1);  // stage b + 1
+        if (b + 2 < nb) lstore(r0, 0);
+        r0 = gload(min(b + 4, last));
+        VK_LDS_BARRIER();
     }
 
-    // D layout of v_mfma_f32_16x16x32_bf16: lane l holds rows 4*(l/16)+r of
-    // column l%16.
+    // Epilogue. D layout of v_mfma_f32_16x16x32_bf16: lane l holds rows
+    // 4*(l/16)+r of column l%16. Each wave owns a 4 KiB LDS slot; per m-subtile
+    // it writes the 16 x 64 strip, then reads it back row-major.
+    float* slot = reinterpret_cast<float*>(&lds_a[0][0]) + wave * 1024;
+    const int col0 = (nt0 + wn * 4) * 16;
+    const bool vec_ok = (ldo % 4 == 0) && (col0 + 64 <= n) &&
+                        (((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(bias)) & 15) == 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int col = (nt0 + wn * 4 + j) * 16 + (lane & 15);
-            if (col >= n) continue;
-            const float bv = bias ? bias[col] : 0.0f;
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = (mt0 + wm * 4 + i) * 16 + 4 * (lane >> 4) + r;
-                if (row < m) out[(size_t)row * ldo + col] = bias ? acc[i][j][r] + bv : acc[i][j][r];
+            for (int r = 0; r < 4; ++r) slot[(4 * (lane >> 4) + r) * 64 + 16 * j + (lane & 15)] = acc[i][j][r];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int row_base = (mt0 + wm * 4 + i) * 16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int rr = 4 * q + (lane >> 4), c4 = 4 * (lane & 15);
+            const int row = row_base + rr;
+            float4 v = *reinterpret_cast<const float4*>(slot + rr * 64 + c4);
+            if (row >= m) continue;
+            if (vec_ok) {
+                if (bias) {
+                    const float4 bv = *reinterpret_cast<const float4*>(bias + col0 + c4);
+                    v.x = v.x + bv.x; v.y = v.y + bv.y; v.z = v.z + bv.z; v.w = v.w + bv.w;
+                }
+                *reinterpret_cast<float4*>(out + (size_t)row * ldo + col0 + c4) = v;
+            } else {
+                const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int col = col0 + c4 + u;
+                    if (col < n) out[(size_t)row * ldo + col] = bias ? e[u] + bias[col] : e[u];
+                }
             }
         }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
 }
 
 template __global__ void vk_quantize_act_b32<false>(const float*, int, int, int, uint4*, float*, int*);
 template __global__ void vk_quantize_act_b32<true>(const float*, int, int, int, uint4*, float*, int*);
 template __global__ void vk_gemm_qblock<false>(const uint4*, const float*, const uint4*, const float*,
-                                               const float*, float*, int, int, int, int);
+                                               const float*, float*, int, int, int, int, int, int);
 template __global__ void vk_gemm_qblock<true>(const uint4*, const float*, const uint4*, const float*,
-                                              const float*, float*, int, int, int, int);
+                                              const float*, float*, int, int, int, int, int, int);
 
 }  // namespace vk
 
@@ -392,6 +454,14 @@ hipError_t launch_dequantize_q0(hipStream_t s, int mode, const uint8_t* bytes, s
     const size_t threads = n_blocks * 4;
     const unsigned grid = (unsigned)((threads + 255) / 256);
     hipLaunchKernelGGL(vk_dequantize_q0, dim3(grid), dim3(256), 0, s, mode, bytes, n_blocks, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_u4(hipStream_t s, const void* src, void* dst, size_t n16) {
+    if (n16 == 0) return hipSuccess;
+    const size_t want = (n16 + 255) / 256;
+    const unsigned grid = (unsigned)(want < 8192 ? want : 8192);
+    hipLaunchKernelGGL(vk_copy_u4, dim3(grid), dim3(256), 0, s, (const uint4*)src, (uint4*)dst, n16);
     return hipGetLastError();
 }
 
@@ -440,13 +510,13 @@ hipError_t launch_repack_w_b32(hipStream_t s, int mode, const uint8_t* wq, int n
 hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
                               const uint4* wfrag, const float* wscale, const float* bias, float* out,
                               int m, int m_pad, int n, int n_pad, int nb) {
-    const dim3 grid((unsigned)(n_pad / gemm::TN), (unsigned)(m_pad / gemm::TM));
+    const dim3 grid((unsigned)((n_pad / gemm::TN) * (m_pad / gemm::TM)));
     if (pow2)
-        hipLaunchKernelGGL(vk_gemm_qblock<true>, grid, dim3(256), 0, s, afrag, ascale, wfrag, wscale, bias,
-                           out, m, n, nb, n);
+        hipLaunchKernelGGL(vk_gemm_qblock<true>, grid, dim3(gemm::THREADS), 0, s, afrag, ascale, wfrag, wscale, bias,
+                           out, m, n, nb, n, m_pad, n_pad);
     else
-        hipLaunchKernelGGL(vk_gemm_qblock<false>, grid, dim3(256), 0, s, afrag, ascale, wfrag, wscale, bias,
-                           out, m, n, nb, n);
+        hipLaunchKernelGGL(vk_gemm_qblock<false>, grid, dim3(gemm::THREADS), 0, s, afrag, ascale, wfrag, wscale, bias,
+                           out, m, n, nb, n, m_pad, n_pad);
     return hipGetLastError();
 }
 

@@ -97,6 +97,7 @@ def _declare(L):
     L.vokra_hip_qweight_free.argtypes = [P]
     L.vokra_hip_qweight_free.restype = None
     L.vokra_hip_gemm_q_f32_dev.argtypes = [P, P, sz, P, P, P, C.c_int]
+    L.vokra_hip_copy_dev.argtypes = [P, P, P, sz]
     L.vokra_hip_quantize_bytes.argtypes = [P, C.c_int, f32p, sz, u8p, sz]
     L.vokra_hip_quantize_bytes_dev.argtypes = [P, C.c_int, P, sz, P]
     L.vokra_hip_qact_create.argtypes = [P, sz, sz, C.POINTER(P)]
@@ -275,6 +276,9 @@ class HipContext:
 
     def synchronize(self):
         _check(lib().vokra_hip_synchronize(self._h))
+
+    def copy_dev(self, d_dst: "DeviceBuffer", d_src: "DeviceBuffer", nbytes: int):
+        _check(lib().vokra_hip_copy_dev(self._h, d_dst.ptr, d_src.ptr, nbytes))
 
     # ---- kv_quant surface ------------------------------------------------
     def dequantize_bytes(self, mode: KvQuant, data) -> np.ndarray:
