@@ -72,6 +72,43 @@ def bench_q8_gemm(ctx, hip, steps, warmup, act):
             "a": a, "wq": wq}
 
 
+def bench_q4_gemv(ctx, hip, n, k=1280, ms=(1, 8, 64), stream_bytes=600 << 20):
+    """Q4_0 decode GEMV: back-to-back launches over distinct weight
+    copies totalling > 512 MB, so weights come from HBM, not the 256 MB MALL.
+    GB/s counts the algorithmic bytes of one launch: Q4_0 weights
+    n*(k/32)*18 + f32 activations m*k*4 + f32 outputs m*n*4."""
+    rng = np.random.default_rng(7)
+    wbytes = n * (k // 32) * 18
+    copies = max(2, stream_bytes // wbytes)
+    base = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    Ws = []
+    for i in range(copies):
+        wq = ctx.quantize_bytes(hip.KvQuant.Q4_0, base if i == 0 else np.roll(base, i, axis=1))
+        Ws.append(ctx.upload_qweight(hip.WDtype.Q4_0, n, k, wq))
+    res = {}
+    for m in ms:
+        a = rng.standard_normal((m, k), dtype=np.float32)
+        d_a = hip.DeviceBuffer.from_array(ctx, a)
+        d_out = hip.DeviceBuffer(ctx, m * n * 4)
+        qa = ctx.qact(m, k)
+        qa.quantize(m, d_a)
+        # one graph replays all launches: host launch cost is not measured
+        graph = ctx.capture(lambda: [ctx.gemm_qact_dev(W, qa, d_out) for W in Ws])
+        graph.launch()
+        e0, e1 = hip.Event(ctx), hip.Event(ctx)
+        e0.record()
+        graph.launch()
+        e1.record()
+        us = e0.elapsed_ms(e1) * 1e3 / len(Ws)
+        nbytes = wbytes + m * k * 4 + m * n * 4
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[f"M{m}"] = {"us_per_launch": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
+                        "frac_hbm": round(gbs / PEAK["hbm_gbs"], 4)}
+    ctx.synchronize()
+    del Ws
+    return {"N": n, "K": k, "weight_copies": copies, **res}
+
+
 def bench_copy(ctx, hip, nbytes=1 << 30, reps=5):
     """Plain streaming copy of 1 GiB (4x the 256 MB MALL): the
     achievable-HBM reference and the rocprof byte-counter calibration kernel."""
@@ -133,6 +170,7 @@ def main():
     main_run = bench_q8_gemm(ctx, hip, args.steps, args.warmup, hip.ActQuant.AMAX127)
     pow2_run = bench_q8_gemm(ctx, hip, args.steps, args.warmup, hip.ActQuant.POW2)
     copy_run = bench_copy(ctx, hip)
+    gemv_runs = [bench_q4_gemv(ctx, hip, n) for n in (5120, 1280)]
 
     M, N, K = main_run["M"], main_run["N"], main_run["K"]
     achieved = main_run["gemm_tops"]
@@ -161,6 +199,7 @@ def main():
         "cpu_baseline": cpu,
         "extra": {
             "hbm_copy_reference": copy_run,
+            "q4_0_gemv_streamed": gemv_runs,
             "gemm_kernel_ms": round(main_run["gemm_ms"], 4),
             "gemm_frac_of_bf16_mfma_peak": round(achieved / PEAK["bf16_tflops"], 4),
             "pow2_act": {"tops": round(pow2_run["tops"], 2), "gemm_tops": round(pow2_run["gemm_tops"], 2),

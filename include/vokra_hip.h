@@ -101,6 +101,18 @@ void vokra_hip_event_destroy(vokra_hip_event_t *ev);
  * counterpart: plumbing for measurement. */
 int vokra_hip_copy_dev(vokra_hip_ctx_t *ctx, void *d_dst, const void *d_src, size_t bytes);
 
+/* ---- HIP graphs: capture a sequence of _dev calls, replay it ------------- */
+/* Launch-bound loops (a decode step, a stream of GEMVs) are recorded once
+ * and replayed as one graph launch. Only calls that allocate nothing may be
+ * captured (resident weights, pre-created qact buffers). The reference has
+ * no counterpart; its sessions synchronize once per step instead
+ * (crates/vokra-backend-cuda/src/context.rs:5310). */
+typedef struct vokra_hip_graph vokra_hip_graph_t;
+int vokra_hip_capture_begin(vokra_hip_ctx_t *ctx);
+int vokra_hip_capture_end(vokra_hip_ctx_t *ctx, vokra_hip_graph_t **out);
+int vokra_hip_graph_launch(vokra_hip_ctx_t *ctx, vokra_hip_graph_t *g);
+void vokra_hip_graph_destroy(vokra_hip_graph_t *g);
+
 /* ---- block dequantization and the fused dequant GEMV ---------------------- */
 
 /* Wire Q4_0/Q5_0/Q8_0 blocks -> f32, bit-exact. Replaces
@@ -140,6 +152,11 @@ int vokra_hip_gemm_q_f32(vokra_hip_ctx_t *ctx, int wdtype, size_t m, size_t n, s
 
 /* Activation convention for the block-format INT8 path of this context. */
 int vokra_hip_set_act_quant(vokra_hip_ctx_t *ctx, int act_quant);
+
+/* Kernel routing for m <= 64 (default 1 = the decode kernel that streams the
+ * compact weights; 0 = the tiled GEMM). Both give bit-identical results; the
+ * switch exists so callers and tests can compare them. */
+int vokra_hip_set_decode_kernel(vokra_hip_ctx_t *ctx, int enable);
 
 /* Device-resident weight: uploads the [n, k] wire payload once and builds
  * the device layouts the kernels stream (the reference keeps weights

@@ -178,6 +178,66 @@ def test_gemm_q_config1_rows_bit_exact(ctx, oracle):
     assert np.array_equal(bits(res), bits(got))
 
 
+@pytest.mark.parametrize("act", [hip.ActQuant.AMAX127, hip.ActQuant.POW2])
+@pytest.mark.parametrize("wd", [hip.WDtype.Q4_0, hip.WDtype.Q8_0])
+@pytest.mark.parametrize("m,n,k", [(1, 16, 128), (3, 100, 256), (8, 1280, 1280), (17, 48, 512),
+                                   (33, 200, 128), (64, 1280, 5120), (64, 5120, 1280)])
+def test_decode_kernel_bit_exact(ctx, oracle, wd, act, m, n, k):
+    """m <= 64 runs the compact-weight decode kernel: bit-exact vs the oracle
+    and bit-identical to the tiled GEMM on the same inputs."""
+    print(f"[case] decode wd={wd.name} act={act.name} m={m} n={n} k={k}", flush=True)
+    a, wq, bias = _gemm_case(oracle, wd, m, n, k, seed=m * 31 + n + k, zero_rows=(0,) if m > 1 else ())
+    ctx.set_act_quant(act)
+    try:
+        got = ctx.gemm_q_f32(m, n, k, a, wq, wd, bias)
+        ctx.set_decode_kernel(False)
+        tiled = ctx.gemm_q_f32(m, n, k, a, wq, wd, bias)
+    finally:
+        ctx.set_decode_kernel(True)
+        ctx.set_act_quant(hip.ActQuant.AMAX127)
+    want = oracle.gemm_qblock_i8(int(wd), m, n, k, a, wq, bias, pow2=(act == hip.ActQuant.POW2))
+    assert np.array_equal(bits(got), bits(want))
+    assert np.array_equal(bits(tiled), bits(got))
+
+
+def test_graph_replay_matches_eager(ctx, oracle):
+    """A captured [activation pass + decode GEMV + tiled GEMM] graph replayed
+    several times, with eager work and synchronizations between replays:
+    every replay equals the eager result bit for bit."""
+    m, n, k = 8, 256, 512
+    a, wq, bias = _gemm_case(oracle, hip.WDtype.Q4_0, m, n, k, seed=99)
+    W = ctx.upload_qweight(hip.WDtype.Q4_0, n, k, wq)
+    a2 = np.concatenate([a] * 9)[:72]
+    W8 = ctx.upload_qweight(hip.WDtype.Q4_0, n, k, wq)
+    da = hip.DeviceBuffer.from_array(ctx, a)
+    da2 = hip.DeviceBuffer.from_array(ctx, a2)
+    db = hip.DeviceBuffer.from_array(ctx, bias)
+    do = hip.DeviceBuffer(ctx, m * n * 4)
+    do2 = hip.DeviceBuffer(ctx, 72 * n * 4)
+    qa, qa2 = ctx.qact(m, k), ctx.qact(72, k)
+
+    def step():
+        qa.quantize(m, da)
+        ctx.gemm_qact_dev(W, qa, do, db)
+        qa2.quantize(72, da2)
+        ctx.gemm_qact_dev(W8, qa2, do2, db)
+
+    step()
+    ctx.synchronize()
+    want1 = do.download(np.float32, m * n)
+    want2 = do2.download(np.float32, 72 * n)
+    assert np.array_equal(bits(want1), bits(oracle.gemm_qblock_i8(2, m, n, k, a, wq, bias).reshape(-1)))
+    g = ctx.capture(step)
+    for rep in range(4):
+        do.upload(np.zeros(m * n, np.float32))
+        do2.upload(np.zeros(72 * n, np.float32))
+        ctx.gemm_q_f32(m, n, k, a, wq, hip.WDtype.Q4_0, bias)  # eager work between replays
+        g.launch()
+        ctx.synchronize()
+        assert np.array_equal(bits(do.download(np.float32, m * n)), bits(want1)), rep
+        assert np.array_equal(bits(do2.download(np.float32, 72 * n)), bits(want2)), rep
+
+
 def test_gemm_q_tracks_f32_within_derived_bound(ctx, oracle):
     """INT8 vs the f32 dequant GEMV oracle: within 2x the activation-rounding
     bound (the rule of kquant_gemm_parity.rs:204-236 at group 32)."""

@@ -105,6 +105,7 @@ struct vokra_hip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     int act_quant = VOKRA_HIP_ACT_AMAX127;
+    bool decode_kernel = true;  // route m <= 64 to the decode kernel
     // Copy-mode staging and the context's own activation workspace.
     DevBuf in0, in1, in2, out0;
     vokra_hip_qact act;
@@ -114,11 +115,21 @@ struct vokra_hip_qweight {
     vokra_hip_ctx* ctx = nullptr;
     int wdtype = 0;
     size_t n = 0, k = 0, n_pad = 0, nb = 0;
-    DevBuf frag, scale;
+    DevBuf frag, scale;  // MFMA-fragment bf16 integers + f32 scales (prefill GEMM)
+    bool has_gemv = false;
+    DevBuf gq, gsc;      // compact decode layout (Q4_0 / Q8_0, k % 128 == 0)
 };
+
+// Largest activation count routed to the decode kernel.
+constexpr size_t kGemvMaxM = 64;
 
 struct vokra_hip_event {
     hipEvent_t ev = nullptr;
+};
+
+struct vokra_hip_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
 };
 
 namespace {
@@ -143,7 +154,7 @@ int quantize_activations(vokra_hip_ctx* c, vokra_hip_qact* qa, const float* d_a,
     }
     const size_t m_pad = round_up(m, vk::GEMM_TM);
     VK_TRY(vk::launch_quantize_act_b32(c->stream, act_quant == VOKRA_HIP_ACT_POW2, d_a, (int)m, (int)m_pad,
-                                       (int)k, (uint4*)qa->frag.p, (float*)qa->scale.p, (int*)qa->gsum.p),
+                                       (int)k, (uint4*)qa->frag.p, (float*)qa->scale.p, (float*)qa->gsum.p),
            "launch(vk_quantize_act_b32)");
     qa->m = m;
     qa->k = k;
@@ -186,11 +197,38 @@ int upload_weight(vokra_hip_ctx* c, int wdtype, size_t n, size_t k, const uint8_
     VK_TRY(vk::launch_repack_w_b32(c->stream, wd_kv_mode(wdtype), d_wq, (int)n, (int)w->n_pad, (int)w->nb,
                                    (uint4*)w->frag.p, (float*)w->scale.p),
            "launch(vk_repack_w_b32)");
+    const int mode = wd_kv_mode(wdtype);
+    w->has_gemv = (mode == VOKRA_HIP_KV_Q4_0 || mode == VOKRA_HIP_KV_Q8_0) && w->nb % 4 == 0;
+    if (w->has_gemv) {
+        const size_t qbytes = w->n_pad * w->nb * (mode == VOKRA_HIP_KV_Q4_0 ? 16 : 32);
+        VK_TRY(w->gq.ensure(qbytes), "hipMalloc(decode weights)");
+        VK_TRY(w->gsc.ensure(w->n_pad * w->nb * 2), "hipMalloc(decode scales)");
+        VK_TRY(vk::launch_repack_w_gemv(c->stream, mode, d_wq, (int)n, (int)w->n_pad, (int)w->nb, (uint4*)w->gq.p,
+                                        (uint2*)w->gsc.p),
+               "launch(vk_repack_w_gemv)");
+    }
     return VOKRA_HIP_OK;
+}
+
+void release_weight(vokra_hip_qweight* w) {
+    w->frag.release();
+    w->scale.release();
+    w->gq.release();
+    w->gsc.release();
 }
 
 int run_gemm_qact(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_qact* qa, const float* d_bias,
                  float* d_out) {
+    // Both kernels produce bit-identical outputs; the decode kernel streams
+    // the compact weights once, the GEMM reuses bf16 tiles across many rows.
+    if (w->has_gemv && qa->m <= kGemvMaxM && c->decode_kernel) {
+        VK_TRY(vk::launch_gemv_qblock(c->stream, wd_kv_mode(w->wdtype), qa->act_quant == VOKRA_HIP_ACT_POW2,
+                                      (const uint4*)qa->frag.p, (const float*)qa->scale.p,
+                                      (const float*)qa->gsum.p, (const uint4*)w->gq.p, (const uint2*)w->gsc.p,
+                                      d_bias, d_out, (int)qa->m, (int)w->n, (int)w->nb, (int)qa->m_pad),
+               "launch(vk_gemv_qblock)");
+        return VOKRA_HIP_OK;
+    }
     VK_TRY(vk::launch_gemm_qblock(c->stream, qa->act_quant == VOKRA_HIP_ACT_POW2, (const uint4*)qa->frag.p,
                                   (const float*)qa->scale.p, (const uint4*)w->frag.p, (const float*)w->scale.p,
                                   d_bias, d_out, (int)qa->m, (int)qa->m_pad, (int)w->n, (int)w->n_pad,
@@ -442,9 +480,14 @@ void vokra_hip_qweight_free(vokra_hip_qweight_t* w) {
         (void)hipSetDevice(w->ctx->device);
         (void)hipStreamSynchronize(w->ctx->stream);
     }
-    w->frag.release();
-    w->scale.release();
+    release_weight(w);
     delete w;
+}
+
+int vokra_hip_set_decode_kernel(vokra_hip_ctx_t* c, int enable) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "set_decode_kernel: ctx is NULL");
+    c->decode_kernel = enable != 0;
+    return VOKRA_HIP_OK;
 }
 
 int vokra_hip_gemm_q_f32_dev(vokra_hip_ctx_t* c, const vokra_hip_qweight_t* w, size_t m, const float* d_a,
@@ -500,9 +543,44 @@ int vokra_hip_gemm_q_f32(vokra_hip_ctx_t* c, int wdtype, size_t m, size_t n, siz
     } else {
         (void)hipStreamSynchronize(c->stream);
     }
-    w.frag.release();
-    w.scale.release();
+    release_weight(&w);
     return st;
+}
+
+int vokra_hip_capture_begin(vokra_hip_ctx_t* c) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "capture_begin: ctx is NULL");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_capture_end(vokra_hip_ctx_t* c, vokra_hip_graph_t** out) {
+    if (!c || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "capture_end: NULL argument");
+    *out = nullptr;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    auto* g = new vokra_hip_graph();
+    hipError_t e = hipStreamEndCapture(c->stream, &g->graph);
+    if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        vokra_hip_graph_destroy(g);
+        return hip_fail(e, "hipStreamEndCapture/hipGraphInstantiate");
+    }
+    *out = g;
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_graph_launch(vokra_hip_ctx_t* c, vokra_hip_graph_t* g) {
+    if (!c || !g) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "graph_launch: NULL argument");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(hipGraphLaunch(g->exec, c->stream), "hipGraphLaunch");
+    return VOKRA_HIP_OK;
+}
+
+void vokra_hip_graph_destroy(vokra_hip_graph_t* g) {
+    if (!g) return;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
 }
 
 int vokra_hip_copy_dev(vokra_hip_ctx_t* c, void* d_dst, const void* d_src, size_t bytes) {

@@ -13,6 +13,11 @@ typedef float vk_f32x16 __attribute__((ext_vector_type(16)));
 
 #define VK_WAVE 64
 
+// Workgroup barrier for LDS hand-offs: this wave's LDS writes are complete,
+// then all waves meet. Unlike __syncthreads() it does not fence global
+// memory, so prefetched global loads stay in flight across it.
+#define VK_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
 // binary16 -> f32, exact for every finite value; NaN decodes to the canonical
 // quiet NaN 0x7FC00000 as f32::NAN does.
 // crates/vokra-core/src/kv_quant/half.rs:53-69 (value-identical bit build).
@@ -26,6 +31,13 @@ __device__ __forceinline__ float vk_f16_to_f32(uint32_t h) {
         return sign ? -v : v;
     }
     return __uint_as_float((sign << 31) | ((exp + 112u) << 23) | (mant << 13));
+}
+
+// Branch-free binary16 -> f32 for hot loops (v_cvt_f32_f16): the same value
+// as vk_f16_to_f32 for every non-NaN input, subnormals included; a NaN scale
+// decodes to some quiet NaN rather than exactly 0x7FC00000.
+__device__ __forceinline__ float vk_f16_to_f32_hw(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
 // f32 -> binary16 with round-to-nearest-even; overflow -> inf, NaN -> 0x7E00

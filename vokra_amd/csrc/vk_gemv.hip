@@ -1,0 +1,259 @@
+// vk_gemv.hip — decode-shaped (M <= 64) block GEMM for gfx950.
+//
+// Same numerics as vk_gemm_qblock (INT8 activations, exact per-block integer
+// dots, combine acc = fmaf(sa * dw, P_b, acc) in block order), so the two
+// kernels are bit-identical and the dispatcher picks by shape. Here the
+// weights stream from HBM once in a compact device layout:
+//
+//  * Q4_0: per (16-row tile nt, group g of 4 blocks) one 1 KiB fragment, lane
+//    l (row l%16, column chunk c = l/16) holding one 32-bit "nibble word" per
+//    block: element 8c+2j at bits 4j..4j+3 and 8c+2j+1 at bits 16+4j..19+4j,
+//    so ((X >> 4j) & 0x000F000F) | 0x43004300 is the bf16 pair (128 + nib).
+//  * Q8_0: two 1 KiB fragments per (nt, g), lane l holding 8 bytes q + 128 per
+//    block; v_cvt_f32_ubyte turns each into the exact bf16 of q + 128.
+//  * scales: f16 per (row, block) at [nt][g][16][4] (one 8-byte load per lane).
+//
+// The weight offsets (+128 on every element, and the Q4_0 nibble bias 8) are
+// removed through the MFMA accumulator input: C = -(128 + 8) * sum(A) for
+// Q4_0 and -128 * sum(A) for Q8_0, where sum(A) is the exact operand sum the
+// activation pass writes. Every product and partial sum is an integer (times
+// a power of two for POW2 activations) below 2^24, so D = P_b exactly.
+#include "vk_common.h"
+
+namespace vk {
+
+namespace gemv {
+constexpr int WAVES = 4;        // waves per workgroup, one 16-column tile each
+constexpr int GB = 4;           // quant blocks per pipeline group
+constexpr int FRAG_U4 = 64;
+}  // namespace gemv
+
+// ---------------------------------------------------------------------------
+// Weight repack for the decode layout (upload time). One thread per (row,
+// group of 4 blocks, column chunk c): reads the row's wire blocks directly.
+__global__ void vk_repack_w_gemv(int mode, const uint8_t* __restrict__ wq, int n, int n_pad, int nb,
+                                 uint4* __restrict__ wq4, uint2* __restrict__ wsc) {
+    const int G = nb / gemv::GB;
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t total = (size_t)n_pad * G * 4;
+    if (gid >= total) return;
+    const int c = (int)(gid & 3);
+    const size_t rg = gid >> 2;
+    const int row = (int)(rg / G), g = (int)(rg % G);
+    const int nt = row >> 4, lane = (row & 15) + 16 * c;
+    const int bb = mode == 3 ? 34 : 18;
+    uint32_t w[4] = {0, 0, 0, 0}, w2[4] = {0, 0, 0, 0};
+    uint16_t sc[4] = {0, 0, 0, 0};
+    for (int u = 0; u < gemv::GB; ++u) {
+        if (row >= n) break;
+        const uint8_t* p = wq + ((size_t)row * nb + g * gemv::GB + u) * bb;
+        sc[u] = (uint16_t)(p[0] | (p[1] << 8));
+        if (mode == 1) {
+            // elements 8c .. 8c+7 are bytes 4c .. 4c+3 (lo nibble = even element)
+            uint32_t x = 0;
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t b = p[2 + 4 * c + j];
+                x |= (b & 0x0fu) << (4 * j);
+                x |= (b >> 4) << (16 + 4 * j);
+            }
+            w[u] = x;
+        } else {
+            uint32_t lo = 0, hi = 0;
+            for (int j = 0; j < 4; ++j) {
+                lo |= (uint32_t)((uint8_t)(p[2 + 8 * c + j] + 128u)) << (8 * j);
+                hi |= (uint32_t)((uint8_t)(p[2 + 8 * c + 4 + j] + 128u)) << (8 * j);
+            }
+            if (u < 2) { w[2 * u] = lo; w[2 * u + 1] = hi; }
+            else { w2[2 * (u - 2)] = lo; w2[2 * (u - 2) + 1] = hi; }
+        }
+    }
+    const size_t fg = (size_t)nt * G + g;
+    if (mode == 1) {
+        wq4[fg * gemv::FRAG_U4 + lane] = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        wq4[(fg * 2) * gemv::FRAG_U4 + lane] = make_uint4(w[0], w[1], w[2], w[3]);
+        wq4[(fg * 2 + 1) * gemv::FRAG_U4 + lane] = make_uint4(w2[0], w2[1], w2[2], w2[3]);
+    }
+    if (c == 0)
+        wsc[fg * 16 + (row & 15)] = make_uint2((uint32_t)sc[0] | ((uint32_t)sc[1] << 16),
+                                               (uint32_t)sc[2] | ((uint32_t)sc[3] << 16));
+}
+
+// bf16 operand (8 values) of one Q4_0 block from its nibble word.
+__device__ __forceinline__ vk_bf16x8 q4_word_to_bf16(uint32_t x) {
+    uint4 r;
+    r.x = (x & 0x000F000Fu) | 0x43004300u;
+    r.y = ((x >> 4) & 0x000F000Fu) | 0x43004300u;
+    r.z = ((x >> 8) & 0x000F000Fu) | 0x43004300u;
+    r.w = ((x >> 12) & 0x000F000Fu) | 0x43004300u;
+    return __builtin_bit_cast(vk_bf16x8, r);
+}
+
+// bf16 operand of one Q8_0 block from 8 offset bytes (u = q + 128, exact).
+__device__ __forceinline__ uint32_t u8pair_to_bf16(uint32_t x, int k) {
+    // bytes k, k+1 of x -> two bf16 (high halves of the exact f32 values)
+    const float a = (float)((x >> (8 * k)) & 0xffu), b = (float)((x >> (8 * (k + 1))) & 0xffu);
+    return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xffff0000u);
+}
+__device__ __forceinline__ vk_bf16x8 q8_bytes_to_bf16(uint32_t lo, uint32_t hi) {
+    uint4 r;
+    r.x = u8pair_to_bf16(lo, 0);
+    r.y = u8pair_to_bf16(lo, 2);
+    r.z = u8pair_to_bf16(hi, 0);
+    r.w = u8pair_to_bf16(hi, 2);
+    return __builtin_bit_cast(vk_bf16x8, r);
+}
+
+// ---------------------------------------------------------------------------
+// Decode kernel. One workgroup = one 16 x 16 output tile (16 activation rows,
+// 16 weight rows). Phase 1: the 4 waves split the K blocks by 4-block group
+// (group g -> wave g % 4), prefetch all their weight words and activation
+// fragments for the chunk up front, and compute the exact block dots P_b
+// (one MFMA per block) into LDS together with the block scales. Phase 2: one
+// thread per output walks the chunk's blocks in order with the same
+// fmaf(sa * dw, P_b, acc) as the tiled GEMM, so the result is bit-identical.
+// K is processed in chunks of CB blocks so P fits LDS.
+namespace gemv {
+constexpr int CB = 48;                 // blocks per chunk (12 groups)
+constexpr int GPW = CB / GB / WAVES;   // groups per wave per chunk (3)
+}  // namespace gemv
+
+template <int MODE, bool POW2>
+__global__ __launch_bounds__(256) void vk_gemv_qblock(
+    const uint4* __restrict__ afrag, const float* __restrict__ ascale, const float* __restrict__ asum,
+    const uint4* __restrict__ wq4, const uint2* __restrict__ wsc, const float* __restrict__ bias,
+    float* __restrict__ out, int m, int n, int nb, int m_pad, int n_tiles) {
+    using namespace gemv;
+    constexpr int WQ = MODE == 1 ? 1 : 2;  // weight uint4 per lane per group
+    constexpr float OFFSET = MODE == 1 ? -136.0f : -128.0f;
+    __shared__ float lds_p[CB][256];       // exact block dots, [block][row*16 + col]
+    __shared__ float lds_sa[CB][16];       // activation scales, [block][row]
+    __shared__ float lds_as[CB][16];       // activation operand sums, [block][row]
+    __shared__ float lds_dw[CB][16];       // weight scales, [block][col]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nt = blockIdx.x, mt = blockIdx.y;
+    const int G = nb / GB;
+    const int rq = 4 * (lane >> 4);        // first of this lane's 4 D rows
+
+    float acc = 0.0f;                      // phase 2: output (row tid/16, col tid%16)
+    for (int g0 = 0; g0 < G; g0 += CB / GB) {
+        const int gn = min(CB / GB, G - g0);  // groups in this chunk
+        // ---- phase 1 loads (everything for this wave's groups, up front)
+        uint4 wq[GPW][WQ];
+        uint2 ws[GPW];
+        uint4 af[GPW][GB];
+#pragma unroll
+        for (int j = 0; j < GPW; ++j) {
+            const int gl = min(wave + WAVES * j, gn - 1);  // clamped: loads stay in bounds
+            const int g = g0 + gl;
+            const size_t fg = (size_t)nt * G + g;
+#pragma unroll
+            for (int h = 0; h < WQ; ++h) wq[j][h] = wq4[(fg * WQ + h) * FRAG_U4 + lane];
+            ws[j] = wsc[fg * 16 + (lane & 15)];
+#pragma unroll
+            for (int u = 0; u < GB; ++u) af[j][u] = afrag[((size_t)mt * nb + g * GB + u) * FRAG_U4 + lane];
+        }
+        // activation scales and operand sums of the chunk: 16 rows x gn*GB
+        // blocks, loaded once per workgroup (3 values of each per thread)
+        float sv[CB * 16 / 256], tv[CB * 16 / 256];
+#pragma unroll
+        for (int h = 0; h < CB * 16 / 256; ++h) {
+            const int idx = min(tid + 256 * h, gn * GB * 16 - 1);
+            const int bl = idx >> 4, r = idx & 15;
+            const size_t o = (size_t)(g0 * GB + bl) * m_pad + mt * 16 + r;
+            sv[h] = ascale[o];
+            tv[h] = asum[o];
+        }
+#pragma unroll
+        for (int h = 0; h < CB * 16 / 256; ++h) {
+            const int idx = tid + 256 * h;
+            if (idx < gn * GB * 16) {
+                lds_sa[idx >> 4][idx & 15] = sv[h];
+                lds_as[idx >> 4][idx & 15] = tv[h];
+            }
+        }
+        VK_LDS_BARRIER();
+        // ---- phase 1 compute: exact P_b for this wave's groups
+#pragma unroll
+        for (int j = 0; j < GPW; ++j) {
+            const int gl = wave + WAVES * j;
+            if (gl >= gn) break;
+            const uint32_t sc_bits[4] = {ws[j].x & 0xffffu, ws[j].x >> 16, ws[j].y & 0xffffu, ws[j].y >> 16};
+#pragma unroll
+            for (int u = 0; u < GB; ++u) {
+                vk_bf16x8 bf;
+                if (MODE == 1) {
+                    const uint4 q = wq[j][0];
+                    const uint32_t x = u == 0 ? q.x : (u == 1 ? q.y : (u == 2 ? q.z : q.w));
+                    bf = q4_word_to_bf16(x);
+                } else {
+                    const uint4 q = wq[j][u >> 1];
+                    bf = (u & 1) ? q8_bytes_to_bf16(q.z, q.w) : q8_bytes_to_bf16(q.x, q.y);
+                }
+                const int bl = gl * GB + u;  // block index within the chunk
+                const float4 t4 = *reinterpret_cast<const float4*>(&lds_as[bl][rq]);
+                const vk_f32x4 cin = {OFFSET * t4.x, OFFSET * t4.y, OFFSET * t4.z, OFFSET * t4.w};
+                const vk_f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(vk_bf16x8, af[j][u]), bf, cin, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) lds_p[bl][(rq + r) * 16 + (lane & 15)] = p[r];
+                if (lane < 16) lds_dw[bl][lane] = vk_f16_to_f32_hw(sc_bits[u]);
+            }
+        }
+        VK_LDS_BARRIER();
+        // ---- phase 2: ordered combine, one thread per output
+        const int row = tid >> 4, col = tid & 15;
+        // gn*GB is a multiple of 4: the reads of 4 blocks are issued together
+        // ahead of the dependent fmaf chain
+        for (int bl = 0; bl < gn * GB; bl += 4) {
+            float p[4], sd[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                p[u] = lds_p[bl + u][tid];
+                sd[u] = POW2 ? lds_dw[bl + u][col] : lds_sa[bl + u][row] * lds_dw[bl + u][col];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc = fmaf(sd[u], p[u], acc);
+        }
+        VK_LDS_BARRIER();
+    }
+    const int row = mt * 16 + (tid >> 4), col = nt * 16 + (tid & 15);
+    if (row < m && col < n) out[(size_t)row * n + col] = bias ? acc + bias[col] : acc;
+}
+
+}  // namespace vk
+
+#include "vk_launch.h"
+
+namespace vk {
+
+hipError_t launch_repack_w_gemv(hipStream_t s, int mode, const uint8_t* wq, int n, int n_pad, int nb, uint4* wq4,
+                                uint2* wsc) {
+    const size_t threads = (size_t)n_pad * (nb / gemv::GB) * 4;
+    if (threads == 0) return hipSuccess;
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    hipLaunchKernelGGL(vk_repack_w_gemv, dim3(grid), dim3(256), 0, s, mode, wq, n, n_pad, nb, wq4, wsc);
+    return hipGetLastError();
+}
+
+template <int MODE, bool POW2>
+static hipError_t go(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum, const uint4* wq4,
+                     const uint2* wsc, const float* bias, float* out, int m, int n, int nb, int m_pad) {
+    const int n_tiles = (n + 15) / 16, m_tiles = (m + 15) / 16;
+    hipLaunchKernelGGL((vk_gemv_qblock<MODE, POW2>), dim3(n_tiles, m_tiles), dim3(256), 0, s, afrag, ascale, asum,
+                       wq4, wsc, bias, out, m, n, nb, m_pad, n_tiles);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_qblock(hipStream_t s, int mode, bool pow2, const uint4* afrag, const float* ascale,
+                              const float* asum, const uint4* wq4, const uint2* wsc, const float* bias, float* out,
+                              int m, int n, int nb, int m_pad) {
+    if (mode == 1)
+        return pow2 ? go<1, true>(s, afrag, ascale, asum, wq4, wsc, bias, out, m, n, nb, m_pad)
+                    : go<1, false>(s, afrag, ascale, asum, wq4, wsc, bias, out, m, n, nb, m_pad);
+    return pow2 ? go<3, true>(s, afrag, ascale, asum, wq4, wsc, bias, out, m, n, nb, m_pad)
+                : go<3, false>(s, afrag, ascale, asum, wq4, wsc, bias, out, m, n, nb, m_pad);
+}
+
+}  // namespace vk

@@ -15,10 +15,18 @@ hipError_t launch_copy_u4(hipStream_t s, const void* src, void* dst, size_t n16)
 hipError_t launch_dequant_gemv_f32(hipStream_t s, int mode, const uint8_t* bytes, int n_rows, int n_bpr,
                                    const float* x, float* y);
 hipError_t launch_quantize_act_b32(hipStream_t s, bool pow2, const float* a, int m, int m_pad, int k,
-                                   uint4* afrag, float* ascale, int* agsum);
+                                   uint4* afrag, float* ascale, float* asum);
 hipError_t launch_repack_w_b32(hipStream_t s, int mode, const uint8_t* wq, int n, int n_pad, int nb,
                                uint4* wfrag, float* wscale);
 hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
                               const uint4* wfrag, const float* wscale, const float* bias, float* out, int m,
                               int m_pad, int n, int n_pad, int nb);
+}  // namespace vk
+
+namespace vk {
+hipError_t launch_repack_w_gemv(hipStream_t s, int mode, const uint8_t* wq, int n, int n_pad, int nb, uint4* wq4,
+                                uint2* wsc);
+hipError_t launch_gemv_qblock(hipStream_t s, int mode, bool pow2, const uint4* afrag, const float* ascale,
+                              const float* asum, const uint4* wq4, const uint2* wsc, const float* bias, float* out,
+                              int m, int n, int nb, int m_pad);
 }  // namespace vk

@@ -162,7 +162,7 @@ __global__ void vk_dequant_gemv_f32(int mode, const uint8_t* __restrict__ bytes,
 template <bool POW2>
 __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pad, int k,
                                     uint4* __restrict__ afrag, float* __restrict__ ascale,
-                                    int* __restrict__ agsum) {
+                                    float* __restrict__ asum) {
     const int nb = k >> 5;
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const size_t total = (size_t)m_pad * nb * 4;
@@ -221,9 +221,12 @@ __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pa
     const int mt = row >> 4, mr = row & 15;
     const size_t frag = (size_t)mt * nb + b;
     afrag[frag * 64 + (size_t)(mr + 16 * c)] = make_uint4(w[0], w[1], w[2], w[3]);
-    if (c == 0) {  // scales and sums are block-major: [nb][m_pad]
+    if (c == 0) {  // scales and operand sums are block-major: [nb][m_pad]
         ascale[(size_t)b * m_pad + row] = s;
-        agsum[(size_t)b * m_pad + row] = gs;
+        // sum of the A operand values of this block (exact: an integer times
+        // a power of two), used to remove the weight-side offsets of the
+        // decode kernel
+        asum[(size_t)b * m_pad + row] = POW2 ? (float)gs * s : (float)gs;
     }
 }
 
@@ -281,9 +284,6 @@ constexpr int MT = TM / 16, NT = TN / 16;  // fragment tiles per workgroup tile
 constexpr int FRAG_U4 = 64;                // uint4 per 16x32 fragment (1 KiB)
 constexpr int N_XCD = 8;
 }  // namespace gemm
-
-// LDS writes of this wave are complete, then all waves meet.
-#define VK_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 
 struct vk_stage_regs {
     uint4 a0, a1, b0;
@@ -432,8 +432,8 @@ __global__ __launch_bounds__(512, 1) void vk_gemm_qblock(
     }
 }
 
-template __global__ void vk_quantize_act_b32<false>(const float*, int, int, int, uint4*, float*, int*);
-template __global__ void vk_quantize_act_b32<true>(const float*, int, int, int, uint4*, float*, int*);
+template __global__ void vk_quantize_act_b32<false>(const float*, int, int, int, uint4*, float*, float*);
+template __global__ void vk_quantize_act_b32<true>(const float*, int, int, int, uint4*, float*, float*);
 template __global__ void vk_gemm_qblock<false>(const uint4*, const float*, const uint4*, const float*,
                                                const float*, float*, int, int, int, int, int, int);
 template __global__ void vk_gemm_qblock<true>(const uint4*, const float*, const uint4*, const float*,
@@ -485,16 +485,16 @@ hipError_t launch_dequant_gemv_f32(hipStream_t s, int mode, const uint8_t* bytes
 }
 
 hipError_t launch_quantize_act_b32(hipStream_t s, bool pow2, const float* a, int m, int m_pad, int k,
-                                   uint4* afrag, float* ascale, int* agsum) {
+                                   uint4* afrag, float* ascale, float* asum) {
     const size_t threads = (size_t)m_pad * (k / 32) * 4;
     if (threads == 0) return hipSuccess;
     const unsigned grid = (unsigned)((threads + 255) / 256);
     if (pow2)
         hipLaunchKernelGGL(vk_quantize_act_b32<true>, dim3(grid), dim3(256), 0, s, a, m, m_pad, k, afrag,
-                           ascale, agsum);
+                           ascale, asum);
     else
         hipLaunchKernelGGL(vk_quantize_act_b32<false>, dim3(grid), dim3(256), 0, s, a, m, m_pad, k, afrag,
-                           ascale, agsum);
+                           ascale, asum);
     return hipGetLastError();
 }
 

@@ -93,11 +93,17 @@ def _declare(L):
     L.vokra_hip_dequant_gemv_f32.argtypes = [P, C.c_int, u8p, sz, sz, sz, f32p, sz, f32p]
     L.vokra_hip_gemm_q_f32.argtypes = [P, C.c_int, sz, sz, sz, f32p, sz, u8p, sz, f32p, f32p, sz]
     L.vokra_hip_set_act_quant.argtypes = [P, C.c_int]
+    L.vokra_hip_set_decode_kernel.argtypes = [P, C.c_int]
     L.vokra_hip_qweight_upload.argtypes = [P, C.c_int, sz, sz, u8p, sz, C.POINTER(P)]
     L.vokra_hip_qweight_free.argtypes = [P]
     L.vokra_hip_qweight_free.restype = None
     L.vokra_hip_gemm_q_f32_dev.argtypes = [P, P, sz, P, P, P, C.c_int]
     L.vokra_hip_copy_dev.argtypes = [P, P, P, sz]
+    L.vokra_hip_capture_begin.argtypes = [P]
+    L.vokra_hip_capture_end.argtypes = [P, C.POINTER(P)]
+    L.vokra_hip_graph_launch.argtypes = [P, P]
+    L.vokra_hip_graph_destroy.argtypes = [P]
+    L.vokra_hip_graph_destroy.restype = None
     L.vokra_hip_quantize_bytes.argtypes = [P, C.c_int, f32p, sz, u8p, sz]
     L.vokra_hip_quantize_bytes_dev.argtypes = [P, C.c_int, P, sz, P]
     L.vokra_hip_qact_create.argtypes = [P, sz, sz, C.POINTER(P)]
@@ -234,6 +240,23 @@ class QWeight:
             pass
 
 
+class Graph:
+    """A captured sequence of device calls, replayed with one launch."""
+
+    def __init__(self, ctx: "HipContext", handle):
+        self.ctx, self._h = ctx, handle
+
+    def launch(self):
+        _check(lib().vokra_hip_graph_launch(self.ctx._h, self._h))
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None):
+                lib().vokra_hip_graph_destroy(self._h)
+        except Exception:
+            pass
+
+
 class QAct:
     """Device-resident INT8-quantized activations (quantize once, many GEMMs)."""
 
@@ -280,6 +303,17 @@ class HipContext:
     def copy_dev(self, d_dst: "DeviceBuffer", d_src: "DeviceBuffer", nbytes: int):
         _check(lib().vokra_hip_copy_dev(self._h, d_dst.ptr, d_src.ptr, nbytes))
 
+    def capture(self, fn) -> Graph:
+        """Records the device calls `fn()` makes on this context into a graph."""
+        _check(lib().vokra_hip_capture_begin(self._h))
+        try:
+            fn()
+        finally:
+            g = C.c_void_p()
+            code = lib().vokra_hip_capture_end(self._h, C.byref(g))
+        _check(code)
+        return Graph(self, g)
+
     # ---- kv_quant surface ------------------------------------------------
     def dequantize_bytes(self, mode: KvQuant, data) -> np.ndarray:
         """kv_quant::dequantize_bytes (kv_quant/mod.rs:307-319) on the device."""
@@ -320,6 +354,9 @@ class HipContext:
     # ---- quantized linear -------------------------------------------------
     def set_act_quant(self, act: ActQuant):
         _check(lib().vokra_hip_set_act_quant(self._h, int(act)))
+
+    def set_decode_kernel(self, enable: bool):
+        _check(lib().vokra_hip_set_decode_kernel(self._h, int(bool(enable))))
 
     def gemm_q_f32(self, m: int, n: int, k: int, a, wq, dtype: WDtype, bias=None, out=None):
         """Compute::gemm_q_f32 (compute.rs:943-963): out[m, n] = a[m, k] . dequant(wq[n, k])^T."""
