@@ -56,14 +56,18 @@ typedef enum vokra_hip_wdtype_t {
     VOKRA_HIP_W_Q4_K = 12
 } vokra_hip_wdtype_t;
 
-/* Activation quantization convention of the block-format INT8 GEMM.
+/* Activation quantization convention of the INT8 matmul.
  * AMAX127: per 32-element block s = amax/127, q = clamp(round(v/s), +-127)
  *          (the K-quant convention of kquant.rs:418-441 at group 32).
  * POW2:    per 32-element block s = smallest power of two >= amax/127
- *          (shared-exponent int8, as in the OCP MXINT8 format). */
+ *          (shared-exponent int8, as in the OCP MXINT8 format).
+ * KQUANT:  per 16-element group exactly kquant.rs:418-441 (s = amax/127,
+ *          q = clamp(round(v/s), +-127), plus the group sum); the only
+ *          convention of Q4_K weights, which always use it. */
 typedef enum vokra_hip_act_quant_t {
     VOKRA_HIP_ACT_AMAX127 = 0,
-    VOKRA_HIP_ACT_POW2 = 1
+    VOKRA_HIP_ACT_POW2 = 1,
+    VOKRA_HIP_ACT_KQUANT = 2
 } vokra_hip_act_quant_t;
 
 typedef struct vokra_hip_ctx vokra_hip_ctx_t;
@@ -120,6 +124,14 @@ void vokra_hip_graph_destroy(vokra_hip_graph_t *g);
 int vokra_hip_dequantize_bytes(vokra_hip_ctx_t *ctx, int mode, const uint8_t *bytes, size_t n_bytes,
                                float *out, size_t out_len);
 
+/* Q4_K super-blocks -> f32, bit-exact (y = d*sc*q - dmin*m, two roundings).
+ * Replaces gguf::quant::dequantize for GgmlType::Q4K
+ * (crates/vokra-core/src/gguf/quant/mod.rs:42-63 -> gguf/quant/q4_k.rs:34-69):
+ * n_elements must be a multiple of 256 and n_bytes = n_elements/256 * 144
+ * (a mismatch is INVALID_ARGUMENT, the reference's TensorSizeMismatch). */
+int vokra_hip_kquant_dequantize(vokra_hip_ctx_t *ctx, int wdtype, const uint8_t *bytes, size_t n_bytes,
+                                size_t n_elements, float *out);
+
 /* f32 -> wire Q4_0/Q5_0/Q8_0 blocks, bit-exact with the reference packers
  * (BlockQ8_0::pack q8_0.rs:40-64, BlockQ4_0::pack q4_0.rs:44-68,
  * BlockQ5_0::pack) as driven by pack_matrix_to_bytes
@@ -145,7 +157,9 @@ int vokra_hip_dequant_gemv_f32(vokra_hip_ctx_t *ctx, int mode, const uint8_t *bl
  * -> kernels::gemm_q_f32 (crates/vokra-backend-cpu/src/kernels/mod.rs:341-364)
  * -> gemm_driver::run_q (gemm_driver.rs:312-332): wq is the untransposed
  * [n, k] payload, a is [m, k], out is [m, n], bias is added after. Block
- * formats use the context's activation convention (default AMAX127). */
+ * formats use the context's activation convention (default AMAX127); Q4_K
+ * runs kquant_gemm_i8 (kquant.rs:845-935): k a multiple of 256, KQUANT
+ * activations, bit-identical outputs. */
 int vokra_hip_gemm_q_f32(vokra_hip_ctx_t *ctx, int wdtype, size_t m, size_t n, size_t k, const float *a,
                          size_t a_len, const uint8_t *wq, size_t wq_len, const float *bias, float *out,
                          size_t out_len);
@@ -166,7 +180,9 @@ int vokra_hip_qweight_upload(vokra_hip_ctx_t *ctx, int wdtype, size_t n, size_t 
 void vokra_hip_qweight_free(vokra_hip_qweight_t *w);
 
 /* gemm_q_f32 on device pointers against a resident weight (async on the
- * context stream). d_a: [m, k] f32, d_bias: [n] or NULL, d_out: [m, n]. */
+ * context stream). d_a: [m, k] f32 (16-byte aligned), d_bias: [n] or NULL,
+ * d_out: [m, n]. act_quant selects the block-format convention; Q4_K
+ * weights ignore it and use KQUANT. */
 int vokra_hip_gemm_q_f32_dev(vokra_hip_ctx_t *ctx, const vokra_hip_qweight_t *w, size_t m,
                              const float *d_a, const float *d_bias, float *d_out, int act_quant);
 
@@ -179,6 +195,8 @@ int vokra_hip_qact_create(vokra_hip_ctx_t *ctx, size_t max_m, size_t k, vokra_hi
 void vokra_hip_qact_free(vokra_hip_qact_t *qa);
 int vokra_hip_qact_quantize_dev(vokra_hip_ctx_t *ctx, vokra_hip_qact_t *qa, size_t m, const float *d_a,
                                 int act_quant);
+/* The weight and the activations must agree: Q4_K weights take KQUANT
+ * activations (k a multiple of 256), block formats AMAX127 or POW2. */
 int vokra_hip_gemm_qact_dev(vokra_hip_ctx_t *ctx, const vokra_hip_qweight_t *w, const vokra_hip_qact_t *qa,
                             const float *d_bias, float *d_out);
 

@@ -117,7 +117,8 @@ struct vokra_hip_qweight {
     size_t n = 0, k = 0, n_pad = 0, nb = 0;
     DevBuf frag, scale;  // MFMA-fragment bf16 integers + f32 scales (prefill GEMM)
     bool has_gemv = false;
-    DevBuf gq, gsc;      // compact decode layout (Q4_0 / Q8_0, k % 128 == 0)
+    DevBuf gq, gsc;      // compact decode layout (Q4_0 / Q8_0, k % 128 == 0); Q4_K: nibble words + (d, m)
+    bool kquant = false; // Q4_K: one matmul kernel for every m
 };
 
 // Largest activation count routed to the decode kernel.
@@ -136,12 +137,14 @@ namespace {
 
 hipError_t set_dev(const vokra_hip_ctx* c) { return hipSetDevice(c->device); }
 
+// Sized for every convention: bf16 fragments of m_pad x k, one scale and one
+// sum per 16 elements (block formats use half of it).
 int qact_reserve(vokra_hip_qact* qa, size_t m, size_t k) {
     const size_t m_pad = round_up(m, vk::GEMM_TM);
-    const size_t nb = k / 32;
+    const size_t ng = k / 16;
     VK_TRY(qa->frag.ensure(m_pad * k * 2), "hipMalloc(activation fragments)");
-    VK_TRY(qa->scale.ensure(m_pad * nb * sizeof(float)), "hipMalloc(activation scales)");
-    VK_TRY(qa->gsum.ensure(m_pad * nb * sizeof(int)), "hipMalloc(activation sums)");
+    VK_TRY(qa->scale.ensure(m_pad * ng * sizeof(float)), "hipMalloc(activation scales)");
+    VK_TRY(qa->gsum.ensure(m_pad * ng * sizeof(float)), "hipMalloc(activation sums)");
     return VOKRA_HIP_OK;
 }
 
@@ -151,6 +154,22 @@ int quantize_activations(vokra_hip_ctx* c, vokra_hip_qact* qa, const float* d_a,
     if (qa->growable) {
         int st = qact_reserve(qa, m, k);
         if (st) return st;
+    }
+    if (act_quant == VOKRA_HIP_ACT_KQUANT) {
+        if (k % 256 != 0)
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                        "K-quant INT8 GEMV needs k to be a positive multiple of 256, got %zu", k);
+        if (reinterpret_cast<uintptr_t>(d_a) % 16 != 0)
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "activations must be 16-byte aligned");
+        const size_t m_pad = round_up(m, 16);
+        VK_TRY(vk::launch_quantize_act_g16(c->stream, d_a, (int)m, (int)m_pad, (int)k, (uint4*)qa->frag.p,
+                                           (float*)qa->scale.p, (float*)qa->gsum.p),
+               "launch(vk_quantize_act_g16)");
+        qa->m = m;
+        qa->k = k;
+        qa->m_pad = m_pad;
+        qa->act_quant = act_quant;
+        return VOKRA_HIP_OK;
     }
     const size_t m_pad = round_up(m, vk::GEMM_TM);
     VK_TRY(vk::launch_quantize_act_b32(c->stream, act_quant == VOKRA_HIP_ACT_POW2, d_a, (int)m, (int)m_pad,
@@ -165,11 +184,22 @@ int quantize_activations(vokra_hip_ctx* c, vokra_hip_qact* qa, const float* d_a,
 
 int check_block_shapes(int wdtype, size_t n, size_t k, size_t wq_len) {
     const int mode = wd_kv_mode(wdtype);
-    if (mode == 0) {
-        if (wdtype == VOKRA_HIP_W_Q4_K)
-            return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "gemm_q_f32: Q4_K is not wired on this arm yet");
-        return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "gemm_q_f32: unsupported weight dtype %d", wdtype);
+    if (wdtype == VOKRA_HIP_W_Q4_K) {
+        // validate_gemv_i8 (crates/vokra-backend-cpu/src/kernels/kquant.rs:545-578)
+        if (k == 0 || k % 256 != 0)
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                        "K-quant INT8 GEMV needs k to be a positive multiple of 256, got %zu", k);
+        size_t want;
+        if (!mul_ok(n, (k / 256) * 144, &want))
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "K-quant weight byte-length overflow");
+        if (wq_len != want)
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "K-quant weight payload is %zu bytes, want %zu (m=%zu rows x %zu)",
+                        wq_len, want, n, (k / 256) * 144);
+        if (n > (size_t)INT32_MAX / 2 || k > (size_t)INT32_MAX)
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32: dimension exceeds int32");
+        return VOKRA_HIP_OK;
     }
+    if (mode == 0) return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "gemm_q_f32: unsupported weight dtype %d", wdtype);
     if (k == 0 || k % 32 != 0)
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
                     "gemm_q_f32 needs k to be a positive multiple of 32, got %zu", k);
@@ -190,6 +220,18 @@ int upload_weight(vokra_hip_ctx* c, int wdtype, size_t n, size_t k, const uint8_
     w->wdtype = wdtype;
     w->n = n;
     w->k = k;
+    if (wdtype == VOKRA_HIP_W_Q4_K) {
+        const size_t nsb = k / 256;
+        w->kquant = true;
+        w->nb = nsb;
+        w->n_pad = round_up(n ? n : 1, 16);
+        VK_TRY(w->gq.ensure(w->n_pad * nsb * 128), "hipMalloc(Q4_K nibble words)");
+        VK_TRY(w->gsc.ensure(w->n_pad * nsb * 8 * sizeof(float) * 2), "hipMalloc(Q4_K scales)");
+        VK_TRY(vk::launch_repack_w_q4k(c->stream, d_wq, (int)n, (int)w->n_pad, (int)nsb, (uint4*)w->gq.p,
+                                       (float2*)w->gsc.p),
+               "launch(vk_repack_w_q4k)");
+        return VOKRA_HIP_OK;
+    }
     w->nb = k / 32;
     w->n_pad = round_up(n ? n : 1, vk::GEMM_TN);
     VK_TRY(w->frag.ensure(w->n_pad * k * 2), "hipMalloc(weight fragments)");
@@ -219,6 +261,17 @@ void release_weight(vokra_hip_qweight* w) {
 
 int run_gemm_qact(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_qact* qa, const float* d_bias,
                  float* d_out) {
+    if (w->kquant) {
+        if (qa->act_quant != VOKRA_HIP_ACT_KQUANT)
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: Q4_K weights need KQUANT activations");
+        VK_TRY(vk::launch_gemm_q4k(c->stream, (const uint4*)qa->frag.p, (const float*)qa->scale.p,
+                                   (const float*)qa->gsum.p, (const uint4*)w->gq.p, (const float2*)w->gsc.p, d_bias,
+                                   d_out, (int)qa->m, (int)w->n, (int)w->nb, (int)qa->m_pad),
+               "launch(vk_gemm_q4k)");
+        return VOKRA_HIP_OK;
+    }
+    if (qa->act_quant == VOKRA_HIP_ACT_KQUANT)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: block-format weights need AMAX127 or POW2 activations");
     // Both kernels produce bit-identical outputs; the decode kernel streams
     // the compact weights once, the GEMM reuses bf16 tiles across many rows.
     if (w->has_gemv && qa->m <= kGemvMaxM && c->decode_kernel) {
@@ -239,7 +292,7 @@ int run_gemm_qact(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_
 
 int run_gemm(vokra_hip_ctx* c, const vokra_hip_qweight* w, size_t m, const float* d_a, const float* d_bias,
              float* d_out, int act_quant) {
-    int st = quantize_activations(c, &c->act, d_a, m, w->k, act_quant);
+    int st = quantize_activations(c, &c->act, d_a, m, w->k, w->kquant ? VOKRA_HIP_ACT_KQUANT : act_quant);
     if (st) return st;
     return run_gemm_qact(c, w, &c->act, d_bias, d_out);
 }
@@ -395,6 +448,33 @@ int vokra_hip_dequantize_bytes(vokra_hip_ctx_t* c, int mode, const uint8_t* byte
     return VOKRA_HIP_OK;
 }
 
+int vokra_hip_kquant_dequantize(vokra_hip_ctx_t* c, int wdtype, const uint8_t* bytes, size_t n_bytes,
+                                size_t n_elements, float* out) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kquant_dequantize: ctx is NULL");
+    if (wdtype != VOKRA_HIP_W_Q4_K)
+        return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "kquant_dequantize: dtype %d is not wired on this arm", wdtype);
+    // GgmlType::payload_size + TensorSizeMismatch (gguf/quant/mod.rs:42-50)
+    if (n_elements % 256 != 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "Q4_K payload needs n_elements a multiple of 256, got %zu", n_elements);
+    const size_t nsb = n_elements / 256;
+    if (n_bytes != nsb * 144)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "tensor <dequant 12>: expected %zu bytes, got %zu", nsb * 144,
+                    n_bytes);
+    if (nsb == 0) return VOKRA_HIP_OK;
+    if (!bytes || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kquant_dequantize: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(c->in0.ensure(n_bytes), "hipMalloc");
+    VK_TRY(c->out0.ensure(n_elements * sizeof(float)), "hipMalloc");
+    VK_TRY(hipMemcpyAsync(c->in0.p, bytes, n_bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+    VK_TRY(vk::launch_dequantize_q4k(c->stream, (const uint8_t*)c->in0.p, nsb, (float*)c->out0.p),
+           "launch(vk_dequantize_q4k)");
+    VK_TRY(hipMemcpyAsync(out, c->out0.p, n_elements * sizeof(float), hipMemcpyDeviceToHost, c->stream),
+           "hipMemcpyAsync(D2H)");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
+
 int vokra_hip_dequant_gemv_f32(vokra_hip_ctx_t* c, int mode, const uint8_t* blocks, size_t n_bytes,
                                size_t n_rows, size_t n_bpr, const float* x, size_t x_len, float* y) {
     if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "fused_dequant_gemv: ctx is NULL");
@@ -498,8 +578,10 @@ int vokra_hip_gemm_q_f32_dev(vokra_hip_ctx_t* c, const vokra_hip_qweight_t* w, s
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
                     "batched gemm_q_f32 needs at least one activation vector, got m = 0");
     if (m > (size_t)INT32_MAX / 2) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: m too large");
-    if (act_quant != VOKRA_HIP_ACT_AMAX127 && act_quant != VOKRA_HIP_ACT_POW2)
+    if (act_quant != VOKRA_HIP_ACT_AMAX127 && act_quant != VOKRA_HIP_ACT_POW2 && act_quant != VOKRA_HIP_ACT_KQUANT)
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: unknown activation convention %d", act_quant);
+    if (act_quant == VOKRA_HIP_ACT_KQUANT && !w->kquant)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: KQUANT activations need Q4_K weights");
     if (!d_a || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: NULL buffer");
     VK_TRY(set_dev(c), "hipSetDevice");
     return run_gemm(c, w, m, d_a, d_bias, d_out, act_quant);
@@ -670,7 +752,7 @@ int vokra_hip_qact_quantize_dev(vokra_hip_ctx_t* c, vokra_hip_qact_t* qa, size_t
     if (qa->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qact_quantize: qact belongs to another context");
     if (m == 0 || m > qa->max_m)
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qact_quantize: m=%zu outside 1..%zu", m, qa->max_m);
-    if (act_quant != VOKRA_HIP_ACT_AMAX127 && act_quant != VOKRA_HIP_ACT_POW2)
+    if (act_quant != VOKRA_HIP_ACT_AMAX127 && act_quant != VOKRA_HIP_ACT_POW2 && act_quant != VOKRA_HIP_ACT_KQUANT)
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qact_quantize: unknown activation convention %d", act_quant);
     VK_TRY(set_dev(c), "hipSetDevice");
     return quantize_activations(c, qa, d_a, m, qa->k, act_quant);

@@ -30,3 +30,14 @@ hipError_t launch_gemv_qblock(hipStream_t s, int mode, bool pow2, const uint4* a
                               const float* asum, const uint4* wq4, const uint2* wsc, const float* bias, float* out,
                               int m, int n, int nb, int m_pad);
 }  // namespace vk
+
+namespace vk {
+hipError_t launch_dequantize_q4k(hipStream_t s, const uint8_t* bytes, size_t nsb, float* out);
+hipError_t launch_quantize_act_g16(hipStream_t s, const float* a, int m, int m_pad, int k, uint4* afrag,
+                                   float* ascale, float* asum);
+hipError_t launch_repack_w_q4k(hipStream_t s, const uint8_t* wq, int n, int n_pad, int nsb, uint4* wq4,
+                               float2* wdm);
+hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum,
+                           const uint4* wq4, const float2* wdm, const float* bias, float* out, int m, int n, int nsb,
+                           int m_pad);
+}  // namespace vk

@@ -64,6 +64,7 @@ class WDtype(IntEnum):
 class ActQuant(IntEnum):
     AMAX127 = 0
     POW2 = 1
+    KQUANT = 2
 
 
 _lib = None
@@ -90,6 +91,7 @@ def _declare(L):
     L.vokra_hip_event_destroy.argtypes = [P]
     L.vokra_hip_event_destroy.restype = None
     L.vokra_hip_dequantize_bytes.argtypes = [P, C.c_int, u8p, sz, f32p, sz]
+    L.vokra_hip_kquant_dequantize.argtypes = [P, C.c_int, u8p, sz, sz, f32p]
     L.vokra_hip_dequant_gemv_f32.argtypes = [P, C.c_int, u8p, sz, sz, sz, f32p, sz, f32p]
     L.vokra_hip_gemm_q_f32.argtypes = [P, C.c_int, sz, sz, sz, f32p, sz, u8p, sz, f32p, f32p, sz]
     L.vokra_hip_set_act_quant.argtypes = [P, C.c_int]
@@ -324,6 +326,14 @@ class HipContext:
         _check(lib().vokra_hip_dequantize_bytes(self._h, int(mode), _ptr(b, C.c_uint8), b.size,
                                                 _ptr(out, C.c_float), n_out))
         return out[:n_out]
+
+    def kquant_dequantize(self, wdtype: WDtype, data, n_elements: int) -> np.ndarray:
+        """gguf::quant::dequantize (gguf/quant/mod.rs:42-63) for Q4_K on the device."""
+        b = _u8(data)
+        out = np.zeros(max(n_elements, 1), np.float32)
+        _check(lib().vokra_hip_kquant_dequantize(self._h, int(wdtype), _ptr(b, C.c_uint8), b.size, n_elements,
+                                                 _ptr(out, C.c_float)))
+        return out[:n_elements]
 
     def quantize_bytes(self, mode: KvQuant, x) -> np.ndarray:
         """pack_matrix_to_bytes (dequant_gemm.rs:137-186) on the device: f32 -> wire blocks."""
