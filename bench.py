@@ -109,6 +109,54 @@ def bench_q4_gemv(ctx, hip, n, k=1280, ms=(1, 8, 64), stream_bytes=600 << 20):
     return {"N": n, "K": k, "weight_copies": copies, **res}
 
 
+Q4K_LAYER = [("q", 2048, 2048), ("k", 256, 2048), ("v", 256, 2048), ("o", 2048, 2048),
+             ("gate", 5632, 2048), ("up", 5632, 2048), ("down", 2048, 5632)]
+
+
+def q4k_random_weight(rng, n, k):
+    """Random Q4_K payload with the f16 d / dmin high bytes pinned small
+    (as the reference's kquant_gemm_parity.rs:45-62 random_blocks)."""
+    b = rng.integers(0, 256, size=(n * (k // 256), 144), dtype=np.uint8)
+    b[:, 1] = 0x2C
+    b[:, 3] = 0x24
+    return b.reshape(-1)
+
+
+def bench_q4k_decode(ctx, hip, m=32, layers=24):
+    """Speech-LLM decode linears (config 4: d=2048, FFN 5632, 16/2 heads x 128)
+    at batch m through the K-quant INT8 path: all 7 linears of `layers`
+    distinct layers (24 x 24.8 MB = 594 MB > the 256 MB MALL) replayed as one
+    graph. GB/s counts Q4_K weight bytes n*(k/256)*144 plus f32 activations
+    and outputs per linear."""
+    rng = np.random.default_rng(4)
+    Ws = []
+    for _ in range(layers):
+        Ws.append([(name, n, k, ctx.upload_qweight(hip.WDtype.Q4_K, n, k, q4k_random_weight(rng, n, k)))
+                   for (name, n, k) in Q4K_LAYER])
+    qa = {}
+    for k in (2048, 5632):
+        a = rng.standard_normal((m, k), dtype=np.float32)
+        q = ctx.qact(m, k)
+        q.quantize(m, hip.DeviceBuffer.from_array(ctx, a), hip.ActQuant.KQUANT)
+        qa[k] = q
+    d_out = hip.DeviceBuffer(ctx, m * 5632 * 4)
+    graph = ctx.capture(lambda: [ctx.gemm_qact_dev(W, qa[k], d_out) for layer in Ws for (_, _, k, W) in layer])
+    graph.launch()
+    e0, e1 = hip.Event(ctx), hip.Event(ctx)
+    e0.record()
+    graph.launch()
+    e1.record()
+    us_layer = e0.elapsed_ms(e1) * 1e3 / layers
+    nbytes = sum(n * (k // 256) * 144 + m * k * 4 + m * n * 4 for (_, n, k) in Q4K_LAYER)
+    ops = sum(2 * m * n * k for (_, n, k) in Q4K_LAYER)
+    ctx.synchronize()
+    del Ws
+    return {"M": m, "layers": layers, "us_per_layer": round(us_layer, 3), "bytes_per_layer": nbytes,
+            "gbs": round(nbytes / (us_layer * 1e-6) / 1e9, 1),
+            "frac_hbm": round(nbytes / (us_layer * 1e-6) / 1e9 / PEAK["hbm_gbs"], 4),
+            "tops": round(ops / (us_layer * 1e-6) / 1e12, 2)}
+
+
 def bench_copy(ctx, hip, nbytes=1 << 30, reps=5):
     """Plain streaming copy of 1 GiB (4x the 256 MB MALL): the
     achievable-HBM reference and the rocprof byte-counter calibration kernel."""
@@ -171,6 +219,7 @@ def main():
     pow2_run = bench_q8_gemm(ctx, hip, args.steps, args.warmup, hip.ActQuant.POW2)
     copy_run = bench_copy(ctx, hip)
     gemv_runs = [bench_q4_gemv(ctx, hip, n) for n in (5120, 1280)]
+    q4k_run = bench_q4k_decode(ctx, hip)
 
     M, N, K = main_run["M"], main_run["N"], main_run["K"]
     achieved = main_run["gemm_tops"]
@@ -200,6 +249,7 @@ def main():
         "extra": {
             "hbm_copy_reference": copy_run,
             "q4_0_gemv_streamed": gemv_runs,
+            "q4_k_decode_layer_m32": q4k_run,
             "gemm_kernel_ms": round(main_run["gemm_ms"], 4),
             "gemm_frac_of_bf16_mfma_peak": round(achieved / PEAK["bf16_tflops"], 4),
             "pow2_act": {"tops": round(pow2_run["tops"], 2), "gemm_tops": round(pow2_run["gemm_tops"], 2),

@@ -24,7 +24,7 @@ namespace kq {
 constexpr int QK = 256;      // elements per super-block
 constexpr int BB = 144;      // bytes per super-block
 constexpr int NG = 16;       // 16-element groups per super-block
-constexpr int CS = 2;        // super-blocks per LDS chunk of the matmul
+constexpr int CS = 4;        // super-blocks per LDS chunk of the matmul (one per wave)
 constexpr int CG = CS * NG;  // groups per chunk
 }  // namespace kq
 
@@ -186,23 +186,34 @@ __device__ __forceinline__ vk_s16x4 q4k_operand(uint32_t w, int j0) {
 
 // ---------------------------------------------------------------------------
 // Matmul, one workgroup per 16 x 16 output tile (16 activation rows, 16
-// weight rows), K in chunks of CS super-blocks.
-// Phase 1: wave u takes half-super-block u of the chunk (8 groups): one
+// weight rows), K in chunks of CS super-blocks (CG = 64 groups).
+// Phase 1: wave w takes super-block w of the chunk (16 groups): one
 //   16x16x16 MFMA per group with accumulator input -128 * gsum (removing the
 //   +128 of the bf16 nibble trick) gives isum exactly; isum goes to LDS.
+//   Right after, the wave issues the global loads of the next chunk into
+//   registers, so they are in flight during the combine.
 // Phase 2: thread (row, col) runs the reference combine over the chunk's
-//   groups in order.
+//   groups in order; waves whose 4 rows are all padding skip it.
+namespace kq {
+struct Stage {
+    uint4 wv[2];     // nibble words of this wave's super-block
+    uint4 af[8];     // activation fragments of this wave's super-block
+    float sv[4], tv[4];  // chunk scales / group sums (4 per thread)
+    float2 dm[2];    // chunk (d_eff, m_eff) (2 per thread)
+};
+}  // namespace kq
+
 template <bool HAS_BIAS>
 __global__ __launch_bounds__(256) void vk_gemm_q4k(
     const uint4* __restrict__ afrag, const float* __restrict__ ascale, const float* __restrict__ asum,
     const uint4* __restrict__ wq4, const float2* __restrict__ wdm, const float* __restrict__ bias,
     float* __restrict__ out, int m, int n, int nsb, int m_pad) {
     using namespace kq;
-    __shared__ float lds_p[CG][256];                  // isum, [group][row * 16 + col]
-    __shared__ __align__(16) float lds_asg[CG][16];   // gsum, [group][row]   (phase 1)
-    __shared__ float4 lds_sa[16][CG / 4];     // s,    [row][group]   (phase 2)
-    __shared__ float4 lds_as[16][CG / 4];     // gsum, [row][group]   (phase 2)
-    __shared__ float4 lds_dm[16][CG / 4];     // (d_eff, m_eff) x 2 sub-blocks, [col][sub-block pair]
+    __shared__ __align__(16) float lds_p[CG][256];    // isum, [group][row * 16 + col]
+    // rows padded by one float4 against bank conflicts on the transposing stores
+    __shared__ float4 lds_sa[16][CG / 4 + 1];         // s,    [row][group]   (phase 2)
+    __shared__ float4 lds_as[16][CG / 4 + 1];         // gsum, [row][group]   (phase 2)
+    __shared__ float4 lds_dm[16][CG / 4 + 1];         // (d_eff, m_eff) x 2 sub-blocks, [col][pair]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nt = blockIdx.x, mt = blockIdx.y;
@@ -211,71 +222,106 @@ __global__ __launch_bounds__(256) void vk_gemm_q4k(
     float* sa_f = reinterpret_cast<float*>(lds_sa);
     float* as_f = reinterpret_cast<float*>(lds_as);
     float2* dm_f = reinterpret_cast<float2*>(lds_dm);
+    const bool rows_live = mt * 16 + 4 * wave < m;    // this wave's phase-2 rows
 
-    float acc = 0.0f;
-    for (int sb0 = 0; sb0 < nsb; sb0 += CS) {
-        const int gsb = min(CS, nsb - sb0);   // super-blocks in this chunk
-        // ---- phase 1 loads: this wave's half super-block (clamped in bounds)
-        const int sbl = min(wave >> 1, gsb - 1), half = wave & 1;
-        const int sb = sb0 + sbl;
-        const uint4 wv = wq4[(((size_t)nt * nsb + sb) * 64 + lane) * 2 + half];
-        uint4 af[4];
+    // Every load index is clamped into the chunk, so no load leaves its buffer.
+    auto load = [&](int sb0) -> Stage {
+        Stage st;
+        const int gsb = min(CS, nsb - sb0);
+        const int sb = sb0 + min(wave, gsb - 1);
 #pragma unroll
-        for (int p = 0; p < 4; ++p) af[p] = afrag[(((size_t)mt * nsb + sb) * 8 + half * 4 + p) * 64 + lane];
-        // ---- cooperative loads of the chunk's scales: 2 per thread
-        float sv[2], tv[2];
+        for (int h = 0; h < 2; ++h) st.wv[h] = wq4[(((size_t)nt * nsb + sb) * 64 + lane) * 2 + h];
+#pragma unroll
+        for (int p = 0; p < 8; ++p) st.af[p] = afrag[(((size_t)mt * nsb + sb) * 8 + p) * 64 + lane];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int idx = min(tid + 256 * h, gsb * 256 - 1);
+            const size_t o = (size_t)(sb0 * NG + (idx >> 4)) * m_pad + mt * 16 + (idx & 15);
+            st.sv[h] = ascale[o];
+            st.tv[h] = asum[o];
+        }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int idx = min(tid + 256 * h, gsb * NG * 16 - 1);
-            const int gl = idx >> 4, r = idx & 15;
-            const size_t o = (size_t)(sb0 * NG + gl) * m_pad + mt * 16 + r;
-            sv[h] = ascale[o];
-            tv[h] = asum[o];
+            const int idx = min(tid + 256 * h, gsb * 128 - 1);
+            st.dm[h] = wdm[(((size_t)nt * nsb + sb0) * 8 + (idx >> 4)) * 16 + (idx & 15)];
         }
-        const int dmi = min(tid, gsb * 8 * 16 - 1);  // (sub-block, col) of the chunk
-        const float2 dmv = wdm[(((size_t)nt * nsb + sb0) * 8 + (dmi >> 4)) * 16 + (dmi & 15)];
+        return st;
+    };
+
+    float acc = 0.0f;
+    Stage st = load(0);
+    for (int sb0 = 0; sb0 < nsb; sb0 += CS) {
+        const int gsb = min(CS, nsb - sb0);   // super-blocks in this chunk
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int idx = tid + 256 * h;
+            if (idx < gsb * 256) {
+                const int gl = idx >> 4, r = idx & 15;
+                sa_f[r * (CG + 4) + gl] = st.sv[h];
+                as_f[r * (CG + 4) + gl] = st.tv[h];
+            }
+        }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int idx = tid + 256 * h;
-            if (idx < gsb * NG * 16) {
-                const int gl = idx >> 4, r = idx & 15;
-                lds_asg[gl][r] = tv[h];
-                sa_f[r * CG + gl] = sv[h];
-                as_f[r * CG + gl] = tv[h];
-            }
+            if (idx < gsb * 128) dm_f[(idx & 15) * (CG / 2 + 2) + (idx >> 4)] = st.dm[h];
         }
-        if (tid < gsb * 8 * 16) dm_f[(tid & 15) * CG / 2 + (tid >> 4)] = dmv;
         VK_LDS_BARRIER();
-        // ---- phase 1 compute
-        if (wave >> 1 < gsb) {
-            const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+        // ---- phase 1: this wave's super-block
+        // (8 groups at a time: all LDS reads, then all MFMAs, then all writes,
+        // so the latencies overlap instead of adding up per group)
+        if (wave < gsb) {
 #pragma unroll
-            for (int gi = 0; gi < 8; ++gi) {
-                const int gl = sbl * NG + half * 8 + gi;  // group within the chunk
-                const uint2 ap = (gi & 1) ? make_uint2(af[gi >> 1].z, af[gi >> 1].w)
-                                          : make_uint2(af[gi >> 1].x, af[gi >> 1].y);
-                const vk_s16x4 b = q4k_operand(words[gi >> 1], 2 * (gi & 1));
-                const float4 t4 = *reinterpret_cast<const float4*>(&lds_asg[gl][rq]);
-                const vk_f32x4 cin = {-128.0f * t4.x, -128.0f * t4.y, -128.0f * t4.z, -128.0f * t4.w};
-                const vk_f32x4 p =
-                    __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(vk_s16x4, ap), b, cin, 0, 0, 0);
+            for (int half = 0; half < 2; ++half) {
+                const uint32_t words[4] = {st.wv[half].x, st.wv[half].y, st.wv[half].z, st.wv[half].w};
+                const int g0 = wave * NG + half * 8;
+                float t[8];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) lds_p[gl][(rq + r) * 16 + (lane & 15)] = p[r];
+                for (int gi = 0; gi < 8; ++gi) t[gi] = as_f[(lane & 15) * (CG + 4) + g0 + gi];
+                vk_f32x4 p[8];
+#pragma unroll
+                for (int gi = 0; gi < 8; ++gi) {
+                    const uint4 a4 = st.af[half * 4 + (gi >> 1)];
+                    const uint2 ap = (gi & 1) ? make_uint2(a4.z, a4.w) : make_uint2(a4.x, a4.y);
+                    const vk_s16x4 w = q4k_operand(words[gi >> 1], 2 * (gi & 1));
+                    const float c = -128.0f * t[gi];
+                    const vk_f32x4 cin = {c, c, c, c};
+                    // transposed product: weights as the A operand, so lane l
+                    // gets activation row l % 16, columns rq..rq+3
+                    p[gi] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(w, __builtin_bit_cast(vk_s16x4, ap), cin, 0, 0,
+                                                                      0);
+                }
+#pragma unroll
+                for (int gi = 0; gi < 8; ++gi)
+                    *reinterpret_cast<float4*>(&lds_p[g0 + gi][(lane & 15) * 16 + rq]) =
+                        make_float4(p[gi][0], p[gi][1], p[gi][2], p[gi][3]);
             }
         }
+        // ---- next chunk's loads (the last chunk reloads itself, unused)
+        st = load(sb0 + CS < nsb ? sb0 + CS : sb0);
         VK_LDS_BARRIER();
         // ---- phase 2: the reference combine, 4 groups (2 sub-blocks) per step
-        for (int q4 = 0; q4 < gsb * NG / 4; ++q4) {
-            const float4 s4 = lds_sa[row][q4];
-            const float4 a4 = lds_as[row][q4];
-            const float4 dm4 = lds_dm[col][q4];  // (d0, m0, d1, m1)
-            float p[4];
+        // (one super-block per step: its 28 LDS reads issue together)
+        if (rows_live) {
+            for (int sbl = 0; sbl < gsb; ++sbl) {
+                float4 s4[4], a4[4], dm4[4];  // dm4 = (d0, m0, d1, m1)
+                float p[16];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) p[u] = lds_p[4 * q4 + u][tid];
-            acc += s4.x * (dm4.x * p[0] - dm4.y * a4.x);
-            acc += s4.y * (dm4.x * p[1] - dm4.y * a4.y);
-            acc += s4.z * (dm4.z * p[2] - dm4.w * a4.z);
-            acc += s4.w * (dm4.z * p[3] - dm4.w * a4.w);
+                for (int u = 0; u < 4; ++u) {
+                    s4[u] = lds_sa[row][4 * sbl + u];
+                    a4[u] = lds_as[row][4 * sbl + u];
+                    dm4[u] = lds_dm[col][4 * sbl + u];
+                }
+#pragma unroll
+                for (int u = 0; u < 16; ++u) p[u] = lds_p[NG * sbl + u][tid];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    acc += s4[u].x * (dm4[u].x * p[4 * u] - dm4[u].y * a4[u].x);
+                    acc += s4[u].y * (dm4[u].x * p[4 * u + 1] - dm4[u].y * a4[u].y);
+                    acc += s4[u].z * (dm4[u].z * p[4 * u + 2] - dm4[u].w * a4[u].z);
+                    acc += s4[u].w * (dm4[u].z * p[4 * u + 3] - dm4[u].w * a4[u].w);
+                }
+            }
         }
         VK_LDS_BARRIER();
     }
