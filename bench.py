@@ -157,6 +157,33 @@ def bench_q4k_decode(ctx, hip, m=32, layers=24):
             "tops": round(ops / (us_layer * 1e-6) / 1e12, 2)}
 
 
+def bench_sdpa(ctx, hip, reps=20, T=1500, H=20, hd=64, batch=1):
+    """Config 1 fused self-attention: 20 heads x 64, 1500 x 1500, non-causal,
+    N(0,1) f32 q/k/v resident in HBM. Timed: the whole attn_f32_dev op (fp16
+    hi/lo split pre-passes + the flash kernel). flops = 4*B*H*T^2*hd."""
+    rng = np.random.default_rng(15)
+    d = [hip.DeviceBuffer.from_array(ctx, rng.standard_normal((batch, T, H * hd), dtype=np.float32))
+         for _ in range(3)]
+    d_out = hip.DeviceBuffer(ctx, batch * T * H * hd * 4)
+
+    def run():
+        ctx.attn_f32_dev(batch, T, T, H, H, hd, d[0], d[1], d[2], hd ** -0.5, False, 0, d_out)
+
+    run()
+    ctx.synchronize()
+    e0, e1 = hip.Event(ctx), hip.Event(ctx)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    ms = e0.elapsed_ms(e1) / reps
+    flops = 4.0 * batch * H * T * T * hd
+    return {"B": batch, "T": T, "H": H, "hd": hd, "ms": round(ms, 4),
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+            "frac_fp16_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK["bf16_tflops"], 4),
+            "mfma_passes_per_product": 3}
+
+
 def bench_copy(ctx, hip, nbytes=1 << 30, reps=5):
     """Plain streaming copy of 1 GiB (4x the 256 MB MALL): the
     achievable-HBM reference and the rocprof byte-counter calibration kernel."""
@@ -220,6 +247,7 @@ def main():
     copy_run = bench_copy(ctx, hip)
     gemv_runs = [bench_q4_gemv(ctx, hip, n) for n in (5120, 1280)]
     q4k_run = bench_q4k_decode(ctx, hip)
+    sdpa_run = bench_sdpa(ctx, hip)
 
     M, N, K = main_run["M"], main_run["N"], main_run["K"]
     achieved = main_run["gemm_tops"]
@@ -250,6 +278,7 @@ def main():
             "hbm_copy_reference": copy_run,
             "q4_0_gemv_streamed": gemv_runs,
             "q4_k_decode_layer_m32": q4k_run,
+            "sdpa_config1": sdpa_run,
             "gemm_kernel_ms": round(main_run["gemm_ms"], 4),
             "gemm_frac_of_bf16_mfma_peak": round(achieved / PEAK["bf16_tflops"], 4),
             "pow2_act": {"tops": round(pow2_run["tops"], 2), "gemm_tops": round(pow2_run["gemm_tops"], 2),

@@ -200,6 +200,33 @@ int vokra_hip_qact_quantize_dev(vokra_hip_ctx_t *ctx, vokra_hip_qact_t *qa, size
 int vokra_hip_gemm_qact_dev(vokra_hip_ctx_t *ctx, const vokra_hip_qweight_t *w, const vokra_hip_qact_t *qa,
                             const float *d_bias, float *d_out);
 
+/* ---- fused attention --------------------------------------------------- */
+
+/* Scaled-dot-product attention, f32 in and out, per batch b and query head h
+ * (kv head h / (n_head_q / n_head_kv)):
+ *   S = (q * scale) . k^T, -inf where causal and key j > q_offset + i,
+ *   P = softmax over keys, out = P . v.
+ * q and out are [batch, t_q, n_head_q * head_dim], k and v
+ * [batch, t_kv, n_head_kv * head_dim], row-major with heads side by side.
+ * Replaces the attention core of Compute::attn_f32
+ * (crates/vokra-models/src/compute.rs:2703-2742) as computed by
+ * attention_from_kv_into (crates/vokra-models/src/whisper/nn.rs:209-325; q is
+ * scaled before the product, scale = head_dim^-0.5 there) and the GQA loop of
+ * crates/vokra-models/src/voxtral/text_decoder.rs:1302-1360 (n_head_kv <
+ * n_head_q). The projections around it are gemm_q_f32 calls. head_dim is 64
+ * or 128 (else UNSUPPORTED_OP); t_kv = 0 gives zeros. Products run as fp16
+ * hi/lo split MFMAs (three per product, f32 accumulation): results agree with
+ * the f32 reference to about 1e-6 relative; inputs must be below 65504 in
+ * magnitude after scaling. */
+int vokra_hip_attn_f32(vokra_hip_ctx_t *ctx, size_t batch, size_t t_q, size_t t_kv, size_t n_head_q,
+                       size_t n_head_kv, size_t head_dim, const float *q, const float *k, const float *v,
+                       float scale, int causal, size_t q_offset, float *out);
+/* Same on device pointers (16-byte aligned q, k, out), async on the context
+ * stream; uses the context's attention workspace (grown on first use). */
+int vokra_hip_attn_f32_dev(vokra_hip_ctx_t *ctx, size_t batch, size_t t_q, size_t t_kv, size_t n_head_q,
+                           size_t n_head_kv, size_t head_dim, const float *d_q, const float *d_k,
+                           const float *d_v, float scale, int causal, size_t q_offset, float *d_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,159 @@
+"""GPU parity of the fused attention kernel (fp16 hi/lo split MFMAs, online
+softmax) through the C ABI.
+
+Bar (north-star f32 tolerance, per element): |gpu - ref| <= 1e-4 + 1e-3 * |ref|
+against the oracle's restatement of the reference loops (whisper nn.rs:209-325,
+voxtral text_decoder.rs:1302-1360) and, at the full config-1 shape, against a
+float64 numpy evaluation.
+"""
+import numpy as np
+import pytest
+
+from vokra_amd import hip
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-4, 1e-3
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = hip.HipContext(0)
+    yield c
+    c.close()
+
+
+def close(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    err = np.abs(got - want) - (ATOL + RTOL * np.abs(want))
+    return bool(np.all(err <= 0)), float(np.max(np.abs(got - want)))
+
+
+def sdpa_f64(q, k, v, n_head_q, n_head_kv, scale, causal=False, q_offset=0):
+    """float64 SDPA on [T, H*hd] rows (independent of the oracle)."""
+    tq, tkv = q.shape[0], k.shape[0]
+    hd = q.shape[1] // n_head_q
+    out = np.zeros((tq, n_head_q * hd))
+    for h in range(n_head_q):
+        hk = h // (n_head_q // n_head_kv)
+        qh = q[:, h * hd:(h + 1) * hd].astype(np.float64) * scale
+        kh = k[:, hk * hd:(hk + 1) * hd].astype(np.float64)
+        vh = v[:, hk * hd:(hk + 1) * hd].astype(np.float64)
+        s = qh @ kh.T
+        if causal:
+            s[np.arange(tq)[:, None] + q_offset < np.arange(tkv)[None, :]] = -np.inf
+        s -= s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=1, keepdims=True)
+        out[:, h * hd:(h + 1) * hd] = p @ vh
+    return out
+
+
+WHISPER_SHAPES = [(1, 1, 1, 64), (5, 7, 2, 64), (64, 64, 4, 64), (100, 130, 3, 64), (130, 65, 2, 128),
+                  (17, 300, 20, 64), (1, 1500, 4, 64)]
+
+
+@pytest.mark.parametrize("tq,tkv,H,hd", WHISPER_SHAPES)
+def test_whisper_attention_vs_oracle(ctx, oracle, tq, tkv, H, hd):
+    print(f"[case] whisper attn tq={tq} tkv={tkv} H={H} hd={hd}", flush=True)
+    g = np.random.default_rng(tq * 7 + tkv)
+    q = g.standard_normal((tq, H * hd)).astype(np.float32)
+    k = g.standard_normal((tkv, H * hd)).astype(np.float32)
+    v = g.standard_normal((tkv, H * hd)).astype(np.float32)
+    got = ctx.attn_f32(q, k, v, H)
+    want = oracle.sdpa_whisper(tq, tkv, H, hd, q, k, v)
+    ok, err = close(got, want)
+    assert ok, err
+
+
+@pytest.mark.parametrize("tq,tkv,off", [(7, 12, 5), (70, 70, 0), (1, 200, 199), (65, 130, 65)])
+def test_causal_with_offset_vs_oracle(ctx, oracle, tq, tkv, off):
+    print(f"[case] causal tq={tq} tkv={tkv} off={off}", flush=True)
+    H, hd = 4, 64
+    g = np.random.default_rng(tq + off)
+    q = g.standard_normal((tq, H * hd)).astype(np.float32)
+    k = g.standard_normal((tkv, H * hd)).astype(np.float32)
+    v = g.standard_normal((tkv, H * hd)).astype(np.float32)
+    got = ctx.attn_f32(q, k, v, H, causal=True, q_offset=off)
+    want = oracle.sdpa_whisper(tq, tkv, H, hd, q, k, v, causal=True, q_pos_offset=off)
+    ok, err = close(got, want)
+    assert ok, err
+
+
+@pytest.mark.parametrize("t,tkv,hq,hkv", [(1, 512, 16, 2), (5, 300, 16, 2), (3, 4096, 16, 2), (8, 64, 4, 4)])
+def test_gqa_vs_oracle(ctx, oracle, t, tkv, hq, hkv):
+    """GQA: kv head = h / (hq / hkv), causal at position_offset = tkv - t."""
+    print(f"[case] gqa t={t} tkv={tkv} hq={hq} hkv={hkv}", flush=True)
+    hd = 128
+    g = np.random.default_rng(t * 31 + tkv)
+    q = g.standard_normal((t, hq * hd)).astype(np.float32)
+    k = g.standard_normal((tkv, hkv * hd)).astype(np.float32)
+    v = g.standard_normal((tkv, hkv * hd)).astype(np.float32)
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    off = tkv - t
+    got = ctx.attn_f32(q, k, v, hq, hkv, scale=scale, causal=True, q_offset=off)
+    want = oracle.gqa_attention(t, tkv, hq, hkv, hd, q, k, v, scale, off)
+    ok, err = close(got, want)
+    assert ok, err
+
+
+def test_batch_equals_separate_calls(ctx):
+    print("[case] batch == separate", flush=True)
+    B, tq, tkv, H, hd = 3, 33, 90, 2, 64
+    g = np.random.default_rng(5)
+    q = g.standard_normal((B, tq, H * hd)).astype(np.float32)
+    k = g.standard_normal((B, tkv, H * hd)).astype(np.float32)
+    v = g.standard_normal((B, tkv, H * hd)).astype(np.float32)
+    full = ctx.attn_f32(q, k, v, H)
+    for b in range(B):
+        one = ctx.attn_f32(q[b], k[b], v[b], H)
+        assert np.array_equal(one, full[b])
+
+
+def test_uniform_keys_give_mean_of_values(ctx):
+    """Identical keys: softmax is uniform, so every output row is mean(v)."""
+    print("[case] uniform keys", flush=True)
+    tq, tkv, H, hd = 20, 77, 2, 64
+    g = np.random.default_rng(6)
+    q = g.standard_normal((tq, H * hd)).astype(np.float32)
+    k = np.tile(g.standard_normal((1, H * hd)).astype(np.float32), (tkv, 1))
+    v = g.standard_normal((tkv, H * hd)).astype(np.float32)
+    got = ctx.attn_f32(q, k, v, H)
+    want = np.tile(v.astype(np.float64).mean(axis=0), (tq, 1))
+    ok, err = close(got, want)
+    assert ok, err
+
+
+def test_empty_kv_gives_zeros(ctx):
+    q = np.ones((4, 128), np.float32)
+    got = ctx.attn_f32(q, np.zeros((0, 128), np.float32), np.zeros((0, 128), np.float32), 2)
+    assert np.array_equal(got, np.zeros_like(q))
+
+
+def test_config1_self_attention_full_shape(ctx):
+    """Config 1: 20 heads x 64, 1500 x 1500, non-causal, N(0,1) inputs; checked
+    against float64 on 3 heads (all queries)."""
+    print("[case] config1 full", flush=True)
+    T, H, hd = 1500, 20, 64
+    g = np.random.default_rng(1500)
+    q = g.standard_normal((T, H * hd)).astype(np.float32)
+    k = g.standard_normal((T, H * hd)).astype(np.float32)
+    v = g.standard_normal((T, H * hd)).astype(np.float32)
+    got = ctx.attn_f32(q, k, v, H)
+    assert np.all(np.isfinite(got))
+    for h in (0, 9, 19):
+        sl = slice(h * hd, (h + 1) * hd)
+        want = sdpa_f64(q[:, sl], k[:, sl], v[:, sl], 1, 1, hd ** -0.5)
+        ok, err = close(got[:, sl], want)
+        assert ok, (h, err)
+
+
+def test_attention_rejections(ctx):
+    q = np.zeros((2, 160), np.float32)
+    with pytest.raises(hip.UnsupportedOp):
+        ctx.attn_f32(q, q, q, 2)                       # head_dim 80
+    q = np.zeros((2, 3 * 64), np.float32)
+    k = np.zeros((2, 2 * 64), np.float32)
+    with pytest.raises(hip.InvalidArgument):
+        ctx.attn_f32(q, k, k, 3, 2)                    # 3 % 2 != 0

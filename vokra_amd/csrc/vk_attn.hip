@@ -1,0 +1,320 @@
+// vk_attn.hip — fused scaled-dot-product attention for gfx950.
+//
+// Semantics (f32): for every batch b, query head h (kv head h / (Hq / Hkv)),
+//   S = (q * scale) . k^T, masked to -inf for key j > q_off + i when causal,
+//   P = softmax_rows(S), O = P . v
+// which is crates/vokra-models/src/whisper/nn.rs:209-325 (q scaled before
+// the product, per-head S, causal mask, softmax, P.V) and, with Hkv < Hq,
+// the GQA loop of crates/vokra-models/src/voxtral/text_decoder.rs:1302-1360.
+//
+// Precision: every f32 operand x is split into two fp16 values x = hi + lo
+// (hi = fp16(x), lo = fp16(x - hi)) and each product runs as three MFMAs,
+// hi*hi + hi*lo + lo*hi, accumulated in f32: about 22 significant bits per
+// product, i.e. f32-level results, at 3x the fp16 MFMA rate. Inputs must stay
+// within the fp16 range (|x| < 65504 after scaling).
+//
+// Kernel shape: one workgroup per (64-query tile, head, batch); each of the 4
+// waves owns 16 queries. Both products are computed transposed,
+//   S^T = K . Q^T  (A = K tile from LDS, B = the wave's Q in registers)
+//   O^T = V^T . P^T (A = V^T tile from LDS, B = P from registers)
+// so every lane holds the scores, softmax statistics and output of one query
+// (lane % 16) and the softmax needs no transposes. K/V tiles of 64 keys are
+// staged through LDS, the next tile's loads in flight during the current one.
+#include <hip/hip_fp16.h>
+
+#include "vk_common.h"
+
+namespace vk {
+
+typedef _Float16 vk_h16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t vk_u32x4 __attribute__((ext_vector_type(4)));
+
+namespace attn {
+constexpr int QT = 64;   // queries per workgroup
+constexpr int KT = 64;   // keys per LDS tile
+constexpr int KPAD = 8;  // halves of row padding in the K tile
+constexpr int VPAD = 8;  // halves of row padding in the V^T tile
+}  // namespace attn
+
+__device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+// ---------------------------------------------------------------------------
+// Pre-pass: x [rows, cols] f32 -> hi / lo fp16 of x * scale (same layout).
+__global__ void vk_split_rows(const float* __restrict__ x, size_t n4, float scale, uint2* __restrict__ hi,
+                              uint2* __restrict__ lo) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    const float4 v = reinterpret_cast<const float4*>(x)[i];
+    const float a[4] = {v.x * scale, v.y * scale, v.z * scale, v.w * scale};
+    _Float16 h[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) split_f16(a[j], h[j], l[j]);
+    hi[i] = make_uint2(__builtin_bit_cast(uint16_t, h[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[1]) << 16),
+                       __builtin_bit_cast(uint16_t, h[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[3]) << 16));
+    lo[i] = make_uint2(__builtin_bit_cast(uint16_t, l[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, l[1]) << 16),
+                       __builtin_bit_cast(uint16_t, l[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, l[3]) << 16));
+}
+
+// Pre-pass: v [B][T][H*HD] f32 -> transposed hi / lo [B][H][HD][T_pad] fp16,
+// zero for t >= T. One workgroup per (64 x 64 tile of (t, c), head, batch).
+__global__ __launch_bounds__(256) void vk_split_vt(const float* __restrict__ v, int t_kv, int t_pad, int h_kv,
+                                                   int hd, uint16_t* __restrict__ vth, uint16_t* __restrict__ vtl) {
+    __shared__ float tile[64][65];
+    const int t0 = blockIdx.x * 64, c0 = (blockIdx.y % (hd / 64)) * 64, h = blockIdx.y / (hd / 64), b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const size_t width = (size_t)h_kv * hd;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = (tid >> 6) + 4 * i, c = tid & 63;
+        const int t = t0 + r;
+        tile[r][c] = t < t_kv ? v[((size_t)b * t_kv + t) * width + (size_t)h * hd + c0 + c] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int c = (tid >> 6) + 4 * i, r = tid & 63;
+        _Float16 hi, lo;
+        split_f16(tile[r][c], hi, lo);
+        const size_t o = (((size_t)b * h_kv + h) * hd + c0 + c) * t_pad + t0 + r;
+        vth[o] = __builtin_bit_cast(uint16_t, hi);
+        vtl[o] = __builtin_bit_cast(uint16_t, lo);
+    }
+}
+
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256) void vk_flash_attn(
+    const uint4* __restrict__ qh, const uint4* __restrict__ ql,    // [B][Tq][Hq*HD] fp16, scaled
+    const uint4* __restrict__ kh, const uint4* __restrict__ kl,    // [B][Tkv][Hkv*HD] fp16
+    const uint4* __restrict__ vth, const uint4* __restrict__ vtl,  // [B][Hkv][HD][Tpad] fp16
+    float* __restrict__ out, int tq, int tkv, int t_pad, int hq, int hkv, int causal, int q_off) {
+    using namespace attn;
+    constexpr int KS = HD / 32;      // 32-wide K steps of S = K . Q^T
+    constexpr int OS = HD / 16;      // 16-row output subtiles of O^T
+    constexpr int KROW = HD + KPAD;  // halves per K tile row
+    constexpr int VROW = KT + VPAD;  // halves per V^T tile row
+    constexpr int KU4 = KT * HD / 8 / 256;  // uint4 per thread per K array
+    constexpr int VU4 = HD * KT / 8 / 256;  // uint4 per thread per V^T array
+    __shared__ __align__(16) _Float16 lk[2][KT * KROW];   // K tile, hi / lo
+    __shared__ __align__(16) _Float16 lv[2][HD * VROW];   // V^T tile, hi / lo
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, lq = lane & 15;
+    const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int hk = h / (hq / hkv);
+    const int q_idx = qt * QT + wave * 16 + lq;  // this lane's query
+    const int q_ld = min(q_idx, tq - 1);
+    const size_t qw = (size_t)hq * HD / 8, kw = (size_t)hkv * HD / 8;  // row widths in uint4
+
+    // this lane's query operand (B of S^T = K . Q^T): hd 32ks + 8g .. +7
+    uint4 qa_h[KS], qa_l[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const size_t o = ((size_t)b * tq + q_ld) * qw + (size_t)h * HD / 8 + 4 * ks + g;
+        qa_h[ks] = qh[o];
+        qa_l[ks] = ql[o];
+    }
+
+    // keys this workgroup has to visit
+    int kv_end = tkv;
+    if (causal) kv_end = min(tkv, q_off + min(qt * QT + QT, tq));
+    const int n_tiles = (kv_end + KT - 1) / KT;
+
+    // staged loads of one K / V^T tile (indices clamped into the arrays)
+    // native vectors (not HIP's uint4 struct) so the stage stays in registers
+    struct Stage {
+        vk_u32x4 kh[KU4], kl[KU4], vh[VU4], vl[VU4];
+    };
+    const vk_u32x4* kh4 = reinterpret_cast<const vk_u32x4*>(kh);
+    const vk_u32x4* kl4 = reinterpret_cast<const vk_u32x4*>(kl);
+    const vk_u32x4* vh4 = reinterpret_cast<const vk_u32x4*>(vth);
+    const vk_u32x4* vl4 = reinterpret_cast<const vk_u32x4*>(vtl);
+    auto load = [&](int kt) __attribute__((always_inline)) -> Stage {
+        Stage st;
+#pragma unroll
+        for (int i = 0; i < KU4; ++i) {
+            const int idx = tid + 256 * i;
+            const int r = idx / (HD / 8), c = idx % (HD / 8);
+            const int t = min(kt * KT + r, tkv - 1);
+            const size_t o = ((size_t)b * tkv + t) * kw + (size_t)hk * HD / 8 + c;
+            st.kh[i] = kh4[o];
+            st.kl[i] = kl4[o];
+        }
+#pragma unroll
+        for (int i = 0; i < VU4; ++i) {
+            const int idx = tid + 256 * i;
+            const int r = idx / (KT / 8), c = idx % (KT / 8);
+            const size_t o = (((size_t)b * hkv + hk) * HD + r) * (t_pad / 8) + (size_t)kt * KT / 8 + c;
+            st.vh[i] = vh4[o];
+            st.vl[i] = vl4[o];
+        }
+        return st;
+    };
+
+    float* orow = out + ((size_t)b * tq + q_idx) * (size_t)hq * HD + (size_t)h * HD;
+    if (n_tiles == 0) {  // no keys: P . V over an empty set is zero
+        if (q_idx < tq)
+#pragma unroll
+            for (int os = 0; os < OS; ++os)
+                *reinterpret_cast<float4*>(orow + 16 * os + 4 * g) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        return;
+    }
+
+    vk_f32x4 o_acc[OS];
+#pragma unroll
+    for (int s = 0; s < OS; ++s) o_acc[s] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // unconditional (clamped) loads keep the stage in registers
+    Stage st = load(0);
+    for (int kt = 0; kt < n_tiles; ++kt) {
+        // ---- stage the tile into LDS
+#pragma unroll
+        for (int i = 0; i < KU4; ++i) {
+            const int idx = tid + 256 * i;
+            const int r = idx / (HD / 8), c = idx % (HD / 8);
+            *reinterpret_cast<vk_u32x4*>(&lk[0][r * KROW + 8 * c]) = st.kh[i];
+            *reinterpret_cast<vk_u32x4*>(&lk[1][r * KROW + 8 * c]) = st.kl[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VU4; ++i) {
+            const int idx = tid + 256 * i;
+            const int r = idx / (KT / 8), c = idx % (KT / 8);
+            *reinterpret_cast<vk_u32x4*>(&lv[0][r * VROW + 8 * c]) = st.vh[i];
+            *reinterpret_cast<vk_u32x4*>(&lv[1][r * VROW + 8 * c]) = st.vl[i];
+        }
+        VK_LDS_BARRIER();
+        st = load(min(kt + 1, n_tiles - 1));
+
+        // ---- S^T for 4 key subtiles of 16: lane holds keys 16n + 4g + r
+        vk_f32x4 s[4];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            s[n] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const int off = (16 * n + lq) * KROW + 32 * ks + 8 * g;
+                const vk_h16x8 ah = *reinterpret_cast<const vk_h16x8*>(&lk[0][off]);
+                const vk_h16x8 al = *reinterpret_cast<const vk_h16x8*>(&lk[1][off]);
+                const vk_h16x8 bh = __builtin_bit_cast(vk_h16x8, qa_h[ks]);
+                const vk_h16x8 bl = __builtin_bit_cast(vk_h16x8, qa_l[ks]);
+                s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, s[n], 0, 0, 0);
+                s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, s[n], 0, 0, 0);
+                s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, s[n], 0, 0, 0);
+            }
+        }
+        // ---- mask, online softmax (per query = per lane, across lanes g)
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = kt * KT + 16 * n + 4 * g + r;
+                const bool ok = key < tkv && (!causal || key <= q_off + q_idx);
+                s[n][r] = ok ? s[n][r] : -INFINITY;
+                mloc = fmaxf(mloc, s[n][r]);
+            }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, VK_WAVE));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, VK_WAVE));
+        const float m_new = fmaxf(m_run, mloc);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __expf(m_run - m_use);
+        float psum = 0.0f;
+        uint32_t ph[4][2], pl[4][2];  // P^T operand halves, [key subtile][pair]
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            _Float16 h4[4], l4[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = __expf(s[n][r] - m_use);
+                psum += p;
+                split_f16(p, h4[r], l4[r]);
+            }
+            ph[n][0] = __builtin_bit_cast(uint16_t, h4[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, h4[1]) << 16);
+            ph[n][1] = __builtin_bit_cast(uint16_t, h4[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, h4[3]) << 16);
+            pl[n][0] = __builtin_bit_cast(uint16_t, l4[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, l4[1]) << 16);
+            pl[n][1] = __builtin_bit_cast(uint16_t, l4[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, l4[3]) << 16);
+        }
+        psum += __shfl_xor(psum, 16, VK_WAVE);
+        psum += __shfl_xor(psum, 32, VK_WAVE);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int os = 0; os < OS; ++os)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o_acc[os][r] *= alpha;
+        // ---- O^T += V^T . P^T over 2 key steps of 32: MFMA k-index 8g + 4j + r
+        //      is key 32ks + 16j + 4g + r (the lane's P values, in order)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const vk_h16x8 bh = __builtin_bit_cast(
+                vk_h16x8, make_uint4(ph[2 * ks][0], ph[2 * ks][1], ph[2 * ks + 1][0], ph[2 * ks + 1][1]));
+            const vk_h16x8 bl = __builtin_bit_cast(
+                vk_h16x8, make_uint4(pl[2 * ks][0], pl[2 * ks][1], pl[2 * ks + 1][0], pl[2 * ks + 1][1]));
+#pragma unroll
+            for (int os = 0; os < OS; ++os) {
+                const int row = (16 * os + lq) * VROW;
+                const int k0 = 32 * ks + 4 * g;
+                const uint2 h0 = *reinterpret_cast<const uint2*>(&lv[0][row + k0]);
+                const uint2 h1 = *reinterpret_cast<const uint2*>(&lv[0][row + k0 + 16]);
+                const uint2 l0 = *reinterpret_cast<const uint2*>(&lv[1][row + k0]);
+                const uint2 l1 = *reinterpret_cast<const uint2*>(&lv[1][row + k0 + 16]);
+                const vk_h16x8 ah = __builtin_bit_cast(vk_h16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
+                const vk_h16x8 al = __builtin_bit_cast(vk_h16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
+                o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, o_acc[os], 0, 0, 0);
+                o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, o_acc[os], 0, 0, 0);
+                o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, o_acc[os], 0, 0, 0);
+            }
+        }
+        VK_LDS_BARRIER();
+    }
+    // ---- O = O^T / l: lane holds query lq, hd 16os + 4g + r
+    if (q_idx < tq) {
+        const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+#pragma unroll
+        for (int os = 0; os < OS; ++os)
+            *reinterpret_cast<float4*>(orow + 16 * os + 4 * g) =
+                make_float4(o_acc[os][0] * inv, o_acc[os][1] * inv, o_acc[os][2] * inv, o_acc[os][3] * inv);
+    }
+}
+
+}  // namespace vk
+
+#include "vk_launch.h"
+
+namespace vk {
+
+hipError_t launch_split_rows(hipStream_t s, const float* x, size_t n, float scale, void* hi, void* lo) {
+    const size_t n4 = n / 4;
+    if (n4 == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_split_rows, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, x, n4, scale, (uint2*)hi,
+                       (uint2*)lo);
+    return hipGetLastError();
+}
+
+hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, int t_pad, int h_kv, int hd, void* vth,
+                           void* vtl) {
+    if (batch == 0 || t_pad == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_split_vt, dim3(t_pad / 64, h_kv * (hd / 64), batch), dim3(256), 0, s, v, t_kv, t_pad, h_kv,
+                       hd, (uint16_t*)vth, (uint16_t*)vtl);
+    return hipGetLastError();
+}
+
+hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* ql, const void* kh, const void* kl,
+                             const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
+                             int hq, int hkv, int causal, int q_off) {
+    const dim3 grid((tq + attn::QT - 1) / attn::QT, hq, batch);
+    if (hd == 64)
+        hipLaunchKernelGGL(vk_flash_attn<64>, grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
+                           (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv,
+                           t_pad, hq, hkv, causal, q_off);
+    else
+        hipLaunchKernelGGL(vk_flash_attn<128>, grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
+                           (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv,
+                           t_pad, hq, hkv, causal, q_off);
+    return hipGetLastError();
+}
+
+}  // namespace vk

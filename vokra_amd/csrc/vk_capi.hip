@@ -109,6 +109,8 @@ struct vokra_hip_ctx {
     // Copy-mode staging and the context's own activation workspace.
     DevBuf in0, in1, in2, out0;
     vokra_hip_qact act;
+    // attention workspace: fp16 hi / lo splits of q, k and transposed v
+    DevBuf at_qh, at_ql, at_kh, at_kl, at_vh, at_vl;
 };
 
 struct vokra_hip_qweight {
@@ -297,9 +299,96 @@ int run_gemm(vokra_hip_ctx* c, const vokra_hip_qweight* w, size_t m, const float
     return run_gemm_qact(c, w, &c->act, d_bias, d_out);
 }
 
+// Shape checks of the attention entry points (no reference counterpart
+// rejects these: the reference's loops accept any shape; these are the
+// limits of the kernels).
+int check_attn(size_t batch, size_t tq, size_t tkv, size_t hq, size_t hkv, size_t hd) {
+    if (hd != 64 && hd != 128)
+        return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "attn_f32: head_dim %zu is not wired (64 or 128)", hd);
+    if (hq == 0 || hkv == 0 || hq % hkv != 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "attn_f32: n_head_q=%zu must be a positive multiple of n_head_kv=%zu", hq, hkv);
+    if (batch == 0 || batch > 65535 || hq > 65535)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn_f32: batch and n_head_q must be in 1..65535");
+    if (tq > (size_t)INT32_MAX / 2 || tkv > (size_t)INT32_MAX / 2)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn_f32: sequence length exceeds int32");
+    return VOKRA_HIP_OK;
+}
+
+int run_attn(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t hq, size_t hkv, size_t hd,
+             const float* d_q, const float* d_k, const float* d_v, float scale, int causal, size_t q_off,
+             float* d_out) {
+    const size_t t_pad = round_up(tkv, 64);
+    const size_t nq = batch * tq * hq * hd, nk = batch * tkv * hkv * hd, nv = batch * hkv * hd * t_pad;
+    VK_TRY(c->at_qh.ensure(nq * 2 + 16), "hipMalloc(attention q)");
+    VK_TRY(c->at_ql.ensure(nq * 2 + 16), "hipMalloc(attention q)");
+    VK_TRY(c->at_kh.ensure(nk * 2 + 16), "hipMalloc(attention k)");
+    VK_TRY(c->at_kl.ensure(nk * 2 + 16), "hipMalloc(attention k)");
+    VK_TRY(c->at_vh.ensure(nv * 2 + 16), "hipMalloc(attention v)");
+    VK_TRY(c->at_vl.ensure(nv * 2 + 16), "hipMalloc(attention v)");
+    VK_TRY(vk::launch_split_rows(c->stream, d_q, nq, scale, c->at_qh.p, c->at_ql.p), "launch(vk_split_rows q)");
+    VK_TRY(vk::launch_split_rows(c->stream, d_k, nk, 1.0f, c->at_kh.p, c->at_kl.p), "launch(vk_split_rows k)");
+    VK_TRY(vk::launch_split_vt(c->stream, d_v, (int)batch, (int)tkv, (int)t_pad, (int)hkv, (int)hd, c->at_vh.p,
+                               c->at_vl.p),
+           "launch(vk_split_vt)");
+    VK_TRY(vk::launch_flash_attn(c->stream, (int)hd, c->at_qh.p, c->at_ql.p, c->at_kh.p, c->at_kl.p, c->at_vh.p,
+                                 c->at_vl.p, d_out, (int)batch, (int)tq, (int)tkv, (int)t_pad, (int)hq, (int)hkv,
+                                 causal ? 1 : 0, (int)q_off),
+           "launch(vk_flash_attn)");
+    return VOKRA_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int vokra_hip_attn_f32_dev(vokra_hip_ctx_t* c, size_t batch, size_t t_q, size_t t_kv, size_t n_head_q,
+                           size_t n_head_kv, size_t head_dim, const float* d_q, const float* d_k, const float* d_v,
+                           float scale, int causal, size_t q_offset, float* d_out) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn_f32: ctx is NULL");
+    int st = check_attn(batch, t_q, t_kv, n_head_q, n_head_kv, head_dim);
+    if (st) return st;
+    if (q_offset > (size_t)INT32_MAX / 2) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn_f32: q_offset too large");
+    if (t_q == 0) return VOKRA_HIP_OK;
+    if (!d_q || !d_out || (t_kv && (!d_k || !d_v)))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn_f32: NULL buffer");
+    if ((reinterpret_cast<uintptr_t>(d_q) | reinterpret_cast<uintptr_t>(d_k) | reinterpret_cast<uintptr_t>(d_out)) & 15)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn_f32: q, k and out must be 16-byte aligned");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    return run_attn(c, batch, t_q, t_kv, n_head_q, n_head_kv, head_dim, d_q, d_k, d_v, scale, causal, q_offset,
+                    d_out);
+}
+
+int vokra_hip_attn_f32(vokra_hip_ctx_t* c, size_t batch, size_t t_q, size_t t_kv, size_t n_head_q, size_t n_head_kv,
+                       size_t head_dim, const float* q, const float* k, const float* v, float scale, int causal,
+                       size_t q_offset, float* out) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn_f32: ctx is NULL");
+    int st = check_attn(batch, t_q, t_kv, n_head_q, n_head_kv, head_dim);
+    if (st) return st;
+    if (q_offset > (size_t)INT32_MAX / 2) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn_f32: q_offset too large");
+    if (t_q == 0) return VOKRA_HIP_OK;
+    if (!q || !out || (t_kv && (!k || !v))) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn_f32: NULL buffer");
+    const size_t nq = batch * t_q * n_head_q * head_dim, nkv = batch * t_kv * n_head_kv * head_dim;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(c->in0.ensure(nq * 4), "hipMalloc");
+    VK_TRY(c->in1.ensure(nkv * 4 + 16), "hipMalloc");
+    VK_TRY(c->in2.ensure(nkv * 4 + 16), "hipMalloc");
+    VK_TRY(c->out0.ensure(nq * 4), "hipMalloc");
+    VK_TRY(hipMemcpyAsync(c->in0.p, q, nq * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+    if (nkv) {
+        VK_TRY(hipMemcpyAsync(c->in1.p, k, nkv * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+        VK_TRY(hipMemcpyAsync(c->in2.p, v, nkv * 4, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+    }
+    st = run_attn(c, batch, t_q, t_kv, n_head_q, n_head_kv, head_dim, (const float*)c->in0.p, (const float*)c->in1.p,
+                  (const float*)c->in2.p, scale, causal, q_offset, (float*)c->out0.p);
+    if (st) {
+        (void)hipStreamSynchronize(c->stream);
+        return st;
+    }
+    VK_TRY(hipMemcpyAsync(out, c->out0.p, nq * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(D2H)");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
 
 const char* vokra_hip_last_error(void) { return g_last_error.c_str(); }
 
@@ -344,7 +433,8 @@ void vokra_hip_destroy(vokra_hip_ctx_t* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
-    for (DevBuf* b : {&c->in0, &c->in1, &c->in2, &c->out0, &c->act.frag, &c->act.scale, &c->act.gsum})
+    for (DevBuf* b : {&c->in0, &c->in1, &c->in2, &c->out0, &c->act.frag, &c->act.scale, &c->act.gsum, &c->at_qh,
+                      &c->at_ql, &c->at_kh, &c->at_kl, &c->at_vh, &c->at_vl})
         b->release();
     (void)hipStreamDestroy(c->stream);
     delete c;

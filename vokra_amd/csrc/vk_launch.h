@@ -41,3 +41,12 @@ hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascal
                            const uint4* wq4, const float2* wdm, const float* bias, float* out, int m, int n, int nsb,
                            int m_pad);
 }  // namespace vk
+
+namespace vk {
+hipError_t launch_split_rows(hipStream_t s, const float* x, size_t n, float scale, void* hi, void* lo);
+hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, int t_pad, int h_kv, int hd, void* vth,
+                           void* vtl);
+hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* ql, const void* kh, const void* kl,
+                             const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
+                             int hq, int hkv, int causal, int q_off);
+}  // namespace vk

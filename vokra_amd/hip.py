@@ -113,6 +113,8 @@ def _declare(L):
     L.vokra_hip_qact_free.restype = None
     L.vokra_hip_qact_quantize_dev.argtypes = [P, P, sz, P, C.c_int]
     L.vokra_hip_gemm_qact_dev.argtypes = [P, P, P, P, P]
+    L.vokra_hip_attn_f32.argtypes = [P, sz, sz, sz, sz, sz, sz, f32p, f32p, f32p, C.c_float, C.c_int, sz, f32p]
+    L.vokra_hip_attn_f32_dev.argtypes = [P, sz, sz, sz, sz, sz, sz, P, P, P, C.c_float, C.c_int, sz, P]
 
 
 def lib():
@@ -393,6 +395,32 @@ class HipContext:
 
     def qact(self, max_m: int, k: int) -> QAct:
         return QAct(self, max_m, k)
+
+    # ---- attention ----------------------------------------------------------
+    def attn_f32(self, q, k, v, n_head_q: int, n_head_kv: int = None, scale: float = None,
+                 causal: bool = False, q_offset: int = 0) -> np.ndarray:
+        """Fused SDPA (compute.rs:2703 attn_f32 core; nn.rs:209-325, text_decoder.rs:1302-1360).
+        q: [B, Tq, Hq*hd] (or [Tq, Hq*hd]); k, v: [B, Tkv, Hkv*hd]. Returns q's shape."""
+        n_head_kv = n_head_q if n_head_kv is None else n_head_kv
+        qv, kv, vv = _f32(q), _f32(k), _f32(v)
+        squeeze = qv.ndim == 2
+        if squeeze:
+            qv, kv, vv = qv[None], kv[None], vv[None]
+        B, tq, wq = qv.shape
+        tkv = kv.shape[1]
+        hd = wq // n_head_q
+        scale = float(hd) ** -0.5 if scale is None else scale
+        out = np.zeros((B, tq, wq), np.float32)
+        _check(lib().vokra_hip_attn_f32(self._h, B, tq, tkv, n_head_q, n_head_kv, hd, _ptr(qv, C.c_float),
+                                        _ptr(kv, C.c_float), _ptr(vv, C.c_float), C.c_float(scale),
+                                        int(bool(causal)), q_offset, _ptr(out, C.c_float)))
+        return out[0] if squeeze else out
+
+    def attn_f32_dev(self, batch, t_q, t_kv, n_head_q, n_head_kv, head_dim, d_q, d_k, d_v, scale, causal,
+                     q_offset, d_out):
+        _check(lib().vokra_hip_attn_f32_dev(self._h, batch, t_q, t_kv, n_head_q, n_head_kv, head_dim, d_q.ptr,
+                                            d_k.ptr, d_v.ptr, C.c_float(scale), int(bool(causal)), q_offset,
+                                            d_out.ptr))
 
     def gemm_qact_dev(self, w: QWeight, qa: QAct, d_out: DeviceBuffer, d_bias=None):
         _check(lib().vokra_hip_gemm_qact_dev(self._h, w._h, qa._h, None if d_bias is None else d_bias.ptr,
