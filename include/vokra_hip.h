@@ -227,6 +227,67 @@ int vokra_hip_attn_f32_dev(vokra_hip_ctx_t *ctx, size_t batch, size_t t_q, size_
                            size_t n_head_kv, size_t head_dim, const float *d_q, const float *d_k,
                            const float *d_v, float scale, int causal, size_t q_offset, float *d_out);
 
+/* ---- paged quantized KV cache in HBM ------------------------------------- */
+
+/* QuantizedPagedKvCache (crates/vokra-core/src/cache/paged_quant.rs:240-545)
+ * on the device, one codebook: pages of block_size time steps x all streams
+ * of one layer, page table entry layer * pages_per_layer + t / block_size,
+ * LIFO free list, rows stored as Q8_0 blocks of 32 (bit-identical packing and
+ * dequantization). The table, free list and allocator state live in device
+ * memory; appends allocate pages on the GPU. This arm stores Q8_0 rows only
+ * (other modes are UNSUPPORTED_OP) with d_head 64 or 128. */
+typedef struct vokra_hip_kv vokra_hip_kv_t;
+
+/* QuantizedPagedKvCache::new (paged_quant.rs:260-307): same rejections. */
+int vokra_hip_kv_create(vokra_hip_ctx_t *ctx, size_t n_layer, size_t n_head, size_t d_head, size_t n_stream,
+                        size_t max_time, size_t block_size, int mode, vokra_hip_kv_t **out);
+void vokra_hip_kv_destroy(vokra_hip_kv_t *kv);
+
+/* append_step (paged_quant.rs:396-437) for items i = 0..n-1 in order:
+ * (streams[i], times[i]) with rows k_rows[i], v_rows[i] of n_head*d_head
+ * floats; host arrays, synchronous. The first item that is out of range
+ * (INVALID_ARGUMENT) or finds no free page (KV_CACHE_EXHAUSTED) stops the
+ * batch; earlier items stay appended, as with successive calls. n <= 1024. */
+int vokra_hip_kv_append(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t layer, size_t n, const int32_t *streams,
+                        const int32_t *times, const float *k_rows, const float *v_rows);
+/* Same with device arrays, asynchronous; the outcome is read by kv_status. */
+int vokra_hip_kv_append_dev(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t layer, size_t n,
+                            const int32_t *d_streams, const int32_t *d_times, const float *d_k, const float *d_v);
+/* Synchronizes and returns the last append's status (n_appended items done). */
+int vokra_hip_kv_status(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t *n_appended);
+
+/* read_step (paged_quant.rs:448-480): dequantized rows, *found = 0 for None. */
+int vokra_hip_kv_read(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t layer, size_t t, size_t s, float *k_out,
+                      float *v_out, int *found);
+/* reset (paged_quant.rs:489-493) and release_layer (:500-515). */
+int vokra_hip_kv_reset(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv);
+int vokra_hip_kv_release_layer(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t layer);
+/* free_pages / pages_in_use (paged_quant.rs:334-343). */
+int vokra_hip_kv_pages(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t *free_pages, size_t *pages_in_use);
+/* The page id of table entry (layer, t / block_size), -1 if none. */
+int vokra_hip_kv_page_of(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t layer, size_t t, long *page);
+/* Resets the cache with the free list set to `order` (a permutation of the
+ * page ids, top of the stack last): places pages at shuffled addresses. No
+ * reference counterpart (the reference always starts from [cap-1 .. 0]). */
+int vokra_hip_kv_set_free_order(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, const int32_t *order, size_t n);
+
+/* Decode attention over the cache: for item i (stream streams[i], keys
+ * 0..lens[i]-1 of `layer`) and query head h (kv head h / (n_head_q / n_head)):
+ * out = softmax((q * scale) . K^T) . V with K, V the cache's dequantized
+ * rows. q and out are [n, n_head_q * d_head]. The single-step case of
+ * attention_from_kv_into (crates/vokra-models/src/whisper/nn.rs:209-325) and
+ * the GQA loop (crates/vokra-models/src/voxtral/text_decoder.rs:1302-1360)
+ * reading QuantizedPagedKvCache rows (the intent of GpuPagedKvCacheOps,
+ * crates/vokra-core/src/cache/paged.rs:941-986). n_head_q / n_head in
+ * {1, 2, 4, 8}. Host arrays, synchronous: */
+int vokra_hip_paged_attn(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t layer, size_t n, const int32_t *streams,
+                         const int32_t *lens, size_t n_head_q, const float *q, float scale, float *out);
+/* Device arrays, asynchronous; max_len bounds every lens[i] (sizes the key
+ * split). */
+int vokra_hip_paged_attn_dev(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t layer, size_t n,
+                             const int32_t *d_streams, const int32_t *d_lens, size_t max_len, size_t n_head_q,
+                             const float *d_q, float scale, float *d_out);
+
 #ifdef __cplusplus
 }
 #endif

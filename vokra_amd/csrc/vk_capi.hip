@@ -11,6 +11,8 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "../../include/vokra_hip.h"
 #include "vk_launch.h"
@@ -128,6 +130,38 @@ constexpr size_t kGemvMaxM = 64;
 
 struct vokra_hip_event {
     hipEvent_t ev = nullptr;
+};
+
+// Paged quantized KV cache (layout and kernels in vk_kvcache.hip).
+struct vokra_hip_kv {
+    vokra_hip_ctx* ctx = nullptr;
+    size_t n_layer = 0, n_head = 0, d_head = 0, n_stream = 0, max_time = 0, bs = 0, ppl = 0, cap = 0, width = 0;
+    size_t pool_bytes = 0, scale_bytes = 0;
+    DevBuf kq, vq, kd, vd, table, free_list, meta;
+    DevBuf items, rows, qbuf, obuf;  // copy-mode staging
+    DevBuf part_ml, part_o;          // split-K partials of paged attention
+    vk::KvView view() const {
+        vk::KvView v;
+        v.kq = kq.p;
+        v.vq = vq.p;
+        v.kd = kd.p;
+        v.vd = vd.p;
+        v.table = (int*)table.p;
+        v.free_list = (int*)free_list.p;
+        v.meta = (int*)meta.p;
+        v.n_layer = (int)n_layer;
+        v.n_stream = (int)n_stream;
+        v.width = (int)width;
+        v.bs = (int)bs;
+        v.ppl = (int)ppl;
+        v.cap = (int)cap;
+        v.max_time = (int)max_time;
+        return v;
+    }
+    void release_all() {
+        for (DevBuf* b : {&kq, &vq, &kd, &vd, &table, &free_list, &meta, &items, &rows, &qbuf, &obuf, &part_ml, &part_o})
+            b->release();
+    }
 };
 
 struct vokra_hip_graph {
@@ -338,9 +372,320 @@ int run_attn(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t hq, s
     return VOKRA_HIP_OK;
 }
 
+int kv_meta(vokra_hip_kv* kv, int* meta4) {
+    VK_TRY(hipMemcpyAsync(meta4, kv->meta.p, 4 * sizeof(int), hipMemcpyDeviceToHost, kv->ctx->stream),
+           "hipMemcpyAsync(kv meta)");
+    VK_TRY(hipStreamSynchronize(kv->ctx->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
+
+// Status of the last append batch, in the reference's error vocabulary.
+int kv_append_status(vokra_hip_kv* kv, size_t n, const int* h_streams, const int* h_times, size_t* appended) {
+    int m[4];
+    int st = kv_meta(kv, m);
+    if (st) return st;
+    if (appended) *appended = (size_t)m[2];
+    if (m[1] == VOKRA_HIP_OK) return VOKRA_HIP_OK;
+    if (m[1] == VOKRA_HIP_ERROR_KV_CACHE_EXHAUSTED)
+        return fail(VOKRA_HIP_ERROR_KV_CACHE_EXHAUSTED,
+                    "paged KV cache exhausted: arena has %zu pages, %zu in use - pre-allocate a larger "
+                    "max_time/n_stream at session construction (item %d of %zu)",
+                    kv->cap, kv->cap, m[2], n);
+    if (h_streams && h_times && (size_t)m[2] < n) {
+        // check_bounds order and wording (paged_quant.rs:518-544)
+        const long t = h_times[m[2]], st = h_streams[m[2]];
+        if (t < 0 || (size_t)t >= kv->max_time)
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "t %ld >= max_time %zu", t, kv->max_time);
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "stream %ld >= n_stream %zu", st, kv->n_stream);
+    }
+    return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "append item %d: layer, stream or t out of range", m[2]);
+}
+
+int kv_split(const vokra_hip_kv* kv, size_t n, size_t max_len, size_t hkv, int* n_split, int* kps) {
+    // enough workgroups to fill the chip, at least 256 keys per split
+    const size_t wgs = n * hkv;
+    size_t want = wgs >= 512 ? 1 : (512 + wgs - 1) / wgs;
+    const size_t max_split = (max_len + 255) / 256;
+    if (want > max_split) want = max_split;
+    if (want < 1) want = 1;
+    const size_t per = (max_len + want - 1) / want;
+    *n_split = (int)want;
+    *kps = (int)(((per + 255) / 256) * 256);
+    (void)kv;
+    return VOKRA_HIP_OK;
+}
+
+int run_paged_attn(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
+                   const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out) {
+    const size_t hkv = kv->n_head;
+    int n_split = 1, kps = 256;
+    kv_split(kv, n, max_len ? max_len : 1, hkv, &n_split, &kps);
+    if (n_split > 1) {
+        VK_TRY(kv->part_ml.ensure(n * hq * n_split * 2 * sizeof(float)), "hipMalloc(paged attention partials)");
+        VK_TRY(kv->part_o.ensure(n * hq * n_split * kv->d_head * sizeof(float)), "hipMalloc(paged attention partials)");
+    }
+    VK_TRY(vk::launch_paged_attn(c->stream, kv->view(), (int)layer, (int)n, d_streams, d_lens, d_q, scale, (int)hq,
+                                 (int)kv->d_head, n_split, kps, d_out, (float*)kv->part_ml.p, (float*)kv->part_o.p),
+           "launch(vk_paged_attn)");
+    return VOKRA_HIP_OK;
+}
+
+int check_paged_attn(const vokra_hip_kv* kv, size_t layer, size_t n, size_t hq) {
+    if (layer >= kv->n_layer)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "layer %zu >= n_layer %zu", layer, kv->n_layer);
+    if (n > 65535) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn: at most 65535 items per call");
+    if (hq == 0 || hq % kv->n_head != 0 || hq / kv->n_head > 8)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "paged_attn: n_head_q=%zu must be 1..8 times the cache's n_head=%zu", hq, kv->n_head);
+    const size_t g = hq / kv->n_head;
+    if (g != 1 && g != 2 && g != 4 && g != 8)
+        return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "paged_attn: query heads per kv head must be 1, 2, 4 or 8");
+    return VOKRA_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int vokra_hip_kv_create(vokra_hip_ctx_t* c, size_t n_layer, size_t n_head, size_t d_head, size_t n_stream,
+                        size_t max_time, size_t block_size, int mode, vokra_hip_kv_t** out) {
+    if (!c || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_create: NULL argument");
+    *out = nullptr;
+    // QuantizedPagedKvCache::new (crates/vokra-core/src/cache/paged_quant.rs:260-307)
+    if (mode == VOKRA_HIP_KV_FP32)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "QuantizedPagedKvCache::new: mode=Fp32 - use PagedKvCache<f32> for FP32");
+    if (!n_layer || !n_head || !d_head || !n_stream || !max_time || !block_size)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "QuantizedPagedKvCache::new: every axis must be > 0");
+    if ((n_head * d_head) % 32 != 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "QuantizedPagedKvCache::new: n_head*d_head=%zu not a multiple of 32", n_head * d_head);
+    if (mode != VOKRA_HIP_KV_Q8_0)
+        return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "kv_create: the device cache stores Q8_0 rows (mode %d)", mode);
+    if (d_head != 64 && d_head != 128)
+        return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "kv_create: d_head %zu is not wired (64 or 128)", d_head);
+    const size_t ppl = (max_time + block_size - 1) / block_size;
+    const size_t cap = ppl * n_layer;
+    if (cap > (size_t)INT32_MAX / 2 || n_stream > 65535 || max_time > (size_t)INT32_MAX / 2)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_create: cache too large for int32 indexing");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    auto* kv = new vokra_hip_kv();
+    kv->ctx = c;
+    kv->n_layer = n_layer;
+    kv->n_head = n_head;
+    kv->d_head = d_head;
+    kv->n_stream = n_stream;
+    kv->max_time = max_time;
+    kv->bs = block_size;
+    kv->ppl = ppl;
+    kv->cap = cap;
+    kv->width = n_head * d_head;
+    kv->pool_bytes = cap * block_size * n_stream * kv->width;
+    kv->scale_bytes = round_up(cap * block_size * n_stream * (kv->width / 32) * 2, 4);
+    hipError_t e = hipSuccess;
+    for (auto pr : {std::make_pair(&kv->kq, kv->pool_bytes), std::make_pair(&kv->vq, kv->pool_bytes),
+                    std::make_pair(&kv->kd, kv->scale_bytes), std::make_pair(&kv->vd, kv->scale_bytes),
+                    std::make_pair(&kv->table, n_layer * ppl * sizeof(int)),
+                    std::make_pair(&kv->free_list, cap * sizeof(int)), std::make_pair(&kv->meta, (4 + 1024) * sizeof(int))})
+        if (e == hipSuccess) e = pr.first->ensure(pr.second);
+    if (e == hipSuccess) e = vk::launch_kv_reset(c->stream, kv->view(), nullptr, kv->pool_bytes, kv->scale_bytes);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        kv->release_all();
+        delete kv;
+        return hip_fail(e, "kv_create");
+    }
+    *out = kv;
+    return VOKRA_HIP_OK;
+}
+
+void vokra_hip_kv_destroy(vokra_hip_kv_t* kv) {
+    if (!kv) return;
+    if (kv->ctx) {
+        (void)hipSetDevice(kv->ctx->device);
+        (void)hipStreamSynchronize(kv->ctx->stream);
+    }
+    kv->release_all();
+    delete kv;
+}
+
+int vokra_hip_kv_append_dev(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv, size_t layer, size_t n, const int32_t* d_streams,
+                            const int32_t* d_times, const float* d_k, const float* d_v) {
+    if (!c || !kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: bad context or cache");
+    if (n > 1024) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: at most 1024 items per call, got %zu", n);
+    if (layer >= kv->n_layer)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "layer %zu >= n_layer %zu", layer, kv->n_layer);
+    if (n && (!d_streams || !d_times || !d_k || !d_v))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_kv_append(c->stream, kv->view(), (int)layer, (int)n, d_streams, d_times, d_k, d_v),
+           "launch(vk_kv_append)");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_kv_status(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv, size_t* n_appended) {
+    if (!c || !kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_status: bad context or cache");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    return kv_append_status(kv, SIZE_MAX, nullptr, nullptr, n_appended);
+}
+
+int vokra_hip_kv_append(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv, size_t layer, size_t n, const int32_t* streams,
+                        const int32_t* times, const float* k_rows, const float* v_rows) {
+    if (!c || !kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: bad context or cache");
+    if (n > 1024) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: at most 1024 items per call, got %zu", n);
+    if (layer >= kv->n_layer)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "layer %zu >= n_layer %zu", layer, kv->n_layer);
+    if (n == 0) return VOKRA_HIP_OK;
+    if (!streams || !times || !k_rows || !v_rows) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    const size_t rb = n * kv->width * sizeof(float);
+    VK_TRY(kv->items.ensure(2 * n * sizeof(int)), "hipMalloc");
+    VK_TRY(kv->rows.ensure(2 * rb), "hipMalloc");
+    int* d_items = (int*)kv->items.p;
+    float* d_rows = (float*)kv->rows.p;
+    VK_TRY(hipMemcpyAsync(d_items, streams, n * sizeof(int), hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
+    VK_TRY(hipMemcpyAsync(d_items + n, times, n * sizeof(int), hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
+    VK_TRY(hipMemcpyAsync(d_rows, k_rows, rb, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
+    VK_TRY(hipMemcpyAsync((char*)d_rows + rb, v_rows, rb, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
+    VK_TRY(vk::launch_kv_append(c->stream, kv->view(), (int)layer, (int)n, d_items, d_items + n, d_rows,
+                                (const float*)((char*)d_rows + rb)),
+           "launch(vk_kv_append)");
+    return kv_append_status(kv, n, streams, times, nullptr);
+}
+
+int vokra_hip_kv_read(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv, size_t layer, size_t t, size_t s, float* k_out,
+                      float* v_out, int* found) {
+    if (!c || !kv || kv->ctx != c || !found) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_read: bad argument");
+    *found = 0;
+    // read_step returns None out of range (paged_quant.rs:455-462)
+    if (layer >= kv->n_layer || t >= kv->max_time || s >= kv->n_stream) return VOKRA_HIP_OK;
+    if (!k_out || !v_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_read: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(kv->obuf.ensure(2 * kv->width * sizeof(float) + 16), "hipMalloc");
+    float* d_out = (float*)kv->obuf.p;
+    int* d_found = (int*)(d_out + 2 * kv->width);
+    VK_TRY(vk::launch_kv_read(c->stream, kv->view(), (int)layer, (int)t, (int)s, d_out, d_found), "launch(vk_kv_read)");
+    int f = 0;
+    VK_TRY(hipMemcpyAsync(&f, d_found, sizeof(int), hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (f) {
+        VK_TRY(hipMemcpyAsync(k_out, d_out, kv->width * sizeof(float), hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync");
+        VK_TRY(hipMemcpyAsync(v_out, d_out + kv->width, kv->width * sizeof(float), hipMemcpyDeviceToHost, c->stream),
+               "hipMemcpyAsync");
+        VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    }
+    *found = f;
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_kv_reset(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv) {
+    if (!c || !kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_reset: bad context or cache");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_kv_reset(c->stream, kv->view(), nullptr, kv->pool_bytes, kv->scale_bytes), "launch(vk_kv_reset)");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_kv_set_free_order(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv, const int32_t* order, size_t n) {
+    if (!c || !kv || kv->ctx != c || !order) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_set_free_order: bad argument");
+    if (n != kv->cap) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_set_free_order: need %zu page ids, got %zu", kv->cap, n);
+    std::vector<char> seen(kv->cap, 0);
+    for (size_t i = 0; i < n; ++i) {
+        if (order[i] < 0 || (size_t)order[i] >= kv->cap || seen[order[i]])
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_set_free_order: not a permutation of 0..%zu", kv->cap - 1);
+        seen[order[i]] = 1;
+    }
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(kv->items.ensure(n * sizeof(int)), "hipMalloc");
+    VK_TRY(hipMemcpyAsync(kv->items.p, order, n * sizeof(int), hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
+    VK_TRY(vk::launch_kv_reset(c->stream, kv->view(), (const int*)kv->items.p, kv->pool_bytes, kv->scale_bytes),
+           "launch(vk_kv_reset)");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_kv_release_layer(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv, size_t layer) {
+    if (!c || !kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_release_layer: bad context or cache");
+    if (layer >= kv->n_layer)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "release_layer: layer %zu >= n_layer %zu", layer, kv->n_layer);
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_kv_release(c->stream, kv->view(), (int)layer), "launch(vk_kv_release)");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_kv_pages(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv, size_t* free_pages, size_t* pages_in_use) {
+    if (!c || !kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_pages: bad context or cache");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    int m[4];
+    int st = kv_meta(kv, m);
+    if (st) return st;
+    if (free_pages) *free_pages = (size_t)m[0];
+    if (pages_in_use) *pages_in_use = kv->cap - (size_t)m[0];
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_kv_page_of(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv, size_t layer, size_t t, long* page) {
+    if (!c || !kv || kv->ctx != c || !page) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_page_of: bad argument");
+    *page = -1;
+    if (layer >= kv->n_layer || t >= kv->max_time) return VOKRA_HIP_OK;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(kv->obuf.ensure(2 * kv->width * sizeof(float) + 16), "hipMalloc");
+    int* d = (int*)kv->obuf.p;
+    VK_TRY(vk::launch_kv_page_of(c->stream, kv->view(), (int)layer, (int)t, d), "launch(vk_kv_page_of)");
+    int h[2];
+    VK_TRY(hipMemcpyAsync(h, d, sizeof h, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    *page = h[0];
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_paged_attn_dev(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv, size_t layer, size_t n, const int32_t* d_streams,
+                             const int32_t* d_lens, size_t max_len, size_t n_head_q, const float* d_q, float scale,
+                             float* d_out) {
+    if (!c || !kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn: bad context or cache");
+    int st = check_paged_attn(kv, layer, n, n_head_q);
+    if (st) return st;
+    if (n == 0) return VOKRA_HIP_OK;
+    if (!d_streams || !d_lens || !d_q || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn: NULL buffer");
+    if (max_len > kv->max_time) max_len = kv->max_time;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    return run_paged_attn(c, kv, layer, n, d_streams, d_lens, max_len, n_head_q, d_q, scale, d_out);
+}
+
+int vokra_hip_paged_attn(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv, size_t layer, size_t n, const int32_t* streams,
+                         const int32_t* lens, size_t n_head_q, const float* q, float scale, float* out) {
+    if (!c || !kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn: bad context or cache");
+    int st = check_paged_attn(kv, layer, n, n_head_q);
+    if (st) return st;
+    if (n == 0) return VOKRA_HIP_OK;
+    if (!streams || !lens || !q || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn: NULL buffer");
+    size_t max_len = 0;
+    for (size_t i = 0; i < n; ++i) {
+        if (streams[i] < 0 || (size_t)streams[i] >= kv->n_stream)
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "stream %d >= n_stream %zu", streams[i], kv->n_stream);
+        if (lens[i] < 0 || (size_t)lens[i] > kv->max_time)
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn: length %d outside 0..max_time %zu", lens[i],
+                        kv->max_time);
+        if ((size_t)lens[i] > max_len) max_len = (size_t)lens[i];
+    }
+    VK_TRY(set_dev(c), "hipSetDevice");
+    const size_t qb = n * n_head_q * kv->d_head * sizeof(float);
+    VK_TRY(kv->items.ensure(2 * n * sizeof(int)), "hipMalloc");
+    VK_TRY(kv->qbuf.ensure(qb), "hipMalloc");
+    VK_TRY(kv->rows.ensure(qb), "hipMalloc");
+    int* d_items = (int*)kv->items.p;
+    VK_TRY(hipMemcpyAsync(d_items, streams, n * sizeof(int), hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
+    VK_TRY(hipMemcpyAsync(d_items + n, lens, n * sizeof(int), hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
+    VK_TRY(hipMemcpyAsync(kv->qbuf.p, q, qb, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync");
+    st = run_paged_attn(c, kv, layer, n, d_items, d_items + n, max_len, n_head_q, (const float*)kv->qbuf.p, scale,
+                        (float*)kv->rows.p);
+    if (st) {
+        (void)hipStreamSynchronize(c->stream);
+        return st;
+    }
+    VK_TRY(hipMemcpyAsync(out, kv->rows.p, qb, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
 
 int vokra_hip_attn_f32_dev(vokra_hip_ctx_t* c, size_t batch, size_t t_q, size_t t_kv, size_t n_head_q,
                            size_t n_head_kv, size_t head_dim, const float* d_q, const float* d_k, const float* d_v,

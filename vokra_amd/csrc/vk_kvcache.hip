@@ -1,0 +1,547 @@
+// vk_kvcache.hip — the quantized paged KV cache resident in HBM, and decode
+// attention over it, for gfx950.
+//
+// Semantics follow QuantizedPagedKvCache (crates/vokra-core/src/cache/
+// paged_quant.rs:240-545) with one codebook:
+//   * a page holds `bs` time steps of one layer for every stream; the page
+//     table entry of (layer, t) is layer * pages_per_layer + t / bs (:414-415);
+//   * pages come from a LIFO free list that starts as [cap-1 .. 0] (pop gives
+//     0, 1, 2, ...), release pushes back in table order (:152-216, :500-515);
+//   * each K / V row (n_head * d_head values) is stored as Q8_0 blocks of 32,
+//     packed exactly as BlockQ8_0::pack (kv_quant/q8_0.rs:40-64), and reads
+//     return q * f32(f16(d)) (:69-80).
+// Device layout (this build's, numerics unaffected): quants and scales in
+// separate arrays, so a head's row slice is one aligned vector load:
+//   q: [cap][bs][n_stream][width] int8,  d: [cap][bs][n_stream][width/32] f16
+// The table, the free list and the allocator state live in device memory and
+// are only touched by kernels: an append batch allocates on the GPU.
+#include "vk_common.h"
+
+namespace vk {
+
+// Device view of one cache, passed by value to every kernel.
+struct KvDev {
+    int8_t* kq;
+    int8_t* vq;
+    uint16_t* kd;
+    uint16_t* vd;
+    int* table;      // [n_layer * ppl], -1 = no page
+    int* free_list;  // stack of page ids, top at free_len - 1
+    int* meta;       // [0] free_len, [1] status of the last append, [2] items appended, [3] scratch,
+                     // [4 ..) per item of the last append: 1 = overwritten by a later item
+    int n_layer, n_stream, width, row_blocks, bs, ppl, cap, max_time;
+};
+
+enum : int { KV_OK = 0, KV_INVALID = 5, KV_EXHAUSTED = 10 };  // vokra_hip_status_t values
+
+__device__ __forceinline__ size_t kv_slot(const KvDev& c, int pid, int t, int s) {
+    return ((size_t)pid * c.bs + (t % c.bs)) * c.n_stream + s;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation for one append batch: items i = 0..n-1 behave as append_step
+// calls in order. Item i needs a new page when its table entry is empty and
+// no earlier item of the batch maps to the same entry; the r-th such item
+// pops free_list[free_len - 1 - r]. The first invalid or unservable item
+// ends the batch (items before it are appended, it and later ones are not).
+// One workgroup of 1024 threads; n <= 1024.
+__global__ __launch_bounds__(1024) void vk_kv_alloc(KvDev c, int layer, int n, const int* __restrict__ streams,
+                                                    const int* __restrict__ times) {
+    __shared__ int s_ti[1024];
+    __shared__ int s_key[1024];
+    __shared__ int s_scan[1024];
+    __shared__ int s_fail;
+    const int i = threadIdx.x;
+    int s = 0, t = 0, ti = -1;
+    bool valid = false;
+    if (i < n) {
+        s = streams[i];
+        t = times[i];
+        valid = layer >= 0 && layer < c.n_layer && s >= 0 && s < c.n_stream && t >= 0 && t < c.max_time;
+        ti = valid ? layer * c.ppl + t / c.bs : -1;
+    }
+    if (i == 0) s_fail = n;
+    s_ti[i] = ti;
+    s_key[i] = valid ? s * c.max_time + t : -1 - i;  // distinct for invalid items
+    __syncthreads();
+    bool first = false;
+    if (valid && c.table[ti] < 0) {
+        first = true;
+        for (int j = 0; j < i; ++j)
+            if (s_ti[j] == ti) {
+                first = false;
+                break;
+            }
+    }
+    // inclusive scan of `first` (Hillis-Steele over the block)
+    s_scan[i] = first ? 1 : 0;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+        const int v = i >= off ? s_scan[i - off] : 0;
+        __syncthreads();
+        s_scan[i] += v;
+        __syncthreads();
+    }
+    const int free_len = c.meta[0];
+    const int rank = s_scan[i] - (first ? 1 : 0);
+    const bool fail = i < n && (!valid || (first && rank >= free_len));
+    if (fail) atomicMin(&s_fail, i);
+    __syncthreads();
+    const int f = s_fail;
+    if (first && i < f) c.table[ti] = c.free_list[free_len - 1 - rank];
+    // a later item of the batch writing the same slot wins, as with
+    // successive append_step calls
+    if (i < n) {
+        int over = 0;
+        for (int j = i + 1; j < f; ++j)
+            if (s_key[j] == s_key[i]) {
+                over = 1;
+                break;
+            }
+        c.meta[4 + i] = over;
+    }
+    if (i == 0) {
+        const int used = f > 0 ? s_scan[f - 1] : 0;
+        int status = KV_OK;
+        if (f < n) {
+            const int sf = streams[f], tf = times[f];
+            const bool vf = layer >= 0 && layer < c.n_layer && sf >= 0 && sf < c.n_stream && tf >= 0 &&
+                            tf < c.max_time;
+            status = vf ? KV_EXHAUSTED : KV_INVALID;
+        }
+        c.meta[0] = free_len - used;
+        c.meta[1] = status;
+        c.meta[2] = f;
+    }
+}
+
+// Packs the K and V rows of the appended items into their slots. One thread
+// per (item, 32-element block, element); 32 consecutive threads form a block.
+// Same arithmetic as BlockQ8_0::pack: amax = max |x|, d = amax / 127,
+// q = round(clamp(x * (1/d), -127, 127)), scale stored as f16(d).
+__device__ __forceinline__ void q8_0_pack_lane(float v, int lane32, int8_t* q, uint16_t* d) {
+    const float amax = vk_group_max<32>(fabsf(v));
+    const float dd = amax == 0.0f ? 0.0f : amax / 127.0f;
+    const float inv = dd == 0.0f ? 0.0f : 1.0f / dd;
+    const float sc = v * inv;
+    const float cl = sc != sc ? sc : fminf(fmaxf(sc, -127.0f), 127.0f);
+    *q = (int8_t)((cl != cl) ? 0 : (int)roundf(cl));
+    if (lane32 == 0) *d = (uint16_t)vk_f32_to_f16_bits(dd);
+}
+
+__global__ void vk_kv_write(KvDev c, int layer, int n, const int* __restrict__ streams,
+                            const int* __restrict__ times, const float* __restrict__ k, const float* __restrict__ v) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int e = (int)(gid % (size_t)c.width);
+    const int item = (int)(gid / (size_t)c.width);
+    // `live` is uniform over each 32-thread block group (width % 32 == 0)
+    const bool live = item < n && item < c.meta[2] && c.meta[4 + min(item, 1023)] == 0;
+    float kv = 0.0f, vv = 0.0f;
+    int s = 0, t = 0;
+    if (live) {
+        s = streams[item];
+        t = times[item];
+        kv = k[(size_t)item * c.width + e];
+        vv = v[(size_t)item * c.width + e];
+    }
+    int8_t qk, qv;
+    uint16_t dk = 0, dv = 0;
+    q8_0_pack_lane(kv, e & 31, &qk, &dk);
+    q8_0_pack_lane(vv, e & 31, &qv, &dv);
+    if (!live) return;
+    const int pid = c.table[layer * c.ppl + t / c.bs];
+    const size_t slot = kv_slot(c, pid, t, s);
+    c.kq[slot * c.width + e] = qk;
+    c.vq[slot * c.width + e] = qv;
+    if ((e & 31) == 0) {
+        c.kd[slot * c.row_blocks + e / 32] = dk;
+        c.vd[slot * c.row_blocks + e / 32] = dv;
+    }
+}
+
+// read_step (paged_quant.rs:448-480): dequantized K and V rows of (layer, t, s)
+// into out[0 .. width) and out[width .. 2 width); found[0] = 0 when the entry
+// has no page (the reference's None).
+__global__ void vk_kv_read(KvDev c, int layer, int t, int s, float* __restrict__ out, int* __restrict__ found) {
+    const int pid = c.table[layer * c.ppl + t / c.bs];
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e == 0) found[0] = pid >= 0 ? 1 : 0;
+    if (pid < 0 || e >= c.width) return;
+    const size_t slot = kv_slot(c, pid, t, s);
+    out[e] = (float)c.kq[slot * c.width + e] * vk_f16_to_f32(c.kd[slot * c.row_blocks + e / 32]);
+    out[c.width + e] = (float)c.vq[slot * c.width + e] * vk_f16_to_f32(c.vd[slot * c.row_blocks + e / 32]);
+}
+
+// release_layer (paged_quant.rs:500-515): entries of `layer` in table order
+// push their pages; meta[3] keeps the old free_len so the zeroing kernel
+// finds the released pages at free_list[meta[3] .. meta[0]).
+__global__ __launch_bounds__(1024) void vk_kv_release(KvDev c, int layer) {
+    __shared__ int s_scan[1024];
+    __shared__ int s_base;
+    const int i = threadIdx.x;
+    if (i == 0) {
+        s_base = c.meta[0];
+        c.meta[3] = c.meta[0];
+    }
+    __syncthreads();
+    for (int p0 = 0; p0 < c.ppl; p0 += 1024) {
+        const int p = p0 + i;
+        const int ti = layer * c.ppl + p;
+        const int pid = p < c.ppl ? c.table[ti] : -1;
+        s_scan[i] = pid >= 0 ? 1 : 0;
+        __syncthreads();
+        for (int off = 1; off < 1024; off <<= 1) {
+            const int v = i >= off ? s_scan[i - off] : 0;
+            __syncthreads();
+            s_scan[i] += v;
+            __syncthreads();
+        }
+        if (pid >= 0) {
+            c.free_list[s_base + s_scan[i] - 1] = pid;
+            c.table[ti] = -1;
+        }
+        __syncthreads();
+        if (i == 0) s_base += s_scan[1023];
+        __syncthreads();
+    }
+    if (i == 0) c.meta[0] = s_base;
+}
+
+// Zeroes the pages at free_list[meta[3] .. meta[0]) (the ones just released).
+__global__ void vk_kv_zero_released(KvDev c) {
+    const int lo = c.meta[3], hi = c.meta[0];
+    const size_t qpage = (size_t)c.bs * c.n_stream * c.width;
+    const size_t dpage = (size_t)c.bs * c.n_stream * c.row_blocks;
+    for (int r = lo + blockIdx.y; r < hi; r += gridDim.y) {
+        const int pid = c.free_list[r];
+        for (size_t x = (size_t)blockIdx.x * blockDim.x + threadIdx.x; x < qpage; x += (size_t)gridDim.x * blockDim.x) {
+            c.kq[(size_t)pid * qpage + x] = 0;
+            c.vq[(size_t)pid * qpage + x] = 0;
+            if (x < dpage) {
+                c.kd[(size_t)pid * dpage + x] = 0;
+                c.vd[(size_t)pid * dpage + x] = 0;
+            }
+        }
+    }
+}
+
+// reset (paged_quant.rs:489-493): empty table, free list [cap-1 .. 0] (or a
+// caller-given order), status cleared. Page memory is cleared by fill kernels.
+__global__ void vk_kv_reset_meta(KvDev c, const int* __restrict__ order) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < c.n_layer * c.ppl) c.table[i] = -1;
+    if (i < c.cap) c.free_list[i] = order ? order[i] : c.cap - 1 - i;
+    if (i == 0) {
+        c.meta[0] = c.cap;
+        c.meta[1] = KV_OK;
+        c.meta[2] = 0;
+        c.meta[3] = c.cap;
+    }
+}
+
+__global__ void vk_fill_u32(uint32_t* __restrict__ p, size_t n, uint32_t v) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+__global__ void vk_kv_page_of(KvDev c, int layer, int t, int* __restrict__ out) {
+    out[0] = c.table[layer * c.ppl + t / c.bs];
+    out[1] = c.meta[0];
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention over the cache. For item i (stream s_i, keys 0..len_i-1)
+// and query head h (kv head h / G):
+//   s_j = (q_h * scale) . k_j,  p = softmax(s),  out_h = sum_j p_j v_j
+// with k_j, v_j the cache's dequantized rows (head slice). One workgroup per
+// (key split, kv head, item) handles the G query heads sharing the kv head;
+// keys go in chunks of 256 (one per thread for the scores). With several
+// splits, each writes (m, l, O) partials that vk_paged_attn_combine merges.
+namespace pa {
+constexpr int CH = 256;
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const int* __restrict__ streams,
+                                                     const int* __restrict__ lens, const float* __restrict__ q,
+                                                     float scale, int hq, int n_split, int keys_per_split,
+                                                     float* __restrict__ out, float* __restrict__ part_ml,
+                                                     float* __restrict__ part_o) {
+    constexpr int NB = HD / 32;            // blocks per head slice
+    constexpr int NO = G * HD;             // outputs of the workgroup
+    constexpr int OPT = NO >= 256 ? NO / 256 : 1;    // outputs per thread
+    constexpr int TPO = NO >= 256 ? 1 : 256 / NO;    // threads per output
+    __shared__ __align__(16) float lq[G][HD];
+    __shared__ float lpd[G][pa::CH][NB];         // p_j * d_{j,b} for the V product
+    __shared__ float lalpha[G];                  // chunk rescale factors (uniform)
+    __shared__ float lml[G][2];                  // final (m, l) per head
+    __shared__ __align__(16) int8_t lv[pa::CH][HD];  // V quants of the chunk
+    __shared__ float red[G][8];
+    __shared__ float lpart[256 * OPT];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int split = blockIdx.x, hk = blockIdx.y, item = blockIdx.z;
+    const int s = streams[item];
+    const int len = min(lens[item], c.max_time);
+    const int k0 = split * keys_per_split, k1 = min(len, k0 + keys_per_split);
+    const size_t hcol = (size_t)hk * HD;
+
+    for (int x = tid; x < G * HD; x += 256) {
+        const int g = x / HD, e = x % HD;
+        lq[g][e] = q[((size_t)item * hq + hk * G + g) * HD + e] * scale;
+    }
+    float m_run[G], l_run[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m_run[g] = -INFINITY;
+        l_run[g] = 0.0f;
+    }
+    float o_acc[OPT];
+#pragma unroll
+    for (int u = 0; u < OPT; ++u) o_acc[u] = 0.0f;
+    __syncthreads();
+
+    for (int j0 = k0; j0 < k1; j0 += pa::CH) {
+        // ---- scores: thread = key
+        const int j = j0 + tid;
+        const bool kv_ok = j < k1;
+        const int jt = kv_ok ? j : k0;
+        int pid = c.table[layer * c.ppl + jt / c.bs];
+        const bool has = kv_ok && pid >= 0;
+        pid = max(pid, 0);
+        const size_t slot = kv_slot(c, pid, jt, s);
+        float sc[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) sc[g] = 0.0f;
+        const uint4* kr = reinterpret_cast<const uint4*>(c.kq + slot * c.width + hcol);
+        const uint4* vr = reinterpret_cast<const uint4*>(c.vq + slot * c.width + hcol);
+#pragma unroll 1
+        for (int b = 0; b < NB; ++b) {
+            const float d = vk_f16_to_f32_hw(c.kd[slot * c.row_blocks + hk * NB + b]);
+            const uint4 w0 = kr[2 * b], w1 = kr[2 * b + 1];
+            const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            float kf[32];  // the block's dequantized keys (exact products)
+#pragma unroll
+            for (int x = 0; x < 32; ++x) kf[x] = (float)(int8_t)((w[x >> 2] >> (8 * (x & 3))) & 0xff) * d;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float4* qg = reinterpret_cast<const float4*>(&lq[g][32 * b]);
+                float a = sc[g];
+#pragma unroll 2
+                for (int x4 = 0; x4 < 8; ++x4) {
+                    const float4 q4 = qg[x4];
+                    a = fmaf(q4.x, kf[4 * x4], a);
+                    a = fmaf(q4.y, kf[4 * x4 + 1], a);
+                    a = fmaf(q4.z, kf[4 * x4 + 2], a);
+                    a = fmaf(q4.w, kf[4 * x4 + 3], a);
+                }
+                sc[g] = a;
+            }
+            // stage V quants and its scale product for the P.V pass
+            const uint4 v0 = vr[2 * b], v1 = vr[2 * b + 1];
+            *reinterpret_cast<uint4*>(&lv[tid][32 * b]) = v0;
+            *reinterpret_cast<uint4*>(&lv[tid][32 * b + 16]) = v1;
+        }
+        float dv[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) dv[b] = has ? vk_f16_to_f32_hw(c.vd[slot * c.row_blocks + hk * NB + b]) : 0.0f;
+        // ---- chunk max per head
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            sc[g] = has ? sc[g] : -INFINITY;
+            float mx = sc[g];
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, VK_WAVE));
+            if (lane == 0) red[g][wave] = mx;
+        }
+        __syncthreads();
+        float alpha[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mx = fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3]));
+            const float m_new = fmaxf(m_run[g], mx);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            alpha[g] = __expf(m_run[g] - m_use);
+            const float p = __expf(sc[g] - m_use);
+            if (tid == 0) lalpha[g] = alpha[g];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) lpd[g][tid][b] = p * dv[b];
+            float ps = p;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) ps += __shfl_xor(ps, o, VK_WAVE);
+            if (lane == 0) red[g][4 + wave] = ps;
+            m_run[g] = m_new;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < G; ++g) l_run[g] = l_run[g] * alpha[g] + ((red[g][4] + red[g][5]) + (red[g][6] + red[g][7]));
+        // ---- O += P . V: output o = (g, e); TPO threads share an output
+        const int nk = min(pa::CH, k1 - j0);
+#pragma unroll
+        for (int u = 0; u < OPT; ++u) {
+            const int o = NO >= 256 ? tid + 256 * u : tid / TPO;
+            const int part = NO >= 256 ? 0 : tid % TPO;
+            const int g = o / HD, e = o % HD;
+            float a = 0.0f;
+            for (int jj = part; jj < nk; jj += TPO) a = fmaf(lpd[g][jj][e >> 5], (float)lv[jj][e], a);
+            o_acc[u] = o_acc[u] * lalpha[g] + a;
+        }
+        __syncthreads();
+    }
+    // ---- reduce the TPO partials of each output (fixed order), then write
+#pragma unroll
+    for (int u = 0; u < OPT; ++u) lpart[tid + 256 * u] = o_acc[u];
+    if (tid == 0)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            lml[g][0] = m_run[g];
+            lml[g][1] = l_run[g];
+        }
+    __syncthreads();
+    for (int o = tid; o < NO; o += 256) {
+        const int g = o / HD, e = o % HD;
+        float a = 0.0f;
+        if (NO >= 256) {
+            a = lpart[(o % 256) + 256 * (o / 256)];
+        } else {
+            for (int r = 0; r < TPO; ++r) a += lpart[o * TPO + r];
+        }
+        const int h = hk * G + g;
+        if (n_split == 1) {
+            const float inv = lml[g][1] > 0.0f ? 1.0f / lml[g][1] : 0.0f;
+            out[((size_t)item * hq + h) * HD + e] = a * inv;
+        } else {
+            const size_t pi = ((size_t)item * hq + h) * n_split + split;
+            part_o[pi * HD + e] = a;
+            if (e == 0) {
+                part_ml[2 * pi] = lml[g][0];
+                part_ml[2 * pi + 1] = lml[g][1];
+            }
+        }
+    }
+}
+
+// Merges split partials: m = max m_s, O = sum O_s e^(m_s - m), l likewise.
+template <int HD>
+__global__ void vk_paged_attn_combine(int n_split, int hq, const float* __restrict__ part_ml,
+                                      const float* __restrict__ part_o, float* __restrict__ out) {
+    const size_t ih = blockIdx.x;  // (item, head)
+    const int e = threadIdx.x;
+    float m = -INFINITY;
+    for (int sp = 0; sp < n_split; ++sp) m = fmaxf(m, part_ml[2 * (ih * n_split + sp)]);
+    const float m_use = m == -INFINITY ? 0.0f : m;
+    float l = 0.0f, o = 0.0f;
+    for (int sp = 0; sp < n_split; ++sp) {
+        const size_t pi = ih * n_split + sp;
+        const float w = __expf(part_ml[2 * pi] - m_use);
+        l += part_ml[2 * pi + 1] * w;
+        if (e < HD) o += part_o[pi * HD + e] * w;
+    }
+    if (e < HD) out[ih * HD + e] = l > 0.0f ? o / l : 0.0f;
+}
+
+}  // namespace vk
+
+#include "vk_launch.h"
+
+namespace vk {
+
+static KvDev kv_view(const KvView& v) {
+    KvDev c;
+    c.kq = (int8_t*)v.kq;
+    c.vq = (int8_t*)v.vq;
+    c.kd = (uint16_t*)v.kd;
+    c.vd = (uint16_t*)v.vd;
+    c.table = v.table;
+    c.free_list = v.free_list;
+    c.meta = v.meta;
+    c.n_layer = v.n_layer;
+    c.n_stream = v.n_stream;
+    c.width = v.width;
+    c.row_blocks = v.width / 32;
+    c.bs = v.bs;
+    c.ppl = v.ppl;
+    c.cap = v.cap;
+    c.max_time = v.max_time;
+    return c;
+}
+
+hipError_t launch_kv_append(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* times,
+                            const float* k, const float* vv) {
+    const KvDev c = kv_view(v);
+    hipLaunchKernelGGL(vk_kv_alloc, dim3(1), dim3(1024), 0, s, c, layer, n, streams, times);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t threads = (size_t)n * v.width;
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_kv_write, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, c, layer, n, streams,
+                       times, k, vv);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_read(hipStream_t s, const KvView& v, int layer, int t, int st, float* out, int* found) {
+    hipLaunchKernelGGL(vk_kv_read, dim3((unsigned)((v.width + 255) / 256)), dim3(256), 0, s, kv_view(v), layer, t, st,
+                       out, found);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_release(hipStream_t s, const KvView& v, int layer) {
+    const KvDev c = kv_view(v);
+    hipLaunchKernelGGL(vk_kv_release, dim3(1), dim3(1024), 0, s, c, layer);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(vk_kv_zero_released, dim3(64, 64), dim3(256), 0, s, c);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_reset(hipStream_t s, const KvView& v, const int* order, size_t pool_bytes, size_t scale_bytes) {
+    const KvDev c = kv_view(v);
+    const int n = max(v.n_layer * v.ppl, v.cap);
+    hipLaunchKernelGGL(vk_kv_reset_meta, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, c, order);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    for (void* p : {v.kq, v.vq})
+        hipLaunchKernelGGL(vk_fill_u32, dim3(2048), dim3(256), 0, s, (uint32_t*)p, pool_bytes / 4, 0u);
+    for (void* p : {(void*)v.kd, (void*)v.vd})
+        hipLaunchKernelGGL(vk_fill_u32, dim3(512), dim3(256), 0, s, (uint32_t*)p, scale_bytes / 4, 0u);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_page_of(hipStream_t s, const KvView& v, int layer, int t, int* out) {
+    hipLaunchKernelGGL(vk_kv_page_of, dim3(1), dim3(1), 0, s, kv_view(v), layer, t, out);
+    return hipGetLastError();
+}
+
+template <int HD, int G>
+static void go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* streams, const int* lens,
+                  const float* q, float scale, int hq, int hkv, int n_split, int kps, float* out, float* pml,
+                  float* po) {
+    hipLaunchKernelGGL((vk_paged_attn<HD, G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams, lens, q,
+                       scale, hq, n_split, kps, out, pml, po);
+}
+
+hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* lens,
+                             const float* q, float scale, int hq, int hd, int n_split, int keys_per_split, float* out,
+                             float* part_ml, float* part_o) {
+    const KvDev c = kv_view(v);
+    const int hkv = v.width / hd, g = hq / hkv;
+#define VK_PA(HDV, GV)                                                                                      \
+    if (hd == HDV && g == GV) {                                                                             \
+        go_pa<HDV, GV>(s, c, layer, n, streams, lens, q, scale, hq, hkv, n_split, keys_per_split, out, part_ml, \
+                       part_o);                                                                             \
+    } else
+    VK_PA(64, 1) VK_PA(64, 2) VK_PA(64, 4) VK_PA(64, 8) VK_PA(128, 1) VK_PA(128, 2) VK_PA(128, 4) VK_PA(128, 8) {
+        return hipErrorInvalidValue;
+    }
+#undef VK_PA
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || n_split == 1) return e;
+    if (hd == 64)
+        hipLaunchKernelGGL(vk_paged_attn_combine<64>, dim3((unsigned)(n * hq)), dim3(64), 0, s, n_split, hq, part_ml,
+                           part_o, out);
+    else
+        hipLaunchKernelGGL(vk_paged_attn_combine<128>, dim3((unsigned)(n * hq)), dim3(128), 0, s, n_split, hq,
+                           part_ml, part_o, out);
+    return hipGetLastError();
+}
+
+}  // namespace vk

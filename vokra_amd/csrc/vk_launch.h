@@ -50,3 +50,21 @@ hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* 
                              const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
                              int hq, int hkv, int causal, int q_off);
 }  // namespace vk
+
+namespace vk {
+// Device pointers and shape of one paged KV cache (see vk_kvcache.hip).
+struct KvView {
+    void *kq, *vq, *kd, *vd;
+    int *table, *free_list, *meta;
+    int n_layer, n_stream, width, bs, ppl, cap, max_time;
+};
+hipError_t launch_kv_append(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* times,
+                            const float* k, const float* vv);
+hipError_t launch_kv_read(hipStream_t s, const KvView& v, int layer, int t, int st, float* out, int* found);
+hipError_t launch_kv_release(hipStream_t s, const KvView& v, int layer);
+hipError_t launch_kv_reset(hipStream_t s, const KvView& v, const int* order, size_t pool_bytes, size_t scale_bytes);
+hipError_t launch_kv_page_of(hipStream_t s, const KvView& v, int layer, int t, int* out);
+hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* lens,
+                             const float* q, float scale, int hq, int hd, int n_split, int keys_per_split, float* out,
+                             float* part_ml, float* part_o);
+}  // namespace vk

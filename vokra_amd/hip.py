@@ -113,6 +113,21 @@ def _declare(L):
     L.vokra_hip_qact_free.restype = None
     L.vokra_hip_qact_quantize_dev.argtypes = [P, P, sz, P, C.c_int]
     L.vokra_hip_gemm_qact_dev.argtypes = [P, P, P, P, P]
+    i32p = C.POINTER(C.c_int32)
+    L.vokra_hip_kv_create.argtypes = [P, sz, sz, sz, sz, sz, sz, C.c_int, C.POINTER(P)]
+    L.vokra_hip_kv_destroy.argtypes = [P]
+    L.vokra_hip_kv_destroy.restype = None
+    L.vokra_hip_kv_append.argtypes = [P, P, sz, sz, i32p, i32p, f32p, f32p]
+    L.vokra_hip_kv_append_dev.argtypes = [P, P, sz, sz, P, P, P, P]
+    L.vokra_hip_kv_status.argtypes = [P, P, C.POINTER(sz)]
+    L.vokra_hip_kv_read.argtypes = [P, P, sz, sz, sz, f32p, f32p, C.POINTER(C.c_int)]
+    L.vokra_hip_kv_reset.argtypes = [P, P]
+    L.vokra_hip_kv_release_layer.argtypes = [P, P, sz]
+    L.vokra_hip_kv_pages.argtypes = [P, P, C.POINTER(sz), C.POINTER(sz)]
+    L.vokra_hip_kv_page_of.argtypes = [P, P, sz, sz, C.POINTER(C.c_long)]
+    L.vokra_hip_kv_set_free_order.argtypes = [P, P, i32p, sz]
+    L.vokra_hip_paged_attn.argtypes = [P, P, sz, sz, i32p, i32p, sz, f32p, C.c_float, f32p]
+    L.vokra_hip_paged_attn_dev.argtypes = [P, P, sz, sz, P, P, sz, sz, P, C.c_float, P]
     L.vokra_hip_attn_f32.argtypes = [P, sz, sz, sz, sz, sz, sz, f32p, f32p, f32p, C.c_float, C.c_int, sz, f32p]
     L.vokra_hip_attn_f32_dev.argtypes = [P, sz, sz, sz, sz, sz, sz, P, P, P, C.c_float, C.c_int, sz, P]
 
@@ -282,6 +297,89 @@ class QAct:
             pass
 
 
+class KvCache:
+    """QuantizedPagedKvCache (paged_quant.rs:240-545) resident on the device."""
+
+    def __init__(self, ctx: "HipContext", n_layer, n_head, d_head, n_stream, max_time, block_size,
+                 mode: KvQuant = KvQuant.Q8_0):
+        self._ctx = ctx
+        self.width = n_head * d_head
+        self.n_head, self.d_head = n_head, d_head
+        h = C.c_void_p()
+        _check(lib().vokra_hip_kv_create(ctx._h, n_layer, n_head, d_head, n_stream, max_time, block_size,
+                                         int(mode), C.byref(h)))
+        self._h = h
+
+    def append(self, layer, streams, times, k_rows, v_rows):
+        """append_step for each (stream, t) in order (host arrays)."""
+        st = np.ascontiguousarray(streams, np.int32)
+        tt = np.ascontiguousarray(times, np.int32)
+        k, v = _f32(k_rows).reshape(-1), _f32(v_rows).reshape(-1)
+        _check(lib().vokra_hip_kv_append(self._ctx._h, self._h, layer, st.size, _ptr(st, C.c_int32),
+                                         _ptr(tt, C.c_int32), _ptr(k, C.c_float), _ptr(v, C.c_float)))
+
+    def append_dev(self, layer, n, d_streams, d_times, d_k, d_v):
+        _check(lib().vokra_hip_kv_append_dev(self._ctx._h, self._h, layer, n, d_streams.ptr, d_times.ptr,
+                                             d_k.ptr, d_v.ptr))
+
+    def status(self):
+        n = C.c_size_t(0)
+        _check(lib().vokra_hip_kv_status(self._ctx._h, self._h, C.byref(n)))
+        return n.value
+
+    def read(self, layer, t, s):
+        """read_step: (k, v) dequantized rows, or None."""
+        k = np.zeros(self.width, np.float32)
+        v = np.zeros(self.width, np.float32)
+        f = C.c_int(0)
+        _check(lib().vokra_hip_kv_read(self._ctx._h, self._h, layer, t, s, _ptr(k, C.c_float),
+                                       _ptr(v, C.c_float), C.byref(f)))
+        return (k, v) if f.value else None
+
+    def reset(self):
+        _check(lib().vokra_hip_kv_reset(self._ctx._h, self._h))
+
+    def release_layer(self, layer):
+        _check(lib().vokra_hip_kv_release_layer(self._ctx._h, self._h, layer))
+
+    def pages(self):
+        fr, used = C.c_size_t(0), C.c_size_t(0)
+        _check(lib().vokra_hip_kv_pages(self._ctx._h, self._h, C.byref(fr), C.byref(used)))
+        return fr.value, used.value
+
+    def page_of(self, layer, t):
+        p = C.c_long(0)
+        _check(lib().vokra_hip_kv_page_of(self._ctx._h, self._h, layer, t, C.byref(p)))
+        return p.value
+
+    def set_free_order(self, order):
+        o = np.ascontiguousarray(order, np.int32)
+        _check(lib().vokra_hip_kv_set_free_order(self._ctx._h, self._h, _ptr(o, C.c_int32), o.size))
+
+    def attn(self, layer, streams, lens, q, n_head_q, scale):
+        """Decode attention of q [n, n_head_q*d_head] over the cached keys 0..lens[i]-1."""
+        st = np.ascontiguousarray(streams, np.int32)
+        ln = np.ascontiguousarray(lens, np.int32)
+        qv = _f32(q).reshape(st.size, -1)
+        out = np.zeros_like(qv)
+        _check(lib().vokra_hip_paged_attn(self._ctx._h, self._h, layer, st.size, _ptr(st, C.c_int32),
+                                          _ptr(ln, C.c_int32), n_head_q, _ptr(qv, C.c_float), C.c_float(scale),
+                                          _ptr(out, C.c_float)))
+        return out
+
+    def attn_dev(self, layer, n, d_streams, d_lens, max_len, n_head_q, d_q, scale, d_out):
+        _check(lib().vokra_hip_paged_attn_dev(self._ctx._h, self._h, layer, n, d_streams.ptr, d_lens.ptr, max_len,
+                                              n_head_q, d_q.ptr, C.c_float(scale), d_out.ptr))
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None) and self._h.value:
+                lib().vokra_hip_kv_destroy(self._h)
+                self._h = C.c_void_p()
+        except Exception:
+            pass
+
+
 class HipContext:
     """One gfx950 device + stream (mirror of CudaContext::new, context.rs:1167)."""
 
@@ -392,6 +490,9 @@ class HipContext:
         """Enqueue gemm_q_f32 on device buffers against a resident weight."""
         _check(lib().vokra_hip_gemm_q_f32_dev(self._h, w._h, m, d_a.ptr,
                                               None if d_bias is None else d_bias.ptr, d_out.ptr, int(act)))
+
+    def kv_cache(self, n_layer, n_head, d_head, n_stream, max_time, block_size, mode=KvQuant.Q8_0) -> KvCache:
+        return KvCache(self, n_layer, n_head, d_head, n_stream, max_time, block_size, mode)
 
     def qact(self, max_m: int, k: int) -> QAct:
         return QAct(self, max_m, k)
