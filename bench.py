@@ -65,7 +65,15 @@ def bench_q8_gemm(ctx, hip, steps, warmup, act):
         if ev is not None:
             ev[1].record()
 
-    wall_ms, kern_ms = timed_steps(ctx, hip, steps, warmup, launch, "vk_gemm_qblock")
+    wall_ms, _ = timed_steps(ctx, hip, steps, warmup, launch, "vk_gemm_qblock")
+    # the GEMM kernel alone: back-to-back launches on the library's stream
+    # between two HIP events (the per-launch average rocprof reports)
+    e0, e1 = hip.Event(ctx), hip.Event(ctx)
+    e0.record()
+    for _ in range(steps):
+        ctx.gemm_qact_dev(W, qa, d_out)
+    e1.record()
+    kern_ms = e0.elapsed_ms(e1) / steps
     ops = 2.0 * M * N * K
     return {"M": M, "N": N, "K": K, "wall_ms": wall_ms, "gemm_ms": kern_ms,
             "tops": ops / (wall_ms * 1e-3) / 1e12, "gemm_tops": ops / (kern_ms * 1e-3) / 1e12,
@@ -184,6 +192,46 @@ def bench_sdpa(ctx, hip, reps=20, T=1500, H=20, hd=64, batch=1):
             "mfma_passes_per_product": 3}
 
 
+def bench_paged_attn(ctx, hip, n_stream, H, hd, hq, len_lo, len_hi, max_time, reps=50, seed=3):
+    """Decode self-attention over the paged Q8_0 KV cache (one layer), 16-token
+    pages placed at shuffled addresses, per-stream lengths U(len_lo..len_hi).
+    GB/s counts per launch the K and V head slices read (int8 + f16 scale per
+    32 values) for every (stream, key) plus f32 q and out."""
+    rng = np.random.default_rng(seed)
+    bs = 16
+    kv = ctx.kv_cache(1, H, hd, n_stream, max_time, bs)
+    kv.set_free_order(rng.permutation((max_time + bs - 1) // bs).astype(np.int32))
+    lens = rng.integers(len_lo, len_hi + 1, n_stream).astype(np.int32)
+    w = H * hd
+    for t in range(int(lens.max())):
+        live = np.nonzero(lens > t)[0].astype(np.int32)
+        rows = rng.standard_normal((live.size, w), dtype=np.float32)
+        kv.append(0, live, np.full(live.size, t, np.int32), rows, rows)
+    d_st = hip.DeviceBuffer.from_array(ctx, np.arange(n_stream, dtype=np.int32))
+    d_len = hip.DeviceBuffer.from_array(ctx, lens)
+    d_q = hip.DeviceBuffer.from_array(ctx, rng.standard_normal((n_stream, hq * hd), dtype=np.float32))
+    d_out = hip.DeviceBuffer(ctx, n_stream * hq * hd * 4)
+
+    def run():
+        kv.attn_dev(0, n_stream, d_st, d_len, int(lens.max()), hq, d_q, hd ** -0.5, d_out)
+
+    run()
+    ctx.synchronize()
+    e0, e1 = hip.Event(ctx), hip.Event(ctx)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    us = e0.elapsed_ms(e1) * 1e3 / reps
+    nbytes = int(lens.sum()) * 2 * (w + (w // 32) * 2) + 2 * n_stream * hq * hd * 4
+    del kv
+    ctx.synchronize()
+    return {"streams": n_stream, "kv_heads": H, "q_heads": hq, "head_dim": hd, "len_range": [len_lo, len_hi],
+            "keys_total": int(lens.sum()), "us": round(us, 3), "bytes": nbytes,
+            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK["hbm_gbs"], 4)}
+
+
 def bench_copy(ctx, hip, nbytes=1 << 30, reps=5):
     """Plain streaming copy of 1 GiB (4x the 256 MB MALL): the
     achievable-HBM reference and the rocprof byte-counter calibration kernel."""
@@ -218,11 +266,14 @@ def cpu_baseline_q8(a, wq, N, K, budget_s=10.0):
 
 
 def load_traffic(name):
+    """HBM bytes per launch of `name`, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes recorded in profiles/traffic.json (calibrated on a 1 GiB copy)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     try:
-        return json.load(open(path)).get(name)
+        entry = json.load(open(path)).get(name)
+        return None if entry is None else entry["bytes_per_launch"]
     except Exception:
         return None
 
@@ -233,21 +284,44 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", default=None,
+                    help="comma list of single legs to run, one JSON line each (for profiling): "
+                         "gemm, gemm_pow2, copy, gemv, q4k, sdpa, paged")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
-              "(every configured workload fits one MI355X; see DESIGN.md for how it would shard)",
-              file=sys.stderr)
+              "(every configured workload fits one MI355X; the design shards decode batches by "
+              "stream and GEMMs by output column, with no exchange)", file=sys.stderr)
         return 2
 
     from vokra_amd import hip
     ctx = hip.HipContext(0)
+    if args.only:
+        legs = {
+            "gemm": lambda: bench_q8_gemm(ctx, hip, args.steps, args.warmup, hip.ActQuant.AMAX127),
+            "gemm_pow2": lambda: bench_q8_gemm(ctx, hip, args.steps, args.warmup, hip.ActQuant.POW2),
+            "copy": lambda: bench_copy(ctx, hip),
+            "gemv": lambda: [bench_q4_gemv(ctx, hip, n) for n in (5120, 1280)],
+            "q4k": lambda: bench_q4k_decode(ctx, hip),
+            "sdpa": lambda: bench_sdpa(ctx, hip),
+            "paged": lambda: [bench_paged_attn(ctx, hip, 64, 20, 64, 20, 1, 448, 448),
+                              bench_paged_attn(ctx, hip, 32, 2, 128, 16, 512, 4096, 4096)],
+        }
+        for name in args.only.split(","):
+            res = legs[name]()
+            if isinstance(res, dict):
+                res = {k: v for k, v in res.items() if not isinstance(v, np.ndarray)}
+            print(json.dumps({"leg": name, "result": res}), flush=True)
+        ctx.close()
+        return 0
     main_run = bench_q8_gemm(ctx, hip, args.steps, args.warmup, hip.ActQuant.AMAX127)
     pow2_run = bench_q8_gemm(ctx, hip, args.steps, args.warmup, hip.ActQuant.POW2)
     copy_run = bench_copy(ctx, hip)
     gemv_runs = [bench_q4_gemv(ctx, hip, n) for n in (5120, 1280)]
     q4k_run = bench_q4k_decode(ctx, hip)
     sdpa_run = bench_sdpa(ctx, hip)
+    paged_runs = [bench_paged_attn(ctx, hip, 64, 20, 64, 20, 1, 448, 448),
+                  bench_paged_attn(ctx, hip, 32, 2, 128, 16, 512, 4096, 4096)]
 
     M, N, K = main_run["M"], main_run["N"], main_run["K"]
     achieved = main_run["gemm_tops"]
@@ -279,6 +353,7 @@ def main():
             "q4_0_gemv_streamed": gemv_runs,
             "q4_k_decode_layer_m32": q4k_run,
             "sdpa_config1": sdpa_run,
+            "paged_attn_config3_config4": paged_runs,
             "gemm_kernel_ms": round(main_run["gemm_ms"], 4),
             "gemm_frac_of_bf16_mfma_peak": round(achieved / PEAK["bf16_tflops"], 4),
             "pow2_act": {"tops": round(pow2_run["tops"], 2), "gemm_tops": round(pow2_run["gemm_tops"], 2),
