@@ -178,3 +178,18 @@ def test_paged_decreasing_error_across_modes(oracle):
         c.append_step(0, 0, 0, k, np.zeros(64, np.float32))
         errs.append(float(((c.read_step(0, 0, 0)[0] - k) ** 2).sum()))
     assert errs[2] <= errs[1] <= errs[0]
+
+
+def test_rms_norm_reference_case_and_float64(oracle):
+    """text_decoder.rs rms_norm_normalises_row_to_unit_rms (gamma = 1, eps = 0,
+    [1, 2, 3, 4] -> unit RMS), and float64 on random rows with gamma, eps."""
+    out = oracle.rms_norm_f32(np.array([1, 2, 3, 4], np.float32), np.ones(4, np.float32), 0.0, 1, 4)
+    assert abs(float((out.astype(np.float64) ** 2).mean()) - 1.0) < 1e-5
+    assert np.allclose(out[0], np.array([1, 2, 3, 4]) / np.sqrt(7.5), rtol=1e-6)
+    g = np.random.default_rng(12)
+    x = g.standard_normal((6, 128)).astype(np.float32)
+    gamma = g.standard_normal(128).astype(np.float32)
+    got = oracle.rms_norm_f32(x, gamma, 1e-6, 6, 128)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6) * gamma
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
