@@ -200,6 +200,48 @@ int vokra_hip_qact_quantize_dev(vokra_hip_ctx_t *ctx, vokra_hip_qact_t *qa, size
 int vokra_hip_gemm_qact_dev(vokra_hip_ctx_t *ctx, const vokra_hip_qweight_t *w, const vokra_hip_qact_t *qa,
                             const float *d_bias, float *d_out);
 
+/* ---- f32 GEMM / GEMV and row kernels -------------------------------------- */
+
+/* out[m, n] = bias[n] + a[m, k] . b[k, n], f32 (matrix cores in f32: exact
+ * products, f32 sums in tree order). Replaces Compute::gemm_f32
+ * (crates/vokra-models/src/compute.rs:901-920) -> kernels::gemm_f32
+ * (crates/vokra-backend-cpu/src/kernels/mod.rs:298-311, scalar.rs:41-72),
+ * with validate_gemm's checks (mod.rs:238-254); bias has n floats or is NULL. */
+int vokra_hip_gemm_f32(vokra_hip_ctx_t *ctx, size_t m, size_t n, size_t k, const float *a, size_t a_len,
+                       const float *b, size_t b_len, const float *bias, float *out, size_t out_len);
+/* Device pointers; b_trans = 1 reads b as [n, k] (weights stored [out, in],
+ * e.g. the tied token embedding of the logits projection). */
+int vokra_hip_gemm_f32_dev(vokra_hip_ctx_t *ctx, size_t m, size_t n, size_t k, const float *d_a, const float *d_b,
+                           int b_trans, const float *d_bias, float *d_out);
+/* out[m] = bias[m] + a[m, k] . x. Replaces Compute::gemv_f32 (compute.rs:966-985)
+ * -> kernels::gemv_f32 (mod.rs:391-407, scalar.rs:74-91). */
+int vokra_hip_gemv_f32(vokra_hip_ctx_t *ctx, size_t m, size_t k, const float *a, size_t a_len, const float *x,
+                       size_t x_len, const float *bias, float *out, size_t out_len);
+int vokra_hip_gemv_f32_dev(vokra_hip_ctx_t *ctx, size_t m, size_t k, const float *d_a, const float *d_x,
+                           const float *d_bias, float *d_out);
+/* Row softmax (scalar.rs:177-199), LayerNorm with population variance
+ * (scalar.rs:201-222), RMSNorm (crates/vokra-models/src/voxtral/text_decoder.rs:801-822).
+ * Replace Compute::softmax_f32 / layer_norm_f32 (compute.rs:988-1030). */
+int vokra_hip_softmax_f32(vokra_hip_ctx_t *ctx, const float *in, size_t in_len, float *out, size_t out_len,
+                          size_t rows, size_t cols);
+int vokra_hip_layer_norm_f32(vokra_hip_ctx_t *ctx, const float *in, size_t in_len, float *out, size_t out_len,
+                             size_t rows, size_t cols, const float *gamma, size_t gamma_len, const float *beta,
+                             size_t beta_len, float eps);
+int vokra_hip_rms_norm_f32(vokra_hip_ctx_t *ctx, const float *in, size_t in_len, float *out, size_t out_len,
+                           size_t rows, size_t cols, const float *gamma, size_t gamma_len, float eps);
+int vokra_hip_softmax_f32_dev(vokra_hip_ctx_t *ctx, const float *d_in, float *d_out, size_t rows, size_t cols);
+int vokra_hip_layer_norm_f32_dev(vokra_hip_ctx_t *ctx, const float *d_in, float *d_out, size_t rows, size_t cols,
+                                 const float *d_gamma, const float *d_beta, float eps);
+int vokra_hip_rms_norm_f32_dev(vokra_hip_ctx_t *ctx, const float *d_in, float *d_out, size_t rows, size_t cols,
+                               const float *d_gamma, float eps);
+/* GELU through the Abramowitz & Stegun 7.1.26 erf (scalar.rs:126-172).
+ * Replaces Compute::gelu_f32. */
+int vokra_hip_gelu_f32(vokra_hip_ctx_t *ctx, const float *x, float *out, size_t n);
+int vokra_hip_gelu_f32_dev(vokra_hip_ctx_t *ctx, const float *d_x, float *d_out, size_t n);
+/* Per-row argmax, first strict maximum from -inf (crates/vokra-core/src/decode/sampler.rs:197-206). */
+int vokra_hip_argmax_f32_dev(vokra_hip_ctx_t *ctx, const float *d_logits, size_t rows, size_t cols,
+                             int32_t *d_out);
+
 /* ---- fused attention --------------------------------------------------- */
 
 /* Scaled-dot-product attention, f32 in and out, per batch b and query head h

@@ -687,6 +687,194 @@ int vokra_hip_paged_attn(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv, size_t layer, s
     return VOKRA_HIP_OK;
 }
 
+// ---- f32 kernels (A11, A12) -------------------------------------------------
+
+namespace {
+// crates/vokra-backend-cpu/src/kernels/mod.rs:228-236 expect_len
+int expect_len(const char* name, size_t got, size_t want) {
+    if (got == want) return VOKRA_HIP_OK;
+    return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "%s length %zu does not match expected %zu", name, got, want);
+}
+bool fits_int(size_t v) { return v <= (size_t)INT32_MAX; }
+
+// Upload `n` host floats into staging buffer `b` (nothing for n == 0).
+int stage_in(vokra_hip_ctx* c, DevBuf& b, const float* h, size_t n) {
+    VK_TRY(b.ensure(n * sizeof(float) + 16), "hipMalloc");
+    if (n) VK_TRY(hipMemcpyAsync(b.p, h, n * sizeof(float), hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+    return VOKRA_HIP_OK;
+}
+int stage_out(vokra_hip_ctx* c, float* h, const void* d, size_t n) {
+    if (n) VK_TRY(hipMemcpyAsync(h, d, n * sizeof(float), hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(D2H)");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
+}  // namespace
+
+int vokra_hip_gemm_f32_dev(vokra_hip_ctx_t* c, size_t m, size_t n, size_t k, const float* d_a, const float* d_b,
+                           int b_trans, const float* d_bias, float* d_out) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_f32: ctx is NULL");
+    if (!fits_int(m) || !fits_int(n) || !fits_int(k))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_f32: dimension exceeds int32");
+    if (m == 0 || n == 0) return VOKRA_HIP_OK;
+    if (!d_out || (k && (!d_a || !d_b))) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_f32: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_gemm_f32(c->stream, b_trans != 0, d_a, d_b, d_bias, d_out, (int)m, (int)n, (int)k),
+           "launch(vk_gemm_f32)");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_gemm_f32(vokra_hip_ctx_t* c, size_t m, size_t n, size_t k, const float* a, size_t a_len, const float* b,
+                       size_t b_len, const float* bias, float* out, size_t out_len) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_f32: ctx is NULL");
+    size_t mk, kn, mn;
+    if (!mul_ok(m, k, &mk) || !mul_ok(k, n, &kn) || !mul_ok(m, n, &mn))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm: dimension product overflows");
+    int st = expect_len("gemm a", a_len, mk);
+    if (!st) st = expect_len("gemm b", b_len, kn);
+    if (!st) st = expect_len("gemm out", out_len, mn);
+    if (st) return st;
+    if (mn == 0) return VOKRA_HIP_OK;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    if ((st = stage_in(c, c->in0, a, mk)) || (st = stage_in(c, c->in1, b, kn)) ||
+        (st = stage_in(c, c->in2, bias, bias ? n : 0)))
+        return st;
+    VK_TRY(c->out0.ensure(mn * sizeof(float)), "hipMalloc");
+    st = vokra_hip_gemm_f32_dev(c, m, n, k, (const float*)c->in0.p, (const float*)c->in1.p, 0,
+                                bias ? (const float*)c->in2.p : nullptr, (float*)c->out0.p);
+    if (st) return st;
+    return stage_out(c, out, c->out0.p, mn);
+}
+
+int vokra_hip_gemv_f32_dev(vokra_hip_ctx_t* c, size_t m, size_t k, const float* d_a, const float* d_x,
+                           const float* d_bias, float* d_out) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemv_f32: ctx is NULL");
+    if (!fits_int(m) || !fits_int(k)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemv_f32: dimension exceeds int32");
+    if (m == 0) return VOKRA_HIP_OK;
+    if (!d_out || (k && (!d_a || !d_x))) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemv_f32: NULL buffer");
+    if ((k & 3) == 0 && ((reinterpret_cast<uintptr_t>(d_a) | reinterpret_cast<uintptr_t>(d_x)) & 15))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemv_f32: a and x must be 16-byte aligned");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_gemv_f32(c->stream, d_a, d_x, d_bias, d_out, (int)m, (int)k), "launch(vk_gemv_f32)");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_gemv_f32(vokra_hip_ctx_t* c, size_t m, size_t k, const float* a, size_t a_len, const float* x,
+                       size_t x_len, const float* bias, float* out, size_t out_len) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemv_f32: ctx is NULL");
+    size_t mk;
+    if (!mul_ok(m, k, &mk)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemv: dimension product overflows");
+    int st = expect_len("gemv a", a_len, mk);
+    if (!st) st = expect_len("gemv x", x_len, k);
+    if (!st) st = expect_len("gemv out", out_len, m);
+    if (st) return st;
+    if (m == 0) return VOKRA_HIP_OK;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    if ((st = stage_in(c, c->in0, a, mk)) || (st = stage_in(c, c->in1, x, k)) ||
+        (st = stage_in(c, c->in2, bias, bias ? m : 0)))
+        return st;
+    VK_TRY(c->out0.ensure(m * sizeof(float)), "hipMalloc");
+    st = vokra_hip_gemv_f32_dev(c, m, k, (const float*)c->in0.p, (const float*)c->in1.p,
+                                bias ? (const float*)c->in2.p : nullptr, (float*)c->out0.p);
+    if (st) return st;
+    return stage_out(c, out, c->out0.p, m);
+}
+
+// Row ops: op 0 softmax, 1 layer_norm, 2 rms_norm; gamma/beta as the op needs.
+static int row_op_dev(vokra_hip_ctx_t* c, int op, const float* d_in, float* d_out, size_t rows, size_t cols,
+                      const float* d_gamma, const float* d_beta, float eps) {
+    if (!fits_int(rows) || !fits_int(cols)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "row op: dimension exceeds int32");
+    if (rows == 0 || cols == 0) return VOKRA_HIP_OK;
+    if (!d_in || !d_out || (op >= 1 && !d_gamma) || (op == 1 && !d_beta))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "row op: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    hipError_t e = op == 0 ? vk::launch_softmax_f32(c->stream, d_in, d_out, (int)rows, (int)cols)
+                 : op == 1 ? vk::launch_layer_norm_f32(c->stream, d_in, d_out, (int)rows, (int)cols, d_gamma, d_beta, eps)
+                           : vk::launch_rms_norm_f32(c->stream, d_in, d_out, (int)rows, (int)cols, d_gamma, eps);
+    VK_TRY(e, "launch(row op)");
+    return VOKRA_HIP_OK;
+}
+
+static int row_op(vokra_hip_ctx_t* c, int op, const float* in, size_t in_len, float* out, size_t out_len, size_t rows,
+                  size_t cols, const float* gamma, size_t gamma_len, const float* beta, size_t beta_len, float eps) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "row op: ctx is NULL");
+    size_t rc;
+    if (!mul_ok(rows, cols, &rc)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "rows*cols overflows");
+    // validate_rows_cols / validate_layer_norm (kernels/mod.rs:488-536)
+    int st = expect_len("input", in_len, rc);
+    if (!st) st = expect_len("out", out_len, rc);
+    if (!st && op >= 1) st = expect_len("gamma", gamma_len, cols);
+    if (!st && op == 1) st = expect_len("beta", beta_len, cols);
+    if (st) return st;
+    if (rc == 0) return VOKRA_HIP_OK;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    if ((st = stage_in(c, c->in0, in, rc)) || (st = stage_in(c, c->in1, gamma, op >= 1 ? cols : 0)) ||
+        (st = stage_in(c, c->in2, beta, op == 1 ? cols : 0)))
+        return st;
+    VK_TRY(c->out0.ensure(rc * sizeof(float)), "hipMalloc");
+    st = row_op_dev(c, op, (const float*)c->in0.p, (float*)c->out0.p, rows, cols, (const float*)c->in1.p,
+                    (const float*)c->in2.p, eps);
+    if (st) return st;
+    return stage_out(c, out, c->out0.p, rc);
+}
+
+int vokra_hip_softmax_f32(vokra_hip_ctx_t* c, const float* in, size_t in_len, float* out, size_t out_len, size_t rows,
+                          size_t cols) {
+    return row_op(c, 0, in, in_len, out, out_len, rows, cols, nullptr, 0, nullptr, 0, 0.0f);
+}
+int vokra_hip_layer_norm_f32(vokra_hip_ctx_t* c, const float* in, size_t in_len, float* out, size_t out_len,
+                             size_t rows, size_t cols, const float* gamma, size_t gamma_len, const float* beta,
+                             size_t beta_len, float eps) {
+    return row_op(c, 1, in, in_len, out, out_len, rows, cols, gamma, gamma_len, beta, beta_len, eps);
+}
+int vokra_hip_rms_norm_f32(vokra_hip_ctx_t* c, const float* in, size_t in_len, float* out, size_t out_len, size_t rows,
+                           size_t cols, const float* gamma, size_t gamma_len, float eps) {
+    return row_op(c, 2, in, in_len, out, out_len, rows, cols, gamma, gamma_len, nullptr, 0, eps);
+}
+int vokra_hip_softmax_f32_dev(vokra_hip_ctx_t* c, const float* d_in, float* d_out, size_t rows, size_t cols) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "softmax: ctx is NULL");
+    return row_op_dev(c, 0, d_in, d_out, rows, cols, nullptr, nullptr, 0.0f);
+}
+int vokra_hip_layer_norm_f32_dev(vokra_hip_ctx_t* c, const float* d_in, float* d_out, size_t rows, size_t cols,
+                                 const float* d_gamma, const float* d_beta, float eps) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "layer_norm: ctx is NULL");
+    return row_op_dev(c, 1, d_in, d_out, rows, cols, d_gamma, d_beta, eps);
+}
+int vokra_hip_rms_norm_f32_dev(vokra_hip_ctx_t* c, const float* d_in, float* d_out, size_t rows, size_t cols,
+                               const float* d_gamma, float eps) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "rms_norm: ctx is NULL");
+    return row_op_dev(c, 2, d_in, d_out, rows, cols, d_gamma, nullptr, eps);
+}
+
+int vokra_hip_gelu_f32_dev(vokra_hip_ctx_t* c, const float* d_x, float* d_out, size_t n) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gelu: ctx is NULL");
+    if (n == 0) return VOKRA_HIP_OK;
+    if (!d_x || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gelu: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_gelu_f32(c->stream, d_x, d_out, n), "launch(vk_gelu_f32)");
+    return VOKRA_HIP_OK;
+}
+int vokra_hip_gelu_f32(vokra_hip_ctx_t* c, const float* x, float* out, size_t n) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gelu: ctx is NULL");
+    if (n == 0) return VOKRA_HIP_OK;
+    if (!x || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gelu: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    int st = stage_in(c, c->in0, x, n);
+    if (st) return st;
+    VK_TRY(c->out0.ensure(n * sizeof(float)), "hipMalloc");
+    if ((st = vokra_hip_gelu_f32_dev(c, (const float*)c->in0.p, (float*)c->out0.p, n))) return st;
+    return stage_out(c, out, c->out0.p, n);
+}
+
+int vokra_hip_argmax_f32_dev(vokra_hip_ctx_t* c, const float* d_logits, size_t rows, size_t cols, int32_t* d_out) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "argmax: ctx is NULL");
+    if (!fits_int(rows) || !fits_int(cols)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "argmax: dimension exceeds int32");
+    if (rows == 0) return VOKRA_HIP_OK;
+    if (!d_logits || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "argmax: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_argmax_f32(c->stream, d_logits, (int)rows, (int)cols, d_out), "launch(vk_argmax_f32)");
+    return VOKRA_HIP_OK;
+}
+
 int vokra_hip_attn_f32_dev(vokra_hip_ctx_t* c, size_t batch, size_t t_q, size_t t_kv, size_t n_head_q,
                            size_t n_head_kv, size_t head_dim, const float* d_q, const float* d_k, const float* d_v,
                            float scale, int causal, size_t q_offset, float* d_out) {

@@ -1,0 +1,342 @@
+// vk_f32.hip — f32 kernels of the path for gfx950: GEMM / GEMV (matrix cores
+// in f32), row softmax, LayerNorm, RMSNorm, GELU, and the small per-step
+// kernels of a decoder step (residual add, embedding gather, argmax).
+//
+// Semantics are the reference's scalar tier (crates/vokra-backend-cpu/src/
+// kernels/scalar.rs); every per-element expression keeps the reference's
+// operation order, reductions run in a different (tree) order, so results
+// agree to f32 rounding rather than bit for bit.
+#include <algorithm>
+
+#include "vk_common.h"
+
+namespace vk {
+
+// ---------------------------------------------------------------------------
+// GEMM: out[m][n] = bias[n] + sum_l a[m][l] * B(l, n) with B(l, n) = b[l][n]
+// (BT = false, the reference's gemm_f32 layout, scalar.rs:41-72) or b[n][l]
+// (BT = true: weights stored [out, in], e.g. tied embeddings). One workgroup
+// per 64 x 64 output tile, K in chunks of 16 staged K-major in LDS, each wave a
+// 32 x 32 sub-tile of v_mfma_f32_16x16x4_f32 (exact f32 products, f32 sums).
+namespace g32 {
+constexpr int T = 64, KC = 16, PAD = 4;
+}
+
+template <bool BT>
+__global__ __launch_bounds__(256) void vk_gemm_f32(const float* __restrict__ a, const float* __restrict__ b,
+                                                   const float* __restrict__ bias, float* __restrict__ out, int m,
+                                                   int n, int k) {
+    using namespace g32;
+    __shared__ float as[KC][T + PAD];
+    __shared__ float bs[KC][T + PAD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = blockIdx.x * T, m0 = blockIdx.y * T;
+    const int wr = 32 * (wave >> 1), wc = 32 * (wave & 1);
+    // this thread's 4 loads of each tile (out-of-range elements read as 0)
+    const int ar = tid >> 2, ak = (tid & 3) * 4;         // A: row, first k
+    const int bk = BT ? (tid & 3) * 4 : tid >> 4;        // B: first k (BT) or k
+    const int bn = BT ? tid >> 2 : (tid & 15) * 4;       // B: n (BT) or first n
+    float ra[4], rb[4];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int gm = m0 + ar, gk = k0 + ak + j;
+            ra[j] = (gm < m && gk < k) ? a[(size_t)gm * k + gk] : 0.0f;
+            if (BT) {
+                const int gn = n0 + bn, gk2 = k0 + bk + j;
+                rb[j] = (gn < n && gk2 < k) ? b[(size_t)gn * k + gk2] : 0.0f;
+            } else {
+                const int gn = n0 + bn + j, gk2 = k0 + bk;
+                rb[j] = (gn < n && gk2 < k) ? b[(size_t)gk2 * n + gn] : 0.0f;
+            }
+        }
+    };
+    vk_f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = {0.0f, 0.0f, 0.0f, 0.0f};
+    load(0);
+    for (int k0 = 0; k0 < k; k0 += KC) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            as[ak + j][ar] = ra[j];
+            if (BT) bs[bk + j][bn] = rb[j];
+            else bs[bk][bn + j] = rb[j];
+        }
+        __syncthreads();
+        if (k0 + KC < k) load(k0 + KC);
+#pragma unroll
+        for (int s = 0; s < KC / 4; ++s) {
+            const int kk = 4 * s + (lane >> 4);
+            float av[2], bv[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                av[t] = as[kk][wr + 16 * t + (lane & 15)];
+                bv[t] = bs[kk][wc + 16 * t + (lane & 15)];
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int gm = m0 + wr + 16 * i + 4 * (lane >> 4) + r, gn = n0 + wc + 16 * j + (lane & 15);
+                if (gm < m && gn < n) out[(size_t)gm * n + gn] = bias ? bias[gn] + acc[i][j][r] : acc[i][j][r];
+            }
+}
+
+// GEMV: out[i] = bias[i] + a[i][:] . x (scalar.rs:74-91). One wave per row,
+// float4 loads when the row stride allows; the row streams from HBM once.
+__global__ __launch_bounds__(256) void vk_gemv_f32(const float* __restrict__ a, const float* __restrict__ x,
+                                                   const float* __restrict__ bias, float* __restrict__ out, int m,
+                                                   int k) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= m) return;
+    const float* ar = a + (size_t)row * k;
+    float s = 0.0f;
+    if ((k & 3) == 0) {
+        const float4* a4 = reinterpret_cast<const float4*>(ar);
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        for (int i = lane; i < k / 4; i += 64) {
+            const float4 u = a4[i], v = x4[i];
+            s = fmaf(u.x, v.x, s);
+            s = fmaf(u.y, v.y, s);
+            s = fmaf(u.z, v.z, s);
+            s = fmaf(u.w, v.w, s);
+        }
+    } else {
+        for (int i = lane; i < k; i += 64) s = fmaf(ar[i], x[i], s);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, VK_WAVE);
+    if (lane == 0) out[row] = bias ? bias[row] + s : s;
+}
+
+// ---------------------------------------------------------------------------
+// Row reductions over a 256-thread workgroup.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, VK_WAVE);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+__device__ __forceinline__ float block_max(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, VK_WAVE));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// softmax (scalar.rs:177-199): e = exp(x - max), out = e * (1 / sum e).
+__global__ __launch_bounds__(256) void vk_softmax_f32(const float* __restrict__ in, float* __restrict__ out,
+                                                      int cols) {
+    __shared__ float red[4];
+    const float* ir = in + (size_t)blockIdx.x * cols;
+    float* orow = out + (size_t)blockIdx.x * cols;
+    float mx = -INFINITY;
+    for (int c = threadIdx.x; c < cols; c += 256) mx = fmaxf(mx, ir[c]);
+    mx = block_max(mx, red);
+    float s = 0.0f;
+    for (int c = threadIdx.x; c < cols; c += 256) {
+        const float e = expf(ir[c] - mx);
+        orow[c] = e;
+        s += e;
+    }
+    const float inv = 1.0f / block_sum(s, red);
+    for (int c = threadIdx.x; c < cols; c += 256) orow[c] *= inv;
+}
+
+// layer_norm (scalar.rs:201-222): population variance, then
+// (x - mean) * inv_std * gamma + beta per element.
+__global__ __launch_bounds__(256) void vk_layer_norm_f32(const float* __restrict__ in, float* __restrict__ out,
+                                                         int cols, const float* __restrict__ gamma,
+                                                         const float* __restrict__ beta, float eps) {
+    __shared__ float red[4];
+    const float* ir = in + (size_t)blockIdx.x * cols;
+    float* orow = out + (size_t)blockIdx.x * cols;
+    const float inv_cols = 1.0f / (float)cols;
+    float s = 0.0f;
+    for (int c = threadIdx.x; c < cols; c += 256) s += ir[c];
+    const float mean = block_sum(s, red) * inv_cols;
+    float v = 0.0f;
+    for (int c = threadIdx.x; c < cols; c += 256) {
+        const float dlt = ir[c] - mean;
+        v += dlt * dlt;
+    }
+    const float inv_std = 1.0f / sqrtf(block_sum(v, red) * inv_cols + eps);
+    for (int c = threadIdx.x; c < cols; c += 256) orow[c] = (ir[c] - mean) * inv_std * gamma[c] + beta[c];
+}
+
+// rms_norm (crates/vokra-models/src/voxtral/text_decoder.rs:801-822).
+__global__ __launch_bounds__(256) void vk_rms_norm_f32(const float* __restrict__ in, float* __restrict__ out,
+                                                       int cols, const float* __restrict__ gamma, float eps) {
+    __shared__ float red[4];
+    const float* ir = in + (size_t)blockIdx.x * cols;
+    float* orow = out + (size_t)blockIdx.x * cols;
+    float s = 0.0f;
+    for (int c = threadIdx.x; c < cols; c += 256) s += ir[c] * ir[c];
+    const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)cols + eps);
+    for (int c = threadIdx.x; c < cols; c += 256) orow[c] = ir[c] * inv * gamma[c];
+}
+
+// GELU through the Abramowitz & Stegun 7.1.26 erf (scalar.rs:126-172).
+__device__ __forceinline__ float erf_as(float x) {
+    const float P = 0.3275911f, A1 = 0.254829592f, A2 = -0.284496736f, A3 = 1.421413741f, A4 = -1.453152027f,
+                A5 = 1.061405429f;
+    const float sign = x < 0.0f ? -1.0f : 1.0f;
+    const float ax = fabsf(x);
+    const float t = 1.0f / (1.0f + P * ax);
+    const float poly = ((((A5 * t + A4) * t + A3) * t + A2) * t + A1) * t;
+    return sign * (1.0f - poly * expf(-ax * ax));
+}
+__device__ __forceinline__ float gelu_as(float x) { return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752440f)); }
+
+__global__ void vk_gelu_f32(const float* __restrict__ x, float* __restrict__ out, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = gelu_as(x[i]);
+}
+
+// out = a + b (residual connections).
+__global__ void vk_add_f32(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out,
+                           size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = a[i] + b[i];
+}
+
+// h[i] = tok_emb[tokens[i]] + pos_emb[positions[i]] (whisper/decoder.rs:420-432).
+__global__ void vk_embed_f32(const float* __restrict__ tok_emb, const float* __restrict__ pos_emb,
+                             const int* __restrict__ tokens, const int* __restrict__ positions, int vocab,
+                             int n_pos, int d, float* __restrict__ out) {
+    const int i = blockIdx.x;
+    const int t = min(max(tokens[i], 0), vocab - 1), p = min(max(positions[i], 0), n_pos - 1);
+    for (int c = threadIdx.x; c < d; c += blockDim.x)
+        out[(size_t)i * d + c] = tok_emb[(size_t)t * d + c] + pos_emb[(size_t)p * d + c];
+}
+
+// argmax per row, first strict maximum from -inf (decode/sampler.rs:197-206):
+// NaN never wins, ties keep the lowest index.
+__global__ __launch_bounds__(256) void vk_argmax_f32(const float* __restrict__ logits, int cols,
+                                                     int* __restrict__ out) {
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    const float* row = logits + (size_t)blockIdx.x * cols;
+    float bv = -INFINITY;
+    int bi = 0;
+    for (int c = threadIdx.x; c < cols; c += 256)
+        if (row[c] > bv) {
+            bv = row[c];
+            bi = c;
+        }
+    // reduce (value desc, index asc); a lane with no strict max keeps (-inf, 0)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, VK_WAVE);
+        const int oi = __shfl_xor(bi, o, VK_WAVE);
+        if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        rv[threadIdx.x >> 6] = bv;
+        ri[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float v = rv[0];
+        int idx = ri[0];
+        for (int w = 1; w < 4; ++w)
+            if (rv[w] > v || (rv[w] == v && ri[w] < idx)) {
+                v = rv[w];
+                idx = ri[w];
+            }
+        out[blockIdx.x] = idx;
+    }
+}
+
+}  // namespace vk
+
+#include "vk_launch.h"
+
+namespace vk {
+
+hipError_t launch_gemm_f32(hipStream_t s, bool b_trans, const float* a, const float* b, const float* bias,
+                           float* out, int m, int n, int k) {
+    if (m == 0 || n == 0) return hipSuccess;
+    const dim3 grid((n + g32::T - 1) / g32::T, (m + g32::T - 1) / g32::T);
+    if (b_trans)
+        hipLaunchKernelGGL(vk_gemm_f32<true>, grid, dim3(256), 0, s, a, b, bias, out, m, n, k);
+    else
+        hipLaunchKernelGGL(vk_gemm_f32<false>, grid, dim3(256), 0, s, a, b, bias, out, m, n, k);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_f32(hipStream_t s, const float* a, const float* x, const float* bias, float* out, int m,
+                           int k) {
+    if (m == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_gemv_f32, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, s, a, x, bias, out, m, k);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax_f32(hipStream_t s, const float* in, float* out, int rows, int cols) {
+    if (rows == 0 || cols == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_softmax_f32, dim3(rows), dim3(256), 0, s, in, out, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_layer_norm_f32(hipStream_t s, const float* in, float* out, int rows, int cols, const float* gamma,
+                                 const float* beta, float eps) {
+    if (rows == 0 || cols == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_layer_norm_f32, dim3(rows), dim3(256), 0, s, in, out, cols, gamma, beta, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm_f32(hipStream_t s, const float* in, float* out, int rows, int cols, const float* gamma,
+                               float eps) {
+    if (rows == 0 || cols == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_rms_norm_f32, dim3(rows), dim3(256), 0, s, in, out, cols, gamma, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_gelu_f32(hipStream_t s, const float* x, float* out, size_t n) {
+    if (n == 0) return hipSuccess;
+    const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(vk_gelu_f32, dim3(grid), dim3(256), 0, s, x, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_f32(hipStream_t s, const float* a, const float* b, float* out, size_t n) {
+    if (n == 0) return hipSuccess;
+    const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(vk_add_f32, dim3(grid), dim3(256), 0, s, a, b, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_f32(hipStream_t s, const float* tok_emb, const float* pos_emb, const int* tokens,
+                            const int* positions, int vocab, int n_pos, int d, int rows, float* out) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_embed_f32, dim3(rows), dim3(256), 0, s, tok_emb, pos_emb, tokens, positions, vocab, n_pos,
+                       d, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_f32(hipStream_t s, const float* logits, int rows, int cols, int* out) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_argmax_f32, dim3(rows), dim3(256), 0, s, logits, cols, out);
+    return hipGetLastError();
+}
+
+}  // namespace vk

@@ -68,3 +68,20 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
                              const float* q, float scale, int hq, int hd, int n_split, int keys_per_split, float* out,
                              float* part_ml, float* part_o);
 }  // namespace vk
+
+namespace vk {
+hipError_t launch_gemm_f32(hipStream_t s, bool b_trans, const float* a, const float* b, const float* bias,
+                           float* out, int m, int n, int k);
+hipError_t launch_gemv_f32(hipStream_t s, const float* a, const float* x, const float* bias, float* out, int m,
+                           int k);
+hipError_t launch_softmax_f32(hipStream_t s, const float* in, float* out, int rows, int cols);
+hipError_t launch_layer_norm_f32(hipStream_t s, const float* in, float* out, int rows, int cols, const float* gamma,
+                                 const float* beta, float eps);
+hipError_t launch_rms_norm_f32(hipStream_t s, const float* in, float* out, int rows, int cols, const float* gamma,
+                               float eps);
+hipError_t launch_gelu_f32(hipStream_t s, const float* x, float* out, size_t n);
+hipError_t launch_add_f32(hipStream_t s, const float* a, const float* b, float* out, size_t n);
+hipError_t launch_embed_f32(hipStream_t s, const float* tok_emb, const float* pos_emb, const int* tokens,
+                            const int* positions, int vocab, int n_pos, int d, int rows, float* out);
+hipError_t launch_argmax_f32(hipStream_t s, const float* logits, int rows, int cols, int* out);
+}  // namespace vk

@@ -128,6 +128,19 @@ def _declare(L):
     L.vokra_hip_kv_set_free_order.argtypes = [P, P, i32p, sz]
     L.vokra_hip_paged_attn.argtypes = [P, P, sz, sz, i32p, i32p, sz, f32p, C.c_float, f32p]
     L.vokra_hip_paged_attn_dev.argtypes = [P, P, sz, sz, P, P, sz, sz, P, C.c_float, P]
+    L.vokra_hip_gemm_f32.argtypes = [P, sz, sz, sz, f32p, sz, f32p, sz, f32p, f32p, sz]
+    L.vokra_hip_gemm_f32_dev.argtypes = [P, sz, sz, sz, P, P, C.c_int, P, P]
+    L.vokra_hip_gemv_f32.argtypes = [P, sz, sz, f32p, sz, f32p, sz, f32p, f32p, sz]
+    L.vokra_hip_gemv_f32_dev.argtypes = [P, sz, sz, P, P, P, P]
+    L.vokra_hip_softmax_f32.argtypes = [P, f32p, sz, f32p, sz, sz, sz]
+    L.vokra_hip_layer_norm_f32.argtypes = [P, f32p, sz, f32p, sz, sz, sz, f32p, sz, f32p, sz, C.c_float]
+    L.vokra_hip_rms_norm_f32.argtypes = [P, f32p, sz, f32p, sz, sz, sz, f32p, sz, C.c_float]
+    L.vokra_hip_softmax_f32_dev.argtypes = [P, P, P, sz, sz]
+    L.vokra_hip_layer_norm_f32_dev.argtypes = [P, P, P, sz, sz, P, P, C.c_float]
+    L.vokra_hip_rms_norm_f32_dev.argtypes = [P, P, P, sz, sz, P, C.c_float]
+    L.vokra_hip_gelu_f32.argtypes = [P, f32p, f32p, sz]
+    L.vokra_hip_gelu_f32_dev.argtypes = [P, P, P, sz]
+    L.vokra_hip_argmax_f32_dev.argtypes = [P, P, sz, sz, P]
     L.vokra_hip_attn_f32.argtypes = [P, sz, sz, sz, sz, sz, sz, f32p, f32p, f32p, C.c_float, C.c_int, sz, f32p]
     L.vokra_hip_attn_f32_dev.argtypes = [P, sz, sz, sz, sz, sz, sz, P, P, P, C.c_float, C.c_int, sz, P]
 
@@ -496,6 +509,58 @@ class HipContext:
 
     def qact(self, max_m: int, k: int) -> QAct:
         return QAct(self, max_m, k)
+
+    # ---- f32 kernels (compute.rs:901-1076) ---------------------------------
+    def gemm_f32(self, m, n, k, a, b, bias=None):
+        av, bv = _f32(a).reshape(-1), _f32(b).reshape(-1)
+        cv = None if bias is None else _f32(bias)
+        out = np.zeros(max(m * n, 1), np.float32)
+        _check(lib().vokra_hip_gemm_f32(self._h, m, n, k, _ptr(av, C.c_float), av.size, _ptr(bv, C.c_float), bv.size,
+                                        _ptr(cv, C.c_float), _ptr(out, C.c_float), m * n))
+        return out[:m * n].reshape(m, n)
+
+    def gemm_f32_dev(self, m, n, k, d_a, d_b, d_out, d_bias=None, b_trans=False):
+        _check(lib().vokra_hip_gemm_f32_dev(self._h, m, n, k, d_a.ptr, d_b.ptr, int(bool(b_trans)),
+                                            None if d_bias is None else d_bias.ptr, d_out.ptr))
+
+    def gemv_f32(self, m, k, a, x, bias=None):
+        av, xv = _f32(a).reshape(-1), _f32(x).reshape(-1)
+        cv = None if bias is None else _f32(bias)
+        out = np.zeros(max(m, 1), np.float32)
+        _check(lib().vokra_hip_gemv_f32(self._h, m, k, _ptr(av, C.c_float), av.size, _ptr(xv, C.c_float), xv.size,
+                                        _ptr(cv, C.c_float), _ptr(out, C.c_float), m))
+        return out[:m]
+
+    def softmax_f32(self, x, rows, cols):
+        xv = _f32(x).reshape(-1)
+        out = np.zeros(max(xv.size, 1), np.float32)
+        _check(lib().vokra_hip_softmax_f32(self._h, _ptr(xv, C.c_float), xv.size, _ptr(out, C.c_float), xv.size,
+                                           rows, cols))
+        return out[:xv.size].reshape(rows, cols)
+
+    def layer_norm_f32(self, x, rows, cols, gamma, beta, eps=1e-5):
+        xv, g, b = _f32(x).reshape(-1), _f32(gamma), _f32(beta)
+        out = np.zeros(max(xv.size, 1), np.float32)
+        _check(lib().vokra_hip_layer_norm_f32(self._h, _ptr(xv, C.c_float), xv.size, _ptr(out, C.c_float), xv.size,
+                                              rows, cols, _ptr(g, C.c_float), g.size, _ptr(b, C.c_float), b.size,
+                                              C.c_float(eps)))
+        return out[:xv.size].reshape(rows, cols)
+
+    def rms_norm_f32(self, x, rows, cols, gamma, eps):
+        xv, g = _f32(x).reshape(-1), _f32(gamma)
+        out = np.zeros(max(xv.size, 1), np.float32)
+        _check(lib().vokra_hip_rms_norm_f32(self._h, _ptr(xv, C.c_float), xv.size, _ptr(out, C.c_float), xv.size,
+                                            rows, cols, _ptr(g, C.c_float), g.size, C.c_float(eps)))
+        return out[:xv.size].reshape(rows, cols)
+
+    def gelu_f32(self, x):
+        xv = _f32(x).reshape(-1)
+        out = np.zeros(max(xv.size, 1), np.float32)
+        _check(lib().vokra_hip_gelu_f32(self._h, _ptr(xv, C.c_float), _ptr(out, C.c_float), xv.size))
+        return out[:xv.size]
+
+    def argmax_f32_dev(self, d_logits, rows, cols, d_out):
+        _check(lib().vokra_hip_argmax_f32_dev(self._h, d_logits.ptr, rows, cols, d_out.ptr))
 
     # ---- attention ----------------------------------------------------------
     def attn_f32(self, q, k, v, n_head_q: int, n_head_kv: int = None, scale: float = None,
