@@ -330,6 +330,96 @@ int vokra_hip_paged_attn_dev(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t la
                              const int32_t *d_streams, const int32_t *d_lens, size_t max_len, size_t n_head_q,
                              const float *d_q, float scale, float *d_out);
 
+/* out = a + b on device (residual connections; add_assign in the reference's
+ * model code, crates/vokra-models/src/whisper/nn.rs). */
+int vokra_hip_add_f32_dev(vokra_hip_ctx_t *ctx, const float *d_a, const float *d_b, float *d_out, size_t n);
+
+/* ---- pre-norm encoder session ------------------------------------------- */
+
+/* One pre-norm block with quantized linears: wire-format weights [out, in]
+ * (block or K-quant dtype), f32 norms and biases (NULL = no bias). The quant
+ * counterpart of PrenormLayer (crates/vokra-core/src/prenorm.rs), which the
+ * reference holds in f32 only. */
+typedef struct vokra_hip_prenorm_layer {
+    const float *ln1_gamma, *ln1_beta;
+    const uint8_t *wq, *wk, *wv, *wo;  /* [d, d] */
+    const float *bq, *bk, *bv, *bo;
+    const float *ln2_gamma, *ln2_beta;
+    const uint8_t *w1, *w2;            /* fc1 [d_ff, d], fc2 [d, d_ff] */
+    const float *b1, *b2;
+} vokra_hip_prenorm_layer_t;
+
+typedef struct vokra_hip_encoder vokra_hip_encoder_t;
+
+/* Device-resident encoder: uploads every layer once (the reference's
+ * Compute::encode_prenorm_encoder, crates/vokra-models/src/compute.rs:2775, over
+ * the blocks of crates/vokra-models/src/whisper/encoder.rs:180-245). max_rows
+ * bounds batch * frames of a forward. */
+int vokra_hip_encoder_create(vokra_hip_ctx_t *ctx, int wdtype, size_t n_layer, size_t d_model, size_t n_head,
+                             size_t d_ff, const vokra_hip_prenorm_layer_t *layers, const float *ln_post_gamma,
+                             const float *ln_post_beta, size_t max_rows, vokra_hip_encoder_t **out);
+void vokra_hip_encoder_destroy(vokra_hip_encoder_t *enc);
+/* x [batch, frames, d] (the conv stem's output) -> out [batch, frames, d]:
+ * per block h += attn(LN1 h) (non-causal, scale head_dim^-0.5), h += MLP(LN2 h)
+ * with GELU, then ln_post. Device pointers, asynchronous. */
+int vokra_hip_encoder_forward_dev(vokra_hip_ctx_t *ctx, vokra_hip_encoder_t *enc, size_t batch, size_t frames,
+                                  const float *d_x, float *d_out);
+/* Host arrays, synchronous. */
+int vokra_hip_encoder_forward(vokra_hip_ctx_t *ctx, vokra_hip_encoder_t *enc, size_t batch, size_t frames,
+                              const float *x, float *out);
+
+/* ---- batched decoder-step session --------------------------------------- */
+
+/* One Whisper decoder block with quantized linears (the quant counterpart of
+ * DecoderLayerView, crates/vokra-core/src/prenorm.rs). */
+typedef struct vokra_hip_decoder_layer {
+    const float *ln1_gamma, *ln1_beta;            /* self-attention LN */
+    const uint8_t *wq, *wk, *wv, *wo;
+    const float *bq, *bk, *bv, *bo;
+    const float *ln2_gamma, *ln2_beta;            /* cross-attention LN */
+    const uint8_t *cwq, *cwk, *cwv, *cwo;
+    const float *cbq, *cbk, *cbv, *cbo;
+    const float *ln3_gamma, *ln3_beta;            /* MLP LN */
+    const uint8_t *w1, *w2;
+    const float *b1, *b2;
+} vokra_hip_decoder_layer_t;
+
+typedef struct vokra_hip_decoder vokra_hip_decoder_t;
+
+/* Device-resident batched decoder for n_stream concurrent streams: quantized
+ * weights, f32 token/positional embeddings (the token embedding doubles as the
+ * tied output projection), a paged Q8_0 self-KV cache (block_size-token pages)
+ * and per-stream cross K/V. Replaces Compute::new_decoder_step_session /
+ * DecoderStepSession (crates/vokra-models/src/compute.rs:2892-3139) with the
+ * batch axis the reference lacks. */
+int vokra_hip_decoder_create(vokra_hip_ctx_t *ctx, int wdtype, size_t n_layer, size_t d_model, size_t n_head,
+                             size_t d_ff, size_t n_vocab, size_t n_text_ctx, size_t n_audio_ctx, size_t n_stream,
+                             size_t block_size, const vokra_hip_decoder_layer_t *layers, const float *token_emb,
+                             const float *pos_emb, const float *ln_post_gamma, const float *ln_post_beta,
+                             vokra_hip_decoder_t **out);
+void vokra_hip_decoder_destroy(vokra_hip_decoder_t *dec);
+/* Sets stream `stream`'s cross K/V from its encoder output enc [n_audio_ctx, d]
+ * for every layer (k = enc.Wk + bk, v = enc.Wv + bv, as
+ * cross_attention_capture, crates/vokra-models/src/whisper/nn.rs:342-399). */
+int vokra_hip_decoder_set_encoder(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t stream, const float *enc);
+int vokra_hip_decoder_set_encoder_dev(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t stream,
+                                      const float *d_enc);
+/* Empties the self-KV cache of every stream. */
+int vokra_hip_decoder_reset(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec);
+/* One decode step of n streams (distinct): stream streams[i] feeds token
+ * tokens[i] at position positions[i] (its current length). Per stream this is
+ * WhisperDecoder::step_into (crates/vokra-models/src/whisper/decoder.rs:413-567)
+ * with one token, then greedy argmax (decode/sampler.rs:197-206) into
+ * next_tokens[i]; logits [n, n_vocab] are written when not NULL. Host arrays,
+ * synchronous; rejects token >= n_vocab and position >= n_text_ctx as the
+ * reference does. */
+int vokra_hip_decoder_step(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t n, const int32_t *streams,
+                           const int32_t *tokens, const int32_t *positions, int32_t *next_tokens, float *logits);
+/* Device arrays, asynchronous (capturable in a HIP graph once warmed up). */
+int vokra_hip_decoder_step_dev(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t n, const int32_t *d_streams,
+                               const int32_t *d_tokens, const int32_t *d_positions, int32_t *d_next_tokens,
+                               float *d_logits);
+
 #ifdef __cplusplus
 }
 #endif

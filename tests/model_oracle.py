@@ -1,0 +1,85 @@
+"""Encoder blocks and decoder steps composed from the oracle's restatements
+(test infrastructure): the sequence of crates/vokra-models/src/whisper/
+encoder.rs:180-245 and decoder.rs:413-567, with every linear through the
+oracle's block-INT8 gemm_q_f32 (the definition the GPU implements bit for bit)
+and the self-attention K/V through the QuantizedPagedKvCache restatement (Q8_0
+rows), one stream at a time."""
+import numpy as np
+
+Q8_0_MODE = 3
+LN_EPS = 1e-5
+
+
+def qlin(orc, wd, x, w, n, k, b=None):
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, k)
+    return orc.gemm_q_f32(wd, x.shape[0], n, k, x, w, b)
+
+
+def ln(orc, x, g, b):
+    x = np.ascontiguousarray(x, np.float32)
+    rows = x.size // g.size
+    return orc.layer_norm_f32(x, rows, g.size, g, b, LN_EPS).reshape(x.shape)
+
+
+def encoder(orc, wd, layers, lnp_g, lnp_b, x, n_head, d_ff):
+    """x [B, T, d] -> [B, T, d] (pre-norm blocks, then ln_post)."""
+    B, T, d = x.shape
+    hd = d // n_head
+    out = np.zeros_like(x)
+    for b in range(B):
+        h = x[b].astype(np.float32).copy()
+        for L in layers:
+            xn = ln(orc, h, L["ln1_gamma"], L["ln1_beta"])
+            q = qlin(orc, wd, xn, L["wq"], d, d, L.get("bq"))
+            k = qlin(orc, wd, xn, L["wk"], d, d, L.get("bk"))
+            v = qlin(orc, wd, xn, L["wv"], d, d, L.get("bv"))
+            a = orc.sdpa_whisper(T, T, n_head, hd, q, k, v)
+            h = h + qlin(orc, wd, a, L["wo"], d, d, L.get("bo"))
+            xn = ln(orc, h, L["ln2_gamma"], L["ln2_beta"])
+            f = orc.gelu_f32(qlin(orc, wd, xn, L["w1"], d_ff, d, L.get("b1")).reshape(-1)).reshape(T, d_ff)
+            h = h + qlin(orc, wd, f, L["w2"], d, d_ff, L.get("b2"))
+        out[b] = ln(orc, h, lnp_g, lnp_b)
+    return out
+
+
+class Decoder:
+    """Per-stream greedy decoder step with a Q8_0 paged self-KV cache."""
+
+    def __init__(self, orc, wd, layers, tok_emb, pos_emb, lnp_g, lnp_b, n_head, d_ff, n_stream, n_text, bs):
+        self.orc, self.wd, self.layers = orc, wd, layers
+        self.tok_emb, self.pos_emb, self.lnp = tok_emb, pos_emb, (lnp_g, lnp_b)
+        self.d = tok_emb.shape[1]
+        self.n_head, self.hd, self.d_ff = n_head, self.d // n_head, d_ff
+        self.cache = orc.PagedCache(len(layers), n_head, self.hd, n_stream, n_text, bs, Q8_0_MODE)
+        self.cross = {}
+
+    def set_encoder(self, s, enc):
+        o, d = self.orc, self.d
+        self.cross[s] = [(qlin(o, self.wd, enc, L["cwk"], d, d, L.get("cbk")),
+                          qlin(o, self.wd, enc, L["cwv"], d, d, L.get("cbv"))) for L in self.layers]
+
+    def step(self, s, token, pos):
+        o, d, wd, H, hd = self.orc, self.d, self.wd, self.n_head, self.hd
+        h = (self.tok_emb[token] + self.pos_emb[pos]).astype(np.float32)[None]
+        for li, L in enumerate(self.layers):
+            xn = ln(o, h, L["ln1_gamma"], L["ln1_beta"])
+            q = qlin(o, wd, xn, L["wq"], d, d, L.get("bq"))
+            k = qlin(o, wd, xn, L["wk"], d, d, L.get("bk"))
+            v = qlin(o, wd, xn, L["wv"], d, d, L.get("bv"))
+            assert self.cache.append_step(li, pos, s, k[0], v[0]) == 0
+            rows = [self.cache.read_step(li, t, s) for t in range(pos + 1)]
+            K = np.stack([r[0] for r in rows])
+            V = np.stack([r[1] for r in rows])
+            a = o.sdpa_whisper(1, pos + 1, H, hd, q, K, V, causal=True, q_pos_offset=pos)
+            h = h + qlin(o, wd, a, L["wo"], d, d, L.get("bo"))
+            xn = ln(o, h, L["ln2_gamma"], L["ln2_beta"])
+            cq = qlin(o, wd, xn, L["cwq"], d, d, L.get("cbq"))
+            CK, CV = self.cross[s][li]
+            a = o.sdpa_whisper(1, CK.shape[0], H, hd, cq, CK, CV)
+            h = h + qlin(o, wd, a, L["cwo"], d, d, L.get("cbo"))
+            xn = ln(o, h, L["ln3_gamma"], L["ln3_beta"])
+            f = o.gelu_f32(qlin(o, wd, xn, L["w1"], self.d_ff, d, L.get("b1")).reshape(-1))
+            h = h + qlin(o, wd, f, L["w2"], d, self.d_ff, L.get("b2"))
+        xn = ln(o, h, *self.lnp)
+        logits = o.gemv_f32(self.tok_emb.shape[0], d, self.tok_emb, xn[0])
+        return logits, o.argmax(logits)

@@ -1,0 +1,197 @@
+"""GPU parity of the device-resident encoder and batched decoder-step sessions.
+
+Two bars:
+  * exact composition: an encoder forward is bit-identical to the same kernels
+    issued one entry point at a time (each covered by its own parity tests);
+    a batched decoder step is bit-identical to stepping the same streams one at
+    a time (every kernel on the path is row-independent);
+  * against the oracle composition (tests/model_oracle.py), which runs the same
+    INT8 linears on inputs that differ only by f32 rounding in LayerNorm, GELU
+    and attention: where one activation sits within an ulp of an INT8 rounding
+    boundary the two quantize one step apart, and that step then spreads
+    through later layers. Bar: max |gpu - oracle| <= 0.1 * rms(oracle), and
+    greedy tokens agree wherever the oracle's top-2 logit gap exceeds that.
+"""
+import numpy as np
+import pytest
+
+from tests import model_oracle
+from vokra_amd import hip
+
+pytestmark = pytest.mark.gpu
+
+W_Q4_0, W_Q8_0, W_Q4_K = 2, 8, 12
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = hip.HipContext(0)
+    yield c
+    c.close()
+
+
+def pack(ctx, wd, w):
+    """f32 [n, k] -> wire bytes of `wd` (device packer; Q4_K via the oracle quantizer)."""
+    if wd == W_Q4_K:
+        from oracle import oracle as orc
+        return orc.kquant_quantize(W_Q4_K, w.reshape(-1))
+    mode = {W_Q4_0: hip.KvQuant.Q4_0, W_Q8_0: hip.KvQuant.Q8_0}[wd]
+    return ctx.quantize_bytes(mode, w)
+
+
+def rand_norm(g, d):
+    return (1.0 + 0.1 * g.standard_normal(d)).astype(np.float32), (0.1 * g.standard_normal(d)).astype(np.float32)
+
+
+def enc_layer(ctx, g, wd, d, ff, scale=0.08):
+    L = {}
+    L["ln1_gamma"], L["ln1_beta"] = rand_norm(g, d)
+    L["ln2_gamma"], L["ln2_beta"] = rand_norm(g, d)
+    for name, n, k in (("wq", d, d), ("wk", d, d), ("wv", d, d), ("wo", d, d), ("w1", ff, d), ("w2", d, ff)):
+        L[name] = pack(ctx, wd, (g.standard_normal((n, k)) * scale).astype(np.float32))
+    for name, n in (("bq", d), ("bv", d), ("bo", d), ("b1", ff), ("b2", d)):
+        L[name] = (0.05 * g.standard_normal(n)).astype(np.float32)
+    return L  # no bk: Whisper's k projection has no bias
+
+
+def within(got, want, frac=0.1):
+    rms = float(np.sqrt(np.mean(np.asarray(want, np.float64) ** 2)))
+    err = float(np.max(np.abs(np.asarray(got, np.float64) - want)))
+    return err <= frac * rms + 1e-4, err, rms
+
+
+def encoder_by_ops(ctx, wd, layers, lpg, lpb, x, H, ff):
+    """The encoder forward issued one C-ABI entry point at a time."""
+    W = hip.WDtype(wd)
+    B, T, d = x.shape
+    h = x.reshape(B * T, d).copy()
+    for L in layers:
+        xn = ctx.layer_norm_f32(h, B * T, d, L["ln1_gamma"], L["ln1_beta"])
+        q, k, v = (ctx.gemm_q_f32(B * T, d, d, xn, L[w], W, bias=L.get(b)).reshape(B, T, d)
+                   for w, b in (("wq", "bq"), ("wk", "bk"), ("wv", "bv")))
+        a = ctx.attn_f32(q, k, v, H).reshape(B * T, d)
+        h = ctx.gemm_q_f32(B * T, d, d, a, L["wo"], W, bias=L.get("bo")) + h
+        xn = ctx.layer_norm_f32(h, B * T, d, L["ln2_gamma"], L["ln2_beta"])
+        f = ctx.gelu_f32(ctx.gemm_q_f32(B * T, ff, d, xn, L["w1"], W, bias=L.get("b1"))).reshape(B * T, ff)
+        h = ctx.gemm_q_f32(B * T, d, ff, f, L["w2"], W, bias=L.get("b2")) + h
+    return ctx.layer_norm_f32(h, B * T, d, lpg, lpb).reshape(B, T, d)
+
+
+@pytest.mark.parametrize("wd,d,H,ff,T,B", [(W_Q8_0, 128, 2, 256, 70, 2), (W_Q4_0, 128, 2, 256, 64, 1),
+                                           (W_Q4_K, 256, 4, 512, 33, 1)])
+def test_encoder_vs_oracle(ctx, oracle, wd, d, H, ff, T, B):
+    print(f"[case] encoder wd={wd} d={d} H={H} T={T} B={B}", flush=True)
+    g = np.random.default_rng(d + T + wd)
+    layers = [enc_layer(ctx, g, wd, d, ff) for _ in range(2)]
+    lpg, lpb = rand_norm(g, d)
+    x = g.standard_normal((B, T, d)).astype(np.float32)
+    enc = hip.Encoder(ctx, wd, d, H, ff, layers, lpg, lpb, max_rows=B * T)
+    got = enc.forward(x)
+    assert np.array_equal(got, encoder_by_ops(ctx, wd, layers, lpg, lpb, x, H, ff))
+    if B > 1:  # batch invariance
+        assert np.array_equal(got[1:2], enc.forward(x[1:2]))
+    want = model_oracle.encoder(oracle, wd, layers, lpg, lpb, x, H, ff)
+    ok, err, rms = within(got, want)
+    assert ok, (err, rms)
+
+
+def test_encoder_config0_layer_full_length(ctx, oracle):
+    """Whisper-base dims (d=512, 8 heads, FFN 2048), 1500 frames, one block."""
+    print("[case] encoder config0 one layer T=1500", flush=True)
+    d, H, ff, T = 512, 8, 2048, 1500
+    g = np.random.default_rng(1500)
+    layers = [enc_layer(ctx, g, W_Q8_0, d, ff, scale=0.02)]
+    lpg, lpb = rand_norm(g, d)
+    x = g.standard_normal((1, T, d)).astype(np.float32)
+    enc = hip.Encoder(ctx, W_Q8_0, d, H, ff, layers, lpg, lpb, max_rows=T)
+    got = enc.forward(x)
+    want = model_oracle.encoder(oracle, W_Q8_0, layers, lpg, lpb, x, H, ff)
+    ok, err, rms = within(got, want)
+    assert ok, (err, rms)
+
+
+def dec_layer(ctx, g, wd, d, ff, scale=0.08):
+    L = enc_layer(ctx, g, wd, d, ff, scale)
+    L["ln3_gamma"], L["ln3_beta"] = rand_norm(g, d)
+    for name in ("cwq", "cwk", "cwv", "cwo"):
+        L[name] = pack(ctx, wd, (g.standard_normal((d, d)) * scale).astype(np.float32))
+    for name in ("cbq", "cbv", "cbo"):
+        L[name] = (0.05 * g.standard_normal(d)).astype(np.float32)
+    return L
+
+
+def make_decoder(ctx, oracle, g, wd=W_Q4_0, d=128, H=2, ff=256, V=300, n_text=24, n_audio=70, n_stream=4,
+                 n_layer=2, bs=4):
+    layers = [dec_layer(ctx, g, wd, d, ff) for _ in range(n_layer)]
+    tok = (g.standard_normal((V, d)) * 0.5).astype(np.float32)
+    pos = (g.standard_normal((n_text, d)) * 0.1).astype(np.float32)
+    lpg, lpb = rand_norm(g, d)
+    gpu = hip.Decoder(ctx, wd, d, H, ff, V, n_text, n_audio, n_stream, layers, tok, pos, lpg, lpb, block_size=bs)
+    ref = model_oracle.Decoder(oracle, wd, layers, tok, pos, lpg, lpb, H, ff, n_stream, n_text, bs)
+    encs = [g.standard_normal((n_audio, d)).astype(np.float32) for _ in range(n_stream)]
+    for s in range(n_stream):
+        gpu.set_encoder(s, encs[s])
+        ref.set_encoder(s, encs[s])
+    return gpu, ref
+
+
+def test_decoder_batch_equals_single_stream_steps(ctx, oracle):
+    """Two sessions with identical weights: one steps all streams together,
+    the other one stream at a time; logits and tokens are bit-identical."""
+    print("[case] decoder batch == single", flush=True)
+    a, _ = make_decoder(ctx, oracle, np.random.default_rng(11))
+    b, _ = make_decoder(ctx, oracle, np.random.default_rng(11))
+    tok, pos = [3, 7, 11, 13], [0, 0, 0, 0]
+    for _ in range(5):
+        na, la = a.step([0, 1, 2, 3], tok, pos, want_logits=True)
+        for i, s in enumerate([3, 1, 0, 2]):
+            nb, lb = b.step([s], [tok[s]], [pos[s]], want_logits=True)
+            assert np.array_equal(lb[0], la[s]) and nb[0] == na[s], s
+        tok, pos = [int(t) for t in na], [p + 1 for p in pos]
+
+
+def test_decoder_steps_vs_oracle(ctx, oracle):
+    """Ragged batches: streams join late and skip steps; tokens follow the
+    GPU's greedy choice in both paths."""
+    print("[case] decoder steps", flush=True)
+    g = np.random.default_rng(42)
+    gpu, ref = make_decoder(ctx, oracle, g)
+    pos = [0, 0, 0, 0]
+    tok = [1, 2, 3, 4]
+    schedule = [[0, 1, 2], [0, 1, 2], [2, 0, 3], [3, 1], [0, 1, 2, 3], [1, 3], [0, 2, 3, 1]]
+    for step, streams in enumerate(schedule):
+        nxt, logits = gpu.step(streams, [tok[s] for s in streams], [pos[s] for s in streams], want_logits=True)
+        for i, s in enumerate(streams):
+            want, want_tok = ref.step(s, tok[s], pos[s])
+            ok, err, rms = within(logits[i], want)
+            assert ok, (step, s, err, rms)
+            top2 = np.sort(want)[-2:]
+            if top2[1] - top2[0] > 0.1 * rms + 1e-4:
+                assert nxt[i] == want_tok, (step, s)
+            tok[s], pos[s] = int(nxt[i]), pos[s] + 1
+
+
+def test_decoder_reset_replays_identically(ctx, oracle):
+    print("[case] decoder reset", flush=True)
+    g = np.random.default_rng(7)
+    gpu, _ = make_decoder(ctx, oracle, g)
+    first = [gpu.step([0, 1], [5, 6], [p, p], want_logits=True)[1] for p in range(3)]
+    gpu.reset()
+    again = [gpu.step([0, 1], [5, 6], [p, p], want_logits=True)[1] for p in range(3)]
+    for a, b in zip(first, again):
+        assert np.array_equal(a, b)
+
+
+def test_decoder_rejections(ctx, oracle):
+    g = np.random.default_rng(8)
+    gpu, _ = make_decoder(ctx, oracle, g)
+    with pytest.raises(hip.InvalidArgument, match="n_vocab"):
+        gpu.step([0], [300], [0])
+    with pytest.raises(hip.InvalidArgument, match="n_text_ctx"):
+        gpu.step([0], [1], [24])
+    with pytest.raises(hip.InvalidArgument, match="distinct"):
+        gpu.step([1, 1], [1, 2], [0, 0])
+    with pytest.raises(hip.UnsupportedOp):
+        hip.Decoder(ctx, W_Q4_0, 160, 2, 256, 10, 4, 8, 1, [dec_layer(ctx, g, W_Q4_0, 160, 256)],
+                    np.zeros((10, 160), np.float32), np.zeros((4, 160), np.float32),
+                    np.ones(160, np.float32), np.zeros(160, np.float32))

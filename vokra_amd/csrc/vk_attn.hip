@@ -90,7 +90,8 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
     const uint4* __restrict__ qh, const uint4* __restrict__ ql,    // [B][Tq][Hq*HD] fp16, scaled
     const uint4* __restrict__ kh, const uint4* __restrict__ kl,    // [B][Tkv][Hkv*HD] fp16
     const uint4* __restrict__ vth, const uint4* __restrict__ vtl,  // [B][Hkv][HD][Tpad] fp16
-    float* __restrict__ out, int tq, int tkv, int t_pad, int hq, int hkv, int causal, int q_off) {
+    float* __restrict__ out, int tq, int tkv, int t_pad, int hq, int hkv, int causal, int q_off,
+    const int* __restrict__ kv_index) {
     using namespace attn;
     constexpr int KS = HD / 32;      // 32-wide K steps of S = K . Q^T
     constexpr int OS = HD / 16;      // 16-row output subtiles of O^T
@@ -103,6 +104,7 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, lq = lane & 15;
     const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int kb = kv_index ? kv_index[b] : b;  // K/V batch of query batch b
     const int hk = h / (hq / hkv);
     const int q_idx = qt * QT + wave * 16 + lq;  // this lane's query
     const int q_ld = min(q_idx, tq - 1);
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
             const int idx = tid + 256 * i;
             const int r = idx / (HD / 8), c = idx % (HD / 8);
             const int t = min(kt * KT + r, tkv - 1);
-            const size_t o = ((size_t)b * tkv + t) * kw + (size_t)hk * HD / 8 + c;
+            const size_t o = ((size_t)kb * tkv + t) * kw + (size_t)hk * HD / 8 + c;
             st.kh[i] = kh4[o];
             st.kl[i] = kl4[o];
         }
@@ -146,7 +148,7 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
         for (int i = 0; i < VU4; ++i) {
             const int idx = tid + 256 * i;
             const int r = idx / (KT / 8), c = idx % (KT / 8);
-            const size_t o = (((size_t)b * hkv + hk) * HD + r) * (t_pad / 8) + (size_t)kt * KT / 8 + c;
+            const size_t o = (((size_t)kb * hkv + hk) * HD + r) * (t_pad / 8) + (size_t)kt * KT / 8 + c;
             st.vh[i] = vh4[o];
             st.vl[i] = vl4[o];
         }
@@ -304,16 +306,16 @@ hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, i
 
 hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* ql, const void* kh, const void* kl,
                              const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
-                             int hq, int hkv, int causal, int q_off) {
+                             int hq, int hkv, int causal, int q_off, const int* kv_index) {
     const dim3 grid((tq + attn::QT - 1) / attn::QT, hq, batch);
     if (hd == 64)
         hipLaunchKernelGGL(vk_flash_attn<64>, grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
                            (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv,
-                           t_pad, hq, hkv, causal, q_off);
+                           t_pad, hq, hkv, causal, q_off, kv_index);
     else
         hipLaunchKernelGGL(vk_flash_attn<128>, grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
                            (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv,
-                           t_pad, hq, hkv, causal, q_off);
+                           t_pad, hq, hkv, causal, q_off, kv_index);
     return hipGetLastError();
 }
 

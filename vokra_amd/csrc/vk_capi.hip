@@ -445,6 +445,13 @@ int check_paged_attn(const vokra_hip_kv* kv, size_t layer, size_t n, size_t hq) 
 
 }  // namespace
 
+// Internal accessors for the sessions (vk_session.hip), which are built on
+// this file's entry points.
+namespace vk {
+hipStream_t ctx_stream(const vokra_hip_ctx* c) { return c->stream; }
+int ctx_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace vk
+
 extern "C" {
 
 int vokra_hip_kv_create(vokra_hip_ctx_t* c, size_t n_layer, size_t n_head, size_t d_head, size_t n_stream,
@@ -863,6 +870,15 @@ int vokra_hip_gelu_f32(vokra_hip_ctx_t* c, const float* x, float* out, size_t n)
     VK_TRY(c->out0.ensure(n * sizeof(float)), "hipMalloc");
     if ((st = vokra_hip_gelu_f32_dev(c, (const float*)c->in0.p, (float*)c->out0.p, n))) return st;
     return stage_out(c, out, c->out0.p, n);
+}
+
+int vokra_hip_add_f32_dev(vokra_hip_ctx_t* c, const float* d_a, const float* d_b, float* d_out, size_t n) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "add: ctx is NULL");
+    if (n == 0) return VOKRA_HIP_OK;
+    if (!d_a || !d_b || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "add: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_add_f32(c->stream, d_a, d_b, d_out, n), "launch(vk_add_f32)");
+    return VOKRA_HIP_OK;
 }
 
 int vokra_hip_argmax_f32_dev(vokra_hip_ctx_t* c, const float* d_logits, size_t rows, size_t cols, int32_t* d_out) {

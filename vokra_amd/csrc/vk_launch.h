@@ -48,7 +48,7 @@ hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, i
                            void* vtl);
 hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* ql, const void* kh, const void* kl,
                              const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
-                             int hq, int hkv, int causal, int q_off);
+                             int hq, int hkv, int causal, int q_off, const int* kv_index = nullptr);
 }  // namespace vk
 
 namespace vk {
@@ -84,4 +84,10 @@ hipError_t launch_add_f32(hipStream_t s, const float* a, const float* b, float* 
 hipError_t launch_embed_f32(hipStream_t s, const float* tok_emb, const float* pos_emb, const int* tokens,
                             const int* positions, int vocab, int n_pos, int d, int rows, float* out);
 hipError_t launch_argmax_f32(hipStream_t s, const float* logits, int rows, int cols, int* out);
+}  // namespace vk
+
+struct vokra_hip_ctx;
+namespace vk {
+hipStream_t ctx_stream(const vokra_hip_ctx* c);
+int ctx_fail(int code, const char* msg);
 }  // namespace vk

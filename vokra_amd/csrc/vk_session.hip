@@ -1,0 +1,534 @@
+// vk_session.hip — device-resident model sessions built on the library's own
+// entry points: the pre-norm encoder (crates/vokra-models/src/whisper/
+// encoder.rs:41-245) and the batched Whisper decoder step (decoder.rs:413-796).
+//
+// Everything a forward or a step touches stays in HBM: quantized weights are
+// uploaded once, activations live in session workspaces, the self-attention
+// K/V go to the paged Q8_0 cache, and the cross-attention K/V of each
+// (stream, layer) are projected once per utterance and stored already split
+// into fp16 hi/lo halves for the fused attention kernel.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../../include/vokra_hip.h"
+#include "vk_launch.h"
+
+namespace vk {
+
+// Per-step indices: lens[i] = positions[i] + 1 (keys 0..t after the append)
+// and, per layer, the cross K/V batch of item i, streams[i] * n_layer + l.
+__global__ void vk_step_index(const int* __restrict__ streams, const int* __restrict__ positions, int n, int n_layer,
+                              int* __restrict__ lens, int* __restrict__ kvidx) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    lens[i] = positions[i] + 1;
+    for (int l = 0; l < n_layer; ++l) kvidx[l * n + i] = streams[i] * n_layer + l;
+}
+
+}  // namespace vk
+
+namespace {
+
+constexpr float kLnEps = 1e-5f;  // LAYER_NORM_DEFAULT_EPS (crates/vokra-backend-cpu/src/kernels/scalar.rs:26)
+
+#define SS_TRY(x)                \
+    do {                         \
+        int _st = (x);           \
+        if (_st) return _st;     \
+    } while (0)
+#define SS_HIP(x, what)                                                                    \
+    do {                                                                                   \
+        hipError_t _e = (x);                                                               \
+        if (_e != hipSuccess) return vk::ctx_fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, what); \
+    } while (0)
+
+size_t wire_bytes(int wdtype, size_t n, size_t k) {
+    switch (wdtype) {
+    case VOKRA_HIP_W_Q4_0: return n * (k / 32) * 18;
+    case VOKRA_HIP_W_Q5_0: return n * (k / 32) * 22;
+    case VOKRA_HIP_W_Q8_0: return n * (k / 32) * 34;
+    case VOKRA_HIP_W_Q4_K: return n * (k / 256) * 144;
+    default: return 0;
+    }
+}
+
+// A device buffer owned by a session.
+struct DBuf {
+    void* p = nullptr;
+    int alloc(vokra_hip_ctx_t* c, size_t n) { return vokra_hip_device_alloc(c, n ? n : 16, &p); }
+    int upload(vokra_hip_ctx_t* c, const void* h, size_t n) {
+        SS_TRY(alloc(c, n));
+        return n ? vokra_hip_memcpy_htod(c, p, h, n) : VOKRA_HIP_OK;
+    }
+    void release(vokra_hip_ctx_t* c) {
+        if (p) (void)vokra_hip_device_free(c, p);
+        p = nullptr;
+    }
+    float* f() const { return (float*)p; }
+    int* i() const { return (int*)p; }
+};
+
+// A quantized linear: resident weight [n, k] plus an optional f32 bias.
+struct QLin {
+    vokra_hip_qweight_t* w = nullptr;
+    DBuf bias;
+    bool has_bias = false;
+    int make(vokra_hip_ctx_t* c, int wdtype, size_t n, size_t k, const uint8_t* wq, const float* b) {
+        if (!wq) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "session: a weight pointer is NULL");
+        SS_TRY(vokra_hip_qweight_upload(c, wdtype, n, k, wq, wire_bytes(wdtype, n, k), &w));
+        has_bias = b != nullptr;
+        if (has_bias) SS_TRY(bias.upload(c, b, n * sizeof(float)));
+        return VOKRA_HIP_OK;
+    }
+    int run(vokra_hip_ctx_t* c, const vokra_hip_qact_t* qa, float* d_out) const {
+        return vokra_hip_gemm_qact_dev(c, w, qa, has_bias ? bias.f() : nullptr, d_out);
+    }
+    void release(vokra_hip_ctx_t* c) {
+        vokra_hip_qweight_free(w);
+        w = nullptr;
+        bias.release(c);
+    }
+};
+
+int upload_vec(vokra_hip_ctx_t* c, DBuf& b, const float* h, size_t n, const char* what) {
+    if (!h) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, what);
+    return b.upload(c, h, n * sizeof(float));
+}
+
+int act_of(int wdtype) { return wdtype == VOKRA_HIP_W_Q4_K ? VOKRA_HIP_ACT_KQUANT : VOKRA_HIP_ACT_AMAX127; }
+
+int check_model_dims(int wdtype, size_t d, size_t n_head, size_t d_ff) {
+    if (wire_bytes(wdtype, 1, 256) == 0) return vk::ctx_fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "session: unknown weight dtype");
+    if (!d || !n_head || d % n_head != 0)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "session: d_model must be a multiple of n_head");
+    const size_t hd = d / n_head;
+    if (hd != 64 && hd != 128) return vk::ctx_fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "session: head_dim must be 64 or 128");
+    const size_t q = wdtype == VOKRA_HIP_W_Q4_K ? 256 : 32;
+    if (d % q != 0 || d_ff % q != 0 || !d_ff)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "session: d_model and d_ff must be multiples of the quant block");
+    return VOKRA_HIP_OK;
+}
+
+struct EncLayer {
+    DBuf ln1g, ln1b, ln2g, ln2b;
+    QLin q, k, v, o, fc1, fc2;
+};
+
+struct DecLayer {
+    DBuf ln1g, ln1b, ln2g, ln2b, ln3g, ln3b;
+    QLin q, k, v, o, cq, ck, cv, co, fc1, fc2;
+};
+
+}  // namespace
+
+struct vokra_hip_encoder {
+    vokra_hip_ctx_t* ctx = nullptr;
+    int wdtype = 0;
+    size_t n_layer = 0, d = 0, n_head = 0, hd = 0, d_ff = 0, max_rows = 0;
+    std::vector<EncLayer> layers;
+    DBuf lnpg, lnpb, h, x, q, k, v, attn, f;
+    vokra_hip_qact_t *qa_d = nullptr, *qa_f = nullptr;
+    void release() {
+        for (auto& L : layers) {
+            for (DBuf* b : {&L.ln1g, &L.ln1b, &L.ln2g, &L.ln2b}) b->release(ctx);
+            for (QLin* w : {&L.q, &L.k, &L.v, &L.o, &L.fc1, &L.fc2}) w->release(ctx);
+        }
+        for (DBuf* b : {&lnpg, &lnpb, &h, &x, &q, &k, &v, &attn, &f}) b->release(ctx);
+        vokra_hip_qact_free(qa_d);
+        vokra_hip_qact_free(qa_f);
+        qa_d = qa_f = nullptr;
+    }
+};
+
+struct vokra_hip_decoder {
+    vokra_hip_ctx_t* ctx = nullptr;
+    int wdtype = 0;
+    size_t n_layer = 0, d = 0, n_head = 0, hd = 0, d_ff = 0, vocab = 0, n_text = 0, n_audio = 0, n_stream = 0;
+    size_t t_pad = 0;
+    std::vector<DecLayer> layers;
+    DBuf tok_emb, pos_emb, lnpg, lnpb;
+    vokra_hip_kv_t* kv = nullptr;
+    DBuf ckh, ckl, cvh, cvl;  // cross K (fp16 hi/lo) and V^T per (stream, layer)
+    DBuf h, x, q, k, v, attn, f, logits, qh, ql, lens, kvidx, next, tk, tv, stage;
+    vokra_hip_qact_t *qa_d = nullptr, *qa_f = nullptr;
+    void release() {
+        for (auto& L : layers) {
+            for (DBuf* b : {&L.ln1g, &L.ln1b, &L.ln2g, &L.ln2b, &L.ln3g, &L.ln3b}) b->release(ctx);
+            for (QLin* w : {&L.q, &L.k, &L.v, &L.o, &L.cq, &L.ck, &L.cv, &L.co, &L.fc1, &L.fc2}) w->release(ctx);
+        }
+        for (DBuf* b : {&tok_emb, &pos_emb, &lnpg, &lnpb, &ckh, &ckl, &cvh, &cvl, &h, &x, &q, &k, &v, &attn, &f,
+                        &logits, &qh, &ql, &lens, &kvidx, &next, &tk, &tv, &stage})
+            b->release(ctx);
+        vokra_hip_kv_destroy(kv);
+        kv = nullptr;
+        vokra_hip_qact_free(qa_d);
+        vokra_hip_qact_free(qa_f);
+        qa_d = qa_f = nullptr;
+    }
+};
+
+namespace {
+
+int enc_setup(vokra_hip_encoder* e, const vokra_hip_prenorm_layer_t* layers, const float* lpg, const float* lpb) {
+    vokra_hip_ctx_t* c = e->ctx;
+    const size_t d = e->d, ff = e->d_ff;
+    e->layers.resize(e->n_layer);
+    for (size_t l = 0; l < e->n_layer; ++l) {
+        const vokra_hip_prenorm_layer_t& s = layers[l];
+        EncLayer& L = e->layers[l];
+        SS_TRY(upload_vec(c, L.ln1g, s.ln1_gamma, d, "encoder: ln1_gamma is NULL"));
+        SS_TRY(upload_vec(c, L.ln1b, s.ln1_beta, d, "encoder: ln1_beta is NULL"));
+        SS_TRY(upload_vec(c, L.ln2g, s.ln2_gamma, d, "encoder: ln2_gamma is NULL"));
+        SS_TRY(upload_vec(c, L.ln2b, s.ln2_beta, d, "encoder: ln2_beta is NULL"));
+        SS_TRY(L.q.make(c, e->wdtype, d, d, s.wq, s.bq));
+        SS_TRY(L.k.make(c, e->wdtype, d, d, s.wk, s.bk));
+        SS_TRY(L.v.make(c, e->wdtype, d, d, s.wv, s.bv));
+        SS_TRY(L.o.make(c, e->wdtype, d, d, s.wo, s.bo));
+        SS_TRY(L.fc1.make(c, e->wdtype, ff, d, s.w1, s.b1));
+        SS_TRY(L.fc2.make(c, e->wdtype, d, ff, s.w2, s.b2));
+    }
+    SS_TRY(upload_vec(c, e->lnpg, lpg, d, "encoder: ln_post_gamma is NULL"));
+    SS_TRY(upload_vec(c, e->lnpb, lpb, d, "encoder: ln_post_beta is NULL"));
+    const size_t rd = e->max_rows * d * sizeof(float);
+    for (DBuf* b : {&e->h, &e->x, &e->q, &e->k, &e->v, &e->attn}) SS_TRY(b->alloc(c, rd));
+    SS_TRY(e->f.alloc(c, e->max_rows * ff * sizeof(float)));
+    SS_TRY(vokra_hip_qact_create(c, e->max_rows, d, &e->qa_d));
+    SS_TRY(vokra_hip_qact_create(c, e->max_rows, ff, &e->qa_f));
+    return VOKRA_HIP_OK;
+}
+
+int enc_forward(vokra_hip_encoder* e, size_t batch, size_t frames, const float* d_x, float* d_out) {
+    vokra_hip_ctx_t* c = e->ctx;
+    const size_t rows = batch * frames, d = e->d;
+    const int act = act_of(e->wdtype);
+    const float scale = powf((float)e->hd, -0.5f);  // (hd as f32).powf(-0.5), nn.rs:267
+    SS_HIP(hipMemcpyAsync(e->h.p, d_x, rows * d * sizeof(float), hipMemcpyDeviceToDevice, vk::ctx_stream(c)),
+           "encoder: hipMemcpyAsync");
+    for (const EncLayer& L : e->layers) {
+        // attention block (encoder.rs:180-220)
+        SS_TRY(vokra_hip_layer_norm_f32_dev(c, e->h.f(), e->x.f(), rows, d, L.ln1g.f(), L.ln1b.f(), kLnEps));
+        SS_TRY(vokra_hip_qact_quantize_dev(c, e->qa_d, rows, e->x.f(), act));
+        SS_TRY(L.q.run(c, e->qa_d, e->q.f()));
+        SS_TRY(L.k.run(c, e->qa_d, e->k.f()));
+        SS_TRY(L.v.run(c, e->qa_d, e->v.f()));
+        SS_TRY(vokra_hip_attn_f32_dev(c, batch, frames, frames, e->n_head, e->n_head, e->hd, e->q.f(), e->k.f(),
+                                      e->v.f(), scale, 0, 0, e->attn.f()));
+        SS_TRY(vokra_hip_qact_quantize_dev(c, e->qa_d, rows, e->attn.f(), act));
+        SS_TRY(L.o.run(c, e->qa_d, e->x.f()));
+        SS_TRY(vokra_hip_add_f32_dev(c, e->h.f(), e->x.f(), e->h.f(), rows * d));
+        // MLP block (nn.rs:134-181)
+        SS_TRY(vokra_hip_layer_norm_f32_dev(c, e->h.f(), e->x.f(), rows, d, L.ln2g.f(), L.ln2b.f(), kLnEps));
+        SS_TRY(vokra_hip_qact_quantize_dev(c, e->qa_d, rows, e->x.f(), act));
+        SS_TRY(L.fc1.run(c, e->qa_d, e->f.f()));
+        SS_TRY(vokra_hip_gelu_f32_dev(c, e->f.f(), e->f.f(), rows * e->d_ff));
+        SS_TRY(vokra_hip_qact_quantize_dev(c, e->qa_f, rows, e->f.f(), act));
+        SS_TRY(L.fc2.run(c, e->qa_f, e->x.f()));
+        SS_TRY(vokra_hip_add_f32_dev(c, e->h.f(), e->x.f(), e->h.f(), rows * d));
+    }
+    return vokra_hip_layer_norm_f32_dev(c, e->h.f(), d_out, rows, d, e->lnpg.f(), e->lnpb.f(), kLnEps);
+}
+
+int dec_setup(vokra_hip_decoder* m, const vokra_hip_decoder_layer_t* layers, const float* tok_emb,
+              const float* pos_emb, const float* lpg, const float* lpb, size_t block_size) {
+    vokra_hip_ctx_t* c = m->ctx;
+    const size_t d = m->d, ff = m->d_ff;
+    m->layers.resize(m->n_layer);
+    for (size_t l = 0; l < m->n_layer; ++l) {
+        const vokra_hip_decoder_layer_t& s = layers[l];
+        DecLayer& L = m->layers[l];
+        SS_TRY(upload_vec(c, L.ln1g, s.ln1_gamma, d, "decoder: ln1_gamma is NULL"));
+        SS_TRY(upload_vec(c, L.ln1b, s.ln1_beta, d, "decoder: ln1_beta is NULL"));
+        SS_TRY(upload_vec(c, L.ln2g, s.ln2_gamma, d, "decoder: ln2_gamma is NULL"));
+        SS_TRY(upload_vec(c, L.ln2b, s.ln2_beta, d, "decoder: ln2_beta is NULL"));
+        SS_TRY(upload_vec(c, L.ln3g, s.ln3_gamma, d, "decoder: ln3_gamma is NULL"));
+        SS_TRY(upload_vec(c, L.ln3b, s.ln3_beta, d, "decoder: ln3_beta is NULL"));
+        SS_TRY(L.q.make(c, m->wdtype, d, d, s.wq, s.bq));
+        SS_TRY(L.k.make(c, m->wdtype, d, d, s.wk, s.bk));
+        SS_TRY(L.v.make(c, m->wdtype, d, d, s.wv, s.bv));
+        SS_TRY(L.o.make(c, m->wdtype, d, d, s.wo, s.bo));
+        SS_TRY(L.cq.make(c, m->wdtype, d, d, s.cwq, s.cbq));
+        SS_TRY(L.ck.make(c, m->wdtype, d, d, s.cwk, s.cbk));
+        SS_TRY(L.cv.make(c, m->wdtype, d, d, s.cwv, s.cbv));
+        SS_TRY(L.co.make(c, m->wdtype, d, d, s.cwo, s.cbo));
+        SS_TRY(L.fc1.make(c, m->wdtype, ff, d, s.w1, s.b1));
+        SS_TRY(L.fc2.make(c, m->wdtype, d, ff, s.w2, s.b2));
+    }
+    SS_TRY(upload_vec(c, m->tok_emb, tok_emb, m->vocab * d, "decoder: token_emb is NULL"));
+    SS_TRY(upload_vec(c, m->pos_emb, pos_emb, m->n_text * d, "decoder: pos_emb is NULL"));
+    SS_TRY(upload_vec(c, m->lnpg, lpg, d, "decoder: ln_post_gamma is NULL"));
+    SS_TRY(upload_vec(c, m->lnpb, lpb, d, "decoder: ln_post_beta is NULL"));
+    SS_TRY(vokra_hip_kv_create(c, m->n_layer, m->n_head, m->hd, m->n_stream, m->n_text, block_size, VOKRA_HIP_KV_Q8_0,
+                               &m->kv));
+    const size_t sl = m->n_stream * m->n_layer;
+    SS_TRY(m->ckh.alloc(c, sl * m->n_audio * d * 2));
+    SS_TRY(m->ckl.alloc(c, sl * m->n_audio * d * 2));
+    SS_TRY(m->cvh.alloc(c, sl * d * m->t_pad * 2));
+    SS_TRY(m->cvl.alloc(c, sl * d * m->t_pad * 2));
+    const size_t rows = m->n_stream, rd = rows * d * sizeof(float);
+    for (DBuf* b : {&m->h, &m->x, &m->q, &m->k, &m->v, &m->attn}) SS_TRY(b->alloc(c, rd));
+    SS_TRY(m->f.alloc(c, rows * ff * sizeof(float)));
+    SS_TRY(m->logits.alloc(c, rows * m->vocab * sizeof(float)));
+    SS_TRY(m->qh.alloc(c, rows * d * 2));
+    SS_TRY(m->ql.alloc(c, rows * d * 2));
+    SS_TRY(m->lens.alloc(c, rows * sizeof(int)));
+    SS_TRY(m->kvidx.alloc(c, m->n_layer * rows * sizeof(int)));
+    SS_TRY(m->next.alloc(c, rows * sizeof(int)));
+    SS_TRY(m->tk.alloc(c, m->n_audio * d * sizeof(float)));
+    SS_TRY(m->tv.alloc(c, m->n_audio * d * sizeof(float)));
+    SS_TRY(m->stage.alloc(c, std::max(m->n_audio * d * sizeof(float), 3 * rows * sizeof(int))));
+    SS_TRY(vokra_hip_qact_create(c, std::max(rows, m->n_audio), d, &m->qa_d));
+    SS_TRY(vokra_hip_qact_create(c, rows, ff, &m->qa_f));
+    return VOKRA_HIP_OK;
+}
+
+int dec_set_encoder(vokra_hip_decoder* m, size_t stream, const float* d_enc) {
+    vokra_hip_ctx_t* c = m->ctx;
+    hipStream_t s = vk::ctx_stream(c);
+    const size_t d = m->d, na = m->n_audio;
+    SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, na, d_enc, act_of(m->wdtype)));
+    for (size_t l = 0; l < m->n_layer; ++l) {
+        const DecLayer& L = m->layers[l];
+        SS_TRY(L.ck.run(c, m->qa_d, m->tk.f()));
+        SS_TRY(L.cv.run(c, m->qa_d, m->tv.f()));
+        const size_t sl = stream * m->n_layer + l;
+        uint16_t* kh = (uint16_t*)m->ckh.p + sl * na * d;
+        uint16_t* kl = (uint16_t*)m->ckl.p + sl * na * d;
+        uint16_t* vh = (uint16_t*)m->cvh.p + sl * d * m->t_pad;
+        uint16_t* vl = (uint16_t*)m->cvl.p + sl * d * m->t_pad;
+        SS_HIP(vk::launch_split_rows(s, m->tk.f(), na * d, 1.0f, kh, kl), "launch(vk_split_rows cross k)");
+        SS_HIP(vk::launch_split_vt(s, m->tv.f(), 1, (int)na, (int)m->t_pad, (int)m->n_head, (int)m->hd, vh, vl),
+               "launch(vk_split_vt cross v)");
+    }
+    return VOKRA_HIP_OK;
+}
+
+int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_tokens, const int* d_positions,
+             int* d_next, float* d_logits) {
+    vokra_hip_ctx_t* c = m->ctx;
+    hipStream_t s = vk::ctx_stream(c);
+    const size_t d = m->d;
+    const int act = act_of(m->wdtype);
+    const float scale = powf((float)m->hd, -0.5f);
+    SS_HIP(vk::launch_embed_f32(s, m->tok_emb.f(), m->pos_emb.f(), d_tokens, d_positions, (int)m->vocab,
+                                (int)m->n_text, (int)d, (int)n, m->h.f()),
+           "launch(vk_embed_f32)");
+    hipLaunchKernelGGL(vk::vk_step_index, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, s, d_streams, d_positions, (int)n,
+                       (int)m->n_layer, m->lens.i(), m->kvidx.i());
+    SS_HIP(hipGetLastError(), "launch(vk_step_index)");
+    for (size_t l = 0; l < m->n_layer; ++l) {
+        const DecLayer& L = m->layers[l];
+        // causal self-attention over the paged cache (decoder.rs:462-490)
+        SS_TRY(vokra_hip_layer_norm_f32_dev(c, m->h.f(), m->x.f(), n, d, L.ln1g.f(), L.ln1b.f(), kLnEps));
+        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->x.f(), act));
+        SS_TRY(L.q.run(c, m->qa_d, m->q.f()));
+        SS_TRY(L.k.run(c, m->qa_d, m->k.f()));
+        SS_TRY(L.v.run(c, m->qa_d, m->v.f()));
+        SS_TRY(vokra_hip_kv_append_dev(c, m->kv, l, n, d_streams, d_positions, m->k.f(), m->v.f()));
+        SS_TRY(vokra_hip_paged_attn_dev(c, m->kv, l, n, d_streams, m->lens.i(), m->n_text, m->n_head, m->q.f(), scale,
+                                        m->attn.f()));
+        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->attn.f(), act));
+        SS_TRY(L.o.run(c, m->qa_d, m->x.f()));
+        SS_TRY(vokra_hip_add_f32_dev(c, m->h.f(), m->x.f(), m->h.f(), n * d));
+        // cross-attention over the stream's encoder frames (decoder.rs:492-510)
+        SS_TRY(vokra_hip_layer_norm_f32_dev(c, m->h.f(), m->x.f(), n, d, L.ln2g.f(), L.ln2b.f(), kLnEps));
+        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->x.f(), act));
+        SS_TRY(L.cq.run(c, m->qa_d, m->q.f()));
+        SS_HIP(vk::launch_split_rows(s, m->q.f(), n * d, scale, m->qh.p, m->ql.p), "launch(vk_split_rows q)");
+        SS_HIP(vk::launch_flash_attn(s, (int)m->hd, m->qh.p, m->ql.p, m->ckh.p, m->ckl.p, m->cvh.p, m->cvl.p,
+                                     m->attn.f(), (int)n, 1, (int)m->n_audio, (int)m->t_pad, (int)m->n_head,
+                                     (int)m->n_head, 0, 0, m->kvidx.i() + l * n),
+               "launch(vk_flash_attn cross)");
+        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->attn.f(), act));
+        SS_TRY(L.co.run(c, m->qa_d, m->x.f()));
+        SS_TRY(vokra_hip_add_f32_dev(c, m->h.f(), m->x.f(), m->h.f(), n * d));
+        // MLP (decoder.rs:512-525)
+        SS_TRY(vokra_hip_layer_norm_f32_dev(c, m->h.f(), m->x.f(), n, d, L.ln3g.f(), L.ln3b.f(), kLnEps));
+        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->x.f(), act));
+        SS_TRY(L.fc1.run(c, m->qa_d, m->f.f()));
+        SS_TRY(vokra_hip_gelu_f32_dev(c, m->f.f(), m->f.f(), n * m->d_ff));
+        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_f, n, m->f.f(), act));
+        SS_TRY(L.fc2.run(c, m->qa_f, m->x.f()));
+        SS_TRY(vokra_hip_add_f32_dev(c, m->h.f(), m->x.f(), m->h.f(), n * d));
+    }
+    // ln_post, tied logits (decoder.rs:754-796), greedy argmax
+    SS_TRY(vokra_hip_layer_norm_f32_dev(c, m->h.f(), m->x.f(), n, d, m->lnpg.f(), m->lnpb.f(), kLnEps));
+    float* lg = d_logits ? d_logits : m->logits.f();
+    SS_TRY(vokra_hip_gemm_f32_dev(c, n, m->vocab, d, m->x.f(), m->tok_emb.f(), 1, nullptr, lg));
+    return vokra_hip_argmax_f32_dev(c, lg, n, m->vocab, d_next);
+}
+
+}  // namespace
+
+extern "C" {
+
+int vokra_hip_encoder_create(vokra_hip_ctx_t* c, int wdtype, size_t n_layer, size_t d_model, size_t n_head,
+                             size_t d_ff, const vokra_hip_prenorm_layer_t* layers, const float* ln_post_gamma,
+                             const float* ln_post_beta, size_t max_rows, vokra_hip_encoder_t** out) {
+    if (!c || !out || (n_layer && !layers))
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_create: NULL argument");
+    *out = nullptr;
+    SS_TRY(check_model_dims(wdtype, d_model, n_head, d_ff));
+    if (!max_rows) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_create: max_rows must be > 0");
+    auto* e = new vokra_hip_encoder();
+    e->ctx = c;
+    e->wdtype = wdtype;
+    e->n_layer = n_layer;
+    e->d = d_model;
+    e->n_head = n_head;
+    e->hd = d_model / n_head;
+    e->d_ff = d_ff;
+    e->max_rows = max_rows;
+    int st = enc_setup(e, layers, ln_post_gamma, ln_post_beta);
+    if (st) {
+        e->release();
+        delete e;
+        return st;
+    }
+    *out = e;
+    return VOKRA_HIP_OK;
+}
+
+void vokra_hip_encoder_destroy(vokra_hip_encoder_t* e) {
+    if (!e) return;
+    e->release();
+    delete e;
+}
+
+int vokra_hip_encoder_forward_dev(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, size_t batch, size_t frames,
+                                  const float* d_x, float* d_out) {
+    if (!c || !e || e->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_forward: bad context");
+    if (batch * frames == 0) return VOKRA_HIP_OK;
+    if (batch * frames > e->max_rows)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_forward: batch * frames exceeds max_rows");
+    if (!d_x || !d_out) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_forward: NULL buffer");
+    return enc_forward(e, batch, frames, d_x, d_out);
+}
+
+int vokra_hip_encoder_forward(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, size_t batch, size_t frames, const float* x,
+                              float* out) {
+    if (!c || !e || e->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_forward: bad context");
+    const size_t n = batch * frames * e->d;
+    if (n == 0) return VOKRA_HIP_OK;
+    if (batch * frames > e->max_rows)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_forward: batch * frames exceeds max_rows");
+    if (!x || !out) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_forward: NULL buffer");
+    DBuf in, o;
+    int st = in.upload(c, x, n * sizeof(float));
+    if (!st) st = o.alloc(c, n * sizeof(float));
+    if (!st) st = enc_forward(e, batch, frames, in.f(), o.f());
+    if (!st) st = vokra_hip_memcpy_dtoh(c, out, o.p, n * sizeof(float));
+    in.release(c);
+    o.release(c);
+    return st;
+}
+
+int vokra_hip_decoder_create(vokra_hip_ctx_t* c, int wdtype, size_t n_layer, size_t d_model, size_t n_head,
+                             size_t d_ff, size_t n_vocab, size_t n_text_ctx, size_t n_audio_ctx, size_t n_stream,
+                             size_t block_size, const vokra_hip_decoder_layer_t* layers, const float* token_emb,
+                             const float* pos_emb, const float* ln_post_gamma, const float* ln_post_beta,
+                             vokra_hip_decoder_t** out) {
+    if (!c || !out || !layers) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_create: NULL argument");
+    *out = nullptr;
+    SS_TRY(check_model_dims(wdtype, d_model, n_head, d_ff));
+    if (!n_layer || !n_vocab || !n_text_ctx || !n_audio_ctx || !n_stream || n_stream > 1024 || n_vocab > 0x7fffffff)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                            "decoder_create: n_layer, n_vocab, n_text_ctx, n_audio_ctx > 0 and n_stream in 1..1024");
+    auto* m = new vokra_hip_decoder();
+    m->ctx = c;
+    m->wdtype = wdtype;
+    m->n_layer = n_layer;
+    m->d = d_model;
+    m->n_head = n_head;
+    m->hd = d_model / n_head;
+    m->d_ff = d_ff;
+    m->vocab = n_vocab;
+    m->n_text = n_text_ctx;
+    m->n_audio = n_audio_ctx;
+    m->n_stream = n_stream;
+    m->t_pad = (n_audio_ctx + 63) / 64 * 64;
+    int st = dec_setup(m, layers, token_emb, pos_emb, ln_post_gamma, ln_post_beta, block_size);
+    if (st) {
+        m->release();
+        delete m;
+        return st;
+    }
+    *out = m;
+    return VOKRA_HIP_OK;
+}
+
+void vokra_hip_decoder_destroy(vokra_hip_decoder_t* m) {
+    if (!m) return;
+    m->release();
+    delete m;
+}
+
+int vokra_hip_decoder_set_encoder_dev(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t stream, const float* d_enc) {
+    if (!c || !m || m->ctx != c || !d_enc)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_set_encoder: bad argument");
+    if (stream >= m->n_stream)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_set_encoder: stream out of range");
+    return dec_set_encoder(m, stream, d_enc);
+}
+
+int vokra_hip_decoder_set_encoder(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t stream, const float* enc) {
+    if (!c || !m || m->ctx != c || !enc)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_set_encoder: bad argument");
+    if (stream >= m->n_stream)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_set_encoder: stream out of range");
+    SS_TRY(vokra_hip_memcpy_htod(c, m->stage.p, enc, m->n_audio * m->d * sizeof(float)));
+    SS_TRY(dec_set_encoder(m, stream, m->stage.f()));
+    return vokra_hip_synchronize(c);
+}
+
+int vokra_hip_decoder_reset(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m) {
+    if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_reset: bad argument");
+    return vokra_hip_kv_reset(c, m->kv);
+}
+
+int vokra_hip_decoder_step_dev(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t n, const int32_t* d_streams,
+                               const int32_t* d_tokens, const int32_t* d_positions, int32_t* d_next, float* d_logits) {
+    if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_step: bad context");
+    if (n == 0) return VOKRA_HIP_OK;
+    if (n > m->n_stream) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_step: more items than streams");
+    if (!d_streams || !d_tokens || !d_positions || !d_next)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_step: NULL buffer");
+    return dec_step(m, n, d_streams, d_tokens, d_positions, d_next, d_logits);
+}
+
+int vokra_hip_decoder_step(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t n, const int32_t* streams,
+                           const int32_t* tokens, const int32_t* positions, int32_t* next_tokens, float* logits) {
+    if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_step: bad context");
+    if (n == 0) return VOKRA_HIP_OK;
+    if (n > m->n_stream) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_step: more items than streams");
+    if (!streams || !tokens || !positions || !next_tokens)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_step: NULL buffer");
+    // WhisperDecoder::step_into's checks (decoder.rs:420-441), per stream
+    std::vector<char> seen(m->n_stream, 0);
+    for (size_t i = 0; i < n; ++i) {
+        if (streams[i] < 0 || (size_t)streams[i] >= m->n_stream || seen[streams[i]])
+            return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_step: streams must be distinct and < n_stream");
+        seen[streams[i]] = 1;
+        if (tokens[i] < 0 || (size_t)tokens[i] >= m->vocab)
+            return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "whisper decoder: token id >= n_vocab");
+        if (positions[i] < 0 || (size_t)positions[i] + 1 > m->n_text)
+            return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "whisper decoder: position exceeds n_text_ctx");
+    }
+    std::vector<int32_t> items(3 * n);
+    memcpy(items.data(), streams, n * 4);
+    memcpy(items.data() + n, tokens, n * 4);
+    memcpy(items.data() + 2 * n, positions, n * 4);
+    int* dv = m->stage.i();
+    SS_TRY(vokra_hip_memcpy_htod(c, dv, items.data(), 3 * n * 4));
+    SS_TRY(dec_step(m, n, dv, dv + n, dv + 2 * n, m->next.i(), m->logits.f()));
+    size_t appended = 0;
+    SS_TRY(vokra_hip_kv_status(c, m->kv, &appended));
+    SS_TRY(vokra_hip_memcpy_dtoh(c, next_tokens, m->next.p, n * 4));
+    if (logits) SS_TRY(vokra_hip_memcpy_dtoh(c, logits, m->logits.p, n * m->vocab * sizeof(float)));
+    return VOKRA_HIP_OK;
+}
+
+}  // extern "C"

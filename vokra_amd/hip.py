@@ -69,6 +69,46 @@ class ActQuant(IntEnum):
 
 _lib = None
 
+_F = C.POINTER(C.c_float)
+_U8 = C.POINTER(C.c_uint8)
+
+
+class PrenormLayer(C.Structure):
+    """vokra_hip_prenorm_layer_t"""
+    _fields_ = [("ln1_gamma", _F), ("ln1_beta", _F), ("wq", _U8), ("wk", _U8), ("wv", _U8), ("wo", _U8),
+                ("bq", _F), ("bk", _F), ("bv", _F), ("bo", _F), ("ln2_gamma", _F), ("ln2_beta", _F),
+                ("w1", _U8), ("w2", _U8), ("b1", _F), ("b2", _F)]
+
+
+class DecoderLayer(C.Structure):
+    """vokra_hip_decoder_layer_t"""
+    _fields_ = [("ln1_gamma", _F), ("ln1_beta", _F), ("wq", _U8), ("wk", _U8), ("wv", _U8), ("wo", _U8),
+                ("bq", _F), ("bk", _F), ("bv", _F), ("bo", _F), ("ln2_gamma", _F), ("ln2_beta", _F),
+                ("cwq", _U8), ("cwk", _U8), ("cwv", _U8), ("cwo", _U8),
+                ("cbq", _F), ("cbk", _F), ("cbv", _F), ("cbo", _F), ("ln3_gamma", _F), ("ln3_beta", _F),
+                ("w1", _U8), ("w2", _U8), ("b1", _F), ("b2", _F)]
+
+
+def _ctx_alive(obj):
+    """True while the context an object was made on is open: handles are only
+    freed through a live context (after close, the process exit reclaims them)."""
+    ctx = getattr(obj, "_ctx", None) or getattr(obj, "ctx", None)
+    return ctx is not None and getattr(ctx, "_h", None) is not None
+
+
+def _fill_struct(st_type, fields, keep):
+    """Builds a layer struct from a dict of numpy arrays (missing / None -> NULL);
+    the arrays are appended to `keep` so they outlive the create call."""
+    st = st_type()
+    for name, ctype in st_type._fields_:
+        arr = fields.get(name)
+        if arr is None:
+            continue
+        arr = np.ascontiguousarray(arr, np.uint8 if ctype is _U8 else np.float32)
+        keep.append(arr)
+        setattr(st, name, arr.ctypes.data_as(ctype))
+    return st
+
 
 def _declare(L):
     P = C.c_void_p
@@ -141,6 +181,22 @@ def _declare(L):
     L.vokra_hip_gelu_f32.argtypes = [P, f32p, f32p, sz]
     L.vokra_hip_gelu_f32_dev.argtypes = [P, P, P, sz]
     L.vokra_hip_argmax_f32_dev.argtypes = [P, P, sz, sz, P]
+    L.vokra_hip_add_f32_dev.argtypes = [P, P, P, P, sz]
+    L.vokra_hip_encoder_create.argtypes = [P, C.c_int, sz, sz, sz, sz, C.POINTER(PrenormLayer), f32p, f32p, sz,
+                                           C.POINTER(P)]
+    L.vokra_hip_encoder_destroy.argtypes = [P]
+    L.vokra_hip_encoder_destroy.restype = None
+    L.vokra_hip_encoder_forward.argtypes = [P, P, sz, sz, f32p, f32p]
+    L.vokra_hip_encoder_forward_dev.argtypes = [P, P, sz, sz, P, P]
+    L.vokra_hip_decoder_create.argtypes = [P, C.c_int, sz, sz, sz, sz, sz, sz, sz, sz, sz,
+                                           C.POINTER(DecoderLayer), f32p, f32p, f32p, f32p, C.POINTER(P)]
+    L.vokra_hip_decoder_destroy.argtypes = [P]
+    L.vokra_hip_decoder_destroy.restype = None
+    L.vokra_hip_decoder_set_encoder.argtypes = [P, P, sz, f32p]
+    L.vokra_hip_decoder_set_encoder_dev.argtypes = [P, P, sz, P]
+    L.vokra_hip_decoder_reset.argtypes = [P, P]
+    L.vokra_hip_decoder_step.argtypes = [P, P, sz, i32p, i32p, i32p, i32p, f32p]
+    L.vokra_hip_decoder_step_dev.argtypes = [P, P, sz, P, P, P, P, P]
     L.vokra_hip_attn_f32.argtypes = [P, sz, sz, sz, sz, sz, sz, f32p, f32p, f32p, C.c_float, C.c_int, sz, f32p]
     L.vokra_hip_attn_f32_dev.argtypes = [P, sz, sz, sz, sz, sz, sz, P, P, P, C.c_float, C.c_int, sz, P]
 
@@ -247,7 +303,7 @@ class Event:
 
     def __del__(self):
         try:
-            if getattr(self, "_h", None):
+            if getattr(self, "_h", None) and _ctx_alive(self):
                 lib().vokra_hip_event_destroy(self._h)
         except Exception:
             pass
@@ -266,7 +322,7 @@ class QWeight:
 
     def __del__(self):
         try:
-            if getattr(self, "_h", None):
+            if getattr(self, "_h", None) and _ctx_alive(self):
                 lib().vokra_hip_qweight_free(self._h)
         except Exception:
             pass
@@ -283,7 +339,7 @@ class Graph:
 
     def __del__(self):
         try:
-            if getattr(self, "_h", None):
+            if getattr(self, "_h", None) and _ctx_alive(self):
                 lib().vokra_hip_graph_destroy(self._h)
         except Exception:
             pass
@@ -304,7 +360,7 @@ class QAct:
 
     def __del__(self):
         try:
-            if getattr(self, "_h", None):
+            if getattr(self, "_h", None) and _ctx_alive(self):
                 lib().vokra_hip_qact_free(self._h)
         except Exception:
             pass
@@ -386,8 +442,91 @@ class KvCache:
 
     def __del__(self):
         try:
-            if getattr(self, "_h", None) and self._h.value:
+            if getattr(self, "_h", None) and self._h.value and _ctx_alive(self):
                 lib().vokra_hip_kv_destroy(self._h)
+                self._h = C.c_void_p()
+        except Exception:
+            pass
+
+
+class Encoder:
+    """Device-resident pre-norm encoder (compute.rs:2775 encode_prenorm_encoder)."""
+
+    def __init__(self, ctx, wdtype, d_model, n_head, d_ff, layers, ln_post_gamma, ln_post_beta, max_rows):
+        self._ctx, self.d = ctx, d_model
+        keep = []
+        arr = (PrenormLayer * max(len(layers), 1))(*[_fill_struct(PrenormLayer, L, keep) for L in layers])
+        g, b = _f32(ln_post_gamma), _f32(ln_post_beta)
+        h = C.c_void_p()
+        _check(lib().vokra_hip_encoder_create(ctx._h, int(wdtype), len(layers), d_model, n_head, d_ff, arr,
+                                              _ptr(g, C.c_float), _ptr(b, C.c_float), max_rows, C.byref(h)))
+        self._h = h
+
+    def forward(self, x):
+        xv = _f32(x)
+        B, T, _ = xv.shape
+        out = np.zeros_like(xv)
+        _check(lib().vokra_hip_encoder_forward(self._ctx._h, self._h, B, T, _ptr(xv, C.c_float),
+                                               _ptr(out, C.c_float)))
+        return out
+
+    def forward_dev(self, batch, frames, d_x, d_out):
+        _check(lib().vokra_hip_encoder_forward_dev(self._ctx._h, self._h, batch, frames, d_x.ptr, d_out.ptr))
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None) and self._h.value and _ctx_alive(self):
+                lib().vokra_hip_encoder_destroy(self._h)
+                self._h = C.c_void_p()
+        except Exception:
+            pass
+
+
+class Decoder:
+    """Batched device-resident decoder step (compute.rs:2892-3139 DecoderStepSession, with a batch axis)."""
+
+    def __init__(self, ctx, wdtype, d_model, n_head, d_ff, n_vocab, n_text_ctx, n_audio_ctx, n_stream, layers,
+                 token_emb, pos_emb, ln_post_gamma, ln_post_beta, block_size=16):
+        self._ctx, self.vocab, self.d, self.n_audio = ctx, n_vocab, d_model, n_audio_ctx
+        keep = []
+        arr = (DecoderLayer * len(layers))(*[_fill_struct(DecoderLayer, L, keep) for L in layers])
+        te, pe, g, b = _f32(token_emb), _f32(pos_emb), _f32(ln_post_gamma), _f32(ln_post_beta)
+        h = C.c_void_p()
+        _check(lib().vokra_hip_decoder_create(ctx._h, int(wdtype), len(layers), d_model, n_head, d_ff, n_vocab,
+                                              n_text_ctx, n_audio_ctx, n_stream, block_size, arr,
+                                              _ptr(te, C.c_float), _ptr(pe, C.c_float), _ptr(g, C.c_float),
+                                              _ptr(b, C.c_float), C.byref(h)))
+        self._h = h
+
+    def set_encoder(self, stream, enc):
+        e = _f32(enc)
+        _check(lib().vokra_hip_decoder_set_encoder(self._ctx._h, self._h, stream, _ptr(e, C.c_float)))
+
+    def set_encoder_dev(self, stream, d_enc):
+        _check(lib().vokra_hip_decoder_set_encoder_dev(self._ctx._h, self._h, stream, d_enc.ptr))
+
+    def reset(self):
+        _check(lib().vokra_hip_decoder_reset(self._ctx._h, self._h))
+
+    def step(self, streams, tokens, positions, want_logits=False):
+        st = np.ascontiguousarray(streams, np.int32)
+        tk = np.ascontiguousarray(tokens, np.int32)
+        ps = np.ascontiguousarray(positions, np.int32)
+        nxt = np.zeros(max(st.size, 1), np.int32)
+        lg = np.zeros((st.size, self.vocab), np.float32) if want_logits else None
+        _check(lib().vokra_hip_decoder_step(self._ctx._h, self._h, st.size, _ptr(st, C.c_int32), _ptr(tk, C.c_int32),
+                                            _ptr(ps, C.c_int32), _ptr(nxt, C.c_int32), _ptr(lg, C.c_float)))
+        return (nxt[:st.size], lg) if want_logits else nxt[:st.size]
+
+    def step_dev(self, n, d_streams, d_tokens, d_positions, d_next, d_logits=None):
+        _check(lib().vokra_hip_decoder_step_dev(self._ctx._h, self._h, n, d_streams.ptr, d_tokens.ptr,
+                                                d_positions.ptr, d_next.ptr,
+                                                None if d_logits is None else d_logits.ptr))
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None) and self._h.value and _ctx_alive(self):
+                lib().vokra_hip_decoder_destroy(self._h)
                 self._h = C.c_void_p()
         except Exception:
             pass
