@@ -232,6 +232,109 @@ def bench_paged_attn(ctx, hip, n_stream, H, hd, hq, len_lo, len_hi, max_time, re
             "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK["hbm_gbs"], 4)}
 
 
+def random_block_weight(rng, wd, n, k, scale):
+    """Random wire payload of n x k block-format weights: uniform quants and
+    one f16 scale for every block (`scale`), i.e. random-init weights."""
+    nb = n * (k // 32)
+    if wd == 8:  # Q8_0: f16 d + 32 int8
+        b = rng.integers(0, 256, size=(nb, 34), dtype=np.uint8)
+    else:        # Q4_0: f16 d + 16 bytes of nibbles
+        b = rng.integers(0, 256, size=(nb, 18), dtype=np.uint8)
+    b[:, 0:2] = np.array([scale], np.float16).view(np.uint8)
+    return b.reshape(-1)
+
+
+def whisper_layer(rng, wd, d, ff, scale, decoder=False):
+    one, zero = np.ones(d, np.float32), np.zeros(d, np.float32)
+    L = {"ln1_gamma": one, "ln1_beta": zero, "ln2_gamma": one, "ln2_beta": zero}
+    mats = [("wq", d, d), ("wk", d, d), ("wv", d, d), ("wo", d, d), ("w1", ff, d), ("w2", d, ff)]
+    if decoder:
+        L.update({"ln3_gamma": one, "ln3_beta": zero})
+        mats += [("cwq", d, d), ("cwk", d, d), ("cwv", d, d), ("cwo", d, d)]
+    for name, n, k in mats:
+        L[name] = random_block_weight(rng, wd, n, k, scale)
+    for name, n in (("bq", d), ("bv", d), ("bo", d), ("b1", ff), ("b2", d)):
+        L[name] = (0.01 * rng.standard_normal(n)).astype(np.float32)
+    return L
+
+
+def bench_encoder(ctx, hip, batch, n_layer=32, d=1280, H=20, ff=5120, T=1500, reps=3):
+    """Config 2: Whisper-large-v3-shaped encoder blocks (32 x d=1280, 20 heads,
+    FFN 5120, Q8_0 random-init weights) over 1500 frames, batch 1 or 16: one
+    forward of the device-resident encoder session on resident input."""
+    rng = np.random.default_rng(2)
+    layers = [whisper_layer(rng, 8, d, ff, 2e-4) for _ in range(n_layer)]
+    enc = hip.Encoder(ctx, 8, d, H, ff, layers, np.ones(d, np.float32), np.zeros(d, np.float32), batch * T)
+    del layers
+    d_x = hip.DeviceBuffer.from_array(ctx, rng.standard_normal((batch, T, d), dtype=np.float32))
+    d_o = hip.DeviceBuffer(ctx, batch * T * d * 4)
+    enc.forward_dev(batch, T, d_x, d_o)
+    ctx.synchronize()
+    e0, e1 = hip.Event(ctx), hip.Event(ctx)
+    e0.record()
+    for _ in range(reps):
+        enc.forward_dev(batch, T, d_x, d_o)
+    e1.record()
+    ms = e0.elapsed_ms(e1) / reps
+    hd = d // H
+    flops = n_layer * batch * (2.0 * T * (4 * d * d + 2 * d * ff) + 4.0 * H * T * T * hd)
+    del enc
+    ctx.synchronize()
+    return {"batch": batch, "layers": n_layer, "frames": T, "ms": round(ms, 3),
+            "frames_per_s": round(batch * T / (ms * 1e-3), 1), "tflops": round(flops / (ms * 1e-3) / 1e12, 2)}
+
+
+def bench_decoder(ctx, hip, n_stream=64, n_layer=32, d=1280, H=20, ff=5120, V=51866, n_text=448, n_audio=1500,
+                  steps=5, max_prefix=440):
+    """Config 3: batched Whisper-large-v3-shaped decoder step, 64 streams with
+    prefixes U(1..max_prefix) already in the paged Q8_0 self-KV cache (16-token
+    pages), cross-attention over 1500 encoder frames per stream, Q4_0
+    random-init weights, tied logits over a 51866-token vocabulary, greedy
+    argmax. Timed: `steps` whole batched steps on device arrays."""
+    rng = np.random.default_rng(3)
+    layers = [whisper_layer(rng, 2, d, ff, 5e-3, decoder=True) for _ in range(n_layer)]
+    tok = (0.02 * rng.standard_normal((V, d))).astype(np.float32)
+    pos = (0.02 * rng.standard_normal((n_text, d))).astype(np.float32)
+    dec = hip.Decoder(ctx, 2, d, H, ff, V, n_text, n_audio, n_stream, layers, tok, pos,
+                      np.ones(d, np.float32), np.zeros(d, np.float32), block_size=16)
+    del layers, tok
+    d_enc = hip.DeviceBuffer.from_array(ctx, rng.standard_normal((n_audio, d), dtype=np.float32))
+    for s in range(n_stream):
+        dec.set_encoder_dev(s, d_enc)
+    lens = rng.integers(1, max_prefix + 1, n_stream)
+    cur = rng.integers(0, V, n_stream).astype(np.int32)
+    for t in range(int(lens.max())):   # prefill the caches one decode step at a time
+        live = np.nonzero(lens > t)[0].astype(np.int32)
+        nxt = dec.step(live, cur[live], np.full(live.size, t, np.int32))
+        cur[live] = nxt
+    streams = hip.DeviceBuffer.from_array(ctx, np.arange(n_stream, dtype=np.int32))
+    toks = hip.DeviceBuffer.from_array(ctx, cur)
+    posb = [hip.DeviceBuffer.from_array(ctx, (lens + k).astype(np.int32)) for k in range(steps + 1)]
+    nxt = hip.DeviceBuffer(ctx, n_stream * 4)
+    dec.step_dev(n_stream, streams, toks, posb[0], nxt)   # warm-up (positions lens)
+    ctx.synchronize()
+    e0, e1 = hip.Event(ctx), hip.Event(ctx)
+    e0.record()
+    for k in range(1, steps + 1):
+        dec.step_dev(n_stream, streams, nxt, posb[k], toks)
+        nxt, toks = toks, nxt
+    e1.record()
+    ms = e0.elapsed_ms(e1) / steps
+    keys = int((lens + 1 + steps // 2).sum())
+    w_bytes = n_layer * (8 * d * d + 2 * d * ff) * 18 // 32
+    kv_bytes = keys * n_layer * 2 * (d + d // 32 * 2)
+    cross_bytes = n_stream * n_layer * n_audio * d * 4 * 2
+    emb_bytes = V * d * 4
+    total = w_bytes + kv_bytes + cross_bytes + emb_bytes
+    del dec
+    ctx.synchronize()
+    return {"streams": n_stream, "layers": n_layer, "vocab": V, "prefix_range": [1, max_prefix],
+            "ms_per_step": round(ms, 3), "tokens_per_s": round(n_stream / (ms * 1e-3), 1),
+            "bytes_per_step": {"weights_q4_0": w_bytes, "self_kv_q8_0": kv_bytes, "cross_kv_fp16x2": cross_bytes,
+                               "tied_embedding_f32": emb_bytes},
+            "gbs": round(total / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(total / (ms * 1e-3) / 1e9 / PEAK["hbm_gbs"], 4)}
+
+
 def bench_copy(ctx, hip, nbytes=1 << 30, reps=5):
     """Plain streaming copy of 1 GiB (4x the 256 MB MALL): the
     achievable-HBM reference and the rocprof byte-counter calibration kernel."""
@@ -286,7 +389,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default=None,
                     help="comma list of single legs to run, one JSON line each (for profiling): "
-                         "gemm, gemm_pow2, copy, gemv, q4k, sdpa, paged")
+                         "gemm, gemm_pow2, copy, gemv, q4k, sdpa, paged, encoder, decoder")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -306,6 +409,8 @@ def main():
             "sdpa": lambda: bench_sdpa(ctx, hip),
             "paged": lambda: [bench_paged_attn(ctx, hip, 64, 20, 64, 20, 1, 448, 448),
                               bench_paged_attn(ctx, hip, 32, 2, 128, 16, 512, 4096, 4096)],
+            "encoder": lambda: [bench_encoder(ctx, hip, 1), bench_encoder(ctx, hip, 16)],
+            "decoder": lambda: bench_decoder(ctx, hip),
         }
         for name in args.only.split(","):
             res = legs[name]()
@@ -322,6 +427,8 @@ def main():
     sdpa_run = bench_sdpa(ctx, hip)
     paged_runs = [bench_paged_attn(ctx, hip, 64, 20, 64, 20, 1, 448, 448),
                   bench_paged_attn(ctx, hip, 32, 2, 128, 16, 512, 4096, 4096)]
+    encoder_runs = [bench_encoder(ctx, hip, 1), bench_encoder(ctx, hip, 16)]
+    decoder_run = bench_decoder(ctx, hip)
 
     M, N, K = main_run["M"], main_run["N"], main_run["K"]
     achieved = main_run["gemm_tops"]
@@ -354,6 +461,8 @@ def main():
             "q4_k_decode_layer_m32": q4k_run,
             "sdpa_config1": sdpa_run,
             "paged_attn_config3_config4": paged_runs,
+            "encoder_config2": encoder_runs,
+            "decoder_step_config3": decoder_run,
             "gemm_kernel_ms": round(main_run["gemm_ms"], 4),
             "gemm_frac_of_bf16_mfma_peak": round(achieved / PEAK["bf16_tflops"], 4),
             "pow2_act": {"tops": round(pow2_run["tops"], 2), "gemm_tops": round(pow2_run["gemm_tops"], 2),
