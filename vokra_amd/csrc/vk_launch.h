@@ -6,8 +6,8 @@
 #include <stdint.h>
 
 namespace vk {
-constexpr int GEMM_TM = 256;  // block GEMM workgroup tile (rows of A)
-constexpr int GEMM_TN = 128;  // block GEMM workgroup tile (rows of W)
+constexpr int GEMM_TM = 128;  // block GEMM padding of m (a multiple of its workgroup tile)
+constexpr int GEMM_TN = 128;  // block GEMM padding of n (a multiple of its workgroup tile)
 
 hipError_t launch_dequantize_q0(hipStream_t s, int mode, const uint8_t* bytes, size_t n_blocks, float* out);
 hipError_t launch_pack_q0(hipStream_t s, int mode, const float* x, size_t n_blocks, uint8_t* out);

@@ -268,41 +268,79 @@ __global__ void vk_repack_w_b32(int mode, const uint8_t* __restrict__ wq, int n,
 // the A operand already carries 2^e and the combine is fmaf(dw, P_b, .),
 // which is the same value (the power-of-two product sa * dw is exact).
 //
-// Workgroup tile 256 (m) x 128 (n): 8 waves in 4 x 2, wave tile 64 x 64 =
-// 4 x 4 MFMA tiles, one quant block (K = 32) per pipeline stage. Operands
-// are staged global -> registers -> LDS (double-buffered): two register sets
-// keep the loads for the next two stages in flight while a stage computes.
-// Barriers are bare s_barrier: __syncthreads() would also fence, which waits
-// for every load in flight and would serialize the pipeline.
+// Workgroup tile 128 (m) x 128 (n): 4 waves in 2 x 2, wave tile 64 x 64 =
+// 4 x 4 MFMA tiles, one quant block (K = 32) per pipeline stage; two
+// workgroups per CU, so one's barrier wait overlaps the other's compute.
+// Operands move global -> LDS directly (no staging registers) through a
+// three-stage ring. Inside a wave the MFMAs of a block are interleaved with
+// the VALU combine of earlier tiles, so the matrix core runs under the VALU
+// work (two VALU ops per output per block: the larger cost of the two).
 // Tile order is XCD-aware: workgroup i runs on XCD i % 8, so each XCD gets a
 // contiguous run of tiles, ordered n-tile-major to share W tiles in its L2.
 // The epilogue transposes each wave's 16 x 64 row strips through LDS so rows
-// leave as full 256-byte dwordx4 stores.
+// leave as full 256-byte dwordx4 stores (streaming: the result is not re-read
+// by this kernel).
 namespace gemm {
-constexpr int TM = 256, TN = 128, THREADS = 512;
-constexpr int MT = TM / 16, NT = TN / 16;  // fragment tiles per workgroup tile
-constexpr int FRAG_U4 = 64;                // uint4 per 16x32 fragment (1 KiB)
+constexpr int WM = 2, WN = 2;                 // waves per workgroup (m x n)
+constexpr int THREADS = 64 * WM * WN;
+constexpr int TM = 64 * WM, TN = 64 * WN;     // workgroup tile
+constexpr int MT = TM / 16, NT = TN / 16;     // fragment tiles per workgroup tile
+constexpr int FRAG_U4 = 64;                   // uint4 per 16x32 fragment (1 KiB)
 constexpr int N_XCD = 8;
+constexpr int NS = 3;                         // LDS stages
+constexpr int LAG = 3;                        // MFMA -> combine distance (tiles)
 }  // namespace gemm
 
-struct vk_stage_regs {
-    uint4 a0, a1, b0;
-    float s;
-};
+// Direct global -> LDS loads (global_load_lds_dwordx4 / _dword). M0 holds the
+// wave-uniform LDS base; lane l writes base + l * size. They are issued from
+// inline asm so the compiler does not fence every LDS read on them; their
+// completion is tracked by hand with vmcnt (loads retire in issue order).
+// Nothing else in the kernels that use them reads M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void vk_dma_b128(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void vk_dma_b32(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_base)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t vk_lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// Wait until at most N of this thread's loads are in flight and every LDS
+// access has completed, then barrier.
+template <int N>
+__device__ __forceinline__ void vk_wait_vm_barrier() {
+    static_assert(N == 0 || N == 5, "vmcnt values in use");
+    if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 template <bool POW2>
-__global__ __launch_bounds__(512, 1) void vk_gemm_qblock(
+__global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
     const uint4* __restrict__ afrag, const float* __restrict__ ascale,
     const uint4* __restrict__ wfrag, const float* __restrict__ wscale, const float* __restrict__ bias,
     float* __restrict__ out, int m, int n, int nb, int ldo, int m_pad, int n_pad) {
     using namespace gemm;
-    __shared__ uint4 lds_a[2][MT * FRAG_U4];  // 2 x 16 KiB; reused by the epilogue
-    __shared__ uint4 lds_b[2][NT * FRAG_U4];  // 2 x 8 KiB
-    __shared__ float lds_sa[2][TM];
-    __shared__ float lds_dw[2][TN];
+    constexpr int WAVES = WM * WN;
+    constexpr int APT = MT * FRAG_U4 / THREADS, BPT = NT * FRAG_U4 / THREADS;  // uint4 loads per thread
+    static_assert(APT * THREADS == MT * FRAG_U4 && BPT * THREADS == NT * FRAG_U4, "fragment split");
+    static_assert(TM + TN <= THREADS, "one scale per thread");
+    constexpr int LOADS = APT + BPT + 1;  // loads per thread per stage
+    static_assert(LOADS == 5, "vk_wait_vm_barrier<5>");
+    __shared__ __align__(16) uint4 lds_a[NS][MT * FRAG_U4];  // 3 x 8 KiB; reused by the epilogue
+    __shared__ __align__(16) uint4 lds_b[NS][NT * FRAG_U4];  // 3 x 8 KiB
+    // Block scales: [0, TM) activation rows, [TM, TM + TN) weight columns.
+    __shared__ __align__(16) float lds_s[NS][THREADS];
+    static_assert(sizeof(lds_a[0]) * 2 >= (size_t)THREADS * 64, "epilogue slots");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave - wm * WN;
 
     // XCD-aware tile index: workgroups L, L+8, L+16, ... share an XCD.
     const int tiles_m = m_pad / TM, tiles_n = n_pad / TN, tiles = tiles_m * tiles_n;
@@ -312,30 +350,28 @@ __global__ __launch_bounds__(512, 1) void vk_gemm_qblock(
     const int ntile = t / tiles_m, mtile = t - ntile * tiles_m;
     const int mt0 = mtile * MT, nt0 = ntile * NT;
 
-    // Per-thread slice of one stage: A fragment quads tid and tid+512, B quad
-    // tid, and one scale (threads 0..255: A, 256..383: W, the rest idle).
-    const size_t a_base0 = (size_t)(mt0 + (tid >> 6)) * nb * FRAG_U4 + lane;
-    const size_t a_base1 = (size_t)(mt0 + 8 + (tid >> 6)) * nb * FRAG_U4 + lane;
-    const size_t b_base0 = (size_t)(nt0 + (tid >> 6)) * nb * FRAG_U4 + lane;
-    const bool s_live = tid < TM + TN;
+    // Per-thread slice of one stage: A fragments wave + q WAVES (q < APT), B
+    // fragments likewise, and one scale (threads [0, TM): A rows, [TM, TM+TN):
+    // W columns).
+    const uint4* a_src = afrag + (size_t)(mt0 + wave) * nb * FRAG_U4 + lane;
+    const uint4* b_src = wfrag + (size_t)(nt0 + wave) * nb * FRAG_U4 + lane;
     const float* s_src = tid < TM ? ascale + mt0 * 16 + tid : wscale + nt0 * 16 + (tid - TM);
     const int s_stride = tid < TM ? m_pad : n_pad;
+    // wave-uniform LDS destinations (bytes)
+    const uint32_t la = __builtin_amdgcn_readfirstlane(vk_lds_addr(&lds_a[0][wave * 64]));
+    const uint32_t lb = __builtin_amdgcn_readfirstlane(vk_lds_addr(&lds_b[0][wave * 64]));
+    const uint32_t ls = __builtin_amdgcn_readfirstlane(vk_lds_addr(&lds_s[0][wave * 64]));
+    constexpr uint32_t A_STAGE = MT * FRAG_U4 * 16, B_STAGE = NT * FRAG_U4 * 16, S_STAGE = THREADS * 4;
 
-    auto gload = [=](int b) -> vk_stage_regs {
+    auto issue = [&](int b, int buf) {
         const size_t o = (size_t)b * FRAG_U4;
-        vk_stage_regs r;
-        r.a0 = afrag[a_base0 + o];
-        r.a1 = afrag[a_base1 + o];
-        r.b0 = wfrag[b_base0 + o];
-        r.s = s_live ? s_src[(size_t)b * s_stride] : 0.0f;
-        return r;
-    };
-    auto lstore = [&](const vk_stage_regs r, int buf) {
-        lds_a[buf][tid] = r.a0;
-        lds_a[buf][tid + THREADS] = r.a1;
-        lds_b[buf][tid] = r.b0;
-        if (tid < TM) lds_sa[buf][tid] = r.s;
-        else if (tid < TM + TN) lds_dw[buf][tid - TM] = r.s;
+#pragma unroll
+        for (int q = 0; q < APT; ++q)
+            vk_dma_b128(a_src + (size_t)q * WAVES * nb * FRAG_U4 + o, la + buf * A_STAGE + q * WAVES * 1024);
+#pragma unroll
+        for (int q = 0; q < BPT; ++q)
+            vk_dma_b128(b_src + (size_t)q * WAVES * nb * FRAG_U4 + o, lb + buf * B_STAGE + q * WAVES * 1024);
+        vk_dma_b32(s_src + (size_t)b * s_stride, ls + buf * S_STAGE);
     };
 
     vk_f32x4 acc[4][4];
@@ -351,46 +387,60 @@ __global__ __launch_bounds__(512, 1) void vk_gemm_qblock(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             af[i] = __builtin_bit_cast(vk_bf16x8, lds_a[buf][(wm * 4 + i) * FRAG_U4 + lane]);
-            const float4 s4 = reinterpret_cast<const float4*>(lds_sa[buf] + (wm * 4 + i) * 16)[lane >> 4];
-            sa[i][0] = s4.x; sa[i][1] = s4.y; sa[i][2] = s4.z; sa[i][3] = s4.w;
+            if (!POW2) {
+                const float4 s4 = reinterpret_cast<const float4*>(lds_s[buf] + (wm * 4 + i) * 16)[lane >> 4];
+                sa[i][0] = s4.x; sa[i][1] = s4.y; sa[i][2] = s4.z; sa[i][3] = s4.w;
+            }
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             bf[j] = __builtin_bit_cast(vk_bf16x8, lds_b[buf][(wn * 4 + j) * FRAG_U4 + lane]);
-            dw[j] = lds_dw[buf][(wn * 4 + j) * 16 + (lane & 15)];
+            dw[j] = lds_s[buf][TM + (wn * 4 + j) * 16 + (lane & 15)];
+        }
+        vk_f32x4 p[16];
+        auto combine = [&](int t) {
+            const int i = t >> 2, j = t & 3;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (POW2) acc[i][j][r] = fmaf(dw[j], p[t][r], acc[i][j][r]);
+                else acc[i][j][r] = fmaf(sa[i][r] * dw[j], p[t][r], acc[i][j][r]);
+            }
+        };
+        // Issue order is pinned (sched_barrier): MFMA t, then the combine of
+        // tile t - LAG, whose product has retired; LAG + 1 products are live.
+        // The combine order per output stays block order.
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            p[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t >> 2], bf[t & 3], zero, 0, 0, 0);
+            if (t >= LAG) combine(t - LAG);
+            __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const vk_f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], zero, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    if (POW2) acc[i][j][r] = fmaf(dw[j], p[r], acc[i][j][r]);
-                    else acc[i][j][r] = fmaf(sa[i][r] * dw[j], p[r], acc[i][j][r]);
-                }
-            }
+        for (int t = 16 - LAG; t < 16; ++t) combine(t);
     };
 
-    // Loads past the last block re-read block nb-1 (in bounds, never used),
-    // which keeps the loop free of conditionals around the staging registers.
+    // Stage ring of NS = 3: the loads for block b+2 are issued once every wave
+    // has passed block b-1 (the barrier), into the buffer block b-1 used. At
+    // the wait, this thread's loads for blocks b and b+1 may be outstanding:
+    // vmcnt(LOADS) retires block b's. Loads past the last block re-read block
+    // nb-1 into a buffer no later block reads, so every iteration issues
+    // exactly LOADS loads. One block per iteration (no unrolling) keeps the
+    // accumulators in fixed registers.
     const int last = nb - 1;
-    vk_stage_regs r0 = gload(0);
-    vk_stage_regs r1 = gload(min(1, last));
-    lstore(r0, 0);
-    r0 = gload(min(2, last));
-    VK_LDS_BARRIER();
-    for (int b = 0; b < nb; b += 2) {
-        compute(0);  // stage b
-        if (b + 1 < nb) lstore(r1, 1);
-        r1 = gload(min(b + 3, last));
-        VK_LDS_BARRIER();
-        if (b + 1 >= nb) break;
-        compute(1);  // stage b + 1
-        if (b + 2 < nb) lstore(r0, 0);
-        r0 = gload(min(b + 4, last));
-        VK_LDS_BARRIER();
+    issue(0, 0);
+    issue(min(1, last), 1);
+    int buf = 0, nbuf = 2;
+#pragma unroll 1
+    for (int b = 0; b < nb; ++b) {
+        vk_wait_vm_barrier<LOADS>();
+        issue(min(b + 2, last), nbuf);
+        compute(buf);
+        buf = buf == NS - 1 ? 0 : buf + 1;
+        nbuf = nbuf == NS - 1 ? 0 : nbuf + 1;
     }
+    // every load has landed and every wave is done reading before the
+    // epilogue reuses the A buffers
+    vk_wait_vm_barrier<0>();
 
     // Epilogue. D layout of v_mfma_f32_16x16x32_bf16: lane l holds rows
     // 4*(l/16)+r of column l%16. Each wave owns a 4 KiB LDS slot; per m-subtile
@@ -418,7 +468,8 @@ __global__ __launch_bounds__(512, 1) void vk_gemm_qblock(
                     const float4 bv = *reinterpret_cast<const float4*>(bias + col0 + c4);
                     v.x = v.x + bv.x; v.y = v.y + bv.y; v.z = v.z + bv.z; v.w = v.w + bv.w;
                 }
-                *reinterpret_cast<float4*>(out + (size_t)row * ldo + col0 + c4) = v;
+                __builtin_nontemporal_store((vk_f32x4){v.x, v.y, v.z, v.w},
+                                            reinterpret_cast<vk_f32x4*>(out + (size_t)row * ldo + col0 + c4));
             } else {
                 const float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -507,9 +558,13 @@ hipError_t launch_repack_w_b32(hipStream_t s, int mode, const uint8_t* wq, int n
     return hipGetLastError();
 }
 
+// The C-ABI layer pads m and n to GEMM_TM / GEMM_TN: whole workgroup tiles.
+static_assert(GEMM_TM % gemm::TM == 0 && GEMM_TN % gemm::TN == 0, "GEMM padding");
+
 hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
                               const uint4* wfrag, const float* wscale, const float* bias, float* out,
                               int m, int m_pad, int n, int n_pad, int nb) {
+    if (m_pad % gemm::TM != 0 || n_pad % gemm::TN != 0 || nb < 1) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((n_pad / gemm::TN) * (m_pad / gemm::TM)));
     if (pow2)
         hipLaunchKernelGGL(vk_gemm_qblock<true>, grid, dim3(gemm::THREADS), 0, s, afrag, ascale, wfrag, wscale, bias,
