@@ -5,7 +5,9 @@ Workload (single GPU): the Whisper-large-v3 Q8_0
 linear, out[M=1500, N=5120] = a[1500, 1280] . dequant(W[5120, 1280])^T with
 a ~ N(0,1) f32 and W ~ N(0,0.02) packed to Q8_0 (synthetic, seeded). One step
 = the whole gemm_q_f32 op on HBM-resident inputs: the INT8 activation pass
-plus the MFMA block GEMM, f32 output written to HBM.
+plus the MFMA block GEMM, f32 output written to HBM. The K timed steps are
+captured into one HIP graph and replayed with one launch (the eager,
+Python-issued loop is reported beside it as extra.eager_step_ms).
 
 Prints ONE JSON line. `value` is whole-op throughput in TOPS (2*M*N*K per
 step); `roofline` is the GEMM kernel alone, timed with HIP events on the
@@ -65,17 +67,31 @@ def bench_q8_gemm(ctx, hip, steps, warmup, act):
         if ev is not None:
             ev[1].record()
 
-    wall_ms, _ = timed_steps(ctx, hip, steps, warmup, launch, "vk_gemm_qblock")
-    # the GEMM kernel alone: back-to-back launches on the library's stream
-    # between two HIP events (the per-launch average rocprof reports)
+    eager_ms, _ = timed_steps(ctx, hip, steps, warmup, launch, "vk_gemm_qblock")
+    # The timed steps: the same two launches (quantize, GEMM) per step, all
+    # `steps` of them captured into one HIP graph and replayed with one launch,
+    # the way a serving loop issues them, so the number is device time rather
+    # than Python call overhead (about 8 us per graph launch from Python).
+    warm = ctx.capture(lambda: [launch(None) for _ in range(max(warmup, 1))])
+    timed = ctx.capture(lambda: [launch(None) for _ in range(steps)])
+    warm.launch()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    timed.launch()
+    ctx.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    # the GEMM kernel alone: `steps` back-to-back launches replayed from one
+    # graph on the library's stream, between two HIP events (the per-launch
+    # average rocprof reports for this kernel)
+    gemms = ctx.capture(lambda: [ctx.gemm_qact_dev(W, qa, d_out) for _ in range(steps)])
+    gemms.launch()
     e0, e1 = hip.Event(ctx), hip.Event(ctx)
     e0.record()
-    for _ in range(steps):
-        ctx.gemm_qact_dev(W, qa, d_out)
+    gemms.launch()
     e1.record()
     kern_ms = e0.elapsed_ms(e1) / steps
     ops = 2.0 * M * N * K
-    return {"M": M, "N": N, "K": K, "wall_ms": wall_ms, "gemm_ms": kern_ms,
+    return {"M": M, "N": N, "K": K, "wall_ms": wall_ms, "eager_ms": eager_ms, "gemm_ms": kern_ms,
             "tops": ops / (wall_ms * 1e-3) / 1e12, "gemm_tops": ops / (kern_ms * 1e-3) / 1e12,
             "a": a, "wq": wq}
 
@@ -464,6 +480,7 @@ def main():
             "encoder_config2": encoder_runs,
             "decoder_step_config3": decoder_run,
             "gemm_kernel_ms": round(main_run["gemm_ms"], 4),
+            "eager_step_ms": round(main_run["eager_ms"], 4),
             "gemm_frac_of_bf16_mfma_peak": round(achieved / PEAK["bf16_tflops"], 4),
             "pow2_act": {"tops": round(pow2_run["tops"], 2), "gemm_tops": round(pow2_run["gemm_tops"], 2),
                          "gemm_ms": round(pow2_run["gemm_ms"], 4),

@@ -163,13 +163,17 @@ template <bool POW2>
 __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pad, int k,
                                     uint4* __restrict__ afrag, float* __restrict__ ascale,
                                     float* __restrict__ asum) {
+    // One wave per 16-row x 32-column fragment: lane l = mr + 16 c quantizes
+    // row mr, elements 8c .. 8c+7, and stores its 16 bytes at lane l of the
+    // fragment, so every wave writes one contiguous KiB.
     const int nb = k >> 5;
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const size_t total = (size_t)m_pad * nb * 4;
-    if (gid >= total) return;  // total is a multiple of 4: whole groups exit together
-    const int c = (int)(gid & 3);
-    const size_t rb = gid >> 2;  // row-block index
-    const int row = (int)(rb / nb), b = (int)(rb % nb);
+    if (gid >= total) return;  // total is a multiple of 64: whole waves exit together
+    const int lane = (int)(gid & 63), c = lane >> 4, mr = lane & 15;
+    const size_t frag = gid >> 6;  // = mt * nb + b
+    const int mt = (int)(frag / nb), b = (int)(frag % nb);
+    const int row = mt * 16 + mr;
     float v[8];
     if (row < m) {
         const float4* src = reinterpret_cast<const float4*>(a + (size_t)row * k + b * 32 + 8 * c);
@@ -183,7 +187,8 @@ __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pa
     float amax = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
-    amax = vk_group_max<4>(amax);
+    amax = fmaxf(amax, __shfl_xor(amax, 16, VK_WAVE));  // the four lanes of a row: l, l^16, l^32, l^48
+    amax = fmaxf(amax, __shfl_xor(amax, 32, VK_WAVE));
     float s = 0.0f;
     int q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (amax != 0.0f) {
@@ -204,7 +209,8 @@ __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pa
     int gs = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) gs += q[e];
-    gs = vk_group_sum_i<4>(gs);
+    gs += __shfl_xor(gs, 16, VK_WAVE);
+    gs += __shfl_xor(gs, 32, VK_WAVE);
     uint32_t w[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -218,9 +224,7 @@ __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pa
         }
         w[e] = lo | (hi << 16);
     }
-    const int mt = row >> 4, mr = row & 15;
-    const size_t frag = (size_t)mt * nb + b;
-    afrag[frag * 64 + (size_t)(mr + 16 * c)] = make_uint4(w[0], w[1], w[2], w[3]);
+    afrag[frag * 64 + (size_t)lane] = make_uint4(w[0], w[1], w[2], w[3]);
     if (c == 0) {  // scales and operand sums are block-major: [nb][m_pad]
         ascale[(size_t)b * m_pad + row] = s;
         // sum of the A operand values of this block (exact: an integer times
@@ -537,6 +541,7 @@ hipError_t launch_dequant_gemv_f32(hipStream_t s, int mode, const uint8_t* bytes
 
 hipError_t launch_quantize_act_b32(hipStream_t s, bool pow2, const float* a, int m, int m_pad, int k,
                                    uint4* afrag, float* ascale, float* asum) {
+    if (m_pad % 16 != 0) return hipErrorInvalidValue;  // whole fragments
     const size_t threads = (size_t)m_pad * (k / 32) * 4;
     if (threads == 0) return hipSuccess;
     const unsigned grid = (unsigned)((threads + 255) / 256);
