@@ -295,14 +295,19 @@ void release_weight(vokra_hip_qweight* w) {
     w->gsc.release();
 }
 
+// Whether w runs on the decode kernel for these activations.
+bool gemv_route(const vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_qact* qa) {
+    return !w->kquant && w->has_gemv && qa->m <= kGemvMaxM && c->decode_kernel;
+}
+
 int run_gemm_qact(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_qact* qa, const float* d_bias,
-                 float* d_out) {
+                  float* d_out, VkEpi epi = {nullptr, 0}) {
     if (w->kquant) {
         if (qa->act_quant != VOKRA_HIP_ACT_KQUANT)
             return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: Q4_K weights need KQUANT activations");
         VK_TRY(vk::launch_gemm_q4k(c->stream, (const uint4*)qa->frag.p, (const float*)qa->scale.p,
                                    (const float*)qa->gsum.p, (const uint4*)w->gq.p, (const float2*)w->gsc.p, d_bias,
-                                   d_out, (int)qa->m, (int)w->n, (int)w->nb, (int)qa->m_pad),
+                                   d_out, (int)qa->m, (int)w->n, (int)w->nb, (int)qa->m_pad, epi),
                "launch(vk_gemm_q4k)");
         return VOKRA_HIP_OK;
     }
@@ -310,18 +315,18 @@ int run_gemm_qact(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: block-format weights need AMAX127 or POW2 activations");
     // Both kernels produce bit-identical outputs; the decode kernel streams
     // the compact weights once, the GEMM reuses bf16 tiles across many rows.
-    if (w->has_gemv && qa->m <= kGemvMaxM && c->decode_kernel) {
+    if (gemv_route(c, w, qa)) {
+        const VkGemvLin lin = {(const uint4*)w->gq.p, (const uint2*)w->gsc.p, d_bias, d_out, epi, (int)w->n};
         VK_TRY(vk::launch_gemv_qblock(c->stream, wd_kv_mode(w->wdtype), qa->act_quant == VOKRA_HIP_ACT_POW2,
                                       (const uint4*)qa->frag.p, (const float*)qa->scale.p,
-                                      (const float*)qa->gsum.p, (const uint4*)w->gq.p, (const uint2*)w->gsc.p,
-                                      d_bias, d_out, (int)qa->m, (int)w->n, (int)w->nb, (int)qa->m_pad),
+                                      (const float*)qa->gsum.p, &lin, 1, (int)qa->m, (int)w->nb, (int)qa->m_pad),
                "launch(vk_gemv_qblock)");
         return VOKRA_HIP_OK;
     }
     VK_TRY(vk::launch_gemm_qblock(c->stream, qa->act_quant == VOKRA_HIP_ACT_POW2, (const uint4*)qa->frag.p,
                                   (const float*)qa->scale.p, (const uint4*)w->frag.p, (const float*)w->scale.p,
                                   d_bias, d_out, (int)qa->m, (int)qa->m_pad, (int)w->n, (int)w->n_pad,
-                                  (int)w->nb),
+                                  (int)w->nb, epi),
            "launch(vk_gemm_qblock)");
     return VOKRA_HIP_OK;
 }
@@ -450,6 +455,87 @@ int check_paged_attn(const vokra_hip_kv* kv, size_t layer, size_t n, size_t hq) 
 namespace vk {
 hipStream_t ctx_stream(const vokra_hip_ctx* c) { return c->stream; }
 int ctx_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+
+static int check_gemm_qact(const vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_qact* qa,
+                           const float* d_out) {
+    if (!c || !w || !qa || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: NULL argument");
+    if (w->ctx != c || qa->ctx != c)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: weight/activations belong to another context");
+    if (qa->m == 0) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: activations were never quantized");
+    if (qa->k != w->k)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: activation k=%zu != weight k=%zu", qa->k, w->k);
+    return VOKRA_HIP_OK;
+}
+
+int gemm_qact_epi(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_qact* qa, const float* d_bias,
+                  float* d_out, VkEpi epi) {
+    int st = check_gemm_qact(c, w, qa, d_out);
+    if (st) return st;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    return run_gemm_qact(c, w, qa, d_bias, d_out, epi);
+}
+
+int gemm_qact_multi(vokra_hip_ctx* c, int n, const vokra_hip_qweight* const* ws, const vokra_hip_qact* qa,
+                    const float* const* biases, float* const* outs) {
+    if (n < 1 || n > 3 || !ws || !outs) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact_multi: bad list");
+    bool one_launch = true;
+    for (int i = 0; i < n; ++i) {
+        int st = check_gemm_qact(c, ws[i], qa, outs[i]);
+        if (st) return st;
+        one_launch = one_launch && gemv_route(c, ws[i], qa) && ws[i]->wdtype == ws[0]->wdtype &&
+                     qa->act_quant != VOKRA_HIP_ACT_KQUANT;
+    }
+    VK_TRY(set_dev(c), "hipSetDevice");
+    if (!one_launch) {
+        for (int i = 0; i < n; ++i) {
+            int st = run_gemm_qact(c, ws[i], qa, biases ? biases[i] : nullptr, outs[i]);
+            if (st) return st;
+        }
+        return VOKRA_HIP_OK;
+    }
+    VkGemvLin lins[3];
+    for (int i = 0; i < n; ++i)
+        lins[i] = {(const uint4*)ws[i]->gq.p, (const uint2*)ws[i]->gsc.p, biases ? biases[i] : nullptr, outs[i],
+                   {nullptr, 0}, (int)ws[i]->n};
+    VK_TRY(vk::launch_gemv_qblock(c->stream, wd_kv_mode(ws[0]->wdtype), qa->act_quant == VOKRA_HIP_ACT_POW2,
+                                  (const uint4*)qa->frag.p, (const float*)qa->scale.p, (const float*)qa->gsum.p, lins,
+                                  n, (int)qa->m, (int)ws[0]->nb, (int)qa->m_pad),
+           "launch(vk_gemv_qblock x n)");
+    return VOKRA_HIP_OK;
+}
+
+int qact_ln_quantize(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, const float* d_in, const float* gamma,
+                     const float* beta, float eps, int act_quant, float* d_scratch) {
+    if (!c || !qa || !d_in || !gamma || !beta)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "ln_quantize: NULL argument");
+    if (qa->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "ln_quantize: qact belongs to another context");
+    if (m == 0 || m > qa->max_m)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "ln_quantize: m=%zu outside 1..%zu", m, qa->max_m);
+    VK_TRY(set_dev(c), "hipSetDevice");
+    const size_t k = qa->k;
+    if (act_quant == VOKRA_HIP_ACT_KQUANT || k > (size_t)vk::kLnQuantMaxK) {
+        // two passes through d_scratch [m, k]
+        if (!d_scratch) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "ln_quantize: this width needs a scratch buffer");
+        VK_TRY(vk::launch_layer_norm_f32(c->stream, d_in, d_scratch, (int)m, (int)k, gamma, beta, eps),
+               "launch(vk_layer_norm_f32)");
+        return quantize_activations(c, qa, d_scratch, m, k, act_quant);
+    }
+    if (act_quant != VOKRA_HIP_ACT_AMAX127 && act_quant != VOKRA_HIP_ACT_POW2)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "ln_quantize: unknown activation convention %d", act_quant);
+    if (qa->growable) {
+        int st = qact_reserve(qa, m, k);
+        if (st) return st;
+    }
+    const size_t m_pad = round_up(m, vk::GEMM_TM);
+    VK_TRY(vk::launch_ln_quantize_b32(c->stream, act_quant == VOKRA_HIP_ACT_POW2, d_in, (int)m, (int)m_pad, (int)k,
+                                      gamma, beta, eps, (uint4*)qa->frag.p, (float*)qa->scale.p,
+                                      (float*)qa->gsum.p),
+           "launch(vk_ln_quantize_b32)");
+    qa->m = m;
+    qa->m_pad = m_pad;
+    qa->act_quant = act_quant;
+    return VOKRA_HIP_OK;
+}
 }  // namespace vk
 
 extern "C" {
@@ -1399,14 +1485,7 @@ int vokra_hip_qact_quantize_dev(vokra_hip_ctx_t* c, vokra_hip_qact_t* qa, size_t
 
 int vokra_hip_gemm_qact_dev(vokra_hip_ctx_t* c, const vokra_hip_qweight_t* w, const vokra_hip_qact_t* qa,
                             const float* d_bias, float* d_out) {
-    if (!c || !w || !qa || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: NULL argument");
-    if (w->ctx != c || qa->ctx != c)
-        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: weight/activations belong to another context");
-    if (qa->m == 0) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: activations were never quantized");
-    if (qa->k != w->k)
-        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: activation k=%zu != weight k=%zu", qa->k, w->k);
-    VK_TRY(set_dev(c), "hipSetDevice");
-    return run_gemm_qact(c, w, qa, d_bias, d_out);
+    return vk::gemm_qact_epi(c, w, qa, d_bias, d_out, VkEpi{nullptr, 0});
 }
 
 }  // extern "C"

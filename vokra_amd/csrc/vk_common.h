@@ -5,6 +5,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include "vk_launch.h"
 #include <stdint.h>
 
 typedef __bf16 vk_bf16x8 __attribute__((ext_vector_type(8)));
@@ -97,4 +98,90 @@ __device__ __forceinline__ int vk_group_sum_i(int v) {
 #pragma unroll
     for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o, VK_WAVE);
     return v;
+}
+
+// GELU through the Abramowitz & Stegun 7.1.26 erf
+// (crates/vokra-backend-cpu/src/kernels/scalar.rs:126-172). Shared by the GELU
+// kernel and the GEMM epilogues, so a fused epilogue equals the separate pass.
+__device__ __forceinline__ float vk_erf_as(float x) {
+    const float P = 0.3275911f, A1 = 0.254829592f, A2 = -0.284496736f, A3 = 1.421413741f, A4 = -1.453152027f,
+                A5 = 1.061405429f;
+    const float sign = x < 0.0f ? -1.0f : 1.0f;
+    const float ax = fabsf(x);
+    const float t = 1.0f / (1.0f + P * ax);
+    const float poly = ((((A5 * t + A4) * t + A3) * t + A2) * t + A1) * t;
+    return sign * (1.0f - poly * expf(-ax * ax));
+}
+__device__ __forceinline__ float vk_gelu_as(float x) { return 0.5f * x * (1.0f + vk_erf_as(x * 0.70710678118654752440f)); }
+
+// What a GEMM epilogue applies after the bias: y = gelu(y) (an MLP's first
+// linear) and/or y = resid + y (a residual connection; resid may be the output
+// buffer itself: each element is read and written by the same thread). The
+// results equal the separate GELU / add passes bit for bit.
+__device__ __forceinline__ float vk_epi_apply(float v, const VkEpi& e, size_t idx) {
+    if (e.gelu) v = vk_gelu_as(v);
+    if (e.resid) v = e.resid[idx] + v;
+    return v;
+}
+
+// Sum over a 256-thread workgroup (4 waves): wave shuffle tree, then
+// (w0 + w1) + (w2 + w3). `red` is 4 floats of LDS. Every row-reduction kernel
+// that must agree bit for bit with another uses this one.
+__device__ __forceinline__ float vk_block_sum256(float v, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, VK_WAVE);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// LayerNorm statistics of one row by a 256-thread workgroup
+// (crates/vokra-backend-cpu/src/kernels/scalar.rs:201-222: mean, population
+// variance): thread t sums columns t, t + 256, ... in order, then
+// vk_block_sum256. Returns mean and 1 / sqrt(var + eps). The LayerNorm kernel
+// and the fused LayerNorm + activation pass both use these, so they agree bit
+// for bit. Rows up to kLnRegCols are held in registers (x[j] = column
+// t + 256 j), loaded together so their latencies overlap.
+constexpr int kLnRegCols = 2048;
+constexpr int kLnRegJ = kLnRegCols / 256;
+__device__ __forceinline__ void vk_row_load256(const float* __restrict__ row, int cols, float (&x)[kLnRegJ]) {
+#pragma unroll
+    for (int j = 0; j < kLnRegJ; ++j) {
+        const int c = (int)threadIdx.x + 256 * j;
+        x[j] = c < cols ? row[c] : 0.0f;
+    }
+}
+__device__ __forceinline__ float2 vk_ln_stats256(const float (&x)[kLnRegJ], int cols, float eps, float* red) {
+    const float inv_cols = 1.0f / (float)cols;
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kLnRegJ; ++j)
+        if ((int)threadIdx.x + 256 * j < cols) s += x[j];
+    const float mean = vk_block_sum256(s, red) * inv_cols;
+    float v = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kLnRegJ; ++j) {
+        const float dlt = x[j] - mean;
+        if ((int)threadIdx.x + 256 * j < cols) v += dlt * dlt;
+    }
+    const float inv_std = 1.0f / sqrtf(vk_block_sum256(v, red) * inv_cols + eps);
+    return make_float2(mean, inv_std);
+}
+// Same statistics, same order of operations, streaming any row length.
+__device__ __forceinline__ float2 vk_ln_stats256(const float* __restrict__ row, int cols, float eps, float* red) {
+    const float inv_cols = 1.0f / (float)cols;
+    float s = 0.0f;
+    for (int c = threadIdx.x; c < cols; c += 256) s += row[c];
+    const float mean = vk_block_sum256(s, red) * inv_cols;
+    float v = 0.0f;
+    for (int c = threadIdx.x; c < cols; c += 256) {
+        const float dlt = row[c] - mean;
+        v += dlt * dlt;
+    }
+    const float inv_std = 1.0f / sqrtf(vk_block_sum256(v, red) * inv_cols + eps);
+    return make_float2(mean, inv_std);
+}
+__device__ __forceinline__ float vk_ln_apply(float x, float2 st, float g, float b) {
+    return (x - st.x) * st.y * g + b;
 }

@@ -123,14 +123,7 @@ __global__ __launch_bounds__(256) void vk_gemv_f32(const float* __restrict__ a, 
 
 // ---------------------------------------------------------------------------
 // Row reductions over a 256-thread workgroup.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, VK_WAVE);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
-}
+__device__ __forceinline__ float block_sum(float v, float* red) { return vk_block_sum256(v, red); }
 __device__ __forceinline__ float block_max(float v, float* red) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, VK_WAVE));
@@ -160,24 +153,26 @@ __global__ __launch_bounds__(256) void vk_softmax_f32(const float* __restrict__ 
 }
 
 // layer_norm (scalar.rs:201-222): population variance, then
-// (x - mean) * inv_std * gamma + beta per element.
+// (x - mean) * inv_std * gamma + beta per element; one row per workgroup.
 __global__ __launch_bounds__(256) void vk_layer_norm_f32(const float* __restrict__ in, float* __restrict__ out,
                                                          int cols, const float* __restrict__ gamma,
                                                          const float* __restrict__ beta, float eps) {
     __shared__ float red[4];
     const float* ir = in + (size_t)blockIdx.x * cols;
     float* orow = out + (size_t)blockIdx.x * cols;
-    const float inv_cols = 1.0f / (float)cols;
-    float s = 0.0f;
-    for (int c = threadIdx.x; c < cols; c += 256) s += ir[c];
-    const float mean = block_sum(s, red) * inv_cols;
-    float v = 0.0f;
-    for (int c = threadIdx.x; c < cols; c += 256) {
-        const float dlt = ir[c] - mean;
-        v += dlt * dlt;
+    if (cols <= kLnRegCols) {
+        float x[kLnRegJ];
+        vk_row_load256(ir, cols, x);
+        const float2 st = vk_ln_stats256(x, cols, eps, red);
+#pragma unroll
+        for (int j = 0; j < kLnRegJ; ++j) {
+            const int c = (int)threadIdx.x + 256 * j;
+            if (c < cols) orow[c] = vk_ln_apply(x[j], st, gamma[c], beta[c]);
+        }
+        return;
     }
-    const float inv_std = 1.0f / sqrtf(block_sum(v, red) * inv_cols + eps);
-    for (int c = threadIdx.x; c < cols; c += 256) orow[c] = (ir[c] - mean) * inv_std * gamma[c] + beta[c];
+    const float2 st = vk_ln_stats256(ir, cols, eps, red);
+    for (int c = threadIdx.x; c < cols; c += 256) orow[c] = vk_ln_apply(ir[c], st, gamma[c], beta[c]);
 }
 
 // rms_norm (crates/vokra-models/src/voxtral/text_decoder.rs:801-822).
@@ -192,26 +187,15 @@ __global__ __launch_bounds__(256) void vk_rms_norm_f32(const float* __restrict__
     for (int c = threadIdx.x; c < cols; c += 256) orow[c] = ir[c] * inv * gamma[c];
 }
 
-// GELU through the Abramowitz & Stegun 7.1.26 erf (scalar.rs:126-172).
-__device__ __forceinline__ float erf_as(float x) {
-    const float P = 0.3275911f, A1 = 0.254829592f, A2 = -0.284496736f, A3 = 1.421413741f, A4 = -1.453152027f,
-                A5 = 1.061405429f;
-    const float sign = x < 0.0f ? -1.0f : 1.0f;
-    const float ax = fabsf(x);
-    const float t = 1.0f / (1.0f + P * ax);
-    const float poly = ((((A5 * t + A4) * t + A3) * t + A2) * t + A1) * t;
-    return sign * (1.0f - poly * expf(-ax * ax));
-}
-__device__ __forceinline__ float gelu_as(float x) { return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752440f)); }
-
+// GELU through the Abramowitz & Stegun 7.1.26 erf (vk_gelu_as, scalar.rs:126-172).
 __global__ void vk_gelu_f32(const float* __restrict__ x, float* __restrict__ out, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        out[i] = gelu_as(x[i]);
+        out[i] = vk_gelu_as(x[i]);
 }
 
 // out = a + b (residual connections).
-__global__ void vk_add_f32(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out,
-                           size_t n) {
+// out may be a or b (in place): each element is read and written by one thread.
+__global__ void vk_add_f32(const float* a, const float* b, float* out, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         out[i] = a[i] + b[i];
 }

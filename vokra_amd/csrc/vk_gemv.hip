@@ -20,6 +20,10 @@
 // a power of two for POW2 activations) below 2^24, so D = P_b exactly.
 #include "vk_common.h"
 
+#include <algorithm>
+
+#include "vk_launch.h"
+
 namespace vk {
 
 namespace gemv {
@@ -118,12 +122,22 @@ constexpr int CB = 48;                 // blocks per chunk (12 groups)
 constexpr int GPW = CB / GB / WAVES;   // groups per wave per chunk (3)
 }  // namespace gemv
 
+// Up to three linears over the same activations in one launch (grid z picks
+// the linear; q, k and v of an attention block share their input).
+struct GemvSet {
+    VkGemvLin lin[3];
+};
+
 template <int MODE, bool POW2>
 __global__ __launch_bounds__(256) void vk_gemv_qblock(
     const uint4* __restrict__ afrag, const float* __restrict__ ascale, const float* __restrict__ asum,
-    const uint4* __restrict__ wq4, const uint2* __restrict__ wsc, const float* __restrict__ bias,
-    float* __restrict__ out, int m, int n, int nb, int m_pad, int n_tiles) {
+    const GemvSet set, int m, int nb, int m_pad) {
     using namespace gemv;
+    const VkGemvLin& lin = set.lin[blockIdx.z];
+    const uint4* __restrict__ wq4 = lin.wq4;
+    const uint2* __restrict__ wsc = lin.wsc;
+    const int n = lin.n;
+    if ((int)blockIdx.x * 16 >= n) return;  // this linear has fewer column tiles (whole workgroup)
     constexpr int WQ = MODE == 1 ? 1 : 2;  // weight uint4 per lane per group
     constexpr float OFFSET = MODE == 1 ? -136.0f : -128.0f;
     __shared__ float lds_p[CB][256];       // exact block dots, [block][row*16 + col]
@@ -219,12 +233,13 @@ __global__ __launch_bounds__(256) void vk_gemv_qblock(
         VK_LDS_BARRIER();
     }
     const int row = mt * 16 + (tid >> 4), col = nt * 16 + (tid & 15);
-    if (row < m && col < n) out[(size_t)row * n + col] = bias ? acc + bias[col] : acc;
+    if (row < m && col < n) {
+        const size_t o = (size_t)row * n + col;
+        lin.out[o] = vk_epi_apply(lin.bias ? acc + lin.bias[col] : acc, lin.epi, o);
+    }
 }
 
 }  // namespace vk
-
-#include "vk_launch.h"
 
 namespace vk {
 
@@ -238,22 +253,29 @@ hipError_t launch_repack_w_gemv(hipStream_t s, int mode, const uint8_t* wq, int 
 }
 
 template <int MODE, bool POW2>
-static hipError_t go(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum, const uint4* wq4,
-                     const uint2* wsc, const float* bias, float* out, int m, int n, int nb, int m_pad) {
-    const int n_tiles = (n + 15) / 16, m_tiles = (m + 15) / 16;
-    hipLaunchKernelGGL((vk_gemv_qblock<MODE, POW2>), dim3(n_tiles, m_tiles), dim3(256), 0, s, afrag, ascale, asum,
-                       wq4, wsc, bias, out, m, n, nb, m_pad, n_tiles);
+static hipError_t go(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum, const GemvSet& set,
+                     int n_lin, int n_max, int m, int nb, int m_pad) {
+    const int n_tiles = (n_max + 15) / 16, m_tiles = (m + 15) / 16;
+    hipLaunchKernelGGL((vk_gemv_qblock<MODE, POW2>), dim3(n_tiles, m_tiles, n_lin), dim3(256), 0, s, afrag, ascale,
+                       asum, set, m, nb, m_pad);
     return hipGetLastError();
 }
 
 hipError_t launch_gemv_qblock(hipStream_t s, int mode, bool pow2, const uint4* afrag, const float* ascale,
-                              const float* asum, const uint4* wq4, const uint2* wsc, const float* bias, float* out,
-                              int m, int n, int nb, int m_pad) {
+                              const float* asum, const VkGemvLin* lins, int n_lin, int m, int nb, int m_pad) {
+    if (n_lin < 1 || n_lin > 3 || m < 1) return hipErrorInvalidValue;
+    GemvSet set = {};
+    int n_max = 0;
+    for (int i = 0; i < n_lin; ++i) {
+        set.lin[i] = lins[i];
+        n_max = std::max(n_max, lins[i].n);
+    }
+    if (n_max < 1) return hipSuccess;
     if (mode == 1)
-        return pow2 ? go<1, true>(s, afrag, ascale, asum, wq4, wsc, bias, out, m, n, nb, m_pad)
-                    : go<1, false>(s, afrag, ascale, asum, wq4, wsc, bias, out, m, n, nb, m_pad);
-    return pow2 ? go<3, true>(s, afrag, ascale, asum, wq4, wsc, bias, out, m, n, nb, m_pad)
-                : go<3, false>(s, afrag, ascale, asum, wq4, wsc, bias, out, m, n, nb, m_pad);
+        return pow2 ? go<1, true>(s, afrag, ascale, asum, set, n_lin, n_max, m, nb, m_pad)
+                    : go<1, false>(s, afrag, ascale, asum, set, n_lin, n_max, m, nb, m_pad);
+    return pow2 ? go<3, true>(s, afrag, ascale, asum, set, n_lin, n_max, m, nb, m_pad)
+                : go<3, false>(s, afrag, ascale, asum, set, n_lin, n_max, m, nb, m_pad);
 }
 
 }  // namespace vk

@@ -206,8 +206,8 @@ struct Stage {
 template <bool HAS_BIAS>
 __global__ __launch_bounds__(256) void vk_gemm_q4k(
     const uint4* __restrict__ afrag, const float* __restrict__ ascale, const float* __restrict__ asum,
-    const uint4* __restrict__ wq4, const float2* __restrict__ wdm, const float* __restrict__ bias,
-    float* __restrict__ out, int m, int n, int nsb, int m_pad) {
+    const uint4* __restrict__ wq4, const float2* __restrict__ wdm, const float* __restrict__ bias, VkEpi epi,
+    float* out, int m, int n, int nsb, int m_pad) {
     using namespace kq;
     __shared__ __align__(16) float lds_p[CG][256];    // isum, [group][row * 16 + col]
     // rows padded by one float4 against bank conflicts on the transposing stores
@@ -326,7 +326,10 @@ __global__ __launch_bounds__(256) void vk_gemm_q4k(
         VK_LDS_BARRIER();
     }
     const int orow = mt * 16 + row, ocol = nt * 16 + col;
-    if (orow < m && ocol < n) out[(size_t)orow * n + ocol] = HAS_BIAS ? acc + bias[ocol] : acc;
+    if (orow < m && ocol < n) {
+        const size_t o = (size_t)orow * n + ocol;
+        out[o] = vk_epi_apply(HAS_BIAS ? acc + bias[ocol] : acc, epi, o);
+    }
 }
 
 }  // namespace vk
@@ -362,14 +365,14 @@ hipError_t launch_repack_w_q4k(hipStream_t s, const uint8_t* wq, int n, int n_pa
 
 hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum,
                            const uint4* wq4, const float2* wdm, const float* bias, float* out, int m, int n, int nsb,
-                           int m_pad) {
+                           int m_pad, VkEpi epi) {
     const dim3 grid((n + 15) / 16, (m + 15) / 16);
     if (bias)
-        hipLaunchKernelGGL(vk_gemm_q4k<true>, grid, dim3(256), 0, s, afrag, ascale, asum, wq4, wdm, bias, out, m, n,
-                           nsb, m_pad);
+        hipLaunchKernelGGL(vk_gemm_q4k<true>, grid, dim3(256), 0, s, afrag, ascale, asum, wq4, wdm, bias, epi, out, m,
+                           n, nsb, m_pad);
     else
-        hipLaunchKernelGGL(vk_gemm_q4k<false>, grid, dim3(256), 0, s, afrag, ascale, asum, wq4, wdm, bias, out, m, n,
-                           nsb, m_pad);
+        hipLaunchKernelGGL(vk_gemm_q4k<false>, grid, dim3(256), 0, s, afrag, ascale, asum, wq4, wdm, bias, epi, out, m,
+                           n, nsb, m_pad);
     return hipGetLastError();
 }
 

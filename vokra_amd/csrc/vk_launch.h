@@ -5,6 +5,22 @@
 #include <stddef.h>
 #include <stdint.h>
 
+// What a GEMM epilogue applies after the bias (vk_common.h vk_epi_apply):
+// gelu != 0 -> y = gelu(y); resid != NULL -> y = resid + y (may alias the output).
+struct VkEpi {
+    const float* resid;
+    int gelu;
+};
+// One linear of a decode-kernel launch: compact weights, optional bias, output [m, n].
+struct VkGemvLin {
+    const uint4* wq4;
+    const uint2* wsc;
+    const float* bias;
+    float* out;
+    VkEpi epi;
+    int n;
+};
+
 namespace vk {
 constexpr int GEMM_TM = 128;  // block GEMM padding of m (a multiple of its workgroup tile)
 constexpr int GEMM_TN = 128;  // block GEMM padding of n (a multiple of its workgroup tile)
@@ -16,19 +32,26 @@ hipError_t launch_dequant_gemv_f32(hipStream_t s, int mode, const uint8_t* bytes
                                    const float* x, float* y);
 hipError_t launch_quantize_act_b32(hipStream_t s, bool pow2, const float* a, int m, int m_pad, int k,
                                    uint4* afrag, float* ascale, float* asum);
+// LayerNorm of [m, k] rows fused with the b32 activation pass (same results
+// as launch_layer_norm_f32 followed by launch_quantize_act_b32); k <= kLnQuantMaxK
+// (its LDS tile is k / 32 KiB).
+constexpr int kLnQuantMaxK = 2048;  // = kLnRegCols (vk_common.h)
+hipError_t launch_ln_quantize_b32(hipStream_t s, bool pow2, const float* a, int m, int m_pad, int k,
+                                  const float* gamma, const float* beta, float eps, uint4* afrag, float* ascale,
+                                  float* asum);
 hipError_t launch_repack_w_b32(hipStream_t s, int mode, const uint8_t* wq, int n, int n_pad, int nb,
                                uint4* wfrag, float* wscale);
 hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
                               const uint4* wfrag, const float* wscale, const float* bias, float* out, int m,
-                              int m_pad, int n, int n_pad, int nb);
+                              int m_pad, int n, int n_pad, int nb, VkEpi epi = {nullptr, 0});
 }  // namespace vk
 
 namespace vk {
 hipError_t launch_repack_w_gemv(hipStream_t s, int mode, const uint8_t* wq, int n, int n_pad, int nb, uint4* wq4,
                                 uint2* wsc);
+// n_lin (1..3) linears over the same activations, one launch.
 hipError_t launch_gemv_qblock(hipStream_t s, int mode, bool pow2, const uint4* afrag, const float* ascale,
-                              const float* asum, const uint4* wq4, const uint2* wsc, const float* bias, float* out,
-                              int m, int n, int nb, int m_pad);
+                              const float* asum, const VkGemvLin* lins, int n_lin, int m, int nb, int m_pad);
 }  // namespace vk
 
 namespace vk {
@@ -39,7 +62,7 @@ hipError_t launch_repack_w_q4k(hipStream_t s, const uint8_t* wq, int n, int n_pa
                                float2* wdm);
 hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum,
                            const uint4* wq4, const float2* wdm, const float* bias, float* out, int m, int n, int nsb,
-                           int m_pad);
+                           int m_pad, VkEpi epi = {nullptr, 0});
 }  // namespace vk
 
 namespace vk {
@@ -87,7 +110,21 @@ hipError_t launch_argmax_f32(hipStream_t s, const float* logits, int rows, int c
 }  // namespace vk
 
 struct vokra_hip_ctx;
+struct vokra_hip_qact;
+struct vokra_hip_qweight;
 namespace vk {
 hipStream_t ctx_stream(const vokra_hip_ctx* c);
 int ctx_fail(int code, const char* msg);
+// Fused forms of entry-point sequences for the sessions (vk_capi.hip); each
+// gives the same results as the sequence it replaces.
+//   gemm_qact_epi    = vokra_hip_gemm_qact_dev, then GELU and/or + resid
+//   gemm_qact_multi  = n (<= 3) vokra_hip_gemm_qact_dev over the same activations
+//   qact_ln_quantize = vokra_hip_layer_norm_f32_dev into d_scratch, then
+//                      vokra_hip_qact_quantize_dev (one kernel for AMAX127 / POW2)
+int gemm_qact_epi(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_qact* qa, const float* d_bias,
+                  float* d_out, VkEpi epi);
+int gemm_qact_multi(vokra_hip_ctx* c, int n, const vokra_hip_qweight* const* ws, const vokra_hip_qact* qa,
+                    const float* const* biases, float* const* outs);
+int qact_ln_quantize(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, const float* d_in, const float* gamma,
+                     const float* beta, float eps, int act_quant, float* d_scratch);
 }  // namespace vk

@@ -235,6 +235,77 @@ __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pa
 }
 
 // ---------------------------------------------------------------------------
+// LayerNorm fused with the activation pass: a 256-thread workgroup normalises
+// a row exactly as vk_layer_norm_f32 (vk_ln_stats256 / vk_ln_apply) and
+// quantizes it per 32-element block exactly as vk_quantize_act_b32 (thread t
+// holds columns t + 256 j, a block is one half-wave). The result equals
+// LayerNorm -> store -> quantize bit for bit, without the f32 round trip.
+//  * TILE: a workgroup takes a 16-row fragment tile, row after row, stages
+//    the bf16 operands in LDS in fragment order ((k / 32) KiB, dynamic) and
+//    stores the tile as contiguous 1 KiB fragments;
+//  * otherwise (a decode-sized batch): one row per workgroup, operands stored
+//    straight to the fragments.
+// Rows m .. m_pad-1 are zeros.
+static_assert(kLnQuantMaxK <= kLnRegCols, "the fused pass holds its row in registers");
+template <bool POW2, bool TILE>
+__global__ __launch_bounds__(256) void vk_ln_quantize_b32(const float* __restrict__ in, int m, int m_pad, int k,
+                                                          const float* __restrict__ gamma,
+                                                          const float* __restrict__ beta, float eps,
+                                                          uint4* __restrict__ afrag, float* __restrict__ ascale,
+                                                          float* __restrict__ asum) {
+    extern __shared__ uint4 lds_tile[];  // TILE: [nb][64] uint4 = the tile's fragments
+    __shared__ float red[4];
+    const int nb = k >> 5, t = threadIdx.x;
+    const int mt = TILE ? (int)blockIdx.x : (int)blockIdx.x >> 4;
+    uint16_t* tile16 = TILE ? reinterpret_cast<uint16_t*>(lds_tile)
+                            : reinterpret_cast<uint16_t*>(afrag + (size_t)mt * nb * 64);
+    for (int r = 0; r < (TILE ? 16 : 1); ++r) {
+        const int mr = TILE ? r : (int)blockIdx.x & 15;
+        const int row = mt * 16 + mr;
+        const bool live = row < m;  // uniform per workgroup
+        float x[kLnRegJ];
+        float2 st = make_float2(0.0f, 0.0f);
+        if (live) {
+            vk_row_load256(in + (size_t)row * k, k, x);
+            st = vk_ln_stats256(x, k, eps, red);
+        }
+#pragma unroll
+        for (int j = 0; j < kLnRegJ; ++j) {
+            const int c = t + 256 * j;
+            if (c - (t & 31) >= k) break;  // k is a multiple of 32: whole half-waves
+            const float v = live ? vk_ln_apply(x[j], st, gamma[c], beta[c]) : 0.0f;
+            // from 0 and through fmaxf, as the separate pass: NaN elements are ignored
+            const float amax = vk_group_max<32>(fmaxf(0.0f, fabsf(v)));
+            float s = 0.0f;
+            int q = 0;
+            if (amax != 0.0f) {
+                s = amax / 127.0f;
+                if (POW2) {
+                    int ex;
+                    const float f = frexpf(s, &ex);
+                    s = ldexpf(1.0f, f == 0.5f ? ex - 1 : ex);
+                }
+                const float rr = vk_round_half_away(v / s);
+                q = (rr != rr) ? 0 : (int)fminf(fmaxf(rr, -127.0f), 127.0f);
+            }
+            const int gs = vk_group_sum_i<32>(q);
+            const int b = c >> 5, e = c & 31;
+            tile16[((size_t)b * 64 + mr + 16 * (e >> 3)) * 8 + (e & 7)] =
+                (uint16_t)(POW2 ? (__float_as_uint((float)q * s) >> 16) : vk_int_to_bf16_bits(q));
+            if (e == 0) {
+                ascale[(size_t)b * m_pad + row] = s;
+                asum[(size_t)b * m_pad + row] = POW2 ? (float)gs * s : (float)gs;
+            }
+        }
+    }
+    if (TILE) {
+        __syncthreads();
+        uint4* dst = afrag + (size_t)mt * nb * 64;  // fragments (mt, 0 .. nb-1) are contiguous
+        for (int i = t; i < nb * 64; i += 256) dst[i] = lds_tile[i];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Weight repack (upload time): wire blocks [n][nb] -> bf16 integer fragments
 // [n_pad/16][nb][64][8] + f32 scales block-major [nb][n_pad]. Rows >= n are zero.
 __global__ void vk_repack_w_b32(int mode, const uint8_t* __restrict__ wq, int n, int n_pad, int nb,
@@ -328,8 +399,8 @@ __device__ __forceinline__ void vk_wait_vm_barrier() {
 template <bool POW2>
 __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
     const uint4* __restrict__ afrag, const float* __restrict__ ascale,
-    const uint4* __restrict__ wfrag, const float* __restrict__ wscale, const float* __restrict__ bias,
-    float* __restrict__ out, int m, int n, int nb, int ldo, int m_pad, int n_pad) {
+    const uint4* __restrict__ wfrag, const float* __restrict__ wscale, const float* __restrict__ bias, VkEpi epi,
+    float* out, int m, int n, int nb, int ldo, int m_pad, int n_pad) {
     using namespace gemm;
     constexpr int WAVES = WM * WN;
     constexpr int APT = MT * FRAG_U4 / THREADS, BPT = NT * FRAG_U4 / THREADS;  // uint4 loads per thread
@@ -452,34 +523,53 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
     float* slot = reinterpret_cast<float*>(&lds_a[0][0]) + wave * 1024;
     const int col0 = (nt0 + wn * 4) * 16;
     const bool vec_ok = (ldo % 4 == 0) && (col0 + 64 <= n) &&
-                        (((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(bias)) & 15) == 0);
+                        (((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(bias) |
+                           reinterpret_cast<uintptr_t>(epi.resid)) & 15) == 0);
+    const int c4 = 4 * (lane & 15);
+    const float4 bv = (bias && vec_ok) ? *reinterpret_cast<const float4*>(bias + col0 + c4)
+                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+        const int row_base = (mt0 + wm * 4 + i) * 16;
+        // residual rows of this strip, loaded before the LDS round trip so the
+        // latency overlaps it (rows past m read row m-1: in bounds, unused)
+        float4 rv[4];
+        if (epi.resid && vec_ok) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int row = min(row_base + 4 * q + (lane >> 4), m - 1);
+                rv[q] = *reinterpret_cast<const float4*>(epi.resid + (size_t)row * ldo + col0 + c4);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) slot[(4 * (lane >> 4) + r) * 64 + 16 * j + (lane & 15)] = acc[i][j][r];
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        const int row_base = (mt0 + wm * 4 + i) * 16;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int rr = 4 * q + (lane >> 4), c4 = 4 * (lane & 15);
+            const int rr = 4 * q + (lane >> 4);
             const int row = row_base + rr;
             float4 v = *reinterpret_cast<const float4*>(slot + rr * 64 + c4);
             if (row >= m) continue;
+            const size_t o = (size_t)row * ldo + col0 + c4;
             if (vec_ok) {
                 if (bias) {
-                    const float4 bv = *reinterpret_cast<const float4*>(bias + col0 + c4);
                     v.x = v.x + bv.x; v.y = v.y + bv.y; v.z = v.z + bv.z; v.w = v.w + bv.w;
                 }
-                __builtin_nontemporal_store((vk_f32x4){v.x, v.y, v.z, v.w},
-                                            reinterpret_cast<vk_f32x4*>(out + (size_t)row * ldo + col0 + c4));
+                if (epi.gelu) {
+                    v.x = vk_gelu_as(v.x); v.y = vk_gelu_as(v.y); v.z = vk_gelu_as(v.z); v.w = vk_gelu_as(v.w);
+                }
+                if (epi.resid) {  // resid + y, as the separate add pass
+                    v.x = rv[q].x + v.x; v.y = rv[q].y + v.y; v.z = rv[q].z + v.z; v.w = rv[q].w + v.w;
+                }
+                __builtin_nontemporal_store((vk_f32x4){v.x, v.y, v.z, v.w}, reinterpret_cast<vk_f32x4*>(out + o));
             } else {
                 const float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int col = col0 + c4 + u;
-                    if (col < n) out[(size_t)row * ldo + col] = bias ? e[u] + bias[col] : e[u];
+                    if (col < n) out[o + u] = vk_epi_apply(bias ? e[u] + bias[col] : e[u], epi, o + u);
                 }
             }
         }
@@ -489,10 +579,11 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
 
 template __global__ void vk_quantize_act_b32<false>(const float*, int, int, int, uint4*, float*, float*);
 template __global__ void vk_quantize_act_b32<true>(const float*, int, int, int, uint4*, float*, float*);
+
 template __global__ void vk_gemm_qblock<false>(const uint4*, const float*, const uint4*, const float*,
-                                               const float*, float*, int, int, int, int, int, int);
+                                               const float*, VkEpi, float*, int, int, int, int, int, int);
 template __global__ void vk_gemm_qblock<true>(const uint4*, const float*, const uint4*, const float*,
-                                              const float*, float*, int, int, int, int, int, int);
+                                              const float*, VkEpi, float*, int, int, int, int, int, int);
 
 }  // namespace vk
 
@@ -554,6 +645,31 @@ hipError_t launch_quantize_act_b32(hipStream_t s, bool pow2, const float* a, int
     return hipGetLastError();
 }
 
+hipError_t launch_ln_quantize_b32(hipStream_t s, bool pow2, const float* a, int m, int m_pad, int k,
+                                  const float* gamma, const float* beta, float eps, uint4* afrag, float* ascale,
+                                  float* asum) {
+    if (m_pad % 16 != 0 || k % 32 != 0 || m > m_pad || k > kLnQuantMaxK) return hipErrorInvalidValue;
+    if (m_pad == 0 || k == 0) return hipSuccess;
+    // one row per workgroup unless there are enough 16-row tiles to fill the
+    // chip with workgroups that stage whole tiles for contiguous stores
+    const bool tile = m_pad / 16 >= 1024;
+    const size_t lds = tile ? (size_t)(k / 32) * 1024 : 0;
+    const dim3 grid(tile ? m_pad / 16 : m_pad), block(256);
+    if (pow2 && tile)
+        hipLaunchKernelGGL((vk_ln_quantize_b32<true, true>), grid, block, lds, s, a, m, m_pad, k, gamma, beta, eps,
+                           afrag, ascale, asum);
+    else if (pow2)
+        hipLaunchKernelGGL((vk_ln_quantize_b32<true, false>), grid, block, lds, s, a, m, m_pad, k, gamma, beta, eps,
+                           afrag, ascale, asum);
+    else if (tile)
+        hipLaunchKernelGGL((vk_ln_quantize_b32<false, true>), grid, block, lds, s, a, m, m_pad, k, gamma, beta, eps,
+                           afrag, ascale, asum);
+    else
+        hipLaunchKernelGGL((vk_ln_quantize_b32<false, false>), grid, block, lds, s, a, m, m_pad, k, gamma, beta, eps,
+                           afrag, ascale, asum);
+    return hipGetLastError();
+}
+
 hipError_t launch_repack_w_b32(hipStream_t s, int mode, const uint8_t* wq, int n, int n_pad, int nb,
                                uint4* wfrag, float* wscale) {
     const size_t threads = (size_t)n_pad * nb * 4;
@@ -568,15 +684,15 @@ static_assert(GEMM_TM % gemm::TM == 0 && GEMM_TN % gemm::TN == 0, "GEMM padding"
 
 hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
                               const uint4* wfrag, const float* wscale, const float* bias, float* out,
-                              int m, int m_pad, int n, int n_pad, int nb) {
+                              int m, int m_pad, int n, int n_pad, int nb, VkEpi epi) {
     if (m_pad % gemm::TM != 0 || n_pad % gemm::TN != 0 || nb < 1) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((n_pad / gemm::TN) * (m_pad / gemm::TM)));
     if (pow2)
         hipLaunchKernelGGL(vk_gemm_qblock<true>, grid, dim3(gemm::THREADS), 0, s, afrag, ascale, wfrag, wscale, bias,
-                           out, m, n, nb, n, m_pad, n_pad);
+                           epi, out, m, n, nb, n, m_pad, n_pad);
     else
         hipLaunchKernelGGL(vk_gemm_qblock<false>, grid, dim3(gemm::THREADS), 0, s, afrag, ascale, wfrag, wscale, bias,
-                           out, m, n, nb, n, m_pad, n_pad);
+                           epi, out, m, n, nb, n, m_pad, n_pad);
     return hipGetLastError();
 }
 

@@ -84,9 +84,10 @@ struct QLin {
         if (has_bias) SS_TRY(bias.upload(c, b, n * sizeof(float)));
         return VOKRA_HIP_OK;
     }
-    int run(vokra_hip_ctx_t* c, const vokra_hip_qact_t* qa, float* d_out) const {
-        return vokra_hip_gemm_qact_dev(c, w, qa, has_bias ? bias.f() : nullptr, d_out);
+    int run(vokra_hip_ctx_t* c, const vokra_hip_qact_t* qa, float* d_out, VkEpi epi = {nullptr, 0}) const {
+        return vk::gemm_qact_epi(c, w, qa, b(), d_out, epi);
     }
+    const float* b() const { return has_bias ? bias.f() : nullptr; }
     void release(vokra_hip_ctx_t* c) {
         vokra_hip_qweight_free(w);
         w = nullptr;
@@ -208,26 +209,27 @@ int enc_forward(vokra_hip_encoder* e, size_t batch, size_t frames, const float* 
     const float scale = powf((float)e->hd, -0.5f);  // (hd as f32).powf(-0.5), nn.rs:267
     SS_HIP(hipMemcpyAsync(e->h.p, d_x, rows * d * sizeof(float), hipMemcpyDeviceToDevice, vk::ctx_stream(c)),
            "encoder: hipMemcpyAsync");
+    // Per block the entry-point sequence is LN -> quantize -> q/k/v -> attention
+    // -> quantize -> out-proj -> + h, LN -> quantize -> fc1 -> GELU -> quantize
+    // -> fc2 -> + h; LN + quantize, out-proj + residual and fc1 + GELU run as
+    // one kernel each (vk::qact_ln_quantize, VkEpi), with the same results.
+    const VkEpi add_h = {e->h.f(), 0}, gelu = {nullptr, 1};
     for (const EncLayer& L : e->layers) {
         // attention block (encoder.rs:180-220)
-        SS_TRY(vokra_hip_layer_norm_f32_dev(c, e->h.f(), e->x.f(), rows, d, L.ln1g.f(), L.ln1b.f(), kLnEps));
-        SS_TRY(vokra_hip_qact_quantize_dev(c, e->qa_d, rows, e->x.f(), act));
-        SS_TRY(L.q.run(c, e->qa_d, e->q.f()));
-        SS_TRY(L.k.run(c, e->qa_d, e->k.f()));
-        SS_TRY(L.v.run(c, e->qa_d, e->v.f()));
+        SS_TRY(vk::qact_ln_quantize(c, e->qa_d, rows, e->h.f(), L.ln1g.f(), L.ln1b.f(), kLnEps, act, e->x.f()));
+        const vokra_hip_qweight_t* qkv[3] = {L.q.w, L.k.w, L.v.w};
+        const float* qkv_b[3] = {L.q.b(), L.k.b(), L.v.b()};
+        float* qkv_o[3] = {e->q.f(), e->k.f(), e->v.f()};
+        SS_TRY(vk::gemm_qact_multi(c, 3, qkv, e->qa_d, qkv_b, qkv_o));
         SS_TRY(vokra_hip_attn_f32_dev(c, batch, frames, frames, e->n_head, e->n_head, e->hd, e->q.f(), e->k.f(),
                                       e->v.f(), scale, 0, 0, e->attn.f()));
         SS_TRY(vokra_hip_qact_quantize_dev(c, e->qa_d, rows, e->attn.f(), act));
-        SS_TRY(L.o.run(c, e->qa_d, e->x.f()));
-        SS_TRY(vokra_hip_add_f32_dev(c, e->h.f(), e->x.f(), e->h.f(), rows * d));
+        SS_TRY(L.o.run(c, e->qa_d, e->h.f(), add_h));
         // MLP block (nn.rs:134-181)
-        SS_TRY(vokra_hip_layer_norm_f32_dev(c, e->h.f(), e->x.f(), rows, d, L.ln2g.f(), L.ln2b.f(), kLnEps));
-        SS_TRY(vokra_hip_qact_quantize_dev(c, e->qa_d, rows, e->x.f(), act));
-        SS_TRY(L.fc1.run(c, e->qa_d, e->f.f()));
-        SS_TRY(vokra_hip_gelu_f32_dev(c, e->f.f(), e->f.f(), rows * e->d_ff));
+        SS_TRY(vk::qact_ln_quantize(c, e->qa_d, rows, e->h.f(), L.ln2g.f(), L.ln2b.f(), kLnEps, act, e->x.f()));
+        SS_TRY(L.fc1.run(c, e->qa_d, e->f.f(), gelu));
         SS_TRY(vokra_hip_qact_quantize_dev(c, e->qa_f, rows, e->f.f(), act));
-        SS_TRY(L.fc2.run(c, e->qa_f, e->x.f()));
-        SS_TRY(vokra_hip_add_f32_dev(c, e->h.f(), e->x.f(), e->h.f(), rows * d));
+        SS_TRY(L.fc2.run(c, e->qa_f, e->h.f(), add_h));
     }
     return vokra_hip_layer_norm_f32_dev(c, e->h.f(), d_out, rows, d, e->lnpg.f(), e->lnpb.f(), kLnEps);
 }
@@ -319,23 +321,24 @@ int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_
     hipLaunchKernelGGL(vk::vk_step_index, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, s, d_streams, d_positions, (int)n,
                        (int)m->n_layer, m->lens.i(), m->kvidx.i());
     SS_HIP(hipGetLastError(), "launch(vk_step_index)");
+    // The same fusions as the encoder (LN + quantize, out-proj + residual,
+    // fc1 + GELU, q/k/v in one launch); results equal the entry-point sequence.
+    const VkEpi add_h = {m->h.f(), 0}, gelu = {nullptr, 1};
     for (size_t l = 0; l < m->n_layer; ++l) {
         const DecLayer& L = m->layers[l];
         // causal self-attention over the paged cache (decoder.rs:462-490)
-        SS_TRY(vokra_hip_layer_norm_f32_dev(c, m->h.f(), m->x.f(), n, d, L.ln1g.f(), L.ln1b.f(), kLnEps));
-        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->x.f(), act));
-        SS_TRY(L.q.run(c, m->qa_d, m->q.f()));
-        SS_TRY(L.k.run(c, m->qa_d, m->k.f()));
-        SS_TRY(L.v.run(c, m->qa_d, m->v.f()));
+        SS_TRY(vk::qact_ln_quantize(c, m->qa_d, n, m->h.f(), L.ln1g.f(), L.ln1b.f(), kLnEps, act, m->x.f()));
+        const vokra_hip_qweight_t* qkv[3] = {L.q.w, L.k.w, L.v.w};
+        const float* qkv_b[3] = {L.q.b(), L.k.b(), L.v.b()};
+        float* qkv_o[3] = {m->q.f(), m->k.f(), m->v.f()};
+        SS_TRY(vk::gemm_qact_multi(c, 3, qkv, m->qa_d, qkv_b, qkv_o));
         SS_TRY(vokra_hip_kv_append_dev(c, m->kv, l, n, d_streams, d_positions, m->k.f(), m->v.f()));
         SS_TRY(vokra_hip_paged_attn_dev(c, m->kv, l, n, d_streams, m->lens.i(), m->n_text, m->n_head, m->q.f(), scale,
                                         m->attn.f()));
         SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->attn.f(), act));
-        SS_TRY(L.o.run(c, m->qa_d, m->x.f()));
-        SS_TRY(vokra_hip_add_f32_dev(c, m->h.f(), m->x.f(), m->h.f(), n * d));
+        SS_TRY(L.o.run(c, m->qa_d, m->h.f(), add_h));
         // cross-attention over the stream's encoder frames (decoder.rs:492-510)
-        SS_TRY(vokra_hip_layer_norm_f32_dev(c, m->h.f(), m->x.f(), n, d, L.ln2g.f(), L.ln2b.f(), kLnEps));
-        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->x.f(), act));
+        SS_TRY(vk::qact_ln_quantize(c, m->qa_d, n, m->h.f(), L.ln2g.f(), L.ln2b.f(), kLnEps, act, m->x.f()));
         SS_TRY(L.cq.run(c, m->qa_d, m->q.f()));
         SS_HIP(vk::launch_split_rows(s, m->q.f(), n * d, scale, m->qh.p, m->ql.p), "launch(vk_split_rows q)");
         SS_HIP(vk::launch_flash_attn(s, (int)m->hd, m->qh.p, m->ql.p, m->ckh.p, m->ckl.p, m->cvh.p, m->cvl.p,
@@ -343,16 +346,12 @@ int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_
                                      (int)m->n_head, 0, 0, m->kvidx.i() + l * n),
                "launch(vk_flash_attn cross)");
         SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->attn.f(), act));
-        SS_TRY(L.co.run(c, m->qa_d, m->x.f()));
-        SS_TRY(vokra_hip_add_f32_dev(c, m->h.f(), m->x.f(), m->h.f(), n * d));
+        SS_TRY(L.co.run(c, m->qa_d, m->h.f(), add_h));
         // MLP (decoder.rs:512-525)
-        SS_TRY(vokra_hip_layer_norm_f32_dev(c, m->h.f(), m->x.f(), n, d, L.ln3g.f(), L.ln3b.f(), kLnEps));
-        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->x.f(), act));
-        SS_TRY(L.fc1.run(c, m->qa_d, m->f.f()));
-        SS_TRY(vokra_hip_gelu_f32_dev(c, m->f.f(), m->f.f(), n * m->d_ff));
+        SS_TRY(vk::qact_ln_quantize(c, m->qa_d, n, m->h.f(), L.ln3g.f(), L.ln3b.f(), kLnEps, act, m->x.f()));
+        SS_TRY(L.fc1.run(c, m->qa_d, m->f.f(), gelu));
         SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_f, n, m->f.f(), act));
-        SS_TRY(L.fc2.run(c, m->qa_f, m->x.f()));
-        SS_TRY(vokra_hip_add_f32_dev(c, m->h.f(), m->x.f(), m->h.f(), n * d));
+        SS_TRY(L.fc2.run(c, m->qa_f, m->h.f(), add_h));
     }
     // ln_post, tied logits (decoder.rs:754-796), greedy argmax
     SS_TRY(vokra_hip_layer_norm_f32_dev(c, m->h.f(), m->x.f(), n, d, m->lnpg.f(), m->lnpb.f(), kLnEps));
