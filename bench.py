@@ -274,6 +274,40 @@ def whisper_layer(rng, wd, d, ff, scale, decoder=False):
     return L
 
 
+def bench_frontend(ctx, hip, batch=16, n_mels=128, d=1280, reps=5):
+    """Config 2's front end: log-mel of `batch` 30 s clips (128 mels) and the
+    conv stem (conv1 128->1280, conv2 1280->1280 stride 2, GELU, + positions)
+    on device-resident arrays. FLOPs: STFT GEMM 2*3000*402*400 and mel GEMM
+    2*3000*128*201 per clip; stem 2*3000*1280*384 + 2*1500*1280*3840."""
+    rng = np.random.default_rng(5)
+    n_samples = 480000
+    d_pcm = hip.DeviceBuffer.from_array(ctx, (0.1 * rng.standard_normal((batch, n_samples))).astype(np.float32))
+    d_mel = hip.DeviceBuffer(ctx, batch * n_mels * 3000 * 4)
+    enc = hip.Encoder(ctx, 8, d, 20, 5120, [], np.ones(d, np.float32), np.zeros(d, np.float32), batch * 1500)
+    enc.set_stem(n_mels, 3000, (0.02 * rng.standard_normal((d, n_mels, 3))).astype(np.float32),
+                 np.zeros(d, np.float32), (0.02 * rng.standard_normal((d, d, 3))).astype(np.float32),
+                 np.zeros(d, np.float32), (0.02 * rng.standard_normal((1500, d))).astype(np.float32))
+    d_out = hip.DeviceBuffer(ctx, batch * 1500 * d * 4)
+    ctx.log_mel_dev(d_pcm, batch, n_samples, n_mels, d_mel)
+    enc.encode_dev(batch, d_mel, d_out)
+    ctx.synchronize()
+    e0, e1, e2 = hip.Event(ctx), hip.Event(ctx), hip.Event(ctx)
+    e0.record()
+    for _ in range(reps):
+        ctx.log_mel_dev(d_pcm, batch, n_samples, n_mels, d_mel)
+    e1.record()
+    for _ in range(reps):
+        enc.encode_dev(batch, d_mel, d_out)  # no blocks: stem + ln_post
+    e2.record()
+    mel_ms, stem_ms = e0.elapsed_ms(e1) / reps, e1.elapsed_ms(e2) / reps
+    mel_flop = batch * (2 * 3000 * 402 * 400 + 2 * 3000 * n_mels * 201)
+    stem_flop = batch * (2 * 3000 * d * n_mels * 3 + 2 * 1500 * d * d * 3)
+    return {"batch": batch, "n_mels": n_mels, "log_mel_ms": round(mel_ms, 3),
+            "log_mel_clips_per_s": round(batch / (mel_ms * 1e-3), 1),
+            "log_mel_tflops": round(mel_flop / (mel_ms * 1e-3) / 1e12, 2),
+            "stem_ms": round(stem_ms, 3), "stem_tflops": round(stem_flop / (stem_ms * 1e-3) / 1e12, 2)}
+
+
 def bench_encoder(ctx, hip, batch, n_layer=32, d=1280, H=20, ff=5120, T=1500, reps=3):
     """Config 2: Whisper-large-v3-shaped encoder blocks (32 x d=1280, 20 heads,
     FFN 5120, Q8_0 random-init weights) over 1500 frames, batch 1 or 16: one
@@ -405,7 +439,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default=None,
                     help="comma list of single legs to run, one JSON line each (for profiling): "
-                         "gemm, gemm_pow2, copy, gemv, q4k, sdpa, paged, encoder, decoder")
+                         "gemm, gemm_pow2, copy, gemv, q4k, sdpa, paged, encoder, decoder, frontend")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -427,6 +461,7 @@ def main():
                               bench_paged_attn(ctx, hip, 32, 2, 128, 16, 512, 4096, 4096)],
             "encoder": lambda: [bench_encoder(ctx, hip, 1), bench_encoder(ctx, hip, 16)],
             "decoder": lambda: bench_decoder(ctx, hip),
+            "frontend": lambda: bench_frontend(ctx, hip),
         }
         for name in args.only.split(","):
             res = legs[name]()
@@ -444,6 +479,7 @@ def main():
     paged_runs = [bench_paged_attn(ctx, hip, 64, 20, 64, 20, 1, 448, 448),
                   bench_paged_attn(ctx, hip, 32, 2, 128, 16, 512, 4096, 4096)]
     encoder_runs = [bench_encoder(ctx, hip, 1), bench_encoder(ctx, hip, 16)]
+    frontend_run = bench_frontend(ctx, hip)
     decoder_run = bench_decoder(ctx, hip)
 
     M, N, K = main_run["M"], main_run["N"], main_run["K"]
@@ -478,6 +514,7 @@ def main():
             "sdpa_config1": sdpa_run,
             "paged_attn_config3_config4": paged_runs,
             "encoder_config2": encoder_runs,
+            "frontend_config2_batch16": frontend_run,
             "decoder_step_config3": decoder_run,
             "gemm_kernel_ms": round(main_run["gemm_ms"], 4),
             "eager_step_ms": round(main_run["eager_ms"], 4),

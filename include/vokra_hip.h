@@ -334,6 +334,31 @@ int vokra_hip_paged_attn_dev(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t la
  * model code, crates/vokra-models/src/whisper/nn.rs). */
 int vokra_hip_add_f32_dev(vokra_hip_ctx_t *ctx, const float *d_a, const float *d_b, float *d_out, size_t n);
 
+/* ---- Whisper front end ---------------------------------------------------- */
+
+/* whisper::mel::log_mel (crates/vokra-models/src/whisper/mel.rs:123-183; fused
+ * form crates/vokra-ops/src/fused_logmel.rs:80-175) for `batch` clips of
+ * n_samples 16 kHz samples each, pcm [batch][n_samples]: each clip zero-padded
+ * or trimmed to 30 s, STFT (n_fft 400, hop 160, periodic Hann, reflect
+ * centre padding, trailing frame dropped), Slaney mel bands, log10 with the
+ * 1e-10 floor, per-clip (max(v, gmax - 8) + 4) / 4. out [batch][n_mels][3000]. */
+int vokra_hip_log_mel(vokra_hip_ctx_t *ctx, const float *pcm, size_t batch, size_t n_samples, size_t n_mels,
+                      float *out, size_t out_len);
+int vokra_hip_log_mel_dev(vokra_hip_ctx_t *ctx, const float *d_pcm, size_t batch, size_t n_samples, size_t n_mels,
+                          float *d_out);
+/* kernels::conv1d_f32 (crates/vokra-backend-cpu/src/kernels/mod.rs:583-822;
+ * Compute::conv1d_f32): input [in_ch, in_len], weight [out_ch, in_ch, kernel],
+ * optional bias [out_ch], out [out_ch, out_len] with
+ * out_len = (in_len + 2 padding - kernel) / stride + 1; the same rejections
+ * (zero stride or kernel, padded length shorter than the kernel, length
+ * mismatches). */
+int vokra_hip_conv1d_f32(vokra_hip_ctx_t *ctx, const float *input, size_t input_len, size_t in_ch, size_t in_len,
+                         const float *weight, size_t weight_len, size_t out_ch, size_t kernel, const float *bias,
+                         size_t stride, size_t padding, float *out, size_t out_len);
+int vokra_hip_conv1d_f32_dev(vokra_hip_ctx_t *ctx, const float *d_input, size_t in_ch, size_t in_len,
+                             const float *d_weight, size_t out_ch, size_t kernel, const float *d_bias, size_t stride,
+                             size_t padding, float *d_out);
+
 /* ---- pre-norm encoder session ------------------------------------------- */
 
 /* One pre-norm block with quantized linears: wire-format weights [out, in]
@@ -367,6 +392,20 @@ int vokra_hip_encoder_forward_dev(vokra_hip_ctx_t *ctx, vokra_hip_encoder_t *enc
 /* Host arrays, synchronous. */
 int vokra_hip_encoder_forward(vokra_hip_ctx_t *ctx, vokra_hip_encoder_t *enc, size_t batch, size_t frames,
                               const float *x, float *out);
+/* The conv stem in front of the blocks (crates/vokra-models/src/whisper/
+ * encoder.rs:58-104): conv1 [d, n_mels, 3] (stride 1, pad 1) + GELU, conv2
+ * [d, d, 3] (stride 2, pad 1) + GELU, transposed to [frames / 2, d] plus the
+ * positional embedding pos_emb [n_frames / 2, d]. Host arrays, copied. */
+int vokra_hip_encoder_set_stem(vokra_hip_ctx_t *ctx, vokra_hip_encoder_t *enc, size_t n_mels, size_t n_frames,
+                               const float *conv1_w, const float *conv1_b, const float *conv2_w,
+                               const float *conv2_b, const float *pos_emb);
+/* WhisperEncoder::encode (encoder.rs:41-178): log-mel [batch][n_mels][n_frames]
+ * -> stem -> blocks -> ln_post, out [batch][n_frames / 2][d]. Device pointers,
+ * asynchronous; needs vokra_hip_encoder_set_stem first. */
+int vokra_hip_encoder_encode_dev(vokra_hip_ctx_t *ctx, vokra_hip_encoder_t *enc, size_t batch,
+                                 const float *d_log_mel, float *d_out);
+int vokra_hip_encoder_encode(vokra_hip_ctx_t *ctx, vokra_hip_encoder_t *enc, size_t batch, const float *log_mel,
+                             float *out);
 
 /* ---- batched decoder-step session --------------------------------------- */
 

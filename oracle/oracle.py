@@ -122,6 +122,10 @@ def _declare(L):
     L.vo_argmax.argtypes = [_f32p, _sz]
     L.vo_xorshift_rand_vec.argtypes = [C.c_uint64, _sz, _f32p]
     L.vo_splitmix_gaussian.argtypes = [C.c_uint64, _sz, _f32p]
+    L.vo_hann_periodic.argtypes = [_sz, _f32p]
+    L.vo_mel_filterbank.argtypes = [_sz, _sz, _sz, C.c_double, C.c_double, _f32p]
+    L.vo_log_mel.argtypes = [_f32p, _sz, _sz, _f32p]
+    L.vo_conv1d_f32.argtypes = [_f32p, _sz, _sz, _f32p, _sz, _sz, _f32p, _sz, _sz, _f32p]
 
 
 def _p(a, t):
@@ -442,3 +446,45 @@ def splitmix_gaussian(seed, n):
     out = np.zeros(max(n, 1), np.float32)
     lib().vo_splitmix_gaussian(seed & 0xFFFFFFFFFFFFFFFF, n, _p(out, _f32p))
     return out[:n]
+
+
+# ---- Whisper log-mel front end and conv1d ----------------------------------
+N_SAMPLES, N_FFT, HOP, N_FRAMES = 480000, 400, 160, 3000
+
+
+def hann_periodic(n):
+    """vo_hann_periodic: window.rs cosine_sum([0.5, 0.5]), periodic."""
+    out = np.zeros(n, np.float32)
+    lib().vo_hann_periodic(n, _p(out, _f32p))
+    return out
+
+
+def mel_filterbank(n_mels, sr=16000, n_fft=N_FFT, fmin=0.0, fmax=8000.0):
+    """vo_mel_filterbank: [n_mels, n_fft/2 + 1], Slaney scale and norm."""
+    out = np.zeros(n_mels * (n_fft // 2 + 1), np.float32)
+    lib().vo_mel_filterbank(sr, n_fft, n_mels, fmin, fmax, _p(out, _f32p))
+    return out.reshape(n_mels, n_fft // 2 + 1)
+
+
+def log_mel(pcm, n_mels):
+    """vo_log_mel: whisper::mel::log_mel -> [n_mels, 3000]."""
+    x = _f32(pcm).reshape(-1)
+    out = np.zeros(n_mels * N_FRAMES, np.float32)
+    _check(lib().vo_log_mel(_p(x, _f32p) if x.size else None, x.size, n_mels, _p(out, _f32p)), "log_mel")
+    return out.reshape(n_mels, N_FRAMES)
+
+
+def conv1d_out_len(in_len, kernel, stride, padding):
+    return (in_len + 2 * padding - kernel) // stride + 1
+
+
+def conv1d_f32(x, in_ch, in_len, w, out_ch, kernel, bias=None, stride=1, padding=0):
+    """vo_conv1d_f32: kernels::conv1d_f32 -> [out_ch, out_len]."""
+    xv, wv = _f32(x), _f32(w)
+    bv = None if bias is None else _f32(bias)
+    out_len = conv1d_out_len(in_len, kernel, stride, padding) if stride and kernel else 0
+    out = np.zeros(max(out_ch * max(out_len, 0), 1), np.float32)
+    _check(lib().vo_conv1d_f32(_p(xv, _f32p), in_ch, in_len, _p(wv, _f32p), out_ch, kernel, _p(bv, _f32p),
+                               stride, padding, _p(out, _f32p)), "conv1d_f32")
+    return out[:out_ch * out_len].reshape(out_ch, out_len)
+

@@ -1121,3 +1121,149 @@ void vo_splitmix_gaussian(uint64_t seed, size_t n, float *out) {
         out[i] = r * cosf(theta);
     }
 }
+
+/* ---- Whisper log-mel front end and conv1d ---------------------------------- */
+
+/* Periodic Hann window (crates/vokra-ops/src/window.rs:31 Hann = cosine_sum
+ * [0.5, 0.5], :42-55 w[n] = sum_i (-1)^i a_i cos(i 2 pi n / denom) in f64, cast
+ * to f32; periodic: denom = length). */
+void vo_hann_periodic(size_t len, float *w) {
+    for (size_t n = 0; n < len; ++n) {
+        const double x = 2.0 * 3.14159265358979323846 * (double)n / (double)len;
+        double acc = 0.0, sign = 1.0;
+        const double a[2] = {0.5, 0.5};
+        for (int i = 0; i < 2; ++i) {
+            acc += sign * a[i] * cos((double)i * x);
+            sign = -sign;
+        }
+        w[n] = (float)acc;
+    }
+}
+
+/* Slaney mel scale (crates/vokra-ops/src/mel.rs hz_to_mel / mel_to_hz). */
+static double vo_hz_to_mel_slaney(double f) {
+    const double f_sp = 200.0 / 3.0, min_log_hz = 1000.0, min_log_mel = min_log_hz / f_sp;
+    const double logstep = log(6.4) / 27.0;
+    return f >= min_log_hz ? min_log_mel + log(f / min_log_hz) / logstep : f / f_sp;
+}
+static double vo_mel_to_hz_slaney(double mel) {
+    const double f_sp = 200.0 / 3.0, min_log_hz = 1000.0, min_log_mel = min_log_hz / f_sp;
+    const double logstep = log(6.4) / 27.0;
+    return mel >= min_log_mel ? min_log_hz * exp(logstep * (mel - min_log_mel)) : f_sp * mel;
+}
+
+/* MelFilterbank::new (crates/vokra-ops/src/mel.rs:29-130) for the Whisper
+ * front end (frontend.rs:62-80): Slaney scale, triangles linear in Hz, Slaney
+ * norm. w is [n_mels][n_fft/2 + 1]. */
+void vo_mel_filterbank(size_t sr, size_t n_fft, size_t n_mels, double fmin, double fmax, float *w) {
+    const size_t nf = n_fft / 2 + 1;
+    const double min_mel = vo_hz_to_mel_slaney(fmin), max_mel = vo_hz_to_mel_slaney(fmax);
+    double *band_hz = (double *)malloc((n_mels + 2) * sizeof(double));
+    for (size_t i = 0; i < n_mels + 2; ++i)
+        band_hz[i] = vo_mel_to_hz_slaney(min_mel + (max_mel - min_mel) * (double)i / (double)(n_mels + 1));
+    for (size_t m = 0; m < n_mels; ++m) {
+        const double left = band_hz[m], center = band_hz[m + 1], right = band_hz[m + 2];
+        const double fdl = center - left, fdh = right - center;
+        for (size_t k = 0; k < nf; ++k) {
+            const double f = (double)k * (double)sr / (double)n_fft;
+            const double lower = fdl > 0.0 ? (f - left) / fdl : 0.0;
+            const double upper = fdh > 0.0 ? (right - f) / fdh : 0.0;
+            double v = lower < upper ? lower : upper;
+            if (v < 0.0) v = 0.0;
+            w[m * nf + k] = (float)v;
+        }
+        const double enorm = 2.0 / (band_hz[m + 2] - band_hz[m]);
+        for (size_t k = 0; k < nf; ++k) w[m * nf + k] = (float)((double)w[m * nf + k] * enorm);
+    }
+    free(band_hz);
+}
+
+/* numpy mode="reflect" index (crates/vokra-ops/src/stft.rs:269-285). */
+static size_t vo_reflect(long i, size_t n) {
+    if (n == 1) return 0;
+    const long period = 2 * (long)(n - 1);
+    long r = i % period;
+    if (r < 0) r += period;
+    return (size_t)(r < (long)n ? r : period - r);
+}
+
+/* whisper::mel::log_mel (crates/vokra-models/src/whisper/mel.rs:123-183) over
+ * the fused single pass (crates/vokra-ops/src/fused_logmel.rs:80-175): PCM
+ * zero-padded / trimmed to 480000 samples, reflect-padded by n_fft/2, frames of
+ * 400 every 160 samples windowed in f32 (periodic Hann), |X_k|^2 of the
+ * unnormalised DFT (k = 0..200), the trailing frame dropped (3000 kept), mel
+ * energy acc += w * p in f32 bin order, log10(max(acc, 1e-10)) into
+ * out[m * 3000 + t], then (max(v, gmax - 8) + 4) / 4. The reference's FFT is
+ * pocketfft in f32; here the DFT is summed in f64 (the reference holds its own
+ * fused and unfused front ends to each other within atol 0.01). */
+int vo_log_mel(const float *pcm, size_t n_pcm, size_t n_mels, float *out) {
+    const size_t NS = 480000, NFFT = 400, HOP = 160, NFR = 3000, NB = 201, PAD = 200;
+    float *buf = (float *)calloc(NS, sizeof(float));
+    float *win = (float *)malloc(NFFT * sizeof(float));
+    float *fb = (float *)malloc(n_mels * NB * sizeof(float));
+    double *cs = (double *)malloc(NB * NFFT * sizeof(double));
+    double *sn = (double *)malloc(NB * NFFT * sizeof(double));
+    float *frame = (float *)malloc(NFFT * sizeof(float));
+    float *pw = (float *)malloc(NB * sizeof(float));
+    if (!buf || !win || !fb || !cs || !sn || !frame || !pw) return VO_BACKEND_UNAVAILABLE;
+    memcpy(buf, pcm, (n_pcm < NS ? n_pcm : NS) * sizeof(float));
+    vo_hann_periodic(NFFT, win);
+    vo_mel_filterbank(16000, NFFT, n_mels, 0.0, 8000.0, fb);
+    for (size_t k = 0; k < NB; ++k)
+        for (size_t n = 0; n < NFFT; ++n) {
+            const double th = 2.0 * 3.14159265358979323846 * (double)((k * n) % NFFT) / (double)NFFT;
+            cs[k * NFFT + n] = cos(th);
+            sn[k * NFFT + n] = sin(th);
+        }
+    float gmax = -INFINITY;
+    for (size_t t = 0; t < NFR; ++t) {
+        for (size_t i = 0; i < NFFT; ++i)
+            frame[i] = buf[vo_reflect((long)(t * HOP + i) - (long)PAD, NS)] * win[i];
+        for (size_t k = 0; k < NB; ++k) {
+            double re = 0.0, im = 0.0;
+            for (size_t n = 0; n < NFFT; ++n) {
+                re += (double)frame[n] * cs[k * NFFT + n];
+                im -= (double)frame[n] * sn[k * NFFT + n];
+            }
+            pw[k] = (float)(re * re + im * im);
+        }
+        for (size_t m = 0; m < n_mels; ++m) {
+            float acc = 0.0f;
+            for (size_t k = 0; k < NB; ++k) acc += fb[m * NB + k] * pw[k];
+            const float l = log10f(acc > 1e-10f ? acc : 1e-10f);
+            out[m * NFR + t] = l;
+            if (l > gmax) gmax = l;
+        }
+    }
+    const float floor_v = gmax - 8.0f;
+    for (size_t i = 0; i < n_mels * NFR; ++i) out[i] = ((out[i] > floor_v ? out[i] : floor_v) + 4.0f) / 4.0f;
+    free(buf); free(win); free(fb); free(cs); free(sn); free(frame); free(pw);
+    return VO_OK;
+}
+
+/* kernels::conv1d_f32 (crates/vokra-backend-cpu/src/kernels/mod.rs:583-822):
+ * im2col col[c*kernel + kk][t] = in[c][t*stride + kk - padding] (zero outside),
+ * out = weight [out_ch, in_ch*kernel] x col by the scalar gemm (accumulating
+ * from 0), then + bias[oc]. Returns INVALID_ARGUMENT for the reference's
+ * rejections (zero stride / kernel, padded length shorter than the kernel). */
+int vo_conv1d_f32(const float *input, size_t in_ch, size_t in_len, const float *weight, size_t out_ch,
+                  size_t kernel, const float *bias, size_t stride, size_t padding, float *out) {
+    if (stride == 0 || kernel == 0) return VO_INVALID_ARGUMENT;
+    const size_t padded = in_len + 2 * padding;
+    if (padded < kernel) return VO_INVALID_ARGUMENT;
+    const size_t out_len = (padded - kernel) / stride + 1, k = in_ch * kernel;
+    float *col = (float *)calloc((k * out_len) > 0 ? k * out_len : 1, sizeof(float));
+    if (!col) return VO_BACKEND_UNAVAILABLE;
+    for (size_t c = 0; c < in_ch; ++c)
+        for (size_t kk = 0; kk < kernel; ++kk)
+            for (size_t t = 0; t < out_len; ++t) {
+                const size_t pos = t * stride + kk;
+                if (pos >= padding && pos < padding + in_len) col[(c * kernel + kk) * out_len + t] = input[c * in_len + (pos - padding)];
+            }
+    vo_gemm_f32(out_ch, out_len, k, weight, col, NULL, out);
+    if (bias)
+        for (size_t oc = 0; oc < out_ch; ++oc)
+            for (size_t t = 0; t < out_len; ++t) out[oc * out_len + t] += bias[oc];
+    free(col);
+    return VO_OK;
+}

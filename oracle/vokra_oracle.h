@@ -126,6 +126,13 @@ uint32_t vo_argmax(const float *logits, size_t n);
 void vo_xorshift_rand_vec(uint64_t seed, size_t n, float *out);
 void vo_splitmix_gaussian(uint64_t seed, size_t n, float *out);
 
+/* Whisper log-mel front end and conv1d */
+void vo_hann_periodic(size_t len, float *w);
+void vo_mel_filterbank(size_t sr, size_t n_fft, size_t n_mels, double fmin, double fmax, float *w);
+int vo_log_mel(const float *pcm, size_t n_pcm, size_t n_mels, float *out);
+int vo_conv1d_f32(const float *input, size_t in_ch, size_t in_len, const float *weight, size_t out_ch,
+                  size_t kernel, const float *bias, size_t stride, size_t padding, float *out);
+
 #ifdef __cplusplus
 }
 #endif

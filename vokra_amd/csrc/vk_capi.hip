@@ -113,6 +113,10 @@ struct vokra_hip_ctx {
     vokra_hip_qact act;
     // attention workspace: fp16 hi / lo splits of q, k and transposed v
     DevBuf at_qh, at_ql, at_kh, at_kl, at_vh, at_vl;
+    // front end: window, DFT basis, filter bank (for fe_mels bands), frames,
+    // spectrum, power, mel energies, per-block maxima; im2col columns
+    DevBuf fe_win, fe_basis, fe_fb, fe_frames, fe_spec, fe_pow, fe_mel, fe_part, cv_col;
+    int fe_mels = 0;
 };
 
 struct vokra_hip_qweight {
@@ -801,6 +805,75 @@ int stage_out(vokra_hip_ctx* c, float* h, const void* d, size_t n) {
     VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     return VOKRA_HIP_OK;
 }
+
+int upload_table(vokra_hip_ctx* c, DevBuf& b, const std::vector<float>& h) {
+    VK_TRY(b.ensure(h.size() * sizeof(float)), "hipMalloc(front-end table)");
+    VK_TRY(hipMemcpyAsync(b.p, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice, c->stream),
+           "hipMemcpyAsync(front-end table)");
+    // the host vector goes out of scope when this returns
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return VOKRA_HIP_OK;
+}
+
+// log_mel of `batch` clips of n_samples each (device), out [batch][n_mels][3000].
+int run_log_mel(vokra_hip_ctx* c, const float* d_pcm, size_t batch, size_t n_samples, size_t n_mels, float* d_out) {
+    const int NFR = vk::fe_n_frames(), NB = vk::fe_n_bins(), NFFT = vk::fe_n_fft();
+    if (!c->fe_win.p) {
+        std::vector<float> w, b;
+        vk::fe_hann_periodic(w);
+        vk::fe_dft_basis(b);
+        int st = upload_table(c, c->fe_win, w);
+        if (!st) st = upload_table(c, c->fe_basis, b);
+        if (st) return st;
+    }
+    if (c->fe_mels != (int)n_mels) {
+        std::vector<float> fb;
+        vk::fe_mel_filterbank((int)n_mels, fb);
+        int st = upload_table(c, c->fe_fb, fb);
+        if (st) return st;
+        c->fe_mels = (int)n_mels;
+    }
+    const size_t rows = batch * (size_t)NFR;
+    VK_TRY(c->fe_frames.ensure(rows * NFFT * sizeof(float)), "hipMalloc(frames)");
+    VK_TRY(c->fe_spec.ensure(rows * 2 * NB * sizeof(float)), "hipMalloc(spectrum)");
+    VK_TRY(c->fe_pow.ensure(rows * NB * sizeof(float)), "hipMalloc(power)");
+    VK_TRY(c->fe_mel.ensure(rows * n_mels * sizeof(float)), "hipMalloc(mel)");
+    VK_TRY(c->fe_part.ensure(batch * vk::logmel_n_partial() * sizeof(float)), "hipMalloc(partials)");
+    float* frames = (float*)c->fe_frames.p;
+    VK_TRY(vk::launch_stft_frames(c->stream, d_pcm, (int)batch, (int)n_samples, (const float*)c->fe_win.p, frames),
+           "launch(vk_stft_frames)");
+    VK_TRY(vk::launch_gemm_f32(c->stream, true, frames, (const float*)c->fe_basis.p, nullptr, (float*)c->fe_spec.p,
+                               (int)rows, 2 * NB, NFFT),
+           "launch(vk_gemm_f32 stft)");
+    VK_TRY(vk::launch_power_spec(c->stream, (const float*)c->fe_spec.p, (float*)c->fe_pow.p, rows),
+           "launch(vk_power_spec)");
+    VK_TRY(vk::launch_gemm_f32(c->stream, true, (const float*)c->fe_pow.p, (const float*)c->fe_fb.p, nullptr,
+                               (float*)c->fe_mel.p, (int)rows, (int)n_mels, NB),
+           "launch(vk_gemm_f32 mel)");
+    VK_TRY(vk::launch_logmel_finish(c->stream, (const float*)c->fe_mel.p, (int)batch, (int)n_mels, d_out,
+                                    (float*)c->fe_part.p),
+           "launch(vk_logmel)");
+    return VOKRA_HIP_OK;
+}
+
+int check_log_mel(size_t batch, size_t n_samples, size_t n_mels) {
+    if (n_mels == 0 || n_mels > 1024) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "log_mel: n_mels must be 1..1024");
+    if (batch == 0 || batch > 4096) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "log_mel: batch must be 1..4096");
+    if (n_samples > (size_t)INT32_MAX / 2) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "log_mel: clip too long");
+    return VOKRA_HIP_OK;
+}
+
+// conv1d shape rules of kernels::conv1d_f32 (mod.rs:754-790).
+int conv1d_out(size_t in_len, size_t kernel, size_t stride, size_t padding, size_t* out_len) {
+    if (stride == 0) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "conv1d stride must be >= 1");
+    if (kernel == 0) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "conv1d kernel must be >= 1");
+    const size_t padded = in_len + 2 * padding;
+    if (padded < kernel)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "conv1d padded length %zu is smaller than kernel %zu", padded,
+                    kernel);
+    *out_len = (padded - kernel) / stride + 1;
+    return VOKRA_HIP_OK;
+}
 }  // namespace
 
 int vokra_hip_gemm_f32_dev(vokra_hip_ctx_t* c, size_t m, size_t n, size_t k, const float* d_a, const float* d_b,
@@ -1069,7 +1142,8 @@ void vokra_hip_destroy(vokra_hip_ctx_t* c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     for (DevBuf* b : {&c->in0, &c->in1, &c->in2, &c->out0, &c->act.frag, &c->act.scale, &c->act.gsum, &c->at_qh,
-                      &c->at_ql, &c->at_kh, &c->at_kl, &c->at_vh, &c->at_vl})
+                      &c->at_ql, &c->at_kh, &c->at_kl, &c->at_vh, &c->at_vl, &c->fe_win, &c->fe_basis, &c->fe_fb,
+                      &c->fe_frames, &c->fe_spec, &c->fe_pow, &c->fe_mel, &c->fe_part, &c->cv_col})
         b->release();
     (void)hipStreamDestroy(c->stream);
     delete c;
@@ -1488,4 +1562,82 @@ int vokra_hip_gemm_qact_dev(vokra_hip_ctx_t* c, const vokra_hip_qweight_t* w, co
     return vk::gemm_qact_epi(c, w, qa, d_bias, d_out, VkEpi{nullptr, 0});
 }
 
+// ---- Whisper front end ------------------------------------------------------
+
+int vokra_hip_log_mel_dev(vokra_hip_ctx_t* c, const float* d_pcm, size_t batch, size_t n_samples, size_t n_mels,
+                          float* d_out) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "log_mel: ctx is NULL");
+    int st = check_log_mel(batch, n_samples, n_mels);
+    if (st) return st;
+    if (!d_out || (n_samples && !d_pcm)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "log_mel: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    return run_log_mel(c, d_pcm, batch, n_samples, n_mels, d_out);
+}
+
+int vokra_hip_log_mel(vokra_hip_ctx_t* c, const float* pcm, size_t batch, size_t n_samples, size_t n_mels, float* out,
+                      size_t out_len) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "log_mel: ctx is NULL");
+    int st = check_log_mel(batch, n_samples, n_mels);
+    if (st) return st;
+    const size_t want = batch * n_mels * (size_t)vk::fe_n_frames();
+    if ((st = expect_len("log_mel out", out_len, want))) return st;
+    if (!out || (n_samples && !pcm)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "log_mel: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    if ((st = stage_in(c, c->in0, pcm, batch * n_samples))) return st;
+    VK_TRY(c->out0.ensure(want * sizeof(float)), "hipMalloc");
+    if ((st = run_log_mel(c, (const float*)c->in0.p, batch, n_samples, n_mels, (float*)c->out0.p))) return st;
+    return stage_out(c, out, c->out0.p, want);
+}
+
+int vokra_hip_conv1d_f32_dev(vokra_hip_ctx_t* c, const float* d_in, size_t in_ch, size_t in_len, const float* d_w,
+                             size_t out_ch, size_t kernel, const float* d_bias, size_t stride, size_t padding,
+                             float* d_out) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "conv1d: ctx is NULL");
+    size_t out_len = 0, kk = 0, col_n = 0;
+    int st = conv1d_out(in_len, kernel, stride, padding, &out_len);
+    if (st) return st;
+    if (!mul_ok(in_ch, kernel, &kk) || !mul_ok(kk, out_len, &col_n) || !fits_int(kk) || !fits_int(out_len) ||
+        !fits_int(out_ch) || !fits_int(in_len) || !fits_int(stride) || !fits_int(padding))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "conv1d: extent exceeds int32");
+    if (out_ch == 0 || out_len == 0) return VOKRA_HIP_OK;
+    if (!d_out || !d_w || (in_ch && !d_in)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "conv1d: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(c->cv_col.ensure(col_n * sizeof(float) + 16), "hipMalloc(im2col)");
+    VK_TRY(vk::launch_im2col(c->stream, false, d_in, 0, in_len, 1, 1, (int)in_ch, (int)in_len, (int)kernel, (int)stride,
+                             (int)padding, (int)out_len, (float*)c->cv_col.p),
+           "launch(vk_im2col)");
+    VK_TRY(vk::launch_gemm_f32(c->stream, false, d_w, (const float*)c->cv_col.p, nullptr, d_out, (int)out_ch,
+                               (int)out_len, (int)kk),
+           "launch(vk_gemm_f32 conv)");
+    if (d_bias)
+        VK_TRY(vk::launch_add_row_bias(c->stream, d_out, d_bias, (int)out_ch, (int)out_len), "launch(vk_add_row_bias)");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_conv1d_f32(vokra_hip_ctx_t* c, const float* input, size_t in_len_total, size_t in_ch, size_t in_len,
+                         const float* weight, size_t w_len, size_t out_ch, size_t kernel, const float* bias,
+                         size_t stride, size_t padding, float* out, size_t out_len_total) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "conv1d: ctx is NULL");
+    size_t out_len = 0, n_in = 0, n_w = 0, n_out = 0, kk = 0;
+    int st = conv1d_out(in_len, kernel, stride, padding, &out_len);
+    if (st) return st;
+    if (!mul_ok(in_ch, in_len, &n_in) || !mul_ok(in_ch, kernel, &kk) || !mul_ok(out_ch, kk, &n_w) ||
+        !mul_ok(out_ch, out_len, &n_out))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "conv1d: extent overflows");
+    if ((st = expect_len("conv1d input", in_len_total, n_in)) || (st = expect_len("conv1d weight", w_len, n_w)) ||
+        (st = expect_len("conv1d out", out_len_total, n_out)))
+        return st;
+    if (n_out == 0) return VOKRA_HIP_OK;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    if ((st = stage_in(c, c->in0, input, n_in)) || (st = stage_in(c, c->in1, weight, n_w)) ||
+        (st = stage_in(c, c->in2, bias, bias ? out_ch : 0)))
+        return st;
+    VK_TRY(c->out0.ensure(n_out * sizeof(float)), "hipMalloc");
+    st = vokra_hip_conv1d_f32_dev(c, (const float*)c->in0.p, in_ch, in_len, (const float*)c->in1.p, out_ch, kernel,
+                                  bias ? (const float*)c->in2.p : nullptr, stride, padding, (float*)c->out0.p);
+    if (st) return st;
+    return stage_out(c, out, c->out0.p, n_out);
+}
+
 }  // extern "C"
+

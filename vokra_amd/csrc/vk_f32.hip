@@ -24,7 +24,7 @@ constexpr int T = 64, KC = 16, PAD = 4;
 
 template <bool BT>
 __global__ __launch_bounds__(256) void vk_gemm_f32(const float* __restrict__ a, const float* __restrict__ b,
-                                                   const float* __restrict__ bias, float* __restrict__ out, int m,
+                                                   const float* __restrict__ bias, VkEpi epi, float* out, int m,
                                                    int n, int k) {
     using namespace g32;
     __shared__ float as[KC][T + PAD];
@@ -89,7 +89,10 @@ __global__ __launch_bounds__(256) void vk_gemm_f32(const float* __restrict__ a, 
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int gm = m0 + wr + 16 * i + 4 * (lane >> 4) + r, gn = n0 + wc + 16 * j + (lane & 15);
-                if (gm < m && gn < n) out[(size_t)gm * n + gn] = bias ? bias[gn] + acc[i][j][r] : acc[i][j][r];
+                if (gm < m && gn < n) {
+                    const size_t o = (size_t)gm * n + gn;
+                    out[o] = vk_epi_apply(bias ? bias[gn] + acc[i][j][r] : acc[i][j][r], epi, o);
+                }
             }
 }
 
@@ -258,13 +261,13 @@ __global__ __launch_bounds__(256) void vk_argmax_f32(const float* __restrict__ l
 namespace vk {
 
 hipError_t launch_gemm_f32(hipStream_t s, bool b_trans, const float* a, const float* b, const float* bias,
-                           float* out, int m, int n, int k) {
+                           float* out, int m, int n, int k, VkEpi epi) {
     if (m == 0 || n == 0) return hipSuccess;
     const dim3 grid((n + g32::T - 1) / g32::T, (m + g32::T - 1) / g32::T);
     if (b_trans)
-        hipLaunchKernelGGL(vk_gemm_f32<true>, grid, dim3(256), 0, s, a, b, bias, out, m, n, k);
+        hipLaunchKernelGGL(vk_gemm_f32<true>, grid, dim3(256), 0, s, a, b, bias, epi, out, m, n, k);
     else
-        hipLaunchKernelGGL(vk_gemm_f32<false>, grid, dim3(256), 0, s, a, b, bias, out, m, n, k);
+        hipLaunchKernelGGL(vk_gemm_f32<false>, grid, dim3(256), 0, s, a, b, bias, epi, out, m, n, k);
     return hipGetLastError();
 }
 

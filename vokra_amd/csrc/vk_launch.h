@@ -94,7 +94,8 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
 
 namespace vk {
 hipError_t launch_gemm_f32(hipStream_t s, bool b_trans, const float* a, const float* b, const float* bias,
-                           float* out, int m, int n, int k);
+                           float* out, int m, int n, int k,
+                           VkEpi epi = {nullptr, 0});
 hipError_t launch_gemv_f32(hipStream_t s, const float* a, const float* x, const float* bias, float* out, int m,
                            int k);
 hipError_t launch_softmax_f32(hipStream_t s, const float* in, float* out, int rows, int cols);
@@ -127,4 +128,26 @@ int gemm_qact_multi(vokra_hip_ctx* c, int n, const vokra_hip_qweight* const* ws,
                     const float* const* biases, float* const* outs);
 int qact_ln_quantize(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, const float* d_in, const float* gamma,
                      const float* beta, float eps, int act_quant, float* d_scratch);
+}  // namespace vk
+
+namespace vk {
+// Whisper front end (vk_frontend.hip): frame grid 3000 x 400, 201 bins.
+int fe_n_frames();
+int fe_n_bins();
+int fe_n_fft();
+int logmel_n_partial();
+}  // namespace vk
+#include <vector>
+namespace vk {
+void fe_hann_periodic(std::vector<float>& w);
+void fe_dft_basis(std::vector<float>& b);
+void fe_mel_filterbank(int n_mels, std::vector<float>& w);
+hipError_t launch_stft_frames(hipStream_t s, const float* pcm, int batch, int n_samples, const float* win,
+                              float* frames);
+hipError_t launch_power_spec(hipStream_t s, const float* spec, float* power, size_t rows);
+hipError_t launch_logmel_finish(hipStream_t s, const float* mel, int batch, int n_mels, float* out, float* partial);
+hipError_t launch_im2col(hipStream_t s, bool trans, const float* x, size_t sb, size_t sc, size_t sp, int batch,
+                         int in_ch, int in_len, int kernel, int stride, int padding, int out_len, float* col);
+hipError_t launch_add_row_bias(hipStream_t s, float* out, const float* bias, int rows, int cols);
+hipError_t launch_add_pos(hipStream_t s, float* out, const float* pos, size_t rows, int d, int period);
 }  // namespace vk

@@ -133,12 +133,16 @@ struct vokra_hip_encoder {
     std::vector<EncLayer> layers;
     DBuf lnpg, lnpb, h, x, q, k, v, attn, f;
     vokra_hip_qact_t *qa_d = nullptr, *qa_f = nullptr;
+    // conv stem (optional): weights, positional embedding, im2col / conv1 workspaces
+    size_t n_mels = 0, n_frames = 0, n_ctx = 0, stem_batch = 0;
+    DBuf c1w, c1b, c2w, c2b, pos, col1, c1, col2;
     void release() {
         for (auto& L : layers) {
             for (DBuf* b : {&L.ln1g, &L.ln1b, &L.ln2g, &L.ln2b}) b->release(ctx);
             for (QLin* w : {&L.q, &L.k, &L.v, &L.o, &L.fc1, &L.fc2}) w->release(ctx);
         }
-        for (DBuf* b : {&lnpg, &lnpb, &h, &x, &q, &k, &v, &attn, &f}) b->release(ctx);
+        for (DBuf* b : {&lnpg, &lnpb, &h, &x, &q, &k, &v, &attn, &f, &c1w, &c1b, &c2w, &c2b, &pos, &col1, &c1, &col2})
+            b->release(ctx);
         vokra_hip_qact_free(qa_d);
         vokra_hip_qact_free(qa_f);
         qa_d = qa_f = nullptr;
@@ -232,6 +236,40 @@ int enc_forward(vokra_hip_encoder* e, size_t batch, size_t frames, const float* 
         SS_TRY(L.fc2.run(c, e->qa_f, e->h.f(), add_h));
     }
     return vokra_hip_layer_norm_f32_dev(c, e->h.f(), d_out, rows, d, e->lnpg.f(), e->lnpb.f(), kLnEps);
+}
+
+// The conv stem of WhisperEncoder::encode (crates/vokra-models/src/whisper/
+// encoder.rs:58-104) as im2col + f32 GEMM with bias and GELU in the GEMM
+// epilogue, conv outputs kept time-major ([frames, d]), then + pos_emb; the
+// blocks follow (enc_forward).
+int enc_encode(vokra_hip_encoder* e, size_t batch, const float* d_mel, float* d_out) {
+    vokra_hip_ctx_t* c = e->ctx;
+    hipStream_t s = vk::ctx_stream(c);
+    const size_t d = e->d, nm = e->n_mels, nf = e->n_frames, nc = e->n_ctx;
+    if (batch > e->stem_batch) {  // workspaces grow with the largest batch seen
+        for (DBuf* b : {&e->col1, &e->c1, &e->col2}) b->release(c);
+        SS_TRY(e->col1.alloc(c, batch * nf * nm * 3 * sizeof(float)));
+        SS_TRY(e->c1.alloc(c, batch * nf * d * sizeof(float)));
+        SS_TRY(e->col2.alloc(c, batch * nc * d * 3 * sizeof(float)));
+        e->stem_batch = batch;
+    }
+    const VkEpi gelu = {nullptr, 1};
+    // conv1: [n_mels, n_frames] per clip, kernel 3, stride 1, pad 1
+    SS_HIP(vk::launch_im2col(s, true, d_mel, nm * nf, nf, 1, (int)batch, (int)nm, (int)nf, 3, 1, 1, (int)nf,
+                             e->col1.f()),
+           "launch(vk_im2col conv1)");
+    SS_HIP(vk::launch_gemm_f32(s, true, e->col1.f(), e->c1w.f(), e->c1b.f(), e->c1.f(), (int)(batch * nf), (int)d,
+                               (int)(nm * 3), gelu),
+           "launch(vk_gemm_f32 conv1)");
+    // conv2: the time-major conv1 output read as [d, n_frames], kernel 3, stride 2, pad 1
+    SS_HIP(vk::launch_im2col(s, true, e->c1.f(), nf * d, 1, d, (int)batch, (int)d, (int)nf, 3, 2, 1, (int)nc,
+                             e->col2.f()),
+           "launch(vk_im2col conv2)");
+    SS_HIP(vk::launch_gemm_f32(s, true, e->col2.f(), e->c2w.f(), e->c2b.f(), e->x.f(), (int)(batch * nc), (int)d,
+                               (int)(d * 3), gelu),
+           "launch(vk_gemm_f32 conv2)");
+    SS_HIP(vk::launch_add_pos(s, e->x.f(), e->pos.f(), batch * nc, (int)d, (int)nc), "launch(vk_add_pos)");
+    return enc_forward(e, batch, nc, e->x.f(), d_out);  // copies x into h before reusing x
 }
 
 int dec_setup(vokra_hip_decoder* m, const vokra_hip_decoder_layer_t* layers, const float* tok_emb,
@@ -405,6 +443,55 @@ int vokra_hip_encoder_forward_dev(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, si
         return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_forward: batch * frames exceeds max_rows");
     if (!d_x || !d_out) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_forward: NULL buffer");
     return enc_forward(e, batch, frames, d_x, d_out);
+}
+
+int vokra_hip_encoder_set_stem(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, size_t n_mels, size_t n_frames,
+                               const float* conv1_w, const float* conv1_b, const float* conv2_w, const float* conv2_b,
+                               const float* pos_emb) {
+    if (!c || !e || e->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_set_stem: bad context");
+    if (!conv1_w || !conv1_b || !conv2_w || !conv2_b || !pos_emb)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_set_stem: NULL weight");
+    if (n_mels == 0 || n_mels > 1024 || n_frames < 2 || n_frames > 65536)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_set_stem: n_mels 1..1024, n_frames 2..65536");
+    const size_t d = e->d, n_ctx = (n_frames + 2 - 3) / 2 + 1;  // conv_out_len(n_frames, 3, 2, 1)
+    for (DBuf* b : {&e->c1w, &e->c1b, &e->c2w, &e->c2b, &e->pos}) b->release(c);
+    SS_TRY(upload_vec(c, e->c1w, conv1_w, d * n_mels * 3, "encoder_set_stem: conv1_w"));
+    SS_TRY(upload_vec(c, e->c1b, conv1_b, d, "encoder_set_stem: conv1_b"));
+    SS_TRY(upload_vec(c, e->c2w, conv2_w, d * d * 3, "encoder_set_stem: conv2_w"));
+    SS_TRY(upload_vec(c, e->c2b, conv2_b, d, "encoder_set_stem: conv2_b"));
+    SS_TRY(upload_vec(c, e->pos, pos_emb, n_ctx * d, "encoder_set_stem: pos_emb"));
+    e->n_mels = n_mels;
+    e->n_frames = n_frames;
+    e->n_ctx = n_ctx;
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_encoder_encode_dev(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, size_t batch, const float* d_log_mel,
+                                 float* d_out) {
+    if (!c || !e || e->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_encode: bad context");
+    if (!e->n_ctx) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_encode: no conv stem (set_stem)");
+    if (batch == 0) return VOKRA_HIP_OK;
+    if (batch * e->n_ctx > e->max_rows)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_encode: batch * n_ctx exceeds max_rows");
+    if (!d_log_mel || !d_out) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_encode: NULL buffer");
+    return enc_encode(e, batch, d_log_mel, d_out);
+}
+
+int vokra_hip_encoder_encode(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, size_t batch, const float* log_mel,
+                             float* out) {
+    if (!c || !e || e->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_encode: bad context");
+    if (!e->n_ctx) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_encode: no conv stem (set_stem)");
+    if (batch == 0) return VOKRA_HIP_OK;
+    if (!log_mel || !out) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_encode: NULL buffer");
+    const size_t n_in = batch * e->n_mels * e->n_frames, n_out = batch * e->n_ctx * e->d;
+    DBuf in, o;
+    int st = in.upload(c, log_mel, n_in * sizeof(float));
+    if (!st) st = o.alloc(c, n_out * sizeof(float));
+    if (!st) st = vokra_hip_encoder_encode_dev(c, e, batch, in.f(), o.f());
+    if (!st) st = vokra_hip_memcpy_dtoh(c, out, o.p, n_out * sizeof(float));
+    in.release(c);
+    o.release(c);
+    return st;
 }
 
 int vokra_hip_encoder_forward(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, size_t batch, size_t frames, const float* x,

@@ -180,6 +180,13 @@ def _declare(L):
     L.vokra_hip_rms_norm_f32_dev.argtypes = [P, P, P, sz, sz, P, C.c_float]
     L.vokra_hip_gelu_f32.argtypes = [P, f32p, f32p, sz]
     L.vokra_hip_gelu_f32_dev.argtypes = [P, P, P, sz]
+    L.vokra_hip_log_mel.argtypes = [P, f32p, sz, sz, sz, f32p, sz]
+    L.vokra_hip_log_mel_dev.argtypes = [P, P, sz, sz, sz, P]
+    L.vokra_hip_conv1d_f32.argtypes = [P, f32p, sz, sz, sz, f32p, sz, sz, sz, f32p, sz, sz, f32p, sz]
+    L.vokra_hip_conv1d_f32_dev.argtypes = [P, P, sz, sz, P, sz, sz, P, sz, sz, P]
+    L.vokra_hip_encoder_set_stem.argtypes = [P, P, sz, sz, f32p, f32p, f32p, f32p, f32p]
+    L.vokra_hip_encoder_encode.argtypes = [P, P, sz, f32p, f32p]
+    L.vokra_hip_encoder_encode_dev.argtypes = [P, P, sz, P, P]
     L.vokra_hip_argmax_f32_dev.argtypes = [P, P, sz, sz, P]
     L.vokra_hip_add_f32_dev.argtypes = [P, P, P, P, sz]
     L.vokra_hip_encoder_create.argtypes = [P, C.c_int, sz, sz, sz, sz, C.POINTER(PrenormLayer), f32p, f32p, sz,
@@ -473,6 +480,25 @@ class Encoder:
     def forward_dev(self, batch, frames, d_x, d_out):
         _check(lib().vokra_hip_encoder_forward_dev(self._ctx._h, self._h, batch, frames, d_x.ptr, d_out.ptr))
 
+    def set_stem(self, n_mels, n_frames, conv1_w, conv1_b, conv2_w, conv2_b, pos_emb):
+        """The conv stem of WhisperEncoder::encode (encoder.rs:58-104)."""
+        keep = [_f32(a).reshape(-1) for a in (conv1_w, conv1_b, conv2_w, conv2_b, pos_emb)]
+        _check(lib().vokra_hip_encoder_set_stem(self._ctx._h, self._h, n_mels, n_frames,
+                                                *[_ptr(a, C.c_float) for a in keep]))
+        self.n_mels, self.n_frames, self.n_ctx = n_mels, n_frames, (n_frames - 1) // 2 + 1
+
+    def encode(self, log_mel):
+        """WhisperEncoder::encode (encoder.rs:41-178): [B, n_mels, n_frames] -> [B, n_ctx, d]."""
+        x = _f32(log_mel)
+        x = x.reshape(-1, self.n_mels, self.n_frames)
+        out = np.zeros((x.shape[0], self.n_ctx, self.d), np.float32)
+        _check(lib().vokra_hip_encoder_encode(self._ctx._h, self._h, x.shape[0], _ptr(x, C.c_float),
+                                              _ptr(out, C.c_float)))
+        return out
+
+    def encode_dev(self, batch, d_log_mel, d_out):
+        _check(lib().vokra_hip_encoder_encode_dev(self._ctx._h, self._h, batch, d_log_mel.ptr, d_out.ptr))
+
     def __del__(self):
         try:
             if getattr(self, "_h", None) and self._h.value and _ctx_alive(self):
@@ -697,6 +723,38 @@ class HipContext:
         out = np.zeros(max(xv.size, 1), np.float32)
         _check(lib().vokra_hip_gelu_f32(self._h, _ptr(xv, C.c_float), _ptr(out, C.c_float), xv.size))
         return out[:xv.size]
+
+    # ---- Whisper front end ----------------------------------------------------
+    def log_mel(self, pcm, n_mels: int):
+        """whisper::mel::log_mel (mel.rs:123-183). pcm [n] or [batch, n] -> [n_mels, 3000] / [batch, n_mels, 3000]."""
+        x = _f32(pcm)
+        single = x.ndim == 1
+        x2 = x.reshape(1 if single else x.shape[0], -1)
+        batch, n = x2.shape
+        out = np.zeros(batch * n_mels * 3000, np.float32)
+        _check(lib().vokra_hip_log_mel(self._h, _ptr(x2, C.c_float) if n else None, batch, n, n_mels,
+                                       _ptr(out, C.c_float), out.size))
+        out = out.reshape(batch, n_mels, 3000)
+        return out[0] if single else out
+
+    def log_mel_dev(self, d_pcm, batch, n_samples, n_mels, d_out):
+        _check(lib().vokra_hip_log_mel_dev(self._h, d_pcm.ptr, batch, n_samples, n_mels, d_out.ptr))
+
+    def conv1d_f32(self, x, in_ch, in_len, w, out_ch, kernel, bias=None, stride=1, padding=0):
+        """kernels::conv1d_f32 (mod.rs:583-822) -> [out_ch, out_len]."""
+        xv, wv = _f32(x).reshape(-1), _f32(w).reshape(-1)
+        bv = None if bias is None else _f32(bias).reshape(-1)
+        out_len = (in_len + 2 * padding - kernel) // stride + 1 if stride and kernel and \
+            in_len + 2 * padding >= kernel else 0
+        out = np.zeros(max(out_ch * out_len, 1), np.float32)
+        _check(lib().vokra_hip_conv1d_f32(self._h, _ptr(xv, C.c_float), xv.size, in_ch, in_len, _ptr(wv, C.c_float),
+                                          wv.size, out_ch, kernel, _ptr(bv, C.c_float), stride, padding,
+                                          _ptr(out, C.c_float), out_ch * out_len))
+        return out[:out_ch * out_len].reshape(out_ch, out_len)
+
+    def conv1d_f32_dev(self, d_x, in_ch, in_len, d_w, out_ch, kernel, d_bias, stride, padding, d_out):
+        _check(lib().vokra_hip_conv1d_f32_dev(self._h, d_x.ptr, in_ch, in_len, d_w.ptr, out_ch, kernel,
+                                              None if d_bias is None else d_bias.ptr, stride, padding, d_out.ptr))
 
     def argmax_f32_dev(self, d_logits, rows, cols, d_out):
         _check(lib().vokra_hip_argmax_f32_dev(self._h, d_logits.ptr, rows, cols, d_out.ptr))
