@@ -31,6 +31,8 @@ extern "C" {
 
 typedef enum vokra_hip_status_t {
     VOKRA_HIP_OK = 0,
+    VOKRA_HIP_ERROR_IO = 1,                  /* VokraError::Io */
+    VOKRA_HIP_ERROR_MODEL_LOAD = 2,          /* VokraError::ModelLoad */
     VOKRA_HIP_ERROR_UNSUPPORTED_OP = 3,      /* VokraError::UnsupportedOp */
     VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE = 4, /* VokraError::BackendUnavailable */
     VOKRA_HIP_ERROR_INVALID_ARGUMENT = 5,    /* VokraError::InvalidArgument */
@@ -358,6 +360,37 @@ int vokra_hip_conv1d_f32(vokra_hip_ctx_t *ctx, const float *input, size_t input_
 int vokra_hip_conv1d_f32_dev(vokra_hip_ctx_t *ctx, const float *d_input, size_t in_ch, size_t in_len,
                              const float *d_weight, size_t out_ch, size_t kernel, const float *d_bias, size_t stride,
                              size_t padding, float *d_out);
+
+/* ---- GGUF model files ------------------------------------------------------- */
+
+typedef struct vokra_hip_gguf vokra_hip_gguf_t;
+
+/* GgufFile::open over a read-only mapping (crates/vokra-core/src/gguf/
+ * reader.rs:126-190 with crates/vokra-mmap): GGUF v3 header, typed metadata,
+ * tensor infos, aligned data region, with the reader's checks (magic,
+ * version, counts, alignment, rank <= 8, duplicate names, offsets inside the
+ * file, whole blocks). Tensor types: F32, F16, Q4_0, Q5_0, Q8_0, Q4_K (the
+ * reference accepts F32/F16/Q4_K/Q5_K/Q6_K/BF16, tensor.rs:85-95; this file
+ * adds the block formats its GEMMs run). No GPU is touched. */
+int vokra_hip_gguf_open(const char *path, vokra_hip_gguf_t **out);
+void vokra_hip_gguf_close(vokra_hip_gguf_t *f);
+int vokra_hip_gguf_tensor_count(const vokra_hip_gguf_t *f, size_t *n);
+/* GgufFile::tensors / tensor_bytes: name, ggml type tag, dims (up to 8, ggml
+ * order: dims[0] is the contiguous axis) and the payload inside the mapping. */
+int vokra_hip_gguf_tensor_info(const vokra_hip_gguf_t *f, size_t index, const char **name, uint32_t *ggml_type,
+                               size_t *n_dims, uint64_t *dims, const void **data, size_t *n_bytes);
+/* GgufFile::tensor_info by name (reader.rs:218); MODEL_LOAD when absent. */
+int vokra_hip_gguf_find(const vokra_hip_gguf_t *f, const char *name, size_t *index);
+/* GgufFile::get (reader.rs:208) for integer / bool and string values. */
+int vokra_hip_gguf_meta_int(const vokra_hip_gguf_t *f, const char *key, int64_t *out);
+int vokra_hip_gguf_meta_str(const vokra_hip_gguf_t *f, const char *key, const char **out, size_t *len);
+/* A 2-D block-quant weight (dims [in, out]) straight from the mapping into a
+ * resident weight, as vokra_hip_qweight_upload: the fused-quant-weights route
+ * of the Whisper loader (crates/vokra-models/src/whisper/weights.rs:454-509). */
+int vokra_hip_gguf_upload_qweight(vokra_hip_ctx_t *ctx, const vokra_hip_gguf_t *f, const char *name,
+                                  vokra_hip_qweight_t **out);
+/* GgufFile::tensor_f32 (reader.rs:256) for F32 / F16 tensors (host output). */
+int vokra_hip_gguf_read_f32(const vokra_hip_gguf_t *f, const char *name, float *out, size_t out_len);
 
 /* ---- pre-norm encoder session ------------------------------------------- */
 

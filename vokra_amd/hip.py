@@ -39,7 +39,16 @@ class KvCacheExhausted(VokraError):
     code = 10
 
 
-_ERRORS = {3: UnsupportedOp, 4: BackendUnavailable, 5: InvalidArgument, 10: KvCacheExhausted}
+class IoError(VokraError):
+    """VokraError::Io (include/vokra.h VOKRA_ERROR_IO)."""
+
+
+class ModelLoad(VokraError):
+    """VokraError::ModelLoad (include/vokra.h VOKRA_ERROR_MODEL_LOAD)."""
+
+
+_ERRORS = {1: IoError, 2: ModelLoad, 3: UnsupportedOp, 4: BackendUnavailable, 5: InvalidArgument,
+           10: KvCacheExhausted}
 
 
 class KvQuant(IntEnum):
@@ -180,6 +189,17 @@ def _declare(L):
     L.vokra_hip_rms_norm_f32_dev.argtypes = [P, P, P, sz, sz, P, C.c_float]
     L.vokra_hip_gelu_f32.argtypes = [P, f32p, f32p, sz]
     L.vokra_hip_gelu_f32_dev.argtypes = [P, P, P, sz]
+    L.vokra_hip_gguf_open.argtypes = [C.c_char_p, C.POINTER(P)]
+    L.vokra_hip_gguf_close.argtypes = [P]
+    L.vokra_hip_gguf_close.restype = None
+    L.vokra_hip_gguf_tensor_count.argtypes = [P, C.POINTER(sz)]
+    L.vokra_hip_gguf_tensor_info.argtypes = [P, sz, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32), C.POINTER(sz),
+                                             C.POINTER(C.c_uint64), C.POINTER(P), C.POINTER(sz)]
+    L.vokra_hip_gguf_find.argtypes = [P, C.c_char_p, C.POINTER(sz)]
+    L.vokra_hip_gguf_meta_int.argtypes = [P, C.c_char_p, C.POINTER(C.c_int64)]
+    L.vokra_hip_gguf_meta_str.argtypes = [P, C.c_char_p, C.POINTER(C.c_char_p), C.POINTER(sz)]
+    L.vokra_hip_gguf_upload_qweight.argtypes = [P, P, C.c_char_p, C.POINTER(P)]
+    L.vokra_hip_gguf_read_f32.argtypes = [P, C.c_char_p, f32p, sz]
     L.vokra_hip_log_mel.argtypes = [P, f32p, sz, sz, sz, f32p, sz]
     L.vokra_hip_log_mel_dev.argtypes = [P, P, sz, sz, sz, P]
     L.vokra_hip_conv1d_f32.argtypes = [P, f32p, sz, sz, sz, f32p, sz, sz, sz, f32p, sz, sz, f32p, sz]
@@ -333,6 +353,73 @@ class QWeight:
                 lib().vokra_hip_qweight_free(self._h)
         except Exception:
             pass
+
+
+class GgufFile:
+    """GgufFile (crates/vokra-core/src/gguf/reader.rs) over a read-only mapping
+    held by the library. Parsing needs no GPU."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        _check(lib().vokra_hip_gguf_open(os.fsencode(path), C.byref(h)))
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            lib().vokra_hip_gguf_close(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __len__(self):
+        n = C.c_size_t()
+        _check(lib().vokra_hip_gguf_tensor_count(self._h, C.byref(n)))
+        return n.value
+
+    def tensor(self, i):
+        """(name, ggml type tag, dims, payload bytes) of tensor i."""
+        name, t, nd, data, nb = C.c_char_p(), C.c_uint32(), C.c_size_t(), C.c_void_p(), C.c_size_t()
+        dims = (C.c_uint64 * 8)()
+        _check(lib().vokra_hip_gguf_tensor_info(self._h, i, C.byref(name), C.byref(t), C.byref(nd), dims,
+                                                C.byref(data), C.byref(nb)))
+        payload = C.string_at(data.value, nb.value) if nb.value else b""
+        return name.value.decode(), t.value, [int(dims[d]) for d in range(nd.value)], payload
+
+    def tensors(self):
+        return [self.tensor(i) for i in range(len(self))]
+
+    def find(self, name) -> int:
+        i = C.c_size_t()
+        _check(lib().vokra_hip_gguf_find(self._h, name.encode(), C.byref(i)))
+        return i.value
+
+    def meta_int(self, key) -> int:
+        v = C.c_int64()
+        _check(lib().vokra_hip_gguf_meta_int(self._h, key.encode(), C.byref(v)))
+        return v.value
+
+    def meta_str(self, key) -> str:
+        p, n = C.c_char_p(), C.c_size_t()
+        _check(lib().vokra_hip_gguf_meta_str(self._h, key.encode(), C.byref(p), C.byref(n)))
+        return C.string_at(p, n.value).decode()
+
+    def read_f32(self, name, n):
+        out = np.zeros(max(n, 1), np.float32)
+        _check(lib().vokra_hip_gguf_read_f32(self._h, name.encode(), _ptr(out, C.c_float), n))
+        return out[:n]
+
+    def upload_qweight(self, ctx, name) -> "QWeight":
+        """vokra_hip_gguf_upload_qweight: the named [in, out] block-quant tensor as a resident weight."""
+        p = C.c_void_p()
+        _check(lib().vokra_hip_gguf_upload_qweight(ctx._h, self._h, name.encode(), C.byref(p)))
+        _, t, dims, _ = self.tensor(self.find(name))
+        w = QWeight.__new__(QWeight)
+        w.ctx, w.wdtype, w.n, w.k, w._h = ctx, WDtype(t), dims[1], dims[0], p
+        return w
 
 
 class Graph:
