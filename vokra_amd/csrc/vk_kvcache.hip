@@ -268,15 +268,18 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
                                                      float* __restrict__ part_o) {
     constexpr int NB = HD / 32;            // blocks per head slice
     constexpr int NO = G * HD;             // outputs of the workgroup
-    constexpr int OPT = NO >= 256 ? NO / 256 : 1;    // outputs per thread
-    constexpr int TPO = NO >= 256 ? 1 : 256 / NO;    // threads per output
+    // P.V work unit: a quad of 4 consecutive outputs of one head (one 32-bit
+    // LDS read of V quants feeds 4 FMAs; the quad shares its block's scale)
+    constexpr int NQ = NO / 4;
+    constexpr int OPT = NQ >= 256 ? NQ / 256 : 1;    // quads per thread
+    constexpr int TPO = NQ >= 256 ? 1 : 256 / NQ;    // threads per quad
     __shared__ __align__(16) float lq[G][HD];
     __shared__ float lpd[G][pa::CH][NB];         // p_j * d_{j,b} for the V product
     __shared__ float lalpha[G];                  // chunk rescale factors (uniform)
     __shared__ float lml[G][2];                  // final (m, l) per head
     __shared__ __align__(16) int8_t lv[pa::CH][HD];  // V quants of the chunk
     __shared__ float red[G][8];
-    __shared__ float lpart[256 * OPT];
+    __shared__ __align__(16) float lpart[256 * OPT][4];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int split = blockIdx.x, hk = blockIdx.y, item = blockIdx.z;
@@ -295,9 +298,11 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
         m_run[g] = -INFINITY;
         l_run[g] = 0.0f;
     }
-    float o_acc[OPT];
+    float o_acc[OPT][4];
 #pragma unroll
-    for (int u = 0; u < OPT; ++u) o_acc[u] = 0.0f;
+    for (int u = 0; u < OPT; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o_acc[u][i] = 0.0f;
     __syncthreads();
 
     for (int j0 = k0; j0 < k1; j0 += pa::CH) {
@@ -374,22 +379,30 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
         __syncthreads();
 #pragma unroll
         for (int g = 0; g < G; ++g) l_run[g] = l_run[g] * alpha[g] + ((red[g][4] + red[g][5]) + (red[g][6] + red[g][7]));
-        // ---- O += P . V: output o = (g, e); TPO threads share an output
+        // ---- O += P . V: quad oq = (g, e0..e0+3); TPO threads share a quad
         const int nk = min(pa::CH, k1 - j0);
 #pragma unroll
         for (int u = 0; u < OPT; ++u) {
-            const int o = NO >= 256 ? tid + 256 * u : tid / TPO;
-            const int part = NO >= 256 ? 0 : tid % TPO;
-            const int g = o / HD, e = o % HD;
-            float a = 0.0f;
-            for (int jj = part; jj < nk; jj += TPO) a = fmaf(lpd[g][jj][e >> 5], (float)lv[jj][e], a);
-            o_acc[u] = o_acc[u] * lalpha[g] + a;
+            const int oq = NQ >= 256 ? tid + 256 * u : tid / TPO;
+            const int part = NQ >= 256 ? 0 : tid % TPO;
+            const int g = (4 * oq) / HD, e0 = (4 * oq) % HD;
+            float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int jj = part; jj < nk; jj += TPO) {
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(&lv[jj][e0]);
+                const float pd = lpd[g][jj][e0 >> 5];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[i] = fmaf(pd, (float)(int8_t)((w >> (8 * i)) & 0xffu), a[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o_acc[u][i] = o_acc[u][i] * lalpha[g] + a[i];
         }
         __syncthreads();
     }
-    // ---- reduce the TPO partials of each output (fixed order), then write
+    // ---- reduce the TPO partials of each quad (fixed order), then write
 #pragma unroll
-    for (int u = 0; u < OPT; ++u) lpart[tid + 256 * u] = o_acc[u];
+    for (int u = 0; u < OPT; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lpart[tid + 256 * u][i] = o_acc[u][i];
     if (tid == 0)
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -398,12 +411,12 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
         }
     __syncthreads();
     for (int o = tid; o < NO; o += 256) {
-        const int g = o / HD, e = o % HD;
+        const int g = o / HD, e = o % HD, oq = o >> 2, i = o & 3;
         float a = 0.0f;
-        if (NO >= 256) {
-            a = lpart[(o % 256) + 256 * (o / 256)];
+        if (NQ >= 256) {
+            a = lpart[(oq % 256) + 256 * (oq / 256)][i];
         } else {
-            for (int r = 0; r < TPO; ++r) a += lpart[o * TPO + r];
+            for (int r = 0; r < TPO; ++r) a += lpart[oq * TPO + r][i];
         }
         const int h = hk * G + g;
         if (n_split == 1) {
