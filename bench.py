@@ -30,7 +30,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "quant-GEMM TOPS + paged-attn GB/s (% peak); decode tok/s, Whisper-large shape"
-PEAK = {"int8_tops": 5000.0, "bf16_tflops": 2500.0, "hbm_gbs": 8000.0}
+PEAK = {"int8_tops": 5000.0, "bf16_tflops": 2500.0, "fp32_tflops": 157.3, "hbm_gbs": 8000.0}
 
 
 def timed_steps(ctx, hip, steps, warmup, launch, kernel_of_interest):
@@ -385,6 +385,41 @@ def bench_decoder(ctx, hip, n_stream=64, n_layer=32, d=1280, H=20, ff=5120, V=51
             "gbs": round(total / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(total / (ms * 1e-3) / 1e9 / PEAK["hbm_gbs"], 4)}
 
 
+def bench_logits(ctx, hip, n=64, V=51866, d=1280, reps=20):
+    """Config 3 tail: tied logits over the Whisper vocabulary (f32 embedding
+    [V, d], 265.6 MB) for 64 streams and the greedy argmax, as one fused pass
+    (vk_logits_argmax + the partial merge) with and without the logits
+    written, beside the unfused route (f32 GEMM into logits, then argmax)."""
+    rng = np.random.default_rng(5)
+    d_x = hip.DeviceBuffer.from_array(ctx, rng.standard_normal((n, d), dtype=np.float32))
+    d_e = hip.DeviceBuffer.from_array(ctx, (0.02 * rng.standard_normal((V, d))).astype(np.float32))
+    d_l = hip.DeviceBuffer(ctx, n * V * 4)
+    d_n = hip.DeviceBuffer(ctx, n * 4)
+    runs = {
+        "fused": lambda: ctx.logits_argmax_dev(n, V, d, d_x, d_e, None, d_n),
+        "fused_with_logits": lambda: ctx.logits_argmax_dev(n, V, d, d_x, d_e, d_l, d_n),
+        "gemm_then_argmax": lambda: (ctx.gemm_f32_dev(n, V, d, d_x, d_e, d_l, b_trans=True),
+                                     ctx.argmax_f32_dev(d_l, n, V, d_n)),
+    }
+    out = {"streams": n, "vocab": V, "d": d, "emb_bytes": V * d * 4, "flop": 2 * n * V * d}
+    for name, fn in runs.items():
+        fn()
+        ctx.synchronize()
+        e0, e1 = hip.Event(ctx), hip.Event(ctx)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        ms = e0.elapsed_ms(e1) / reps
+        out[name] = {"us": round(ms * 1e3, 2), "emb_gbs": round(V * d * 4 / (ms * 1e-3) / 1e9, 1),
+                     "tflops": round(2 * n * V * d / (ms * 1e-3) / 1e12, 2)}
+    out["fused"]["frac_f32_mfma_peak"] = round(out["fused"]["tflops"] / PEAK["fp32_tflops"], 4)
+    out["fused"]["frac_hbm"] = round(out["fused"]["emb_gbs"] / PEAK["hbm_gbs"], 4)
+    for b in (d_x, d_e, d_l, d_n):
+        b.free()
+    return out
+
+
 def bench_copy(ctx, hip, nbytes=1 << 30, reps=5):
     """Plain streaming copy of 1 GiB (4x the 256 MB MALL): the
     achievable-HBM reference and the rocprof byte-counter calibration kernel."""
@@ -439,7 +474,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default=None,
                     help="comma list of single legs to run, one JSON line each (for profiling): "
-                         "gemm, gemm_pow2, copy, gemv, q4k, sdpa, paged, encoder, decoder, frontend")
+                         "gemm, gemm_pow2, copy, gemv, q4k, sdpa, paged, encoder, decoder, frontend, logits")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -462,6 +497,7 @@ def main():
             "encoder": lambda: [bench_encoder(ctx, hip, 1), bench_encoder(ctx, hip, 16)],
             "decoder": lambda: bench_decoder(ctx, hip),
             "frontend": lambda: bench_frontend(ctx, hip),
+            "logits": lambda: bench_logits(ctx, hip),
         }
         for name in args.only.split(","):
             res = legs[name]()
@@ -480,6 +516,7 @@ def main():
                   bench_paged_attn(ctx, hip, 32, 2, 128, 16, 512, 4096, 4096)]
     encoder_runs = [bench_encoder(ctx, hip, 1), bench_encoder(ctx, hip, 16)]
     frontend_run = bench_frontend(ctx, hip)
+    logits_run = bench_logits(ctx, hip)
     decoder_run = bench_decoder(ctx, hip)
 
     M, N, K = main_run["M"], main_run["N"], main_run["K"]
@@ -515,6 +552,7 @@ def main():
             "paged_attn_config3_config4": paged_runs,
             "encoder_config2": encoder_runs,
             "frontend_config2_batch16": frontend_run,
+            "logits_argmax_config3": logits_run,
             "decoder_step_config3": decoder_run,
             "gemm_kernel_ms": round(main_run["gemm_ms"], 4),
             "eager_step_ms": round(main_run["eager_ms"], 4),

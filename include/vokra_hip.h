@@ -244,6 +244,19 @@ int vokra_hip_gelu_f32_dev(vokra_hip_ctx_t *ctx, const float *d_x, float *d_out,
 int vokra_hip_argmax_f32_dev(vokra_hip_ctx_t *ctx, const float *d_logits, size_t rows, size_t cols,
                              int32_t *d_out);
 
+/* Tied logits and greedy argmax in one pass over the embedding:
+ * logits[s, v] = emb[v, :] . x[s, :] for s < rows, v < vocab, then
+ * next[s] = the first strict maximum of row s from -inf (NaN never wins, ties
+ * keep the lowest index, 0 when nothing beats -inf). Replaces
+ * project_logits_into (crates/vokra-models/src/whisper/decoder.rs:754-796:
+ * gemv_f32 / gemm_f32 of token_emb [vocab, d] against h) followed by argmax
+ * (crates/vokra-core/src/decode/sampler.rs:197-206). f32 products and sums
+ * (sum order differs from the sequential fold). d must be a multiple of 64;
+ * x and emb 16-byte aligned. d_logits may be NULL: the logits are then not
+ * written at all. Device pointers. */
+int vokra_hip_logits_argmax_dev(vokra_hip_ctx_t *ctx, size_t rows, size_t vocab, size_t d, const float *d_x,
+                                const float *d_emb, float *d_logits, int32_t *d_next);
+
 /* ---- fused attention --------------------------------------------------- */
 
 /* Scaled-dot-product attention, f32 in and out, per batch b and query head h

@@ -155,3 +155,65 @@ def test_f32_rejections(ctx):
         ctx.gemv_f32(2, 3, np.zeros(6), np.zeros(2))
     with pytest.raises(hip.InvalidArgument):
         ctx.layer_norm_f32(np.zeros(8), 2, 4, np.zeros(3), np.zeros(4))
+
+
+def fused_logits(ctx, x, e, write=True):
+    n, d = x.shape
+    v = e.shape[0]
+    d_x, d_e = hip.DeviceBuffer.from_array(ctx, x), hip.DeviceBuffer.from_array(ctx, e)
+    d_l = hip.DeviceBuffer(ctx, n * v * 4) if write else None
+    d_n = hip.DeviceBuffer(ctx, n * 4)
+    ctx.logits_argmax_dev(n, v, d, d_x, d_e, d_l, d_n)
+    logits = d_l.download(np.float32, n * v).reshape(n, v) if write else None
+    return logits, d_n.download(np.int32, n)
+
+
+@pytest.mark.parametrize("n,v,d", [(1, 51866, 1280), (5, 1000, 128), (16, 4099, 384), (17, 333, 512),
+                                   (33, 2049, 256), (64, 51866, 1280), (70, 777, 640)])
+def test_logits_argmax(ctx, oracle, n, v, d):
+    """Fused tied logits + argmax: logits within the f32 dot-product bound of
+    float64; next = the sampler's argmax of the kernel's own logits, exactly,
+    with and without the logits written."""
+    print(f"[case] logits_argmax n={n} v={v} d={d}", flush=True)
+    g = np.random.default_rng(n * 1000 + d)
+    x = g.standard_normal((n, d)).astype(np.float32)
+    e = (g.standard_normal((v, d)) * 0.05).astype(np.float32)
+    logits, nxt = fused_logits(ctx, x, e)
+    exact = x.astype(np.float64) @ e.astype(np.float64).T
+    assert np.all(np.abs(logits - exact) <= dot_bound(x, e.T, d))
+    assert nxt.tolist() == [oracle.argmax(r) for r in logits]
+    _, nxt2 = fused_logits(ctx, x, e, write=False)
+    assert np.array_equal(nxt, nxt2)
+
+
+def test_logits_argmax_rules(ctx, oracle):
+    """Ties across workgroups keep the lowest index, NaN rows never win, +inf
+    wins at its first index, and rows with nothing above -inf give 0."""
+    print("[case] logits_argmax rules", flush=True)
+    g = np.random.default_rng(77)
+    n, v, d = 6, 40100, 256
+    x = np.abs(g.standard_normal((n, d))).astype(np.float32) + 0.1
+    e = (g.standard_normal((v, d)) * 0.01).astype(np.float32)
+    e[40001] = e[7] = e[33] = 0.5       # equal maxima in three workgroups
+    e[3] = np.nan                       # a NaN logit for every stream
+    logits, nxt = fused_logits(ctx, x, e)
+    assert np.isnan(logits[:, 3]).all()
+    assert np.array_equal(logits[:, 7], logits[:, 40001]) and np.array_equal(logits[:, 7], logits[:, 33])
+    assert nxt.tolist() == [7] * n == [oracle.argmax(r) for r in logits]
+    e[39000] = np.inf
+    e[39500] = np.inf
+    logits, nxt = fused_logits(ctx, x, e)
+    assert nxt.tolist() == [39000] * n == [oracle.argmax(r) for r in logits]
+    for fill in (-np.inf, np.nan):
+        _, nxt = fused_logits(ctx, x[:, :128].copy(), np.full((300, 128), fill, np.float32), write=False)
+        assert nxt.tolist() == [0] * n
+
+
+def test_logits_argmax_rejections(ctx):
+    x = hip.DeviceBuffer(ctx, 4 * 200)
+    e = hip.DeviceBuffer(ctx, 4 * 200 * 10)
+    nx = hip.DeviceBuffer(ctx, 16)
+    with pytest.raises(hip.InvalidArgument, match="multiple of 128"):
+        ctx.logits_argmax_dev(1, 10, 200, x, e, None, nx)
+    with pytest.raises(hip.InvalidArgument, match="vocab"):
+        ctx.logits_argmax_dev(1, 0, 128, x, e, None, nx)

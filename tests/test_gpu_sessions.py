@@ -150,6 +150,20 @@ def test_decoder_batch_equals_single_stream_steps(ctx, oracle):
         tok, pos = [int(t) for t in na], [p + 1 for p in pos]
 
 
+def test_decoder_tokens_without_logits(ctx, oracle):
+    """Steps that do not ask for logits (the fused logits + argmax then never
+    writes them) choose the same tokens as steps that do."""
+    print("[case] decoder tokens without logits", flush=True)
+    a, _ = make_decoder(ctx, oracle, np.random.default_rng(11))
+    b, _ = make_decoder(ctx, oracle, np.random.default_rng(11))
+    tok, pos = [3, 7, 11, 13], [0, 0, 0, 0]
+    for _ in range(4):
+        na, _ = a.step([0, 1, 2, 3], tok, pos, want_logits=True)
+        nb = b.step([0, 1, 2, 3], tok, pos)
+        assert np.array_equal(na, nb)
+        tok, pos = [int(t) for t in na], [p + 1 for p in pos]
+
+
 def test_decoder_steps_vs_oracle(ctx, oracle):
     """Ragged batches: streams join late and skip steps; tokens follow the
     GPU's greedy choice in both paths."""

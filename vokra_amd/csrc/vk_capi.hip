@@ -117,6 +117,7 @@ struct vokra_hip_ctx {
     // spectrum, power, mel energies, per-block maxima; im2col columns
     DevBuf fe_win, fe_basis, fe_fb, fe_frames, fe_spec, fe_pow, fe_mel, fe_part, cv_col;
     int fe_mels = 0;
+    DevBuf lg_part;  // per-workgroup (max, index) partials of the fused logits argmax
 };
 
 struct vokra_hip_qweight {
@@ -1050,6 +1051,40 @@ int vokra_hip_argmax_f32_dev(vokra_hip_ctx_t* c, const float* d_logits, size_t r
     return VOKRA_HIP_OK;
 }
 
+namespace vk {
+int check_logits_argmax(size_t rows, size_t vocab, size_t d, const float* x, const float* emb, const float* logits,
+                        const int32_t* next) {
+    if (!fits_int(rows) || !fits_int(vocab) || !fits_int(d))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "logits_argmax: dimension exceeds int32");
+    if (vocab == 0) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "logits_argmax: vocab must be positive");
+    if (d < (size_t)logits_min_d() || d % logits_d_multiple() != 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "logits_argmax: d must be a positive multiple of %d",
+                    logits_d_multiple());
+    size_t vd;
+    if (!mul_ok(vocab, d, &vd)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "logits_argmax: dimension product overflows");
+    if (rows && (!x || !emb || !next)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "logits_argmax: NULL buffer");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(emb)) & 15)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "logits_argmax: x and emb must be 16-byte aligned");
+    (void)logits;
+    return VOKRA_HIP_OK;
+}
+}  // namespace vk
+
+int vokra_hip_logits_argmax_dev(vokra_hip_ctx_t* c, size_t rows, size_t vocab, size_t d, const float* d_x,
+                                const float* d_emb, float* d_logits, int32_t* d_next) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "logits_argmax: ctx is NULL");
+    int st = vk::check_logits_argmax(rows, vocab, d, d_x, d_emb, d_logits, d_next);
+    if (st) return st;
+    if (rows == 0) return VOKRA_HIP_OK;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(c->lg_part.ensure(rows * (size_t)vk::logits_n_vt((int)vocab) * sizeof(float2)),
+           "hipMalloc(logits argmax partials)");
+    VK_TRY(vk::launch_logits_argmax(c->stream, d_x, d_emb, d_logits, (float2*)c->lg_part.p, d_next, (int)rows,
+                                    (int)vocab, (int)d),
+           "launch(vk_logits_argmax)");
+    return VOKRA_HIP_OK;
+}
+
 int vokra_hip_attn_f32_dev(vokra_hip_ctx_t* c, size_t batch, size_t t_q, size_t t_kv, size_t n_head_q,
                            size_t n_head_kv, size_t head_dim, const float* d_q, const float* d_k, const float* d_v,
                            float scale, int causal, size_t q_offset, float* d_out) {
@@ -1143,7 +1178,7 @@ void vokra_hip_destroy(vokra_hip_ctx_t* c) {
     (void)hipStreamSynchronize(c->stream);
     for (DevBuf* b : {&c->in0, &c->in1, &c->in2, &c->out0, &c->act.frag, &c->act.scale, &c->act.gsum, &c->at_qh,
                       &c->at_ql, &c->at_kh, &c->at_kl, &c->at_vh, &c->at_vl, &c->fe_win, &c->fe_basis, &c->fe_fb,
-                      &c->fe_frames, &c->fe_spec, &c->fe_pow, &c->fe_mel, &c->fe_part, &c->cv_col})
+                      &c->fe_frames, &c->fe_spec, &c->fe_pow, &c->fe_mel, &c->fe_part, &c->cv_col, &c->lg_part})
         b->release();
     (void)hipStreamDestroy(c->stream);
     delete c;

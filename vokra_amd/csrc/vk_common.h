@@ -185,3 +185,32 @@ __device__ __forceinline__ float2 vk_ln_stats256(const float* __restrict__ row, 
 __device__ __forceinline__ float vk_ln_apply(float x, float2 st, float g, float b) {
     return (x - st.x) * st.y * g + b;
 }
+
+// Direct global -> LDS loads (global_load_lds_dwordx4 / _dword). M0 holds the
+// wave-uniform LDS base; lane l writes base + l * size. They are issued from
+// inline asm so the compiler does not fence every LDS read on them; their
+// completion is tracked by hand with vmcnt (loads retire in issue order).
+// Nothing else in the kernels that use them reads M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void vk_dma_b128(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void vk_dma_b32(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_base)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t vk_lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// Wait until at most N of this wave's vector-memory loads (the direct-to-LDS
+// loads above included) are in flight.
+template <int N>
+__device__ __forceinline__ void vk_wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+

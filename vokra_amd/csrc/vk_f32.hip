@@ -254,6 +254,189 @@ __global__ __launch_bounds__(256) void vk_argmax_f32(const float* __restrict__ l
     }
 }
 
+// ---------------------------------------------------------------------------
+// Tied logits and greedy argmax in one pass over the embedding
+// (whisper/decoder.rs:754-796 project_logits_into, then decode/sampler.rs:
+// 197-206 argmax): logits[s][v] = emb[v][:] . x[s][:].
+//
+// One workgroup per 16*J vocabulary rows and up to 16*NCT streams (1621
+// workgroups at the Whisper vocabulary: fine-grained enough to balance 256
+// CUs). Its 4 waves split d into quarters and their partial dots are summed
+// in wave order. Operands are v_mfma_f32_16x16x4f32 fragments taken straight
+// from row-major memory: vocabulary rows on the 16-row side, streams on the
+// 16-column side, lane l holding k = 4*(l/16) .. +3 of row l%16 of a 16-wide
+// k chunk as one float4, MFMA s of the chunk taking component s of both
+// operands (A and B agree on k). Each wave moves its chunks global -> LDS with
+// direct loads (lane l lands at slot + 16*l and reads the same 16 bytes back)
+// through a private three-slot ring, two chunks ahead of the MFMAs; a stream's
+// x row is read by every workgroup from L2.
+//
+// The argmax keeps the sampler's rule: first strict maximum from -inf (NaN
+// never wins, ties keep the lowest index, index 0 when nothing beats -inf).
+// Each workgroup stores its (max, index) per stream; vk_argmax_parts scans
+// those in vocabulary order with the same rule.
+namespace lg {
+#ifndef VK_LG_WAVES
+#define VK_LG_WAVES 4
+#endif
+#ifndef VK_LG_J
+#define VK_LG_J 2
+#endif
+#ifndef VK_LG_NSLOT
+#define VK_LG_NSLOT 3
+#endif
+constexpr int WAVES = VK_LG_WAVES, J = VK_LG_J, NSLOT = VK_LG_NSLOT;
+static_assert(NSLOT >= 2 && NSLOT <= 4, "ring depth");
+static_assert(WAVES >= 1 && WAVES <= 16, "workgroup of 64 * WAVES threads");
+}
+
+__device__ __forceinline__ float vk_f4c(const float4& v, int s) {
+    return s == 0 ? v.x : (s == 1 ? v.y : (s == 2 ? v.z : v.w));
+}
+
+// (value desc, index asc) merge of two argmax candidates
+__device__ __forceinline__ void vk_am_merge(float& bv, int& bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+    }
+}
+
+template <int NCT, bool WRITE>
+__global__ __launch_bounds__(64 * lg::WAVES) void vk_logits_argmax(const float* __restrict__ x, const float* __restrict__ emb,
+                                                           float* __restrict__ logits, float2* __restrict__ part,
+                                                           int n, int vocab, int d, int n_vt) {
+    using namespace lg;
+    constexpr int Q = J + NCT;  // 1 KiB direct loads per wave per chunk
+    __shared__ __align__(16) uint4 ring[WAVES][NSLOT][Q][64];
+    // after the k loop the ring holds the partial dots of waves 1..3
+    static_assert(sizeof(ring) >= sizeof(vk_f32x4) * (WAVES - 1) * J * NCT * 64, "reduction fits the ring");
+    vk_f32x4* red = reinterpret_cast<vk_f32x4*>(&ring[0][0][0][0]);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int v0 = blockIdx.x * 16 * J, s0 = blockIdx.y * 16 * NCT;
+    const int dq = d / WAVES;                    // this wave's k range: [wave*dq, wave*dq + dq)
+    const int kq = wave * dq + 4 * (lane >> 4);  // the lane's first k within a chunk
+    const float* ep[J];
+    const float* xp[NCT];
+#pragma unroll
+    for (int j = 0; j < J; ++j) ep[j] = emb + (size_t)min(v0 + 16 * j + (lane & 15), vocab - 1) * d + kq;
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) xp[c] = x + (size_t)min(s0 + 16 * c + (lane & 15), n - 1) * d + kq;
+    const uint32_t base = __builtin_amdgcn_readfirstlane(vk_lds_addr(&ring[wave][0][0][0]));
+    constexpr uint32_t SLOT = Q * 1024;
+    auto issue = [&](int ck, int slot) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) vk_dma_b128(ep[j] + 16 * ck, base + slot * SLOT + j * 1024);
+#pragma unroll
+        for (int c = 0; c < NCT; ++c) vk_dma_b128(xp[c] + 16 * ck, base + slot * SLOT + (J + c) * 1024);
+    };
+    vk_f32x4 acc[J][NCT];
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int c = 0; c < NCT; ++c) acc[j][c] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int nk = dq / 16;  // 16-wide k chunks of this wave (>= NSLOT - 1)
+#pragma unroll
+    for (int p = 0; p < NSLOT - 1; ++p) issue(p, p);
+    int slot = 0;
+#pragma unroll 1
+    for (int ck = 0; ck < nk; ++ck) {
+        // chunk ck's loads are the oldest in flight: wait for exactly those
+        const int ahead = nk - 1 - ck;  // chunks loaded after ck, once the ring is full
+        if (ahead >= NSLOT - 1) {
+            issue(ck + NSLOT - 1, slot == 0 ? NSLOT - 1 : slot - 1);
+            vk_wait_vm<(NSLOT - 1) * Q>();
+        } else if (NSLOT > 3 && ahead == 2) {
+            vk_wait_vm<2 * Q>();
+        } else if (ahead == 1) {
+            vk_wait_vm<Q>();
+        } else {
+            vk_wait_vm<0>();
+        }
+        float4 ce[J], cx[NCT];
+#pragma unroll
+        for (int j = 0; j < J; ++j) ce[j] = *reinterpret_cast<const float4*>(&ring[wave][slot][j][lane]);
+#pragma unroll
+        for (int c = 0; c < NCT; ++c) cx[c] = *reinterpret_cast<const float4*>(&ring[wave][slot][J + c][lane]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+#pragma unroll
+                for (int c = 0; c < NCT; ++c)
+                    acc[j][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vk_f4c(ce[j], s), vk_f4c(cx[c], s), acc[j][c],
+                                                                     0, 0, 0);
+        slot = slot == NSLOT - 1 ? 0 : slot + 1;
+    }
+    __syncthreads();  // every wave is done with the ring (its loads have all landed)
+    if (wave > 0) {
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int c = 0; c < NCT; ++c) red[((wave - 1) * J * NCT + j * NCT + c) * 64 + lane] = acc[j][c];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) {
+        const int s = s0 + 16 * c + (lane & 15);
+        float bv = -INFINITY;
+        int bi = INT_MAX;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            vk_f32x4 t = acc[j][c];
+#pragma unroll
+            for (int w = 0; w < WAVES - 1; ++w) {
+                const vk_f32x4 o = red[(w * J * NCT + j * NCT + c) * 64 + lane];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) t[r] += o[r];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int v = v0 + 16 * j + 4 * (lane >> 4) + r;  // ascending within the lane
+                if (v < vocab) {
+                    if (WRITE && s < n) logits[(size_t)s * vocab + v] = t[r];
+                    if (t[r] > bv) {
+                        bv = t[r];
+                        bi = v;
+                    }
+                }
+            }
+        }
+        // lanes l, l^16, l^32, l^48 hold the same stream
+        vk_am_merge(bv, bi, __shfl_xor(bv, 16, VK_WAVE), __shfl_xor(bi, 16, VK_WAVE));
+        vk_am_merge(bv, bi, __shfl_xor(bv, 32, VK_WAVE), __shfl_xor(bi, 32, VK_WAVE));
+        if (lane < 16 && s < n) part[(size_t)s * n_vt + blockIdx.x] = make_float2(bv, __int_as_float(bi));
+    }
+}
+
+// One workgroup per stream: merge its n_vt (max, index) partials. A partial
+// whose max is -inf holds no candidate; the result is index 0 when no value
+// beats -inf, as in the sampler.
+__global__ __launch_bounds__(256) void vk_argmax_parts(const float2* __restrict__ part, int n_vt,
+                                                       int* __restrict__ out) {
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    const float2* p = part + (size_t)blockIdx.x * n_vt;
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for (int t = threadIdx.x; t < n_vt; t += 256) {
+        const float2 q = p[t];
+        vk_am_merge(bv, bi, q.x, __float_as_int(q.y));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) vk_am_merge(bv, bi, __shfl_xor(bv, o, VK_WAVE), __shfl_xor(bi, o, VK_WAVE));
+    if ((threadIdx.x & 63) == 0) {
+        rv[threadIdx.x >> 6] = bv;
+        ri[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) vk_am_merge(bv, bi, rv[w], ri[w]);
+        out[blockIdx.x] = bv > -INFINITY ? bi : 0;
+    }
+}
+
 }  // namespace vk
 
 #include "vk_launch.h"
@@ -323,6 +506,39 @@ hipError_t launch_embed_f32(hipStream_t s, const float* tok_emb, const float* po
 hipError_t launch_argmax_f32(hipStream_t s, const float* logits, int rows, int cols, int* out) {
     if (rows == 0) return hipSuccess;
     hipLaunchKernelGGL(vk_argmax_f32, dim3(rows), dim3(256), 0, s, logits, cols, out);
+    return hipGetLastError();
+}
+
+int logits_n_vt(int vocab) { return (vocab + 16 * lg::J - 1) / (16 * lg::J); }
+
+template <int NCT>
+static void go_logits(hipStream_t s, const float* x, const float* emb, float* logits, float2* part, int n, int vocab,
+                      int d, int n_vt) {
+    const dim3 grid((unsigned)n_vt, (unsigned)((n + 16 * NCT - 1) / (16 * NCT)));
+    const dim3 block(64 * lg::WAVES);  // the kernel's wave count sets its k split and LDS ring
+    if (logits)
+        hipLaunchKernelGGL((vk_logits_argmax<NCT, true>), grid, block, 0, s, x, emb, logits, part, n, vocab, d, n_vt);
+    else
+        hipLaunchKernelGGL((vk_logits_argmax<NCT, false>), grid, block, 0, s, x, emb, logits, part, n, vocab, d, n_vt);
+}
+
+hipError_t launch_logits_argmax(hipStream_t s, const float* x, const float* emb, float* logits, float2* part,
+                                int* next, int n, int vocab, int d) {
+    if (n == 0) return hipSuccess;
+    // the kernel's loads assume whole 16-wide chunks per wave quarter and
+    // 16-byte aligned rows
+    if (vocab < 1 || d < logits_min_d() || d % logits_d_multiple() != 0) return hipErrorInvalidValue;
+    // whole chunks per wave, and enough of them to fill the ring
+    if (d % (16 * lg::WAVES) != 0 || d / (16 * lg::WAVES) < lg::NSLOT - 1) return hipErrorInvalidValue;
+    const int n_vt = logits_n_vt(vocab);
+    if ((n + 63) / 64 > 65535) return hipErrorInvalidValue;  // grid.y limit
+    if (n <= 16) go_logits<1>(s, x, emb, logits, part, n, vocab, d, n_vt);
+    else if (n <= 32) go_logits<2>(s, x, emb, logits, part, n, vocab, d, n_vt);
+    else if (n <= 48) go_logits<3>(s, x, emb, logits, part, n, vocab, d, n_vt);
+    else go_logits<4>(s, x, emb, logits, part, n, vocab, d, n_vt);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(vk_argmax_parts, dim3((unsigned)n), dim3(256), 0, s, part, n_vt, next);
     return hipGetLastError();
 }
 

@@ -108,6 +108,15 @@ hipError_t launch_add_f32(hipStream_t s, const float* a, const float* b, float* 
 hipError_t launch_embed_f32(hipStream_t s, const float* tok_emb, const float* pos_emb, const int* tokens,
                             const int* positions, int vocab, int n_pos, int d, int rows, float* out);
 hipError_t launch_argmax_f32(hipStream_t s, const float* logits, int rows, int cols, int* out);
+// Fused tied logits + argmax: d a multiple of 128 (an even number of 16-wide
+// k chunks in each of the kernel's four d quarters), rows of x and emb
+// 16-byte aligned; logits may be null. part holds rows * logits_n_vt(vocab)
+// float2.
+constexpr int logits_min_d() { return 128; }
+constexpr int logits_d_multiple() { return 128; }
+int logits_n_vt(int vocab);
+hipError_t launch_logits_argmax(hipStream_t s, const float* x, const float* emb, float* logits, float2* part,
+                                int* next, int n, int vocab, int d);
 }  // namespace vk
 
 struct vokra_hip_ctx;

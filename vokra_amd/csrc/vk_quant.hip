@@ -366,27 +366,6 @@ constexpr int NS = 3;                         // LDS stages
 constexpr int LAG = 3;                        // MFMA -> combine distance (tiles)
 }  // namespace gemm
 
-// Direct global -> LDS loads (global_load_lds_dwordx4 / _dword). M0 holds the
-// wave-uniform LDS base; lane l writes base + l * size. They are issued from
-// inline asm so the compiler does not fence every LDS read on them; their
-// completion is tracked by hand with vmcnt (loads retire in issue order).
-// Nothing else in the kernels that use them reads M0.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void vk_dma_b128(const void* g, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void vk_dma_b32(const void* g, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_base)
-                 : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-__device__ __forceinline__ uint32_t vk_lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
-
 // Wait until at most N of this thread's loads are in flight and every LDS
 // access has completed, then barrier.
 template <int N>

@@ -158,7 +158,7 @@ struct vokra_hip_decoder {
     DBuf tok_emb, pos_emb, lnpg, lnpb;
     vokra_hip_kv_t* kv = nullptr;
     DBuf ckh, ckl, cvh, cvl;  // cross K (fp16 hi/lo) and V^T per (stream, layer)
-    DBuf h, x, q, k, v, attn, f, logits, qh, ql, lens, kvidx, next, tk, tv, stage;
+    DBuf h, x, q, k, v, attn, f, logits, lpart, qh, ql, lens, kvidx, next, tk, tv, stage;
     vokra_hip_qact_t *qa_d = nullptr, *qa_f = nullptr;
     void release() {
         for (auto& L : layers) {
@@ -166,7 +166,7 @@ struct vokra_hip_decoder {
             for (QLin* w : {&L.q, &L.k, &L.v, &L.o, &L.cq, &L.ck, &L.cv, &L.co, &L.fc1, &L.fc2}) w->release(ctx);
         }
         for (DBuf* b : {&tok_emb, &pos_emb, &lnpg, &lnpb, &ckh, &ckl, &cvh, &cvl, &h, &x, &q, &k, &v, &attn, &f,
-                        &logits, &qh, &ql, &lens, &kvidx, &next, &tk, &tv, &stage})
+                        &logits, &lpart, &qh, &ql, &lens, &kvidx, &next, &tk, &tv, &stage})
             b->release(ctx);
         vokra_hip_kv_destroy(kv);
         kv = nullptr;
@@ -312,6 +312,7 @@ int dec_setup(vokra_hip_decoder* m, const vokra_hip_decoder_layer_t* layers, con
     for (DBuf* b : {&m->h, &m->x, &m->q, &m->k, &m->v, &m->attn}) SS_TRY(b->alloc(c, rd));
     SS_TRY(m->f.alloc(c, rows * ff * sizeof(float)));
     SS_TRY(m->logits.alloc(c, rows * m->vocab * sizeof(float)));
+    SS_TRY(m->lpart.alloc(c, rows * (size_t)vk::logits_n_vt((int)m->vocab) * sizeof(float2)));
     SS_TRY(m->qh.alloc(c, rows * d * 2));
     SS_TRY(m->ql.alloc(c, rows * d * 2));
     SS_TRY(m->lens.alloc(c, rows * sizeof(int)));
@@ -391,8 +392,15 @@ int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_
         SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_f, n, m->f.f(), act));
         SS_TRY(L.fc2.run(c, m->qa_f, m->h.f(), add_h));
     }
-    // ln_post, tied logits (decoder.rs:754-796), greedy argmax
+    // ln_post, then tied logits (decoder.rs:754-796) and greedy argmax in one
+    // pass over the embedding; the logits are written only when asked for
     SS_TRY(vokra_hip_layer_norm_f32_dev(c, m->h.f(), m->x.f(), n, d, m->lnpg.f(), m->lnpb.f(), kLnEps));
+    if (d % vk::logits_d_multiple() == 0) {
+        SS_HIP(vk::launch_logits_argmax(s, m->x.f(), m->tok_emb.f(), d_logits, (float2*)m->lpart.p, d_next, (int)n,
+                                        (int)m->vocab, (int)d),
+               "launch(vk_logits_argmax)");
+        return VOKRA_HIP_OK;
+    }
     float* lg = d_logits ? d_logits : m->logits.f();
     SS_TRY(vokra_hip_gemm_f32_dev(c, n, m->vocab, d, m->x.f(), m->tok_emb.f(), 1, nullptr, lg));
     return vokra_hip_argmax_f32_dev(c, lg, n, m->vocab, d_next);
@@ -609,7 +617,7 @@ int vokra_hip_decoder_step(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t n,
     memcpy(items.data() + 2 * n, positions, n * 4);
     int* dv = m->stage.i();
     SS_TRY(vokra_hip_memcpy_htod(c, dv, items.data(), 3 * n * 4));
-    SS_TRY(dec_step(m, n, dv, dv + n, dv + 2 * n, m->next.i(), m->logits.f()));
+    SS_TRY(dec_step(m, n, dv, dv + n, dv + 2 * n, m->next.i(), logits ? m->logits.f() : nullptr));
     size_t appended = 0;
     SS_TRY(vokra_hip_kv_status(c, m->kv, &appended));
     SS_TRY(vokra_hip_memcpy_dtoh(c, next_tokens, m->next.p, n * 4));

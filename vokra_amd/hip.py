@@ -208,6 +208,7 @@ def _declare(L):
     L.vokra_hip_encoder_encode.argtypes = [P, P, sz, f32p, f32p]
     L.vokra_hip_encoder_encode_dev.argtypes = [P, P, sz, P, P]
     L.vokra_hip_argmax_f32_dev.argtypes = [P, P, sz, sz, P]
+    L.vokra_hip_logits_argmax_dev.argtypes = [P, sz, sz, sz, P, P, P, P]
     L.vokra_hip_add_f32_dev.argtypes = [P, P, P, P, sz]
     L.vokra_hip_encoder_create.argtypes = [P, C.c_int, sz, sz, sz, sz, C.POINTER(PrenormLayer), f32p, f32p, sz,
                                            C.POINTER(P)]
@@ -845,6 +846,12 @@ class HipContext:
 
     def argmax_f32_dev(self, d_logits, rows, cols, d_out):
         _check(lib().vokra_hip_argmax_f32_dev(self._h, d_logits.ptr, rows, cols, d_out.ptr))
+
+    def logits_argmax_dev(self, rows, vocab, d, d_x, d_emb, d_logits, d_next):
+        """Tied logits emb[vocab, d] . x[rows, d] and the per-row greedy argmax in
+        one pass (decoder.rs:754-796 then sampler.rs:197-206); d_logits may be None."""
+        _check(lib().vokra_hip_logits_argmax_dev(self._h, rows, vocab, d, d_x.ptr, d_emb.ptr,
+                                                 None if d_logits is None else d_logits.ptr, d_next.ptr))
 
     # ---- attention ----------------------------------------------------------
     def attn_f32(self, q, k, v, n_head_q: int, n_head_kv: int = None, scale: float = None,
