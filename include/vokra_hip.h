@@ -489,6 +489,16 @@ void vokra_hip_decoder_destroy(vokra_hip_decoder_t *dec);
 int vokra_hip_decoder_set_encoder(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t stream, const float *enc);
 int vokra_hip_decoder_set_encoder_dev(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t stream,
                                       const float *d_enc);
+/* Precision of the cross-attention K/V reads. VOKRA_HIP_CROSS_F32 (default)
+ * keeps f32-level products: K and V are held as fp16 hi + lo pairs, the
+ * reference's f32 cross_attention (crates/vokra-models/src/whisper/nn.rs:
+ * 342-399, decoder.rs:492-510) to f32 rounding. VOKRA_HIP_CROSS_F16 reads the
+ * fp16 hi parts only: half the bytes of the step's largest stream, with K and
+ * V rounded to fp16 (relative 2^-11). A performance mode with no counterpart in
+ * the reference; it may be switched between steps (both parts stay stored). */
+#define VOKRA_HIP_CROSS_F32 0
+#define VOKRA_HIP_CROSS_F16 1
+int vokra_hip_decoder_set_cross_precision(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, int precision);
 /* Empties the self-KV cache of every stream. */
 int vokra_hip_decoder_reset(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec);
 /* One decode step of n streams (distinct): stream streams[i] feeds token

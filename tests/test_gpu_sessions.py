@@ -209,3 +209,35 @@ def test_decoder_rejections(ctx, oracle):
         hip.Decoder(ctx, W_Q4_0, 160, 2, 256, 10, 4, 8, 1, [dec_layer(ctx, g, W_Q4_0, 160, 256)],
                     np.zeros((10, 160), np.float32), np.zeros((4, 160), np.float32),
                     np.ones(160, np.float32), np.zeros(160, np.float32))
+
+
+def test_decoder_cross_f16_mode(ctx, oracle):
+    """The half-precision cross-attention mode (K/V read as fp16) stays within
+    the oracle bar, keeps batch == single-stream bit identity, and switching
+    back to F32 restores the F32 results bit for bit."""
+    print("[case] decoder cross f16", flush=True)
+    g = np.random.default_rng(42)
+    gpu, ref = make_decoder(ctx, oracle, g)
+    twin, _ = make_decoder(ctx, oracle, np.random.default_rng(42))
+    gpu.set_cross_precision(hip.CrossPrecision.F16)
+    twin.set_cross_precision(hip.CrossPrecision.F16)
+    tok, pos = [1, 2, 3, 4], [0, 0, 0, 0]
+    for step in range(4):
+        nxt, logits = gpu.step([0, 1, 2, 3], tok, pos, want_logits=True)
+        for i in range(4):
+            want, _ = ref.step(i, tok[i], pos[i])
+            ok, err, rms = within(logits[i], want)
+            assert ok, (step, i, err, rms)
+            n1, l1 = twin.step([i], [tok[i]], [pos[i]], want_logits=True)
+            assert np.array_equal(l1[0], logits[i]) and n1[0] == nxt[i]
+        tok, pos = [int(t) for t in nxt], [p + 1 for p in pos]
+    # F32 again: a fresh F32 session on the same history gives the same logits
+    gpu.set_cross_precision(hip.CrossPrecision.F32)
+    fresh, _ = make_decoder(ctx, oracle, np.random.default_rng(42))
+    gpu.reset()
+    for step in range(2):
+        a = gpu.step([0, 1], [5, 6], [step, step], want_logits=True)[1]
+        b = fresh.step([0, 1], [5, 6], [step, step], want_logits=True)[1]
+        assert np.array_equal(a, b)
+    with pytest.raises(hip.InvalidArgument):
+        gpu.set_cross_precision(7)

@@ -13,6 +13,10 @@
 // product, i.e. f32-level results, at 3x the fp16 MFMA rate. Inputs must stay
 // within the fp16 range (|x| < 65504 after scaling).
 //
+// With LO = false (the decoder's half-precision cross-attention mode) K and V
+// are taken as their fp16 hi parts only: two MFMAs per product (k_hi*q_hi +
+// k_hi*q_lo, v_hi*p_hi + v_hi*p_lo) and half the K/V bytes.
+//
 // Kernel shape: one workgroup per (64-query tile, head, batch); each of the 4
 // waves owns 16 queries. Both products are computed transposed,
 //   S^T = K . Q^T  (A = K tile from LDS, B = the wave's Q in registers)
@@ -85,7 +89,7 @@ __global__ __launch_bounds__(256) void vk_split_vt(const float* __restrict__ v, 
 }
 
 // ---------------------------------------------------------------------------
-template <int HD>
+template <int HD, bool LO>
 __global__ __launch_bounds__(256) void vk_flash_attn(
     const uint4* __restrict__ qh, const uint4* __restrict__ ql,    // [B][Tq][Hq*HD] fp16, scaled
     const uint4* __restrict__ kh, const uint4* __restrict__ kl,    // [B][Tkv][Hkv*HD] fp16
@@ -99,8 +103,9 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
     constexpr int VROW = KT + VPAD;  // halves per V^T tile row
     constexpr int KU4 = KT * HD / 8 / 256;  // uint4 per thread per K array
     constexpr int VU4 = HD * KT / 8 / 256;  // uint4 per thread per V^T array
-    __shared__ __align__(16) _Float16 lk[2][KT * KROW];   // K tile, hi / lo
-    __shared__ __align__(16) _Float16 lv[2][HD * VROW];   // V^T tile, hi / lo
+    constexpr int NP = LO ? 2 : 1;                         // fp16 parts of K and V in use
+    __shared__ __align__(16) _Float16 lk[NP][KT * KROW];  // K tile, hi (/ lo)
+    __shared__ __align__(16) _Float16 lv[NP][HD * VROW];  // V^T tile, hi (/ lo)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, lq = lane & 15;
     const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -142,7 +147,7 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
             const int t = min(kt * KT + r, tkv - 1);
             const size_t o = ((size_t)kb * tkv + t) * kw + (size_t)hk * HD / 8 + c;
             st.kh[i] = kh4[o];
-            st.kl[i] = kl4[o];
+            if (LO) st.kl[i] = kl4[o];
         }
 #pragma unroll
         for (int i = 0; i < VU4; ++i) {
@@ -150,7 +155,7 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
             const int r = idx / (KT / 8), c = idx % (KT / 8);
             const size_t o = (((size_t)kb * hkv + hk) * HD + r) * (t_pad / 8) + (size_t)kt * KT / 8 + c;
             st.vh[i] = vh4[o];
-            st.vl[i] = vl4[o];
+            if (LO) st.vl[i] = vl4[o];
         }
         return st;
     };
@@ -178,14 +183,14 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
             const int idx = tid + 256 * i;
             const int r = idx / (HD / 8), c = idx % (HD / 8);
             *reinterpret_cast<vk_u32x4*>(&lk[0][r * KROW + 8 * c]) = st.kh[i];
-            *reinterpret_cast<vk_u32x4*>(&lk[1][r * KROW + 8 * c]) = st.kl[i];
+            if (LO) *reinterpret_cast<vk_u32x4*>(&lk[NP - 1][r * KROW + 8 * c]) = st.kl[i];
         }
 #pragma unroll
         for (int i = 0; i < VU4; ++i) {
             const int idx = tid + 256 * i;
             const int r = idx / (KT / 8), c = idx % (KT / 8);
             *reinterpret_cast<vk_u32x4*>(&lv[0][r * VROW + 8 * c]) = st.vh[i];
-            *reinterpret_cast<vk_u32x4*>(&lv[1][r * VROW + 8 * c]) = st.vl[i];
+            if (LO) *reinterpret_cast<vk_u32x4*>(&lv[NP - 1][r * VROW + 8 * c]) = st.vl[i];
         }
         VK_LDS_BARRIER();
         st = load(min(kt + 1, n_tiles - 1));
@@ -199,12 +204,14 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
             for (int ks = 0; ks < KS; ++ks) {
                 const int off = (16 * n + lq) * KROW + 32 * ks + 8 * g;
                 const vk_h16x8 ah = *reinterpret_cast<const vk_h16x8*>(&lk[0][off]);
-                const vk_h16x8 al = *reinterpret_cast<const vk_h16x8*>(&lk[1][off]);
                 const vk_h16x8 bh = __builtin_bit_cast(vk_h16x8, qa_h[ks]);
                 const vk_h16x8 bl = __builtin_bit_cast(vk_h16x8, qa_l[ks]);
                 s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, s[n], 0, 0, 0);
                 s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, s[n], 0, 0, 0);
-                s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, s[n], 0, 0, 0);
+                if (LO) {
+                    const vk_h16x8 al = *reinterpret_cast<const vk_h16x8*>(&lk[NP - 1][off]);
+                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, s[n], 0, 0, 0);
+                }
             }
         }
         // ---- mask, online softmax (per query = per lane, across lanes g)
@@ -261,13 +268,15 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
                 const int k0 = 32 * ks + 4 * g;
                 const uint2 h0 = *reinterpret_cast<const uint2*>(&lv[0][row + k0]);
                 const uint2 h1 = *reinterpret_cast<const uint2*>(&lv[0][row + k0 + 16]);
-                const uint2 l0 = *reinterpret_cast<const uint2*>(&lv[1][row + k0]);
-                const uint2 l1 = *reinterpret_cast<const uint2*>(&lv[1][row + k0 + 16]);
                 const vk_h16x8 ah = __builtin_bit_cast(vk_h16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
-                const vk_h16x8 al = __builtin_bit_cast(vk_h16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
                 o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, o_acc[os], 0, 0, 0);
                 o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, o_acc[os], 0, 0, 0);
-                o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, o_acc[os], 0, 0, 0);
+                if (LO) {
+                    const uint2 l0 = *reinterpret_cast<const uint2*>(&lv[NP - 1][row + k0]);
+                    const uint2 l1 = *reinterpret_cast<const uint2*>(&lv[NP - 1][row + k0 + 16]);
+                    const vk_h16x8 al = __builtin_bit_cast(vk_h16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
+                    o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, o_acc[os], 0, 0, 0);
+                }
             }
         }
         VK_LDS_BARRIER();
@@ -304,18 +313,26 @@ hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, i
     return hipGetLastError();
 }
 
+template <int HD, bool LO>
+static void go_flash(hipStream_t s, dim3 grid, const void* qh, const void* ql, const void* kh, const void* kl,
+                     const void* vth, const void* vtl, float* out, int tq, int tkv, int t_pad, int hq, int hkv,
+                     int causal, int q_off, const int* kv_index) {
+    hipLaunchKernelGGL((vk_flash_attn<HD, LO>), grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
+                       (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv, t_pad,
+                       hq, hkv, causal, q_off, kv_index);
+}
+
 hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* ql, const void* kh, const void* kl,
                              const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
-                             int hq, int hkv, int causal, int q_off, const int* kv_index) {
+                             int hq, int hkv, int causal, int q_off, const int* kv_index, bool kv_lo) {
     const dim3 grid((tq + attn::QT - 1) / attn::QT, hq, batch);
-    if (hd == 64)
-        hipLaunchKernelGGL(vk_flash_attn<64>, grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
-                           (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv,
-                           t_pad, hq, hkv, causal, q_off, kv_index);
-    else
-        hipLaunchKernelGGL(vk_flash_attn<128>, grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
-                           (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv,
-                           t_pad, hq, hkv, causal, q_off, kv_index);
+    if (hd == 64) {
+        if (kv_lo) go_flash<64, true>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index);
+        else go_flash<64, false>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index);
+    } else {
+        if (kv_lo) go_flash<128, true>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index);
+        else go_flash<128, false>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index);
+    }
     return hipGetLastError();
 }
 

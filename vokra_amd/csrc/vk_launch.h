@@ -71,7 +71,8 @@ hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, i
                            void* vtl);
 hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* ql, const void* kh, const void* kl,
                              const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
-                             int hq, int hkv, int causal, int q_off, const int* kv_index = nullptr);
+                             int hq, int hkv, int causal, int q_off, const int* kv_index = nullptr,
+                             bool kv_lo = true);  // false: K/V fp16 hi parts only (kl, vtl unused)
 }  // namespace vk
 
 namespace vk {

@@ -158,6 +158,7 @@ struct vokra_hip_decoder {
     DBuf tok_emb, pos_emb, lnpg, lnpb;
     vokra_hip_kv_t* kv = nullptr;
     DBuf ckh, ckl, cvh, cvl;  // cross K (fp16 hi/lo) and V^T per (stream, layer)
+    int cross_precision = VOKRA_HIP_CROSS_F32;  // F16: cross-attention reads the hi parts only
     DBuf h, x, q, k, v, attn, f, logits, lpart, qh, ql, lens, kvidx, next, tk, tv, stage;
     vokra_hip_qact_t *qa_d = nullptr, *qa_f = nullptr;
     void release() {
@@ -382,7 +383,8 @@ int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_
         SS_HIP(vk::launch_split_rows(s, m->q.f(), n * d, scale, m->qh.p, m->ql.p), "launch(vk_split_rows q)");
         SS_HIP(vk::launch_flash_attn(s, (int)m->hd, m->qh.p, m->ql.p, m->ckh.p, m->ckl.p, m->cvh.p, m->cvl.p,
                                      m->attn.f(), (int)n, 1, (int)m->n_audio, (int)m->t_pad, (int)m->n_head,
-                                     (int)m->n_head, 0, 0, m->kvidx.i() + l * n),
+                                     (int)m->n_head, 0, 0, m->kvidx.i() + l * n,
+                                     m->cross_precision == VOKRA_HIP_CROSS_F32),
                "launch(vk_flash_attn cross)");
         SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->attn.f(), act));
         SS_TRY(L.co.run(c, m->qa_d, m->h.f(), add_h));
@@ -576,6 +578,15 @@ int vokra_hip_decoder_set_encoder(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, si
     SS_TRY(vokra_hip_memcpy_htod(c, m->stage.p, enc, m->n_audio * m->d * sizeof(float)));
     SS_TRY(dec_set_encoder(m, stream, m->stage.f()));
     return vokra_hip_synchronize(c);
+}
+
+int vokra_hip_decoder_set_cross_precision(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, int precision) {
+    if (!c || !m || m->ctx != c)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_set_cross_precision: bad argument");
+    if (precision != VOKRA_HIP_CROSS_F32 && precision != VOKRA_HIP_CROSS_F16)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_set_cross_precision: unknown precision");
+    m->cross_precision = precision;  // both fp16 parts are always stored: switching needs no re-upload
+    return VOKRA_HIP_OK;
 }
 
 int vokra_hip_decoder_reset(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m) {

@@ -76,6 +76,12 @@ class ActQuant(IntEnum):
     KQUANT = 2
 
 
+class CrossPrecision(IntEnum):
+    """Decoder cross-attention K/V reads (VOKRA_HIP_CROSS_*)."""
+    F32 = 0
+    F16 = 1
+
+
 _lib = None
 
 _F = C.POINTER(C.c_float)
@@ -209,6 +215,7 @@ def _declare(L):
     L.vokra_hip_encoder_encode_dev.argtypes = [P, P, sz, P, P]
     L.vokra_hip_argmax_f32_dev.argtypes = [P, P, sz, sz, P]
     L.vokra_hip_logits_argmax_dev.argtypes = [P, sz, sz, sz, P, P, P, P]
+    L.vokra_hip_decoder_set_cross_precision.argtypes = [P, P, C.c_int]
     L.vokra_hip_add_f32_dev.argtypes = [P, P, P, P, sz]
     L.vokra_hip_encoder_create.argtypes = [P, C.c_int, sz, sz, sz, sz, C.POINTER(PrenormLayer), f32p, f32p, sz,
                                            C.POINTER(P)]
@@ -631,6 +638,11 @@ class Decoder:
         _check(lib().vokra_hip_decoder_step(self._ctx._h, self._h, st.size, _ptr(st, C.c_int32), _ptr(tk, C.c_int32),
                                             _ptr(ps, C.c_int32), _ptr(nxt, C.c_int32), _ptr(lg, C.c_float)))
         return (nxt[:st.size], lg) if want_logits else nxt[:st.size]
+
+    def set_cross_precision(self, precision: "CrossPrecision"):
+        """CrossPrecision.F32 (default, f32-level cross-attention) or .F16 (K/V
+        read as fp16: half the bytes; a performance mode)."""
+        _check(lib().vokra_hip_decoder_set_cross_precision(self._ctx._h, self._h, int(precision)))
 
     def step_dev(self, n, d_streams, d_tokens, d_positions, d_next, d_logits=None):
         _check(lib().vokra_hip_decoder_step_dev(self._ctx._h, self._h, n, d_streams.ptr, d_tokens.ptr,
