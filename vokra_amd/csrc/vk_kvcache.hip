@@ -319,36 +319,74 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
         for (int g = 0; g < G; ++g) sc[g] = 0.0f;
         const uint4* kr = reinterpret_cast<const uint4*>(c.kq + slot * c.width + hcol);
         const uint4* vr = reinterpret_cast<const uint4*>(c.vq + slot * c.width + hcol);
-#pragma unroll 1
-        for (int b = 0; b < NB; ++b) {
-            const float d = vk_f16_to_f32_hw(c.kd[slot * c.row_blocks + hk * NB + b]);
-            const uint4 w0 = kr[2 * b], w1 = kr[2 * b + 1];
-            const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-            float kf[32];  // the block's dequantized keys (exact products)
+        float dv[NB];
+        if constexpr (G == 1) {
+            // one head: every load of the key's row is issued before any is
+            // used (one memory round trip after the page-table lookup)
+            uint4 kw[NB][2], vw[NB][2];
+            uint16_t kd16[NB], vd16[NB];
 #pragma unroll
-            for (int x = 0; x < 32; ++x) kf[x] = (float)(int8_t)((w[x >> 2] >> (8 * (x & 3))) & 0xff) * d;
+            for (int b = 0; b < NB; ++b) {
+                kw[b][0] = kr[2 * b];
+                kw[b][1] = kr[2 * b + 1];
+                vw[b][0] = vr[2 * b];
+                vw[b][1] = vr[2 * b + 1];
+                kd16[b] = c.kd[slot * c.row_blocks + hk * NB + b];
+                vd16[b] = c.vd[slot * c.row_blocks + hk * NB + b];
+            }
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float4* qg = reinterpret_cast<const float4*>(&lq[g][32 * b]);
-                float a = sc[g];
-#pragma unroll 2
+            for (int b = 0; b < NB; ++b) {
+                const float d = vk_f16_to_f32_hw(kd16[b]);
+                const uint32_t w[8] = {kw[b][0].x, kw[b][0].y, kw[b][0].z, kw[b][0].w,
+                                       kw[b][1].x, kw[b][1].y, kw[b][1].z, kw[b][1].w};
+                const float4* qg = reinterpret_cast<const float4*>(&lq[0][32 * b]);
+                float a = sc[0];
+#pragma unroll
                 for (int x4 = 0; x4 < 8; ++x4) {
                     const float4 q4 = qg[x4];
-                    a = fmaf(q4.x, kf[4 * x4], a);
-                    a = fmaf(q4.y, kf[4 * x4 + 1], a);
-                    a = fmaf(q4.z, kf[4 * x4 + 2], a);
-                    a = fmaf(q4.w, kf[4 * x4 + 3], a);
+                    const uint32_t wx = w[x4];
+                    a = fmaf(q4.x, (float)(int8_t)(wx & 0xff) * d, a);
+                    a = fmaf(q4.y, (float)(int8_t)((wx >> 8) & 0xff) * d, a);
+                    a = fmaf(q4.z, (float)(int8_t)((wx >> 16) & 0xff) * d, a);
+                    a = fmaf(q4.w, (float)(int8_t)(wx >> 24) * d, a);
                 }
-                sc[g] = a;
+                sc[0] = a;
+                *reinterpret_cast<uint4*>(&lv[tid][32 * b]) = vw[b][0];
+                *reinterpret_cast<uint4*>(&lv[tid][32 * b + 16]) = vw[b][1];
+                dv[b] = has ? vk_f16_to_f32_hw(vd16[b]) : 0.0f;
             }
-            // stage V quants and its scale product for the P.V pass
-            const uint4 v0 = vr[2 * b], v1 = vr[2 * b + 1];
-            *reinterpret_cast<uint4*>(&lv[tid][32 * b]) = v0;
-            *reinterpret_cast<uint4*>(&lv[tid][32 * b + 16]) = v1;
-        }
-        float dv[NB];
+        } else {
+#pragma unroll 1
+            for (int b = 0; b < NB; ++b) {
+                const float d = vk_f16_to_f32_hw(c.kd[slot * c.row_blocks + hk * NB + b]);
+                const uint4 w0 = kr[2 * b], w1 = kr[2 * b + 1];
+                const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                float kf[32];  // the block's dequantized keys (exact products)
 #pragma unroll
-        for (int b = 0; b < NB; ++b) dv[b] = has ? vk_f16_to_f32_hw(c.vd[slot * c.row_blocks + hk * NB + b]) : 0.0f;
+                for (int x = 0; x < 32; ++x) kf[x] = (float)(int8_t)((w[x >> 2] >> (8 * (x & 3))) & 0xff) * d;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float4* qg = reinterpret_cast<const float4*>(&lq[g][32 * b]);
+                    float a = sc[g];
+#pragma unroll 2
+                    for (int x4 = 0; x4 < 8; ++x4) {
+                        const float4 q4 = qg[x4];
+                        a = fmaf(q4.x, kf[4 * x4], a);
+                        a = fmaf(q4.y, kf[4 * x4 + 1], a);
+                        a = fmaf(q4.z, kf[4 * x4 + 2], a);
+                        a = fmaf(q4.w, kf[4 * x4 + 3], a);
+                    }
+                    sc[g] = a;
+                }
+                // stage V quants and its scale product for the P.V pass
+                const uint4 v0 = vr[2 * b], v1 = vr[2 * b + 1];
+                *reinterpret_cast<uint4*>(&lv[tid][32 * b]) = v0;
+                *reinterpret_cast<uint4*>(&lv[tid][32 * b + 16]) = v1;
+            }
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+                dv[b] = has ? vk_f16_to_f32_hw(c.vd[slot * c.row_blocks + hk * NB + b]) : 0.0f;
+        }
         // ---- chunk max per head
 #pragma unroll
         for (int g = 0; g < G; ++g) {
