@@ -471,6 +471,268 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
     }
 }
 
+// ---------------------------------------------------------------------------
+// Grouped-query decode attention on the matrix cores: head_dim 128 and G = 2..8
+// query heads per kv head (config 4 is G = 8). Same contract as vk_paged_attn
+// (one workgroup per (split, kv head, item), (m, l, O) partials for the
+// combine when split), f32-level numerics through fp16 hi/lo operands:
+//
+//   S^T[key][head] = sum_b d_k[key][b] * (K_b . (q_hi + q_lo))_b
+//     K quants are exact fp16 integers, so each block dot is the exact integer
+//     dot against the two fp16 halves of q * scale; the key's f16 block scale
+//     is applied to the block sum (v_mfma_f32_16x16x32_f16, keys on the 16-row
+//     side, heads on the 16-column side, padded to 16);
+//   O^T[dim][head] += V^T . (p * d_v)^T
+//     the V block scale of each key folds into P, split hi/lo; V^T comes from
+//     a per-wave LDS copy of the tile converted to fp16.
+//
+// Each wave owns the 32-key tiles j0 = k0 + 32 w + 128 i of the split and keeps
+// its own online softmax; the four states merge in wave order at the end.
+// Within a tile, MFMA row i of key subtile n is key 8 (i / 4) + 4 n + i % 4, so
+// lane (g = l / 16, head l % 16) ends up holding the scores of keys 8g .. 8g+7,
+// exactly the P^T operand slots 8g .. 8g+7 of the P.V product: no shuffles.
+namespace pg {
+constexpr int HD = 128, NB = HD / 32, KT = 32, WAVES = 4;
+constexpr int VROW = KT + 8;  // fp16 per V^T row in LDS (padded; rows stay 16-byte aligned)
+static_assert((VROW * 2) % 16 == 0, "16-byte LDS reads of V^T rows");
+}  // namespace pg
+
+typedef _Float16 vk_h16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 vk_h16x2_t __attribute__((ext_vector_type(2)));
+
+// Two signed bytes (selected by `sel` from {hi_src:lo_src}) -> two exact fp16:
+// 0x64uu with u = x + 128 is the fp16 1024 + u; subtracting 1152 leaves x.
+__device__ __forceinline__ uint32_t vk_i8pair_f16(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
+    const uint32_t t = __builtin_amdgcn_perm(hi_src, lo_src, sel) ^ 0x64806480u;
+    vk_h16x2_t h = __builtin_bit_cast(vk_h16x2_t, t);
+    h = h + (vk_h16x2_t){(_Float16)-1152.0f, (_Float16)-1152.0f};
+    return __builtin_bit_cast(uint32_t, h);
+}
+// eight signed bytes (little-endian in w) -> eight fp16 in order
+__device__ __forceinline__ vk_h16x8_t vk_i8x8_f16(uint2 w) {
+    uint4 r;
+    r.x = vk_i8pair_f16(0, w.x, 0x0c010c00u);
+    r.y = vk_i8pair_f16(0, w.x, 0x0c030c02u);
+    r.z = vk_i8pair_f16(0, w.y, 0x0c010c00u);
+    r.w = vk_i8pair_f16(0, w.y, 0x0c030c02u);
+    return __builtin_bit_cast(vk_h16x8_t, r);
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void vk_paged_attn_gqa(KvDev c, int layer, const int* __restrict__ streams,
+                                                         const int* __restrict__ lens, const float* __restrict__ q,
+                                                         float scale, int hq, int n_split, int keys_per_split,
+                                                         float* __restrict__ out, float* __restrict__ part_ml,
+                                                         float* __restrict__ part_o) {
+    using namespace pg;
+    static_assert(G >= 2 && G <= 16, "query heads per kv head");
+    __shared__ __align__(16) _Float16 lvt[WAVES][HD][VROW];  // per wave: V^T of its tile (reused by the merge)
+    __shared__ float lm[WAVES][16], ll[WAVES][16];
+    static_assert(sizeof(lvt) >= sizeof(vk_f32x4) * (WAVES - 1) * (HD / 16) * 64, "merge buffer fits");
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, hh = lane & 15;
+    const int split = blockIdx.x, hk = blockIdx.y, item = blockIdx.z;
+    const int s = streams[item];
+    const int len = min(lens[item], c.max_time);
+    const int k0 = split * keys_per_split, k1 = min(len, k0 + keys_per_split);
+    const size_t hcol = (size_t)hk * HD;
+
+    // q * scale of head hh (zero for padding heads) as the S^T B operand:
+    // lane (g, hh) holds dims 32b + 8g .. +7, split into fp16 hi + lo
+    vk_h16x8_t qh[NB], ql[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        if (hh < G) {
+            const float4* qp =
+                reinterpret_cast<const float4*>(q + ((size_t)item * hq + hk * G + hh) * HD + 32 * b + 8 * g);
+            const float4 u = qp[0], v = qp[1];
+            x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
+            x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float xs = x[i] * scale;
+            const _Float16 h = (_Float16)xs;
+            qh[b][i] = h;
+            ql[b][i] = (_Float16)(xs - (float)h);
+        }
+    }
+    float m_run = -INFINITY, l_run = 0.0f;
+    vk_f32x4 o[HD / 16];
+#pragma unroll
+    for (int et = 0; et < HD / 16; ++et) o[et] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int trow = layer * c.ppl;
+    const int va = lane & 7, vc = lane >> 3;  // V staging: keys 4va .. +3, dims 16vc .. +15
+
+    for (int j0 = k0 + KT * wave; j0 < k1; j0 += KT * WAVES) {
+        // slot of key j0 + kk, kk = lane % 32 (lanes 32..63 repeat lanes 0..31)
+        const int jk = j0 + (lane & 31);
+        const int pid = jk < k1 ? c.table[trow + jk / c.bs] : -1;
+        const int slot = pid >= 0 ? (int)kv_slot(c, pid, jk, s) : 0;  // slot 0: in bounds, masked below
+        const int has = pid >= 0 ? 1 : 0;
+
+        // ---- issue every load of the tile
+        uint2 kw[2][NB];  // K operand rows: subtile n, row hh <-> key 8 (hh / 4) + 4 n + hh % 4
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            const int sl = __shfl(slot, 8 * (hh >> 2) + 4 * n + (hh & 3), VK_WAVE);
+            const uint2* kr = reinterpret_cast<const uint2*>(c.kq + (size_t)sl * c.width + hcol);
+#pragma unroll
+            for (int b = 0; b < NB; ++b) kw[n][b] = kr[4 * b + g];
+        }
+        uint2 kds[8], vds[8];  // f16 block scales of keys 8g + j (j = 4n + r)
+        int kval[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int sl = __shfl(slot, 8 * g + j, VK_WAVE);
+            kval[j] = __shfl(has, 8 * g + j, VK_WAVE);
+            kds[j] = *reinterpret_cast<const uint2*>(c.kd + (size_t)sl * c.row_blocks + hk * NB);
+            vds[j] = *reinterpret_cast<const uint2*>(c.vd + (size_t)sl * c.row_blocks + hk * NB);
+        }
+        uint4 vw[4];  // V rows of keys 4va + t, dims 16vc .. +15
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int sl = __shfl(slot, 4 * va + t, VK_WAVE);
+            vw[t] = *reinterpret_cast<const uint4*>(c.vq + (size_t)sl * c.width + hcol + 16 * vc);
+        }
+
+        // ---- S^T = K . (q hi + lo)^T per key subtile, block scales applied per block
+        float sc[8];
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            vk_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const vk_h16x8_t a = vk_i8x8_f16(kw[n][b]);
+                vk_f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[b], d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[b], d, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint2 kd = kds[4 * n + r];
+                    const uint32_t bits = (b < 2 ? kd.x : kd.y) >> (16 * (b & 1));
+                    acc[r] = fmaf(vk_f16_to_f32_hw(bits & 0xffffu), d[r], acc[r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sc[4 * n + r] = kval[4 * n + r] ? acc[r] : -INFINITY;
+        }
+
+        // ---- online softmax of head hh over the tile's 32 keys
+        float mloc = sc[0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) mloc = fmaxf(mloc, sc[j]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, VK_WAVE));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, VK_WAVE));
+        const float m_new = fmaxf(m_run, mloc);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __expf(m_run - m_use);
+        float p[8], psum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            p[j] = __expf(sc[j] - m_use);
+            psum += p[j];
+        }
+        psum += __shfl_xor(psum, 16, VK_WAVE);
+        psum += __shfl_xor(psum, 32, VK_WAVE);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int et = 0; et < HD / 16; ++et)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[et][r] *= alpha;
+
+        // ---- V^T of the tile into this wave's LDS, as fp16 (keys 4va .. +3 of dim 16vc + x)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
+            const int cw = x >> 2, sb = x & 3;  // component and byte of dim x in each row's 16 bytes
+            const uint32_t w0 = cw == 0 ? vw[0].x : cw == 1 ? vw[0].y : cw == 2 ? vw[0].z : vw[0].w;
+            const uint32_t w1 = cw == 0 ? vw[1].x : cw == 1 ? vw[1].y : cw == 2 ? vw[1].z : vw[1].w;
+            const uint32_t w2 = cw == 0 ? vw[2].x : cw == 1 ? vw[2].y : cw == 2 ? vw[2].z : vw[2].w;
+            const uint32_t w3 = cw == 0 ? vw[3].x : cw == 1 ? vw[3].y : cw == 2 ? vw[3].z : vw[3].w;
+            const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + sb) << 16) | (uint32_t)sb;
+            uint2 h;
+            h.x = vk_i8pair_f16(w1, w0, sel);
+            h.y = vk_i8pair_f16(w3, w2, sel);
+            *reinterpret_cast<uint2*>(&lvt[wave][16 * vc + x][4 * va]) = h;
+        }
+
+        // ---- O^T += V^T . (p d_v)^T, one V block scale per pair of 16-dim tiles
+#pragma unroll
+        for (int vb = 0; vb < NB; ++vb) {
+            vk_h16x8_t bh, bl;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t bits = (vb < 2 ? vds[j].x : vds[j].y) >> (16 * (vb & 1));
+                const float pd = p[j] * vk_f16_to_f32_hw(bits & 0xffffu);
+                const _Float16 h = (_Float16)pd;
+                bh[j] = h;
+                bl[j] = (_Float16)(pd - (float)h);
+            }
+#pragma unroll
+            for (int e2 = 0; e2 < 2; ++e2) {
+                const int et = 2 * vb + e2;
+                const vk_h16x8_t a = *reinterpret_cast<const vk_h16x8_t*>(&lvt[wave][16 * et + hh][8 * g]);
+                o[et] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, o[et], 0, 0, 0);
+                o[et] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, o[et], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- merge the four waves (fixed order), then write
+    if (lane < 16) {
+        lm[wave][lane] = m_run;
+        ll[wave][lane] = l_run;
+    }
+    __syncthreads();  // all waves are done with their V^T tiles too
+    float M = lm[0][hh];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) M = fmaxf(M, lm[w][hh]);
+    const float M_use = M == -INFINITY ? 0.0f : M;
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) L += ll[w][hh] * __expf(lm[w][hh] - M_use);
+    const float f = __expf(m_run - M_use);
+    vk_f32x4* red = reinterpret_cast<vk_f32x4*>(&lvt[0][0][0]);
+    if (wave > 0) {
+#pragma unroll
+        for (int et = 0; et < HD / 16; ++et) {
+            vk_f32x4 t = o[et];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) t[r] *= f;
+            red[((wave - 1) * (HD / 16) + et) * 64 + lane] = t;
+        }
+    }
+    __syncthreads();
+    if (wave > 0 || hh >= G) return;
+    const int h = hk * G + hh;
+    const size_t pi = ((size_t)item * hq + h) * n_split + split;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+    for (int et = 0; et < HD / 16; ++et) {
+        vk_f32x4 t = o[et];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) t[r] *= f;
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) {
+            const vk_f32x4 u = red[((w - 1) * (HD / 16) + et) * 64 + lane];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) t[r] += u[r];
+        }
+        const int e = 16 * et + 4 * g;
+        if (n_split == 1)
+            *reinterpret_cast<float4*>(out + ((size_t)item * hq + h) * HD + e) =
+                make_float4(t[0] * inv, t[1] * inv, t[2] * inv, t[3] * inv);
+        else
+            *reinterpret_cast<float4*>(part_o + pi * HD + e) = make_float4(t[0], t[1], t[2], t[3]);
+    }
+    if (n_split > 1 && g == 0) {
+        part_ml[2 * pi] = M;
+        part_ml[2 * pi + 1] = L;
+    }
+}
+
 // Merges split partials: m = max m_s, O = sum O_s e^(m_s - m), l likewise.
 template <int HD>
 __global__ void vk_paged_attn_combine(int n_split, int hq, const float* __restrict__ part_ml,
@@ -566,6 +828,19 @@ template <int HD, int G>
 static void go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* streams, const int* lens,
                   const float* q, float scale, int hq, int hkv, int n_split, int kps, float* out, float* pml,
                   float* po) {
+    // head_dim 128 with several query heads per kv head: the matrix-core
+    // kernel (its slots travel through 32-bit lane shuffles; it moves q and
+    // O as float4)
+    const bool small_slots = (size_t)c.cap * c.bs * c.n_stream <= (size_t)INT32_MAX;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
+                           reinterpret_cast<uintptr_t>(po)) & 15) == 0;
+    if constexpr (HD == pg::HD && G >= 2) {
+        if (small_slots && aligned) {
+            hipLaunchKernelGGL((vk_paged_attn_gqa<G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams,
+                               lens, q, scale, hq, n_split, kps, out, pml, po);
+            return;
+        }
+    }
     hipLaunchKernelGGL((vk_paged_attn<HD, G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams, lens, q,
                        scale, hq, n_split, kps, out, pml, po);
 }
