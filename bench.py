@@ -98,8 +98,9 @@ def bench_q8_gemm(ctx, hip, steps, warmup, act):
 
 def bench_q4_gemv(ctx, hip, n, k=1280, ms=(1, 8, 64), stream_bytes=600 << 20):
     """Q4_0 decode GEMV: back-to-back launches over distinct weight
-    copies totalling > 512 MB, so weights come from HBM, not the 256 MB MALL.
-    GB/s counts the algorithmic bytes of one launch: Q4_0 weights
+    copies totalling > 512 MB, so weights come from HBM, not the 256 MB MALL;
+    then the same linears as one grouped launch (vokra_hip_linear_group_run).
+    GB/s counts the algorithmic bytes of one linear: Q4_0 weights
     n*(k/32)*18 + f32 activations m*k*4 + f32 outputs m*n*4."""
     rng = np.random.default_rng(7)
     wbytes = n * (k // 32) * 18
@@ -126,8 +127,23 @@ def bench_q4_gemv(ctx, hip, n, k=1280, ms=(1, 8, 64), stream_bytes=600 << 20):
         us = e0.elapsed_ms(e1) * 1e3 / len(Ws)
         nbytes = wbytes + m * k * 4 + m * n * 4
         gbs = nbytes / (us * 1e-6) / 1e9
+        # the same linears as one grouped launch (one output buffer each): the
+        # decode kernel's streaming rate without a launch per linear
+        outs = [hip.DeviceBuffer(ctx, m * n * 4) for _ in Ws]
+        group = hip.LinearGroup(ctx, Ws, outs)
+        group.run(qa)
+        ctx.synchronize()
+        e0.record()
+        for _ in range(3):
+            group.run(qa)
+        e1.record()
+        gus = e0.elapsed_ms(e1) * 1e3 / (3 * len(Ws))
+        ggbs = nbytes / (gus * 1e-6) / 1e9
+        del group, outs
         res[f"M{m}"] = {"us_per_launch": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
-                        "frac_hbm": round(gbs / PEAK["hbm_gbs"], 4)}
+                        "frac_hbm": round(gbs / PEAK["hbm_gbs"], 4),
+                        "grouped": {"us_per_linear": round(gus, 3), "gbs": round(ggbs, 1),
+                                    "frac_hbm": round(ggbs / PEAK["hbm_gbs"], 4)}}
     ctx.synchronize()
     del Ws
     return {"N": n, "K": k, "weight_copies": copies, **res}

@@ -202,6 +202,22 @@ int vokra_hip_qact_quantize_dev(vokra_hip_ctx_t *ctx, vokra_hip_qact_t *qa, size
 int vokra_hip_gemm_qact_dev(vokra_hip_ctx_t *ctx, const vokra_hip_qweight_t *w, const vokra_hip_qact_t *qa,
                             const float *d_bias, float *d_out);
 
+/* A fixed set of decode linears over the same activations, run as ONE launch:
+ * count (1..65535) block-format weights of one dtype and one k, each with its
+ * own bias (d_biases NULL, or per-entry NULL = no bias) and output [m, n_i]
+ * (device pointers, kept by the group). Every output is bit-identical to
+ * vokra_hip_gemm_qact_dev of the same weight. Rows m <= 64 run as one decode-
+ * kernel launch over a device descriptor table (any mix of n); larger m falls
+ * back to one block-GEMM launch per linear. No counterpart in the reference
+ * (it issues one gemm_q_f32 per linear, compute.rs:943-963): it serves callers
+ * that apply many linears to one batch (q/k/v, heads, expert groups) and
+ * streams their weights at HBM rate instead of paying one launch each. */
+typedef struct vokra_hip_linear_group vokra_hip_linear_group_t;
+int vokra_hip_linear_group_create(vokra_hip_ctx_t *ctx, size_t count, const vokra_hip_qweight_t *const *weights,
+                                  const float *const *d_biases, float *const *d_outs, vokra_hip_linear_group_t **out);
+int vokra_hip_linear_group_run(vokra_hip_ctx_t *ctx, vokra_hip_linear_group_t *group, const vokra_hip_qact_t *qa);
+void vokra_hip_linear_group_destroy(vokra_hip_linear_group_t *group);
+
 /* ---- f32 GEMM / GEMV and row kernels -------------------------------------- */
 
 /* out[m, n] = bias[n] + a[m, k] . b[k, n], f32 (matrix cores in f32: exact

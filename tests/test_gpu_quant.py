@@ -264,3 +264,49 @@ def test_gemm_q_rejections(ctx):
         ctx.gemm_q_f32(0, 16, 32, np.zeros(0), wq, hip.WDtype.Q8_0)
     with pytest.raises(hip.UnsupportedOp):
         ctx.gemm_q_f32(1, 16, 32, np.zeros(32), wq, 99)
+
+
+@pytest.mark.parametrize("wd,m", [(hip.WDtype.Q4_0, 1), (hip.WDtype.Q4_0, 37), (hip.WDtype.Q8_0, 64),
+                                  (hip.WDtype.Q8_0, 65)])
+def test_linear_group_equals_single_linears(ctx, wd, m):
+    """One grouped launch over linears of different widths (some with bias)
+    gives the same bits as gemm_qact_dev per weight; m = 65 takes the
+    per-linear block-GEMM route."""
+    print(f"[case] linear group wd={int(wd)} m={m}", flush=True)
+    g = np.random.default_rng(int(wd) * 100 + m)
+    k = 256
+    mode = hip.KvQuant.Q4_0 if wd == hip.WDtype.Q4_0 else hip.KvQuant.Q8_0
+    ns = [48, 1280, 16, 333, 512]
+    Ws = [ctx.upload_qweight(wd, n, k, ctx.quantize_bytes(mode, (g.standard_normal((n, k)) * 0.05).astype(np.float32)))
+          for n in ns]
+    biases = [None if i % 2 else hip.DeviceBuffer.from_array(ctx, g.standard_normal(n).astype(np.float32))
+              for i, n in enumerate(ns)]
+    a = g.standard_normal((m, k)).astype(np.float32)
+    qa = ctx.qact(m, k)
+    qa.quantize(m, hip.DeviceBuffer.from_array(ctx, a))
+    outs = [hip.DeviceBuffer(ctx, m * n * 4) for n in ns]
+    group = hip.LinearGroup(ctx, Ws, outs, biases)
+    group.run(qa)
+    got = [o.download(np.float32, m * n) for o, n in zip(outs, ns)]
+    for W, b, n, gv in zip(Ws, biases, ns, got):
+        d_o = hip.DeviceBuffer(ctx, m * n * 4)
+        ctx.gemm_qact_dev(W, qa, d_o, d_bias=b)
+        assert np.array_equal(gv.view(np.uint32), d_o.download(np.float32, m * n).view(np.uint32)), n
+
+
+def test_linear_group_rejections(ctx):
+    g = np.random.default_rng(3)
+    k = 256
+    w8 = ctx.upload_qweight(hip.WDtype.Q8_0, 32, k, ctx.quantize_bytes(hip.KvQuant.Q8_0, g.standard_normal((32, k))))
+    w4 = ctx.upload_qweight(hip.WDtype.Q4_0, 32, k, ctx.quantize_bytes(hip.KvQuant.Q4_0, g.standard_normal((32, k))))
+    w8b = ctx.upload_qweight(hip.WDtype.Q8_0, 32, 512, ctx.quantize_bytes(hip.KvQuant.Q8_0, g.standard_normal((32, 512))))
+    o = hip.DeviceBuffer(ctx, 64 * 32 * 4)
+    with pytest.raises(hip.InvalidArgument, match="differs from weight 0"):
+        hip.LinearGroup(ctx, [w8, w4], [o, o])
+    with pytest.raises(hip.InvalidArgument, match="differs from weight 0"):
+        hip.LinearGroup(ctx, [w8, w8b], [o, o])
+    group = hip.LinearGroup(ctx, [w8], [o])
+    qa = ctx.qact(4, 512)
+    qa.quantize(4, hip.DeviceBuffer.from_array(ctx, g.standard_normal((4, 512)).astype(np.float32)))
+    with pytest.raises(hip.InvalidArgument, match="activation k=512"):
+        group.run(qa)

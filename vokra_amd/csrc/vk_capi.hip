@@ -10,6 +10,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
+#include <new>
 #include <string>
 #include <utility>
 #include <vector>
@@ -1596,6 +1598,102 @@ int vokra_hip_qact_quantize_dev(vokra_hip_ctx_t* c, vokra_hip_qact_t* qa, size_t
 int vokra_hip_gemm_qact_dev(vokra_hip_ctx_t* c, const vokra_hip_qweight_t* w, const vokra_hip_qact_t* qa,
                             const float* d_bias, float* d_out) {
     return vk::gemm_qact_epi(c, w, qa, d_bias, d_out, VkEpi{nullptr, 0});
+}
+
+// ---- grouped decode linears ---------------------------------------------------
+
+struct vokra_hip_linear_group {
+    vokra_hip_ctx* ctx = nullptr;
+    size_t k = 0, nb = 0, n_max = 0;
+    int wdtype = 0;
+    std::vector<const vokra_hip_qweight*> ws;
+    std::vector<const float*> biases;
+    std::vector<float*> outs;
+    DevBuf desc;  // VkGemvLin[count], read by the decode kernel
+};
+
+int vokra_hip_linear_group_create(vokra_hip_ctx_t* c, size_t count, const vokra_hip_qweight_t* const* weights,
+                                  const float* const* d_biases, float* const* d_outs, vokra_hip_linear_group_t** out) {
+    if (!c || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "linear_group_create: NULL argument");
+    *out = nullptr;
+    if (count == 0 || count > 65535)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "linear_group_create: count %zu outside 1..65535", count);
+    if (!weights || !d_outs) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "linear_group_create: NULL list");
+    std::vector<VkGemvLin> lins(count);
+    size_t n_max = 0;
+    for (size_t i = 0; i < count; ++i) {
+        const vokra_hip_qweight* w = weights[i];
+        if (!w || !d_outs[i]) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "linear_group_create: NULL entry %zu", i);
+        if (w->ctx != c)
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "linear_group_create: weight %zu belongs to another context", i);
+        if (w->kquant || !w->has_gemv)
+            return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP,
+                        "linear_group_create: weight %zu has no decode layout (Q4_0 / Q8_0 with k %% 128 == 0)", i);
+        if (w->wdtype != weights[0]->wdtype || w->k != weights[0]->k)
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                        "linear_group_create: weight %zu differs from weight 0 in dtype or k", i);
+        if (!fits_int(w->n)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "linear_group_create: n exceeds int32");
+        lins[i] = {(const uint4*)w->gq.p, (const uint2*)w->gsc.p, d_biases ? d_biases[i] : nullptr, d_outs[i],
+                   {nullptr, 0}, (int)w->n};
+        n_max = std::max(n_max, w->n);
+    }
+    VK_TRY(set_dev(c), "hipSetDevice");
+    vokra_hip_linear_group* g = new (std::nothrow) vokra_hip_linear_group;
+    if (!g) return fail(VOKRA_HIP_ERROR_OTHER, "linear_group_create: out of host memory");
+    g->ctx = c;
+    g->k = weights[0]->k;
+    g->nb = weights[0]->nb;
+    g->n_max = n_max;
+    g->wdtype = weights[0]->wdtype;
+    g->ws.assign(weights, weights + count);
+    g->biases.resize(count);
+    for (size_t i = 0; i < count; ++i) g->biases[i] = d_biases ? d_biases[i] : nullptr;
+    g->outs.assign(d_outs, d_outs + count);
+    hipError_t e = g->desc.ensure(count * sizeof(VkGemvLin));
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(g->desc.p, lins.data(), count * sizeof(VkGemvLin), hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        g->desc.release();
+        delete g;
+        return fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, "linear_group_create: %s", hipGetErrorString(e));
+    }
+    *out = g;
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_linear_group_run(vokra_hip_ctx_t* c, vokra_hip_linear_group_t* g, const vokra_hip_qact_t* qa) {
+    if (!c || !g || !qa) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "linear_group_run: NULL argument");
+    if (g->ctx != c || qa->ctx != c)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "linear_group_run: group/activations belong to another context");
+    if (qa->m == 0) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "linear_group_run: activations were never quantized");
+    if (qa->k != g->k)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "linear_group_run: activation k=%zu != weight k=%zu", qa->k, g->k);
+    if (qa->act_quant == VOKRA_HIP_ACT_KQUANT)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "linear_group_run: block-format weights need AMAX127 or POW2 activations");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    if (qa->m > kGemvMaxM || !c->decode_kernel) {  // prefill rows: the block GEMM, one launch per linear
+        for (size_t i = 0; i < g->ws.size(); ++i) {
+            int st = run_gemm_qact(c, g->ws[i], qa, g->biases[i], g->outs[i]);
+            if (st) return st;
+        }
+        return VOKRA_HIP_OK;
+    }
+    VK_TRY(vk::launch_gemv_qblock_group(c->stream, wd_kv_mode(g->wdtype), qa->act_quant == VOKRA_HIP_ACT_POW2,
+                                        (const uint4*)qa->frag.p, (const float*)qa->scale.p, (const float*)qa->gsum.p,
+                                        (const VkGemvLin*)g->desc.p, (int)g->ws.size(), (int)g->n_max, (int)qa->m,
+                                        (int)g->nb, (int)qa->m_pad),
+           "launch(vk_gemv_qblock group)");
+    return VOKRA_HIP_OK;
+}
+
+void vokra_hip_linear_group_destroy(vokra_hip_linear_group_t* g) {
+    if (!g) return;
+    (void)hipSetDevice(g->ctx->device);
+    (void)hipStreamSynchronize(g->ctx->stream);
+    g->desc.release();
+    delete g;
 }
 
 // ---- Whisper front end ------------------------------------------------------

@@ -128,12 +128,14 @@ struct GemvSet {
     VkGemvLin lin[3];
 };
 
-template <int MODE, bool POW2>
+// DEV: the linears come from a device array (any count, one per grid z) rather
+// than the kernel arguments.
+template <int MODE, bool POW2, bool DEV>
 __global__ __launch_bounds__(256) void vk_gemv_qblock(
     const uint4* __restrict__ afrag, const float* __restrict__ ascale, const float* __restrict__ asum,
-    const GemvSet set, int m, int nb, int m_pad) {
+    const GemvSet set, const VkGemvLin* __restrict__ dlins, int m, int nb, int m_pad) {
     using namespace gemv;
-    const VkGemvLin& lin = set.lin[blockIdx.z];
+    const VkGemvLin lin = DEV ? dlins[blockIdx.z] : set.lin[blockIdx.z];
     const uint4* __restrict__ wq4 = lin.wq4;
     const uint2* __restrict__ wsc = lin.wsc;
     const int n = lin.n;
@@ -252,12 +254,12 @@ hipError_t launch_repack_w_gemv(hipStream_t s, int mode, const uint8_t* wq, int 
     return hipGetLastError();
 }
 
-template <int MODE, bool POW2>
+template <int MODE, bool POW2, bool DEV>
 static hipError_t go(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum, const GemvSet& set,
-                     int n_lin, int n_max, int m, int nb, int m_pad) {
+                     const VkGemvLin* dlins, int n_lin, int n_max, int m, int nb, int m_pad) {
     const int n_tiles = (n_max + 15) / 16, m_tiles = (m + 15) / 16;
-    hipLaunchKernelGGL((vk_gemv_qblock<MODE, POW2>), dim3(n_tiles, m_tiles, n_lin), dim3(256), 0, s, afrag, ascale,
-                       asum, set, m, nb, m_pad);
+    hipLaunchKernelGGL((vk_gemv_qblock<MODE, POW2, DEV>), dim3(n_tiles, m_tiles, n_lin), dim3(256), 0, s, afrag,
+                       ascale, asum, set, dlins, m, nb, m_pad);
     return hipGetLastError();
 }
 
@@ -272,10 +274,23 @@ hipError_t launch_gemv_qblock(hipStream_t s, int mode, bool pow2, const uint4* a
     }
     if (n_max < 1) return hipSuccess;
     if (mode == 1)
-        return pow2 ? go<1, true>(s, afrag, ascale, asum, set, n_lin, n_max, m, nb, m_pad)
-                    : go<1, false>(s, afrag, ascale, asum, set, n_lin, n_max, m, nb, m_pad);
-    return pow2 ? go<3, true>(s, afrag, ascale, asum, set, n_lin, n_max, m, nb, m_pad)
-                : go<3, false>(s, afrag, ascale, asum, set, n_lin, n_max, m, nb, m_pad);
+        return pow2 ? go<1, true, false>(s, afrag, ascale, asum, set, nullptr, n_lin, n_max, m, nb, m_pad)
+                    : go<1, false, false>(s, afrag, ascale, asum, set, nullptr, n_lin, n_max, m, nb, m_pad);
+    return pow2 ? go<3, true, false>(s, afrag, ascale, asum, set, nullptr, n_lin, n_max, m, nb, m_pad)
+                : go<3, false, false>(s, afrag, ascale, asum, set, nullptr, n_lin, n_max, m, nb, m_pad);
+}
+
+hipError_t launch_gemv_qblock_group(hipStream_t s, int mode, bool pow2, const uint4* afrag, const float* ascale,
+                                    const float* asum, const VkGemvLin* d_lins, int n_lin, int n_max, int m, int nb,
+                                    int m_pad) {
+    if (n_lin < 1 || n_lin > 65535 || m < 1 || !d_lins) return hipErrorInvalidValue;
+    if (n_max < 1) return hipSuccess;
+    const GemvSet none = {};
+    if (mode == 1)
+        return pow2 ? go<1, true, true>(s, afrag, ascale, asum, none, d_lins, n_lin, n_max, m, nb, m_pad)
+                    : go<1, false, true>(s, afrag, ascale, asum, none, d_lins, n_lin, n_max, m, nb, m_pad);
+    return pow2 ? go<3, true, true>(s, afrag, ascale, asum, none, d_lins, n_lin, n_max, m, nb, m_pad)
+                : go<3, false, true>(s, afrag, ascale, asum, none, d_lins, n_lin, n_max, m, nb, m_pad);
 }
 
 }  // namespace vk

@@ -52,6 +52,11 @@ hipError_t launch_repack_w_gemv(hipStream_t s, int mode, const uint8_t* wq, int 
 // n_lin (1..3) linears over the same activations, one launch.
 hipError_t launch_gemv_qblock(hipStream_t s, int mode, bool pow2, const uint4* afrag, const float* ascale,
                               const float* asum, const VkGemvLin* lins, int n_lin, int m, int nb, int m_pad);
+// n_lin (1..65535) linears described by a device array d_lins, one launch;
+// n_max is the largest n among them.
+hipError_t launch_gemv_qblock_group(hipStream_t s, int mode, bool pow2, const uint4* afrag, const float* ascale,
+                                    const float* asum, const VkGemvLin* d_lins, int n_lin, int n_max, int m, int nb,
+                                    int m_pad);
 }  // namespace vk
 
 namespace vk {

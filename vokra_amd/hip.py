@@ -168,6 +168,10 @@ def _declare(L):
     L.vokra_hip_qact_free.restype = None
     L.vokra_hip_qact_quantize_dev.argtypes = [P, P, sz, P, C.c_int]
     L.vokra_hip_gemm_qact_dev.argtypes = [P, P, P, P, P]
+    L.vokra_hip_linear_group_create.argtypes = [P, sz, C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P)]
+    L.vokra_hip_linear_group_run.argtypes = [P, P, P]
+    L.vokra_hip_linear_group_destroy.argtypes = [P]
+    L.vokra_hip_linear_group_destroy.restype = None
     i32p = C.POINTER(C.c_int32)
     L.vokra_hip_kv_create.argtypes = [P, sz, sz, sz, sz, sz, sz, C.c_int, C.POINTER(P)]
     L.vokra_hip_kv_destroy.argtypes = [P]
@@ -443,6 +447,35 @@ class Graph:
         try:
             if getattr(self, "_h", None) and _ctx_alive(self):
                 lib().vokra_hip_graph_destroy(self._h)
+        except Exception:
+            pass
+
+
+class LinearGroup:
+    """A fixed set of decode linears over one activation batch, run as one launch
+    (vokra_hip_linear_group_*): outputs equal gemm_qact_dev of each weight."""
+
+    def __init__(self, ctx: "HipContext", weights, d_outs, d_biases=None):
+        n = len(weights)
+        if len(d_outs) != n or (d_biases is not None and len(d_biases) != n):
+            raise InvalidArgument("linear group: weights, outputs and biases differ in length")
+        self.ctx = ctx
+        self._keep = (list(weights), list(d_outs), None if d_biases is None else list(d_biases))
+        ws = (C.c_void_p * n)(*[w._h for w in weights])
+        outs = (C.c_void_p * n)(*[d.ptr for d in d_outs])
+        bs = None if d_biases is None else (C.c_void_p * n)(*[None if b is None else b.ptr for b in d_biases])
+        h = C.c_void_p()
+        _check(lib().vokra_hip_linear_group_create(ctx._h, n, ws, bs, outs, C.byref(h)))
+        self._h = h
+
+    def run(self, qa: "QAct"):
+        _check(lib().vokra_hip_linear_group_run(self.ctx._h, self._h, qa._h))
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None) and self._h.value and _ctx_alive(self):
+                lib().vokra_hip_linear_group_destroy(self._h)
+                self._h = C.c_void_p()
         except Exception:
             pass
 
