@@ -31,7 +31,7 @@ def dot_bound(a, b, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 1, 1), (3, 5, 7), (64, 64, 16), (65, 130, 33), (200, 51, 1280),
-                                   (17, 300, 2048)])
+                                   (17, 300, 2048), (130, 260, 96), (257, 128, 1280), (1, 4, 32)])
 def test_gemm_f32(ctx, oracle, m, n, k):
     print(f"[case] gemm_f32 {m}x{n}x{k}", flush=True)
     g = np.random.default_rng(m * 31 + n * 7 + k)
@@ -44,6 +44,23 @@ def test_gemm_f32(ctx, oracle, m, n, k):
     assert np.all(np.abs(got - exact) <= bound)
     want = oracle.gemm_f32(m, n, k, a, b, bias)
     assert np.all(np.abs(want - exact) <= bound)
+
+
+@pytest.mark.parametrize("m,n,k", [(100, 77, 64), (3000, 1280, 384), (5, 402, 400)])
+def test_gemm_f32_b_transposed_tiled(ctx, m, n, k):
+    """B stored [n, k] (weights [out, in]) through the tiled kernel (k % 16 == 0),
+    ragged m and n; GELU epilogue path via the bias-free product."""
+    print(f"[case] gemm_f32 b^T tiled {m}x{n}x{k}", flush=True)
+    g = np.random.default_rng(m + n + k)
+    a = g.standard_normal((m, k)).astype(np.float32)
+    e = (g.standard_normal((n, k)) * 0.05).astype(np.float32)
+    bias = g.standard_normal(n).astype(np.float32)
+    d_a, d_e, d_b = (hip.DeviceBuffer.from_array(ctx, x) for x in (a, e, bias))
+    d_o = hip.DeviceBuffer(ctx, m * n * 4)
+    ctx.gemm_f32_dev(m, n, k, d_a, d_e, d_o, d_bias=d_b, b_trans=True)
+    got = d_o.download(np.float32, m * n).reshape(m, n)
+    exact = a.astype(np.float64) @ e.astype(np.float64).T + bias
+    assert np.all(np.abs(got - exact) <= dot_bound(a, e.T, k + 1) + U * np.abs(bias))
 
 
 def test_gemm_f32_b_transposed_dev(ctx):

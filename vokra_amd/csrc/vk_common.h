@@ -193,12 +193,16 @@ __device__ __forceinline__ float vk_ln_apply(float x, float2 st, float g, float 
 // Nothing else in the kernels that use them reads M0.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
+// lds_base must be wave-uniform; it is passed through readfirstlane so that M0
+// is always written from a scalar register (free when it already is one).
 __device__ __forceinline__ void vk_dma_b128(const void* g, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base)
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_base);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0v)
                  : "memory", "m0");
 }
 __device__ __forceinline__ void vk_dma_b32(const void* g, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_base)
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_base);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m0v)
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop

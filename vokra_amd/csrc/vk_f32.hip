@@ -96,6 +96,120 @@ __global__ __launch_bounds__(256) void vk_gemm_f32(const float* __restrict__ a, 
             }
 }
 
+__device__ __forceinline__ float vk_f4c(const float4& v, int s) {
+    return s == 0 ? v.x : (s == 1 ? v.y : (s == 2 ? v.z : v.w));
+}
+
+// Tiled GEMM for K % 16 == 0: 128 x 128 workgroup tiles (four 64 x 64 waves),
+// K in 16-wide stages moved global -> LDS by direct loads through a ring of
+// three stages (two ahead of the MFMAs), XCD-aware tile order. Fragments of
+// v_mfma_f32_16x16x4f32 are read as float4: lane group g = l / 16 holds k =
+// 4g .. 4g+3 of the stage and MFMA s takes component s, so one 16-byte LDS read
+// feeds four MFMAs (for BT = false the B values come as four 4-byte reads).
+// Rows / columns past M / N read the last valid one (in bounds, discarded).
+namespace g32f {
+constexpr int TM = 128, TN = 128, KC = 16, NS = 3, N_XCD = 8;
+}
+
+template <bool BT>
+__global__ __launch_bounds__(256, 2) void vk_gemm_f32_tiled(const float* __restrict__ a, const float* __restrict__ b,
+                                                            const float* __restrict__ bias, VkEpi epi, float* out,
+                                                            int m, int n, int k) {
+    using namespace g32f;
+    __shared__ __align__(16) float la[NS][TM * KC];  // [row][k], 8 KiB per stage
+    __shared__ __align__(16) float lb[NS][TN * KC];  // BT: [col][k]; else [k][col]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int tiles_m = (m + TM - 1) / TM, tiles_n = (n + TN - 1) / TN, tiles = tiles_m * tiles_n;
+    const int L = blockIdx.x;
+    const int per_xcd = tiles / N_XCD;
+    const int t = (per_xcd * N_XCD == tiles) ? (L % N_XCD) * per_xcd + L / N_XCD : L;
+    const int mt = t % tiles_m, nt = t / tiles_m;
+    const int m0 = mt * TM, n0 = nt * TN;
+
+    // direct loads: each wave moves 2 KiB of A and 2 KiB of B per stage (two
+    // 1 KiB instructions each); lane l of instruction i lands at +16 l
+    const float* asrc[2];
+    const float* bsrc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = 16 * (2 * wave + i) + (lane >> 2);  // A row of the tile (16 rows x 64 B per KiB)
+        asrc[i] = a + (size_t)min(m0 + r, m - 1) * k + 4 * (lane & 3);
+        if (BT) {
+            bsrc[i] = b + (size_t)min(n0 + r, n - 1) * k + 4 * (lane & 3);
+        } else {
+            const int kr = 2 * (2 * wave + i) + (lane >> 5);          // k row of the stage (2 rows x 512 B per KiB)
+            const int cq = min(n0 / 4 + (lane & 31), n / 4 - 1);      // column quad (n % 4 == 0)
+            bsrc[i] = b + (size_t)kr * n + 4 * cq;
+        }
+    }
+    // wave-uniform LDS destinations (M0 takes a scalar register)
+    const uint32_t la0 = __builtin_amdgcn_readfirstlane(vk_lds_addr(&la[0][0]) + wave * 2048);
+    const uint32_t lb0 = __builtin_amdgcn_readfirstlane(vk_lds_addr(&lb[0][0]) + wave * 2048);
+    constexpr uint32_t STAGE = TM * KC * 4;
+    auto issue = [&](int kc, int buf) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            vk_dma_b128(asrc[i] + kc, la0 + buf * STAGE + i * 1024);
+            vk_dma_b128(BT ? bsrc[i] + kc : bsrc[i] + (size_t)kc * n, lb0 + buf * STAGE + i * 1024);
+        }
+    };
+    vk_f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int nk = k / KC;  // >= 2
+    issue(0, 0);
+    issue(KC, 1);
+    int buf = 0, nbuf = 2;
+#pragma unroll 1
+    for (int kc = 0; kc < nk; ++kc) {
+        // this thread's stage kc has landed (stage kc+1 may be in flight), then
+        // every wave's has: the buffer of stage kc-1 is free for kc+2
+        if (kc + 1 < nk) asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kc + 2 < nk) issue((kc + 2) * KC, nbuf);
+        float4 av[4];
+        float bv[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            av[i] = *reinterpret_cast<const float4*>(&la[buf][(wm * 64 + 16 * i + l16) * KC + 4 * g]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = wn * 64 + 16 * j + l16;
+            if (BT) {
+                const float4 v = *reinterpret_cast<const float4*>(&lb[buf][col * KC + 4 * g]);
+                bv[j][0] = v.x; bv[j][1] = v.y; bv[j][2] = v.z; bv[j][3] = v.w;
+            } else {
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) bv[j][s2] = lb[buf][(4 * g + s2) * TN + col];
+            }
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vk_f4c(av[i], s2), bv[j][s2], acc[i][j], 0, 0, 0);
+        buf = buf == NS - 1 ? 0 : buf + 1;
+        nbuf = nbuf == NS - 1 ? 0 : nbuf + 1;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int gm = m0 + wm * 64 + 16 * i + 4 * g + r, gn = n0 + wn * 64 + 16 * j + l16;
+                if (gm < m && gn < n) {
+                    const size_t o = (size_t)gm * n + gn;
+                    out[o] = vk_epi_apply(bias ? bias[gn] + acc[i][j][r] : acc[i][j][r], epi, o);
+                }
+            }
+}
+
 // GEMV: out[i] = bias[i] + a[i][:] . x (scalar.rs:74-91). One wave per row,
 // float4 loads when the row stride allows; the row streams from HBM once.
 __global__ __launch_bounds__(256) void vk_gemv_f32(const float* __restrict__ a, const float* __restrict__ x,
@@ -290,9 +404,6 @@ static_assert(NSLOT >= 2 && NSLOT <= 4, "ring depth");
 static_assert(WAVES >= 1 && WAVES <= 16, "workgroup of 64 * WAVES threads");
 }
 
-__device__ __forceinline__ float vk_f4c(const float4& v, int s) {
-    return s == 0 ? v.x : (s == 1 ? v.y : (s == 2 ? v.z : v.w));
-}
 
 // (value desc, index asc) merge of two argmax candidates
 __device__ __forceinline__ void vk_am_merge(float& bv, int& bi, float ov, int oi) {
@@ -446,6 +557,17 @@ namespace vk {
 hipError_t launch_gemm_f32(hipStream_t s, bool b_trans, const float* a, const float* b, const float* bias,
                            float* out, int m, int n, int k, VkEpi epi) {
     if (m == 0 || n == 0) return hipSuccess;
+    // the tiled kernel: whole 16-wide K stages (at least two), 16-byte aligned
+    // rows, and for B [k, n] whole column quads
+    const bool aligned = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0;
+    if (k % g32f::KC == 0 && k >= 2 * g32f::KC && aligned && (b_trans || n % 4 == 0)) {
+        const unsigned tiles = (unsigned)(((m + g32f::TM - 1) / g32f::TM) * ((n + g32f::TN - 1) / g32f::TN));
+        if (b_trans)
+            hipLaunchKernelGGL(vk_gemm_f32_tiled<true>, dim3(tiles), dim3(256), 0, s, a, b, bias, epi, out, m, n, k);
+        else
+            hipLaunchKernelGGL(vk_gemm_f32_tiled<false>, dim3(tiles), dim3(256), 0, s, a, b, bias, epi, out, m, n, k);
+        return hipGetLastError();
+    }
     const dim3 grid((n + g32::T - 1) / g32::T, (m + g32::T - 1) / g32::T);
     if (b_trans)
         hipLaunchKernelGGL(vk_gemm_f32<true>, grid, dim3(256), 0, s, a, b, bias, epi, out, m, n, k);
