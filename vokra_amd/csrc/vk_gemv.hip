@@ -241,6 +241,129 @@ __global__ __launch_bounds__(256) void vk_gemv_qblock(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Wave-per-tile decode kernel: one wave (its own workgroup) owns a 16 x 16
+// output tile and walks the K blocks in order: the exact block dot P_b of the
+// MFMA (accumulator input OFFSET * operand sum, as above) is folded right away,
+// acc = fmaf(s_a * d_w, P_b, acc), for the lane's 4 outputs. No LDS exchange of
+// block dots and no barriers; the operands of each 4-block group (A fragments,
+// weight words, weight scales, activation scales and sums) stream global -> LDS
+// through a private ring of RING groups with direct loads. Same products, same
+// order: bit-identical to the two-phase kernel.
+namespace gw {
+#ifndef VK_GW_RING
+#define VK_GW_RING 3
+#endif
+constexpr int RING = VK_GW_RING;        // groups in flight per wave (<= 8: the wait counts stay < 64)
+constexpr int SLOT = 7 * 1024;          // bytes per ring slot: A 4 KiB, W <= 2 KiB, scales 768 B
+constexpr int OFF_W = 4096, OFF_WS = 6144, OFF_SA = 6400, OFF_AS = 6656;
+}  // namespace gw
+
+template <int MODE, bool POW2, bool DEV>
+__global__ __launch_bounds__(64) void vk_gemv_qblock_w(
+    const uint4* __restrict__ afrag, const float* __restrict__ ascale, const float* __restrict__ asum,
+    const GemvSet set, const VkGemvLin* __restrict__ dlins, int m, int nb, int m_pad) {
+    using namespace gw;
+    constexpr int WQ = MODE == 1 ? 1 : 2;           // weight KiB per group
+    constexpr int LG = 4 + WQ + 3;                  // direct loads per lane per group
+    constexpr float OFFSET = MODE == 1 ? -136.0f : -128.0f;
+    __shared__ __align__(16) uint8_t ring[RING][SLOT];
+    const VkGemvLin lin = DEV ? dlins[blockIdx.z] : set.lin[blockIdx.z];
+    const int nt = blockIdx.x, mt = blockIdx.y;
+    if (nt * 16 >= lin.n) return;  // this linear has fewer column tiles (the whole wave)
+    const int lane = threadIdx.x, rq = 4 * (lane >> 4), col = lane & 15;
+    const int G = nb / gemv::GB;
+    const uint32_t base = __builtin_amdgcn_readfirstlane(vk_lds_addr(&ring[0][0]));
+    // per-lane sources (advanced by group)
+    const uint4* a_src = afrag + (size_t)mt * nb * gemv::FRAG_U4 + lane;
+    const uint4* w_src = lin.wq4 + (size_t)nt * G * WQ * gemv::FRAG_U4 + lane;
+    const uint32_t* ws_src = reinterpret_cast<const uint32_t*>(lin.wsc + (size_t)nt * G * 16) + (lane & 31);
+    const size_t s_off = (size_t)(lane >> 4) * m_pad + mt * 16 + (lane & 15);
+    auto issue = [&](int g, int slot) {
+        const uint32_t b = base + slot * SLOT;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) vk_dma_b128(a_src + (size_t)(4 * g + u) * gemv::FRAG_U4, b + u * 1024);
+#pragma unroll
+        for (int h = 0; h < WQ; ++h) vk_dma_b128(w_src + (size_t)(g * WQ + h) * gemv::FRAG_U4, b + OFF_W + h * 1024);
+        vk_dma_b32(ws_src + (size_t)g * 32, b + OFF_WS);
+        vk_dma_b32(ascale + (size_t)4 * g * m_pad + s_off, b + OFF_SA);
+        vk_dma_b32(asum + (size_t)4 * g * m_pad + s_off, b + OFF_AS);
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int p = 0; p < RING - 1; ++p)
+        if (p < G) issue(p, p);
+    static_assert(RING >= 3 && RING <= 8 && (RING - 1) * LG < 64, "ring depth");
+    int slot = 0;
+#pragma unroll 1
+    for (int g = 0; g < G; ++g) {
+        // group g's loads are the oldest in flight: wait for exactly those
+        const int ahead = G - 1 - g;
+        if (ahead >= RING - 1) {
+            issue(g + RING - 1, slot == 0 ? RING - 1 : slot - 1);
+            vk_wait_vm<(RING - 1) * LG>();
+        } else if (RING > 7 && ahead == 6) {
+            vk_wait_vm<6 * LG>();
+        } else if (RING > 6 && ahead == 5) {
+            vk_wait_vm<5 * LG>();
+        } else if (RING > 5 && ahead == 4) {
+            vk_wait_vm<4 * LG>();
+        } else if (RING > 4 && ahead == 3) {
+            vk_wait_vm<3 * LG>();
+        } else if (ahead == 2) {
+            vk_wait_vm<2 * LG>();
+        } else if (ahead == 1) {
+            vk_wait_vm<LG>();
+        } else {
+            vk_wait_vm<0>();
+        }
+        const uint8_t* sl = &ring[slot][0];
+        uint4 af[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) af[u] = reinterpret_cast<const uint4*>(sl + u * 1024)[lane];
+        uint4 wq[WQ];
+#pragma unroll
+        for (int h = 0; h < WQ; ++h) wq[h] = reinterpret_cast<const uint4*>(sl + OFF_W + h * 1024)[lane];
+        const uint2 ws = reinterpret_cast<const uint2*>(sl + OFF_WS)[col];
+        float4 sa[4], as[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            sa[u] = reinterpret_cast<const float4*>(sl + OFF_SA)[u * 4 + (lane >> 4)];
+            as[u] = reinterpret_cast<const float4*>(sl + OFF_AS)[u * 4 + (lane >> 4)];
+        }
+        const uint32_t sc_bits[4] = {ws.x & 0xffffu, ws.x >> 16, ws.y & 0xffffu, ws.y >> 16};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            vk_bf16x8 bf;
+            if (MODE == 1) {
+                const uint4 q = wq[0];
+                const uint32_t x = u == 0 ? q.x : (u == 1 ? q.y : (u == 2 ? q.z : q.w));
+                bf = q4_word_to_bf16(x);
+            } else {
+                const uint4 q = wq[u >> 1];
+                bf = (u & 1) ? q8_bytes_to_bf16(q.z, q.w) : q8_bytes_to_bf16(q.x, q.y);
+            }
+            const vk_f32x4 cin = {OFFSET * as[u].x, OFFSET * as[u].y, OFFSET * as[u].z, OFFSET * as[u].w};
+            const vk_f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(vk_bf16x8, af[u]), bf, cin,
+                                                                       0, 0, 0);
+            const float dw = vk_f16_to_f32_hw(sc_bits[u]);
+            const float sar[4] = {sa[u].x, sa[u].y, sa[u].z, sa[u].w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] = fmaf(POW2 ? dw : sar[r] * dw, p[r], acc[r]);
+        }
+        slot = slot == RING - 1 ? 0 : slot + 1;
+    }
+    const int c = nt * 16 + col;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = mt * 16 + rq + r;
+        if (row < m && c < lin.n) {
+            const size_t o = (size_t)row * lin.n + c;
+            lin.out[o] = vk_epi_apply(lin.bias ? acc[r] + lin.bias[c] : acc[r], lin.epi, o);
+        }
+    }
+}
+
 }  // namespace vk
 
 namespace vk {
@@ -254,12 +377,21 @@ hipError_t launch_repack_w_gemv(hipStream_t s, int mode, const uint8_t* wq, int 
     return hipGetLastError();
 }
 
+// Which decode kernel: the wave-per-tile one streams weights faster once the
+// grid is large (>= ~1000 tiles, or a grouped launch), the two-phase one has
+// the shorter latency for a small grid (one memory round trip per workgroup).
+constexpr int kWptMinTiles = 1024;
+
 template <int MODE, bool POW2, bool DEV>
 static hipError_t go(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum, const GemvSet& set,
                      const VkGemvLin* dlins, int n_lin, int n_max, int m, int nb, int m_pad) {
     const int n_tiles = (n_max + 15) / 16, m_tiles = (m + 15) / 16;
-    hipLaunchKernelGGL((vk_gemv_qblock<MODE, POW2, DEV>), dim3(n_tiles, m_tiles, n_lin), dim3(256), 0, s, afrag,
-                       ascale, asum, set, dlins, m, nb, m_pad);
+    if (DEV || (size_t)n_tiles * m_tiles * n_lin >= (size_t)kWptMinTiles)
+        hipLaunchKernelGGL((vk_gemv_qblock_w<MODE, POW2, DEV>), dim3(n_tiles, m_tiles, n_lin), dim3(64), 0, s, afrag,
+                           ascale, asum, set, dlins, m, nb, m_pad);
+    else
+        hipLaunchKernelGGL((vk_gemv_qblock<MODE, POW2, DEV>), dim3(n_tiles, m_tiles, n_lin), dim3(256), 0, s, afrag,
+                           ascale, asum, set, dlins, m, nb, m_pad);
     return hipGetLastError();
 }
 
