@@ -259,16 +259,23 @@ __global__ __launch_bounds__(256) void vk_ln_quantize_b32(const float* __restric
     const int mt = TILE ? (int)blockIdx.x : (int)blockIdx.x >> 4;
     uint16_t* tile16 = TILE ? reinterpret_cast<uint16_t*>(lds_tile)
                             : reinterpret_cast<uint16_t*>(afrag + (size_t)mt * nb * 64);
+    // TILE: the rows are unrolled and row r+1 is loaded while row r reduces
+    float xn[kLnRegJ];
+    {
+        const int row0 = mt * 16 + (TILE ? 0 : ((int)blockIdx.x & 15));
+        if (row0 < m) vk_row_load256(in + (size_t)row0 * k, k, xn);
+    }
+#pragma unroll
     for (int r = 0; r < (TILE ? 16 : 1); ++r) {
         const int mr = TILE ? r : (int)blockIdx.x & 15;
         const int row = mt * 16 + mr;
         const bool live = row < m;  // uniform per workgroup
         float x[kLnRegJ];
+#pragma unroll
+        for (int j = 0; j < kLnRegJ; ++j) x[j] = xn[j];
+        if (TILE && r + 1 < 16 && row + 1 < m) vk_row_load256(in + (size_t)(row + 1) * k, k, xn);
         float2 st = make_float2(0.0f, 0.0f);
-        if (live) {
-            vk_row_load256(in + (size_t)row * k, k, x);
-            st = vk_ln_stats256(x, k, eps, red);
-        }
+        if (live) st = vk_ln_stats256(x, k, eps, red);
 #pragma unroll
         for (int j = 0; j < kLnRegJ; ++j) {
             const int c = t + 256 * j;
