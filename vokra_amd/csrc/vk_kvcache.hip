@@ -73,10 +73,11 @@ __global__ __launch_bounds__(1024) void vk_kv_alloc(KvDev c, int layer, int n, c
                 break;
             }
     }
-    // inclusive scan of `first` (Hillis-Steele over the block)
+    // inclusive scan of `first` (Hillis-Steele over the block; the block is
+    // the smallest power of two >= n, at least one wave)
     s_scan[i] = first ? 1 : 0;
     __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
+    for (int off = 1; off < (int)blockDim.x; off <<= 1) {
         const int v = i >= off ? s_scan[i - off] : 0;
         __syncthreads();
         s_scan[i] += v;
@@ -782,7 +783,10 @@ static KvDev kv_view(const KvView& v) {
 hipError_t launch_kv_append(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* times,
                             const float* k, const float* vv) {
     const KvDev c = kv_view(v);
-    hipLaunchKernelGGL(vk_kv_alloc, dim3(1), dim3(1024), 0, s, c, layer, n, streams, times);
+    if (n > 1024) return hipErrorInvalidValue;
+    int block = 64;  // the smallest power of two >= n (at least one wave)
+    while (block < n) block <<= 1;
+    hipLaunchKernelGGL(vk_kv_alloc, dim3(1), dim3(block), 0, s, c, layer, n, streams, times);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const size_t threads = (size_t)n * v.width;
