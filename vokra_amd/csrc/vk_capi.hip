@@ -495,6 +495,23 @@ int gemm_qact_multi(vokra_hip_ctx* c, int n, const vokra_hip_qweight* const* ws,
     }
     VK_TRY(set_dev(c), "hipSetDevice");
     if (!one_launch) {
+        // block formats of one width on the prefill route: one block-GEMM grid
+        bool one_gemm = qa->act_quant != VOKRA_HIP_ACT_KQUANT;
+        for (int i = 0; i < n && one_gemm; ++i)
+            one_gemm = !ws[i]->kquant && !gemv_route(c, ws[i], qa) && ws[i]->n == ws[0]->n &&
+                       ws[i]->n_pad == ws[0]->n_pad;
+        if (one_gemm && n > 1) {
+            VkGemmLin lins[3];
+            for (int i = 0; i < n; ++i)
+                lins[i] = {(const uint4*)ws[i]->frag.p, (const float*)ws[i]->scale.p, biases ? biases[i] : nullptr,
+                           outs[i], {nullptr, 0}};
+            VK_TRY(vk::launch_gemm_qblock_multi(c->stream, qa->act_quant == VOKRA_HIP_ACT_POW2,
+                                                (const uint4*)qa->frag.p, (const float*)qa->scale.p, lins, n,
+                                                (int)qa->m, (int)qa->m_pad, (int)ws[0]->n, (int)ws[0]->n_pad,
+                                                (int)ws[0]->nb),
+                   "launch(vk_gemm_qblock x n)");
+            return VOKRA_HIP_OK;
+        }
         for (int i = 0; i < n; ++i) {
             int st = run_gemm_qact(c, ws[i], qa, biases ? biases[i] : nullptr, outs[i]);
             if (st) return st;

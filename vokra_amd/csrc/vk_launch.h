@@ -11,6 +11,15 @@ struct VkEpi {
     const float* resid;
     int gelu;
 };
+// One linear of a multi-linear block-GEMM launch: bf16 fragments + scales,
+// optional bias, output [m, n].
+struct VkGemmLin {
+    const uint4* wfrag;
+    const float* wscale;
+    const float* bias;
+    float* out;
+    VkEpi epi;
+};
 // One linear of a decode-kernel launch: compact weights, optional bias, output [m, n].
 struct VkGemvLin {
     const uint4* wq4;
@@ -44,6 +53,9 @@ hipError_t launch_repack_w_b32(hipStream_t s, int mode, const uint8_t* wq, int n
 hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
                               const uint4* wfrag, const float* wscale, const float* bias, float* out, int m,
                               int m_pad, int n, int n_pad, int nb, VkEpi epi = {nullptr, 0});
+// n_lin (1..3) linears of the same n over the same activations, one grid.
+hipError_t launch_gemm_qblock_multi(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
+                                    const VkGemmLin* lins, int n_lin, int m, int m_pad, int n, int n_pad, int nb);
 }  // namespace vk
 
 namespace vk {

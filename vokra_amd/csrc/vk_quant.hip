@@ -382,11 +382,18 @@ __device__ __forceinline__ void vk_wait_vm_barrier() {
     else asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Up to three linears over the same activations and of the same width in one
+// grid (q, k and v of an attention block): tile t of the launch belongs to
+// linear t / (tiles per linear), so each one's outputs are those of its own
+// launch.
+struct GemmSet {
+    VkGemmLin lin[3];
+};
+
 template <bool POW2>
 __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
-    const uint4* __restrict__ afrag, const float* __restrict__ ascale,
-    const uint4* __restrict__ wfrag, const float* __restrict__ wscale, const float* __restrict__ bias, VkEpi epi,
-    float* out, int m, int n, int nb, int ldo, int m_pad, int n_pad) {
+    const uint4* __restrict__ afrag, const float* __restrict__ ascale, const GemmSet set, int n_lin,
+    int m, int n, int nb, int ldo, int m_pad, int n_pad) {
     using namespace gemm;
     constexpr int WAVES = WM * WN;
     constexpr int APT = MT * FRAG_U4 / THREADS, BPT = NT * FRAG_U4 / THREADS;  // uint4 loads per thread
@@ -404,12 +411,18 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
     const int wm = wave / WN, wn = wave - wm * WN;
 
     // XCD-aware tile index: workgroups L, L+8, L+16, ... share an XCD.
-    const int tiles_m = m_pad / TM, tiles_n = n_pad / TN, tiles = tiles_m * tiles_n;
+    const int tiles_m = m_pad / TM, tiles_n = n_pad / TN, tiles_lin = tiles_m * tiles_n, tiles = tiles_lin * n_lin;
     const int L = blockIdx.x;
     const int per_xcd = tiles / N_XCD;
-    const int t = (per_xcd * N_XCD == tiles) ? (L % N_XCD) * per_xcd + L / N_XCD : L;
+    const int tt = (per_xcd * N_XCD == tiles) ? (L % N_XCD) * per_xcd + L / N_XCD : L;
+    const int li = tt / tiles_lin, t = tt - li * tiles_lin;
     const int ntile = t / tiles_m, mtile = t - ntile * tiles_m;
     const int mt0 = mtile * MT, nt0 = ntile * NT;
+    const uint4* __restrict__ wfrag = set.lin[li].wfrag;
+    const float* __restrict__ wscale = set.lin[li].wscale;
+    const float* __restrict__ bias = set.lin[li].bias;
+    float* out = set.lin[li].out;
+    const VkEpi epi = set.lin[li].epi;
 
     // Per-thread slice of one stage: A fragments wave + q WAVES (q < APT), B
     // fragments likewise, and one scale (threads [0, TM): A rows, [TM, TM+TN):
@@ -566,10 +579,10 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
 template __global__ void vk_quantize_act_b32<false>(const float*, int, int, int, uint4*, float*, float*);
 template __global__ void vk_quantize_act_b32<true>(const float*, int, int, int, uint4*, float*, float*);
 
-template __global__ void vk_gemm_qblock<false>(const uint4*, const float*, const uint4*, const float*,
-                                               const float*, VkEpi, float*, int, int, int, int, int, int);
-template __global__ void vk_gemm_qblock<true>(const uint4*, const float*, const uint4*, const float*,
-                                              const float*, VkEpi, float*, int, int, int, int, int, int);
+template __global__ void vk_gemm_qblock<false>(const uint4*, const float*, const GemmSet, int, int, int, int, int,
+                                               int, int);
+template __global__ void vk_gemm_qblock<true>(const uint4*, const float*, const GemmSet, int, int, int, int, int,
+                                              int, int);
 
 }  // namespace vk
 
@@ -668,18 +681,27 @@ hipError_t launch_repack_w_b32(hipStream_t s, int mode, const uint8_t* wq, int n
 // The C-ABI layer pads m and n to GEMM_TM / GEMM_TN: whole workgroup tiles.
 static_assert(GEMM_TM % gemm::TM == 0 && GEMM_TN % gemm::TN == 0, "GEMM padding");
 
+hipError_t launch_gemm_qblock_multi(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
+                                    const VkGemmLin* lins, int n_lin, int m, int m_pad, int n, int n_pad, int nb) {
+    if (m_pad % gemm::TM != 0 || n_pad % gemm::TN != 0 || nb < 1 || n_lin < 1 || n_lin > 3)
+        return hipErrorInvalidValue;
+    GemmSet set = {};
+    for (int i = 0; i < n_lin; ++i) set.lin[i] = lins[i];
+    const dim3 grid((unsigned)((n_pad / gemm::TN) * (m_pad / gemm::TM) * n_lin));
+    if (pow2)
+        hipLaunchKernelGGL(vk_gemm_qblock<true>, grid, dim3(gemm::THREADS), 0, s, afrag, ascale, set, n_lin, m, n, nb,
+                           n, m_pad, n_pad);
+    else
+        hipLaunchKernelGGL(vk_gemm_qblock<false>, grid, dim3(gemm::THREADS), 0, s, afrag, ascale, set, n_lin, m, n,
+                           nb, n, m_pad, n_pad);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
                               const uint4* wfrag, const float* wscale, const float* bias, float* out,
                               int m, int m_pad, int n, int n_pad, int nb, VkEpi epi) {
-    if (m_pad % gemm::TM != 0 || n_pad % gemm::TN != 0 || nb < 1) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((n_pad / gemm::TN) * (m_pad / gemm::TM)));
-    if (pow2)
-        hipLaunchKernelGGL(vk_gemm_qblock<true>, grid, dim3(gemm::THREADS), 0, s, afrag, ascale, wfrag, wscale, bias,
-                           epi, out, m, n, nb, n, m_pad, n_pad);
-    else
-        hipLaunchKernelGGL(vk_gemm_qblock<false>, grid, dim3(gemm::THREADS), 0, s, afrag, ascale, wfrag, wscale, bias,
-                           epi, out, m, n, nb, n, m_pad, n_pad);
-    return hipGetLastError();
+    const VkGemmLin lin = {wfrag, wscale, bias, out, epi};
+    return launch_gemm_qblock_multi(s, pow2, afrag, ascale, &lin, 1, m, m_pad, n, n_pad, nb);
 }
 
 }  // namespace vk
