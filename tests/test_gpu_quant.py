@@ -179,6 +179,25 @@ def test_gemm_q_config1_rows_bit_exact(ctx, oracle):
 
 
 @pytest.mark.parametrize("act", [hip.ActQuant.AMAX127, hip.ActQuant.POW2])
+@pytest.mark.parametrize("m,n,k", [(2100, 1930, 64), (1500, 1280, 96), (1500, 5120, 64)])
+def test_gemm_q_tile_routes_rows_bit_exact(ctx, oracle, act, m, n, k):
+    """Grids of >= 256 128 x 128 tiles run 64 x 64 wave tiles, smaller ones
+    32 x 32 (2100 x 1930: 272 tiles; 1500 x 1280: 120; 1500 x 5120: 480).
+    Ragged m and n, bias, both activation schemes: sampled rows bit-exact."""
+    print(f"[case] gemm_q routes act={act.name} m={m} n={n} k={k}", flush=True)
+    a, wq, bias = _gemm_case(oracle, hip.WDtype.Q8_0, m, n, k, seed=m + n + k, zero_rows=(5,))
+    ctx.set_act_quant(act)
+    try:
+        got = ctx.gemm_q_f32(m, n, k, a, wq, hip.WDtype.Q8_0, bias)
+    finally:
+        ctx.set_act_quant(hip.ActQuant.AMAX127)
+    rows = sorted(set([0, 5, 63, 64, 127, 128, m - 65, m - 64, m - 1] + list(range(9, m, 97))))
+    want = oracle.gemm_qblock_i8(int(hip.WDtype.Q8_0), len(rows), n, k, a[rows], wq, bias,
+                                 pow2=(act == hip.ActQuant.POW2))
+    assert np.array_equal(bits(got[rows]), bits(want))
+
+
+@pytest.mark.parametrize("act", [hip.ActQuant.AMAX127, hip.ActQuant.POW2])
 @pytest.mark.parametrize("wd", [hip.WDtype.Q4_0, hip.WDtype.Q8_0])
 @pytest.mark.parametrize("m,n,k", [(1, 16, 128), (3, 100, 256), (8, 1280, 1280), (17, 48, 512),
                                    (33, 200, 128), (64, 1280, 5120), (64, 5120, 1280)])

@@ -377,9 +377,8 @@ constexpr int LAG = 3;                        // MFMA -> combine distance (tiles
 // access has completed, then barrier.
 template <int N>
 __device__ __forceinline__ void vk_wait_vm_barrier() {
-    static_assert(N == 0 || N == 5, "vmcnt values in use");
-    if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 // Up to three linears over the same activations and of the same width in one
@@ -390,22 +389,29 @@ struct GemmSet {
     VkGemmLin lin[3];
 };
 
-template <bool POW2>
+// WT: 16 x 16 MFMA tiles per wave side (4: 64 x 64 waves, 128 x 128
+// workgroup tiles; 2: 32 x 32 waves, 64 x 64 workgroup tiles for grids that
+// would not fill the chip). Per-output arithmetic is the same for both.
+template <bool POW2, int WT>
 __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
     const uint4* __restrict__ afrag, const float* __restrict__ ascale, const GemmSet set, int n_lin,
     int m, int n, int nb, int ldo, int m_pad, int n_pad) {
     using namespace gemm;
+    static_assert(WT == 2 || WT == 4, "wave tile");
     constexpr int WAVES = WM * WN;
+    constexpr int TM = 16 * WT * WM, TN = 16 * WT * WN;  // workgroup tile (hides the namespace's)
+    constexpr int MT = TM / 16, NT = TN / 16;
+    constexpr int NTILE = WT * WT;                        // MFMA tiles per wave
+    constexpr int CPR = 4 * WT;                           // float4 per row of a wave's output strip
     constexpr int APT = MT * FRAG_U4 / THREADS, BPT = NT * FRAG_U4 / THREADS;  // uint4 loads per thread
     static_assert(APT * THREADS == MT * FRAG_U4 && BPT * THREADS == NT * FRAG_U4, "fragment split");
     static_assert(TM + TN <= THREADS, "one scale per thread");
     constexpr int LOADS = APT + BPT + 1;  // loads per thread per stage
-    static_assert(LOADS == 5, "vk_wait_vm_barrier<5>");
     __shared__ __align__(16) uint4 lds_a[NS][MT * FRAG_U4];  // 3 x 8 KiB; reused by the epilogue
     __shared__ __align__(16) uint4 lds_b[NS][NT * FRAG_U4];  // 3 x 8 KiB
     // Block scales: [0, TM) activation rows, [TM, TM + TN) weight columns.
     __shared__ __align__(16) float lds_s[NS][THREADS];
-    static_assert(sizeof(lds_a[0]) * 2 >= (size_t)THREADS * 64, "epilogue slots");
+    static_assert(sizeof(lds_a) >= (size_t)WAVES * 16 * 16 * WT * 4, "epilogue slots");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave - wm * WN;
@@ -429,7 +435,8 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
     // W columns).
     const uint4* a_src = afrag + (size_t)(mt0 + wave) * nb * FRAG_U4 + lane;
     const uint4* b_src = wfrag + (size_t)(nt0 + wave) * nb * FRAG_U4 + lane;
-    const float* s_src = tid < TM ? ascale + mt0 * 16 + tid : wscale + nt0 * 16 + (tid - TM);
+    // (threads past TM + TN re-read a column scale into an unused slot)
+    const float* s_src = tid < TM ? ascale + mt0 * 16 + tid : wscale + nt0 * 16 + (tid - TM) % TN;
     const int s_stride = tid < TM ? m_pad : n_pad;
     // wave-uniform LDS destinations (bytes)
     const uint32_t la = __builtin_amdgcn_readfirstlane(vk_lds_addr(&lds_a[0][wave * 64]));
@@ -448,32 +455,32 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
         vk_dma_b32(s_src + (size_t)b * s_stride, ls + buf * S_STAGE);
     };
 
-    vk_f32x4 acc[4][4];
+    vk_f32x4 acc[WT][WT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < WT; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = (vk_f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < WT; ++j) acc[i][j] = (vk_f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
     const vk_f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](int buf) {
-        vk_bf16x8 af[4], bf[4];
-        float sa[4][4], dw[4];
+        vk_bf16x8 af[WT], bf[WT];
+        float sa[WT][4], dw[WT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            af[i] = __builtin_bit_cast(vk_bf16x8, lds_a[buf][(wm * 4 + i) * FRAG_U4 + lane]);
+        for (int i = 0; i < WT; ++i) {
+            af[i] = __builtin_bit_cast(vk_bf16x8, lds_a[buf][(wm * WT + i) * FRAG_U4 + lane]);
             if (!POW2) {
-                const float4 s4 = reinterpret_cast<const float4*>(lds_s[buf] + (wm * 4 + i) * 16)[lane >> 4];
+                const float4 s4 = reinterpret_cast<const float4*>(lds_s[buf] + (wm * WT + i) * 16)[lane >> 4];
                 sa[i][0] = s4.x; sa[i][1] = s4.y; sa[i][2] = s4.z; sa[i][3] = s4.w;
             }
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            bf[j] = __builtin_bit_cast(vk_bf16x8, lds_b[buf][(wn * 4 + j) * FRAG_U4 + lane]);
-            dw[j] = lds_s[buf][TM + (wn * 4 + j) * 16 + (lane & 15)];
+        for (int j = 0; j < WT; ++j) {
+            bf[j] = __builtin_bit_cast(vk_bf16x8, lds_b[buf][(wn * WT + j) * FRAG_U4 + lane]);
+            dw[j] = lds_s[buf][TM + (wn * WT + j) * 16 + (lane & 15)];
         }
-        vk_f32x4 p[16];
+        vk_f32x4 p[NTILE];
         auto combine = [&](int t) {
-            const int i = t >> 2, j = t & 3;
+            const int i = t / WT, j = t % WT;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if (POW2) acc[i][j][r] = fmaf(dw[j], p[t][r], acc[i][j][r]);
@@ -484,13 +491,13 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
         // tile t - LAG, whose product has retired; LAG + 1 products are live.
         // The combine order per output stays block order.
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            p[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t >> 2], bf[t & 3], zero, 0, 0, 0);
+        for (int t = 0; t < NTILE; ++t) {
+            p[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t / WT], bf[t % WT], zero, 0, 0, 0);
             if (t >= LAG) combine(t - LAG);
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int t = 16 - LAG; t < 16; ++t) combine(t);
+        for (int t = NTILE - LAG; t < NTILE; ++t) combine(t);
     };
 
     // Stage ring of NS = 3: the loads for block b+2 are issued once every wave
@@ -517,39 +524,39 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
     vk_wait_vm_barrier<0>();
 
     // Epilogue. D layout of v_mfma_f32_16x16x32_bf16: lane l holds rows
-    // 4*(l/16)+r of column l%16. Each wave owns a 4 KiB LDS slot; per m-subtile
-    // it writes the 16 x 64 strip, then reads it back row-major.
-    float* slot = reinterpret_cast<float*>(&lds_a[0][0]) + wave * 1024;
-    const int col0 = (nt0 + wn * 4) * 16;
-    const bool vec_ok = (ldo % 4 == 0) && (col0 + 64 <= n) &&
+    // 4*(l/16)+r of column l%16. Each wave owns an LDS slot; per m-subtile it
+    // writes the 16 x (16 WT) strip, then reads it back row-major.
+    float* slot = reinterpret_cast<float*>(&lds_a[0][0]) + wave * (256 * WT);
+    const int col0 = (nt0 + wn * WT) * 16;
+    const bool vec_ok = (ldo % 4 == 0) && (col0 + 16 * WT <= n) &&
                         (((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(bias) |
                            reinterpret_cast<uintptr_t>(epi.resid)) & 15) == 0);
-    const int c4 = 4 * (lane & 15);
+    const int c4 = 4 * (lane % CPR);
     const float4 bv = (bias && vec_ok) ? *reinterpret_cast<const float4*>(bias + col0 + c4)
                                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row_base = (mt0 + wm * 4 + i) * 16;
+    for (int i = 0; i < WT; ++i) {
+        const int row_base = (mt0 + wm * WT + i) * 16;
         // residual rows of this strip, loaded before the LDS round trip so the
         // latency overlaps it (rows past m read row m-1: in bounds, unused)
-        float4 rv[4];
+        float4 rv[WT];
         if (epi.resid && vec_ok) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int row = min(row_base + 4 * q + (lane >> 4), m - 1);
+            for (int q = 0; q < WT; ++q) {
+                const int row = min(row_base + (64 / CPR) * q + lane / CPR, m - 1);
                 rv[q] = *reinterpret_cast<const float4*>(epi.resid + (size_t)row * ldo + col0 + c4);
             }
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < WT; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) slot[(4 * (lane >> 4) + r) * 64 + 16 * j + (lane & 15)] = acc[i][j][r];
+            for (int r = 0; r < 4; ++r) slot[(4 * (lane >> 4) + r) * (16 * WT) + 16 * j + (lane & 15)] = acc[i][j][r];
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int rr = 4 * q + (lane >> 4);
+        for (int q = 0; q < WT; ++q) {
+            const int rr = (64 / CPR) * q + lane / CPR;
             const int row = row_base + rr;
-            float4 v = *reinterpret_cast<const float4*>(slot + rr * 64 + c4);
+            float4 v = *reinterpret_cast<const float4*>(slot + rr * (16 * WT) + c4);
             if (row >= m) continue;
             const size_t o = (size_t)row * ldo + col0 + c4;
             if (vec_ok) {
@@ -579,10 +586,14 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
 template __global__ void vk_quantize_act_b32<false>(const float*, int, int, int, uint4*, float*, float*);
 template __global__ void vk_quantize_act_b32<true>(const float*, int, int, int, uint4*, float*, float*);
 
-template __global__ void vk_gemm_qblock<false>(const uint4*, const float*, const GemmSet, int, int, int, int, int,
-                                               int, int);
-template __global__ void vk_gemm_qblock<true>(const uint4*, const float*, const GemmSet, int, int, int, int, int,
-                                              int, int);
+template __global__ void vk_gemm_qblock<false, 4>(const uint4*, const float*, const GemmSet, int, int, int, int,
+                                                  int, int, int);
+template __global__ void vk_gemm_qblock<true, 4>(const uint4*, const float*, const GemmSet, int, int, int, int, int,
+                                                 int, int);
+template __global__ void vk_gemm_qblock<false, 2>(const uint4*, const float*, const GemmSet, int, int, int, int,
+                                                  int, int, int);
+template __global__ void vk_gemm_qblock<true, 2>(const uint4*, const float*, const GemmSet, int, int, int, int, int,
+                                                 int, int);
 
 }  // namespace vk
 
@@ -681,19 +692,35 @@ hipError_t launch_repack_w_b32(hipStream_t s, int mode, const uint8_t* wq, int n
 // The C-ABI layer pads m and n to GEMM_TM / GEMM_TN: whole workgroup tiles.
 static_assert(GEMM_TM % gemm::TM == 0 && GEMM_TN % gemm::TN == 0, "GEMM padding");
 
+// Below three quarters of one resident round (256 CUs x 2 workgroups) of
+// 128 x 128 tiles, 64 x 64 tiles win (measured: 120 tiles 26.5 -> 16.6 us,
+// 360 tiles 37.8 -> 35.4 us; 480 tiles 39.5 -> 46.7 us, so those stay).
+constexpr int kGemmSmallTileBelow = 384;  // 128 x 128 tiles per launch
+
 hipError_t launch_gemm_qblock_multi(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
                                     const VkGemmLin* lins, int n_lin, int m, int m_pad, int n, int n_pad, int nb) {
     if (m_pad % gemm::TM != 0 || n_pad % gemm::TN != 0 || nb < 1 || n_lin < 1 || n_lin > 3)
         return hipErrorInvalidValue;
     GemmSet set = {};
     for (int i = 0; i < n_lin; ++i) set.lin[i] = lins[i];
-    const dim3 grid((unsigned)((n_pad / gemm::TN) * (m_pad / gemm::TM) * n_lin));
-    if (pow2)
-        hipLaunchKernelGGL(vk_gemm_qblock<true>, grid, dim3(gemm::THREADS), 0, s, afrag, ascale, set, n_lin, m, n, nb,
-                           n, m_pad, n_pad);
-    else
-        hipLaunchKernelGGL(vk_gemm_qblock<false>, grid, dim3(gemm::THREADS), 0, s, afrag, ascale, set, n_lin, m, n,
-                           nb, n, m_pad, n_pad);
+    // 128 x 128 workgroup tiles unless they leave CUs idle; then 64 x 64
+    const int big = (n_pad / gemm::TN) * (m_pad / gemm::TM) * n_lin;
+    if (big >= kGemmSmallTileBelow) {
+        if (pow2)
+            hipLaunchKernelGGL((vk_gemm_qblock<true, 4>), dim3((unsigned)big), dim3(gemm::THREADS), 0, s, afrag, ascale,
+                               set, n_lin, m, n, nb, n, m_pad, n_pad);
+        else
+            hipLaunchKernelGGL((vk_gemm_qblock<false, 4>), dim3((unsigned)big), dim3(gemm::THREADS), 0, s, afrag,
+                               ascale, set, n_lin, m, n, nb, n, m_pad, n_pad);
+    } else {
+        const unsigned small = (unsigned)big * 4;
+        if (pow2)
+            hipLaunchKernelGGL((vk_gemm_qblock<true, 2>), dim3(small), dim3(gemm::THREADS), 0, s, afrag, ascale, set,
+                               n_lin, m, n, nb, n, m_pad, n_pad);
+        else
+            hipLaunchKernelGGL((vk_gemm_qblock<false, 2>), dim3(small), dim3(gemm::THREADS), 0, s, afrag, ascale, set,
+                               n_lin, m, n, nb, n, m_pad, n_pad);
+    }
     return hipGetLastError();
 }
 
