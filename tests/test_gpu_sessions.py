@@ -132,7 +132,75 @@ def make_decoder(ctx, oracle, g, wd=W_Q4_0, d=128, H=2, ff=256, V=300, n_text=24
     for s in range(n_stream):
         gpu.set_encoder(s, encs[s])
         ref.set_encoder(s, encs[s])
+    gpu.parts = dict(wd=wd, d=d, H=H, ff=ff, V=V, n_text=n_text, bs=bs, layers=layers, tok=tok, pos=pos, lpg=lpg,
+                     lpb=lpb, encs=encs)
     return gpu, ref
+
+
+class DecoderByOps:
+    """The decoder step issued one C-ABI entry point at a time: LayerNorm,
+    INT8 linears (+ bias, + residual in numpy, GELU), the paged cache's append
+    and decode attention, per-stream cross SDPA over the stream's encoder K/V,
+    and the fused tied logits + argmax."""
+
+    def __init__(self, ctx, parts, n_stream):
+        self.ctx, self.p = ctx, parts
+        P = parts
+        self.W = hip.WDtype(P["wd"])
+        d, H = P["d"], P["H"]
+        self.kv = ctx.kv_cache(len(P["layers"]), H, d // H, n_stream, P["n_text"], P["bs"])
+        na = P["encs"][0].shape[0]
+        self.cross = [[(ctx.gemm_q_f32(na, d, d, enc, L["cwk"], self.W, bias=L.get("cbk")),
+                        ctx.gemm_q_f32(na, d, d, enc, L["cwv"], self.W, bias=L.get("cbv")))
+                       for L in P["layers"]] for enc in P["encs"]]
+
+    def step(self, streams, tokens, positions):
+        ctx, P, W = self.ctx, self.p, self.W
+        n, d, H, ff = len(streams), P["d"], P["H"], P["ff"]
+        scale = float(np.float32(d // H) ** np.float32(-0.5))
+        h = (P["tok"][tokens] + P["pos"][positions]).astype(np.float32)
+        lens = [p + 1 for p in positions]
+        for l, L in enumerate(P["layers"]):
+            xn = ctx.layer_norm_f32(h, n, d, L["ln1_gamma"], L["ln1_beta"])
+            q, k, v = (ctx.gemm_q_f32(n, d, d, xn, L[w], W, bias=L.get(b))
+                       for w, b in (("wq", "bq"), ("wk", "bk"), ("wv", "bv")))
+            self.kv.append(l, streams, positions, k, v)
+            a = self.kv.attn(l, streams, lens, q, H, scale)
+            h = ctx.gemm_q_f32(n, d, d, a, L["wo"], W, bias=L["bo"]) + h
+            xn = ctx.layer_norm_f32(h, n, d, L["ln2_gamma"], L["ln2_beta"])
+            cq = ctx.gemm_q_f32(n, d, d, xn, L["cwq"], W, bias=L["cbq"])
+            ca = np.concatenate([ctx.attn_f32(cq[i:i + 1], *self.cross[s][l], H, scale=scale)
+                                 for i, s in enumerate(streams)])
+            h = ctx.gemm_q_f32(n, d, d, ca, L["cwo"], W, bias=L["cbo"]) + h
+            xn = ctx.layer_norm_f32(h, n, d, L["ln3_gamma"], L["ln3_beta"])
+            f = ctx.gelu_f32(ctx.gemm_q_f32(n, ff, d, xn, L["w1"], W, bias=L["b1"])).reshape(n, ff)
+            h = ctx.gemm_q_f32(n, d, ff, f, L["w2"], W, bias=L["b2"]) + h
+        x = ctx.layer_norm_f32(h, n, d, P["lpg"], P["lpb"])
+        V = P["V"]
+        d_x, d_e = hip.DeviceBuffer.from_array(ctx, x), hip.DeviceBuffer.from_array(ctx, P["tok"])
+        d_l, d_n = hip.DeviceBuffer(ctx, n * V * 4), hip.DeviceBuffer(ctx, n * 4)
+        ctx.logits_argmax_dev(n, V, d, d_x, d_e, d_l, d_n)
+        ctx.synchronize()
+        return d_n.download(np.int32, n), d_l.download(np.float32, n * V).reshape(n, V)
+
+
+@pytest.mark.parametrize("wd", [W_Q4_0, W_Q8_0])
+def test_decoder_step_equals_entry_points(ctx, oracle, wd):
+    """A batched decoder step (fused LN + quantize, q split and activation
+    pass inside the attention kernels, residual / GELU epilogues, fused
+    logits) is bit-identical to the same step issued one entry point at a
+    time, over ragged batches."""
+    print(f"[case] decoder == entry points wd={wd}", flush=True)
+    gpu, _ = make_decoder(ctx, oracle, np.random.default_rng(5), wd=wd)
+    ops = DecoderByOps(ctx, gpu.parts, 4)
+    pos, tok = [0, 0, 0, 0], [1, 2, 3, 4]
+    for streams in ([0, 1, 2, 3], [2, 0], [3, 1, 0, 2], [1]):
+        args = ([tok[s] for s in streams], [pos[s] for s in streams])
+        nxt, logits = gpu.step(streams, *args, want_logits=True)
+        n2, l2 = ops.step(streams, *args)
+        assert np.array_equal(logits, l2) and np.array_equal(nxt, n2), streams
+        for i, s in enumerate(streams):
+            tok[s], pos[s] = int(nxt[i]), pos[s] + 1
 
 
 def test_decoder_batch_equals_single_stream_steps(ctx, oracle):

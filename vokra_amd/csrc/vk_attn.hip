@@ -27,6 +27,7 @@
 #include <hip/hip_fp16.h>
 
 #include "vk_common.h"
+#include "vk_launch.h"
 
 namespace vk {
 
@@ -43,6 +44,25 @@ constexpr int VPAD = 8;  // halves of row padding in the V^T tile
 __device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
     hi = (_Float16)x;
     lo = (_Float16)(x - (float)hi);
+}
+
+// hi / lo fp16 of x[0..7] * scale packed as two uint4 (vk_split_rows's
+// arithmetic for 8 consecutive elements).
+__device__ __forceinline__ void split8_f16(const float* __restrict__ x, float scale, uint4& hi, uint4& lo) {
+    const float4 u = reinterpret_cast<const float4*>(x)[0], w = reinterpret_cast<const float4*>(x)[1];
+    const float a[8] = {u.x * scale, u.y * scale, u.z * scale, u.w * scale,
+                        w.x * scale, w.y * scale, w.z * scale, w.w * scale};
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        _Float16 h0, l0, h1, l1;
+        split_f16(a[2 * j], h0, l0);
+        split_f16(a[2 * j + 1], h1, l1);
+        h[j] = __builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        l[j] = __builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+    }
+    hi = make_uint4(h[0], h[1], h[2], h[3]);
+    lo = make_uint4(l[0], l[1], l[2], l[3]);
 }
 
 // ---------------------------------------------------------------------------
@@ -95,7 +115,9 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
     const uint4* __restrict__ kh, const uint4* __restrict__ kl,    // [B][Tkv][Hkv*HD] fp16
     const uint4* __restrict__ vth, const uint4* __restrict__ vtl,  // [B][Hkv][HD][Tpad] fp16
     float* __restrict__ out, int tq, int tkv, int t_pad, int hq, int hkv, int causal, int q_off,
-    const int* __restrict__ kv_index) {
+    const int* __restrict__ kv_index,
+    const float* __restrict__ qf, float q_scale,  // qf != null: f32 q, split here (qh / ql unused)
+    const VkQOut qo) {                            // qo.afrag != null: quantize O (out may be null)
     using namespace attn;
     constexpr int KS = HD / 32;      // 32-wide K steps of S = K . Q^T
     constexpr int OS = HD / 16;      // 16-row output subtiles of O^T
@@ -120,8 +142,12 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         const size_t o = ((size_t)b * tq + q_ld) * qw + (size_t)h * HD / 8 + 4 * ks + g;
-        qa_h[ks] = qh[o];
-        qa_l[ks] = ql[o];
+        if (qf) {
+            split8_f16(qf + 8 * o, q_scale, qa_h[ks], qa_l[ks]);
+        } else {
+            qa_h[ks] = qh[o];
+            qa_l[ks] = ql[o];
+        }
     }
 
     // keys this workgroup has to visit
@@ -160,18 +186,76 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
         return st;
     };
 
-    float* orow = out + ((size_t)b * tq + q_idx) * (size_t)hq * HD + (size_t)h * HD;
-    if (n_tiles == 0) {  // no keys: P . V over an empty set is zero
-        if (q_idx < tq)
+    // O = O^T * inv: lane holds query lq, hd 16os + 4g + r. The four lanes of
+    // a query (l, l^16, l^32, l^48) hold its row; with qo, they quantize each
+    // 32-wide block of it (os 2bq and 2bq+1) as the activation pass would.
+    auto finish = [&](const vk_f32x4* o_acc, float inv) {
+        float ov[OS][4];
+#pragma unroll
+        for (int os = 0; os < OS; ++os)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ov[os][r] = o_acc[os][r] * inv;
+        const size_t row = (size_t)b * tq + q_idx;
+        if (out && q_idx < tq) {
+            float* orow = out + row * (size_t)hq * HD + (size_t)h * HD;
 #pragma unroll
             for (int os = 0; os < OS; ++os)
-                *reinterpret_cast<float4*>(orow + 16 * os + 4 * g) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        return;
-    }
+                *reinterpret_cast<float4*>(orow + 16 * os + 4 * g) =
+                    make_float4(ov[os][0], ov[os][1], ov[os][2], ov[os][3]);
+        }
+        if (!qo.afrag) return;
+        const int nb = qo.k >> 5;
+#pragma unroll
+        for (int bq = 0; bq < HD / 32; ++bq) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) amax = fmaxf(amax, fabsf(ov[2 * bq + hf][r]));
+            amax = fmaxf(amax, __shfl_xor(amax, 16, VK_WAVE));
+            amax = fmaxf(amax, __shfl_xor(amax, 32, VK_WAVE));
+            float sc = 0.0f;
+            int qv[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+            if (amax != 0.0f) {
+                sc = vk_act_scale(amax, qo.pow2);
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) qv[hf][r] = vk_act_q(ov[2 * bq + hf][r], sc);
+            }
+            int gs = 0;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) gs += qv[hf][r];
+            gs += __shfl_xor(gs, 16, VK_WAVE);
+            gs += __shfl_xor(gs, 32, VK_WAVE);
+            if (q_idx < tq) {
+                const int kb = h * (HD / 32) + bq;
+                uint16_t* f16 = reinterpret_cast<uint16_t*>(qo.afrag);
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    // elements 16 hf + 4g .. +3: four consecutive uint16 of one lane's uint4
+                    const size_t at = vk_afrag_u16(row, kb, nb, 16 * hf + 4 * g);
+                    uint32_t w0 = vk_act_bits(qv[hf][0], sc, qo.pow2) | (vk_act_bits(qv[hf][1], sc, qo.pow2) << 16);
+                    uint32_t w1 = vk_act_bits(qv[hf][2], sc, qo.pow2) | (vk_act_bits(qv[hf][3], sc, qo.pow2) << 16);
+                    *reinterpret_cast<uint2*>(f16 + at) = make_uint2(w0, w1);
+                }
+                if (g == 0) {
+                    qo.ascale[(size_t)kb * qo.m_pad + row] = sc;
+                    qo.asum[(size_t)kb * qo.m_pad + row] = qo.pow2 ? (float)gs * sc : (float)gs;
+                }
+            }
+        }
+    };
 
     vk_f32x4 o_acc[OS];
 #pragma unroll
     for (int s = 0; s < OS; ++s) o_acc[s] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (n_tiles == 0) {  // no keys: P . V over an empty set is zero
+        finish(o_acc, 0.0f);
+        return;
+    }
     float m_run = -INFINITY, l_run = 0.0f;
 
     // unconditional (clamped) loads keep the stage in registers
@@ -281,14 +365,7 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
         }
         VK_LDS_BARRIER();
     }
-    // ---- O = O^T / l: lane holds query lq, hd 16os + 4g + r
-    if (q_idx < tq) {
-        const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-#pragma unroll
-        for (int os = 0; os < OS; ++os)
-            *reinterpret_cast<float4*>(orow + 16 * os + 4 * g) =
-                make_float4(o_acc[os][0] * inv, o_acc[os][1] * inv, o_acc[os][2] * inv, o_acc[os][3] * inv);
-    }
+    finish(o_acc, l_run > 0.0f ? 1.0f / l_run : 0.0f);
 }
 
 }  // namespace vk
@@ -316,24 +393,40 @@ hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, i
 template <int HD, bool LO>
 static void go_flash(hipStream_t s, dim3 grid, const void* qh, const void* ql, const void* kh, const void* kl,
                      const void* vth, const void* vtl, float* out, int tq, int tkv, int t_pad, int hq, int hkv,
-                     int causal, int q_off, const int* kv_index) {
+                     int causal, int q_off, const int* kv_index, const float* qf, float q_scale, const VkQOut& qo) {
     hipLaunchKernelGGL((vk_flash_attn<HD, LO>), grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
                        (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv, t_pad,
-                       hq, hkv, causal, q_off, kv_index);
+                       hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+}
+
+static hipError_t flash_any(hipStream_t s, int hd, const void* qh, const void* ql, const float* qf, float q_scale,
+                            const void* kh, const void* kl, const void* vth, const void* vtl, float* out, int batch,
+                            int tq, int tkv, int t_pad, int hq, int hkv, int causal, int q_off, const int* kv_index,
+                            bool kv_lo, const VkQOut& qo) {
+    const dim3 grid((tq + attn::QT - 1) / attn::QT, hq, batch);
+    if (hd == 64) {
+        if (kv_lo) go_flash<64, true>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+        else go_flash<64, false>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+    } else {
+        if (kv_lo) go_flash<128, true>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+        else go_flash<128, false>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* ql, const void* kh, const void* kl,
                              const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
                              int hq, int hkv, int causal, int q_off, const int* kv_index, bool kv_lo) {
-    const dim3 grid((tq + attn::QT - 1) / attn::QT, hq, batch);
-    if (hd == 64) {
-        if (kv_lo) go_flash<64, true>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index);
-        else go_flash<64, false>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index);
-    } else {
-        if (kv_lo) go_flash<128, true>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index);
-        else go_flash<128, false>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index);
-    }
-    return hipGetLastError();
+    return flash_any(s, hd, qh, ql, nullptr, 1.0f, kh, kl, vth, vtl, out, batch, tq, tkv, t_pad, hq, hkv, causal,
+                     q_off, kv_index, kv_lo, VkQOut{});
+}
+
+hipError_t launch_flash_attn_f32q(hipStream_t s, int hd, const float* q, float q_scale, const void* kh, const void* kl,
+                                  const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
+                                  int hq, int hkv, int causal, int q_off, const int* kv_index, bool kv_lo,
+                                  const VkQOut* qo) {
+    return flash_any(s, hd, nullptr, nullptr, q, q_scale, kh, kl, vth, vtl, out, batch, tq, tkv, t_pad, hq, hkv,
+                     causal, q_off, kv_index, kv_lo, qo ? *qo : VkQOut{});
 }
 
 }  // namespace vk

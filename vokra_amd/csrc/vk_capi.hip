@@ -361,26 +361,46 @@ int check_attn(size_t batch, size_t tq, size_t tkv, size_t hq, size_t hkv, size_
     return VOKRA_HIP_OK;
 }
 
+// With qo (a fused activation pass over the output rows), d_out is still
+// written when keep_out is set or q is unaligned (the pass then runs on it).
 int run_attn(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t hq, size_t hkv, size_t hd,
              const float* d_q, const float* d_k, const float* d_v, float scale, int causal, size_t q_off,
-             float* d_out) {
+             float* d_out, const VkQOut* qo = nullptr, bool keep_out = true) {
     const size_t t_pad = round_up(tkv, 64);
     const size_t nq = batch * tq * hq * hd, nk = batch * tkv * hkv * hd, nv = batch * hkv * hd * t_pad;
-    VK_TRY(c->at_qh.ensure(nq * 2 + 16), "hipMalloc(attention q)");
-    VK_TRY(c->at_ql.ensure(nq * 2 + 16), "hipMalloc(attention q)");
+    // an aligned f32 q is split inside the attention kernel (same values as
+    // the split pass)
+    const bool q_in_kernel = ((uintptr_t)d_q & 15) == 0;
+    if (!q_in_kernel) {
+        VK_TRY(c->at_qh.ensure(nq * 2 + 16), "hipMalloc(attention q)");
+        VK_TRY(c->at_ql.ensure(nq * 2 + 16), "hipMalloc(attention q)");
+    }
     VK_TRY(c->at_kh.ensure(nk * 2 + 16), "hipMalloc(attention k)");
     VK_TRY(c->at_kl.ensure(nk * 2 + 16), "hipMalloc(attention k)");
     VK_TRY(c->at_vh.ensure(nv * 2 + 16), "hipMalloc(attention v)");
     VK_TRY(c->at_vl.ensure(nv * 2 + 16), "hipMalloc(attention v)");
-    VK_TRY(vk::launch_split_rows(c->stream, d_q, nq, scale, c->at_qh.p, c->at_ql.p), "launch(vk_split_rows q)");
+    if (!q_in_kernel)
+        VK_TRY(vk::launch_split_rows(c->stream, d_q, nq, scale, c->at_qh.p, c->at_ql.p), "launch(vk_split_rows q)");
     VK_TRY(vk::launch_split_rows(c->stream, d_k, nk, 1.0f, c->at_kh.p, c->at_kl.p), "launch(vk_split_rows k)");
     VK_TRY(vk::launch_split_vt(c->stream, d_v, (int)batch, (int)tkv, (int)t_pad, (int)hkv, (int)hd, c->at_vh.p,
                                c->at_vl.p),
            "launch(vk_split_vt)");
+    if (q_in_kernel) {
+        VK_TRY(vk::launch_flash_attn_f32q(c->stream, (int)hd, d_q, scale, c->at_kh.p, c->at_kl.p, c->at_vh.p,
+                                          c->at_vl.p, (qo && !keep_out) ? nullptr : d_out, (int)batch, (int)tq,
+                                          (int)tkv, (int)t_pad, (int)hq, (int)hkv, causal ? 1 : 0, (int)q_off,
+                                          nullptr, true, qo),
+               "launch(vk_flash_attn)");
+        return VOKRA_HIP_OK;
+    }
     VK_TRY(vk::launch_flash_attn(c->stream, (int)hd, c->at_qh.p, c->at_ql.p, c->at_kh.p, c->at_kl.p, c->at_vh.p,
                                  c->at_vl.p, d_out, (int)batch, (int)tq, (int)tkv, (int)t_pad, (int)hq, (int)hkv,
                                  causal ? 1 : 0, (int)q_off),
            "launch(vk_flash_attn)");
+    if (qo)
+        VK_TRY(vk::launch_quantize_act_b32(c->stream, qo->pow2 != 0, d_out, (int)(batch * tq), qo->m_pad, qo->k,
+                                           qo->afrag, qo->ascale, qo->asum),
+               "launch(vk_quantize_act_b32)");
     return VOKRA_HIP_OK;
 }
 
@@ -429,7 +449,8 @@ int kv_split(const vokra_hip_kv* kv, size_t n, size_t max_len, size_t hkv, int* 
 }
 
 int run_paged_attn(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
-                   const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out) {
+                   const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
+                   const VkQOut* qo = nullptr) {
     const size_t hkv = kv->n_head;
     int n_split = 1, kps = 256;
     kv_split(kv, n, max_len ? max_len : 1, hkv, &n_split, &kps);
@@ -438,7 +459,8 @@ int run_paged_attn(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, c
         VK_TRY(kv->part_o.ensure(n * hq * n_split * kv->d_head * sizeof(float)), "hipMalloc(paged attention partials)");
     }
     VK_TRY(vk::launch_paged_attn(c->stream, kv->view(), (int)layer, (int)n, d_streams, d_lens, d_q, scale, (int)hq,
-                                 (int)kv->d_head, n_split, kps, d_out, (float*)kv->part_ml.p, (float*)kv->part_o.p),
+                                 (int)kv->d_head, n_split, kps, d_out, (float*)kv->part_ml.p, (float*)kv->part_o.p,
+                                 qo),
            "launch(vk_paged_attn)");
     return VOKRA_HIP_OK;
 }
@@ -561,6 +583,82 @@ int qact_ln_quantize(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, const float
     qa->act_quant = act_quant;
     return VOKRA_HIP_OK;
 }
+
+// The output side of an activation pass over m rows of qa's width, for a
+// producer kernel that quantizes its own rows; qo->afrag stays NULL for the
+// K-quant convention (its groups of 16 have no fused form). qact_commit then
+// records what quantize_activations would.
+static int qact_bind(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, int act_quant, VkQOut* qo) {
+    *qo = VkQOut{};
+    if (!qa || qa->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qact: bad activation buffer");
+    if (m == 0 || m > qa->max_m)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qact_quantize: m=%zu outside 1..%zu", m, qa->max_m);
+    if (act_quant == VOKRA_HIP_ACT_KQUANT) return VOKRA_HIP_OK;
+    if (act_quant != VOKRA_HIP_ACT_AMAX127 && act_quant != VOKRA_HIP_ACT_POW2)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "qact_quantize: unknown activation convention %d", act_quant);
+    if (qa->growable) {
+        int st = qact_reserve(qa, m, qa->k);
+        if (st) return st;
+    }
+    *qo = VkQOut{(uint4*)qa->frag.p, (float*)qa->scale.p, (float*)qa->gsum.p, (int)round_up(m, vk::GEMM_TM),
+                 (int)qa->k, act_quant == VOKRA_HIP_ACT_POW2 ? 1 : 0};
+    return VOKRA_HIP_OK;
+}
+static void qact_commit(vokra_hip_qact* qa, size_t m, int act_quant) {
+    qa->m = m;
+    qa->m_pad = round_up(m, vk::GEMM_TM);
+    qa->act_quant = act_quant;
+}
+
+int attn_quantize(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t hq, size_t hkv, size_t hd,
+                  const float* d_q, const float* d_k, const float* d_v, float scale, int causal, size_t q_off,
+                  float* d_out, vokra_hip_qact* qa, int act_quant) {
+    VkQOut qo;
+    int st = qact_bind(c, qa, batch * tq, act_quant, &qo);
+    if (st) return st;
+    if (!qo.afrag) {
+        st = vokra_hip_attn_f32_dev(c, batch, tq, tkv, hq, hkv, hd, d_q, d_k, d_v, scale, causal, q_off, d_out);
+        return st ? st : vokra_hip_qact_quantize_dev(c, qa, batch * tq, d_out, act_quant);
+    }
+    if (qa->k != hq * hd) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn: qact width != n_head_q * head_dim");
+    st = check_attn(batch, tq, tkv, hq, hkv, hd);
+    if (st) return st;
+    if (!d_q || !d_out || (tkv && (!d_k || !d_v))) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn: NULL buffer");
+    if ((reinterpret_cast<uintptr_t>(d_q) | reinterpret_cast<uintptr_t>(d_k) | reinterpret_cast<uintptr_t>(d_out)) & 15)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn: q, k and out must be 16-byte aligned");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    st = run_attn(c, batch, tq, tkv, hq, hkv, hd, d_q, d_k, d_v, scale, causal, q_off, d_out, &qo, false);
+    if (st) return st;
+    qact_commit(qa, batch * tq, act_quant);
+    return VOKRA_HIP_OK;
+}
+
+int paged_attn_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
+                        const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
+                        vokra_hip_qact* qa, int act_quant) {
+    VkQOut qo;
+    int st = qact_bind(c, qa, n, act_quant, &qo);
+    if (st) return st;
+    if (!qo.afrag || qa->k != hq * kv->d_head) {
+        st = vokra_hip_paged_attn_dev(c, kv, layer, n, d_streams, d_lens, max_len, hq, d_q, scale, d_out);
+        return st ? st : vokra_hip_qact_quantize_dev(c, qa, n, d_out, act_quant);
+    }
+    if (!kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn: bad context or cache");
+    st = check_paged_attn(kv, layer, n, hq);
+    if (st) return st;
+    if (!d_streams || !d_lens || !d_q || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn: NULL buffer");
+    if (max_len > kv->max_time) max_len = kv->max_time;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    st = run_paged_attn(c, kv, layer, n, d_streams, d_lens, max_len, hq, d_q, scale, d_out, &qo);
+    if (st) return st;
+    qact_commit(qa, n, act_quant);
+    return VOKRA_HIP_OK;
+}
+
+int qact_output(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, int act_quant, VkQOut* qo) {
+    return qact_bind(c, qa, m, act_quant, qo);
+}
+void qact_outputs_written(vokra_hip_qact* qa, size_t m, int act_quant) { qact_commit(qa, m, act_quant); }
 }  // namespace vk
 
 extern "C" {

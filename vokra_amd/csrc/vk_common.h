@@ -100,6 +100,33 @@ __device__ __forceinline__ int vk_group_sum_i(int v) {
     return v;
 }
 
+// Activation-pass arithmetic of one 32-element block (the convention of
+// vk_quantize_act_b32), for producers that quantize their own output rows.
+// amax = max |v| over the block from 0 through fmaxf (NaN ignored); when
+// amax == 0 the scale and every q are 0.
+__device__ __forceinline__ float vk_act_scale(float amax, bool pow2) {  // amax != 0
+    float s = amax / 127.0f;
+    if (pow2) {
+        int ex;
+        const float f = frexpf(s, &ex);  // s = f * 2^ex, f in [0.5, 1)
+        s = ldexpf(1.0f, f == 0.5f ? ex - 1 : ex);
+    }
+    return s;
+}
+__device__ __forceinline__ int vk_act_q(float v, float s) {
+    const float r = vk_round_half_away(v / s);
+    return (r != r) ? 0 : (int)fminf(fmaxf(r, -127.0f), 127.0f);
+}
+// bf16 bits of the A operand: q, or q * 2^e under the power-of-two convention
+__device__ __forceinline__ uint32_t vk_act_bits(int q, float s, bool pow2) {
+    return pow2 ? (__float_as_uint((float)q * s) >> 16) : vk_int_to_bf16_bits(q);
+}
+// uint16 offset of element e (0..31) of k-block kb of row `row` in the A
+// fragments [m_pad / 16][nb][64 lanes][8]: lane = row % 16 + 16 (e / 8).
+__device__ __forceinline__ size_t vk_afrag_u16(size_t row, int kb, int nb, int e) {
+    return ((((row >> 4) * (size_t)nb + kb) * 64) + (row & 15) + 16 * (e >> 3)) * 8 + (e & 7);
+}
+
 // GELU through the Abramowitz & Stegun 7.1.26 erf
 // (crates/vokra-backend-cpu/src/kernels/scalar.rs:126-172). Shared by the GELU
 // kernel and the GEMM epilogues, so a fused epilogue equals the separate pass.

@@ -16,6 +16,7 @@
 // The table, the free list and the allocator state live in device memory and
 // are only touched by kernels: an append batch allocates on the GPU.
 #include "vk_common.h"
+#include "vk_launch.h"
 
 namespace vk {
 
@@ -266,7 +267,7 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
                                                      const int* __restrict__ lens, const float* __restrict__ q,
                                                      float scale, int hq, int n_split, int keys_per_split,
                                                      float* __restrict__ out, float* __restrict__ part_ml,
-                                                     float* __restrict__ part_o) {
+                                                     float* __restrict__ part_o, const VkQOut qo) {
     constexpr int NB = HD / 32;            // blocks per head slice
     constexpr int NO = G * HD;             // outputs of the workgroup
     // P.V work unit: a quad of 4 consecutive outputs of one head (one 32-bit
@@ -460,7 +461,27 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
         const int h = hk * G + g;
         if (n_split == 1) {
             const float inv = lml[g][1] > 0.0f ? 1.0f / lml[g][1] : 0.0f;
-            out[((size_t)item * hq + h) * HD + e] = a * inv;
+            const float val = a * inv;
+            out[((size_t)item * hq + h) * HD + e] = val;
+            if (qo.afrag) {
+                // the activation pass over this row (row = item, width hq * HD);
+                // a 32-wide block is one half-wave (NO is a multiple of 64)
+                const float amax = vk_group_max<32>(fmaxf(0.0f, fabsf(val)));
+                float sc = 0.0f;
+                int qv = 0;
+                if (amax != 0.0f) {
+                    sc = vk_act_scale(amax, qo.pow2);
+                    qv = vk_act_q(val, sc);
+                }
+                const int gs = vk_group_sum_i<32>(qv);
+                const int col = h * HD + e, kb = col >> 5;
+                reinterpret_cast<uint16_t*>(qo.afrag)[vk_afrag_u16((size_t)item, kb, qo.k >> 5, col & 31)] =
+                    (uint16_t)vk_act_bits(qv, sc, qo.pow2);
+                if ((col & 31) == 0) {
+                    qo.ascale[(size_t)kb * qo.m_pad + item] = sc;
+                    qo.asum[(size_t)kb * qo.m_pad + item] = qo.pow2 ? (float)gs * sc : (float)gs;
+                }
+            }
         } else {
             const size_t pi = ((size_t)item * hq + h) * n_split + split;
             part_o[pi * HD + e] = a;
@@ -829,10 +850,11 @@ hipError_t launch_kv_page_of(hipStream_t s, const KvView& v, int layer, int t, i
     return hipGetLastError();
 }
 
+// Returns whether the kernel that ran also quantized the output (qo).
 template <int HD, int G>
-static void go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* streams, const int* lens,
+static bool go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* streams, const int* lens,
                   const float* q, float scale, int hq, int hkv, int n_split, int kps, float* out, float* pml,
-                  float* po) {
+                  float* po, const VkQOut& qo) {
     // head_dim 128 with several query heads per kv head: the matrix-core
     // kernel (its slots travel through 32-bit lane shuffles; it moves q and
     // O as float4)
@@ -843,36 +865,46 @@ static void go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* st
         if (small_slots && aligned) {
             hipLaunchKernelGGL((vk_paged_attn_gqa<G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams,
                                lens, q, scale, hq, n_split, kps, out, pml, po);
-            return;
+            return false;
         }
     }
     hipLaunchKernelGGL((vk_paged_attn<HD, G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams, lens, q,
-                       scale, hq, n_split, kps, out, pml, po);
+                       scale, hq, n_split, kps, out, pml, po, n_split == 1 ? qo : VkQOut{});
+    return n_split == 1 && qo.afrag;
 }
 
 hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* lens,
                              const float* q, float scale, int hq, int hd, int n_split, int keys_per_split, float* out,
-                             float* part_ml, float* part_o) {
+                             float* part_ml, float* part_o, const VkQOut* qo) {
     const KvDev c = kv_view(v);
     const int hkv = v.width / hd, g = hq / hkv;
-#define VK_PA(HDV, GV)                                                                                      \
-    if (hd == HDV && g == GV) {                                                                             \
-        go_pa<HDV, GV>(s, c, layer, n, streams, lens, q, scale, hq, hkv, n_split, keys_per_split, out, part_ml, \
-                       part_o);                                                                             \
+    const VkQOut qz = qo ? *qo : VkQOut{};
+    bool fused = false;
+#define VK_PA(HDV, GV)                                                                                          \
+    if (hd == HDV && g == GV) {                                                                                 \
+        fused = go_pa<HDV, GV>(s, c, layer, n, streams, lens, q, scale, hq, hkv, n_split, keys_per_split, out,  \
+                               part_ml, part_o, qz);                                                            \
     } else
     VK_PA(64, 1) VK_PA(64, 2) VK_PA(64, 4) VK_PA(64, 8) VK_PA(128, 1) VK_PA(128, 2) VK_PA(128, 4) VK_PA(128, 8) {
         return hipErrorInvalidValue;
     }
 #undef VK_PA
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || n_split == 1) return e;
-    if (hd == 64)
-        hipLaunchKernelGGL(vk_paged_attn_combine<64>, dim3((unsigned)(n * hq)), dim3(64), 0, s, n_split, hq, part_ml,
-                           part_o, out);
-    else
-        hipLaunchKernelGGL(vk_paged_attn_combine<128>, dim3((unsigned)(n * hq)), dim3(128), 0, s, n_split, hq,
-                           part_ml, part_o, out);
-    return hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (n_split > 1) {
+        if (hd == 64)
+            hipLaunchKernelGGL(vk_paged_attn_combine<64>, dim3((unsigned)(n * hq)), dim3(64), 0, s, n_split, hq,
+                               part_ml, part_o, out);
+        else
+            hipLaunchKernelGGL(vk_paged_attn_combine<128>, dim3((unsigned)(n * hq)), dim3(128), 0, s, n_split, hq,
+                               part_ml, part_o, out);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    // kernels without the fused pass: the separate activation pass over out
+    if (qz.afrag && !fused)
+        return launch_quantize_act_b32(s, qz.pow2 != 0, out, n, qz.m_pad, qz.k, qz.afrag, qz.ascale, qz.asum);
+    return hipSuccess;
 }
 
 }  // namespace vk

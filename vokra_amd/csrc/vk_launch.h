@@ -11,6 +11,18 @@ struct VkEpi {
     const float* resid;
     int gelu;
 };
+// The activation pass fused into the kernel that produces its input: for
+// every row < m it writes, the producer stores the A fragments, scales and
+// block sums launch_quantize_act_b32 would store (afrag == NULL: no fusion).
+// Rows m .. m_pad-1 are not written (only their own GEMM rows read them).
+struct VkQOut {
+    uint4* afrag;
+    float* ascale;
+    float* asum;
+    int m_pad;  // the fragments' padded row count
+    int k;      // the quantized row width (a multiple of 32)
+    int pow2;   // the power-of-two scale convention
+};
 // One linear of a multi-linear block-GEMM launch: bf16 fragments + scales,
 // optional bias, output [m, n].
 struct VkGemmLin {
@@ -90,6 +102,14 @@ hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* 
                              const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
                              int hq, int hkv, int causal, int q_off, const int* kv_index = nullptr,
                              bool kv_lo = true);  // false: K/V fp16 hi parts only (kl, vtl unused)
+// The same with q given as f32 [B][Tq][Hq*hd] (16-byte aligned): the kernel
+// splits q * q_scale itself exactly as launch_split_rows would. With qo, the
+// kernel also quantizes O (rows b * tq + i, width hq * hd) into qo's
+// activation fragments, and out may be null.
+hipError_t launch_flash_attn_f32q(hipStream_t s, int hd, const float* q, float q_scale, const void* kh, const void* kl,
+                                  const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
+                                  int hq, int hkv, int causal, int q_off, const int* kv_index = nullptr,
+                                  bool kv_lo = true, const VkQOut* qo = nullptr);
 }  // namespace vk
 
 namespace vk {
@@ -107,7 +127,8 @@ hipError_t launch_kv_reset(hipStream_t s, const KvView& v, const int* order, siz
 hipError_t launch_kv_page_of(hipStream_t s, const KvView& v, int layer, int t, int* out);
 hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* lens,
                              const float* q, float scale, int hq, int hd, int n_split, int keys_per_split, float* out,
-                             float* part_ml, float* part_o);
+                             float* part_ml, float* part_o,
+                             const VkQOut* qo = nullptr);  // also the activation pass over out (rows = items)
 }  // namespace vk
 
 namespace vk {
@@ -140,6 +161,7 @@ hipError_t launch_logits_argmax(hipStream_t s, const float* x, const float* emb,
 struct vokra_hip_ctx;
 struct vokra_hip_qact;
 struct vokra_hip_qweight;
+struct vokra_hip_kv;
 namespace vk {
 hipStream_t ctx_stream(const vokra_hip_ctx* c);
 int ctx_fail(int code, const char* msg);
@@ -155,6 +177,22 @@ int gemm_qact_multi(vokra_hip_ctx* c, int n, const vokra_hip_qweight* const* ws,
                     const float* const* biases, float* const* outs);
 int qact_ln_quantize(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, const float* d_in, const float* gamma,
                      const float* beta, float eps, int act_quant, float* d_scratch);
+//   attn_quantize       = vokra_hip_attn_f32_dev into d_out, then
+//                         vokra_hip_qact_quantize_dev of its batch * t_q rows
+//                         (d_out is then scratch: the fused kernel may skip it)
+//   paged_attn_quantize = vokra_hip_paged_attn_dev into d_out, then
+//                         vokra_hip_qact_quantize_dev of its n rows
+int attn_quantize(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t hq, size_t hkv, size_t hd,
+                  const float* d_q, const float* d_k, const float* d_v, float scale, int causal, size_t q_off,
+                  float* d_out, vokra_hip_qact* qa, int act_quant);
+int paged_attn_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
+                        const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
+                        vokra_hip_qact* qa, int act_quant);
+// For a session's own fused producer: the output binding of an activation
+// pass over m rows of qa (qo->afrag NULL: no fused form, run the pass), and
+// the record of it once the producer is launched.
+int qact_output(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, int act_quant, VkQOut* qo);
+void qact_outputs_written(vokra_hip_qact* qa, size_t m, int act_quant);
 }  // namespace vk
 
 namespace vk {

@@ -159,7 +159,7 @@ struct vokra_hip_decoder {
     vokra_hip_kv_t* kv = nullptr;
     DBuf ckh, ckl, cvh, cvl;  // cross K (fp16 hi/lo) and V^T per (stream, layer)
     int cross_precision = VOKRA_HIP_CROSS_F32;  // F16: cross-attention reads the hi parts only
-    DBuf h, x, q, k, v, attn, f, logits, lpart, qh, ql, lens, kvidx, next, tk, tv, stage;
+    DBuf h, x, q, k, v, attn, f, logits, lpart, lens, kvidx, next, tk, tv, stage;
     vokra_hip_qact_t *qa_d = nullptr, *qa_f = nullptr;
     void release() {
         for (auto& L : layers) {
@@ -167,7 +167,7 @@ struct vokra_hip_decoder {
             for (QLin* w : {&L.q, &L.k, &L.v, &L.o, &L.cq, &L.ck, &L.cv, &L.co, &L.fc1, &L.fc2}) w->release(ctx);
         }
         for (DBuf* b : {&tok_emb, &pos_emb, &lnpg, &lnpb, &ckh, &ckl, &cvh, &cvl, &h, &x, &q, &k, &v, &attn, &f,
-                        &logits, &lpart, &qh, &ql, &lens, &kvidx, &next, &tk, &tv, &stage})
+                        &logits, &lpart, &lens, &kvidx, &next, &tk, &tv, &stage})
             b->release(ctx);
         vokra_hip_kv_destroy(kv);
         kv = nullptr;
@@ -226,9 +226,8 @@ int enc_forward(vokra_hip_encoder* e, size_t batch, size_t frames, const float* 
         const float* qkv_b[3] = {L.q.b(), L.k.b(), L.v.b()};
         float* qkv_o[3] = {e->q.f(), e->k.f(), e->v.f()};
         SS_TRY(vk::gemm_qact_multi(c, 3, qkv, e->qa_d, qkv_b, qkv_o));
-        SS_TRY(vokra_hip_attn_f32_dev(c, batch, frames, frames, e->n_head, e->n_head, e->hd, e->q.f(), e->k.f(),
-                                      e->v.f(), scale, 0, 0, e->attn.f()));
-        SS_TRY(vokra_hip_qact_quantize_dev(c, e->qa_d, rows, e->attn.f(), act));
+        SS_TRY(vk::attn_quantize(c, batch, frames, frames, e->n_head, e->n_head, e->hd, e->q.f(), e->k.f(), e->v.f(),
+                                 scale, 0, 0, e->attn.f(), e->qa_d, act));
         SS_TRY(L.o.run(c, e->qa_d, e->h.f(), add_h));
         // MLP block (nn.rs:134-181)
         SS_TRY(vk::qact_ln_quantize(c, e->qa_d, rows, e->h.f(), L.ln2g.f(), L.ln2b.f(), kLnEps, act, e->x.f()));
@@ -314,8 +313,6 @@ int dec_setup(vokra_hip_decoder* m, const vokra_hip_decoder_layer_t* layers, con
     SS_TRY(m->f.alloc(c, rows * ff * sizeof(float)));
     SS_TRY(m->logits.alloc(c, rows * m->vocab * sizeof(float)));
     SS_TRY(m->lpart.alloc(c, rows * (size_t)vk::logits_n_vt((int)m->vocab) * sizeof(float2)));
-    SS_TRY(m->qh.alloc(c, rows * d * 2));
-    SS_TRY(m->ql.alloc(c, rows * d * 2));
     SS_TRY(m->lens.alloc(c, rows * sizeof(int)));
     SS_TRY(m->kvidx.alloc(c, m->n_layer * rows * sizeof(int)));
     SS_TRY(m->next.alloc(c, rows * sizeof(int)));
@@ -373,20 +370,24 @@ int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_
         float* qkv_o[3] = {m->q.f(), m->k.f(), m->v.f()};
         SS_TRY(vk::gemm_qact_multi(c, 3, qkv, m->qa_d, qkv_b, qkv_o));
         SS_TRY(vokra_hip_kv_append_dev(c, m->kv, l, n, d_streams, d_positions, m->k.f(), m->v.f()));
-        SS_TRY(vokra_hip_paged_attn_dev(c, m->kv, l, n, d_streams, m->lens.i(), m->n_text, m->n_head, m->q.f(), scale,
-                                        m->attn.f()));
-        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->attn.f(), act));
+        SS_TRY(vk::paged_attn_quantize(c, m->kv, l, n, d_streams, m->lens.i(), m->n_text, m->n_head, m->q.f(), scale,
+                                       m->attn.f(), m->qa_d, act));
         SS_TRY(L.o.run(c, m->qa_d, m->h.f(), add_h));
         // cross-attention over the stream's encoder frames (decoder.rs:492-510)
         SS_TRY(vk::qact_ln_quantize(c, m->qa_d, n, m->h.f(), L.ln2g.f(), L.ln2b.f(), kLnEps, act, m->x.f()));
         SS_TRY(L.cq.run(c, m->qa_d, m->q.f()));
-        SS_HIP(vk::launch_split_rows(s, m->q.f(), n * d, scale, m->qh.p, m->ql.p), "launch(vk_split_rows q)");
-        SS_HIP(vk::launch_flash_attn(s, (int)m->hd, m->qh.p, m->ql.p, m->ckh.p, m->ckl.p, m->cvh.p, m->cvl.p,
-                                     m->attn.f(), (int)n, 1, (int)m->n_audio, (int)m->t_pad, (int)m->n_head,
-                                     (int)m->n_head, 0, 0, m->kvidx.i() + l * n,
-                                     m->cross_precision == VOKRA_HIP_CROSS_F32),
+        // (q * scale split into fp16 hi / lo inside the kernel, which also
+        // runs the activation pass over its output rows when that has a
+        // fused form)
+        VkQOut qo;
+        SS_TRY(vk::qact_output(c, m->qa_d, n, act, &qo));
+        SS_HIP(vk::launch_flash_attn_f32q(s, (int)m->hd, m->q.f(), scale, m->ckh.p, m->ckl.p, m->cvh.p, m->cvl.p,
+                                          qo.afrag ? nullptr : m->attn.f(), (int)n, 1, (int)m->n_audio,
+                                          (int)m->t_pad, (int)m->n_head, (int)m->n_head, 0, 0, m->kvidx.i() + l * n,
+                                          m->cross_precision == VOKRA_HIP_CROSS_F32, qo.afrag ? &qo : nullptr),
                "launch(vk_flash_attn cross)");
-        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->attn.f(), act));
+        if (qo.afrag) vk::qact_outputs_written(m->qa_d, n, act);
+        else SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->attn.f(), act));
         SS_TRY(L.co.run(c, m->qa_d, m->h.f(), add_h));
         // MLP (decoder.rs:512-525)
         SS_TRY(vk::qact_ln_quantize(c, m->qa_d, n, m->h.f(), L.ln3g.f(), L.ln3b.f(), kLnEps, act, m->x.f()));
