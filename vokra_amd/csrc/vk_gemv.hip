@@ -378,9 +378,11 @@ hipError_t launch_repack_w_gemv(hipStream_t s, int mode, const uint8_t* wq, int 
 }
 
 // Which decode kernel: the wave-per-tile one streams weights faster once the
-// grid is large (>= ~1000 tiles, or a grouped launch), the two-phase one has
-// the shorter latency for a small grid (one memory round trip per workgroup).
-constexpr int kWptMinTiles = 1024;
+// grid is large (>= 512 tiles, or a grouped launch), the two-phase one has the
+// shorter latency for a small grid (one memory round trip per workgroup).
+// Measured at M=64: 320 tiles 6.5 us two-phase vs 7.3 wave-per-tile; the
+// decoder step (q/k/v: 960 tiles) 10.46 -> 10.39 ms with 512 rather than 1024.
+constexpr int kWptMinTiles = 512;
 
 template <int MODE, bool POW2, bool DEV>
 static hipError_t go(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum, const GemvSet& set,
