@@ -159,6 +159,7 @@ struct vokra_hip_kv {
         v.n_layer = (int)n_layer;
         v.n_stream = (int)n_stream;
         v.width = (int)width;
+        v.hd = (int)d_head;
         v.bs = (int)bs;
         v.ppl = (int)ppl;
         v.cap = (int)cap;

@@ -31,12 +31,25 @@ struct KvDev {
     int* meta;       // [0] free_len, [1] status of the last append, [2] items appended, [3] scratch,
                      // [4 ..) per item of the last append: 1 = overwritten by a later item
     int n_layer, n_stream, width, row_blocks, bs, ppl, cap, max_time;
+    int hd, nh, hb;  // head size, heads per row, 32-blocks per head
 };
 
 enum : int { KV_OK = 0, KV_INVALID = 5, KV_EXHAUSTED = 10 };  // vokra_hip_status_t values
 
-__device__ __forceinline__ size_t kv_slot(const KvDev& c, int pid, int t, int s) {
-    return ((size_t)pid * c.bs + (t % c.bs)) * c.n_stream + s;
+// Page layout: a page holds bs time steps of every stream; inside it the
+// head rows are ordered [stream][head][t % bs], so one head's keys of a page
+// are contiguous (bs x hd quants, bs x hd/32 scales) for the attention reads.
+// Head row index of (page, t, stream, head); its hd quants start at
+// hrow * hd in kq / vq and its hd/32 f16 scales at hrow * hb in kd / vd.
+__device__ __forceinline__ size_t kv_hrow(const KvDev& c, int pid, int t, int s, int h) {
+    return (((size_t)pid * c.n_stream + s) * c.nh + h) * c.bs + (t % c.bs);
+}
+// Offsets of row element e (0 .. width-1) of (page, t, stream): quant, scale.
+__device__ __forceinline__ size_t kv_qoff(const KvDev& c, int pid, int t, int s, int e) {
+    return kv_hrow(c, pid, t, s, e / c.hd) * c.hd + (e % c.hd);
+}
+__device__ __forceinline__ size_t kv_doff(const KvDev& c, int pid, int t, int s, int e) {
+    return kv_hrow(c, pid, t, s, e / c.hd) * c.hb + (e % c.hd) / 32;
 }
 
 // ---------------------------------------------------------------------------
@@ -152,12 +165,13 @@ __global__ void vk_kv_write(KvDev c, int layer, int n, const int* __restrict__ s
     q8_0_pack_lane(vv, e & 31, &qv, &dv);
     if (!live) return;
     const int pid = c.table[layer * c.ppl + t / c.bs];
-    const size_t slot = kv_slot(c, pid, t, s);
-    c.kq[slot * c.width + e] = qk;
-    c.vq[slot * c.width + e] = qv;
+    const size_t qo = kv_qoff(c, pid, t, s, e);
+    c.kq[qo] = qk;
+    c.vq[qo] = qv;
     if ((e & 31) == 0) {
-        c.kd[slot * c.row_blocks + e / 32] = dk;
-        c.vd[slot * c.row_blocks + e / 32] = dv;
+        const size_t dof = kv_doff(c, pid, t, s, e);
+        c.kd[dof] = dk;
+        c.vd[dof] = dv;
     }
 }
 
@@ -169,9 +183,9 @@ __global__ void vk_kv_read(KvDev c, int layer, int t, int s, float* __restrict__
     const int e = blockIdx.x * blockDim.x + threadIdx.x;
     if (e == 0) found[0] = pid >= 0 ? 1 : 0;
     if (pid < 0 || e >= c.width) return;
-    const size_t slot = kv_slot(c, pid, t, s);
-    out[e] = (float)c.kq[slot * c.width + e] * vk_f16_to_f32(c.kd[slot * c.row_blocks + e / 32]);
-    out[c.width + e] = (float)c.vq[slot * c.width + e] * vk_f16_to_f32(c.vd[slot * c.row_blocks + e / 32]);
+    const size_t qo = kv_qoff(c, pid, t, s, e), dof = kv_doff(c, pid, t, s, e);
+    out[e] = (float)c.kq[qo] * vk_f16_to_f32(c.kd[dof]);
+    out[c.width + e] = (float)c.vq[qo] * vk_f16_to_f32(c.vd[dof]);
 }
 
 // release_layer (paged_quant.rs:500-515): entries of `layer` in table order
@@ -288,7 +302,6 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
     const int s = streams[item];
     const int len = min(lens[item], c.max_time);
     const int k0 = split * keys_per_split, k1 = min(len, k0 + keys_per_split);
-    const size_t hcol = (size_t)hk * HD;
 
     for (int x = tid; x < G * HD; x += 256) {
         const int g = x / HD, e = x % HD;
@@ -315,12 +328,14 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
         int pid = c.table[layer * c.ppl + jt / c.bs];
         const bool has = kv_ok && pid >= 0;
         pid = max(pid, 0);
-        const size_t slot = kv_slot(c, pid, jt, s);
+        const size_t hr = kv_hrow(c, pid, jt, s, hk);
+        const uint16_t* kds = c.kd + hr * NB;
+        const uint16_t* vds = c.vd + hr * NB;
         float sc[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) sc[g] = 0.0f;
-        const uint4* kr = reinterpret_cast<const uint4*>(c.kq + slot * c.width + hcol);
-        const uint4* vr = reinterpret_cast<const uint4*>(c.vq + slot * c.width + hcol);
+        const uint4* kr = reinterpret_cast<const uint4*>(c.kq + hr * HD);
+        const uint4* vr = reinterpret_cast<const uint4*>(c.vq + hr * HD);
         float dv[NB];
         if constexpr (G == 1) {
             // one head: every load of the key's row is issued before any is
@@ -333,8 +348,8 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
                 kw[b][1] = kr[2 * b + 1];
                 vw[b][0] = vr[2 * b];
                 vw[b][1] = vr[2 * b + 1];
-                kd16[b] = c.kd[slot * c.row_blocks + hk * NB + b];
-                vd16[b] = c.vd[slot * c.row_blocks + hk * NB + b];
+                kd16[b] = kds[b];
+                vd16[b] = vds[b];
             }
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
@@ -360,7 +375,7 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
         } else {
 #pragma unroll 1
             for (int b = 0; b < NB; ++b) {
-                const float d = vk_f16_to_f32_hw(c.kd[slot * c.row_blocks + hk * NB + b]);
+                const float d = vk_f16_to_f32_hw(kds[b]);
                 const uint4 w0 = kr[2 * b], w1 = kr[2 * b + 1];
                 const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
                 float kf[32];  // the block's dequantized keys (exact products)
@@ -387,7 +402,7 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
             }
 #pragma unroll
             for (int b = 0; b < NB; ++b)
-                dv[b] = has ? vk_f16_to_f32_hw(c.vd[slot * c.row_blocks + hk * NB + b]) : 0.0f;
+                dv[b] = has ? vk_f16_to_f32_hw(vds[b]) : 0.0f;
         }
         // ---- chunk max per head
 #pragma unroll
@@ -558,7 +573,6 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
     const int s = streams[item];
     const int len = min(lens[item], c.max_time);
     const int k0 = split * keys_per_split, k1 = min(len, k0 + keys_per_split);
-    const size_t hcol = (size_t)hk * HD;
 
     // q * scale of head hh (zero for padding heads) as the S^T B operand:
     // lane (g, hh) holds dims 32b + 8g .. +7, split into fp16 hi + lo
@@ -592,7 +606,7 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
         // slot of key j0 + kk, kk = lane % 32 (lanes 32..63 repeat lanes 0..31)
         const int jk = j0 + (lane & 31);
         const int pid = jk < k1 ? c.table[trow + jk / c.bs] : -1;
-        const int slot = pid >= 0 ? (int)kv_slot(c, pid, jk, s) : 0;  // slot 0: in bounds, masked below
+        const int slot = pid >= 0 ? (int)kv_hrow(c, pid, jk, s, hk) : 0;  // row 0: in bounds, masked below
         const int has = pid >= 0 ? 1 : 0;
 
         // ---- issue every load of the tile
@@ -600,7 +614,7 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
 #pragma unroll
         for (int n = 0; n < 2; ++n) {
             const int sl = __shfl(slot, 8 * (hh >> 2) + 4 * n + (hh & 3), VK_WAVE);
-            const uint2* kr = reinterpret_cast<const uint2*>(c.kq + (size_t)sl * c.width + hcol);
+            const uint2* kr = reinterpret_cast<const uint2*>(c.kq + (size_t)sl * HD);
 #pragma unroll
             for (int b = 0; b < NB; ++b) kw[n][b] = kr[4 * b + g];
         }
@@ -610,14 +624,14 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
         for (int j = 0; j < 8; ++j) {
             const int sl = __shfl(slot, 8 * g + j, VK_WAVE);
             kval[j] = __shfl(has, 8 * g + j, VK_WAVE);
-            kds[j] = *reinterpret_cast<const uint2*>(c.kd + (size_t)sl * c.row_blocks + hk * NB);
-            vds[j] = *reinterpret_cast<const uint2*>(c.vd + (size_t)sl * c.row_blocks + hk * NB);
+            kds[j] = *reinterpret_cast<const uint2*>(c.kd + (size_t)sl * NB);
+            vds[j] = *reinterpret_cast<const uint2*>(c.vd + (size_t)sl * NB);
         }
         uint4 vw[4];  // V rows of keys 4va + t, dims 16vc .. +15
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int sl = __shfl(slot, 4 * va + t, VK_WAVE);
-            vw[t] = *reinterpret_cast<const uint4*>(c.vq + (size_t)sl * c.width + hcol + 16 * vc);
+            vw[t] = *reinterpret_cast<const uint4*>(c.vq + (size_t)sl * HD + 16 * vc);
         }
 
         // ---- S^T = K . (q hi + lo)^T per key subtile, block scales applied per block
@@ -798,6 +812,9 @@ static KvDev kv_view(const KvView& v) {
     c.ppl = v.ppl;
     c.cap = v.cap;
     c.max_time = v.max_time;
+    c.hd = v.hd;
+    c.nh = v.width / v.hd;
+    c.hb = v.hd / 32;
     return c;
 }
 
@@ -858,7 +875,7 @@ static bool go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* st
     // head_dim 128 with several query heads per kv head: the matrix-core
     // kernel (its slots travel through 32-bit lane shuffles; it moves q and
     // O as float4)
-    const bool small_slots = (size_t)c.cap * c.bs * c.n_stream <= (size_t)INT32_MAX;
+    const bool small_slots = (size_t)c.cap * c.bs * c.n_stream * c.nh <= (size_t)INT32_MAX;
     const bool aligned = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
                            reinterpret_cast<uintptr_t>(po)) & 15) == 0;
     if constexpr (HD == pg::HD && G >= 2) {

@@ -117,7 +117,7 @@ namespace vk {
 struct KvView {
     void *kq, *vq, *kd, *vd;
     int *table, *free_list, *meta;
-    int n_layer, n_stream, width, bs, ppl, cap, max_time;
+    int n_layer, n_stream, width, hd, bs, ppl, cap, max_time;
 };
 hipError_t launch_kv_append(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* times,
                             const float* k, const float* vv);
