@@ -656,6 +656,32 @@ int paged_attn_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t
     return VOKRA_HIP_OK;
 }
 
+int gemm_qact_quantize(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_qact* qa, const float* d_bias,
+                       float* d_out, VkEpi epi, vokra_hip_qact* qa_out, int act_quant) {
+    int st = check_gemm_qact(c, w, qa, d_out);
+    if (st) return st;
+    if (!qa_out || qa_out->k != w->n)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact_quantize: output activations must be %zu wide", w->n);
+    VkQOut qo;
+    st = qact_bind(c, qa_out, qa->m, act_quant, &qo);
+    if (st) return st;
+    const bool fused = qo.afrag && !w->kquant && qa->act_quant != VOKRA_HIP_ACT_KQUANT && !gemv_route(c, w, qa) &&
+                       w->n % 128 == 0 && w->n_pad == w->n && qa_out->k == w->n &&
+                       ((reinterpret_cast<uintptr_t>(d_bias) | reinterpret_cast<uintptr_t>(epi.resid)) & 15) == 0;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    if (!fused) {
+        st = run_gemm_qact(c, w, qa, d_bias, d_out, epi);
+        return st ? st : quantize_activations(c, qa_out, d_out, qa->m, w->n, act_quant);
+    }
+    VK_TRY(vk::launch_gemm_qblock(c->stream, qa->act_quant == VOKRA_HIP_ACT_POW2, (const uint4*)qa->frag.p,
+                                  (const float*)qa->scale.p, (const uint4*)w->frag.p, (const float*)w->scale.p,
+                                  d_bias, nullptr, (int)qa->m, (int)qa->m_pad, (int)w->n, (int)w->n_pad, (int)w->nb,
+                                  epi, &qo),
+           "launch(vk_gemm_qblock + activation pass)");
+    qact_commit(qa_out, qa->m, act_quant);
+    return VOKRA_HIP_OK;
+}
+
 int qact_output(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, int act_quant, VkQOut* qo) {
     return qact_bind(c, qa, m, act_quant, qo);
 }

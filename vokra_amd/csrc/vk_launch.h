@@ -29,8 +29,9 @@ struct VkGemmLin {
     const uint4* wfrag;
     const float* wscale;
     const float* bias;
-    float* out;
+    float* out;  // may be null when qo is set
     VkEpi epi;
+    VkQOut qo;   // qo.afrag != null: the activation pass over the outputs (n % 128 == 0)
 };
 // One linear of a decode-kernel launch: compact weights, optional bias, output [m, n].
 struct VkGemvLin {
@@ -64,7 +65,8 @@ hipError_t launch_repack_w_b32(hipStream_t s, int mode, const uint8_t* wq, int n
                                uint4* wfrag, float* wscale);
 hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
                               const uint4* wfrag, const float* wscale, const float* bias, float* out, int m,
-                              int m_pad, int n, int n_pad, int nb, VkEpi epi = {nullptr, 0});
+                              int m_pad, int n, int n_pad, int nb, VkEpi epi = {nullptr, 0},
+                              const VkQOut* qo = nullptr);
 // n_lin (1..3) linears of the same n over the same activations, one grid.
 hipError_t launch_gemm_qblock_multi(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
                                     const VkGemmLin* lins, int n_lin, int m, int m_pad, int n, int n_pad, int nb);
@@ -182,6 +184,11 @@ int qact_ln_quantize(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, const float
 //                         (d_out is then scratch: the fused kernel may skip it)
 //   paged_attn_quantize = vokra_hip_paged_attn_dev into d_out, then
 //                         vokra_hip_qact_quantize_dev of its n rows
+//   gemm_qact_quantize  = gemm_qact_epi into d_out, then vokra_hip_qact_quantize_dev
+//                         of its rows into qa_out (d_out is then scratch: the
+//                         fused block-GEMM epilogue skips it)
+int gemm_qact_quantize(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_qact* qa, const float* d_bias,
+                       float* d_out, VkEpi epi, vokra_hip_qact* qa_out, int act_quant);
 int attn_quantize(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t hq, size_t hkv, size_t hd,
                   const float* d_q, const float* d_k, const float* d_v, float scale, int causal, size_t q_off,
                   float* d_out, vokra_hip_qact* qa, int act_quant);

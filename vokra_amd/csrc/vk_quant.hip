@@ -392,7 +392,7 @@ struct GemmSet {
 // WT: 16 x 16 MFMA tiles per wave side (4: 64 x 64 waves, 128 x 128
 // workgroup tiles; 2: 32 x 32 waves, 64 x 64 workgroup tiles for grids that
 // would not fill the chip). Per-output arithmetic is the same for both.
-template <bool POW2, int WT>
+template <bool POW2, int WT, bool QOUT>
 __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
     const uint4* __restrict__ afrag, const float* __restrict__ ascale, const GemmSet set, int n_lin,
     int m, int n, int nb, int ldo, int m_pad, int n_pad) {
@@ -429,6 +429,7 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
     const float* __restrict__ bias = set.lin[li].bias;
     float* out = set.lin[li].out;
     const VkEpi epi = set.lin[li].epi;
+    const VkQOut qo = set.lin[li].qo;  // used when QOUT (every linear of the launch has it)
 
     // Per-thread slice of one stage: A fragments wave + q WAVES (q < APT), B
     // fragments likewise, and one scale (threads [0, TM): A rows, [TM, TM+TN):
@@ -557,7 +558,6 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
             const int rr = (64 / CPR) * q + lane / CPR;
             const int row = row_base + rr;
             float4 v = *reinterpret_cast<const float4*>(slot + rr * (16 * WT) + c4);
-            if (row >= m) continue;
             const size_t o = (size_t)row * ldo + col0 + c4;
             if (vec_ok) {
                 if (bias) {
@@ -569,8 +569,34 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
                 if (epi.resid) {  // resid + y, as the separate add pass
                     v.x = rv[q].x + v.x; v.y = rv[q].y + v.y; v.z = rv[q].z + v.z; v.w = rv[q].w + v.w;
                 }
-                __builtin_nontemporal_store((vk_f32x4){v.x, v.y, v.z, v.w}, reinterpret_cast<vk_f32x4*>(out + o));
-            } else {
+                if (QOUT) {
+                    // the activation pass over this row's 32-column block:
+                    // 8 consecutive lanes hold it (columns 4 (lane % 8) ..)
+                    float amax = fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fmaxf(fabsf(v.y), fabsf(v.z))), fabsf(v.w));
+                    amax = vk_group_max<8>(amax);
+                    float sc = 0.0f;
+                    int q4[4] = {0, 0, 0, 0};
+                    if (amax != 0.0f) {
+                        sc = vk_act_scale(amax, qo.pow2);
+                        q4[0] = vk_act_q(v.x, sc); q4[1] = vk_act_q(v.y, sc);
+                        q4[2] = vk_act_q(v.z, sc); q4[3] = vk_act_q(v.w, sc);
+                    }
+                    const int gs = vk_group_sum_i<8>((q4[0] + q4[1]) + (q4[2] + q4[3]));
+                    if (row < m) {
+                        const int col = col0 + c4, kb = col >> 5;
+                        const size_t at = vk_afrag_u16((size_t)row, kb, qo.k >> 5, col & 31);
+                        const uint32_t w0 = vk_act_bits(q4[0], sc, qo.pow2) | (vk_act_bits(q4[1], sc, qo.pow2) << 16);
+                        const uint32_t w1 = vk_act_bits(q4[2], sc, qo.pow2) | (vk_act_bits(q4[3], sc, qo.pow2) << 16);
+                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(qo.afrag) + at) = make_uint2(w0, w1);
+                        if ((lane & 7) == 0) {
+                            qo.ascale[(size_t)kb * qo.m_pad + row] = sc;
+                            qo.asum[(size_t)kb * qo.m_pad + row] = qo.pow2 ? (float)gs * sc : (float)gs;
+                        }
+                    }
+                }
+                if (row < m && out)
+                    __builtin_nontemporal_store((vk_f32x4){v.x, v.y, v.z, v.w}, reinterpret_cast<vk_f32x4*>(out + o));
+            } else if (row < m) {
                 const float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
@@ -586,14 +612,22 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
 template __global__ void vk_quantize_act_b32<false>(const float*, int, int, int, uint4*, float*, float*);
 template __global__ void vk_quantize_act_b32<true>(const float*, int, int, int, uint4*, float*, float*);
 
-template __global__ void vk_gemm_qblock<false, 4>(const uint4*, const float*, const GemmSet, int, int, int, int,
-                                                  int, int, int);
-template __global__ void vk_gemm_qblock<true, 4>(const uint4*, const float*, const GemmSet, int, int, int, int, int,
-                                                 int, int);
-template __global__ void vk_gemm_qblock<false, 2>(const uint4*, const float*, const GemmSet, int, int, int, int,
-                                                  int, int, int);
-template __global__ void vk_gemm_qblock<true, 2>(const uint4*, const float*, const GemmSet, int, int, int, int, int,
-                                                 int, int);
+template __global__ void vk_gemm_qblock<false, 4, false>(const uint4*, const float*, const GemmSet, int, int, int, int,
+                                                       int, int, int);
+template __global__ void vk_gemm_qblock<false, 4, true>(const uint4*, const float*, const GemmSet, int, int, int, int,
+                                                       int, int, int);
+template __global__ void vk_gemm_qblock<false, 2, false>(const uint4*, const float*, const GemmSet, int, int, int, int,
+                                                       int, int, int);
+template __global__ void vk_gemm_qblock<false, 2, true>(const uint4*, const float*, const GemmSet, int, int, int, int,
+                                                       int, int, int);
+template __global__ void vk_gemm_qblock<true, 4, false>(const uint4*, const float*, const GemmSet, int, int, int, int,
+                                                       int, int, int);
+template __global__ void vk_gemm_qblock<true, 4, true>(const uint4*, const float*, const GemmSet, int, int, int, int,
+                                                       int, int, int);
+template __global__ void vk_gemm_qblock<true, 2, false>(const uint4*, const float*, const GemmSet, int, int, int, int,
+                                                       int, int, int);
+template __global__ void vk_gemm_qblock<true, 2, true>(const uint4*, const float*, const GemmSet, int, int, int, int,
+                                                       int, int, int);
 
 }  // namespace vk
 
@@ -705,29 +739,35 @@ hipError_t launch_gemm_qblock_multi(hipStream_t s, bool pow2, const uint4* afrag
     for (int i = 0; i < n_lin; ++i) set.lin[i] = lins[i];
     // 128 x 128 workgroup tiles unless they leave CUs idle; then 64 x 64
     const int big = (n_pad / gemm::TN) * (m_pad / gemm::TM) * n_lin;
-    if (big >= kGemmSmallTileBelow) {
-        if (pow2)
-            hipLaunchKernelGGL((vk_gemm_qblock<true, 4>), dim3((unsigned)big), dim3(gemm::THREADS), 0, s, afrag, ascale,
-                               set, n_lin, m, n, nb, n, m_pad, n_pad);
-        else
-            hipLaunchKernelGGL((vk_gemm_qblock<false, 4>), dim3((unsigned)big), dim3(gemm::THREADS), 0, s, afrag,
-                               ascale, set, n_lin, m, n, nb, n, m_pad, n_pad);
+    const bool small = big < kGemmSmallTileBelow;
+    bool qout = lins[0].qo.afrag != nullptr;
+    for (int i = 1; i < n_lin; ++i)
+        if ((lins[i].qo.afrag != nullptr) != qout) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(small ? big * 4 : big)), block(gemm::THREADS);
+#define VK_GQ(P, W, Q) hipLaunchKernelGGL((vk_gemm_qblock<P, W, Q>), grid, block, 0, s, afrag, ascale, set, n_lin, m, n, \
+                                          nb, n, m_pad, n_pad)
+    if (pow2) {
+        if (small) { if (qout) VK_GQ(true, 2, true); else VK_GQ(true, 2, false); }
+        else { if (qout) VK_GQ(true, 4, true); else VK_GQ(true, 4, false); }
     } else {
-        const unsigned small = (unsigned)big * 4;
-        if (pow2)
-            hipLaunchKernelGGL((vk_gemm_qblock<true, 2>), dim3(small), dim3(gemm::THREADS), 0, s, afrag, ascale, set,
-                               n_lin, m, n, nb, n, m_pad, n_pad);
-        else
-            hipLaunchKernelGGL((vk_gemm_qblock<false, 2>), dim3(small), dim3(gemm::THREADS), 0, s, afrag, ascale, set,
-                               n_lin, m, n, nb, n, m_pad, n_pad);
+        if (small) { if (qout) VK_GQ(false, 2, true); else VK_GQ(false, 2, false); }
+        else { if (qout) VK_GQ(false, 4, true); else VK_GQ(false, 4, false); }
     }
+#undef VK_GQ
     return hipGetLastError();
 }
 
 hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
                               const uint4* wfrag, const float* wscale, const float* bias, float* out,
-                              int m, int m_pad, int n, int n_pad, int nb, VkEpi epi) {
-    const VkGemmLin lin = {wfrag, wscale, bias, out, epi};
+                              int m, int m_pad, int n, int n_pad, int nb, VkEpi epi, const VkQOut* qo) {
+    // the fused pass runs in the vector epilogue: whole 128-column tiles and
+    // 16-byte aligned rows
+    if (qo && qo->afrag &&
+        (n % 128 != 0 || n_pad != n || qo->k != n || qo->m_pad != m_pad ||
+         ((reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(epi.resid) |
+           reinterpret_cast<uintptr_t>(out)) & 15) != 0))
+        return hipErrorInvalidValue;
+    const VkGemmLin lin = {wfrag, wscale, bias, out, epi, qo ? *qo : VkQOut{}};
     return launch_gemm_qblock_multi(s, pow2, afrag, ascale, &lin, 1, m, m_pad, n, n_pad, nb);
 }
 

@@ -87,6 +87,12 @@ struct QLin {
     int run(vokra_hip_ctx_t* c, const vokra_hip_qact_t* qa, float* d_out, VkEpi epi = {nullptr, 0}) const {
         return vk::gemm_qact_epi(c, w, qa, b(), d_out, epi);
     }
+    // the same, then the activation pass over the outputs into qa_out (fused
+    // into the GEMM epilogue where it has a fused form; d_out is scratch)
+    int run_quantize(vokra_hip_ctx_t* c, const vokra_hip_qact_t* qa, float* d_out, VkEpi epi,
+                     vokra_hip_qact_t* qa_out, int act) const {
+        return vk::gemm_qact_quantize(c, w, qa, b(), d_out, epi, qa_out, act);
+    }
     const float* b() const { return has_bias ? bias.f() : nullptr; }
     void release(vokra_hip_ctx_t* c) {
         vokra_hip_qweight_free(w);
@@ -231,8 +237,7 @@ int enc_forward(vokra_hip_encoder* e, size_t batch, size_t frames, const float* 
         SS_TRY(L.o.run(c, e->qa_d, e->h.f(), add_h));
         // MLP block (nn.rs:134-181)
         SS_TRY(vk::qact_ln_quantize(c, e->qa_d, rows, e->h.f(), L.ln2g.f(), L.ln2b.f(), kLnEps, act, e->x.f()));
-        SS_TRY(L.fc1.run(c, e->qa_d, e->f.f(), gelu));
-        SS_TRY(vokra_hip_qact_quantize_dev(c, e->qa_f, rows, e->f.f(), act));
+        SS_TRY(L.fc1.run_quantize(c, e->qa_d, e->f.f(), gelu, e->qa_f, act));
         SS_TRY(L.fc2.run(c, e->qa_f, e->h.f(), add_h));
     }
     return vokra_hip_layer_norm_f32_dev(c, e->h.f(), d_out, rows, d, e->lnpg.f(), e->lnpb.f(), kLnEps);
@@ -391,8 +396,7 @@ int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_
         SS_TRY(L.co.run(c, m->qa_d, m->h.f(), add_h));
         // MLP (decoder.rs:512-525)
         SS_TRY(vk::qact_ln_quantize(c, m->qa_d, n, m->h.f(), L.ln3g.f(), L.ln3b.f(), kLnEps, act, m->x.f()));
-        SS_TRY(L.fc1.run(c, m->qa_d, m->f.f(), gelu));
-        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_f, n, m->f.f(), act));
+        SS_TRY(L.fc1.run_quantize(c, m->qa_d, m->f.f(), gelu, m->qa_f, act));
         SS_TRY(L.fc2.run(c, m->qa_f, m->h.f(), add_h));
     }
     // ln_post, then tied logits (decoder.rs:754-796) and greedy argmax in one
