@@ -451,7 +451,8 @@ int kv_split(const vokra_hip_kv* kv, size_t n, size_t max_len, size_t hkv, int* 
 
 int run_paged_attn(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                    const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
-                   const VkQOut* qo = nullptr) {
+                   const VkQOut* qo = nullptr, const float* d_ak = nullptr, const float* d_av = nullptr,
+                   const int* d_at = nullptr) {
     const size_t hkv = kv->n_head;
     int n_split = 1, kps = 256;
     kv_split(kv, n, max_len ? max_len : 1, hkv, &n_split, &kps);
@@ -461,7 +462,7 @@ int run_paged_attn(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, c
     }
     VK_TRY(vk::launch_paged_attn(c->stream, kv->view(), (int)layer, (int)n, d_streams, d_lens, d_q, scale, (int)hq,
                                  (int)kv->d_head, n_split, kps, d_out, (float*)kv->part_ml.p, (float*)kv->part_o.p,
-                                 qo),
+                                 qo, d_ak, d_av, d_at),
            "launch(vk_paged_attn)");
     return VOKRA_HIP_OK;
 }
@@ -680,6 +681,45 @@ int gemm_qact_quantize(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra
            "launch(vk_gemm_qblock + activation pass)");
     qact_commit(qa_out, qa->m, act_quant);
     return VOKRA_HIP_OK;
+}
+
+int kv_alloc_layers(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer0, size_t n_layers, size_t n,
+                    const int* d_streams, const int* d_times) {
+    if (!c || !kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: bad context or cache");
+    if (n_layers == 0 || layer0 + n_layers > kv->n_layer || n * n_layers > 4096)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: %zu layers from %zu of %zu, %zu items", n_layers,
+                    layer0, kv->n_layer, n);
+    if (n && (!d_streams || !d_times)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_kv_alloc_layers(c->stream, kv->view(), (int)layer0, (int)n_layers, (int)n, d_streams, d_times),
+           "launch(vk_kv_alloc_layers)");
+    return VOKRA_HIP_OK;
+}
+
+int paged_attn_append_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
+                               const int* d_times, const float* d_k, const float* d_v, const int* d_lens,
+                               size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
+                               vokra_hip_qact* qa, int act_quant) {
+    if (!kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn: bad context or cache");
+    int st = check_paged_attn(kv, layer, n, hq);
+    if (st) return st;
+    if (n == 0) return VOKRA_HIP_OK;
+    if (!d_streams || !d_times || !d_k || !d_v || !d_lens || !d_q || !d_out)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn: NULL buffer");
+    VkQOut qo;
+    st = qact_bind(c, qa, n, act_quant, &qo);
+    if (st) return st;
+    if (qa->k != hq * kv->d_head) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn: qact width");
+    if (max_len > kv->max_time) max_len = kv->max_time;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    st = run_paged_attn(c, kv, layer, n, d_streams, d_lens, max_len, hq, d_q, scale, d_out, qo.afrag ? &qo : nullptr,
+                        d_k, d_v, d_times);
+    if (st) return st;
+    if (qo.afrag) {
+        qact_commit(qa, n, act_quant);
+        return VOKRA_HIP_OK;
+    }
+    return vokra_hip_qact_quantize_dev(c, qa, n, d_out, act_quant);
 }
 
 int qact_output(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, int act_quant, VkQOut* qo) {

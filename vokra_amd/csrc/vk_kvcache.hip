@@ -130,6 +130,92 @@ __global__ __launch_bounds__(1024) void vk_kv_alloc(KvDev c, int layer, int n, c
     }
 }
 
+// Allocation for the same items appended to layers layer0 .. layer0+nl-1 in
+// that order (item q = l * n + i, as n append_step calls per layer, layer
+// after layer), in one launch: the r-th item whose table entry is empty and
+// which is the first of its layer's batch with that entry pops
+// free_list[free_len - 1 - r]; the first invalid or unservable item ends the
+// batch. Writes the table, free_len, the status and the appended count
+// (meta[2], in items q); no per-item overwrite flags (its caller appends
+// distinct streams). One workgroup of 1024 threads; nl * n <= 4096.
+__global__ __launch_bounds__(1024) void vk_kv_alloc_layers(KvDev c, int layer0, int nl, int n,
+                                                           const int* __restrict__ streams,
+                                                           const int* __restrict__ times) {
+    constexpr int QMAX = 4096, U = QMAX / 1024;
+    __shared__ int s_ti[QMAX];
+    __shared__ int s_rank[QMAX];
+    __shared__ int s_scan[1024];
+    __shared__ int s_bad, s_total;
+    const int tid = threadIdx.x, N = nl * n;
+    bool valid[U], first[U];
+    int ti[U];
+    if (tid == 0) { s_bad = N; s_total = 0; }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int q = 1024 * u + tid;
+        valid[u] = false;
+        ti[u] = -1;
+        if (q < N) {
+            const int l = layer0 + q / n, i = q % n;
+            const int s = streams[i], t = times[i];
+            valid[u] = l >= 0 && l < c.n_layer && s >= 0 && s < c.n_stream && t >= 0 && t < c.max_time;
+            ti[u] = valid[u] ? l * c.ppl + t / c.bs : -1;
+            s_ti[q] = ti[u];
+        }
+    }
+    __syncthreads();
+    const int free_len = c.meta[0];
+    int base = 0;  // first-flags of earlier chunks
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int q = 1024 * u + tid;
+        first[u] = false;
+        if (valid[u] && c.table[ti[u]] < 0) {
+            first[u] = true;
+            for (int j = q - q % n; j < q; ++j)  // earlier items of the same layer
+                if (s_ti[j] == ti[u]) {
+                    first[u] = false;
+                    break;
+                }
+        }
+        // inclusive scan of this chunk's flags (Hillis-Steele)
+        s_scan[tid] = first[u] ? 1 : 0;
+        __syncthreads();
+        for (int off = 1; off < 1024; off <<= 1) {
+            const int v = tid >= off ? s_scan[tid - off] : 0;
+            __syncthreads();
+            s_scan[tid] += v;
+            __syncthreads();
+        }
+        const int rank = base + s_scan[tid] - (first[u] ? 1 : 0);
+        if (q < N && (!valid[u] || (first[u] && rank >= free_len))) atomicMin(&s_bad, q);
+        if (q < N) s_rank[q] = rank;
+        base += s_scan[1023];
+        __syncthreads();
+    }
+    const int bad = s_bad;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int q = 1024 * u + tid;
+        if (first[u] && q < bad) {
+            c.table[ti[u]] = c.free_list[free_len - 1 - s_rank[q]];
+            atomicAdd(&s_total, 1);
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int status = KV_OK;
+        if (bad < N) {
+            const int i = bad % n, l = layer0 + bad / n, sf = streams[i], tf = times[i];
+            const bool vf = l >= 0 && l < c.n_layer && sf >= 0 && sf < c.n_stream && tf >= 0 && tf < c.max_time;
+            status = vf ? KV_EXHAUSTED : KV_INVALID;
+        }
+        c.meta[0] = free_len - s_total;
+        c.meta[1] = status;
+        c.meta[2] = bad;
+    }
+}
+
 // Packs the K and V rows of the appended items into their slots. One thread
 // per (item, 32-element block, element); 32 consecutive threads form a block.
 // Same arithmetic as BlockQ8_0::pack: amax = max |x|, d = amax / 127,
@@ -281,7 +367,9 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
                                                      const int* __restrict__ lens, const float* __restrict__ q,
                                                      float scale, int hq, int n_split, int keys_per_split,
                                                      float* __restrict__ out, float* __restrict__ part_ml,
-                                                     float* __restrict__ part_o, const VkQOut qo) {
+                                                     float* __restrict__ part_o, const VkQOut qo,
+                                                     const float* __restrict__ ak, const float* __restrict__ av,
+                                                     const int* __restrict__ at) {
     constexpr int NB = HD / 32;            // blocks per head slice
     constexpr int NO = G * HD;             // outputs of the workgroup
     // P.V work unit: a quad of 4 consecutive outputs of one head (one 32-bit
@@ -303,6 +391,32 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
     const int len = min(lens[item], c.max_time);
     const int k0 = split * keys_per_split, k1 = min(len, k0 + keys_per_split);
 
+    // Fused append (ak != null): the workgroup whose key range holds the
+    // item's new time step packs that step's K and V head slices into the
+    // cache first, exactly as vk_kv_write would, then reads them back with
+    // the other keys. The page comes from an earlier allocation launch.
+    if (ak) {
+        const int t = at[item];
+        if (t >= k0 && t < k1) {  // uniform per workgroup
+            const int pid = c.table[layer * c.ppl + t / c.bs];
+            if (pid >= 0 && wave < 2) {
+                const size_t hr = kv_hrow(c, pid, t, s, hk);
+                const float* src = (wave == 0 ? ak : av) + (size_t)item * c.width + (size_t)hk * HD;
+                int8_t* dq = (wave == 0 ? c.kq : c.vq) + hr * HD;
+                uint16_t* dd = (wave == 0 ? c.kd : c.vd) + hr * NB;
+#pragma unroll
+                for (int e = lane; e < HD; e += 64) {
+                    int8_t qb;
+                    uint16_t db = 0;
+                    q8_0_pack_lane(src[e], e & 31, &qb, &db);
+                    dq[e] = qb;
+                    if ((e & 31) == 0) dd[e >> 5] = db;
+                }
+            }
+            __threadfence_block();
+            __syncthreads();
+        }
+    }
     for (int x = tid; x < G * HD; x += 256) {
         const int g = x / HD, e = x % HD;
         lq[g][e] = q[((size_t)item * hq + hk * G + g) * HD + e] * scale;
@@ -834,6 +948,14 @@ hipError_t launch_kv_append(hipStream_t s, const KvView& v, int layer, int n, co
     return hipGetLastError();
 }
 
+hipError_t launch_kv_alloc_layers(hipStream_t s, const KvView& v, int layer0, int n_layers, int n, const int* streams,
+                                  const int* times) {
+    if (n_layers < 1 || n < 0 || (size_t)n_layers * n > 4096) return hipErrorInvalidValue;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_kv_alloc_layers, dim3(1), dim3(1024), 0, s, kv_view(v), layer0, n_layers, n, streams, times);
+    return hipGetLastError();
+}
+
 hipError_t launch_kv_read(hipStream_t s, const KvView& v, int layer, int t, int st, float* out, int* found) {
     hipLaunchKernelGGL(vk_kv_read, dim3((unsigned)((v.width + 255) / 256)), dim3(256), 0, s, kv_view(v), layer, t, st,
                        out, found);
@@ -867,11 +989,13 @@ hipError_t launch_kv_page_of(hipStream_t s, const KvView& v, int layer, int t, i
     return hipGetLastError();
 }
 
-// Returns whether the kernel that ran also quantized the output (qo).
+// Returns whether the kernel that ran also quantized the output (qo). A fused
+// append (ak) runs only in the generic kernel: the caller routes by
+// paged_attn_fuses_append.
 template <int HD, int G>
 static bool go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* streams, const int* lens,
                   const float* q, float scale, int hq, int hkv, int n_split, int kps, float* out, float* pml,
-                  float* po, const VkQOut& qo) {
+                  float* po, const VkQOut& qo, const float* ak, const float* av, const int* at) {
     // head_dim 128 with several query heads per kv head: the matrix-core
     // kernel (its slots travel through 32-bit lane shuffles; it moves q and
     // O as float4)
@@ -879,20 +1003,21 @@ static bool go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* st
     const bool aligned = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
                            reinterpret_cast<uintptr_t>(po)) & 15) == 0;
     if constexpr (HD == pg::HD && G >= 2) {
-        if (small_slots && aligned) {
+        if (small_slots && aligned && !ak) {
             hipLaunchKernelGGL((vk_paged_attn_gqa<G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams,
                                lens, q, scale, hq, n_split, kps, out, pml, po);
             return false;
         }
     }
     hipLaunchKernelGGL((vk_paged_attn<HD, G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams, lens, q,
-                       scale, hq, n_split, kps, out, pml, po, n_split == 1 ? qo : VkQOut{});
+                       scale, hq, n_split, kps, out, pml, po, n_split == 1 ? qo : VkQOut{}, ak, av, at);
     return n_split == 1 && qo.afrag;
 }
 
 hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* lens,
                              const float* q, float scale, int hq, int hd, int n_split, int keys_per_split, float* out,
-                             float* part_ml, float* part_o, const VkQOut* qo) {
+                             float* part_ml, float* part_o, const VkQOut* qo, const float* ak, const float* av,
+                             const int* at) {
     const KvDev c = kv_view(v);
     const int hkv = v.width / hd, g = hq / hkv;
     const VkQOut qz = qo ? *qo : VkQOut{};
@@ -900,7 +1025,7 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
 #define VK_PA(HDV, GV)                                                                                          \
     if (hd == HDV && g == GV) {                                                                                 \
         fused = go_pa<HDV, GV>(s, c, layer, n, streams, lens, q, scale, hq, hkv, n_split, keys_per_split, out,  \
-                               part_ml, part_o, qz);                                                            \
+                               part_ml, part_o, qz, ak, av, at);                                                \
     } else
     VK_PA(64, 1) VK_PA(64, 2) VK_PA(64, 4) VK_PA(64, 8) VK_PA(128, 1) VK_PA(128, 2) VK_PA(128, 4) VK_PA(128, 8) {
         return hipErrorInvalidValue;

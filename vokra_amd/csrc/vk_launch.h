@@ -130,7 +130,15 @@ hipError_t launch_kv_page_of(hipStream_t s, const KvView& v, int layer, int t, i
 hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* lens,
                              const float* q, float scale, int hq, int hd, int n_split, int keys_per_split, float* out,
                              float* part_ml, float* part_o,
-                             const VkQOut* qo = nullptr);  // also the activation pass over out (rows = items)
+                             const VkQOut* qo = nullptr,  // also the activation pass over out (rows = items)
+                             // fused append: item i's K / V rows (ak, av [n][width]) at time at[i] are
+                             // packed into pages allocated beforehand (distinct streams; the generic
+                             // kernel runs every head shape then)
+                             const float* ak = nullptr, const float* av = nullptr, const int* at = nullptr);
+// The allocation of launch_kv_append for the same items appended to layers
+// layer0 .. layer0 + n_layers - 1 in that order, in one launch (n_layers * n <= 4096).
+hipError_t launch_kv_alloc_layers(hipStream_t s, const KvView& v, int layer0, int n_layers, int n, const int* streams,
+                                  const int* times);
 }  // namespace vk
 
 namespace vk {
@@ -195,6 +203,16 @@ int attn_quantize(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t 
 int paged_attn_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                         const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
                         vokra_hip_qact* qa, int act_quant);
+//   kv_alloc_layers + paged_attn_append_quantize (one per layer, in layer
+//   order) = per layer vokra_hip_kv_append_dev of the items' K / V rows at
+//   d_times, then paged_attn_quantize; for distinct streams whose new time
+//   step lies inside d_lens, and a cache with room for every append.
+int kv_alloc_layers(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer0, size_t n_layers, size_t n,
+                    const int* d_streams, const int* d_times);
+int paged_attn_append_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
+                               const int* d_times, const float* d_k, const float* d_v, const int* d_lens,
+                               size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
+                               vokra_hip_qact* qa, int act_quant);
 // For a session's own fused producer: the output binding of an activation
 // pass over m rows of qa (qo->afrag NULL: no fused form, run the pass), and
 // the record of it once the producer is launched.

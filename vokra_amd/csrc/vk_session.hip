@@ -363,6 +363,11 @@ int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_
     hipLaunchKernelGGL(vk::vk_step_index, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, s, d_streams, d_positions, (int)n,
                        (int)m->n_layer, m->lens.i(), m->kvidx.i());
     SS_HIP(hipGetLastError(), "launch(vk_step_index)");
+    // the self-attention cache pages of this step, every layer in layer order
+    // (the same pages as one append per layer); each layer's attention kernel
+    // then packs its new K / V rows into them
+    for (size_t l0 = 0, per = std::max<size_t>(1, 4096 / n); l0 < m->n_layer; l0 += per)
+        SS_TRY(vk::kv_alloc_layers(c, m->kv, l0, std::min(per, m->n_layer - l0), n, d_streams, d_positions));
     // The same fusions as the encoder (LN + quantize, out-proj + residual,
     // fc1 + GELU, q/k/v in one launch); results equal the entry-point sequence.
     const VkEpi add_h = {m->h.f(), 0}, gelu = {nullptr, 1};
@@ -374,9 +379,8 @@ int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_
         const float* qkv_b[3] = {L.q.b(), L.k.b(), L.v.b()};
         float* qkv_o[3] = {m->q.f(), m->k.f(), m->v.f()};
         SS_TRY(vk::gemm_qact_multi(c, 3, qkv, m->qa_d, qkv_b, qkv_o));
-        SS_TRY(vokra_hip_kv_append_dev(c, m->kv, l, n, d_streams, d_positions, m->k.f(), m->v.f()));
-        SS_TRY(vk::paged_attn_quantize(c, m->kv, l, n, d_streams, m->lens.i(), m->n_text, m->n_head, m->q.f(), scale,
-                                       m->attn.f(), m->qa_d, act));
+        SS_TRY(vk::paged_attn_append_quantize(c, m->kv, l, n, d_streams, d_positions, m->k.f(), m->v.f(), m->lens.i(),
+                                              m->n_text, m->n_head, m->q.f(), scale, m->attn.f(), m->qa_d, act));
         SS_TRY(L.o.run(c, m->qa_d, m->h.f(), add_h));
         // cross-attention over the stream's encoder frames (decoder.rs:492-510)
         SS_TRY(vk::qact_ln_quantize(c, m->qa_d, n, m->h.f(), L.ln2g.f(), L.ln2b.f(), kLnEps, act, m->x.f()));
