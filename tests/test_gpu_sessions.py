@@ -309,3 +309,18 @@ def test_decoder_cross_f16_mode(ctx, oracle):
         assert np.array_equal(a, b)
     with pytest.raises(hip.InvalidArgument):
         gpu.set_cross_precision(7)
+
+
+def test_decoder_long_context_split_attention(ctx, oracle):
+    """Positions past the first 256-key split (the paged-attention kernel then
+    splits keys and the split holding the new step packs it into the cache):
+    still bit-identical to the entry points issued one at a time."""
+    print("[case] decoder long context", flush=True)
+    gpu, _ = make_decoder(ctx, oracle, np.random.default_rng(9), n_text=600)
+    ops = DecoderByOps(ctx, gpu.parts, 4)
+    streams, tok, pos = [0, 1, 2, 3], [5, 6, 7, 8], [300, 450, 10, 599]
+    for _ in range(2):
+        nxt, logits = gpu.step(streams, tok, pos, want_logits=True)
+        n2, l2 = ops.step(streams, tok, pos)
+        assert np.array_equal(logits, l2) and np.array_equal(nxt, n2), pos
+        tok, pos = [int(t) for t in nxt], [min(p + 1, 599) for p in pos]
