@@ -153,13 +153,15 @@ __device__ __forceinline__ float vk_epi_apply(float v, const VkEpi& e, size_t id
 
 // Sum over a 256-thread workgroup (4 waves): wave shuffle tree, then
 // (w0 + w1) + (w2 + w3). `red` is 4 floats of LDS. Every row-reduction kernel
-// that must agree bit for bit with another uses this one.
+// that must agree bit for bit with another uses this one. Its barriers wait
+// for LDS only (not for global loads in flight), so a caller's prefetch of
+// the next row stays in flight across the reduction.
 __device__ __forceinline__ float vk_block_sum256(float v, float* red) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, VK_WAVE);
-    __syncthreads();
+    VK_LDS_BARRIER();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
+    VK_LDS_BARRIER();
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
