@@ -300,15 +300,22 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
         }
         // ---- mask, online softmax (per query = per lane, across lanes g)
         float mloc = -INFINITY;
+        if (!causal && kt * KT + KT <= tkv) {  // a whole tile of live keys: nothing to mask
 #pragma unroll
-        for (int n = 0; n < 4; ++n)
+            for (int n = 0; n < 4; ++n)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = kt * KT + 16 * n + 4 * g + r;
-                const bool ok = key < tkv && (!causal || key <= q_off + q_idx);
-                s[n][r] = ok ? s[n][r] : -INFINITY;
-                mloc = fmaxf(mloc, s[n][r]);
-            }
+                for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[n][r]);
+        } else {
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = kt * KT + 16 * n + 4 * g + r;
+                    const bool ok = key < tkv && (!causal || key <= q_off + q_idx);
+                    s[n][r] = ok ? s[n][r] : -INFINITY;
+                    mloc = fmaxf(mloc, s[n][r]);
+                }
+        }
         mloc = fmaxf(mloc, __shfl_xor(mloc, 16, VK_WAVE));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, VK_WAVE));
         const float m_new = fmaxf(m_run, mloc);
@@ -334,10 +341,13 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
         psum += __shfl_xor(psum, 32, VK_WAVE);
         l_run = l_run * alpha + psum;
         m_run = m_new;
+        // o * 1.0f is o: when no lane's running max moved, the rescale is skipped
+        if (__any(alpha != 1.0f)) {
 #pragma unroll
-        for (int os = 0; os < OS; ++os)
+            for (int os = 0; os < OS; ++os)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o_acc[os][r] *= alpha;
+                for (int r = 0; r < 4; ++r) o_acc[os][r] *= alpha;
+        }
         // ---- O^T += V^T . P^T over 2 key steps of 32: MFMA k-index 8g + 4j + r
         //      is key 32ks + 16j + 4g + r (the lane's P values, in order)
 #pragma unroll
