@@ -353,6 +353,9 @@ __global__ void vk_repack_w_b32(int mode, const uint8_t* __restrict__ wq, int n,
 // Workgroup tile 128 (m) x 128 (n): 4 waves in 2 x 2, wave tile 64 x 64 =
 // 4 x 4 MFMA tiles, one quant block (K = 32) per pipeline stage; two
 // workgroups per CU, so one's barrier wait overlaps the other's compute.
+// Grids that would fill less than three quarters of the chip with such
+// tiles run 32 x 32 wave tiles (64 x 64 workgroup tiles, four times the
+// workgroups) with the same per-output arithmetic.
 // Operands move global -> LDS directly (no staging registers) through a
 // three-stage ring. Inside a wave the MFMAs of a block are interleaved with
 // the VALU combine of earlier tiles, so the matrix core runs under the VALU
