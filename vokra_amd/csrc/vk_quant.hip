@@ -259,6 +259,16 @@ __global__ __launch_bounds__(256) void vk_ln_quantize_b32(const float* __restric
     const int mt = TILE ? (int)blockIdx.x : (int)blockIdx.x >> 4;
     uint16_t* tile16 = TILE ? reinterpret_cast<uint16_t*>(lds_tile)
                             : reinterpret_cast<uint16_t*>(afrag + (size_t)mt * nb * 64);
+    // gamma and beta in registers up front: a global load inside the row
+    // loop would make its wait (loads retire in order) also wait for the
+    // next row's prefetch
+    float gv[kLnRegJ], bv[kLnRegJ];
+#pragma unroll
+    for (int j = 0; j < kLnRegJ; ++j) {
+        const int c = t + 256 * j;
+        gv[j] = c < k ? gamma[c] : 0.0f;
+        bv[j] = c < k ? beta[c] : 0.0f;
+    }
     // TILE: the rows are unrolled and row r+1 is loaded while row r reduces
     float xn[kLnRegJ];
     {
@@ -280,7 +290,7 @@ __global__ __launch_bounds__(256) void vk_ln_quantize_b32(const float* __restric
         for (int j = 0; j < kLnRegJ; ++j) {
             const int c = t + 256 * j;
             if (c - (t & 31) >= k) break;  // k is a multiple of 32: whole half-waves
-            const float v = live ? vk_ln_apply(x[j], st, gamma[c], beta[c]) : 0.0f;
+            const float v = live ? vk_ln_apply(x[j], st, gv[j], bv[j]) : 0.0f;
             // from 0 and through fmaxf, as the separate pass: NaN elements are ignored
             const float amax = vk_group_max<32>(fmaxf(0.0f, fabsf(v)));
             float s = 0.0f;
