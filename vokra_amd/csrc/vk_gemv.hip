@@ -153,12 +153,16 @@ __global__ __launch_bounds__(256) void vk_gemv_qblock(
     const int rq = 4 * (lane >> 4);        // first of this lane's 4 D rows
 
     float acc = 0.0f;                      // phase 2: output (row tid/16, col tid%16)
-    for (int g0 = 0; g0 < G; g0 += CB / GB) {
-        const int gn = min(CB / GB, G - g0);  // groups in this chunk
-        // ---- phase 1 loads (everything for this wave's groups, up front)
-        uint4 wq[GPW][WQ];
-        uint2 ws[GPW];
-        uint4 af[GPW][GB];
+    // Operands of one chunk (everything for this wave's groups, plus the
+    // chunk's activation scales and operand sums, 3 of each per thread). The
+    // next chunk's are loaded into the same registers once phase 1 has used
+    // them, so they are in flight during phase 2.
+    uint4 wq[GPW][WQ];
+    uint2 ws[GPW];
+    uint4 af[GPW][GB];
+    float sv[CB * 16 / 256], tv[CB * 16 / 256];
+    auto load_chunk = [&](int g0) {
+        const int gn = min(CB / GB, G - g0);
 #pragma unroll
         for (int j = 0; j < GPW; ++j) {
             const int gl = min(wave + WAVES * j, gn - 1);  // clamped: loads stay in bounds
@@ -170,9 +174,6 @@ __global__ __launch_bounds__(256) void vk_gemv_qblock(
 #pragma unroll
             for (int u = 0; u < GB; ++u) af[j][u] = afrag[((size_t)mt * nb + g * GB + u) * FRAG_U4 + lane];
         }
-        // activation scales and operand sums of the chunk: 16 rows x gn*GB
-        // blocks, loaded once per workgroup (3 values of each per thread)
-        float sv[CB * 16 / 256], tv[CB * 16 / 256];
 #pragma unroll
         for (int h = 0; h < CB * 16 / 256; ++h) {
             const int idx = min(tid + 256 * h, gn * GB * 16 - 1);
@@ -181,6 +182,10 @@ __global__ __launch_bounds__(256) void vk_gemv_qblock(
             sv[h] = ascale[o];
             tv[h] = asum[o];
         }
+    };
+    load_chunk(0);
+    for (int g0 = 0; g0 < G; g0 += CB / GB) {
+        const int gn = min(CB / GB, G - g0);  // groups in this chunk
 #pragma unroll
         for (int h = 0; h < CB * 16 / 256; ++h) {
             const int idx = tid + 256 * h;
@@ -218,6 +223,7 @@ __global__ __launch_bounds__(256) void vk_gemv_qblock(
             }
         }
         VK_LDS_BARRIER();
+        if (g0 + CB / GB < G) load_chunk(g0 + CB / GB);  // uniform
         // ---- phase 2: ordered combine, one thread per output
         const int row = tid >> 4, col = tid & 15;
         // gn*GB is a multiple of 4: the reads of 4 blocks are issued together
