@@ -109,7 +109,7 @@ __global__ __launch_bounds__(256) void vk_split_vt(const float* __restrict__ v, 
 }
 
 // ---------------------------------------------------------------------------
-template <int HD, bool LO>
+template <int HD, bool LO, bool ONEQ>
 __global__ __launch_bounds__(256) void vk_flash_attn(
     const uint4* __restrict__ qh, const uint4* __restrict__ ql,    // [B][Tq][Hq*HD] fp16, scaled
     const uint4* __restrict__ kh, const uint4* __restrict__ kl,    // [B][Tkv][Hkv*HD] fp16
@@ -134,6 +134,9 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
     const int kb = kv_index ? kv_index[b] : b;  // K/V batch of query batch b
     const int hk = h / (hq / hkv);
     const int q_idx = qt * QT + wave * 16 + lq;  // this lane's query
+    // ONEQ (t_q = 1, decode): only wave 0 holds a live query; the other waves
+    // only help stage the K/V tiles
+    const bool active = !ONEQ || wave == 0;
     const int q_ld = min(q_idx, tq - 1);
     const size_t qw = (size_t)hq * HD / 8, kw = (size_t)hkv * HD / 8;  // row widths in uint4
 
@@ -279,103 +282,105 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
         VK_LDS_BARRIER();
         st = load(min(kt + 1, n_tiles - 1));
 
-        // ---- S^T for 4 key subtiles of 16: lane holds keys 16n + 4g + r
-        vk_f32x4 s[4];
+        if (active) {
+            // ---- S^T for 4 key subtiles of 16: lane holds keys 16n + 4g + r
+            vk_f32x4 s[4];
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
-            s[n] = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int n = 0; n < 4; ++n) {
+                s[n] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const int off = (16 * n + lq) * KROW + 32 * ks + 8 * g;
-                const vk_h16x8 ah = *reinterpret_cast<const vk_h16x8*>(&lk[0][off]);
-                const vk_h16x8 bh = __builtin_bit_cast(vk_h16x8, qa_h[ks]);
-                const vk_h16x8 bl = __builtin_bit_cast(vk_h16x8, qa_l[ks]);
-                s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, s[n], 0, 0, 0);
-                s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, s[n], 0, 0, 0);
-                if (LO) {
-                    const vk_h16x8 al = *reinterpret_cast<const vk_h16x8*>(&lk[NP - 1][off]);
-                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, s[n], 0, 0, 0);
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int off = (16 * n + lq) * KROW + 32 * ks + 8 * g;
+                    const vk_h16x8 ah = *reinterpret_cast<const vk_h16x8*>(&lk[0][off]);
+                    const vk_h16x8 bh = __builtin_bit_cast(vk_h16x8, qa_h[ks]);
+                    const vk_h16x8 bl = __builtin_bit_cast(vk_h16x8, qa_l[ks]);
+                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, s[n], 0, 0, 0);
+                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, s[n], 0, 0, 0);
+                    if (LO) {
+                        const vk_h16x8 al = *reinterpret_cast<const vk_h16x8*>(&lk[NP - 1][off]);
+                        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, s[n], 0, 0, 0);
+                    }
                 }
             }
-        }
-        // ---- mask, online softmax (per query = per lane, across lanes g)
-        float mloc = -INFINITY;
-        if (!causal && kt * KT + KT <= tkv) {  // a whole tile of live keys: nothing to mask
+            // ---- mask, online softmax (per query = per lane, across lanes g)
+            float mloc = -INFINITY;
+            if (!causal && kt * KT + KT <= tkv) {  // a whole tile of live keys: nothing to mask
 #pragma unroll
-            for (int n = 0; n < 4; ++n)
+                for (int n = 0; n < 4; ++n)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[n][r]);
-        } else {
+                    for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[n][r]);
+            } else {
 #pragma unroll
-            for (int n = 0; n < 4; ++n)
+                for (int n = 0; n < 4; ++n)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int key = kt * KT + 16 * n + 4 * g + r;
+                        const bool ok = key < tkv && (!causal || key <= q_off + q_idx);
+                        s[n][r] = ok ? s[n][r] : -INFINITY;
+                        mloc = fmaxf(mloc, s[n][r]);
+                    }
+            }
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 16, VK_WAVE));
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, VK_WAVE));
+            const float m_new = fmaxf(m_run, mloc);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = __expf(m_run - m_use);
+            float psum = 0.0f;
+            uint32_t ph[4][2], pl[4][2];  // P^T operand halves, [key subtile][pair]
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                _Float16 h4[4], l4[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int key = kt * KT + 16 * n + 4 * g + r;
-                    const bool ok = key < tkv && (!causal || key <= q_off + q_idx);
-                    s[n][r] = ok ? s[n][r] : -INFINITY;
-                    mloc = fmaxf(mloc, s[n][r]);
+                    const float p = __expf(s[n][r] - m_use);
+                    psum += p;
+                    split_f16(p, h4[r], l4[r]);
                 }
-        }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, VK_WAVE));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, VK_WAVE));
-        const float m_new = fmaxf(m_run, mloc);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = __expf(m_run - m_use);
-        float psum = 0.0f;
-        uint32_t ph[4][2], pl[4][2];  // P^T operand halves, [key subtile][pair]
-#pragma unroll
-        for (int n = 0; n < 4; ++n) {
-            _Float16 h4[4], l4[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float p = __expf(s[n][r] - m_use);
-                psum += p;
-                split_f16(p, h4[r], l4[r]);
+                ph[n][0] = __builtin_bit_cast(uint16_t, h4[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, h4[1]) << 16);
+                ph[n][1] = __builtin_bit_cast(uint16_t, h4[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, h4[3]) << 16);
+                pl[n][0] = __builtin_bit_cast(uint16_t, l4[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, l4[1]) << 16);
+                pl[n][1] = __builtin_bit_cast(uint16_t, l4[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, l4[3]) << 16);
             }
-            ph[n][0] = __builtin_bit_cast(uint16_t, h4[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, h4[1]) << 16);
-            ph[n][1] = __builtin_bit_cast(uint16_t, h4[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, h4[3]) << 16);
-            pl[n][0] = __builtin_bit_cast(uint16_t, l4[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, l4[1]) << 16);
-            pl[n][1] = __builtin_bit_cast(uint16_t, l4[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, l4[3]) << 16);
-        }
-        psum += __shfl_xor(psum, 16, VK_WAVE);
-        psum += __shfl_xor(psum, 32, VK_WAVE);
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        // o * 1.0f is o: when no lane's running max moved, the rescale is skipped
-        if (__any(alpha != 1.0f)) {
+            psum += __shfl_xor(psum, 16, VK_WAVE);
+            psum += __shfl_xor(psum, 32, VK_WAVE);
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+            // o * 1.0f is o: when no lane's running max moved, the rescale is skipped
+            if (__any(alpha != 1.0f)) {
 #pragma unroll
-            for (int os = 0; os < OS; ++os)
+                for (int os = 0; os < OS; ++os)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) o_acc[os][r] *= alpha;
-        }
-        // ---- O^T += V^T . P^T over 2 key steps of 32: MFMA k-index 8g + 4j + r
-        //      is key 32ks + 16j + 4g + r (the lane's P values, in order)
+                    for (int r = 0; r < 4; ++r) o_acc[os][r] *= alpha;
+            }
+            // ---- O^T += V^T . P^T over 2 key steps of 32: MFMA k-index 8g + 4j + r
+            //      is key 32ks + 16j + 4g + r (the lane's P values, in order)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const vk_h16x8 bh = __builtin_bit_cast(
-                vk_h16x8, make_uint4(ph[2 * ks][0], ph[2 * ks][1], ph[2 * ks + 1][0], ph[2 * ks + 1][1]));
-            const vk_h16x8 bl = __builtin_bit_cast(
-                vk_h16x8, make_uint4(pl[2 * ks][0], pl[2 * ks][1], pl[2 * ks + 1][0], pl[2 * ks + 1][1]));
+            for (int ks = 0; ks < 2; ++ks) {
+                const vk_h16x8 bh = __builtin_bit_cast(
+                    vk_h16x8, make_uint4(ph[2 * ks][0], ph[2 * ks][1], ph[2 * ks + 1][0], ph[2 * ks + 1][1]));
+                const vk_h16x8 bl = __builtin_bit_cast(
+                    vk_h16x8, make_uint4(pl[2 * ks][0], pl[2 * ks][1], pl[2 * ks + 1][0], pl[2 * ks + 1][1]));
 #pragma unroll
-            for (int os = 0; os < OS; ++os) {
-                const int row = (16 * os + lq) * VROW;
-                const int k0 = 32 * ks + 4 * g;
-                const uint2 h0 = *reinterpret_cast<const uint2*>(&lv[0][row + k0]);
-                const uint2 h1 = *reinterpret_cast<const uint2*>(&lv[0][row + k0 + 16]);
-                const vk_h16x8 ah = __builtin_bit_cast(vk_h16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
-                o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, o_acc[os], 0, 0, 0);
-                o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, o_acc[os], 0, 0, 0);
-                if (LO) {
-                    const uint2 l0 = *reinterpret_cast<const uint2*>(&lv[NP - 1][row + k0]);
-                    const uint2 l1 = *reinterpret_cast<const uint2*>(&lv[NP - 1][row + k0 + 16]);
-                    const vk_h16x8 al = __builtin_bit_cast(vk_h16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
-                    o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, o_acc[os], 0, 0, 0);
+                for (int os = 0; os < OS; ++os) {
+                    const int row = (16 * os + lq) * VROW;
+                    const int k0 = 32 * ks + 4 * g;
+                    const uint2 h0 = *reinterpret_cast<const uint2*>(&lv[0][row + k0]);
+                    const uint2 h1 = *reinterpret_cast<const uint2*>(&lv[0][row + k0 + 16]);
+                    const vk_h16x8 ah = __builtin_bit_cast(vk_h16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
+                    o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, o_acc[os], 0, 0, 0);
+                    o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, o_acc[os], 0, 0, 0);
+                    if (LO) {
+                        const uint2 l0 = *reinterpret_cast<const uint2*>(&lv[NP - 1][row + k0]);
+                        const uint2 l1 = *reinterpret_cast<const uint2*>(&lv[NP - 1][row + k0 + 16]);
+                        const vk_h16x8 al = __builtin_bit_cast(vk_h16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
+                        o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, o_acc[os], 0, 0, 0);
+                    }
                 }
             }
         }
         VK_LDS_BARRIER();
     }
-    finish(o_acc, l_run > 0.0f ? 1.0f / l_run : 0.0f);
+    if (active) finish(o_acc, l_run > 0.0f ? 1.0f / l_run : 0.0f);
 }
 
 }  // namespace vk
@@ -401,12 +406,17 @@ hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, i
 }
 
 template <int HD, bool LO>
-static void go_flash(hipStream_t s, dim3 grid, const void* qh, const void* ql, const void* kh, const void* kl,
+static void go_flash1(hipStream_t s, dim3 grid, const void* qh, const void* ql, const void* kh, const void* kl,
                      const void* vth, const void* vtl, float* out, int tq, int tkv, int t_pad, int hq, int hkv,
                      int causal, int q_off, const int* kv_index, const float* qf, float q_scale, const VkQOut& qo) {
-    hipLaunchKernelGGL((vk_flash_attn<HD, LO>), grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
-                       (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv, t_pad,
-                       hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+    if (tq == 1)
+        hipLaunchKernelGGL((vk_flash_attn<HD, LO, true>), grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
+                           (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv,
+                           t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+    else
+        hipLaunchKernelGGL((vk_flash_attn<HD, LO, false>), grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
+                           (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv,
+                           t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
 }
 
 static hipError_t flash_any(hipStream_t s, int hd, const void* qh, const void* ql, const float* qf, float q_scale,
@@ -415,11 +425,11 @@ static hipError_t flash_any(hipStream_t s, int hd, const void* qh, const void* q
                             bool kv_lo, const VkQOut& qo) {
     const dim3 grid((tq + attn::QT - 1) / attn::QT, hq, batch);
     if (hd == 64) {
-        if (kv_lo) go_flash<64, true>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
-        else go_flash<64, false>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+        if (kv_lo) go_flash1<64, true>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+        else go_flash1<64, false>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
     } else {
-        if (kv_lo) go_flash<128, true>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
-        else go_flash<128, false>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+        if (kv_lo) go_flash1<128, true>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+        else go_flash1<128, false>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
     }
     return hipGetLastError();
 }
