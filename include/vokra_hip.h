@@ -90,7 +90,10 @@ void vokra_hip_destroy(vokra_hip_ctx_t *ctx);
 /* Message of the last failed call on this thread ("" if none). */
 const char *vokra_hip_last_error(void);
 
-/* Blocks until the context stream drains; reports asynchronous faults. */
+/* Blocks until the context stream drains; reports asynchronous faults, and
+ * INVALID_ARGUMENT when an attention kernel met an operand outside its fp16
+ * range since the last such check (the flag is per device and is cleared by
+ * the report). */
 int vokra_hip_synchronize(vokra_hip_ctx_t *ctx);
 
 /* ---- device memory and timing (resident mode plumbing) ------------------ */
@@ -289,8 +292,9 @@ int vokra_hip_logits_argmax_dev(vokra_hip_ctx_t *ctx, size_t rows, size_t vocab,
  * n_head_q). The projections around it are gemm_q_f32 calls. head_dim is 64
  * or 128 (else UNSUPPORTED_OP); t_kv = 0 gives zeros. Products run as fp16
  * hi/lo split MFMAs (three per product, f32 accumulation): results agree with
- * the f32 reference to about 1e-6 relative; inputs must be below 65504 in
- * magnitude after scaling. */
+ * the f32 reference to about 1e-6 relative. A finite q * scale, k or v element
+ * of magnitude >= 65520 (beyond fp16) is INVALID_ARGUMENT: here after the
+ * launch, for the _dev form at the next vokra_hip_synchronize. */
 int vokra_hip_attn_f32(vokra_hip_ctx_t *ctx, size_t batch, size_t t_q, size_t t_kv, size_t n_head_q,
                        size_t n_head_kv, size_t head_dim, const float *q, const float *k, const float *v,
                        float scale, int causal, size_t q_offset, float *out);
@@ -523,13 +527,28 @@ int vokra_hip_decoder_reset(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec);
  * with one token, then greedy argmax (decode/sampler.rs:197-206) into
  * next_tokens[i]; logits [n, n_vocab] are written when not NULL. Host arrays,
  * synchronous; rejects token >= n_vocab and position >= n_text_ctx as the
- * reference does. */
+ * reference does, a stream whose encoder output was never set (the reference
+ * builds cross K/V before the first step, decoder.rs:171-211), and a position
+ * other than the stream's current length (the reference takes the position
+ * from its cache, decoder.rs:427-434) or 0 (which restarts the stream; later
+ * rows of its old history are never read). */
 int vokra_hip_decoder_step(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t n, const int32_t *streams,
                            const int32_t *tokens, const int32_t *positions, int32_t *next_tokens, float *logits);
-/* Device arrays, asynchronous (capturable in a HIP graph once warmed up). */
+/* Device arrays, asynchronous (capturable in a HIP graph once warmed up). The
+ * caller guarantees what the host variant checks: distinct streams in range,
+ * tokens < n_vocab, positions = the stream's length or 0 and < n_text_ctx.
+ * A stream whose encoder output is not set attends over zero cross K/V. These
+ * calls do not update the lengths the host variant checks: drive a session
+ * through one of the two. An item outside the cache ends the step's page
+ * allocation; vokra_hip_decoder_status reports it. */
 int vokra_hip_decoder_step_dev(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t n, const int32_t *d_streams,
                                const int32_t *d_tokens, const int32_t *d_positions, int32_t *d_next_tokens,
                                float *d_logits);
+/* Synchronizes and reports the last step's page allocation as
+ * vokra_hip_kv_status does (INVALID_ARGUMENT for an item outside the cache,
+ * KV_CACHE_EXHAUSTED; *n_appended = (layer, item) appends done, layer-major),
+ * then INVALID_ARGUMENT if an attention operand left the fp16 range. */
+int vokra_hip_decoder_status(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t *n_appended);
 
 #ifdef __cplusplus
 }

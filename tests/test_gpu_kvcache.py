@@ -247,3 +247,25 @@ def test_config3_self_attention_shape(ctx):
             want = (p / p.sum()) @ V[:, sl]
             ok, err = close(got[s, sl], want)
             assert ok, (s, h, err)
+
+
+@pytest.mark.parametrize("H,hd,hq", [(20, 64, 20), (2, 128, 16)])
+def test_paged_attention_item_independent_of_batch(ctx, H, hd, hq):
+    """An item's output depends on its own keys only: the same query over the
+    same stream gives the same bits alone, in a large batch and next to
+    longer items (which change the launch's key split), for lengths below,
+    at and above the 512-key split."""
+    print(f"[case] paged attn batch independence H={H} hd={hd} hq={hq}", flush=True)
+    n_stream, max_time, bs = 8, 4096, 16
+    kv = ctx.kv_cache(1, H, hd, n_stream, max_time, bs)
+    rng = np.random.default_rng(hd + hq)
+    lens = [1, 300, 512, 513, 1500, 3584, 3585, 4096]
+    fill_cache(kv, None, 0, lens, H * hd, rng, n_stream)
+    q = rng.standard_normal((n_stream, hq * hd)).astype(np.float32)
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    batch = kv.attn(0, list(range(n_stream)), lens, q, hq, scale)
+    for s in range(n_stream):
+        alone = kv.attn(0, [s], [lens[s]], q[s:s + 1], hq, scale)
+        assert np.array_equal(alone[0], batch[s]), s
+        pair = kv.attn(0, [s, 7], [lens[s], 4096], q[[s, 7]], hq, scale)
+        assert np.array_equal(pair[0], batch[s]), s

@@ -312,15 +312,103 @@ def test_decoder_cross_f16_mode(ctx, oracle):
 
 
 def test_decoder_long_context_split_attention(ctx, oracle):
-    """Positions past the first 256-key split (the paged-attention kernel then
-    splits keys and the split holding the new step packs it into the cache):
-    still bit-identical to the entry points issued one at a time."""
+    """Histories past the first 256-key split (the paged-attention kernel then
+    splits keys and the split holding the new step packs it into the cache),
+    built by real steps: streams 0 and 1 step every time, stream 2 joins at
+    step 200, stream 3 steps every other time. Every step is bit-identical to
+    the entry points issued one at a time."""
     print("[case] decoder long context", flush=True)
     gpu, _ = make_decoder(ctx, oracle, np.random.default_rng(9), n_text=600)
     ops = DecoderByOps(ctx, gpu.parts, 4)
-    streams, tok, pos = [0, 1, 2, 3], [5, 6, 7, 8], [300, 450, 10, 599]
-    for _ in range(2):
-        nxt, logits = gpu.step(streams, tok, pos, want_logits=True)
-        n2, l2 = ops.step(streams, tok, pos)
-        assert np.array_equal(logits, l2) and np.array_equal(nxt, n2), pos
-        tok, pos = [int(t) for t in nxt], [min(p + 1, 599) for p in pos]
+    tok, pos = [5, 6, 7, 8], [0, 0, 0, 0]
+    for step in range(520):
+        streams = [s for s in range(4) if (s < 2 or (s == 2 and step >= 200) or (s == 3 and step % 2 == 0))]
+        args = ([tok[s] for s in streams], [pos[s] for s in streams])
+        nxt, logits = gpu.step(streams, *args, want_logits=True)
+        n2, l2 = ops.step(streams, *args)
+        assert np.array_equal(logits, l2) and np.array_equal(nxt, n2), (step, streams)
+        for i, s in enumerate(streams):
+            tok[s], pos[s] = int(nxt[i]), pos[s] + 1
+    assert pos == [520, 520, 320, 260]
+
+
+def test_decoder_stream_state_rejections(ctx, oracle):
+    """A stream without an encoder output, and a position other than the
+    stream's length (or 0, a restart), are rejected by the host step."""
+    print("[case] decoder stream state", flush=True)
+    g = np.random.default_rng(21)
+    d, H, ff, V, n_text, n_audio = 128, 2, 256, 300, 24, 70
+    layers = [dec_layer(ctx, g, W_Q4_0, d, ff)]
+    tok = (g.standard_normal((V, d)) * 0.5).astype(np.float32)
+    pos = (g.standard_normal((n_text, d)) * 0.1).astype(np.float32)
+    lpg, lpb = rand_norm(g, d)
+    dec = hip.Decoder(ctx, W_Q4_0, d, H, ff, V, n_text, n_audio, 2, layers, tok, pos, lpg, lpb, block_size=4)
+    dec.set_encoder(0, g.standard_normal((n_audio, d)).astype(np.float32))
+    with pytest.raises(hip.InvalidArgument, match="no encoder output"):
+        dec.step([1], [1], [0])
+    t = int(dec.step([0], [1], [0])[0])
+    with pytest.raises(hip.InvalidArgument, match="position"):
+        dec.step([0], [t], [2])
+    t = int(dec.step([0], [t], [1])[0])
+    a = dec.step([0], [3], [0], want_logits=True)[1]  # restart
+    dec.reset()
+    b = dec.step([0], [3], [0], want_logits=True)[1]
+    assert np.array_equal(a, b)
+    with pytest.raises(hip.InvalidArgument, match="position"):
+        dec.step([0], [3], [5])
+
+
+def test_decoder_many_streams_split_page_allocation(ctx, oracle):
+    """1024 streams x 5 layers = 5120 (layer, item) appends per step, above the
+    4096 of one allocation launch: the step allocates in two launches. A
+    batched step equals the same streams stepped alone in a twin session, and
+    the cache holds exactly the pages the steps need."""
+    print("[case] decoder 1024 streams x 5 layers", flush=True)
+    n_stream, n_layer, n_audio, n_text, bs = 1024, 5, 16, 8, 4
+
+    def build(seed):
+        g = np.random.default_rng(seed)
+        d, H, ff, V = 128, 2, 256, 64
+        layers = [dec_layer(ctx, g, W_Q4_0, d, ff) for _ in range(n_layer)]
+        tok = (g.standard_normal((V, d)) * 0.5).astype(np.float32)
+        pos = (g.standard_normal((n_text, d)) * 0.1).astype(np.float32)
+        lpg, lpb = rand_norm(g, d)
+        dec = hip.Decoder(ctx, W_Q4_0, d, H, ff, V, n_text, n_audio, n_stream, layers, tok, pos, lpg, lpb,
+                          block_size=bs)
+        enc = g.standard_normal((n_audio, d)).astype(np.float32)
+        for s in range(n_stream):
+            dec.set_encoder(s, enc)
+        return dec
+
+    a, b = build(3), build(3)
+    streams = list(range(n_stream))
+    tokens = [s % 64 for s in streams]
+    na, la = a.step(streams, tokens, [0] * n_stream, want_logits=True)
+    for s in (0, 511, 1023):
+        nb, lb = b.step([s], [tokens[s]], [0], want_logits=True)
+        assert np.array_equal(lb[0], la[s]) and nb[0] == na[s], s
+    na2, la2 = a.step(streams, [int(t) for t in na], [1] * n_stream, want_logits=True)
+    assert np.isfinite(la2).all()
+
+
+def test_attention_fp16_range_is_an_error(ctx):
+    """An operand beyond the fp16 range of the split products is
+    INVALID_ARGUMENT, not a silent inf / NaN; the next call is clean."""
+    print("[case] attention fp16 range", flush=True)
+    g = np.random.default_rng(2)
+    q = g.standard_normal((1, 8, 128)).astype(np.float32)
+    k = g.standard_normal((1, 16, 128)).astype(np.float32)
+    v = g.standard_normal((1, 16, 128)).astype(np.float32)
+    for which in range(3):
+        ops = [q.copy(), k.copy(), v.copy()]
+        ops[which][0, 3, 70] = 1.0e5 if which else 1.0e5 / 0.125  # q is scaled by 0.125 first
+        with pytest.raises(hip.InvalidArgument, match="fp16 range"):
+            ctx.attn_f32(*ops, 2, scale=0.125)
+    ok = ctx.attn_f32(q, k, v, 2, scale=0.125)
+    assert np.isfinite(ok).all()
+    kv = ctx.kv_cache(1, 1, 128, 1, 16, 4)
+    kv.append(0, [0] * 4, [0, 1, 2, 3], g.standard_normal((4, 128)), g.standard_normal((4, 128)))
+    qb = g.standard_normal((1, 8 * 128)).astype(np.float32)
+    qb[0, 5] = 1.0e6
+    with pytest.raises(hip.InvalidArgument, match="fp16 range"):
+        kv.attn(0, [0], [4], qb, 8, 0.125)

@@ -41,6 +41,12 @@ constexpr int KPAD = 8;  // halves of row padding in the K tile
 constexpr int VPAD = 8;  // halves of row padding in the V^T tile
 }  // namespace attn
 
+// Set (to 1) by any kernel of this file that meets an operand outside the
+// fp16 range; read and cleared by the host (attn_range_take). One per device.
+static __device__ unsigned int vk_attn_range_flag;
+
+__device__ __forceinline__ void attn_range_raise() { atomicOr(&vk_attn_range_flag, 1u); }
+
 __device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
     hi = (_Float16)x;
     lo = (_Float16)(x - (float)hi);
@@ -52,6 +58,10 @@ __device__ __forceinline__ void split8_f16(const float* __restrict__ x, float sc
     const float4 u = reinterpret_cast<const float4*>(x)[0], w = reinterpret_cast<const float4*>(x)[1];
     const float a[8] = {u.x * scale, u.y * scale, u.z * scale, u.w * scale,
                         w.x * scale, w.y * scale, w.z * scale, w.w * scale};
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bad |= vk_f16_overflow(a[j]);
+    if (bad) attn_range_raise();
     uint32_t h[4], l[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -73,6 +83,8 @@ __global__ void vk_split_rows(const float* __restrict__ x, size_t n4, float scal
     if (i >= n4) return;
     const float4 v = reinterpret_cast<const float4*>(x)[i];
     const float a[4] = {v.x * scale, v.y * scale, v.z * scale, v.w * scale};
+    if (vk_f16_overflow(a[0]) || vk_f16_overflow(a[1]) || vk_f16_overflow(a[2]) || vk_f16_overflow(a[3]))
+        attn_range_raise();
     _Float16 h[4], l[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) split_f16(a[j], h[j], l[j]);
@@ -95,6 +107,7 @@ __global__ __launch_bounds__(256) void vk_split_vt(const float* __restrict__ v, 
         const int r = (tid >> 6) + 4 * i, c = tid & 63;
         const int t = t0 + r;
         tile[r][c] = t < t_kv ? v[((size_t)b * t_kv + t) * width + (size_t)h * hd + c0 + c] : 0.0f;
+        if (vk_f16_overflow(tile[r][c])) attn_range_raise();
     }
     __syncthreads();
 #pragma unroll
@@ -447,6 +460,21 @@ hipError_t launch_flash_attn_f32q(hipStream_t s, int hd, const float* q, float q
                                   const VkQOut* qo) {
     return flash_any(s, hd, nullptr, nullptr, q, q_scale, kh, kl, vth, vtl, out, batch, tq, tkv, t_pad, hq, hkv,
                      causal, q_off, kv_index, kv_lo, qo ? *qo : VkQOut{});
+}
+
+// Reads and clears this file's fp16-range flag on the current device; the
+// copies run on stream s, which is drained first.
+hipError_t attn_range_take(hipStream_t s, unsigned* raised) {
+    unsigned v = 0;
+    hipError_t e = hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(vk_attn_range_flag), sizeof v, 0, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e == hipSuccess && v) {
+        const unsigned z = 0;
+        e = hipMemcpyToSymbolAsync(HIP_SYMBOL(vk_attn_range_flag), &z, sizeof z, 0, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+    }
+    *raised = v;
+    return e;
 }
 
 }  // namespace vk

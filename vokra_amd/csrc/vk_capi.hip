@@ -423,7 +423,7 @@ int kv_append_status(vokra_hip_kv* kv, size_t n, const int* h_streams, const int
         return fail(VOKRA_HIP_ERROR_KV_CACHE_EXHAUSTED,
                     "paged KV cache exhausted: arena has %zu pages, %zu in use - pre-allocate a larger "
                     "max_time/n_stream at session construction (item %d of %zu)",
-                    kv->cap, kv->cap, m[2], n);
+                    kv->cap, kv->cap - (size_t)m[0], m[2], n);
     if (h_streams && h_times && (size_t)m[2] < n) {
         // check_bounds order and wording (paged_quant.rs:518-544)
         const long t = h_times[m[2]], st = h_streams[m[2]];
@@ -434,34 +434,19 @@ int kv_append_status(vokra_hip_kv* kv, size_t n, const int* h_streams, const int
     return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "append item %d: layer, stream or t out of range", m[2]);
 }
 
-int kv_split(const vokra_hip_kv* kv, size_t n, size_t max_len, size_t hkv, int* n_split, int* kps) {
-    // enough workgroups to fill the chip, at least 256 keys per split
-    // (targets of 1024 and 2048 workgroups measured slower at configs 3 and 4)
-    const size_t wgs = n * hkv;
-    size_t want = wgs >= 512 ? 1 : (512 + wgs - 1) / wgs;
-    const size_t max_split = (max_len + 255) / 256;
-    if (want > max_split) want = max_split;
-    if (want < 1) want = 1;
-    const size_t per = (max_len + want - 1) / want;
-    *n_split = (int)want;
-    *kps = (int)(((per + 255) / 256) * 256);
-    (void)kv;
-    return VOKRA_HIP_OK;
-}
-
 int run_paged_attn(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                    const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
                    const VkQOut* qo = nullptr, const float* d_ak = nullptr, const float* d_av = nullptr,
                    const int* d_at = nullptr) {
-    const size_t hkv = kv->n_head;
-    int n_split = 1, kps = 256;
-    kv_split(kv, n, max_len ? max_len : 1, hkv, &n_split, &kps);
+    // each item splits its keys by its own length (at most 8 splits of >= 512
+    // keys), so its results never depend on the rest of the batch
+    const int n_split = vk::paged_attn_grid_splits((int)std::min<size_t>(max_len ? max_len : 1, kv->max_time));
     if (n_split > 1) {
         VK_TRY(kv->part_ml.ensure(n * hq * n_split * 2 * sizeof(float)), "hipMalloc(paged attention partials)");
         VK_TRY(kv->part_o.ensure(n * hq * n_split * kv->d_head * sizeof(float)), "hipMalloc(paged attention partials)");
     }
     VK_TRY(vk::launch_paged_attn(c->stream, kv->view(), (int)layer, (int)n, d_streams, d_lens, d_q, scale, (int)hq,
-                                 (int)kv->d_head, n_split, kps, d_out, (float*)kv->part_ml.p, (float*)kv->part_o.p,
+                                 (int)kv->d_head, n_split, d_out, (float*)kv->part_ml.p, (float*)kv->part_o.p,
                                  qo, d_ak, d_av, d_at),
            "launch(vk_paged_attn)");
     return VOKRA_HIP_OK;
@@ -486,7 +471,28 @@ int check_paged_attn(const vokra_hip_kv* kv, size_t layer, size_t n, size_t hq) 
 // this file's entry points.
 namespace vk {
 hipStream_t ctx_stream(const vokra_hip_ctx* c) { return c->stream; }
-int ctx_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+
+// Drains the context stream and turns a raised fp16-range flag of the
+// attention kernels into INVALID_ARGUMENT (the explicit failure of
+// compute.rs:649-696 instead of an inf / NaN result).
+int range_check(vokra_hip_ctx* c) {
+    unsigned a = 0, b = 0;
+    VK_TRY(attn_range_take(c->stream, &a), "attention range flag");
+    VK_TRY(kv_range_take(c->stream, &b), "attention range flag");
+    if (a || b)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "attention: an operand is outside the fp16 range of the split products (|x| >= 65520 after "
+                    "scaling); the results of the calls since the last check are not valid");
+    return VOKRA_HIP_OK;
+}
+int ctx_fail(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    return fail(code, "%s", buf);
+}
 
 static int check_gemm_qact(const vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_qact* qa,
                            const float* d_out) {
@@ -683,15 +689,20 @@ int gemm_qact_quantize(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra
     return VOKRA_HIP_OK;
 }
 
-int kv_alloc_layers(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer0, size_t n_layers, size_t n,
+int kv_alloc_layers(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t first_layer, size_t layer0, size_t n_layers, size_t n,
                     const int* d_streams, const int* d_times) {
     if (!c || !kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: bad context or cache");
-    if (n_layers == 0 || layer0 + n_layers > kv->n_layer || n * n_layers > 4096)
+    if (n_layers == 0 || layer0 < first_layer || layer0 + n_layers > kv->n_layer || n * n_layers > 4096 ||
+        (layer0 - first_layer) * n > 0x7fffffff)
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: %zu layers from %zu of %zu, %zu items", n_layers,
                     layer0, kv->n_layer, n);
     if (n && (!d_streams || !d_times)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: NULL buffer");
     VK_TRY(set_dev(c), "hipSetDevice");
-    VK_TRY(vk::launch_kv_alloc_layers(c->stream, kv->view(), (int)layer0, (int)n_layers, (int)n, d_streams, d_times),
+    // the launches of one step continue one batch: items of earlier layers
+    // count first, and a failure stops every later launch
+    const int q_base = (int)((layer0 - first_layer) * n);
+    VK_TRY(vk::launch_kv_alloc_layers(c->stream, kv->view(), (int)layer0, (int)n_layers, (int)n, q_base, d_streams,
+                                      d_times),
            "launch(vk_kv_alloc_layers)");
     return VOKRA_HIP_OK;
 }
@@ -967,7 +978,7 @@ int vokra_hip_paged_attn(vokra_hip_ctx_t* c, vokra_hip_kv_t* kv, size_t layer, s
     }
     VK_TRY(hipMemcpyAsync(out, kv->rows.p, qb, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync");
     VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    return VOKRA_HIP_OK;
+    return vk::range_check(c);
 }
 
 // ---- f32 kernels (A11, A12) -------------------------------------------------
@@ -1315,7 +1326,7 @@ int vokra_hip_attn_f32(vokra_hip_ctx_t* c, size_t batch, size_t t_q, size_t t_kv
     }
     VK_TRY(hipMemcpyAsync(out, c->out0.p, nq * 4, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(D2H)");
     VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    return VOKRA_HIP_OK;
+    return vk::range_check(c);
 }
 
 const char* vokra_hip_last_error(void) { return g_last_error.c_str(); }
@@ -1373,7 +1384,7 @@ int vokra_hip_synchronize(vokra_hip_ctx_t* c) {
     if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "synchronize: ctx is NULL");
     VK_TRY(set_dev(c), "hipSetDevice");
     VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    return VOKRA_HIP_OK;
+    return vk::range_check(c);
 }
 
 int vokra_hip_device_alloc(vokra_hip_ctx_t* c, size_t bytes, void** dptr) {

@@ -85,6 +85,13 @@ __device__ __forceinline__ uint32_t vk_int_to_bf16_bits(int v) {
 // Rust `f32::round` (half away from zero) — roundf is exactly that.
 __device__ __forceinline__ float vk_round_half_away(float x) { return roundf(x); }
 
+// A finite f32 whose fp16 rounding is infinite (|x| >= 65520): the fp16
+// hi / lo operands of the attention kernels cannot represent it.
+__device__ __forceinline__ bool vk_f16_overflow(float x) {
+    const float a = fabsf(x);
+    return a >= 65520.0f && a <= 3.40282347e38f;
+}
+
 // Max-reduce over groups of `G` consecutive lanes (G power of two <= 64).
 template <int G>
 __device__ __forceinline__ float vk_group_max(float v) {

@@ -57,7 +57,7 @@ int fail(int code, const char* fmt, ...) {
     va_start(ap, fmt);
     vsnprintf(buf, sizeof buf, fmt, ap);
     va_end(ap);
-    return vk::ctx_fail(code, buf);
+    return vk::ctx_fail(code, "%s", buf);
 }
 
 // Bytes per block and elements per block of the accepted tensor types.

@@ -20,6 +20,10 @@
 
 namespace vk {
 
+// Set (to 1) by the GQA decode kernel when q * scale is outside the fp16
+// range of its operands; read and cleared by the host (kv_range_take).
+static __device__ unsigned int vk_kv_range_flag;
+
 // Device view of one cache, passed by value to every kernel.
 struct KvDev {
     int8_t* kq;
@@ -138,7 +142,10 @@ __global__ __launch_bounds__(1024) void vk_kv_alloc(KvDev c, int layer, int n, c
 // batch. Writes the table, free_len, the status and the appended count
 // (meta[2], in items q); no per-item overwrite flags (its caller appends
 // distinct streams). One workgroup of 1024 threads; nl * n <= 4096.
-__global__ __launch_bounds__(1024) void vk_kv_alloc_layers(KvDev c, int layer0, int nl, int n,
+// q_base > 0 continues a batch split over several launches (q_base items
+// before this one): a launch after a failed one allocates nothing and keeps
+// the first failure's status and count.
+__global__ __launch_bounds__(1024) void vk_kv_alloc_layers(KvDev c, int layer0, int nl, int n, int q_base,
                                                            const int* __restrict__ streams,
                                                            const int* __restrict__ times) {
     constexpr int QMAX = 4096, U = QMAX / 1024;
@@ -147,6 +154,7 @@ __global__ __launch_bounds__(1024) void vk_kv_alloc_layers(KvDev c, int layer0, 
     __shared__ int s_scan[1024];
     __shared__ int s_bad, s_total;
     const int tid = threadIdx.x, N = nl * n;
+    if (q_base > 0 && c.meta[1] != KV_OK) return;  // uniform: one value for the whole workgroup
     bool valid[U], first[U];
     int ti[U];
     if (tid == 0) { s_bad = N; s_total = 0; }
@@ -212,7 +220,7 @@ __global__ __launch_bounds__(1024) void vk_kv_alloc_layers(KvDev c, int layer0, 
         }
         c.meta[0] = free_len - s_total;
         c.meta[1] = status;
-        c.meta[2] = bad;
+        c.meta[2] = q_base + bad;
     }
 }
 
@@ -360,12 +368,24 @@ __global__ void vk_kv_page_of(KvDev c, int layer, int t, int* __restrict__ out) 
 // splits, each writes (m, l, O) partials that vk_paged_attn_combine merges.
 namespace pa {
 constexpr int CH = 256;
+constexpr int KPS = 512, MAX_SPLIT = 8;  // keys per split grow by KPS so an item never has more than 8
+}
+
+// Key split of one item, a function of its length only (never of the batch
+// or of the grid): splits of pa_kps(len) keys, pa_splits(len) <= 8 of them.
+// An item's results therefore do not depend on what else is in the launch.
+__host__ __device__ __forceinline__ int pa_kps(int len) {
+    return pa::KPS * (len > 0 ? (len + pa::KPS * pa::MAX_SPLIT - 1) / (pa::KPS * pa::MAX_SPLIT) : 1);
+}
+__host__ __device__ __forceinline__ int pa_splits(int len) {
+    const int k = pa_kps(len);
+    return len > k ? (len + k - 1) / k : 1;
 }
 
 template <int HD, int G>
 __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const int* __restrict__ streams,
                                                      const int* __restrict__ lens, const float* __restrict__ q,
-                                                     float scale, int hq, int n_split, int keys_per_split,
+                                                     float scale, int hq, int n_split,
                                                      float* __restrict__ out, float* __restrict__ part_ml,
                                                      float* __restrict__ part_o, const VkQOut qo,
                                                      const float* __restrict__ ak, const float* __restrict__ av,
@@ -389,7 +409,9 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
     const int split = blockIdx.x, hk = blockIdx.y, item = blockIdx.z;
     const int s = streams[item];
     const int len = min(lens[item], c.max_time);
-    const int k0 = split * keys_per_split, k1 = min(len, k0 + keys_per_split);
+    const int kps = pa_kps(len), nsp = pa_splits(len);
+    if (split >= nsp) return;  // uniform per workgroup, before any barrier
+    const int k0 = split * kps, k1 = min(len, k0 + kps);
 
     // Fused append (ak != null): the workgroup whose key range holds the
     // item's new time step packs that step's K and V head slices into the
@@ -588,7 +610,7 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
             for (int r = 0; r < TPO; ++r) a += lpart[oq * TPO + r][i];
         }
         const int h = hk * G + g;
-        if (n_split == 1) {
+        if (nsp == 1) {
             const float inv = lml[g][1] > 0.0f ? 1.0f / lml[g][1] : 0.0f;
             const float val = a * inv;
             out[((size_t)item * hq + h) * HD + e] = val;
@@ -673,7 +695,7 @@ __device__ __forceinline__ vk_h16x8_t vk_i8x8_f16(uint2 w) {
 template <int G>
 __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, const int* __restrict__ streams,
                                                          const int* __restrict__ lens, const float* __restrict__ q,
-                                                         float scale, int hq, int n_split, int keys_per_split,
+                                                         float scale, int hq, int n_split,
                                                          float* __restrict__ out, float* __restrict__ part_ml,
                                                          float* __restrict__ part_o) {
     using namespace pg;
@@ -686,7 +708,9 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
     const int split = blockIdx.x, hk = blockIdx.y, item = blockIdx.z;
     const int s = streams[item];
     const int len = min(lens[item], c.max_time);
-    const int k0 = split * keys_per_split, k1 = min(len, k0 + keys_per_split);
+    const int kps = pa_kps(len), nsp = pa_splits(len);
+    if (split >= nsp) return;  // uniform per workgroup, before any barrier
+    const int k0 = split * kps, k1 = min(len, k0 + kps);
 
     // q * scale of head hh (zero for padding heads) as the S^T B operand:
     // lane (g, hh) holds dims 32b + 8g .. +7, split into fp16 hi + lo
@@ -704,6 +728,7 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float xs = x[i] * scale;
+            if (vk_f16_overflow(xs)) atomicOr(&vk_kv_range_flag, 1u);
             const _Float16 h = (_Float16)xs;
             qh[b][i] = h;
             ql[b][i] = (_Float16)(xs - (float)h);
@@ -872,29 +897,34 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
             for (int r = 0; r < 4; ++r) t[r] += u[r];
         }
         const int e = 16 * et + 4 * g;
-        if (n_split == 1)
+        if (nsp == 1)
             *reinterpret_cast<float4*>(out + ((size_t)item * hq + h) * HD + e) =
                 make_float4(t[0] * inv, t[1] * inv, t[2] * inv, t[3] * inv);
         else
             *reinterpret_cast<float4*>(part_o + pi * HD + e) = make_float4(t[0], t[1], t[2], t[3]);
     }
-    if (n_split > 1 && g == 0) {
+    if (nsp > 1 && g == 0) {
         part_ml[2 * pi] = M;
         part_ml[2 * pi + 1] = L;
     }
 }
 
-// Merges split partials: m = max m_s, O = sum O_s e^(m_s - m), l likewise.
+// Merges split partials: m = max m_s, O = sum O_s e^(m_s - m), l likewise,
+// over the item's own pa_splits(len) splits (partials at stride n_split);
+// items with one split were written whole by the attention kernel.
 template <int HD>
-__global__ void vk_paged_attn_combine(int n_split, int hq, const float* __restrict__ part_ml,
-                                      const float* __restrict__ part_o, float* __restrict__ out) {
+__global__ void vk_paged_attn_combine(int n_split, int hq, const int* __restrict__ lens, int max_time,
+                                      const float* __restrict__ part_ml, const float* __restrict__ part_o,
+                                      float* __restrict__ out) {
     const size_t ih = blockIdx.x;  // (item, head)
     const int e = threadIdx.x;
+    const int nsp = pa_splits(min(lens[ih / hq], max_time));
+    if (nsp == 1) return;
     float m = -INFINITY;
-    for (int sp = 0; sp < n_split; ++sp) m = fmaxf(m, part_ml[2 * (ih * n_split + sp)]);
+    for (int sp = 0; sp < nsp; ++sp) m = fmaxf(m, part_ml[2 * (ih * n_split + sp)]);
     const float m_use = m == -INFINITY ? 0.0f : m;
     float l = 0.0f, o = 0.0f;
-    for (int sp = 0; sp < n_split; ++sp) {
+    for (int sp = 0; sp < nsp; ++sp) {
         const size_t pi = ih * n_split + sp;
         const float w = __expf(part_ml[2 * pi] - m_use);
         l += part_ml[2 * pi + 1] * w;
@@ -948,11 +978,12 @@ hipError_t launch_kv_append(hipStream_t s, const KvView& v, int layer, int n, co
     return hipGetLastError();
 }
 
-hipError_t launch_kv_alloc_layers(hipStream_t s, const KvView& v, int layer0, int n_layers, int n, const int* streams,
-                                  const int* times) {
-    if (n_layers < 1 || n < 0 || (size_t)n_layers * n > 4096) return hipErrorInvalidValue;
+hipError_t launch_kv_alloc_layers(hipStream_t s, const KvView& v, int layer0, int n_layers, int n, int q_base,
+                                  const int* streams, const int* times) {
+    if (n_layers < 1 || n < 0 || (size_t)n_layers * n > 4096 || q_base < 0) return hipErrorInvalidValue;
     if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(vk_kv_alloc_layers, dim3(1), dim3(1024), 0, s, kv_view(v), layer0, n_layers, n, streams, times);
+    hipLaunchKernelGGL(vk_kv_alloc_layers, dim3(1), dim3(1024), 0, s, kv_view(v), layer0, n_layers, n, q_base, streams,
+                       times);
     return hipGetLastError();
 }
 
@@ -994,7 +1025,7 @@ hipError_t launch_kv_page_of(hipStream_t s, const KvView& v, int layer, int t, i
 // paged_attn_fuses_append.
 template <int HD, int G>
 static bool go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* streams, const int* lens,
-                  const float* q, float scale, int hq, int hkv, int n_split, int kps, float* out, float* pml,
+                  const float* q, float scale, int hq, int hkv, int n_split, float* out, float* pml,
                   float* po, const VkQOut& qo, const float* ak, const float* av, const int* at) {
     // head_dim 128 with several query heads per kv head: the matrix-core
     // kernel (its slots travel through 32-bit lane shuffles; it moves q and
@@ -1005,17 +1036,24 @@ static bool go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* st
     if constexpr (HD == pg::HD && G >= 2) {
         if (small_slots && aligned && !ak) {
             hipLaunchKernelGGL((vk_paged_attn_gqa<G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams,
-                               lens, q, scale, hq, n_split, kps, out, pml, po);
+                               lens, q, scale, hq, n_split, out, pml, po);
             return false;
         }
     }
     hipLaunchKernelGGL((vk_paged_attn<HD, G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams, lens, q,
-                       scale, hq, n_split, kps, out, pml, po, n_split == 1 ? qo : VkQOut{}, ak, av, at);
+                       scale, hq, n_split, out, pml, po, n_split == 1 ? qo : VkQOut{}, ak, av, at);
     return n_split == 1 && qo.afrag;
 }
 
+int paged_attn_grid_splits(int max_len) {
+    // pa_splits(len) = ceil(len / 512) up to 4096 keys and never above 8
+    // beyond (it is not monotone there): this bounds it for every len <= max_len
+    const int k = (max_len + pa::KPS - 1) / pa::KPS;
+    return k < 1 ? 1 : (k > pa::MAX_SPLIT ? pa::MAX_SPLIT : k);
+}
+
 hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* lens,
-                             const float* q, float scale, int hq, int hd, int n_split, int keys_per_split, float* out,
+                             const float* q, float scale, int hq, int hd, int n_split, float* out,
                              float* part_ml, float* part_o, const VkQOut* qo, const float* ak, const float* av,
                              const int* at) {
     const KvDev c = kv_view(v);
@@ -1024,7 +1062,7 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
     bool fused = false;
 #define VK_PA(HDV, GV)                                                                                          \
     if (hd == HDV && g == GV) {                                                                                 \
-        fused = go_pa<HDV, GV>(s, c, layer, n, streams, lens, q, scale, hq, hkv, n_split, keys_per_split, out,  \
+        fused = go_pa<HDV, GV>(s, c, layer, n, streams, lens, q, scale, hq, hkv, n_split, out,                  \
                                part_ml, part_o, qz, ak, av, at);                                                \
     } else
     VK_PA(64, 1) VK_PA(64, 2) VK_PA(64, 4) VK_PA(64, 8) VK_PA(128, 1) VK_PA(128, 2) VK_PA(128, 4) VK_PA(128, 8) {
@@ -1035,11 +1073,11 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
     if (e != hipSuccess) return e;
     if (n_split > 1) {
         if (hd == 64)
-            hipLaunchKernelGGL(vk_paged_attn_combine<64>, dim3((unsigned)(n * hq)), dim3(64), 0, s, n_split, hq,
-                               part_ml, part_o, out);
+            hipLaunchKernelGGL(vk_paged_attn_combine<64>, dim3((unsigned)(n * hq)), dim3(64), 0, s, n_split, hq, lens,
+                               c.max_time, part_ml, part_o, out);
         else
             hipLaunchKernelGGL(vk_paged_attn_combine<128>, dim3((unsigned)(n * hq)), dim3(128), 0, s, n_split, hq,
-                               part_ml, part_o, out);
+                               lens, c.max_time, part_ml, part_o, out);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -1047,6 +1085,21 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
     if (qz.afrag && !fused)
         return launch_quantize_act_b32(s, qz.pow2 != 0, out, n, qz.m_pad, qz.k, qz.afrag, qz.ascale, qz.asum);
     return hipSuccess;
+}
+
+// Reads and clears this file's fp16-range flag on the current device; the
+// copies run on stream s, which is drained first.
+hipError_t kv_range_take(hipStream_t s, unsigned* raised) {
+    unsigned v = 0;
+    hipError_t e = hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(vk_kv_range_flag), sizeof v, 0, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e == hipSuccess && v) {
+        const unsigned z = 0;
+        e = hipMemcpyToSymbolAsync(HIP_SYMBOL(vk_kv_range_flag), &z, sizeof z, 0, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+    }
+    *raised = v;
+    return e;
 }
 
 }  // namespace vk

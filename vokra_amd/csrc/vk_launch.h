@@ -127,8 +127,11 @@ hipError_t launch_kv_read(hipStream_t s, const KvView& v, int layer, int t, int 
 hipError_t launch_kv_release(hipStream_t s, const KvView& v, int layer);
 hipError_t launch_kv_reset(hipStream_t s, const KvView& v, const int* order, size_t pool_bytes, size_t scale_bytes);
 hipError_t launch_kv_page_of(hipStream_t s, const KvView& v, int layer, int t, int* out);
+// The grid's split count for keys up to max_len; each item uses its own
+// length's split (pa_splits), at most this many.
+int paged_attn_grid_splits(int max_len);
 hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* lens,
-                             const float* q, float scale, int hq, int hd, int n_split, int keys_per_split, float* out,
+                             const float* q, float scale, int hq, int hd, int n_split, float* out,
                              float* part_ml, float* part_o,
                              const VkQOut* qo = nullptr,  // also the activation pass over out (rows = items)
                              // fused append: item i's K / V rows (ak, av [n][width]) at time at[i] are
@@ -137,8 +140,12 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
                              const float* ak = nullptr, const float* av = nullptr, const int* at = nullptr);
 // The allocation of launch_kv_append for the same items appended to layers
 // layer0 .. layer0 + n_layers - 1 in that order, in one launch (n_layers * n <= 4096).
-hipError_t launch_kv_alloc_layers(hipStream_t s, const KvView& v, int layer0, int n_layers, int n, const int* streams,
-                                  const int* times);
+// Read and clear the fp16-range flags of the attention kernels (vk_attn.hip)
+// and of the GQA decode kernel (vk_kvcache.hip) on the current device.
+hipError_t attn_range_take(hipStream_t s, unsigned* raised);
+hipError_t kv_range_take(hipStream_t s, unsigned* raised);
+hipError_t launch_kv_alloc_layers(hipStream_t s, const KvView& v, int layer0, int n_layers, int n, int q_base,
+                                  const int* streams, const int* times);
 }  // namespace vk
 
 namespace vk {
@@ -174,7 +181,8 @@ struct vokra_hip_qweight;
 struct vokra_hip_kv;
 namespace vk {
 hipStream_t ctx_stream(const vokra_hip_ctx* c);
-int ctx_fail(int code, const char* msg);
+int range_check(vokra_hip_ctx* c);  // INVALID_ARGUMENT when an fp16-range flag is raised
+int ctx_fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Fused forms of entry-point sequences for the sessions (vk_capi.hip); each
 // gives the same results as the sequence it replaces.
 //   gemm_qact_epi    = vokra_hip_gemm_qact_dev, then GELU and/or + resid
@@ -207,7 +215,7 @@ int paged_attn_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t
 //   order) = per layer vokra_hip_kv_append_dev of the items' K / V rows at
 //   d_times, then paged_attn_quantize; for distinct streams whose new time
 //   step lies inside d_lens, and a cache with room for every append.
-int kv_alloc_layers(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer0, size_t n_layers, size_t n,
+int kv_alloc_layers(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t first_layer, size_t layer0, size_t n_layers, size_t n,
                     const int* d_streams, const int* d_times);
 int paged_attn_append_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                                const int* d_times, const float* d_k, const float* d_v, const int* d_lens,

@@ -43,7 +43,7 @@ constexpr float kLnEps = 1e-5f;  // LAYER_NORM_DEFAULT_EPS (crates/vokra-backend
 #define SS_HIP(x, what)                                                                    \
     do {                                                                                   \
         hipError_t _e = (x);                                                               \
-        if (_e != hipSuccess) return vk::ctx_fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, what); \
+        if (_e != hipSuccess) return vk::ctx_fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, "%s", what); \
     } while (0)
 
 size_t wire_bytes(int wdtype, size_t n, size_t k) {
@@ -102,7 +102,7 @@ struct QLin {
 };
 
 int upload_vec(vokra_hip_ctx_t* c, DBuf& b, const float* h, size_t n, const char* what) {
-    if (!h) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, what);
+    if (!h) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "%s", what);
     return b.upload(c, h, n * sizeof(float));
 }
 
@@ -167,6 +167,10 @@ struct vokra_hip_decoder {
     int cross_precision = VOKRA_HIP_CROSS_F32;  // F16: cross-attention reads the hi parts only
     DBuf h, x, q, k, v, attn, f, logits, lpart, lens, kvidx, next, tk, tv, stage;
     vokra_hip_qact_t *qa_d = nullptr, *qa_f = nullptr;
+    // host mirror of each stream's state: cross K/V set from an encoder
+    // output, and the number of positions in its self-KV history
+    std::vector<char> enc_set;
+    std::vector<int32_t> length;
     void release() {
         for (auto& L : layers) {
             for (DBuf* b : {&L.ln1g, &L.ln1b, &L.ln2g, &L.ln2b, &L.ln3g, &L.ln3b}) b->release(ctx);
@@ -313,6 +317,14 @@ int dec_setup(vokra_hip_decoder* m, const vokra_hip_decoder_layer_t* layers, con
     SS_TRY(m->ckl.alloc(c, sl * m->n_audio * d * 2));
     SS_TRY(m->cvh.alloc(c, sl * d * m->t_pad * 2));
     SS_TRY(m->cvl.alloc(c, sl * d * m->t_pad * 2));
+    // zero cross K/V: a stream stepped through the _dev path before its
+    // encoder output is set attends over zeros, never over stale memory
+    for (DBuf* b : {&m->ckh, &m->ckl})
+        SS_HIP(hipMemsetAsync(b->p, 0, sl * m->n_audio * d * 2, vk::ctx_stream(c)), "hipMemsetAsync(cross k)");
+    for (DBuf* b : {&m->cvh, &m->cvl})
+        SS_HIP(hipMemsetAsync(b->p, 0, sl * d * m->t_pad * 2, vk::ctx_stream(c)), "hipMemsetAsync(cross v)");
+    m->enc_set.assign(m->n_stream, 0);
+    m->length.assign(m->n_stream, 0);
     const size_t rows = m->n_stream, rd = rows * d * sizeof(float);
     for (DBuf* b : {&m->h, &m->x, &m->q, &m->k, &m->v, &m->attn}) SS_TRY(b->alloc(c, rd));
     SS_TRY(m->f.alloc(c, rows * ff * sizeof(float)));
@@ -367,7 +379,7 @@ int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_
     // (the same pages as one append per layer); each layer's attention kernel
     // then packs its new K / V rows into them
     for (size_t l0 = 0, per = std::max<size_t>(1, 4096 / n); l0 < m->n_layer; l0 += per)
-        SS_TRY(vk::kv_alloc_layers(c, m->kv, l0, std::min(per, m->n_layer - l0), n, d_streams, d_positions));
+        SS_TRY(vk::kv_alloc_layers(c, m->kv, 0, l0, std::min(per, m->n_layer - l0), n, d_streams, d_positions));
     // The same fusions as the encoder (LN + quantize, out-proj + residual,
     // fc1 + GELU, q/k/v in one launch); results equal the entry-point sequence.
     const VkEpi add_h = {m->h.f(), 0}, gelu = {nullptr, 1};
@@ -510,7 +522,7 @@ int vokra_hip_encoder_encode(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, size_t 
     if (!st) st = vokra_hip_memcpy_dtoh(c, out, o.p, n_out * sizeof(float));
     in.release(c);
     o.release(c);
-    return st;
+    return st ? st : vk::range_check(c);
 }
 
 int vokra_hip_encoder_forward(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, size_t batch, size_t frames, const float* x,
@@ -528,7 +540,7 @@ int vokra_hip_encoder_forward(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, size_t
     if (!st) st = vokra_hip_memcpy_dtoh(c, out, o.p, n * sizeof(float));
     in.release(c);
     o.release(c);
-    return st;
+    return st ? st : vk::range_check(c);
 }
 
 int vokra_hip_decoder_create(vokra_hip_ctx_t* c, int wdtype, size_t n_layer, size_t d_model, size_t n_head,
@@ -576,7 +588,9 @@ int vokra_hip_decoder_set_encoder_dev(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m
         return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_set_encoder: bad argument");
     if (stream >= m->n_stream)
         return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_set_encoder: stream out of range");
-    return dec_set_encoder(m, stream, d_enc);
+    SS_TRY(dec_set_encoder(m, stream, d_enc));
+    m->enc_set[stream] = 1;
+    return VOKRA_HIP_OK;
 }
 
 int vokra_hip_decoder_set_encoder(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t stream, const float* enc) {
@@ -586,7 +600,9 @@ int vokra_hip_decoder_set_encoder(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, si
         return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_set_encoder: stream out of range");
     SS_TRY(vokra_hip_memcpy_htod(c, m->stage.p, enc, m->n_audio * m->d * sizeof(float)));
     SS_TRY(dec_set_encoder(m, stream, m->stage.f()));
-    return vokra_hip_synchronize(c);
+    SS_TRY(vokra_hip_synchronize(c));
+    m->enc_set[stream] = 1;
+    return VOKRA_HIP_OK;
 }
 
 int vokra_hip_decoder_set_cross_precision(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, int precision) {
@@ -600,7 +616,17 @@ int vokra_hip_decoder_set_cross_precision(vokra_hip_ctx_t* c, vokra_hip_decoder_
 
 int vokra_hip_decoder_reset(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m) {
     if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_reset: bad argument");
-    return vokra_hip_kv_reset(c, m->kv);
+    SS_TRY(vokra_hip_kv_reset(c, m->kv));
+    std::fill(m->length.begin(), m->length.end(), 0);
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_decoder_status(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t* n_appended) {
+    if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_status: bad argument");
+    size_t a = 0;
+    const int st = vokra_hip_kv_status(c, m->kv, &a);
+    if (n_appended) *n_appended = a;
+    return st ? st : vk::range_check(c);
 }
 
 int vokra_hip_decoder_step_dev(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t n, const int32_t* d_streams,
@@ -626,10 +652,19 @@ int vokra_hip_decoder_step(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t n,
         if (streams[i] < 0 || (size_t)streams[i] >= m->n_stream || seen[streams[i]])
             return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_step: streams must be distinct and < n_stream");
         seen[streams[i]] = 1;
+        if (!m->enc_set[streams[i]])
+            return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                                "decoder_step: stream %d has no encoder output (call set_encoder first)", streams[i]);
         if (tokens[i] < 0 || (size_t)tokens[i] >= m->vocab)
             return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "whisper decoder: token id >= n_vocab");
         if (positions[i] < 0 || (size_t)positions[i] + 1 > m->n_text)
             return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "whisper decoder: position exceeds n_text_ctx");
+        // the step position is the stream's current length (decoder.rs:427-434
+        // takes start = self_kv.positions()); 0 restarts the stream
+        if (positions[i] != 0 && positions[i] != m->length[streams[i]])
+            return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                                "decoder_step: stream %d is at position %d, got %d (0 restarts it)", streams[i],
+                                m->length[streams[i]], positions[i]);
     }
     std::vector<int32_t> items(3 * n);
     memcpy(items.data(), streams, n * 4);
@@ -640,9 +675,10 @@ int vokra_hip_decoder_step(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t n,
     SS_TRY(dec_step(m, n, dv, dv + n, dv + 2 * n, m->next.i(), logits ? m->logits.f() : nullptr));
     size_t appended = 0;
     SS_TRY(vokra_hip_kv_status(c, m->kv, &appended));
+    for (size_t i = 0; i < n; ++i) m->length[streams[i]] = positions[i] + 1;  // the rows are appended
     SS_TRY(vokra_hip_memcpy_dtoh(c, next_tokens, m->next.p, n * 4));
     if (logits) SS_TRY(vokra_hip_memcpy_dtoh(c, logits, m->logits.p, n * m->vocab * sizeof(float)));
-    return VOKRA_HIP_OK;
+    return vk::range_check(c);
 }
 
 }  // extern "C"

@@ -236,6 +236,7 @@ def _declare(L):
     L.vokra_hip_decoder_reset.argtypes = [P, P]
     L.vokra_hip_decoder_step.argtypes = [P, P, sz, i32p, i32p, i32p, i32p, f32p]
     L.vokra_hip_decoder_step_dev.argtypes = [P, P, sz, P, P, P, P, P]
+    L.vokra_hip_decoder_status.argtypes = [P, P, C.POINTER(sz)]
     L.vokra_hip_attn_f32.argtypes = [P, sz, sz, sz, sz, sz, sz, f32p, f32p, f32p, C.c_float, C.c_int, sz, f32p]
     L.vokra_hip_attn_f32_dev.argtypes = [P, sz, sz, sz, sz, sz, sz, P, P, P, C.c_float, C.c_int, sz, P]
 
@@ -681,6 +682,13 @@ class Decoder:
         _check(lib().vokra_hip_decoder_step_dev(self._ctx._h, self._h, n, d_streams.ptr, d_tokens.ptr,
                                                 d_positions.ptr, d_next.ptr,
                                                 None if d_logits is None else d_logits.ptr))
+
+    def status(self) -> int:
+        """Synchronizes; raises for a failed page allocation of the last
+        step, returns the (layer, item) appends done."""
+        n = C.c_size_t(0)
+        _check(lib().vokra_hip_decoder_status(self._ctx._h, self._h, C.byref(n)))
+        return n.value
 
     def __del__(self):
         try:
