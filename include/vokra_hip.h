@@ -550,6 +550,86 @@ int vokra_hip_decoder_step_dev(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, s
  * then INVALID_ARGUMENT if an attention operand left the fp16 range. */
 int vokra_hip_decoder_status(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t *n_appended);
 
+/* ---- speech-LLM text decoder (Voxtral-style backbone) ------------------- */
+
+/* rope_apply (crates/vokra-models/src/voxtral/text_decoder.rs:858-891) on every
+ * head of x [seq_len, n_head * head_dim], in place, host memory: row i is at
+ * position position_offset + i and each head's pairs (j, j + head_dim/2)
+ * rotate by m * theta_j. theta_j = rope_base^(-2j/head_dim) is evaluated on the
+ * host with the reference's f32 expression (so the angle is its f32 product),
+ * sin / cos on the device (about 1 ulp of libm). An odd head_dim or a length
+ * mismatch is INVALID_ARGUMENT, as rope_apply's. */
+int vokra_hip_rope_f32(vokra_hip_ctx_t *ctx, float *x, size_t x_len, size_t seq_len, size_t n_head, size_t head_dim,
+                       float rope_base, size_t position_offset);
+/* Device rows d_x [rows, n_head * head_dim], row r at position d_positions[r].
+ * The context keeps the frequency table of the last (rope_base, head_dim); a
+ * new pair uploads its table synchronously first (not capturable). */
+int vokra_hip_rope_f32_dev(vokra_hip_ctx_t *ctx, float *d_x, size_t rows, size_t n_head, size_t head_dim,
+                           float rope_base, const int32_t *d_positions);
+/* The SwiGLU gate: silu_inplace then hadamard_inplace (text_decoder.rs:
+ * 826-847, sequenced at :1405-1410): out = (g * (1 / (1 + e^-g))) * up with the
+ * reference's roundings (device expf). A length mismatch is INVALID_ARGUMENT. */
+int vokra_hip_swiglu_f32(vokra_hip_ctx_t *ctx, const float *gate, size_t gate_len, const float *up, size_t up_len,
+                         float *out);
+int vokra_hip_swiglu_f32_dev(vokra_hip_ctx_t *ctx, const float *d_gate, const float *d_up, size_t n, float *d_out);
+
+/* One pre-norm block of the text decoder with quantized, bias-free linears
+ * (the quant counterpart of DecoderBlock with its GqaAttention and SwiGluFfn,
+ * crates/vokra-models/src/voxtral/text_decoder.rs:82-107, which hold
+ * transposed f32 weights); wire-format weights [out, in]. */
+typedef struct vokra_hip_text_decoder_layer {
+    const float *attn_norm_gamma;          /* [d] */
+    const uint8_t *wq, *wk, *wv, *wo;      /* [n_head_q*hd, d], [n_head_kv*hd, d] x 2, [d, n_head_q*hd] */
+    const float *ffn_norm_gamma;           /* [d] */
+    const uint8_t *w_gate, *w_up, *w_down; /* [ffn, d] x 2, [d, ffn] */
+} vokra_hip_text_decoder_layer_t;
+
+typedef struct vokra_hip_text_decoder vokra_hip_text_decoder_t;
+
+/* Device-resident text decoder for n_stream concurrent streams. Replaces
+ * voxtral::TextDecoderSession (crates/vokra-models/src/voxtral/
+ * text_decoder_session.rs:54-330) with a batch axis and, instead of the
+ * reference's f32 KvCache, the paged Q8_0 cache of vokra_hip_kv_* (n_head_kv
+ * heads, block_size-token pages, n_ctx positions). Every linear is
+ * gemm_q_f32 of wdtype (Q4_K: kquant_gemm_i8). lm_head: wire bytes [vocab, d]
+ * of wdtype, or NULL for the tied f32 token embedding
+ * (TextDecoder::output_head, text_decoder.rs:665). Config checks as TextDecoderSession::new
+ * (0-sentinels and n_head_q % n_head_kv are MODEL_LOAD); head_dim 64 or 128
+ * and 1, 2, 4 or 8 query heads per kv head (else UNSUPPORTED_OP). */
+int vokra_hip_text_decoder_create(vokra_hip_ctx_t *ctx, int wdtype, size_t n_layer, size_t d_model,
+                                  size_t n_head_q, size_t n_head_kv, size_t head_dim, size_t ffn_dim, size_t vocab,
+                                  size_t n_ctx, size_t n_stream, size_t block_size, float rope_base,
+                                  float rms_norm_eps, const vokra_hip_text_decoder_layer_t *layers,
+                                  const float *token_emb, const float *final_norm_gamma, const uint8_t *lm_head,
+                                  vokra_hip_text_decoder_t **out);
+void vokra_hip_text_decoder_destroy(vokra_hip_text_decoder_t *dec);
+/* TextDecoderSession::reset (text_decoder_session.rs:192): every stream back to position 0. */
+int vokra_hip_text_decoder_reset(vokra_hip_ctx_t *ctx, vokra_hip_text_decoder_t *dec);
+/* TextDecoderSession::position (text_decoder_session.rs:187) of one stream. */
+int vokra_hip_text_decoder_position(vokra_hip_ctx_t *ctx, vokra_hip_text_decoder_t *dec, size_t stream,
+                                    size_t *position);
+/* TextDecoderSession::kv_restore (text_decoder_session.rs:390-405) for one
+ * stream from rows instead of a snapshot: k_rows / v_rows [n_layer][n_pos]
+ * [n_head_kv * head_dim] (K after RoPE, as the cache holds them) become the
+ * stream's history and its position is set to n_pos. Host arrays, synchronous. */
+int vokra_hip_text_decoder_kv_restore(vokra_hip_ctx_t *ctx, vokra_hip_text_decoder_t *dec, size_t stream,
+                                      size_t n_pos, const float *k_rows, const float *v_rows);
+/* TextDecoderSession::step_into (text_decoder_session.rs:207-240) with one
+ * token for each of n distinct streams, at each stream's own position, then
+ * greedy argmax into next_tokens[i]; logits [n, vocab] when not NULL. Host
+ * arrays, synchronous; forward_step's rejections (token >= vocab, position
+ * beyond n_ctx; text_decoder.rs:1007-1045). */
+int vokra_hip_text_decoder_step(vokra_hip_ctx_t *ctx, vokra_hip_text_decoder_t *dec, size_t n,
+                                const int32_t *streams, const int32_t *tokens, int32_t *next_tokens, float *logits);
+/* Device arrays, asynchronous; positions[i] is stream i's position, which the
+ * caller tracks (these calls do not move the host clocks of the host variant:
+ * drive a session through one of the two). vokra_hip_text_decoder_status
+ * reports the step's page allocation and the attention range check. */
+int vokra_hip_text_decoder_step_dev(vokra_hip_ctx_t *ctx, vokra_hip_text_decoder_t *dec, size_t n,
+                                    const int32_t *d_streams, const int32_t *d_tokens, const int32_t *d_positions,
+                                    int32_t *d_next_tokens, float *d_logits);
+int vokra_hip_text_decoder_status(vokra_hip_ctx_t *ctx, vokra_hip_text_decoder_t *dec, size_t *n_appended);
+
 #ifdef __cplusplus
 }
 #endif

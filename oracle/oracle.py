@@ -104,6 +104,9 @@ def _declare(L):
     L.vo_erf_as.restype = C.c_float
     L.vo_erf_as.argtypes = [C.c_float]
     L.vo_rms_norm_f32.argtypes = [_f32p, _f32p, C.c_float, _sz, _sz, _f32p]
+    L.vo_rope_apply.argtypes = [_f32p, _sz, _sz, _sz, C.c_float, _sz]
+    L.vo_silu_inplace.argtypes = [_f32p, _sz]
+    L.vo_hadamard_inplace.argtypes = [_f32p, _sz, _f32p, _sz]
     L.vo_sdpa_whisper.argtypes = [_sz, _sz, _sz, _sz, _f32p, _f32p, _f32p, C.c_int, _sz, _f32p]
     L.vo_gqa_attention.argtypes = [_sz, _sz, _sz, _sz, _sz, _f32p, _f32p, _f32p, C.c_float, _sz, _f32p]
     L.vo_paged_create.argtypes = [_sz, _sz, _sz, _sz, _sz, _sz, C.c_int, C.POINTER(C.c_void_p)]
@@ -367,6 +370,45 @@ def rms_norm_f32(x, gamma, eps, rows, d):
     out = np.zeros(rows * d, np.float32)
     lib().vo_rms_norm_f32(_p(xv, _f32p), _p(g, _f32p), eps, rows, d, _p(out, _f32p))
     return out.reshape(rows, d)
+
+
+def rope_apply(x, seq_len, head_dim, rope_base, position_offset):
+    """text_decoder.rs:858-891 on one head's [seq_len, head_dim]; returns a copy."""
+    xv = _f32(x).copy()
+    _check(lib().vo_rope_apply(_p(xv, _f32p), xv.size, seq_len, head_dim, rope_base, position_offset),
+           "rope_apply")
+    return xv
+
+
+def rope_heads(x, n_head, head_dim, rope_base, position_offset):
+    """rope_apply per head of x [seq_len, n_head * head_dim] (the loop of
+    text_decoder.rs:1230-1275)."""
+    xv = _f32(x)
+    t = xv.size // (n_head * head_dim)
+    xv = xv.reshape(t, n_head, head_dim)
+    out = np.empty_like(xv)
+    for h in range(n_head):
+        out[:, h, :] = rope_apply(xv[:, h, :], t, head_dim, rope_base, position_offset).reshape(t, head_dim)
+    return out.reshape(t, n_head * head_dim)
+
+
+def silu(x):
+    """text_decoder.rs:826-831 silu_inplace, on a copy."""
+    xv = _f32(x).copy()
+    lib().vo_silu_inplace(_p(xv, _f32p), xv.size)
+    return xv
+
+
+def hadamard(a, b):
+    """text_decoder.rs:835-847 hadamard_inplace, on a copy of a."""
+    av, bv = _f32(a).copy(), _f32(b)
+    _check(lib().vo_hadamard_inplace(_p(av, _f32p), av.size, _p(bv, _f32p), bv.size), "hadamard_inplace")
+    return av
+
+
+def swiglu(gate, up):
+    """silu(gate) * up exactly as text_decoder.rs:1405-1410 sequences it."""
+    return hadamard(silu(gate), up)
 
 
 # ---- attention ---------------------------------------------------------

@@ -853,6 +853,46 @@ void vo_rms_norm_f32(const float *x, const float *gamma, float eps, size_t rows,
     }
 }
 
+/* crates/vokra-models/src/voxtral/text_decoder.rs:858-891 rope_apply: one
+ * head's x [seq_len, head_dim] in place; row i at position
+ * position_offset + i rotates the pairs (j, j + head_dim/2) by the angle
+ * m * theta_j, theta_j = rope_base^(-2j / head_dim), evaluated per element as
+ * the reference does (powf, then the f32 product, then sinf / cosf). */
+int vo_rope_apply(float *x, size_t x_len, size_t seq_len, size_t head_dim, float rope_base, size_t position_offset) {
+    if (head_dim % 2 != 0) return VO_INVALID_ARGUMENT;
+    if (x_len != seq_len * head_dim) return VO_INVALID_ARGUMENT;
+    size_t half = head_dim / 2;
+    for (size_t i = 0; i < seq_len; ++i) {
+        float m = (float)(position_offset + i);
+        float *row = x + i * head_dim;
+        for (size_t j = 0; j < half; ++j) {
+            float theta = powf(rope_base, -2.0f * (float)j / (float)head_dim);
+            float angle = m * theta;
+            float s = sinf(angle), c = cosf(angle);
+            float a = row[j], b = row[j + half];
+            row[j] = a * c - b * s;
+            row[j + half] = a * s + b * c;
+        }
+    }
+    return VO_OK;
+}
+
+/* text_decoder.rs:826-831 silu_inplace: x <- x * (1 / (1 + exp(-x))). */
+void vo_silu_inplace(float *x, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        float s = 1.0f / (1.0f + expf(-x[i]));
+        x[i] = x[i] * s;
+    }
+}
+
+/* text_decoder.rs:835-847 hadamard_inplace: a <- a * b; a length mismatch is
+ * InvalidArgument. */
+int vo_hadamard_inplace(float *a, size_t a_len, const float *b, size_t b_len) {
+    if (a_len != b_len) return VO_INVALID_ARGUMENT;
+    for (size_t i = 0; i < a_len; ++i) a[i] = a[i] * b[i];
+    return VO_OK;
+}
+
 /* ========================================================================
  * Attention (A13, A14)
  * ====================================================================== */

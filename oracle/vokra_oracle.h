@@ -98,6 +98,9 @@ void vo_layer_norm_f32(const float *in, float *out, size_t rows, size_t cols, co
 void vo_gelu_f32(const float *x, float *out, size_t n);
 float vo_erf_as(float x);
 void vo_rms_norm_f32(const float *x, const float *gamma, float eps, size_t rows, size_t d, float *out);
+int vo_rope_apply(float *x, size_t x_len, size_t seq_len, size_t head_dim, float rope_base, size_t position_offset);
+void vo_silu_inplace(float *x, size_t n);
+int vo_hadamard_inplace(float *a, size_t a_len, const float *b, size_t b_len);
 
 /* ---- attention (A13, A14) ----------------------------------------------- */
 int vo_sdpa_whisper(size_t t_q, size_t t_kv, size_t n_head, size_t hd, const float *q,

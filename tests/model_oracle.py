@@ -83,3 +83,70 @@ class Decoder:
         xn = ln(o, h, *self.lnp)
         logits = o.gemv_f32(self.tok_emb.shape[0], d, self.tok_emb, xn[0])
         return logits, o.argmax(logits)
+
+
+W_Q4_K = 12
+
+
+def random_text_layer(orc, g, d, hq, hkv, hd, ff, scale=0.05):
+    """One speech-LLM block with Q4_K linears quantized by the oracle's
+    quantize.rs restatement, norms near one."""
+    L = {"attn_norm_gamma": (1 + 0.1 * g.standard_normal(d)).astype(np.float32),
+         "ffn_norm_gamma": (1 + 0.1 * g.standard_normal(d)).astype(np.float32)}
+    for name, n, k in (("wq", hq * hd, d), ("wk", hkv * hd, d), ("wv", hkv * hd, d), ("wo", d, hq * hd),
+                       ("w_gate", ff, d), ("w_up", ff, d), ("w_down", d, ff)):
+        L[name] = orc.kquant_quantize(W_Q4_K, (g.standard_normal((n, k)) * scale).astype(np.float32).reshape(-1))
+    return L
+
+
+class TextDecoder:
+    """Per-stream speech-LLM decode step: the sequence of
+    crates/vokra-models/src/voxtral/text_decoder.rs:1147-1420 (RMSNorm, q/k/v,
+    RoPE per head at the stream's position, GQA over the cache with the scale
+    after the dot, o-proj + residual, RMSNorm, SwiGLU FFN + residual, final
+    RMSNorm, LM head), every linear through the oracle's gemm_q_f32 (Q4_K:
+    kquant_gemm_i8) and the K/V through the QuantizedPagedKvCache restatement
+    (Q8_0 rows). lm_head: Q4_K wire bytes [vocab, d], or None for the f32
+    token embedding (tied)."""
+
+    def __init__(self, orc, layers, tok_emb, final_gamma, lm_head, hq, hkv, hd, ff, n_stream, n_ctx, bs,
+                 rope_base, eps):
+        self.orc, self.layers, self.tok_emb, self.final_gamma, self.lm_head = orc, layers, tok_emb, final_gamma, lm_head
+        self.d = tok_emb.shape[1]
+        self.hq, self.hkv, self.hd, self.ff = hq, hkv, hd, ff
+        self.rope_base, self.eps = rope_base, eps
+        self.scale = np.float32(1.0) / np.sqrt(np.float32(hd))   # 1 / (hd as f32).sqrt()
+        self.cache = orc.PagedCache(len(layers), hkv, hd, n_stream, n_ctx, bs, Q8_0_MODE)
+
+    def restore(self, s, k_rows, v_rows):
+        """Appends history rows [n_layer][n_pos][kv_hidden] for stream s."""
+        for li in range(len(self.layers)):
+            for t in range(k_rows.shape[1]):
+                assert self.cache.append_step(li, t, s, k_rows[li, t], v_rows[li, t]) == 0
+
+    def lin(self, x, w, n, k):
+        return qlin(self.orc, W_Q4_K, x, w, n, k)
+
+    def step(self, s, token, pos):
+        o, d, hq, hkv, hd, ff = self.orc, self.d, self.hq, self.hkv, self.hd, self.ff
+        h = self.tok_emb[token].astype(np.float32)[None].copy()
+        for li, L in enumerate(self.layers):
+            x = o.rms_norm_f32(h, L["attn_norm_gamma"], self.eps, 1, d)
+            q = o.rope_heads(self.lin(x, L["wq"], hq * hd, d), hq, hd, self.rope_base, pos)
+            k = o.rope_heads(self.lin(x, L["wk"], hkv * hd, d), hkv, hd, self.rope_base, pos)
+            v = self.lin(x, L["wv"], hkv * hd, d)
+            assert self.cache.append_step(li, pos, s, k[0], v[0]) == 0
+            rows = [self.cache.read_step(li, t, s) for t in range(pos + 1)]
+            K = np.stack([r[0] for r in rows])
+            V = np.stack([r[1] for r in rows])
+            a = o.gqa_attention(1, pos + 1, hq, hkv, hd, q, K, V, float(self.scale), pos)
+            h = h + self.lin(a, L["wo"], d, hq * hd)
+            x = o.rms_norm_f32(h, L["ffn_norm_gamma"], self.eps, 1, d)
+            f = o.swiglu(self.lin(x, L["w_gate"], ff, d), self.lin(x, L["w_up"], ff, d))
+            h = h + self.lin(f, L["w_down"], d, ff)
+        x = o.rms_norm_f32(h, self.final_gamma, self.eps, 1, d)
+        if self.lm_head is None:
+            logits = o.gemv_f32(self.tok_emb.shape[0], d, self.tok_emb, x[0])
+        else:
+            logits = self.lin(x, self.lm_head, self.tok_emb.shape[0], d)[0]
+        return logits, o.argmax(logits)

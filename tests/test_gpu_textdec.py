@@ -1,0 +1,331 @@
+"""GPU parity of the speech-LLM text-decoder path (config 4): RoPE, SwiGLU and
+the batched device-resident step over Q4_K linears and the paged Q8_0 cache.
+
+Bars:
+  * ops: RoPE and SwiGLU against the oracle's restatements of rope_apply /
+    silu_inplace + hadamard_inplace, within bounds derived from the one place
+    they differ (device sin / cos / exp against libm, a few ulp);
+  * session == the same step issued one C-ABI entry point at a time, bit for
+    bit, at config-4 dims (every kernel on the path is row-independent, and
+    the paged attention's results depend only on an item's own keys);
+  * teacher-forced: every entry point of that chain, fed the GPU's own inputs,
+    against the oracle function it replaces (Q4_K linears bit-exact, RMSNorm
+    / RoPE / SwiGLU / attention within their derived bounds), so a systematic
+    error anywhere in the step fails;
+  * free-running session vs the oracle composition (tests/model_oracle.py):
+    logits within 0.1 rms (INT8 rounding flips spread) and greedy tokens equal
+    wherever the oracle's top-2 gap is wider than that.
+"""
+import numpy as np
+import pytest
+
+from tests import model_oracle
+from vokra_amd import hip
+
+pytestmark = pytest.mark.gpu
+
+W_Q4_K = 12
+U = 2.0 ** -24
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = hip.HipContext(0)
+    yield c
+    c.close()
+
+
+# ---- ops -----------------------------------------------------------------
+@pytest.mark.parametrize("n_head,hd,base", [(16, 128, 1e6), (2, 128, 1e6), (4, 64, 1e4)])
+def test_rope_vs_oracle(ctx, oracle, n_head, hd, base):
+    print(f"[case] rope H={n_head} hd={hd}", flush=True)
+    g = np.random.default_rng(hd + n_head)
+    for off, t in ((0, 1), (5, 3), (511, 2), (4094, 2)):
+        x = g.standard_normal((t, n_head * hd)).astype(np.float32)
+        got = ctx.rope_f32(x, t, n_head, hd, base, off).reshape(t, n_head * hd)
+        want = oracle.rope_heads(x, n_head, hd, base, off)
+        xr = x.reshape(t, n_head, 2, hd // 2)
+        mag = np.abs(xr[:, :, 0, :]) + np.abs(xr[:, :, 1, :])
+        bound = np.concatenate([mag, mag], axis=-1).reshape(t, -1).astype(np.float64) * 8 * U
+        err = np.abs(got.astype(np.float64) - want)
+        assert np.all(err <= bound + 1e-30), (off, float(np.max(err - bound)))
+    # position 0 is the identity, exactly
+    x = g.standard_normal((1, n_head * hd)).astype(np.float32)
+    assert np.array_equal(ctx.rope_f32(x, 1, n_head, hd, base, 0), x)
+    # per-row positions on device == copy mode at the same offsets
+    rows = g.standard_normal((3, n_head * hd)).astype(np.float32)
+    d_x = hip.DeviceBuffer.from_array(ctx, rows)
+    d_p = hip.DeviceBuffer.from_array(ctx, np.array([7, 0, 4000], np.int32))
+    ctx.rope_f32_dev(d_x, 3, n_head, hd, base, d_p)
+    dev = d_x.download(np.float32, rows.size).reshape(3, -1)
+    for r, p in enumerate((7, 0, 4000)):
+        assert np.array_equal(dev[r], ctx.rope_f32(rows[r], 1, n_head, hd, base, p).reshape(-1))
+
+
+def test_rope_rejections(ctx):
+    with pytest.raises(hip.InvalidArgument, match="even"):
+        ctx.rope_f32(np.zeros(3, np.float32), 1, 1, 3, 1e4, 0)
+    with pytest.raises(hip.InvalidArgument, match="len"):
+        ctx.rope_f32(np.zeros(5, np.float32), 1, 1, 4, 1e4, 0)
+
+
+def test_swiglu_vs_oracle(ctx, oracle):
+    print("[case] swiglu", flush=True)
+    g = np.random.default_rng(3)
+    gate = np.concatenate([np.linspace(-30, 30, 6001), g.standard_normal(20000) * 4]).astype(np.float32)
+    up = g.standard_normal(gate.size).astype(np.float32)
+    got = ctx.swiglu_f32(gate, up).astype(np.float64)
+    want = oracle.swiglu(gate, up).astype(np.float64)
+    # the device expf and libm expf differ by at most a couple of ulp; the
+    # add, divide and two products then keep it within 8 ulp of the result
+    assert np.all(np.abs(got - want) <= 8 * U * np.abs(want) + 1e-38)
+    with pytest.raises(hip.InvalidArgument, match="length mismatch"):
+        ctx.swiglu_f32(gate[:4], up[:3])
+
+
+# ---- the session -----------------------------------------------------------
+def make_layers(oracle, g, n_layer, d, hq, hkv, hd, ff, scale=0.03):
+    return [model_oracle.random_text_layer(oracle, g, d, hq, hkv, hd, ff, scale) for _ in range(n_layer)]
+
+
+class TextDecoderByOps:
+    """The text-decoder step issued one C-ABI entry point at a time: RMSNorm,
+    Q4_K linears (kquant_gemm_i8), RoPE per row at its position, the paged
+    cache's append and decode attention, SwiGLU, residual adds in numpy,
+    final RMSNorm, LM head and argmax. With `check`, each entry point's
+    output is also held against the oracle on the same inputs."""
+
+    def __init__(self, ctx, P, n_stream, check=None):
+        self.ctx, self.P, self.check = ctx, P, check
+        self.kv = ctx.kv_cache(len(P["layers"]), P["hkv"], P["hd"], n_stream, P["n_ctx"], P["bs"])
+        self.pos = [0] * n_stream
+        self.worst = {}
+
+    def note(self, what, err):
+        self.worst[what] = max(self.worst.get(what, 0.0), float(err))
+
+    def restore(self, s, k_rows, v_rows):
+        for l in range(k_rows.shape[0]):
+            for t0 in range(0, k_rows.shape[1], 1024):
+                t1 = min(k_rows.shape[1], t0 + 1024)
+                self.kv.append(l, [s] * (t1 - t0), list(range(t0, t1)), k_rows[l, t0:t1], v_rows[l, t0:t1])
+        self.pos[s] = k_rows.shape[1]
+
+    def lin(self, x, w, n, k):
+        y = self.ctx.gemm_q_f32(x.shape[0], n, k, x, w, hip.WDtype.Q4_K)
+        if self.check is not None:
+            rows = min(2, x.shape[0])
+            want = self.check.gemm_q_f32(W_Q4_K, rows, n, k, x[:rows], w)
+            assert np.array_equal(y[:rows].view(np.uint32), want.view(np.uint32)), "Q4_K linear"
+        return y
+
+    def rms(self, h, gamma):
+        n, d = h.shape
+        y = self.ctx.rms_norm_f32(h, n, d, gamma, self.P["eps"])
+        if self.check is not None:
+            want = self.check.rms_norm_f32(h, gamma, self.P["eps"], n, d).astype(np.float64)
+            err = np.abs(y - want) / (np.abs(want) + 1e-30)
+            self.note("rms_norm rel", err.max())
+            assert np.all(np.abs(y - want) <= (d / 2 + 8) * U * np.abs(want) + 1e-30), "rms_norm"
+        return y
+
+    def rope(self, x, n_head, positions):
+        P = self.P
+        out = np.stack([self.ctx.rope_f32(x[i], 1, n_head, P["hd"], P["base"], p) for i, p in enumerate(positions)])
+        if self.check is not None:
+            for i, p in enumerate(positions[:2]):
+                want = self.check.rope_heads(x[i:i + 1], n_head, P["hd"], P["base"], p)[0]
+                xr = x[i].reshape(n_head, 2, P["hd"] // 2)
+                mag = np.abs(xr[:, 0]) + np.abs(xr[:, 1])
+                bound = np.concatenate([mag, mag], axis=-1).reshape(-1) * 8 * U
+                assert np.all(np.abs(out[i] - want) <= bound + 1e-30), "rope"
+        return out
+
+    def step(self, streams, tokens):
+        ctx, P = self.ctx, self.P
+        n, d, hq, hkv, hd, ff = len(streams), P["d"], P["hq"], P["hkv"], P["hd"], P["ff"]
+        positions = [self.pos[s] for s in streams]
+        lens = [p + 1 for p in positions]
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+        h = P["tok"][tokens].astype(np.float32)
+        for l, L in enumerate(P["layers"]):
+            x = self.rms(h, L["attn_norm_gamma"])
+            q = self.rope(self.lin(x, L["wq"], hq * hd, d), hq, positions)
+            k = self.rope(self.lin(x, L["wk"], hkv * hd, d), hkv, positions)
+            v = self.lin(x, L["wv"], hkv * hd, d)
+            self.kv.append(l, streams, positions, k, v)
+            a = self.kv.attn(l, streams, lens, q, hq, scale)
+            if self.check is not None:
+                s0 = streams[0]
+                rows = [self.kv.read(l, t, s0) for t in range(lens[0])]
+                K = np.stack([r[0] for r in rows])
+                V = np.stack([r[1] for r in rows])
+                want = self.check.gqa_attention(1, lens[0], hq, hkv, hd, q[0:1], K, V, scale, positions[0])[0]
+                err = np.abs(a[0] - want)
+                self.note("attention", err.max())
+                assert np.all(err <= 1e-4 + 1e-3 * np.abs(want)), "attention"
+            h = self.lin(a, L["wo"], d, hq * hd) + h
+            x = self.rms(h, L["ffn_norm_gamma"])
+            gt, up = self.lin(x, L["w_gate"], ff, d), self.lin(x, L["w_up"], ff, d)
+            f = ctx.swiglu_f32(gt, up).reshape(n, ff)
+            if self.check is not None:
+                want = self.check.swiglu(gt[:2], up[:2]).astype(np.float64)
+                assert np.all(np.abs(f[:2] - want) <= 8 * U * np.abs(want) + 1e-38), "swiglu"
+            h = self.lin(f, L["w_down"], d, ff) + h
+        x = self.rms(h, P["final"])
+        for s in streams:
+            self.pos[s] += 1
+        if P["head"] is not None:
+            logits = self.lin(x, P["head"], P["V"], d)
+            return np.argmax(logits, axis=1).astype(np.int32), logits
+        # tied head: the fused f32 logits + argmax entry point
+        V = P["V"]
+        d_x, d_e = hip.DeviceBuffer.from_array(ctx, x), hip.DeviceBuffer.from_array(ctx, P["tok"])
+        d_l, d_n = hip.DeviceBuffer(ctx, n * V * 4), hip.DeviceBuffer(ctx, n * 4)
+        ctx.logits_argmax_dev(n, V, d, d_x, d_e, d_l, d_n)
+        ctx.synchronize()
+        return d_n.download(np.int32, n), d_l.download(np.float32, n * V).reshape(n, V)
+
+
+def build(ctx, oracle, seed, n_layer, d, hq, hkv, hd, ff, V, n_ctx, n_stream, bs=16, tied=False, base=1e6,
+          eps=1e-5):
+    g = np.random.default_rng(seed)
+    layers = make_layers(oracle, g, n_layer, d, hq, hkv, hd, ff)
+    tok = (g.standard_normal((V, d)) * 0.5).astype(np.float32)
+    fin = (1 + 0.1 * g.standard_normal(d)).astype(np.float32)
+    head = None if tied else oracle.kquant_quantize(W_Q4_K, (g.standard_normal((V, d)) * 0.03).astype(np.float32)
+                                                     .reshape(-1))
+    P = dict(layers=layers, tok=tok, final=fin, head=head, d=d, hq=hq, hkv=hkv, hd=hd, ff=ff, V=V, n_ctx=n_ctx,
+             bs=bs, base=base, eps=eps)
+    dec = hip.TextDecoder(ctx, W_Q4_K, d, hq, hkv, hd, ff, V, n_ctx, n_stream, layers, tok, fin, head,
+                          rope_base=base, rms_norm_eps=eps, block_size=bs)
+    return dec, P
+
+
+def history(g, n_layer, n_pos, w, scale=1.0):
+    k = (g.standard_normal((n_layer, n_pos, w)) * scale).astype(np.float32)
+    v = (g.standard_normal((n_layer, n_pos, w)) * scale).astype(np.float32)
+    return k, v
+
+
+@pytest.mark.parametrize("tied", [False, True])
+def test_text_decoder_small_vs_oracle(ctx, oracle, tied):
+    """Toy dims (d=256, 4/2 heads x 64): session == entry points bit for bit,
+    teacher-forced entry points vs the oracle, free-running vs the oracle."""
+    print(f"[case] text decoder small tied={tied}", flush=True)
+    d, hq, hkv, hd, ff, V, n_ctx, n_stream = 256, 4, 2, 64, 512, 96, 64, 3
+    dec, P = build(ctx, oracle, 11, 2, d, hq, hkv, hd, ff, V, n_ctx, n_stream, bs=4, tied=tied)
+    ops = TextDecoderByOps(ctx, P, n_stream, check=oracle)
+    ref = model_oracle.TextDecoder(oracle, P["layers"], P["tok"], P["final"], P["head"], hq, hkv, hd, ff, n_stream,
+                                   n_ctx, 4, P["base"], P["eps"])
+    tok = [1, 2, 3]
+    schedule = [[0, 1, 2], [0, 1], [2, 0], [1, 2, 0], [0], [2, 1, 0]]
+    for step, streams in enumerate(schedule):
+        args = [tok[s] for s in streams]
+        nxt, logits = dec.step(streams, args, want_logits=True)
+        n2, l2 = ops.step(streams, args)
+        assert np.array_equal(logits, l2) and np.array_equal(nxt, n2), (step, streams)
+        for i, s in enumerate(streams):
+            want, want_tok = ref.step(s, tok[s], dec.position(s) - 1)
+            rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+            err = float(np.max(np.abs(logits[i] - want)))
+            assert err <= 0.1 * rms + 1e-4, (step, s, err, rms)
+            top2 = np.sort(want)[-2:]
+            if top2[1] - top2[0] > 0.1 * rms + 1e-4:
+                assert nxt[i] == want_tok, (step, s)
+            tok[s] = int(nxt[i])
+
+
+def test_text_decoder_config4_dims(ctx, oracle):
+    """Config-4 shapes (d=2048, 16/2 heads x 128, FFN 5632, 32000-token Q4_K
+    LM head) with 2 layers and 6 streams whose histories (restored rows)
+    reach 512..4096 positions: session == entry points bit for bit over
+    ragged steps, every entry point teacher-forced against the oracle, the
+    session free-running against the oracle composition, and batch ==
+    single-stream steps in a twin session."""
+    print("[case] text decoder config-4 dims", flush=True)
+    d, hq, hkv, hd, ff, V, n_ctx, n_stream, n_layer = 2048, 16, 2, 128, 5632, 32000, 4096, 6, 2
+    dec, P = build(ctx, oracle, 4, n_layer, d, hq, hkv, hd, ff, V, n_ctx, n_stream)
+    twin, _ = build(ctx, oracle, 4, n_layer, d, hq, hkv, hd, ff, V, n_ctx, n_stream)
+    ops = TextDecoderByOps(ctx, P, n_stream, check=oracle)
+    ref = model_oracle.TextDecoder(oracle, P["layers"], P["tok"], P["final"], P["head"], hq, hkv, hd, ff, n_stream,
+                                   n_ctx, 16, P["base"], P["eps"])
+    g = np.random.default_rng(40)
+    lens = [512, 4090, 1000, 2048, 3584, 600]
+    for s, n_pos in enumerate(lens):
+        k, v = history(g, n_layer, n_pos, hkv * hd)
+        dec.kv_restore(s, k, v)
+        twin.kv_restore(s, k, v)
+        ops.restore(s, k, v)
+        ref.restore(s, k, v)
+        assert dec.position(s) == n_pos
+    tok = [int(t) for t in g.integers(0, V, n_stream)]
+    for step, streams in enumerate([[0, 1, 2, 3, 4, 5], [5, 1, 3], [2, 0, 4, 1]]):
+        args = [tok[s] for s in streams]
+        pos_before = [dec.position(s) for s in streams]
+        nxt, logits = dec.step(streams, args, want_logits=True)
+        n2, l2 = ops.step(streams, args)
+        assert np.array_equal(logits, l2) and np.array_equal(nxt, n2), (step, streams)
+        for i, s in enumerate(streams):
+            n1, l1 = twin.step([s], [args[i]], want_logits=True)
+            assert np.array_equal(l1[0], logits[i]) and n1[0] == nxt[i], (step, s)
+        for i, s in enumerate(streams):
+            want, want_tok = ref.step(s, tok[s], pos_before[i])
+            rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+            err = float(np.max(np.abs(logits[i] - want)))
+            assert err <= 0.1 * rms + 1e-4, (step, s, err, rms)
+            top2 = np.sort(want)[-2:]
+            if top2[1] - top2[0] > 0.1 * rms + 1e-4:
+                assert nxt[i] == want_tok, (step, s)
+        for i, s in enumerate(streams):
+            tok[s] = int(nxt[i])
+    print("[worst teacher-forced errors]", ops.worst, flush=True)
+
+
+def test_text_decoder_full_depth_equals_entry_points(ctx, oracle):
+    """All 24 config-4 layers, 32 streams with histories U(512..4096): two
+    batched steps are bit-identical to the entry-point chain."""
+    print("[case] text decoder 24 layers x 32 streams", flush=True)
+    d, hq, hkv, hd, ff, V, n_ctx, n_stream, n_layer = 2048, 16, 2, 128, 5632, 32000, 4096, 32, 24
+    dec, P = build(ctx, oracle, 24, n_layer, d, hq, hkv, hd, ff, V, n_ctx, n_stream)
+    ops = TextDecoderByOps(ctx, P, n_stream)
+    g = np.random.default_rng(24)
+    lens = g.integers(512, 4097, n_stream)
+    kk, vv = history(g, n_layer, int(lens.max()), hkv * hd)
+    for s in range(n_stream):
+        dec.kv_restore(s, kk[:, :lens[s]], vv[:, :lens[s]])
+        ops.restore(s, kk[:, :lens[s]], vv[:, :lens[s]])
+    streams = list(range(n_stream))
+    tok = [int(t) for t in g.integers(0, V, n_stream)]
+    for step in range(2):
+        live = [s for s in streams if lens[s] + step < n_ctx]
+        nxt, logits = dec.step(live, [tok[s] for s in live], want_logits=True)
+        n2, l2 = ops.step(live, [tok[s] for s in live])
+        assert np.array_equal(logits, l2) and np.array_equal(nxt, n2), step
+        for i, s in enumerate(live):
+            tok[s] = int(nxt[i])
+
+
+def test_text_decoder_rejections(ctx, oracle):
+    g = np.random.default_rng(5)
+    d, hq, hkv, hd, ff, V = 256, 4, 2, 64, 512, 50
+    layers = make_layers(oracle, g, 1, d, hq, hkv, hd, ff)
+    tok = np.zeros((V, d), np.float32)
+    fin = np.ones(d, np.float32)
+    dec = hip.TextDecoder(ctx, W_Q4_K, d, hq, hkv, hd, ff, V, 8, 2, layers, tok, fin, None, block_size=4)
+    with pytest.raises(hip.InvalidArgument, match="token id 50 >= vocab 50"):
+        dec.step([0], [50])
+    with pytest.raises(hip.InvalidArgument, match="distinct"):
+        dec.step([1, 1], [1, 2])
+    k, v = history(g, 1, 8, hkv * hd)
+    dec.kv_restore(0, k, v)
+    with pytest.raises(hip.InvalidArgument, match="position 9 > n_ctx 8"):
+        dec.step([0], [1])
+    dec.step([1], [1])                 # the other stream is unaffected
+    assert dec.position(1) == 1
+    dec.reset()
+    assert dec.position(0) == 0 and dec.position(1) == 0
+    with pytest.raises(hip.ModelLoad, match="divisible"):
+        hip.TextDecoder(ctx, W_Q4_K, d, 3, 2, hd, ff, V, 8, 1, layers, tok, fin)
+    with pytest.raises(hip.UnsupportedOp):
+        hip.TextDecoder(ctx, W_Q4_K, d, 4, 2, 96, ff, V, 8, 1, layers, tok, fin)

@@ -120,6 +120,10 @@ struct vokra_hip_ctx {
     DevBuf fe_win, fe_basis, fe_fb, fe_frames, fe_spec, fe_pow, fe_mel, fe_part, cv_col;
     int fe_mels = 0;
     DevBuf lg_part;  // per-workgroup (max, index) partials of the fused logits argmax
+    // RoPE frequency table of the last (rope_base, head_dim) the _dev entry saw
+    DevBuf rope_theta, rope_pos;
+    float rope_base = 0.0f;
+    size_t rope_hd = 0;
 };
 
 struct vokra_hip_qweight {
@@ -707,6 +711,18 @@ int kv_alloc_layers(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t first_layer, size
     return VOKRA_HIP_OK;
 }
 
+int kv_write_allocated(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
+                       const int* d_times, const float* d_k, const float* d_v) {
+    if (!c || !kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: bad context or cache");
+    if (layer >= kv->n_layer || n > 65535)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: layer %zu of %zu, %zu items", layer, kv->n_layer, n);
+    if (n && (!d_streams || !d_times || !d_k || !d_v)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_kv_write_allocated(c->stream, kv->view(), (int)layer, (int)n, d_streams, d_times, d_k, d_v),
+           "launch(vk_kv_write_allocated)");
+    return VOKRA_HIP_OK;
+}
+
 int paged_attn_append_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                                const int* d_times, const float* d_k, const float* d_v, const int* d_lens,
                                size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
@@ -1228,6 +1244,102 @@ int vokra_hip_gelu_f32(vokra_hip_ctx_t* c, const float* x, float* out, size_t n)
     return stage_out(c, out, c->out0.p, n);
 }
 
+// ---- speech-LLM text-decoder elementwise ops ---------------------------------
+
+namespace {
+// theta_j = rope_base.powf(-2.0 * (j as f32) / (head_dim as f32)), on the host
+// with the reference's f32 expression (text_decoder.rs:880), uploaded once per
+// (rope_base, head_dim).
+int rope_table(vokra_hip_ctx* c, float base, size_t hd) {
+    if (c->rope_theta.p && c->rope_base == base && c->rope_hd == hd) return VOKRA_HIP_OK;
+    std::vector<float> th(hd / 2);
+    for (size_t j = 0; j < th.size(); ++j) th[j] = powf(base, -2.0f * (float)j / (float)hd);
+    VK_TRY(c->rope_theta.ensure(th.size() * sizeof(float)), "hipMalloc(rope table)");
+    VK_TRY(hipMemcpyAsync(c->rope_theta.p, th.data(), th.size() * sizeof(float), hipMemcpyHostToDevice, c->stream),
+           "hipMemcpyAsync(rope table)");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    c->rope_base = base;
+    c->rope_hd = hd;
+    return VOKRA_HIP_OK;
+}
+
+int rope_check(size_t head_dim, size_t n_head, float rope_base) {
+    if (head_dim % 2 != 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "rope_apply: head_dim (%zu) must be even", head_dim);
+    if (head_dim == 0 || n_head == 0) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "rope_apply: head_dim and n_head > 0");
+    if (!(rope_base > 0.0f)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "rope_apply: rope_base must be > 0");
+    return VOKRA_HIP_OK;
+}
+}  // namespace
+
+int vokra_hip_rope_f32_dev(vokra_hip_ctx_t* c, float* d_x, size_t rows, size_t n_head, size_t head_dim,
+                           float rope_base, const int32_t* d_positions) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "rope_apply: ctx is NULL");
+    int st = rope_check(head_dim, n_head, rope_base);
+    if (st) return st;
+    if (rows == 0) return VOKRA_HIP_OK;
+    if (!d_x || !d_positions) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "rope_apply: NULL buffer");
+    if (rows * n_head * (head_dim / 2) > (size_t)INT32_MAX)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "rope_apply: too many elements");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    if ((st = rope_table(c, rope_base, head_dim))) return st;
+    VK_TRY(vk::launch_rope_rows(c->stream, d_x, (int)rows, (int)n_head, (int)head_dim, (const float*)c->rope_theta.p,
+                                d_positions, 0),
+           "launch(vk_rope_rows)");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_rope_f32(vokra_hip_ctx_t* c, float* x, size_t x_len, size_t seq_len, size_t n_head, size_t head_dim,
+                       float rope_base, size_t position_offset) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "rope_apply: ctx is NULL");
+    int st = rope_check(head_dim, n_head, rope_base);
+    if (st) return st;
+    if (x_len != seq_len * n_head * head_dim)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "rope_apply: x len %zu != seq_len*n_head*head_dim %zu", x_len,
+                    seq_len * n_head * head_dim);
+    if (seq_len == 0) return VOKRA_HIP_OK;
+    if (!x) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "rope_apply: NULL buffer");
+    if (position_offset + seq_len > (size_t)INT32_MAX)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "rope_apply: position too large");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    std::vector<int32_t> pos(seq_len);
+    for (size_t i = 0; i < seq_len; ++i) pos[i] = (int32_t)(position_offset + i);
+    VK_TRY(c->rope_pos.ensure(seq_len * sizeof(int32_t)), "hipMalloc");
+    VK_TRY(hipMemcpyAsync(c->rope_pos.p, pos.data(), seq_len * sizeof(int32_t), hipMemcpyHostToDevice, c->stream),
+           "hipMemcpyAsync(H2D)");
+    if ((st = stage_in(c, c->in0, x, x_len))) return st;
+    if ((st = vokra_hip_rope_f32_dev(c, (float*)c->in0.p, seq_len, n_head, head_dim, rope_base,
+                                     (const int32_t*)c->rope_pos.p)))
+        return st;
+    return stage_out(c, x, c->in0.p, x_len);
+}
+
+int vokra_hip_swiglu_f32_dev(vokra_hip_ctx_t* c, const float* d_gate, const float* d_up, size_t n, float* d_out) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "swiglu: ctx is NULL");
+    if (n == 0) return VOKRA_HIP_OK;
+    if (!d_gate || !d_up || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "swiglu: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_swiglu_f32(c->stream, d_gate, d_up, d_out, n), "launch(vk_swiglu_f32)");
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_swiglu_f32(vokra_hip_ctx_t* c, const float* gate, size_t gate_len, const float* up, size_t up_len,
+                         float* out) {
+    if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "swiglu: ctx is NULL");
+    if (gate_len != up_len)  // hadamard_inplace's rejection (text_decoder.rs:836-843)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "hadamard_inplace: length mismatch %zu != %zu", gate_len, up_len);
+    if (gate_len == 0) return VOKRA_HIP_OK;
+    if (!gate || !up || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "swiglu: NULL buffer");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    int st = stage_in(c, c->in0, gate, gate_len);
+    if (!st) st = stage_in(c, c->in1, up, up_len);
+    if (st) return st;
+    VK_TRY(c->out0.ensure(gate_len * sizeof(float)), "hipMalloc");
+    if ((st = vokra_hip_swiglu_f32_dev(c, (const float*)c->in0.p, (const float*)c->in1.p, gate_len, (float*)c->out0.p)))
+        return st;
+    return stage_out(c, out, c->out0.p, gate_len);
+}
+
 int vokra_hip_add_f32_dev(vokra_hip_ctx_t* c, const float* d_a, const float* d_b, float* d_out, size_t n) {
     if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "add: ctx is NULL");
     if (n == 0) return VOKRA_HIP_OK;
@@ -1374,7 +1486,8 @@ void vokra_hip_destroy(vokra_hip_ctx_t* c) {
     (void)hipStreamSynchronize(c->stream);
     for (DevBuf* b : {&c->in0, &c->in1, &c->in2, &c->out0, &c->act.frag, &c->act.scale, &c->act.gsum, &c->at_qh,
                       &c->at_ql, &c->at_kh, &c->at_kl, &c->at_vh, &c->at_vl, &c->fe_win, &c->fe_basis, &c->fe_fb,
-                      &c->fe_frames, &c->fe_spec, &c->fe_pow, &c->fe_mel, &c->fe_part, &c->cv_col, &c->lg_part})
+                      &c->fe_frames, &c->fe_spec, &c->fe_pow, &c->fe_mel, &c->fe_part, &c->cv_col, &c->lg_part,
+                      &c->rope_theta, &c->rope_pos})
         b->release();
     (void)hipStreamDestroy(c->stream);
     delete c;

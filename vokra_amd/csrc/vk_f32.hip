@@ -317,12 +317,19 @@ __global__ void vk_add_f32(const float* a, const float* b, float* out, size_t n)
         out[i] = a[i] + b[i];
 }
 
-// h[i] = tok_emb[tokens[i]] + pos_emb[positions[i]] (whisper/decoder.rs:420-432).
+// h[i] = tok_emb[tokens[i]] + pos_emb[positions[i]] (whisper/decoder.rs:420-432);
+// with pos_emb NULL, the embedding row alone (rotary models add no position
+// vector, voxtral/text_decoder.rs:1080-1095).
 __global__ void vk_embed_f32(const float* __restrict__ tok_emb, const float* __restrict__ pos_emb,
                              const int* __restrict__ tokens, const int* __restrict__ positions, int vocab,
                              int n_pos, int d, float* __restrict__ out) {
     const int i = blockIdx.x;
-    const int t = min(max(tokens[i], 0), vocab - 1), p = min(max(positions[i], 0), n_pos - 1);
+    const int t = min(max(tokens[i], 0), vocab - 1);
+    if (!pos_emb) {
+        for (int c = threadIdx.x; c < d; c += blockDim.x) out[(size_t)i * d + c] = tok_emb[(size_t)t * d + c];
+        return;
+    }
+    const int p = min(max(positions[i], 0), n_pos - 1);
     for (int c = threadIdx.x; c < d; c += blockDim.x)
         out[(size_t)i * d + c] = tok_emb[(size_t)t * d + c] + pos_emb[(size_t)p * d + c];
 }

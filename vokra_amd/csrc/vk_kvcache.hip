@@ -269,6 +269,46 @@ __global__ void vk_kv_write(KvDev c, int layer, int n, const int* __restrict__ s
     }
 }
 
+// Packs item i's K and V rows (width floats each) at time times[i] into the
+// page that an earlier vk_kv_alloc_layers launch gave (layer, times[i] /
+// block_size); items whose entry is empty (allocation failed) or out of range
+// are skipped. Same packing as vk_kv_write. One thread per (item, element).
+__global__ void vk_kv_write_allocated(KvDev c, int layer, int n, const int* __restrict__ streams,
+                                      const int* __restrict__ times, const float* __restrict__ k,
+                                      const float* __restrict__ v) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int e = (int)(gid % (size_t)c.width);
+    const int item = (int)(gid / (size_t)c.width);
+    bool live = false;
+    int s = 0, t = 0, pid = -1;
+    if (item < n) {  // uniform over each 32-thread block group (width % 32 == 0)
+        s = streams[item];
+        t = times[item];
+        if (s >= 0 && s < c.n_stream && t >= 0 && t < c.max_time) {
+            pid = c.table[layer * c.ppl + t / c.bs];
+            live = pid >= 0;
+        }
+    }
+    float kv = 0.0f, vv = 0.0f;
+    if (live) {
+        kv = k[(size_t)item * c.width + e];
+        vv = v[(size_t)item * c.width + e];
+    }
+    int8_t qk, qv;
+    uint16_t dk = 0, dv = 0;
+    q8_0_pack_lane(kv, e & 31, &qk, &dk);
+    q8_0_pack_lane(vv, e & 31, &qv, &dv);
+    if (!live) return;
+    const size_t qo = kv_qoff(c, pid, t, s, e);
+    c.kq[qo] = qk;
+    c.vq[qo] = qv;
+    if ((e & 31) == 0) {
+        const size_t dof = kv_doff(c, pid, t, s, e);
+        c.kd[dof] = dk;
+        c.vd[dof] = dv;
+    }
+}
+
 // read_step (paged_quant.rs:448-480): dequantized K and V rows of (layer, t, s)
 // into out[0 .. width) and out[width .. 2 width); found[0] = 0 when the entry
 // has no page (the reference's None).
@@ -975,6 +1015,16 @@ hipError_t launch_kv_append(hipStream_t s, const KvView& v, int layer, int n, co
     if (threads == 0) return hipSuccess;
     hipLaunchKernelGGL(vk_kv_write, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, c, layer, n, streams,
                        times, k, vv);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_write_allocated(hipStream_t s, const KvView& v, int layer, int n, const int* streams,
+                                    const int* times, const float* k, const float* vv) {
+    const KvDev c = kv_view(v);
+    const size_t threads = (size_t)n * v.width;
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_kv_write_allocated, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, c, layer, n,
+                       streams, times, k, vv);
     return hipGetLastError();
 }
 

@@ -144,6 +144,16 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
 // and of the GQA decode kernel (vk_kvcache.hip) on the current device.
 hipError_t attn_range_take(hipStream_t s, unsigned* raised);
 hipError_t kv_range_take(hipStream_t s, unsigned* raised);
+// Packs rows into pages given by an earlier launch_kv_alloc_layers (items
+// whose page is missing are skipped).
+hipError_t launch_kv_write_allocated(hipStream_t s, const KvView& v, int layer, int n, const int* streams,
+                                    const int* times, const float* k, const float* vv);
+// RoPE in place over x [rows][n_head * hd]: row r at positions[r] (or
+// pos_offset + r when positions is NULL), theta [hd / 2] from the host.
+hipError_t launch_rope_rows(hipStream_t s, float* x, int rows, int n_head, int hd, const float* theta,
+                            const int* positions, int pos_offset);
+// out = silu(g) * u elementwise (out may alias g).
+hipError_t launch_swiglu_f32(hipStream_t s, const float* g, const float* u, float* out, size_t n);
 hipError_t launch_kv_alloc_layers(hipStream_t s, const KvView& v, int layer0, int n_layers, int n, int q_base,
                                   const int* streams, const int* times);
 }  // namespace vk
@@ -217,6 +227,10 @@ int paged_attn_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t
 //   step lies inside d_lens, and a cache with room for every append.
 int kv_alloc_layers(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t first_layer, size_t layer0, size_t n_layers, size_t n,
                     const int* d_streams, const int* d_times);
+//   kv_alloc_layers + kv_write_allocated (per layer) = per layer
+//   vokra_hip_kv_append_dev of the items' rows at d_times.
+int kv_write_allocated(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
+                       const int* d_times, const float* d_k, const float* d_v);
 int paged_attn_append_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                                const int* d_times, const float* d_k, const float* d_v, const int* d_lens,
                                size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,

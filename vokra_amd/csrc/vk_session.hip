@@ -682,3 +682,339 @@ int vokra_hip_decoder_step(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t n,
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Speech-LLM text decoder (crates/vokra-models/src/voxtral/text_decoder.rs:
+// 1147-1420 per stream, as driven by TextDecoderSession::step_into,
+// text_decoder_session.rs:207-240), batched over streams: RMSNorm, q / k / v,
+// RoPE at each stream's position, the paged Q8_0 cache, grouped-query decode
+// attention, o-proj + residual, RMSNorm, SwiGLU FFN + residual, final
+// RMSNorm, LM head and greedy argmax, all device-resident.
+
+namespace vk {
+
+// lens[i] = positions[i] + 1: the keys 0..t a step attends after its append.
+__global__ void vk_lens_of(const int* __restrict__ positions, int n, int* __restrict__ lens) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) lens[i] = positions[i] + 1;
+}
+
+}  // namespace vk
+
+namespace {
+
+struct TextLayer {
+    DBuf attn_g, ffn_g;
+    QLin q, k, v, o, gate, up, down;
+};
+
+}  // namespace
+
+struct vokra_hip_text_decoder {
+    vokra_hip_ctx_t* ctx = nullptr;
+    int wdtype = 0;
+    size_t n_layer = 0, d = 0, hq = 0, hkv = 0, hd = 0, ff = 0, vocab = 0, n_ctx = 0, n_stream = 0;
+    float rope_base = 0.0f, eps = 0.0f, scale = 0.0f;
+    std::vector<TextLayer> layers;
+    DBuf tok_emb, final_g, theta, h, x, q, k, v, attn, g, u, logits, lpart, lens, next, stage;
+    QLin lm_head;
+    bool tied = true;
+    vokra_hip_kv_t* kv = nullptr;
+    vokra_hip_qact_t *qa_d = nullptr, *qa_q = nullptr, *qa_f = nullptr;
+    std::vector<int32_t> position;  // host clock per stream (TextDecoderSession::position)
+    void release() {
+        for (auto& L : layers) {
+            for (DBuf* b : {&L.attn_g, &L.ffn_g}) b->release(ctx);
+            for (QLin* w : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down}) w->release(ctx);
+        }
+        for (DBuf* b : {&tok_emb, &final_g, &theta, &h, &x, &q, &k, &v, &attn, &g, &u, &logits, &lpart, &lens, &next,
+                        &stage})
+            b->release(ctx);
+        lm_head.release(ctx);
+        vokra_hip_kv_destroy(kv);
+        kv = nullptr;
+        for (vokra_hip_qact_t** qa : {&qa_d, &qa_q, &qa_f}) {
+            vokra_hip_qact_free(*qa);
+            *qa = nullptr;
+        }
+    }
+};
+
+namespace {
+
+int td_setup(vokra_hip_text_decoder* m, const vokra_hip_text_decoder_layer_t* layers, const float* tok_emb,
+             const float* final_g, const uint8_t* lm_head, size_t block_size) {
+    vokra_hip_ctx_t* c = m->ctx;
+    const size_t d = m->d, qh = m->hq * m->hd, kvh = m->hkv * m->hd, ff = m->ff;
+    m->layers.resize(m->n_layer);
+    for (size_t l = 0; l < m->n_layer; ++l) {
+        const vokra_hip_text_decoder_layer_t& s = layers[l];
+        TextLayer& L = m->layers[l];
+        SS_TRY(upload_vec(c, L.attn_g, s.attn_norm_gamma, d, "text_decoder: attn_norm_gamma is NULL"));
+        SS_TRY(upload_vec(c, L.ffn_g, s.ffn_norm_gamma, d, "text_decoder: ffn_norm_gamma is NULL"));
+        SS_TRY(L.q.make(c, m->wdtype, qh, d, s.wq, nullptr));
+        SS_TRY(L.k.make(c, m->wdtype, kvh, d, s.wk, nullptr));
+        SS_TRY(L.v.make(c, m->wdtype, kvh, d, s.wv, nullptr));
+        SS_TRY(L.o.make(c, m->wdtype, d, qh, s.wo, nullptr));
+        SS_TRY(L.gate.make(c, m->wdtype, ff, d, s.w_gate, nullptr));
+        SS_TRY(L.up.make(c, m->wdtype, ff, d, s.w_up, nullptr));
+        SS_TRY(L.down.make(c, m->wdtype, d, ff, s.w_down, nullptr));
+    }
+    SS_TRY(upload_vec(c, m->tok_emb, tok_emb, m->vocab * d, "text_decoder: token_emb is NULL"));
+    SS_TRY(upload_vec(c, m->final_g, final_g, d, "text_decoder: final_norm_gamma is NULL"));
+    m->tied = lm_head == nullptr;
+    if (!m->tied) SS_TRY(m->lm_head.make(c, m->wdtype, m->vocab, d, lm_head, nullptr));
+    // the rotary frequencies, evaluated as the reference does per element:
+    // rope_base.powf(-2.0 * (j as f32) / (head_dim as f32))
+    std::vector<float> th(m->hd / 2);
+    for (size_t j = 0; j < th.size(); ++j) th[j] = powf(m->rope_base, -2.0f * (float)j / (float)m->hd);
+    SS_TRY(m->theta.upload(c, th.data(), th.size() * sizeof(float)));
+    SS_TRY(vokra_hip_kv_create(c, m->n_layer, m->hkv, m->hd, m->n_stream, m->n_ctx, block_size, VOKRA_HIP_KV_Q8_0,
+                               &m->kv));
+    const size_t rows = m->n_stream;
+    SS_TRY(m->h.alloc(c, rows * d * sizeof(float)));
+    SS_TRY(m->x.alloc(c, rows * d * sizeof(float)));
+    SS_TRY(m->q.alloc(c, rows * qh * sizeof(float)));
+    SS_TRY(m->attn.alloc(c, rows * qh * sizeof(float)));
+    SS_TRY(m->k.alloc(c, rows * kvh * sizeof(float)));
+    SS_TRY(m->v.alloc(c, rows * kvh * sizeof(float)));
+    SS_TRY(m->g.alloc(c, rows * ff * sizeof(float)));
+    SS_TRY(m->u.alloc(c, rows * ff * sizeof(float)));
+    SS_TRY(m->logits.alloc(c, rows * m->vocab * sizeof(float)));
+    SS_TRY(m->lpart.alloc(c, rows * (size_t)vk::logits_n_vt((int)m->vocab) * sizeof(float2)));
+    SS_TRY(m->lens.alloc(c, rows * sizeof(int)));
+    SS_TRY(m->next.alloc(c, rows * sizeof(int)));
+    SS_TRY(m->stage.alloc(c, 3 * rows * sizeof(int)));
+    SS_TRY(vokra_hip_qact_create(c, rows, d, &m->qa_d));
+    SS_TRY(vokra_hip_qact_create(c, rows, qh, &m->qa_q));
+    SS_TRY(vokra_hip_qact_create(c, rows, ff, &m->qa_f));
+    m->position.assign(m->n_stream, 0);
+    return VOKRA_HIP_OK;
+}
+
+// RMSNorm of rows n of in into scratch, then the activation pass into qa.
+int td_rms_quantize(vokra_hip_text_decoder* m, vokra_hip_qact_t* qa, size_t n, const float* in, const float* gamma) {
+    hipStream_t s = vk::ctx_stream(m->ctx);
+    SS_HIP(vk::launch_rms_norm_f32(s, in, m->x.f(), (int)n, (int)m->d, gamma, m->eps), "launch(vk_rms_norm_f32)");
+    return vokra_hip_qact_quantize_dev(m->ctx, qa, n, m->x.f(), act_of(m->wdtype));
+}
+
+int td_step(vokra_hip_text_decoder* m, size_t n, const int* d_streams, const int* d_tokens, const int* d_positions,
+            int* d_next, float* d_logits) {
+    vokra_hip_ctx_t* c = m->ctx;
+    hipStream_t s = vk::ctx_stream(c);
+    const int act = act_of(m->wdtype);
+    const size_t d = m->d, ff = m->ff;
+    SS_HIP(vk::launch_embed_f32(s, m->tok_emb.f(), nullptr, d_tokens, nullptr, (int)m->vocab, 1, (int)d, (int)n,
+                                m->h.f()),
+           "launch(vk_embed_f32)");
+    hipLaunchKernelGGL(vk::vk_lens_of, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, s, d_positions, (int)n,
+                       m->lens.i());
+    SS_HIP(hipGetLastError(), "launch(vk_lens_of)");
+    // this step's cache pages for every layer, in layer order
+    for (size_t l0 = 0, per = std::max<size_t>(1, 4096 / n); l0 < m->n_layer; l0 += per)
+        SS_TRY(vk::kv_alloc_layers(c, m->kv, 0, l0, std::min(per, m->n_layer - l0), n, d_streams, d_positions));
+    const VkEpi add_h = {m->h.f(), 0};
+    for (size_t l = 0; l < m->n_layer; ++l) {
+        const TextLayer& L = m->layers[l];
+        // pre-norm self-attention (text_decoder.rs:1212-1351)
+        SS_TRY(td_rms_quantize(m, m->qa_d, n, m->h.f(), L.attn_g.f()));
+        SS_TRY(L.q.run(c, m->qa_d, m->q.f()));
+        SS_TRY(L.k.run(c, m->qa_d, m->k.f()));
+        SS_TRY(L.v.run(c, m->qa_d, m->v.f()));
+        SS_HIP(vk::launch_rope_rows(s, m->q.f(), (int)n, (int)m->hq, (int)m->hd, m->theta.f(), d_positions, 0),
+               "launch(vk_rope_rows q)");
+        SS_HIP(vk::launch_rope_rows(s, m->k.f(), (int)n, (int)m->hkv, (int)m->hd, m->theta.f(), d_positions, 0),
+               "launch(vk_rope_rows k)");
+        SS_TRY(vk::kv_write_allocated(c, m->kv, l, n, d_streams, d_positions, m->k.f(), m->v.f()));
+        SS_TRY(vk::paged_attn_quantize(c, m->kv, l, n, d_streams, m->lens.i(), m->n_ctx, m->hq, m->q.f(), m->scale,
+                                       m->attn.f(), m->qa_q, act));
+        SS_TRY(L.o.run(c, m->qa_q, m->h.f(), add_h));
+        // pre-norm SwiGLU FFN (text_decoder.rs:1385-1418)
+        SS_TRY(td_rms_quantize(m, m->qa_d, n, m->h.f(), L.ffn_g.f()));
+        SS_TRY(L.gate.run(c, m->qa_d, m->g.f()));
+        SS_TRY(L.up.run(c, m->qa_d, m->u.f()));
+        SS_HIP(vk::launch_swiglu_f32(s, m->g.f(), m->u.f(), m->g.f(), n * ff), "launch(vk_swiglu_f32)");
+        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_f, n, m->g.f(), act));
+        SS_TRY(L.down.run(c, m->qa_f, m->h.f(), add_h));
+    }
+    // final RMSNorm, LM head, greedy argmax (text_decoder.rs:1423-1451,
+    // text_decoder_session.rs argmax)
+    SS_HIP(vk::launch_rms_norm_f32(s, m->h.f(), m->x.f(), (int)n, (int)d, m->final_g.f(), m->eps),
+           "launch(vk_rms_norm_f32 final)");
+    if (!m->tied) {
+        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->x.f(), act));
+        float* lg = d_logits ? d_logits : m->logits.f();
+        SS_TRY(m->lm_head.run(c, m->qa_d, lg));
+        return vokra_hip_argmax_f32_dev(c, lg, n, m->vocab, d_next);
+    }
+    if (d % vk::logits_d_multiple() == 0) {
+        SS_HIP(vk::launch_logits_argmax(s, m->x.f(), m->tok_emb.f(), d_logits, (float2*)m->lpart.p, d_next, (int)n,
+                                        (int)m->vocab, (int)d),
+               "launch(vk_logits_argmax)");
+        return VOKRA_HIP_OK;
+    }
+    float* lg = d_logits ? d_logits : m->logits.f();
+    SS_TRY(vokra_hip_gemm_f32_dev(c, n, m->vocab, d, m->x.f(), m->tok_emb.f(), 1, nullptr, lg));
+    return vokra_hip_argmax_f32_dev(c, lg, n, m->vocab, d_next);
+}
+
+}  // namespace
+
+extern "C" {
+
+int vokra_hip_text_decoder_create(vokra_hip_ctx_t* c, int wdtype, size_t n_layer, size_t d_model, size_t n_head_q,
+                                  size_t n_head_kv, size_t head_dim, size_t ffn_dim, size_t vocab, size_t n_ctx,
+                                  size_t n_stream, size_t block_size, float rope_base, float rms_norm_eps,
+                                  const vokra_hip_text_decoder_layer_t* layers, const float* token_emb,
+                                  const float* final_norm_gamma, const uint8_t* lm_head,
+                                  vokra_hip_text_decoder_t** out) {
+    if (!c || !out || !layers) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_create: NULL argument");
+    *out = nullptr;
+    // TextDecoderSession::new's checks (text_decoder_session.rs:90-140)
+    if (!n_layer || !d_model || !vocab || !n_head_q || !n_head_kv || !head_dim)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_MODEL_LOAD,
+                            "voxtral::TextDecoderSession: config carries 0-sentinel (n_layer, d, vocab, heads, head_dim)");
+    if (n_head_q % n_head_kv != 0)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_MODEL_LOAD,
+                            "voxtral::TextDecoderSession: n_head_q (%zu) must be divisible by n_head_kv (%zu) - GQA",
+                            n_head_q, n_head_kv);
+    const size_t grp = n_head_q / n_head_kv;
+    if (head_dim != 64 && head_dim != 128)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "text_decoder_create: head_dim must be 64 or 128");
+    if (grp != 1 && grp != 2 && grp != 4 && grp != 8)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP,
+                            "text_decoder_create: query heads per kv head must be 1, 2, 4 or 8");
+    if (wire_bytes(wdtype, 1, 256) == 0)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "text_decoder_create: unknown weight dtype");
+    const size_t qb = wdtype == VOKRA_HIP_W_Q4_K ? 256 : 32;
+    if (d_model % qb || ffn_dim % qb || !ffn_dim || (n_head_q * head_dim) % qb || (n_head_kv * head_dim) % 32)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                            "text_decoder_create: d_model, ffn_dim and n_head_q * head_dim must be multiples of the "
+                            "quant block");
+    if (!n_ctx || !n_stream || n_stream > 1024 || vocab > 0x7fffffff || !(rope_base > 0.0f) || !(rms_norm_eps >= 0.0f))
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                            "text_decoder_create: n_ctx > 0, n_stream in 1..1024, rope_base > 0, rms_norm_eps >= 0");
+    auto* m = new vokra_hip_text_decoder();
+    m->ctx = c;
+    m->wdtype = wdtype;
+    m->n_layer = n_layer;
+    m->d = d_model;
+    m->hq = n_head_q;
+    m->hkv = n_head_kv;
+    m->hd = head_dim;
+    m->ff = ffn_dim;
+    m->vocab = vocab;
+    m->n_ctx = n_ctx;
+    m->n_stream = n_stream;
+    m->rope_base = rope_base;
+    m->eps = rms_norm_eps;
+    m->scale = 1.0f / sqrtf((float)head_dim);  // 1.0f32 / (head_dim as f32).sqrt(), text_decoder.rs:1176
+    int st = td_setup(m, layers, token_emb, final_norm_gamma, lm_head, block_size);
+    if (st) {
+        m->release();
+        delete m;
+        return st;
+    }
+    *out = m;
+    return VOKRA_HIP_OK;
+}
+
+void vokra_hip_text_decoder_destroy(vokra_hip_text_decoder_t* m) {
+    if (!m) return;
+    m->release();
+    delete m;
+}
+
+int vokra_hip_text_decoder_reset(vokra_hip_ctx_t* c, vokra_hip_text_decoder_t* m) {
+    if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_reset: bad argument");
+    SS_TRY(vokra_hip_kv_reset(c, m->kv));
+    std::fill(m->position.begin(), m->position.end(), 0);
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_text_decoder_position(vokra_hip_ctx_t* c, vokra_hip_text_decoder_t* m, size_t stream, size_t* position) {
+    if (!c || !m || m->ctx != c || !position || stream >= m->n_stream)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_position: bad argument");
+    *position = (size_t)m->position[stream];
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_text_decoder_kv_restore(vokra_hip_ctx_t* c, vokra_hip_text_decoder_t* m, size_t stream, size_t n_pos,
+                                      const float* k_rows, const float* v_rows) {
+    if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_kv_restore: bad argument");
+    if (stream >= m->n_stream) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_kv_restore: stream out of range");
+    if (n_pos > m->n_ctx)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_kv_restore: position %zu > n_ctx %zu", n_pos,
+                            m->n_ctx);
+    if (n_pos && (!k_rows || !v_rows)) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_kv_restore: NULL rows");
+    const size_t w = m->hkv * m->hd;
+    std::vector<int32_t> st(1024, (int32_t)stream), tt(1024);
+    for (size_t l = 0; l < m->n_layer; ++l)
+        for (size_t t0 = 0; t0 < n_pos; t0 += 1024) {
+            const size_t cnt = std::min<size_t>(1024, n_pos - t0);
+            for (size_t i = 0; i < cnt; ++i) tt[i] = (int32_t)(t0 + i);
+            const size_t off = (l * n_pos + t0) * w;
+            SS_TRY(vokra_hip_kv_append(c, m->kv, l, cnt, st.data(), tt.data(), k_rows + off, v_rows + off));
+        }
+    m->position[stream] = (int32_t)n_pos;
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_text_decoder_step_dev(vokra_hip_ctx_t* c, vokra_hip_text_decoder_t* m, size_t n, const int32_t* d_streams,
+                                    const int32_t* d_tokens, const int32_t* d_positions, int32_t* d_next,
+                                    float* d_logits) {
+    if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_step: bad context");
+    if (n == 0) return VOKRA_HIP_OK;
+    if (n > m->n_stream) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_step: more items than streams");
+    if (!d_streams || !d_tokens || !d_positions || !d_next)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_step: NULL buffer");
+    return td_step(m, n, d_streams, d_tokens, d_positions, d_next, d_logits);
+}
+
+int vokra_hip_text_decoder_step(vokra_hip_ctx_t* c, vokra_hip_text_decoder_t* m, size_t n, const int32_t* streams,
+                                const int32_t* tokens, int32_t* next_tokens, float* logits) {
+    if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_step: bad context");
+    if (n == 0) return VOKRA_HIP_OK;
+    if (n > m->n_stream) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_step: more items than streams");
+    if (!streams || !tokens || !next_tokens)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_step: NULL buffer");
+    // forward_step's checks (text_decoder.rs:1007-1045), per stream
+    std::vector<char> seen(m->n_stream, 0);
+    std::vector<int32_t> items(3 * n);
+    for (size_t i = 0; i < n; ++i) {
+        if (streams[i] < 0 || (size_t)streams[i] >= m->n_stream || seen[streams[i]])
+            return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                                "text_decoder_step: streams must be distinct and < n_stream");
+        seen[streams[i]] = 1;
+        if (tokens[i] < 0 || (size_t)tokens[i] >= m->vocab)
+            return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                                "voxtral text_decoder.forward_step: token id %d >= vocab %zu", tokens[i], m->vocab);
+        const int32_t p = m->position[streams[i]];
+        if ((size_t)p + 1 > m->n_ctx)
+            return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "voxtral text_decoder.forward_step: position %d > n_ctx %zu",
+                                p + 1, m->n_ctx);
+        items[i] = streams[i];
+        items[n + i] = tokens[i];
+        items[2 * n + i] = p;
+    }
+    int* dv = m->stage.i();
+    SS_TRY(vokra_hip_memcpy_htod(c, dv, items.data(), 3 * n * 4));
+    SS_TRY(td_step(m, n, dv, dv + n, dv + 2 * n, m->next.i(), logits ? m->logits.f() : nullptr));
+    size_t appended = 0;
+    SS_TRY(vokra_hip_kv_status(c, m->kv, &appended));
+    for (size_t i = 0; i < n; ++i) m->position[streams[i]] += 1;  // the rows are appended
+    SS_TRY(vokra_hip_memcpy_dtoh(c, next_tokens, m->next.p, n * 4));
+    if (logits) SS_TRY(vokra_hip_memcpy_dtoh(c, logits, m->logits.p, n * m->vocab * sizeof(float)));
+    return vk::range_check(c);
+}
+
+int vokra_hip_text_decoder_status(vokra_hip_ctx_t* c, vokra_hip_text_decoder_t* m, size_t* n_appended) {
+    if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_status: bad argument");
+    size_t a = 0;
+    const int st = vokra_hip_kv_status(c, m->kv, &a);
+    if (n_appended) *n_appended = a;
+    return st ? st : vk::range_check(c);
+}
+
+}  // extern "C"

@@ -104,6 +104,12 @@ class DecoderLayer(C.Structure):
                 ("w1", _U8), ("w2", _U8), ("b1", _F), ("b2", _F)]
 
 
+class TextDecoderLayer(C.Structure):
+    """vokra_hip_text_decoder_layer_t"""
+    _fields_ = [("attn_norm_gamma", _F), ("wq", _U8), ("wk", _U8), ("wv", _U8), ("wo", _U8),
+                ("ffn_norm_gamma", _F), ("w_gate", _U8), ("w_up", _U8), ("w_down", _U8)]
+
+
 def _ctx_alive(obj):
     """True while the context an object was made on is open: handles are only
     freed through a live context (after close, the process exit reclaims them)."""
@@ -238,6 +244,22 @@ def _declare(L):
     L.vokra_hip_decoder_step_dev.argtypes = [P, P, sz, P, P, P, P, P]
     L.vokra_hip_decoder_status.argtypes = [P, P, C.POINTER(sz)]
     L.vokra_hip_attn_f32.argtypes = [P, sz, sz, sz, sz, sz, sz, f32p, f32p, f32p, C.c_float, C.c_int, sz, f32p]
+    u8p = C.POINTER(C.c_uint8)
+    L.vokra_hip_rope_f32.argtypes = [P, f32p, sz, sz, sz, sz, C.c_float, sz]
+    L.vokra_hip_rope_f32_dev.argtypes = [P, P, sz, sz, sz, C.c_float, P]
+    L.vokra_hip_swiglu_f32.argtypes = [P, f32p, sz, f32p, sz, f32p]
+    L.vokra_hip_swiglu_f32_dev.argtypes = [P, P, P, sz, P]
+    L.vokra_hip_text_decoder_create.argtypes = [P, C.c_int, sz, sz, sz, sz, sz, sz, sz, sz, sz, sz, C.c_float,
+                                                C.c_float, C.POINTER(TextDecoderLayer), f32p, f32p, u8p,
+                                                C.POINTER(P)]
+    L.vokra_hip_text_decoder_destroy.argtypes = [P]
+    L.vokra_hip_text_decoder_destroy.restype = None
+    L.vokra_hip_text_decoder_reset.argtypes = [P, P]
+    L.vokra_hip_text_decoder_position.argtypes = [P, P, sz, C.POINTER(sz)]
+    L.vokra_hip_text_decoder_kv_restore.argtypes = [P, P, sz, sz, f32p, f32p]
+    L.vokra_hip_text_decoder_step.argtypes = [P, P, sz, i32p, i32p, i32p, f32p]
+    L.vokra_hip_text_decoder_step_dev.argtypes = [P, P, sz, P, P, P, P, P]
+    L.vokra_hip_text_decoder_status.argtypes = [P, P, C.POINTER(sz)]
     L.vokra_hip_attn_f32_dev.argtypes = [P, sz, sz, sz, sz, sz, sz, P, P, P, C.c_float, C.c_int, sz, P]
 
 
@@ -699,6 +721,73 @@ class Decoder:
             pass
 
 
+class TextDecoder:
+    """Batched device-resident speech-LLM text decoder
+    (voxtral::TextDecoderSession, text_decoder_session.rs:54-405, with a batch
+    axis and the paged Q8_0 cache)."""
+
+    def __init__(self, ctx, wdtype, d_model, n_head_q, n_head_kv, head_dim, ffn_dim, vocab, n_ctx, n_stream,
+                 layers, token_emb, final_norm_gamma, lm_head=None, rope_base=1e6, rms_norm_eps=1e-5,
+                 block_size=16):
+        self._ctx, self.vocab, self.n_layer = ctx, vocab, len(layers)
+        self.kv_hidden = n_head_kv * head_dim
+        keep = []
+        arr = (TextDecoderLayer * len(layers))(*[_fill_struct(TextDecoderLayer, L, keep) for L in layers])
+        te, fg = _f32(token_emb), _f32(final_norm_gamma)
+        lm = None if lm_head is None else _u8(lm_head)
+        h = C.c_void_p()
+        _check(lib().vokra_hip_text_decoder_create(ctx._h, int(wdtype), len(layers), d_model, n_head_q, n_head_kv,
+                                                   head_dim, ffn_dim, vocab, n_ctx, n_stream, block_size,
+                                                   C.c_float(rope_base), C.c_float(rms_norm_eps), arr,
+                                                   _ptr(te, C.c_float), _ptr(fg, C.c_float), _ptr(lm, C.c_uint8),
+                                                   C.byref(h)))
+        self._h = h
+
+    def reset(self):
+        _check(lib().vokra_hip_text_decoder_reset(self._ctx._h, self._h))
+
+    def position(self, stream) -> int:
+        p = C.c_size_t(0)
+        _check(lib().vokra_hip_text_decoder_position(self._ctx._h, self._h, stream, C.byref(p)))
+        return p.value
+
+    def kv_restore(self, stream, k_rows, v_rows):
+        """k_rows / v_rows [n_layer, n_pos, kv_hidden] become the stream's history."""
+        k, v = _f32(k_rows), _f32(v_rows)
+        n_pos = k.size // (self.n_layer * self.kv_hidden) if k.size else 0
+        if k.size != self.n_layer * n_pos * self.kv_hidden or v.size != k.size:
+            raise InvalidArgument("kv_restore: rows must be [n_layer, n_pos, kv_hidden]")
+        _check(lib().vokra_hip_text_decoder_kv_restore(self._ctx._h, self._h, stream, n_pos, _ptr(k, C.c_float),
+                                                       _ptr(v, C.c_float)))
+
+    def step(self, streams, tokens, want_logits=False):
+        st = np.ascontiguousarray(streams, np.int32)
+        tk = np.ascontiguousarray(tokens, np.int32)
+        nxt = np.zeros(max(st.size, 1), np.int32)
+        lg = np.zeros((st.size, self.vocab), np.float32) if want_logits else None
+        _check(lib().vokra_hip_text_decoder_step(self._ctx._h, self._h, st.size, _ptr(st, C.c_int32),
+                                                 _ptr(tk, C.c_int32), _ptr(nxt, C.c_int32), _ptr(lg, C.c_float)))
+        return (nxt[:st.size], lg) if want_logits else nxt[:st.size]
+
+    def step_dev(self, n, d_streams, d_tokens, d_positions, d_next, d_logits=None):
+        _check(lib().vokra_hip_text_decoder_step_dev(self._ctx._h, self._h, n, d_streams.ptr, d_tokens.ptr,
+                                                     d_positions.ptr, d_next.ptr,
+                                                     None if d_logits is None else d_logits.ptr))
+
+    def status(self) -> int:
+        n = C.c_size_t(0)
+        _check(lib().vokra_hip_text_decoder_status(self._ctx._h, self._h, C.byref(n)))
+        return n.value
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None) and self._h.value and _ctx_alive(self):
+                lib().vokra_hip_text_decoder_destroy(self._h)
+                self._h = C.c_void_p()
+        except Exception:
+            pass
+
+
 class HipContext:
     """One gfx950 device + stream (mirror of CudaContext::new, context.rs:1167)."""
 
@@ -858,6 +947,25 @@ class HipContext:
         _check(lib().vokra_hip_rms_norm_f32(self._h, _ptr(xv, C.c_float), xv.size, _ptr(out, C.c_float), xv.size,
                                             rows, cols, _ptr(g, C.c_float), g.size, C.c_float(eps)))
         return out[:xv.size].reshape(rows, cols)
+
+    def rope_f32(self, x, seq_len, n_head, head_dim, rope_base, position_offset=0):
+        """rope_apply on every head of x [seq_len, n_head*head_dim]; returns the rotated copy."""
+        xv = _f32(x).copy()
+        _check(lib().vokra_hip_rope_f32(self._h, _ptr(xv, C.c_float), xv.size, seq_len, n_head, head_dim,
+                                        C.c_float(rope_base), position_offset))
+        return xv
+
+    def rope_f32_dev(self, d_x, rows, n_head, head_dim, rope_base, d_positions):
+        _check(lib().vokra_hip_rope_f32_dev(self._h, d_x.ptr, rows, n_head, head_dim, C.c_float(rope_base),
+                                            d_positions.ptr))
+
+    def swiglu_f32(self, gate, up):
+        """silu(gate) * up (silu_inplace then hadamard_inplace)."""
+        g, u = _f32(gate), _f32(up)
+        out = np.zeros_like(g)
+        _check(lib().vokra_hip_swiglu_f32(self._h, _ptr(g, C.c_float), g.size, _ptr(u, C.c_float), u.size,
+                                          _ptr(out, C.c_float)))
+        return out
 
     def gelu_f32(self, x):
         xv = _f32(x).reshape(-1)
