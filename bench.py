@@ -414,6 +414,70 @@ def bench_decoder(ctx, hip, n_stream=64, n_layer=32, d=1280, H=20, ff=5120, V=51
             "gbs": round(total / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(total / (ms * 1e-3) / 1e9 / PEAK["hbm_gbs"], 4)}
 
 
+def q4k_scaled_weight(rng, n, k, d_hi=0x10, dmin_hi=0x0C):
+    """Random Q4_K payload (the reference's random_blocks pattern) with the
+    f16 d / dmin high bytes pinned to give weights of a few 0.01 (random-init
+    scale), so a 24-layer residual stream stays well inside f32 and fp16."""
+    b = rng.integers(0, 256, size=(n * (k // 256), 144), dtype=np.uint8)
+    b[:, 1] = d_hi
+    b[:, 3] = dmin_hi
+    return b.reshape(-1)
+
+
+def bench_text_decoder(ctx, hip, n_stream=32, n_layer=24, d=2048, hq=16, hkv=2, hd=128, ff=5632, V=32000,
+                       n_ctx=4096, len_lo=512, len_hi=4096, steps=10):
+    """Config 4: batched speech-LLM decode step, 32 streams whose histories
+    (rows restored into the paged Q8_0 cache, 16-token pages) are U(512..4096)
+    positions, 24 layers of Q4_K linears (d=2048, GQA 16/2 x 128, SwiGLU FFN
+    5632), Q4_K LM head over 32000 tokens, greedy argmax; seeded token IDs.
+    Timed: `steps` whole batched steps on device arrays."""
+    rng = np.random.default_rng(44)
+    layers = []
+    for _ in range(n_layer):
+        L = {"attn_norm_gamma": np.ones(d, np.float32), "ffn_norm_gamma": np.ones(d, np.float32)}
+        for name, n, k in (("wq", hq * hd, d), ("wk", hkv * hd, d), ("wv", hkv * hd, d), ("wo", d, hq * hd),
+                           ("w_gate", ff, d), ("w_up", ff, d), ("w_down", d, ff)):
+            L[name] = q4k_scaled_weight(rng, n, k)
+        layers.append(L)
+    tok = (0.02 * rng.standard_normal((V, d))).astype(np.float32)
+    head = q4k_scaled_weight(rng, V, d)
+    dec = hip.TextDecoder(ctx, 12, d, hq, hkv, hd, ff, V, n_ctx, n_stream, layers, tok, np.ones(d, np.float32),
+                          head, rope_base=1e6, rms_norm_eps=1e-5, block_size=16)
+    del layers
+    lens = rng.integers(len_lo, len_hi - steps, n_stream)
+    kk = rng.standard_normal((n_layer, int(lens.max()), hkv * hd), dtype=np.float32)
+    vv = rng.standard_normal((n_layer, int(lens.max()), hkv * hd), dtype=np.float32)
+    for s in range(n_stream):
+        dec.kv_restore(s, kk[:, :lens[s]], vv[:, :lens[s]])
+    del kk, vv
+    streams = hip.DeviceBuffer.from_array(ctx, np.arange(n_stream, dtype=np.int32))
+    toks = hip.DeviceBuffer.from_array(ctx, rng.integers(0, V, n_stream).astype(np.int32))
+    posb = [hip.DeviceBuffer.from_array(ctx, (lens + k).astype(np.int32)) for k in range(steps + 1)]
+    nxt = hip.DeviceBuffer(ctx, n_stream * 4)
+    dec.step_dev(n_stream, streams, toks, posb[0], nxt)   # warm-up
+    dec.status()
+    e0, e1 = hip.Event(ctx), hip.Event(ctx)
+    e0.record()
+    for k in range(1, steps + 1):
+        dec.step_dev(n_stream, streams, nxt, posb[k], toks)
+        nxt, toks = toks, nxt
+    e1.record()
+    dec.status()
+    ms = e0.elapsed_ms(e1) / steps
+    keys = int((lens + 1 + steps // 2).sum())
+    w_layer = sum(n * (k // 256) * 144 for (_, n, k) in Q4K_LAYER)
+    w_bytes = n_layer * w_layer + V * (d // 256) * 144
+    kv_bytes = keys * n_layer * 2 * (hkv * hd + hkv * hd // 32 * 2)
+    total = w_bytes + kv_bytes
+    del dec
+    ctx.synchronize()
+    return {"streams": n_stream, "layers": n_layer, "vocab": V, "context_range": [len_lo, len_hi],
+            "mean_context": round(float(lens.mean()), 1), "ms_per_step": round(ms, 3),
+            "tokens_per_s": round(n_stream / (ms * 1e-3), 1),
+            "bytes_per_step": {"weights_q4_k": w_bytes, "kv_q8_0": kv_bytes},
+            "gbs": round(total / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(total / (ms * 1e-3) / 1e9 / PEAK["hbm_gbs"], 4)}
+
+
 def bench_logits(ctx, hip, n=64, V=51866, d=1280, reps=20):
     """Config 3 tail: tied logits over the Whisper vocabulary (f32 embedding
     [V, d], 265.6 MB) for 64 streams and the greedy argmax, as one fused pass
@@ -503,7 +567,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default=None,
                     help="comma list of single legs to run, one JSON line each (for profiling): "
-                         "gemm, gemm_pow2, copy, gemv, q4k, sdpa, paged, encoder, decoder, frontend, logits")
+                         "gemm, gemm_pow2, copy, gemv, q4k, sdpa, paged, encoder, decoder, textdec, frontend, "
+                         "logits")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -525,6 +590,7 @@ def main():
                               bench_paged_attn(ctx, hip, 32, 2, 128, 16, 512, 4096, 4096)],
             "encoder": lambda: [bench_encoder(ctx, hip, 1), bench_encoder(ctx, hip, 16)],
             "decoder": lambda: bench_decoder(ctx, hip),
+            "textdec": lambda: bench_text_decoder(ctx, hip),
             "frontend": lambda: bench_frontend(ctx, hip),
             "logits": lambda: bench_logits(ctx, hip),
         }
@@ -547,6 +613,7 @@ def main():
     frontend_run = bench_frontend(ctx, hip)
     logits_run = bench_logits(ctx, hip)
     decoder_run = bench_decoder(ctx, hip)
+    textdec_run = bench_text_decoder(ctx, hip)
 
     M, N, K = main_run["M"], main_run["N"], main_run["K"]
     achieved = main_run["gemm_tops"]
@@ -583,6 +650,7 @@ def main():
             "frontend_config2_batch16": frontend_run,
             "logits_argmax_config3": logits_run,
             "decoder_step_config3": decoder_run,
+            "text_decoder_step_config4": textdec_run,
             "gemm_kernel_ms": round(main_run["gemm_ms"], 4),
             "eager_step_ms": round(main_run["eager_ms"], 4),
             "gemm_frac_of_bf16_mfma_peak": round(achieved / PEAK["bf16_tflops"], 4),

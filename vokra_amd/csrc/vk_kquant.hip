@@ -24,8 +24,6 @@ namespace kq {
 constexpr int QK = 256;      // elements per super-block
 constexpr int BB = 144;      // bytes per super-block
 constexpr int NG = 16;       // 16-element groups per super-block
-constexpr int CS = 4;        // super-blocks per LDS chunk of the matmul (one per wave)
-constexpr int CG = CS * NG;  // groups per chunk
 }  // namespace kq
 
 typedef short vk_s16x4 __attribute__((ext_vector_type(4)));
@@ -185,150 +183,151 @@ __device__ __forceinline__ vk_s16x4 q4k_operand(uint32_t w, int j0) {
 }
 
 // ---------------------------------------------------------------------------
-// Matmul, one workgroup per 16 x 16 output tile (16 activation rows, 16
-// weight rows), K in chunks of CS super-blocks (CG = 64 groups).
-// Phase 1: wave w takes super-block w of the chunk (16 groups): one
-//   16x16x16 MFMA per group with accumulator input -128 * gsum (removing the
-//   +128 of the bf16 nibble trick) gives isum exactly; isum goes to LDS.
-//   Right after, the wave issues the global loads of the next chunk into
-//   registers, so they are in flight during the combine.
-// Phase 2: thread (row, col) runs the reference combine over the chunk's
-//   groups in order; waves whose 4 rows are all padding skip it.
+// Matmul, one workgroup of 8 waves per 16 x 16 output tile (16 activation
+// rows, 16 weight rows), K in chunks of two super-blocks (32 groups).
+//
+// The reference combine is, per output, acc += s * (d_eff * isum - m_eff *
+// gsum) over the groups in order. Only the final add is a dependent chain;
+// the term t = s * (d_eff * isum - m_eff * gsum) (four roundings) depends on
+// one group alone. So:
+//   phase 1 (chunk c+1): wave w takes 4 groups of the chunk; per group one
+//     16x16x16 MFMA with accumulator input -128 * gsum (removing the +128 of
+//     the bf16 nibble trick) gives isum exactly for 4 outputs per lane, and
+//     the lane turns them into the 4 terms with the reference's roundings;
+//     the terms go to the LDS buffer of chunk c+1;
+//   phase 2 (chunk c): thread (row, col) of waves 0..3 adds the chunk's 32
+//     terms of its output to acc, in group order;
+//   one barrier per chunk: chunk c+1's terms are complete, chunk c's free.
+// Operands are loaded two chunks ahead into two register sets, each load a
+// wave-uniform base plus a 32-bit lane offset (a chunk past the end loads the
+// last super-block again, unused). Outputs are bit-identical to
+// kquant_gemm_i8: the same terms, added in the same order.
 namespace kq {
-struct Stage {
-    uint4 wv[2];     // nibble words of this wave's super-block
-    uint4 af[8];     // activation fragments of this wave's super-block
-    float sv[4], tv[4];  // chunk scales / group sums (4 per thread)
-    float2 dm[2];    // chunk (d_eff, m_eff) (2 per thread)
+constexpr int CHG = 32;  // groups per chunk (two super-blocks)
+constexpr int CHS = 2;   // super-blocks per chunk
+struct Pipe {
+    uint2 wv;            // nibble words of this wave's 4 groups
+    uint4 af[2];         // activation fragments of its 4 groups (2 pairs)
+    float s[4], a[4];    // s and gsum of this lane's row, per group
+    float4 dm[2][2];     // [sub-block][half]: (d_eff, m_eff) of cols rq + 2 half, +1
 };
 }  // namespace kq
 
 template <bool HAS_BIAS>
-__global__ __launch_bounds__(256) void vk_gemm_q4k(
+__global__ __launch_bounds__(512) void vk_gemm_q4k(
     const uint4* __restrict__ afrag, const float* __restrict__ ascale, const float* __restrict__ asum,
     const uint4* __restrict__ wq4, const float2* __restrict__ wdm, const float* __restrict__ bias, VkEpi epi,
     float* out, int m, int n, int nsb, int m_pad) {
     using namespace kq;
-    __shared__ __align__(16) float lds_p[CG][256];    // isum, [group][row * 16 + col]
-    // rows padded by one float4 against bank conflicts on the transposing stores
-    __shared__ float4 lds_sa[16][CG / 4 + 1];         // s,    [row][group]   (phase 2)
-    __shared__ float4 lds_as[16][CG / 4 + 1];         // gsum, [row][group]   (phase 2)
-    __shared__ float4 lds_dm[16][CG / 4 + 1];         // (d_eff, m_eff) x 2 sub-blocks, [col][pair]
+    __shared__ __align__(16) float lds_t[2][CHG][256];  // terms, [chunk parity][group][row * 16 + col]
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar load bases
     const int nt = blockIdx.x, mt = blockIdx.y;
-    const int rq = 4 * (lane >> 4);
-    const int row = tid >> 4, col = tid & 15;
-    float* sa_f = reinterpret_cast<float*>(lds_sa);
-    float* as_f = reinterpret_cast<float*>(lds_as);
-    float2* dm_f = reinterpret_cast<float2*>(lds_dm);
-    const bool rows_live = mt * 16 + 4 * wave < m;    // this wave's phase-2 rows
+    const int row_l = lane & 15, rq = 4 * (lane >> 4);  // MFMA lane: activation row, first weight column
+    const int q4 = wave & 3, sbw = wave >> 2;           // this wave's quarter of a super-block, and which one
+    const int n_chunk = (nsb + CHS - 1) / CHS;
+    const bool owner = wave < 4 && mt * 16 + 4 * wave < m;  // phase-2 thread with a live row
 
-    // Every load index is clamped into the chunk, so no load leaves its buffer.
-    auto load = [&](int sb0) -> Stage {
-        Stage st;
-        const int gsb = min(CS, nsb - sb0);
-        const int sb = sb0 + min(wave, gsb - 1);
+    // per-lane byte offsets (constant over the K loop)
+    const uint32_t vo_w = lane * 32 + 8 * q4;
+    const uint32_t vo_a = lane * 16;
+    const uint32_t vo_d = rq * 8;
+    uint32_t vo_s[4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) st.wv[h] = wq4[(((size_t)nt * nsb + sb) * 64 + lane) * 2 + h];
+    for (int i = 0; i < 4; ++i) vo_s[i] = (uint32_t)(i * m_pad + mt * 16 + row_l) * 4;
+
+    // chunk c's operands for this wave (super-block 2c + sbw, clamped into
+    // the tensor: a super-block past the end loads the last one, unused).
+    // Each load is a wave-uniform base plus a 32-bit per-lane offset.
+    auto load = [&](int c) -> Pipe {
+        Pipe p;
+        const int sb = min(c * CHS + sbw, nsb - 1);
+        const char* bw = reinterpret_cast<const char*>(wq4) + (size_t)((nt * nsb + sb) * 64) * 32;
+        const char* ba = reinterpret_cast<const char*>(afrag) + (size_t)(((mt * nsb + sb) * 8 + 2 * q4) * 64) * 16;
+        const size_t so_s = (size_t)(sb * NG + 4 * q4) * m_pad * 4;
+        const char* bs = reinterpret_cast<const char*>(ascale) + so_s;
+        const char* bg = reinterpret_cast<const char*>(asum) + so_s;
+        const char* bd = reinterpret_cast<const char*>(wdm) + (size_t)((nt * nsb + sb) * 8 + 2 * q4) * 128;
+        p.wv = *reinterpret_cast<const uint2*>(bw + vo_w);
 #pragma unroll
-        for (int p = 0; p < 8; ++p) st.af[p] = afrag[(((size_t)mt * nsb + sb) * 8 + p) * 64 + lane];
+        for (int h = 0; h < 2; ++h) p.af[h] = *reinterpret_cast<const uint4*>(ba + vo_a + h * 1024);
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            const int idx = min(tid + 256 * h, gsb * 256 - 1);
-            const size_t o = (size_t)(sb0 * NG + (idx >> 4)) * m_pad + mt * 16 + (idx & 15);
-            st.sv[h] = ascale[o];
-            st.tv[h] = asum[o];
+        for (int i = 0; i < 4; ++i) {
+            p.s[i] = *reinterpret_cast<const float*>(bs + vo_s[i]);
+            p.a[i] = *reinterpret_cast<const float*>(bg + vo_s[i]);
         }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int idx = min(tid + 256 * h, gsb * 128 - 1);
-            st.dm[h] = wdm[(((size_t)nt * nsb + sb0) * 8 + (idx >> 4)) * 16 + (idx & 15)];
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) p.dm[jj][h] = *reinterpret_cast<const float4*>(bd + vo_d + jj * 128 + h * 16);
+        return p;
+    };
+    // phase 1: the terms of this wave's 4 groups of chunk c into buffer par
+    auto terms = [&](const Pipe& p, int c, int par) {
+        if (c * CHS + sbw >= nsb) return;  // a chunk with one super-block: waves 4..7 idle
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t word = (i < 2) ? p.wv.x : p.wv.y;
+            const vk_s16x4 w = q4k_operand(word, 2 * (i & 1));
+            const uint4 a4 = p.af[i >> 1];
+            const uint2 ap = (i & 1) ? make_uint2(a4.z, a4.w) : make_uint2(a4.x, a4.y);
+            const float c0 = -128.0f * p.a[i];
+            const vk_f32x4 cin = {c0, c0, c0, c0};
+            // transposed product: weights as the A operand, so lane l gets
+            // activation row l % 16, columns rq..rq+3
+            const vk_f32x4 isum =
+                __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(w, __builtin_bit_cast(vk_s16x4, ap), cin, 0, 0, 0);
+            const float4 d01 = p.dm[i >> 1][0], d23 = p.dm[i >> 1][1];  // (d, m) of cols rq .. rq + 3
+            const float s = p.s[i], a = p.a[i];
+            float4 t;
+            t.x = s * (d01.x * isum[0] - d01.y * a);
+            t.y = s * (d01.z * isum[1] - d01.w * a);
+            t.z = s * (d23.x * isum[2] - d23.y * a);
+            t.w = s * (d23.z * isum[3] - d23.w * a);
+            *reinterpret_cast<float4*>(&lds_t[par][16 * sbw + 4 * q4 + i][row_l * 16 + rq]) = t;
         }
-        return st;
+    };
+    // phase 2: the ordered adds of chunk c (waves 0..3, one output per thread)
+    float acc = 0.0f;
+    auto chain = [&](int c, int par) {
+        if (!owner) return;
+        const int ng = min(CHS, nsb - c * CHS) * NG;
+        if (ng == CHG) {
+#pragma unroll
+            for (int g = 0; g < CHG; ++g) acc += lds_t[par][g][tid];
+        } else {
+#pragma unroll
+            for (int g = 0; g < NG; ++g) acc += lds_t[par][g][tid];
+        }
     };
 
-    float acc = 0.0f;
-    Stage st = load(0);
-    for (int sb0 = 0; sb0 < nsb; sb0 += CS) {
-        const int gsb = min(CS, nsb - sb0);   // super-blocks in this chunk
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            const int idx = tid + 256 * h;
-            if (idx < gsb * 256) {
-                const int gl = idx >> 4, r = idx & 15;
-                sa_f[r * (CG + 4) + gl] = st.sv[h];
-                as_f[r * (CG + 4) + gl] = st.tv[h];
-            }
+    Pipe pa = load(0);
+    Pipe pb = load(n_chunk > 1 ? 1 : 0);
+    terms(pa, 0, 0);
+    if (n_chunk > 2) pa = load(2);
+    VK_LDS_BARRIER();
+    for (int c = 0; c < n_chunk; c += 2) {
+        if (c + 1 < n_chunk) {
+            terms(pb, c + 1, 1);
+            if (c + 3 < n_chunk) pb = load(c + 3);
         }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int idx = tid + 256 * h;
-            if (idx < gsb * 128) dm_f[(idx & 15) * (CG / 2 + 2) + (idx >> 4)] = st.dm[h];
-        }
+        chain(c, 0);
         VK_LDS_BARRIER();
-        // ---- phase 1: this wave's super-block
-        // (8 groups at a time: all LDS reads, then all MFMAs, then all writes,
-        // so the latencies overlap instead of adding up per group)
-        if (wave < gsb) {
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const uint32_t words[4] = {st.wv[half].x, st.wv[half].y, st.wv[half].z, st.wv[half].w};
-                const int g0 = wave * NG + half * 8;
-                float t[8];
-#pragma unroll
-                for (int gi = 0; gi < 8; ++gi) t[gi] = as_f[(lane & 15) * (CG + 4) + g0 + gi];
-                vk_f32x4 p[8];
-#pragma unroll
-                for (int gi = 0; gi < 8; ++gi) {
-                    const uint4 a4 = st.af[half * 4 + (gi >> 1)];
-                    const uint2 ap = (gi & 1) ? make_uint2(a4.z, a4.w) : make_uint2(a4.x, a4.y);
-                    const vk_s16x4 w = q4k_operand(words[gi >> 1], 2 * (gi & 1));
-                    const float c = -128.0f * t[gi];
-                    const vk_f32x4 cin = {c, c, c, c};
-                    // transposed product: weights as the A operand, so lane l
-                    // gets activation row l % 16, columns rq..rq+3
-                    p[gi] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(w, __builtin_bit_cast(vk_s16x4, ap), cin, 0, 0,
-                                                                      0);
-                }
-#pragma unroll
-                for (int gi = 0; gi < 8; ++gi)
-                    *reinterpret_cast<float4*>(&lds_p[g0 + gi][(lane & 15) * 16 + rq]) =
-                        make_float4(p[gi][0], p[gi][1], p[gi][2], p[gi][3]);
-            }
+        if (c + 1 >= n_chunk) break;
+        if (c + 2 < n_chunk) {
+            terms(pa, c + 2, 0);
+            if (c + 4 < n_chunk) pa = load(c + 4);
         }
-        // ---- next chunk's loads (the last chunk reloads itself, unused)
-        st = load(sb0 + CS < nsb ? sb0 + CS : sb0);
-        VK_LDS_BARRIER();
-        // ---- phase 2: the reference combine, 4 groups (2 sub-blocks) per step
-        // (one super-block per step: its 28 LDS reads issue together)
-        if (rows_live) {
-            for (int sbl = 0; sbl < gsb; ++sbl) {
-                float4 s4[4], a4[4], dm4[4];  // dm4 = (d0, m0, d1, m1)
-                float p[16];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    s4[u] = lds_sa[row][4 * sbl + u];
-                    a4[u] = lds_as[row][4 * sbl + u];
-                    dm4[u] = lds_dm[col][4 * sbl + u];
-                }
-#pragma unroll
-                for (int u = 0; u < 16; ++u) p[u] = lds_p[NG * sbl + u][tid];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    acc += s4[u].x * (dm4[u].x * p[4 * u] - dm4[u].y * a4[u].x);
-                    acc += s4[u].y * (dm4[u].x * p[4 * u + 1] - dm4[u].y * a4[u].y);
-                    acc += s4[u].z * (dm4[u].z * p[4 * u + 2] - dm4[u].w * a4[u].z);
-                    acc += s4[u].w * (dm4[u].z * p[4 * u + 3] - dm4[u].w * a4[u].w);
-                }
-            }
-        }
+        chain(c + 1, 1);
         VK_LDS_BARRIER();
     }
-    const int orow = mt * 16 + row, ocol = nt * 16 + col;
-    if (orow < m && ocol < n) {
-        const size_t o = (size_t)orow * n + ocol;
-        out[o] = vk_epi_apply(HAS_BIAS ? acc + bias[ocol] : acc, epi, o);
+    if (wave < 4) {
+        const int orow = mt * 16 + (tid >> 4), ocol = nt * 16 + (tid & 15);
+        if (orow < m && ocol < n) {
+            const size_t o = (size_t)orow * n + ocol;
+            out[o] = vk_epi_apply(HAS_BIAS ? acc + bias[ocol] : acc, epi, o);
+        }
     }
 }
 
@@ -368,10 +367,10 @@ hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascal
                            int m_pad, VkEpi epi) {
     const dim3 grid((n + 15) / 16, (m + 15) / 16);
     if (bias)
-        hipLaunchKernelGGL(vk_gemm_q4k<true>, grid, dim3(256), 0, s, afrag, ascale, asum, wq4, wdm, bias, epi, out, m,
+        hipLaunchKernelGGL(vk_gemm_q4k<true>, grid, dim3(512), 0, s, afrag, ascale, asum, wq4, wdm, bias, epi, out, m,
                            n, nsb, m_pad);
     else
-        hipLaunchKernelGGL(vk_gemm_q4k<false>, grid, dim3(256), 0, s, afrag, ascale, asum, wq4, wdm, bias, epi, out, m,
+        hipLaunchKernelGGL(vk_gemm_q4k<false>, grid, dim3(512), 0, s, afrag, ascale, asum, wq4, wdm, bias, epi, out, m,
                            n, nsb, m_pad);
     return hipGetLastError();
 }
