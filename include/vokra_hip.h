@@ -191,6 +191,19 @@ void vokra_hip_qweight_free(vokra_hip_qweight_t *w);
 int vokra_hip_gemm_q_f32_dev(vokra_hip_ctx_t *ctx, const vokra_hip_qweight_t *w, size_t m,
                              const float *d_a, const float *d_bias, float *d_out, int act_quant);
 
+/* gemm_q_f32_dev that allocates nothing. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The INT8
+ * activation pass writes its fragments, scales and sums into a 32 MiB
+ * workspace that the library holds per device for the life of the process;
+ * every byte a call reads is written by that call. Results are bit-identical
+ * to vokra_hip_gemm_q_f32_dev. Shapes whose workspace exceeds 32 MiB
+ * (2.5 * round_up(m, 128) * k bytes, 256-byte aligned regions) are
+ * INVALID_ARGUMENT. Calls on one device share the workspace: calls that
+ * overlap in time on that device (other streams or contexts) race. */
+int vokra_hip_gemm_q_f32_dev_noalloc(vokra_hip_ctx_t *ctx, const vokra_hip_qweight_t *w, size_t m,
+                                     const float *d_a, const float *d_bias, float *d_out, int act_quant);
+
 /* gemm_q_f32_dev split in its two launches, for callers that feed one
  * activation matrix to several weights (the q/k/v projections of
  * crates/vokra-models/src/whisper/nn.rs:185-197 read the same LN output):

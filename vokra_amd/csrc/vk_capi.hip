@@ -14,6 +14,7 @@
 #include <new>
 #include <string>
 #include <utility>
+#include <mutex>
 #include <vector>
 
 #include "../../include/vokra_hip.h"
@@ -35,6 +36,32 @@ int fail(int code, const char* fmt, ...) {
 
 int hip_fail(hipError_t e, const char* what) {
     return fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Workspace of the no-allocation GEMM entry point: activation fragments,
+// scales and sums of one call. Each device holds its own copy for the life of
+// the process; host code uses the per-device address from
+// hipGetSymbolAddress (kept in g_scratch_dev), never the array's name.
+constexpr size_t kScratchBytes = 32u << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+void* g_scratch_dev[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// The device address of `scratch` on `device` (current), looked up once.
+int scratch_address(int device, void** out) {
+    if (device < 0 || device >= kMaxDevices)
+        return fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, "device %d beyond the scratch table", device);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[device]) {
+        void* ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!ptr) return fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, "hipGetSymbolAddress(scratch) returned NULL");
+        g_scratch_dev[device] = ptr;
+    }
+    *out = g_scratch_dev[device];
+    return VOKRA_HIP_OK;
 }
 
 #define VK_TRY(call, what)                                 \
@@ -122,6 +149,7 @@ struct vokra_hip_ctx {
     DevBuf lg_part;  // per-workgroup (max, index) partials of the fused logits argmax
     // RoPE frequency table of the last (rope_base, head_dim) the _dev entry saw
     DevBuf rope_theta, rope_pos;
+    void* scratch = nullptr;  // this device's address of the no-allocation workspace
     float rope_base = 0.0f;
     size_t rope_hd = 0;
 };
@@ -1467,10 +1495,13 @@ int vokra_hip_create(int device, vokra_hip_ctx_t** out) {
         return fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, "device %d is %s; this library is built for gfx950",
                     device, prop.gcnArchName);
     VK_TRY(hipSetDevice(device), "hipSetDevice");
+    void* scr = nullptr;
+    if ((st = scratch_address(device, &scr))) return st;
     auto* c = new vokra_hip_ctx();
     c->device = device;
     c->act.ctx = c;
     c->act.growable = true;
+    c->scratch = scr;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         delete c;
@@ -1728,6 +1759,53 @@ int vokra_hip_gemm_q_f32_dev(vokra_hip_ctx_t* c, const vokra_hip_qweight_t* w, s
     if (!d_a || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: NULL buffer");
     VK_TRY(set_dev(c), "hipSetDevice");
     return run_gemm(c, w, m, d_a, d_bias, d_out, act_quant);
+}
+
+int vokra_hip_gemm_q_f32_dev_noalloc(vokra_hip_ctx_t* c, const vokra_hip_qweight_t* w, size_t m, const float* d_a,
+                                     const float* d_bias, float* d_out, int act_quant) {
+    if (!c || !w) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev_noalloc: NULL context or weight");
+    if (w->ctx != c)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev_noalloc: weight belongs to another context");
+    if (m == 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "batched gemm_q_f32 needs at least one activation vector, got m = 0");
+    if (act_quant != VOKRA_HIP_ACT_AMAX127 && act_quant != VOKRA_HIP_ACT_POW2 && act_quant != VOKRA_HIP_ACT_KQUANT)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev_noalloc: unknown activation convention %d",
+                    act_quant);
+    if (act_quant == VOKRA_HIP_ACT_KQUANT && !w->kquant)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev_noalloc: KQUANT activations need Q4_K weights");
+    if (!d_a || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev_noalloc: NULL buffer");
+    // the workspace regions of qact_reserve(m, k), 256-byte aligned, in the static array
+    const size_t k = w->k;
+    if (m > ((size_t)1 << 30) / (k ? k : 1))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev_noalloc: m=%zu k=%zu too large", m, k);
+    const size_t m_pad = round_up(m, vk::GEMM_TM), ng = k / 16;
+    const size_t frag = round_up(m_pad * k * 2, 256), sc = round_up(m_pad * ng * sizeof(float), 256);
+    const size_t need = frag + 2 * sc;
+    if (need > kScratchBytes)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "gemm_q_f32_dev_noalloc: m=%zu k=%zu needs %zu bytes of workspace, the maximum is %zu "
+                    "(use vokra_hip_gemm_q_f32_dev)",
+                    m, k, need, kScratchBytes);
+    if (!c->scratch) return fail(VOKRA_HIP_ERROR_BACKEND_UNAVAILABLE, "gemm_q_f32_dev_noalloc: no workspace address");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    // a non-owning activation buffer over the workspace: fixed capacity,
+    // never grown or freed (DevBuf frees only through release())
+    vokra_hip_qact qa;
+    qa.ctx = c;
+    qa.max_m = m;
+    qa.k = k;
+    qa.growable = false;
+    unsigned char* base = static_cast<unsigned char*>(c->scratch);
+    qa.frag.p = base;
+    qa.frag.cap = frag;
+    qa.scale.p = base + frag;
+    qa.scale.cap = sc;
+    qa.gsum.p = base + frag + sc;
+    qa.gsum.cap = sc;
+    int st = quantize_activations(c, &qa, d_a, m, k, w->kquant ? VOKRA_HIP_ACT_KQUANT : act_quant);
+    if (st) return st;
+    return run_gemm_qact(c, w, &qa, d_bias, d_out);
 }
 
 int vokra_hip_gemm_q_f32(vokra_hip_ctx_t* c, int wdtype, size_t m, size_t n, size_t k, const float* a, size_t a_len,

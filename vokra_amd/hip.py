@@ -899,6 +899,13 @@ class HipContext:
         _check(lib().vokra_hip_gemm_q_f32_dev(self._h, w._h, m, d_a.ptr,
                                               None if d_bias is None else d_bias.ptr, d_out.ptr, int(act)))
 
+    def gemm_q_f32_dev_noalloc(self, w: QWeight, m: int, d_a: DeviceBuffer, d_out: DeviceBuffer, d_bias=None,
+                               act: ActQuant = ActQuant.AMAX127):
+        """gemm_q_f32_dev whose activation pass uses the library's fixed per-device
+        workspace (no device allocation)."""
+        _check(lib().vokra_hip_gemm_q_f32_dev_noalloc(self._h, w._h, m, d_a.ptr,
+                                                      None if d_bias is None else d_bias.ptr, d_out.ptr, int(act)))
+
     def kv_cache(self, n_layer, n_head, d_head, n_stream, max_time, block_size, mode=KvQuant.Q8_0) -> KvCache:
         return KvCache(self, n_layer, n_head, d_head, n_stream, max_time, block_size, mode)
 
