@@ -485,6 +485,12 @@ int vokra_hip_encoder_encode_dev(vokra_hip_ctx_t *ctx, vokra_hip_encoder_t *enc,
                                  const float *d_log_mel, float *d_out);
 int vokra_hip_encoder_encode(vokra_hip_ctx_t *ctx, vokra_hip_encoder_t *enc, size_t batch, const float *log_mel,
                              float *out);
+/* The stem part of encode alone (encoder.rs:58-104): log-mel -> conv1 + GELU
+ * -> conv2 + GELU -> + pos_emb into d_x [batch][n_frames / 2][d], the input
+ * encode then hands to the blocks (encode == stem, then forward, bit for
+ * bit). Device pointers, asynchronous. */
+int vokra_hip_encoder_stem_dev(vokra_hip_ctx_t *ctx, vokra_hip_encoder_t *enc, size_t batch,
+                               const float *d_log_mel, float *d_x);
 
 /* ---- batched decoder-step session --------------------------------------- */
 

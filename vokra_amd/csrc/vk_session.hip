@@ -249,9 +249,9 @@ int enc_forward(vokra_hip_encoder* e, size_t batch, size_t frames, const float* 
 
 // The conv stem of WhisperEncoder::encode (crates/vokra-models/src/whisper/
 // encoder.rs:58-104) as im2col + f32 GEMM with bias and GELU in the GEMM
-// epilogue, conv outputs kept time-major ([frames, d]), then + pos_emb; the
-// blocks follow (enc_forward).
-int enc_encode(vokra_hip_encoder* e, size_t batch, const float* d_mel, float* d_out) {
+// epilogue, conv outputs kept time-major ([frames, d]), then + pos_emb, into
+// d_x [batch, n_ctx, d].
+int enc_stem(vokra_hip_encoder* e, size_t batch, const float* d_mel, float* d_x) {
     vokra_hip_ctx_t* c = e->ctx;
     hipStream_t s = vk::ctx_stream(c);
     const size_t d = e->d, nm = e->n_mels, nf = e->n_frames, nc = e->n_ctx;
@@ -274,11 +274,17 @@ int enc_encode(vokra_hip_encoder* e, size_t batch, const float* d_mel, float* d_
     SS_HIP(vk::launch_im2col(s, true, e->c1.f(), nf * d, 1, d, (int)batch, (int)d, (int)nf, 3, 2, 1, (int)nc,
                              e->col2.f()),
            "launch(vk_im2col conv2)");
-    SS_HIP(vk::launch_gemm_f32(s, true, e->col2.f(), e->c2w.f(), e->c2b.f(), e->x.f(), (int)(batch * nc), (int)d,
+    SS_HIP(vk::launch_gemm_f32(s, true, e->col2.f(), e->c2w.f(), e->c2b.f(), d_x, (int)(batch * nc), (int)d,
                                (int)(d * 3), gelu),
            "launch(vk_gemm_f32 conv2)");
-    SS_HIP(vk::launch_add_pos(s, e->x.f(), e->pos.f(), batch * nc, (int)d, (int)nc), "launch(vk_add_pos)");
-    return enc_forward(e, batch, nc, e->x.f(), d_out);  // copies x into h before reusing x
+    SS_HIP(vk::launch_add_pos(s, d_x, e->pos.f(), batch * nc, (int)d, (int)nc), "launch(vk_add_pos)");
+    return VOKRA_HIP_OK;
+}
+
+// The whole of WhisperEncoder::encode: the stem, then the blocks (enc_forward).
+int enc_encode(vokra_hip_encoder* e, size_t batch, const float* d_mel, float* d_out) {
+    SS_TRY(enc_stem(e, batch, d_mel, e->x.f()));
+    return enc_forward(e, batch, e->n_ctx, e->x.f(), d_out);  // copies x into h before reusing x
 }
 
 int dec_setup(vokra_hip_decoder* m, const vokra_hip_decoder_layer_t* layers, const float* tok_emb,
@@ -506,6 +512,17 @@ int vokra_hip_encoder_encode_dev(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, siz
         return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_encode: batch * n_ctx exceeds max_rows");
     if (!d_log_mel || !d_out) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_encode: NULL buffer");
     return enc_encode(e, batch, d_log_mel, d_out);
+}
+
+int vokra_hip_encoder_stem_dev(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, size_t batch, const float* d_log_mel,
+                               float* d_x) {
+    if (!c || !e || e->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_stem: bad context");
+    if (!e->n_ctx) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_stem: no conv stem (set_stem)");
+    if (batch == 0) return VOKRA_HIP_OK;
+    if (batch * e->n_ctx > e->max_rows)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_stem: batch * n_ctx exceeds max_rows");
+    if (!d_log_mel || !d_x) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "encoder_stem: NULL buffer");
+    return enc_stem(e, batch, d_log_mel, d_x);
 }
 
 int vokra_hip_encoder_encode(vokra_hip_ctx_t* c, vokra_hip_encoder_t* e, size_t batch, const float* log_mel,

@@ -335,6 +335,15 @@ class DeviceBuffer:
         _check(lib().vokra_hip_memcpy_dtoh(self.ctx._h, out.ctypes.data_as(C.c_void_p), self.ptr, out.nbytes))
         return out
 
+    def download_at(self, dtype, offset, count):
+        """count elements of dtype starting at element `offset`."""
+        out = np.empty(count, dtype)
+        start = int(offset) * out.itemsize
+        assert start + out.nbytes <= self.nbytes
+        _check(lib().vokra_hip_memcpy_dtoh(self.ctx._h, out.ctypes.data_as(C.c_void_p),
+                                           C.c_void_p(self.ptr.value + start), out.nbytes))
+        return out
+
     def free(self):
         if self.ptr:
             _check(lib().vokra_hip_device_free(self.ctx._h, self.ptr))
@@ -647,6 +656,10 @@ class Encoder:
                                               _ptr(out, C.c_float)))
         return out
 
+    def stem_dev(self, batch, d_log_mel, d_x):
+        """The conv stem alone (log-mel -> [batch, n_frames/2, d] block input)."""
+        _check(lib().vokra_hip_encoder_stem_dev(self._ctx._h, self._h, batch, d_log_mel.ptr, d_x.ptr))
+
     def encode_dev(self, batch, d_log_mel, d_out):
         _check(lib().vokra_hip_encoder_encode_dev(self._ctx._h, self._h, batch, d_log_mel.ptr, d_out.ptr))
 
@@ -947,6 +960,17 @@ class HipContext:
                                               rows, cols, _ptr(g, C.c_float), g.size, _ptr(b, C.c_float), b.size,
                                               C.c_float(eps)))
         return out[:xv.size].reshape(rows, cols)
+
+    def layer_norm_f32_dev(self, d_in, d_out, rows, cols, d_gamma, d_beta, eps=1e-5):
+        _check(lib().vokra_hip_layer_norm_f32_dev(self._h, d_in.ptr, d_out.ptr, rows, cols, d_gamma.ptr, d_beta.ptr,
+                                                  C.c_float(eps)))
+
+    def gelu_f32_dev(self, d_x, d_out, n):
+        _check(lib().vokra_hip_gelu_f32_dev(self._h, d_x.ptr, d_out.ptr, n))
+
+    def add_f32_dev(self, d_a, d_b, d_out, n):
+        """out = a + b on device (residual connections)."""
+        _check(lib().vokra_hip_add_f32_dev(self._h, d_a.ptr, d_b.ptr, d_out.ptr, n))
 
     def rms_norm_f32(self, x, rows, cols, gamma, eps):
         xv, g = _f32(x).reshape(-1), _f32(gamma)
