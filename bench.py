@@ -224,44 +224,61 @@ def bench_sdpa(ctx, hip, reps=20, T=1500, H=20, hd=64, batch=1):
             "mfma_passes_per_product": 3}
 
 
-def bench_paged_attn(ctx, hip, n_stream, H, hd, hq, len_lo, len_hi, max_time, reps=50, seed=3):
-    """Decode self-attention over the paged Q8_0 KV cache (one layer), 16-token
-    pages placed at shuffled addresses, per-stream lengths U(len_lo..len_hi).
+def bench_paged_attn(ctx, hip, n_stream, H, hd, hq, len_lo, len_hi, max_time, n_layer=16, reps=10, seed=3):
+    """Decode self-attention over the paged Q8_0 KV cache, 16-token pages placed
+    at shuffled addresses, per-stream lengths U(len_lo..len_hi), for n_layer
+    layers whose caches together exceed twice the 256 MB MALL; the timed loop
+    launches the layers in rotation, so each launch reads its cache from HBM.
     GB/s counts per launch the K and V head slices read (int8 + f16 scale per
-    32 values) for every (stream, key) plus f32 q and out."""
+    32 values) for every (stream, key) plus f32 q and out. The same launch
+    repeated on one layer (its cache then served from the MALL) is reported
+    beside it as `single_layer_repeat`."""
     rng = np.random.default_rng(seed)
     bs = 16
-    kv = ctx.kv_cache(1, H, hd, n_stream, max_time, bs)
-    kv.set_free_order(rng.permutation((max_time + bs - 1) // bs).astype(np.int32))
+    kv = ctx.kv_cache(n_layer, H, hd, n_stream, max_time, bs)
+    ppl = (max_time + bs - 1) // bs
+    kv.set_free_order(rng.permutation(n_layer * ppl).astype(np.int32))
     lens = rng.integers(len_lo, len_hi + 1, n_stream).astype(np.int32)
     w = H * hd
-    for t in range(int(lens.max())):
-        live = np.nonzero(lens > t)[0].astype(np.int32)
-        rows = rng.standard_normal((live.size, w), dtype=np.float32)
-        kv.append(0, live, np.full(live.size, t, np.int32), rows, rows)
+    st = np.concatenate([np.full(int(lens[s]), s, np.int32) for s in range(n_stream)])
+    tt = np.concatenate([np.arange(int(lens[s]), dtype=np.int32) for s in range(n_stream)])
+    for layer in range(n_layer):
+        for i0 in range(0, st.size, 1024):
+            i1 = min(st.size, i0 + 1024)
+            rows = rng.standard_normal((i1 - i0, w), dtype=np.float32)
+            kv.append(layer, st[i0:i1], tt[i0:i1], rows, rows[::-1].copy())
     d_st = hip.DeviceBuffer.from_array(ctx, np.arange(n_stream, dtype=np.int32))
     d_len = hip.DeviceBuffer.from_array(ctx, lens)
     d_q = hip.DeviceBuffer.from_array(ctx, rng.standard_normal((n_stream, hq * hd), dtype=np.float32))
     d_out = hip.DeviceBuffer(ctx, n_stream * hq * hd * 4)
 
-    def run():
-        kv.attn_dev(0, n_stream, d_st, d_len, int(lens.max()), hq, d_q, hd ** -0.5, d_out)
+    def run(layer):
+        kv.attn_dev(layer, n_stream, d_st, d_len, int(lens.max()), hq, d_q, hd ** -0.5, d_out)
 
-    run()
+    for layer in range(n_layer):
+        run(layer)
     ctx.synchronize()
     e0, e1 = hip.Event(ctx), hip.Event(ctx)
     e0.record()
     for _ in range(reps):
-        run()
+        for layer in range(n_layer):
+            run(layer)
     e1.record()
-    us = e0.elapsed_ms(e1) * 1e3 / reps
+    us = e0.elapsed_ms(e1) * 1e3 / (reps * n_layer)
+    e0.record()
+    for _ in range(reps * n_layer):
+        run(0)
+    e1.record()
+    us_one = e0.elapsed_ms(e1) * 1e3 / (reps * n_layer)
     nbytes = int(lens.sum()) * 2 * (w + (w // 32) * 2) + 2 * n_stream * hq * hd * 4
     del kv
     ctx.synchronize()
     return {"streams": n_stream, "kv_heads": H, "q_heads": hq, "head_dim": hd, "len_range": [len_lo, len_hi],
-            "keys_total": int(lens.sum()), "us": round(us, 3), "bytes": nbytes,
-            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
-            "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK["hbm_gbs"], 4)}
+            "keys_total": int(lens.sum()), "layers_rotated": n_layer, "working_set_bytes": n_layer * nbytes,
+            "us": round(us, 3), "bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK["hbm_gbs"], 4),
+            "single_layer_repeat": {"us": round(us_one, 3), "gbs": round(nbytes / (us_one * 1e-6) / 1e9, 1),
+                                    "note": "one layer's cache, served from the MALL"}}
 
 
 def random_block_weight(rng, wd, n, k, scale):
@@ -351,12 +368,14 @@ def bench_encoder(ctx, hip, batch, n_layer=32, d=1280, H=20, ff=5120, T=1500, re
 
 
 def bench_decoder(ctx, hip, n_stream=64, n_layer=32, d=1280, H=20, ff=5120, V=51866, n_text=448, n_audio=1500,
-                  steps=5, max_prefix=440):
+                  steps=5, max_prefix=442):
     """Config 3: batched Whisper-large-v3-shaped decoder step, 64 streams with
     prefixes U(1..max_prefix) already in the paged Q8_0 self-KV cache (16-token
     pages), cross-attention over 1500 encoder frames per stream, Q4_0
     random-init weights, tied logits over a 51866-token vocabulary, greedy
-    argmax. Timed: `steps` whole batched steps on device arrays."""
+    argmax. Timed: `steps` whole batched steps on device arrays. The prefix
+    ceiling leaves room for the timed steps: prefix + 1 + steps <= 448
+    positions (n_text_ctx), so the last timed step reaches position 447."""
     rng = np.random.default_rng(3)
     layers = [whisper_layer(rng, 2, d, ff, 5e-3, decoder=True) for _ in range(n_layer)]
     tok = (0.02 * rng.standard_normal((V, d))).astype(np.float32)
@@ -399,7 +418,9 @@ def bench_decoder(ctx, hip, n_stream=64, n_layer=32, d=1280, H=20, ff=5120, V=51
     e1.record()
     ms_f16 = e0.elapsed_ms(e1) / steps
     keys = int((lens + 1 + steps // 2).sum())
-    w_bytes = n_layer * (8 * d * d + 2 * d * ff) * 18 // 32
+    # a step reads 8 of the 10 d x d linears per layer (q, k, v, o, cross q,
+    # cross o; cross k / v are applied once per utterance) and fc1 / fc2
+    w_bytes = n_layer * (6 * d * d + 2 * d * ff) * 18 // 32
     kv_bytes = keys * n_layer * 2 * (d + d // 32 * 2)
     cross_bytes = n_stream * n_layer * n_audio * d * 4 * 2
     emb_bytes = V * d * 4
@@ -407,6 +428,7 @@ def bench_decoder(ctx, hip, n_stream=64, n_layer=32, d=1280, H=20, ff=5120, V=51
     del dec
     ctx.synchronize()
     return {"streams": n_stream, "layers": n_layer, "vocab": V, "prefix_range": [1, max_prefix],
+            "last_position": int(lens.max()) + steps,
             "ms_per_step": round(ms, 3), "tokens_per_s": round(n_stream / (ms * 1e-3), 1),
             "cross_f16_mode": {"ms_per_step": round(ms_f16, 3), "tokens_per_s": round(n_stream / (ms_f16 * 1e-3), 1)},
             "bytes_per_step": {"weights_q4_0": w_bytes, "self_kv_q8_0": kv_bytes, "cross_kv_fp16x2": cross_bytes,
@@ -546,6 +568,160 @@ def cpu_baseline_q8(a, wq, N, K, budget_s=10.0):
                       f"{t_total:.1f} s on host {platform.processor() or platform.machine()}"}
 
 
+def _host():
+    return f"{platform.processor() or platform.machine()}, {os.cpu_count()} logical cores"
+
+
+def _per_call(fn, budget_s):
+    """Median seconds per call of fn: one warm-up, then calls until the budget
+    is spent (at least three)."""
+    fn()
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < 3 or (time.perf_counter() < t_end and len(ts) < 50):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), len(ts)
+
+
+def cpu_baselines(budget_s=3.0):
+    """Each leg's CPU column: the oracle's restatement of the reference's CPU
+    route (oracle/vokra_oracle.c, the vokra-backend-cpu scalar tier) timed on
+    this host on a bounded sample of the leg's workload, with the reference's
+    threading (the INT8 and block routes are single-threaded; f32 GEMMs use
+    the pool, i.e. every core). Values are in the leg's own unit."""
+    from oracle import oracle as orc
+    orc.lib()
+    rng = np.random.default_rng(5)
+    host = _host()
+    ncpu = os.cpu_count() or 1
+    out = {}
+
+    # Q4_0 GEMV (dequant_gemv_scalar, 1 thread): one activation vector
+    n, k = 5120, 1280
+    wq = rng.integers(0, 256, n * (k // 32) * 18, dtype=np.uint8)
+    wq.reshape(-1, 18)[:, 0:2] = np.frombuffer(np.float16(0.002).tobytes(), np.uint8)
+    x = rng.standard_normal(k, dtype=np.float32)
+    sec, reps = _per_call(lambda: orc.dequant_gemv_scalar(1, wq, n, k // 32, x), budget_s)
+    nbytes = n * (k // 32) * 18 + k * 4 + n * 4
+    out["q4_0_gemv_streamed"] = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "us_per_linear": round(sec * 1e6, 1),
+                                 "cores": 1, "kind": "port",
+                                 "sample": f"M=1 N={n} K={k}, dequant_gemv_scalar (vo_dequant_gemv_scalar), "
+                                           f"median of {reps} on {host}"}
+    # Q4_K decode layer (kquant_gemm_i8, 1 thread): the 7 linears at M = 32
+    total = 0.0
+    for (_, n, k) in Q4K_LAYER:
+        w = q4k_random_weight(rng, n, k)
+        a = rng.standard_normal((32, k), dtype=np.float32)
+        sec, _ = _per_call(lambda: orc.kquant_gemm_i8(12, n, k, 32, w, a), budget_s / 7)
+        total += sec
+    nbytes = sum(n * (k // 256) * 144 + 32 * k * 4 + 32 * n * 4 for (_, n, k) in Q4K_LAYER)
+    out["q4_k_decode_layer_m32"] = {"value": round(nbytes / total / 1e9, 3), "unit": "GB/s",
+                                    "us_per_layer": round(total * 1e6, 1), "cores": 1, "kind": "port",
+                                    "sample": f"one config-4 layer (7 linears) at M=32 through kquant_gemm_i8 "
+                                              f"(vo_kquant_gemm_i8) on {host}"}
+    # fused SDPA config 1 (attention_from_kv_into per head: f32 GEMMs + softmax, 1 thread)
+    T, hd = 1500, 64
+    q, kk, v = (rng.standard_normal((T, hd), dtype=np.float32) for _ in range(3))
+    sec, reps = _per_call(lambda: orc.sdpa_whisper(T, T, 1, hd, q, kk, v), budget_s)
+    flops = 4.0 * T * T * hd
+    out["sdpa_config1"] = {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s",
+                           "ms_per_op": round(sec * 20 * 1e3, 1), "cores": 1, "kind": "port",
+                           "sample": f"one of the 20 heads (1500 x 1500 x 64, vo_sdpa_whisper), x20 for the op; "
+                                     f"median of {reps} on {host}"}
+    # paged decode attention (config 4: one stream, 16/2 heads x 128, 2300 keys)
+    t_kv = 2300
+    Kc = rng.standard_normal((t_kv, 256), dtype=np.float32)
+    Vc = rng.standard_normal((t_kv, 256), dtype=np.float32)
+    qg = rng.standard_normal((1, 2048), dtype=np.float32)
+    sec, reps = _per_call(lambda: orc.gqa_attention(1, t_kv, 16, 2, 128, qg, Kc, Vc, 0.0884, t_kv - 1), budget_s)
+    nbytes = t_kv * 2 * (256 + 16)
+    out["paged_attn_config4"] = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s",
+                                 "us_per_stream": round(sec * 1e6, 1), "cores": 1, "kind": "port",
+                                 "sample": f"one stream, 2300 keys, GQA 16/2 x 128 over dequantized rows "
+                                           f"(vo_gqa_attention), median of {reps} on {host}"}
+    # Whisper-large encoder block (config 2): INT8 linears (1 thread) + f32 attention, on 96 query rows
+    rows, d, ff = 96, 1280, 5120
+    a = rng.standard_normal((rows, d), dtype=np.float32)
+    w8 = random_block_weight(rng, 8, d, d, 0.02)
+    w8f = random_block_weight(rng, 8, ff, d, 0.02)
+    w8b = random_block_weight(rng, 8, d, ff, 0.02)
+    af = rng.standard_normal((rows, ff), dtype=np.float32)
+    qh, kh, vh = rng.standard_normal((rows, 64), dtype=np.float32), q, v
+
+    def enc_sample():
+        for _ in range(4):
+            orc.gemm_q_f32(8, rows, d, d, a, w8)
+        orc.gemm_q_f32(8, rows, ff, d, a, w8f)
+        orc.gemm_q_f32(8, rows, d, ff, af, w8b)
+        for _ in range(20):
+            orc.sdpa_whisper(rows, T, 1, 64, qh, kh, vh)
+    sec, reps = _per_call(enc_sample, budget_s)
+    per_block = sec * (1500 / rows)
+    flops_block = 2 * 1500 * (4 * d * d + 2 * d * ff) + 4 * 20 * 1500 * 1500 * 64
+    out["encoder_config2"] = {"value": round(flops_block / per_block / 1e12, 4), "unit": "TFLOP/s",
+                              "ms_per_utterance": round(per_block * 32 * 1e3, 0), "cores": 1, "kind": "port",
+                              "sample": f"one block's linears (gemm_q_f32 Q8_0) and 20 attention heads for {rows} of "
+                                        f"1500 rows, scaled to 1500 rows x 32 blocks; median of {reps} on {host}"}
+    # Whisper decoder step (config 3): one stream, one layer's 8 step linears + self/cross attention + logits
+    Vv = 51866
+    a1 = rng.standard_normal((1, d), dtype=np.float32)
+    f1 = rng.standard_normal((1, ff), dtype=np.float32)
+    w4 = random_block_weight(rng, 2, d, d, 0.02)
+    w4f = random_block_weight(rng, 2, ff, d, 0.02)
+    w4b = random_block_weight(rng, 2, d, ff, 0.02)
+    ck = rng.standard_normal((1500, d), dtype=np.float32)
+    sk = rng.standard_normal((224, d), dtype=np.float32)
+    emb = rng.standard_normal((Vv, d), dtype=np.float32)
+
+    def dec_layer():
+        for _ in range(6):
+            orc.gemm_q_f32(2, 1, d, d, a1, w4)
+        orc.gemm_q_f32(2, 1, ff, d, a1, w4f)
+        orc.gemm_q_f32(2, 1, d, ff, f1, w4b)
+        orc.sdpa_whisper(1, 224, 20, 64, a1, sk, sk, causal=True, q_pos_offset=223)
+        orc.sdpa_whisper(1, 1500, 20, 64, a1, ck, ck)
+    sec_l, _ = _per_call(dec_layer, budget_s / 2)
+    sec_g, _ = _per_call(lambda: orc.gemm_f32(1, Vv, d, a1, emb.T.copy(), threads=ncpu), budget_s / 2)
+    step = 32 * sec_l + sec_g
+    out["decoder_step_config3"] = {"value": round(1.0 / step, 2), "unit": "tokens/s",
+                                   "ms_per_stream_step": round(step * 1e3, 1), "cores": 1, "kind": "port",
+                                   "sample": f"one stream: one layer (8 Q4_0 step linears, self-attention over 224 "
+                                             f"keys, cross over 1500) x 32, plus the tied logits (gemm_f32 on "
+                                             f"{ncpu} threads); streams run one after another, so 64 streams "
+                                             f"take 64x; on {host}"}
+    # speech-LLM step (config 4): one stream, one layer's 7 Q4_K linears + GQA over 2300 keys
+    def td_layer():
+        for (_, n, k) in Q4K_LAYER:
+            orc.kquant_gemm_i8(12, n, k, 1, q4k_w[(n, k)], x4[k])
+        orc.gqa_attention(1, t_kv, 16, 2, 128, qg, Kc, Vc, 0.0884, t_kv - 1)
+    q4k_w = {(n, k): q4k_random_weight(rng, n, k) for (_, n, k) in Q4K_LAYER}
+    x4 = {k: rng.standard_normal((1, k), dtype=np.float32) for k in (2048, 5632)}
+    head = q4k_random_weight(rng, 32000, 2048)
+    sec_l, _ = _per_call(td_layer, budget_s / 2)
+    sec_h, _ = _per_call(lambda: orc.kquant_gemm_i8(12, 32000, 2048, 1, head, x4[2048]), budget_s / 2)
+    step = 24 * sec_l + sec_h
+    out["text_decoder_step_config4"] = {"value": round(1.0 / step, 2), "unit": "tokens/s",
+                                        "ms_per_stream_step": round(step * 1e3, 1), "cores": 1, "kind": "port",
+                                        "sample": f"one stream: one layer (7 Q4_K linears via kquant_gemm_i8, GQA "
+                                                  f"over 2300 keys) x 24 plus the Q4_K LM head; on {host}"}
+    # log-mel front end (one 30 s clip, 128 mels; the oracle's f64 DFT)
+    pcm = rng.standard_normal(480000, dtype=np.float32) * 0.1
+    sec, reps = _per_call(lambda: orc.log_mel(pcm, 128), budget_s)
+    out["frontend_config2_batch16"] = {"value": round(1.0 / sec, 2), "unit": "clips/s", "cores": 1, "kind": "port",
+                                       "sample": f"log-mel of one 30 s clip, 128 mels (vo_log_mel, f64 DFT), median "
+                                                 f"of {reps} on {host}"}
+    # tied logits + argmax (config 3): gemm_f32 over the embedding on every core
+    xs = rng.standard_normal((8, d), dtype=np.float32)
+    sec, reps = _per_call(lambda: orc.gemm_f32(8, Vv, d, xs, emb.T.copy(), threads=ncpu), budget_s)
+    out["logits_argmax_config3"] = {"value": round(2.0 * 8 * Vv * d / sec / 1e12, 4), "unit": "TFLOP/s",
+                                    "cores": ncpu, "kind": "port",
+                                    "sample": f"8 of 64 stream rows x 51866 x 1280 (vo_gemm_f32_mt, {ncpu} threads), "
+                                              f"median of {reps} on {host}"}
+    return out
+
+
 def load_traffic(name):
     """HBM bytes per launch of `name`, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
     passes recorded in profiles/traffic.json (calibrated on a 1 GiB copy)."""
@@ -621,8 +797,10 @@ def main():
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK["int8_tops"], 4),
                 "traffic": load_traffic("vk_gemm_qblock")}
     cpu = None
+    legs_cpu = {}
     if not args.no_cpu_baseline:
         cpu = cpu_baseline_q8(main_run["a"], main_run["wq"], N, K)
+        legs_cpu = cpu_baselines()
     line = {
         "metric": METRIC,
         "value": round(main_run["tops"], 2),
@@ -659,6 +837,16 @@ def main():
                          "frac_int8_peak": round(pow2_run["gemm_tops"] / PEAK["int8_tops"], 4)},
         },
     }
+    for leg, base in legs_cpu.items():
+        key = "paged_attn_config3_config4" if leg == "paged_attn_config4" else leg
+        entry = line["extra"].get(key)
+        if isinstance(entry, dict):
+            entry["cpu_baseline"] = base
+        elif isinstance(entry, list) and entry and isinstance(entry[-1], dict):
+            # the sampled shape: the first GEMV line (N = 5120) and the batch-1
+            # encoder line; the last paged-attention line (config 4)
+            first = leg in ("q4_0_gemv_streamed", "encoder_config2")
+            entry[0 if first else -1]["cpu_baseline"] = base
     print(json.dumps(line), flush=True)
     ctx.close()
     return 0

@@ -199,8 +199,10 @@ def test_gemm_q_tile_routes_rows_bit_exact(ctx, oracle, act, m, n, k):
 
 @pytest.mark.parametrize("act", [hip.ActQuant.AMAX127, hip.ActQuant.POW2])
 @pytest.mark.parametrize("wd", [hip.WDtype.Q4_0, hip.WDtype.Q8_0])
-@pytest.mark.parametrize("m,n,k", [(1, 16, 128), (3, 100, 256), (8, 1280, 1280), (17, 48, 512),
-                                   (33, 200, 128), (64, 1280, 5120), (64, 5120, 1280)])
+@pytest.mark.parametrize("m,n,k", [(1, 16, 128), (3, 100, 256), (17, 48, 512), (33, 200, 128), (64, 1280, 5120),
+                                   # the config-1 Q4_0 GEMV shapes: M in {1, 8, 64}, K = 1280, N in {1280, 5120}
+                                   (1, 1280, 1280), (1, 5120, 1280), (8, 1280, 1280), (8, 5120, 1280),
+                                   (64, 1280, 1280), (64, 5120, 1280)])
 def test_decode_kernel_bit_exact(ctx, oracle, wd, act, m, n, k):
     """m <= 64 runs the compact-weight decode kernel: bit-exact vs the oracle
     and bit-identical to the tiled GEMM on the same inputs."""
