@@ -430,9 +430,10 @@ int vokra_hip_gguf_find(const vokra_hip_gguf_t *f, const char *name, size_t *ind
 /* GgufFile::get (reader.rs:208) for integer / bool and string values. */
 int vokra_hip_gguf_meta_int(const vokra_hip_gguf_t *f, const char *key, int64_t *out);
 int vokra_hip_gguf_meta_str(const vokra_hip_gguf_t *f, const char *key, const char **out, size_t *len);
-/* A 2-D block-quant weight (dims [in, out]) straight from the mapping into a
- * resident weight, as vokra_hip_qweight_upload: the fused-quant-weights route
- * of the Whisper loader (crates/vokra-models/src/whisper/weights.rs:454-509). */
+/* A 2-D block-quant weight straight from the mapping into a resident weight,
+ * as vokra_hip_qweight_upload. Dims are read as the reference's loader reads a
+ * Linear weight, [out_features, in_features] (crates/vokra-models/src/whisper/
+ * weights.rs:460-470): the fused-quant-weights route (weights.rs:454-509). */
 int vokra_hip_gguf_upload_qweight(vokra_hip_ctx_t *ctx, const vokra_hip_gguf_t *f, const char *name,
                                   vokra_hip_qweight_t **out);
 /* GgufFile::tensor_f32 (reader.rs:256) for F32 / F16 tensors (host output). */
@@ -568,6 +569,49 @@ int vokra_hip_decoder_step_dev(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, s
  * KV_CACHE_EXHAUSTED; *n_appended = (layer, item) appends done, layer-major),
  * then INVALID_ARGUMENT if an attention operand left the fp16 range. */
 int vokra_hip_decoder_status(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t *n_appended);
+
+/* ---- Whisper sessions from a GGUF file ------------------------------------ */
+
+/* WhisperConfig (crates/vokra-models/src/whisper/config.rs:58-100) as read by
+ * WhisperConfig::from_gguf (config.rs:106-170): the vokra.whisper.* keys, each
+ * an unsigned u32-range integer, decoder_start_ids a non-empty u32 array, the
+ * optional alignment_heads an even-length array of in-range (layer, head)
+ * pairs, n_text_state == n_audio_state, head counts dividing d_model, no zero
+ * hyperparameter. MODEL_LOAD with the reference's "whisper config: ..."
+ * message otherwise. */
+typedef struct vokra_hip_whisper_config {
+    size_t n_mels, d_model, n_audio_ctx, n_audio_head, n_audio_layer;
+    size_t n_text_ctx, n_text_head, n_text_layer, n_vocab, ffn_dim;
+    uint32_t eot;
+} vokra_hip_whisper_config_t;
+int vokra_hip_whisper_config_from_gguf(const vokra_hip_gguf_t *f, vokra_hip_whisper_config_t *cfg);
+
+/* How the Linear weights were bound (the counterpart of QuantBindReport,
+ * weights.rs:145-160): taken verbatim from the mapping (already in the session
+ * dtype), or packed from F32/F16 on the device. */
+typedef struct vokra_hip_whisper_load_report {
+    size_t verbatim, packed;
+} vokra_hip_whisper_load_report_t;
+
+/* WhisperWeights::load_with (weights.rs:302-378) with fused-quant weights,
+ * building the sessions directly: the encoder half (conv stem, embed_positions,
+ * model.encoder.layers.{i}.{self_attn_layer_norm, self_attn.{q,k,v,out}_proj,
+ * final_layer_norm, fc1, fc2}, model.encoder.layer_norm) into an encoder
+ * session with its stem set, and the decoder half (embed_tokens,
+ * embed_positions, model.decoder.layers.{i}.{self_attn..., encoder_attn...,
+ * fc1, fc2}, model.decoder.layer_norm) into a decoder session. Tensors are
+ * checked in the reference's order with its shapes (PyTorch order) and
+ * messages ("whisper weight `<name>`: missing from GGUF", "... shape [..] !=
+ * expected [..]"). A Linear whose ggml type equals wdtype goes to the session
+ * from the mapping; an F32/F16 Linear is packed when wdtype is Q8_0, Q4_0 or
+ * Q5_0; anything else is UNSUPPORTED_OP naming the tensor. report may be NULL. */
+int vokra_hip_whisper_encoder_from_gguf(vokra_hip_ctx_t *ctx, const vokra_hip_gguf_t *f,
+                                        const vokra_hip_whisper_config_t *cfg, int wdtype, size_t max_rows,
+                                        vokra_hip_whisper_load_report_t *report, vokra_hip_encoder_t **out);
+int vokra_hip_whisper_decoder_from_gguf(vokra_hip_ctx_t *ctx, const vokra_hip_gguf_t *f,
+                                        const vokra_hip_whisper_config_t *cfg, int wdtype, size_t n_stream,
+                                        size_t block_size, vokra_hip_whisper_load_report_t *report,
+                                        vokra_hip_decoder_t **out);
 
 /* ---- speech-LLM text decoder (Voxtral-style backbone) ------------------- */
 

@@ -1,6 +1,7 @@
 """Block-quant weights loaded straight from a GGUF mapping give the same GEMM
 outputs, bit for bit, as the same wire bytes uploaded directly, on both the
-prefill (block GEMM) and decode (M <= 64) kernels."""
+prefill (block GEMM) and decode (M <= 64) kernels. Dims are [out, in], as the
+reference's Whisper loader reads a Linear weight."""
 import numpy as np
 import pytest
 
@@ -28,7 +29,7 @@ def test_gguf_weights_match_direct_upload(ctx, oracle, tmp_path):
         "q5": (hip.WDtype.Q5_0, ctx.quantize_bytes(hip.KvQuant.Q5_0, w)),
         "qk": (hip.WDtype.Q4_K, oracle.kquant_quantize(12, w.reshape(-1))),
     }
-    tensors = [(f"blk.0.{name}.weight", [k, n], int(wd), bytes(np.asarray(b, np.uint8)))
+    tensors = [(f"blk.0.{name}.weight", [n, k], int(wd), bytes(np.asarray(b, np.uint8)))
                for name, (wd, b) in wires.items()]
     path = tmp_path / "w.gguf"
     path.write_bytes(gw.build([("general.architecture", gw.STRING, "whisper")], tensors, alignment=64))

@@ -21,6 +21,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -40,8 +41,9 @@ struct Meta {
     int64_t i = 0;           // integer types and bool
     double f = 0.0;          // float types
     std::string s;           // string
-    uint64_t array_len = 0;  // arrays: element count (elements are skipped)
+    uint64_t array_len = 0;  // arrays: element count
     int array_type = -1;
+    std::vector<int64_t> ints;  // top-level arrays of integers: the elements
 };
 
 struct Tensor {
@@ -148,10 +150,12 @@ int read_value(Reader& r, int t, int depth, Meta* m) {
         if (len > r.remaining()) return fail(VOKRA_HIP_ERROR_MODEL_LOAD, "gguf: truncated (array length exceeds file size)");
         m->array_len = len;
         m->array_type = (int)et;
+        const bool keep = depth == 0 && (et <= 5 || et == 10 || et == 11);
         Meta e;
         for (uint64_t i = 0; i < len; ++i) {
             int st = read_value(r, (int)et, depth + 1, &e);
             if (st) return st;
+            if (keep) m->ints.push_back(e.i);
         }
         return VOKRA_HIP_OK;
     }
@@ -371,8 +375,9 @@ int vokra_hip_gguf_upload_qweight(vokra_hip_ctx_t* c, const vokra_hip_gguf_t* f,
                     t->type);
     if (t->dims.size() != 2)
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gguf: weight '%s' must be 2-D, has %zu dims", name, t->dims.size());
-    // ggml order: dims[0] = row length (in features), dims[1] = rows (out features)
-    const size_t k = (size_t)t->dims[0], n = (size_t)t->dims[1];
+    // dims as the reference's loader reads a Linear weight (whisper/weights.rs:460-470):
+    // [out_features, in_features], rows of in_features values back to back
+    const size_t n = (size_t)t->dims[0], k = (size_t)t->dims[1];
     return vokra_hip_qweight_upload(c, (int)t->type, n, k, f->base + f->data_offset + t->offset, (size_t)t->nbytes, out);
 }
 
@@ -394,6 +399,304 @@ int vokra_hip_gguf_read_f32(const vokra_hip_gguf_t* f, const char* name, float* 
             out[i] = f16_to_f32(h);
         }
     }
+    return VOKRA_HIP_OK;
+}
+
+}  // extern "C"
+
+// ---- Whisper sessions straight from a GGUF file ------------------------------
+//
+// WhisperConfig::from_gguf (crates/vokra-models/src/whisper/config.rs:106-170)
+// and WhisperWeights::load_with (whisper/weights.rs:302-378) with
+// fused_quant_weights: the tensor names, the expected shapes (PyTorch order,
+// [out_features, in_features] for a Linear) and the order in which they are
+// checked follow the reference, so the first bad tensor is the one it names.
+// A Linear already in the session's block dtype is handed to the session
+// straight from the mapping; an F32/F16 Linear is packed to Q8_0/Q4_0/Q5_0 on
+// the device (pack_matrix_to_bytes, kv_quant/dequant_gemm.rs:137-186).
+// Norms, biases, embeddings and the conv stem decode to f32.
+
+namespace {
+
+bool unsigned_meta(int t) { return t == 0 || t == 2 || t == 4 || t == 10; }
+
+int cfg_bad(const char* fmt, ...) {
+    char buf[400];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    return fail(VOKRA_HIP_ERROR_MODEL_LOAD, "whisper config: %s", buf);
+}
+
+int req_u32(const vokra_hip_gguf* f, const char* key, size_t* out) {
+    const Meta* m = find_meta(f, key);
+    if (!m) return cfg_bad("missing metadata key `%s`", key);
+    if (!unsigned_meta(m->type) || (uint64_t)m->i > UINT32_MAX)
+        return cfg_bad("metadata key `%s` is not a u32-range integer", key);
+    *out = (size_t)(uint64_t)m->i;
+    return VOKRA_HIP_OK;
+}
+
+// A u32 array's length after checking its elements (config.rs:189-203).
+int req_u32_array(const vokra_hip_gguf* f, const char* key, size_t* len) {
+    const Meta* m = find_meta(f, key);
+    if (!m) return cfg_bad("missing metadata key `%s`", key);
+    if (m->type != 9) return cfg_bad("metadata key `%s` is not an array", key);
+    if (!unsigned_meta(m->array_type) && m->array_len) return cfg_bad("`%s` element is not a u32-range integer", key);
+    for (int64_t v : m->ints)
+        if ((uint64_t)v > UINT32_MAX) return cfg_bad("`%s` element is not a u32-range integer", key);
+    *len = (size_t)m->array_len;
+    return VOKRA_HIP_OK;
+}
+
+// The optional (layer, head) pairs (config.rs:205-240): absent is fine,
+// anything present must be an even-length unsigned array of in-range layers.
+int opt_pair_array(const vokra_hip_gguf* f, const char* key, size_t n_layer) {
+    const Meta* m = find_meta(f, key);
+    if (!m) return VOKRA_HIP_OK;
+    if (m->type != 9) return cfg_bad("metadata key `%s` is not an array", key);
+    if (m->array_len % 2)
+        return cfg_bad("`%s` must be an even-length (layer, head) pair array, got %llu", key,
+                       (unsigned long long)m->array_len);
+    if (!unsigned_meta(m->array_type) && m->array_len) return cfg_bad("`%s` element is not a usize-range integer", key);
+    for (size_t i = 0; i + 1 < m->ints.size(); i += 2)
+        if ((uint64_t)m->ints[i] >= n_layer)
+            return cfg_bad("`%s` layer index %llu >= n_text_layer %zu", key, (unsigned long long)(uint64_t)m->ints[i],
+                           n_layer);
+    return VOKRA_HIP_OK;
+}
+
+std::string dims_str(const uint64_t* d, size_t n) {
+    std::string s = "[";
+    for (size_t i = 0; i < n; ++i) {
+        if (i) s += ", ";
+        s += std::to_string((unsigned long long)d[i]);
+    }
+    return s + "]";
+}
+
+int weight_err(int code, const std::string& name, const char* fmt, ...) {
+    char buf[400];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    return fail(code, "whisper weight `%s`: %s", name.c_str(), buf);
+}
+
+// Checks presence and shape as weights.rs:400-410 `tensor` does.
+int shaped(const vokra_hip_gguf* f, const std::string& name, std::initializer_list<uint64_t> want, const Tensor** out) {
+    const Tensor* t = find(f, name.c_str());
+    if (!t) return weight_err(VOKRA_HIP_ERROR_MODEL_LOAD, name, "missing from GGUF");
+    const std::vector<uint64_t> w(want);
+    if (t->dims != w)
+        return weight_err(VOKRA_HIP_ERROR_MODEL_LOAD, name, "shape %s != expected %s",
+                          dims_str(t->dims.data(), t->dims.size()).c_str(), dims_str(w.data(), w.size()).c_str());
+    *out = t;
+    return VOKRA_HIP_OK;
+}
+
+// Owns the f32 decodes and packed weights until the session has uploaded them.
+struct Loader {
+    vokra_hip_ctx_t* ctx;
+    const vokra_hip_gguf* f;
+    int wdtype;
+    std::vector<std::vector<float>> floats;
+    std::vector<std::vector<uint8_t>> packed;
+    size_t verbatim = 0, n_packed = 0;
+
+    int f32(const std::string& name, std::initializer_list<uint64_t> want, const float** out) {
+        const Tensor* t;
+        int st = shaped(f, name, want, &t);
+        if (st) return st;
+        if (t->type != 0 && t->type != 1)
+            return weight_err(VOKRA_HIP_ERROR_UNSUPPORTED_OP, name, "ggml type %u where F32 or F16 is needed", t->type);
+        const size_t n = (size_t)t->nbytes / (t->type == 0 ? 4 : 2);
+        floats.emplace_back(n);
+        if ((st = vokra_hip_gguf_read_f32(f, name.c_str(), floats.back().data(), n))) return st;
+        *out = floats.back().data();
+        return VOKRA_HIP_OK;
+    }
+
+    // linear_with (weights.rs:439-521): bias first, then the [out, in] weight.
+    int linear(const std::string& prefix, size_t in, size_t outf, bool has_bias, const uint8_t** w, const float** b) {
+        int st;
+        *b = nullptr;
+        if (has_bias && (st = f32(prefix + ".bias", {outf}, b))) return st;
+        const std::string wname = prefix + ".weight";
+        const Tensor* t;
+        if ((st = shaped(f, wname, {outf, in}, &t))) return st;
+        if ((int)t->type == wdtype) {
+            const size_t be = wdtype == VOKRA_HIP_W_Q4_K ? 256 : 32;
+            if (in % be)
+                return weight_err(VOKRA_HIP_ERROR_UNSUPPORTED_OP, wname,
+                                  "in_features %zu is not a multiple of %zu, so a block would straddle two rows", in, be);
+            *w = f->base + f->data_offset + t->offset;
+            ++verbatim;
+            return VOKRA_HIP_OK;
+        }
+        const char* names[] = {"F32", "F16", "Q4_0", "", "", "", "Q5_0", "", "Q8_0", "", "", "", "Q4_K"};
+        const int mode = wdtype == VOKRA_HIP_W_Q8_0 ? VOKRA_HIP_KV_Q8_0
+                         : wdtype == VOKRA_HIP_W_Q4_0 ? VOKRA_HIP_KV_Q4_0
+                         : wdtype == VOKRA_HIP_W_Q5_0 ? VOKRA_HIP_KV_Q5_0 : -1;
+        if ((t->type != 0 && t->type != 1) || mode < 0)
+            return weight_err(VOKRA_HIP_ERROR_UNSUPPORTED_OP, wname,
+                              "%s on disk, and the session's %s weights cannot be made from it (same block dtype, or "
+                              "F32/F16 packed to Q8_0 / Q4_0 / Q5_0)",
+                              names[t->type], names[wdtype]);
+        if (in % 32)
+            return weight_err(VOKRA_HIP_ERROR_UNSUPPORTED_OP, wname,
+                              "in_features %zu is not a multiple of 32, so its rows cannot be packed to %s blocks", in,
+                              names[wdtype]);
+        std::vector<float> x(in * outf);
+        if ((st = vokra_hip_gguf_read_f32(f, wname.c_str(), x.data(), x.size()))) return st;
+        const size_t bb = wdtype == VOKRA_HIP_W_Q8_0 ? 34 : wdtype == VOKRA_HIP_W_Q4_0 ? 18 : 22;
+        packed.emplace_back(x.size() / 32 * bb);
+        if ((st = vokra_hip_quantize_bytes(ctx, mode, x.data(), x.size(), packed.back().data(), packed.back().size())))
+            return st;
+        *w = packed.back().data();
+        ++n_packed;
+        return VOKRA_HIP_OK;
+    }
+
+    // attention_with (weights.rs:540-552): k_proj has no bias.
+    int attention(const std::string& p, size_t d, const uint8_t** wq, const uint8_t** wk, const uint8_t** wv,
+                  const uint8_t** wo, const float** bq, const float** bk, const float** bv, const float** bo) {
+        int st;
+        if ((st = linear(p + ".q_proj", d, d, true, wq, bq))) return st;
+        if ((st = linear(p + ".k_proj", d, d, false, wk, bk))) return st;
+        if ((st = linear(p + ".v_proj", d, d, true, wv, bv))) return st;
+        return linear(p + ".out_proj", d, d, true, wo, bo);
+    }
+
+    int layer_norm(const std::string& p, size_t d, const float** g, const float** b) {
+        int st = f32(p + ".weight", {d}, g);
+        return st ? st : f32(p + ".bias", {d}, b);
+    }
+
+    void report(vokra_hip_whisper_load_report_t* r) const {
+        if (r) {
+            r->verbatim = verbatim;
+            r->packed = n_packed;
+        }
+    }
+};
+
+bool whisper_wdtype(int w) {
+    return w == VOKRA_HIP_W_Q8_0 || w == VOKRA_HIP_W_Q4_0 || w == VOKRA_HIP_W_Q5_0 || w == VOKRA_HIP_W_Q4_K;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vokra_hip_whisper_config_from_gguf(const vokra_hip_gguf_t* f, vokra_hip_whisper_config_t* cfg) {
+    if (!f || !cfg) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "whisper_config_from_gguf: NULL argument");
+    vokra_hip_whisper_config_t c{};
+    size_t n_text_state = 0, eot = 0, n_start = 0;
+    int st;
+    if ((st = req_u32(f, "vokra.whisper.n_mels", &c.n_mels)) || (st = req_u32(f, "vokra.whisper.n_audio_state", &c.d_model)) ||
+        (st = req_u32(f, "vokra.whisper.n_text_state", &n_text_state)) ||
+        (st = req_u32(f, "vokra.whisper.n_audio_ctx", &c.n_audio_ctx)) ||
+        (st = req_u32(f, "vokra.whisper.n_audio_head", &c.n_audio_head)) ||
+        (st = req_u32(f, "vokra.whisper.n_audio_layer", &c.n_audio_layer)) ||
+        (st = req_u32(f, "vokra.whisper.n_text_ctx", &c.n_text_ctx)) ||
+        (st = req_u32(f, "vokra.whisper.n_text_head", &c.n_text_head)) ||
+        (st = req_u32(f, "vokra.whisper.n_text_layer", &c.n_text_layer)) ||
+        (st = req_u32(f, "vokra.whisper.n_vocab", &c.n_vocab)) || (st = req_u32(f, "vokra.whisper.ffn_dim", &c.ffn_dim)) ||
+        (st = req_u32(f, "vokra.whisper.eot", &eot)) ||
+        (st = req_u32_array(f, "vokra.whisper.decoder_start_ids", &n_start)) ||
+        (st = opt_pair_array(f, "vokra.whisper.alignment_heads", c.n_text_layer)))
+        return st;
+    if (n_text_state != c.d_model)
+        return cfg_bad("n_text_state (%zu) != n_audio_state (%zu); Whisper shares d_model across encoder and decoder",
+                       n_text_state, c.d_model);
+    if (c.n_audio_head == 0 || c.d_model % c.n_audio_head)
+        return cfg_bad("n_audio_head (%zu) must divide d_model (%zu)", c.n_audio_head, c.d_model);
+    if (c.n_text_head == 0 || c.d_model % c.n_text_head)
+        return cfg_bad("n_text_head (%zu) must divide d_model (%zu)", c.n_text_head, c.d_model);
+    if (!c.n_mels || !c.n_audio_ctx || !c.n_audio_layer || !c.n_text_ctx || !c.n_text_layer || !c.n_vocab || !c.ffn_dim)
+        return cfg_bad("a required Whisper hyperparameter was zero");
+    if (!n_start) return cfg_bad("decoder_start_ids must not be empty");
+    c.eot = (uint32_t)eot;
+    *cfg = c;
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_whisper_encoder_from_gguf(vokra_hip_ctx_t* ctx, const vokra_hip_gguf_t* f,
+                                        const vokra_hip_whisper_config_t* cfg, int wdtype, size_t max_rows,
+                                        vokra_hip_whisper_load_report_t* report, vokra_hip_encoder_t** out) {
+    if (!ctx || !f || !cfg || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "whisper_encoder_from_gguf: NULL argument");
+    *out = nullptr;
+    if (!whisper_wdtype(wdtype)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "whisper_encoder_from_gguf: unknown weight dtype %d", wdtype);
+    const size_t d = cfg->d_model, ff = cfg->ffn_dim;
+    Loader L{ctx, f, wdtype};
+    const float *c1w, *c1b, *c2w, *c2b, *pos, *lg, *lb;
+    int st;
+    if ((st = L.f32("model.encoder.conv1.weight", {d, cfg->n_mels, 3}, &c1w)) ||
+        (st = L.f32("model.encoder.conv1.bias", {d}, &c1b)) || (st = L.f32("model.encoder.conv2.weight", {d, d, 3}, &c2w)) ||
+        (st = L.f32("model.encoder.conv2.bias", {d}, &c2b)) ||
+        (st = L.f32("model.encoder.embed_positions.weight", {cfg->n_audio_ctx, d}, &pos)))
+        return st;
+    std::vector<vokra_hip_prenorm_layer_t> layers(cfg->n_audio_layer);
+    for (size_t i = 0; i < cfg->n_audio_layer; ++i) {
+        const std::string p = "model.encoder.layers." + std::to_string(i);
+        vokra_hip_prenorm_layer_t& y = layers[i];
+        if ((st = L.layer_norm(p + ".self_attn_layer_norm", d, &y.ln1_gamma, &y.ln1_beta)) ||
+            (st = L.attention(p + ".self_attn", d, &y.wq, &y.wk, &y.wv, &y.wo, &y.bq, &y.bk, &y.bv, &y.bo)) ||
+            (st = L.layer_norm(p + ".final_layer_norm", d, &y.ln2_gamma, &y.ln2_beta)) ||
+            (st = L.linear(p + ".fc1", d, ff, true, &y.w1, &y.b1)) || (st = L.linear(p + ".fc2", ff, d, true, &y.w2, &y.b2)))
+            return st;
+    }
+    if ((st = L.layer_norm("model.encoder.layer_norm", d, &lg, &lb))) return st;
+    vokra_hip_encoder_t* enc = nullptr;
+    if ((st = vokra_hip_encoder_create(ctx, wdtype, cfg->n_audio_layer, d, cfg->n_audio_head, ff, layers.data(), lg, lb,
+                                       max_rows, &enc)))
+        return st;
+    if ((st = vokra_hip_encoder_set_stem(ctx, enc, cfg->n_mels, 2 * cfg->n_audio_ctx, c1w, c1b, c2w, c2b, pos))) {
+        vokra_hip_encoder_destroy(enc);
+        return st;
+    }
+    L.report(report);
+    *out = enc;
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_whisper_decoder_from_gguf(vokra_hip_ctx_t* ctx, const vokra_hip_gguf_t* f,
+                                        const vokra_hip_whisper_config_t* cfg, int wdtype, size_t n_stream,
+                                        size_t block_size, vokra_hip_whisper_load_report_t* report,
+                                        vokra_hip_decoder_t** out) {
+    if (!ctx || !f || !cfg || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "whisper_decoder_from_gguf: NULL argument");
+    *out = nullptr;
+    if (!whisper_wdtype(wdtype)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "whisper_decoder_from_gguf: unknown weight dtype %d", wdtype);
+    const size_t d = cfg->d_model, ff = cfg->ffn_dim;
+    Loader L{ctx, f, wdtype};
+    const float *tok, *pos, *lg, *lb;
+    int st;
+    if ((st = L.f32("model.decoder.embed_tokens.weight", {cfg->n_vocab, d}, &tok)) ||
+        (st = L.f32("model.decoder.embed_positions.weight", {cfg->n_text_ctx, d}, &pos)))
+        return st;
+    std::vector<vokra_hip_decoder_layer_t> layers(cfg->n_text_layer);
+    for (size_t i = 0; i < cfg->n_text_layer; ++i) {
+        const std::string p = "model.decoder.layers." + std::to_string(i);
+        vokra_hip_decoder_layer_t& y = layers[i];
+        if ((st = L.layer_norm(p + ".self_attn_layer_norm", d, &y.ln1_gamma, &y.ln1_beta)) ||
+            (st = L.attention(p + ".self_attn", d, &y.wq, &y.wk, &y.wv, &y.wo, &y.bq, &y.bk, &y.bv, &y.bo)) ||
+            (st = L.layer_norm(p + ".encoder_attn_layer_norm", d, &y.ln2_gamma, &y.ln2_beta)) ||
+            (st = L.attention(p + ".encoder_attn", d, &y.cwq, &y.cwk, &y.cwv, &y.cwo, &y.cbq, &y.cbk, &y.cbv, &y.cbo)) ||
+            (st = L.layer_norm(p + ".final_layer_norm", d, &y.ln3_gamma, &y.ln3_beta)) ||
+            (st = L.linear(p + ".fc1", d, ff, true, &y.w1, &y.b1)) || (st = L.linear(p + ".fc2", ff, d, true, &y.w2, &y.b2)))
+            return st;
+    }
+    if ((st = L.layer_norm("model.decoder.layer_norm", d, &lg, &lb))) return st;
+    vokra_hip_decoder_t* dec = nullptr;
+    if ((st = vokra_hip_decoder_create(ctx, wdtype, cfg->n_text_layer, d, cfg->n_text_head, ff, cfg->n_vocab,
+                                       cfg->n_text_ctx, cfg->n_audio_ctx, n_stream, block_size, layers.data(), tok, pos,
+                                       lg, lb, &dec)))
+        return st;
+    L.report(report);
+    *out = dec;
     return VOKRA_HIP_OK;
 }
 

@@ -104,6 +104,18 @@ class DecoderLayer(C.Structure):
                 ("w1", _U8), ("w2", _U8), ("b1", _F), ("b2", _F)]
 
 
+class WhisperConfig(C.Structure):
+    """vokra_hip_whisper_config_t (whisper/config.rs WhisperConfig)."""
+    _fields_ = [(n, C.c_size_t) for n in ("n_mels", "d_model", "n_audio_ctx", "n_audio_head", "n_audio_layer",
+                                          "n_text_ctx", "n_text_head", "n_text_layer", "n_vocab", "ffn_dim")] + \
+               [("eot", C.c_uint32)]
+
+
+class WhisperLoadReport(C.Structure):
+    """vokra_hip_whisper_load_report_t: Linear weights taken verbatim / packed at load."""
+    _fields_ = [("verbatim", C.c_size_t), ("packed", C.c_size_t)]
+
+
 class TextDecoderLayer(C.Structure):
     """vokra_hip_text_decoder_layer_t"""
     _fields_ = [("attn_norm_gamma", _F), ("wq", _U8), ("wk", _U8), ("wv", _U8), ("wo", _U8),
@@ -216,6 +228,11 @@ def _declare(L):
     L.vokra_hip_gguf_meta_str.argtypes = [P, C.c_char_p, C.POINTER(C.c_char_p), C.POINTER(sz)]
     L.vokra_hip_gguf_upload_qweight.argtypes = [P, P, C.c_char_p, C.POINTER(P)]
     L.vokra_hip_gguf_read_f32.argtypes = [P, C.c_char_p, f32p, sz]
+    L.vokra_hip_whisper_config_from_gguf.argtypes = [P, C.POINTER(WhisperConfig)]
+    L.vokra_hip_whisper_encoder_from_gguf.argtypes = [P, P, C.POINTER(WhisperConfig), C.c_int, sz,
+                                                      C.POINTER(WhisperLoadReport), C.POINTER(P)]
+    L.vokra_hip_whisper_decoder_from_gguf.argtypes = [P, P, C.POINTER(WhisperConfig), C.c_int, sz, sz,
+                                                      C.POINTER(WhisperLoadReport), C.POINTER(P)]
     L.vokra_hip_log_mel.argtypes = [P, f32p, sz, sz, sz, f32p, sz]
     L.vokra_hip_log_mel_dev.argtypes = [P, P, sz, sz, sz, P]
     L.vokra_hip_conv1d_f32.argtypes = [P, f32p, sz, sz, sz, f32p, sz, sz, sz, f32p, sz, sz, f32p, sz]
@@ -457,13 +474,19 @@ class GgufFile:
         return out[:n]
 
     def upload_qweight(self, ctx, name) -> "QWeight":
-        """vokra_hip_gguf_upload_qweight: the named [in, out] block-quant tensor as a resident weight."""
+        """vokra_hip_gguf_upload_qweight: the named [out, in] block-quant tensor as a resident weight."""
         p = C.c_void_p()
         _check(lib().vokra_hip_gguf_upload_qweight(ctx._h, self._h, name.encode(), C.byref(p)))
         _, t, dims, _ = self.tensor(self.find(name))
         w = QWeight.__new__(QWeight)
-        w.ctx, w.wdtype, w.n, w.k, w._h = ctx, WDtype(t), dims[1], dims[0], p
+        w.ctx, w.wdtype, w.n, w.k, w._h = ctx, WDtype(t), dims[0], dims[1], p
         return w
+
+    def whisper_config(self) -> dict:
+        """WhisperConfig::from_gguf (whisper/config.rs:106-170); no GPU is touched."""
+        c = WhisperConfig()
+        _check(lib().vokra_hip_whisper_config_from_gguf(self._h, C.byref(c)))
+        return {n: getattr(c, n) for n, _ in WhisperConfig._fields_}
 
 
 class Graph:
@@ -629,6 +652,21 @@ class Encoder:
                                               _ptr(g, C.c_float), _ptr(b, C.c_float), max_rows, C.byref(h)))
         self._h = h
 
+    @classmethod
+    def from_gguf(cls, ctx, gguf, wdtype, max_rows):
+        """vokra_hip_whisper_encoder_from_gguf: the encoder half of WhisperWeights::load_with
+        (whisper/weights.rs:302-333) as a session with its stem set. Returns (encoder, report)."""
+        cfg = WhisperConfig()
+        _check(lib().vokra_hip_whisper_config_from_gguf(gguf._h, C.byref(cfg)))
+        rep, h = WhisperLoadReport(), C.c_void_p()
+        _check(lib().vokra_hip_whisper_encoder_from_gguf(ctx._h, gguf._h, C.byref(cfg), int(wdtype), max_rows,
+                                                         C.byref(rep), C.byref(h)))
+        enc = cls.__new__(cls)
+        enc._ctx, enc.d, enc._h = ctx, cfg.d_model, h
+        enc.n_mels, enc.n_frames = cfg.n_mels, 2 * cfg.n_audio_ctx
+        enc.n_ctx = (enc.n_frames - 1) // 2 + 1
+        return enc, {"verbatim": rep.verbatim, "packed": rep.packed}
+
     def forward(self, x):
         xv = _f32(x)
         B, T, _ = xv.shape
@@ -687,6 +725,19 @@ class Decoder:
                                               _ptr(te, C.c_float), _ptr(pe, C.c_float), _ptr(g, C.c_float),
                                               _ptr(b, C.c_float), C.byref(h)))
         self._h = h
+
+    @classmethod
+    def from_gguf(cls, ctx, gguf, wdtype, n_stream, block_size=16):
+        """vokra_hip_whisper_decoder_from_gguf: the decoder half of WhisperWeights::load_with
+        (whisper/weights.rs:335-357) as a batched session. Returns (decoder, report)."""
+        cfg = WhisperConfig()
+        _check(lib().vokra_hip_whisper_config_from_gguf(gguf._h, C.byref(cfg)))
+        rep, h = WhisperLoadReport(), C.c_void_p()
+        _check(lib().vokra_hip_whisper_decoder_from_gguf(ctx._h, gguf._h, C.byref(cfg), int(wdtype), n_stream,
+                                                         block_size, C.byref(rep), C.byref(h)))
+        dec = cls.__new__(cls)
+        dec._ctx, dec.vocab, dec.d, dec.n_audio, dec._h = ctx, cfg.n_vocab, cfg.d_model, cfg.n_audio_ctx, h
+        return dec, {"verbatim": rep.verbatim, "packed": rep.packed}
 
     def set_encoder(self, stream, enc):
         e = _f32(enc)
