@@ -345,9 +345,9 @@ int run_gemm_qact(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_
     if (w->kquant) {
         if (qa->act_quant != VOKRA_HIP_ACT_KQUANT)
             return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: Q4_K weights need KQUANT activations");
+        const VkQ4kLin lin = {(const uint4*)w->gq.p, (const float2*)w->gsc.p, d_bias, d_out, epi, (int)w->n};
         VK_TRY(vk::launch_gemm_q4k(c->stream, (const uint4*)qa->frag.p, (const float*)qa->scale.p,
-                                   (const float*)qa->gsum.p, (const uint4*)w->gq.p, (const float2*)w->gsc.p, d_bias,
-                                   d_out, (int)qa->m, (int)w->n, (int)w->nb, (int)qa->m_pad, epi),
+                                   (const float*)qa->gsum.p, &lin, 1, (int)qa->m, (int)w->nb, (int)qa->m_pad),
                "launch(vk_gemm_q4k)");
         return VOKRA_HIP_OK;
     }
@@ -556,6 +556,19 @@ int gemm_qact_multi(vokra_hip_ctx* c, int n, const vokra_hip_qweight* const* ws,
                      qa->act_quant != VOKRA_HIP_ACT_KQUANT;
     }
     VK_TRY(set_dev(c), "hipSetDevice");
+    bool q4k_all = qa->act_quant == VOKRA_HIP_ACT_KQUANT;
+    for (int i = 0; i < n && q4k_all; ++i) q4k_all = ws[i]->kquant && ws[i]->nb == ws[0]->nb;
+    if (q4k_all && n > 1) {
+        // K-quant linears over the same activations: one grid
+        VkQ4kLin lins[3];
+        for (int i = 0; i < n; ++i)
+            lins[i] = {(const uint4*)ws[i]->gq.p, (const float2*)ws[i]->gsc.p, biases ? biases[i] : nullptr, outs[i],
+                       {nullptr, 0}, (int)ws[i]->n};
+        VK_TRY(vk::launch_gemm_q4k(c->stream, (const uint4*)qa->frag.p, (const float*)qa->scale.p,
+                                   (const float*)qa->gsum.p, lins, n, (int)qa->m, (int)ws[0]->nb, (int)qa->m_pad),
+               "launch(vk_gemm_q4k x n)");
+        return VOKRA_HIP_OK;
+    }
     if (!one_launch) {
         // block formats of one width on the prefill route: one block-GEMM grid
         bool one_gemm = qa->act_quant != VOKRA_HIP_ACT_KQUANT;

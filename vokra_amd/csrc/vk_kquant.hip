@@ -71,7 +71,8 @@ __global__ void vk_dequantize_q4k(const uint8_t* __restrict__ bytes, size_t nsb,
 //          (16-row tile mt, super-block sb, group pair gp) 64 lanes x 16 bytes:
 //          lane l = row % 16 + 16 c holds K 4c..4c+3 of group 2gp (bytes 0..7)
 //          and of group 2gp + 1 (bytes 8..15);
-//   ascale[g * m_pad + row] = s, asum[g * m_pad + row] = (float) gsum.
+//   ascale / asum: per run of 4 groups (g / 4), per row, the 4 groups' s and
+//          (float) gsum back to back: index ((g / 4) * m_pad + row) * 4 + g % 4.
 // Rows m..m_pad-1 are written as zeros.
 __global__ void vk_quantize_act_g16(const float* __restrict__ a, int m, int m_pad, int k,
                                     uint2* __restrict__ afrag, float* __restrict__ ascale,
@@ -119,8 +120,9 @@ __global__ void vk_quantize_act_g16(const float* __restrict__ a, int m, int m_pa
                                    vk_int_to_bf16_bits(r[4 * c + 2]) | (vk_int_to_bf16_bits(r[4 * c + 3]) << 16));
         afrag[base + (size_t)lane * 2] = w;
     }
-    ascale[(size_t)g * m_pad + row] = s;
-    asum[(size_t)g * m_pad + row] = (float)gsum;
+    const size_t si = ((size_t)(g >> 2) * m_pad + row) * 4 + (g & 3);
+    ascale[si] = s;
+    asum[si] = (float)gsum;
 }
 
 // ---------------------------------------------------------------------------
@@ -192,71 +194,76 @@ __device__ __forceinline__ vk_s16x4 q4k_operand(uint32_t w, int j0) {
 // one group alone. So:
 //   phase 1 (chunk c+1): wave w takes 4 groups of the chunk; per group one
 //     16x16x16 MFMA with accumulator input -128 * gsum (removing the +128 of
-//     the bf16 nibble trick) gives isum exactly for 4 outputs per lane, and
-//     the lane turns them into the 4 terms with the reference's roundings;
-//     the terms go to the LDS buffer of chunk c+1;
-//   phase 2 (chunk c): thread (row, col) of waves 0..3 adds the chunk's 32
-//     terms of its output to acc, in group order;
+//     the bf16 nibble trick) gives isum exactly for 4 outputs per lane (the
+//     4 MFMAs are issued before any of their results is used), and the lane
+//     turns them into the 4 terms with the reference's roundings; the terms
+//     go to the LDS buffer of chunk c+1;
+//   phase 2 (chunk c): thread t of waves 0..3 adds the chunk's 32 terms of
+//     its output to acc, in group order;
 //   one barrier per chunk: chunk c+1's terms are complete, chunk c's free.
+// Term buffer layout per group: output (row, col) at (col / 4) * 64 + row * 4
+// + col % 4, so a wave's float4 stores (lane l: row l % 16, cols 4 (l / 16)
+// ..+3) cover 256 consecutive floats and phase 2's thread t reads float t:
+// no bank conflicts on either side.
 // Operands are loaded two chunks ahead into two register sets, each load a
 // wave-uniform base plus a 32-bit lane offset (a chunk past the end loads the
-// last super-block again, unused). Outputs are bit-identical to
-// kquant_gemm_i8: the same terms, added in the same order.
+// last super-block again, unused). Up to three linears over the same
+// activations share one grid (blockIdx.x runs over their column tiles in
+// turn). Outputs are bit-identical to kquant_gemm_i8: the same terms, added
+// in the same order.
 namespace kq {
 constexpr int CHG = 32;  // groups per chunk (two super-blocks)
 constexpr int CHS = 2;   // super-blocks per chunk
 struct Pipe {
     uint2 wv;            // nibble words of this wave's 4 groups
     uint4 af[2];         // activation fragments of its 4 groups (2 pairs)
-    float s[4], a[4];    // s and gsum of this lane's row, per group
+    float4 s, a;         // s and gsum of this lane's row for its 4 groups
     float4 dm[2][2];     // [sub-block][half]: (d_eff, m_eff) of cols rq + 2 half, +1
 };
 }  // namespace kq
 
-template <bool HAS_BIAS>
-__global__ __launch_bounds__(512) void vk_gemm_q4k(
-    const uint4* __restrict__ afrag, const float* __restrict__ ascale, const float* __restrict__ asum,
-    const uint4* __restrict__ wq4, const float2* __restrict__ wdm, const float* __restrict__ bias, VkEpi epi,
-    float* out, int m, int n, int nsb, int m_pad) {
+__global__ __launch_bounds__(512) void vk_gemm_q4k(const uint4* __restrict__ afrag, const float* __restrict__ ascale,
+                                                   const float* __restrict__ asum, VkQ4kSet set, int m, int nsb,
+                                                   int m_pad) {
     using namespace kq;
-    __shared__ __align__(16) float lds_t[2][CHG][256];  // terms, [chunk parity][group][row * 16 + col]
+    __shared__ __align__(16) float lds_t[2][CHG][256];  // terms, [chunk parity][group][(col/4)*64 + row*4 + col%4]
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar load bases
-    const int nt = blockIdx.x, mt = blockIdx.y;
+    // this workgroup's linear (uniform selects, no indexing into the set)
+    const int bx = blockIdx.x, mt = blockIdx.y;
+    const int li = (set.count > 2 && bx >= set.tile0[2]) ? 2 : (set.count > 1 && bx >= set.tile0[1]) ? 1 : 0;
+    const VkQ4kLin L = li == 2 ? set.l[2] : li == 1 ? set.l[1] : set.l[0];
+    const int nt = bx - (li == 2 ? set.tile0[2] : li == 1 ? set.tile0[1] : 0);
     const int row_l = lane & 15, rq = 4 * (lane >> 4);  // MFMA lane: activation row, first weight column
     const int q4 = wave & 3, sbw = wave >> 2;           // this wave's quarter of a super-block, and which one
     const int n_chunk = (nsb + CHS - 1) / CHS;
-    const bool owner = wave < 4 && mt * 16 + 4 * wave < m;  // phase-2 thread with a live row
+    // phase-2 thread: waves 0..3, output (row, col) of the term layout
+    const int orow = (tid >> 2) & 15, ocol = 4 * (tid >> 6) + (tid & 3);
+    const bool owner = wave < 4;
 
     // per-lane byte offsets (constant over the K loop)
     const uint32_t vo_w = lane * 32 + 8 * q4;
     const uint32_t vo_a = lane * 16;
     const uint32_t vo_d = rq * 8;
-    uint32_t vo_s[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) vo_s[i] = (uint32_t)(i * m_pad + mt * 16 + row_l) * 4;
+    const uint32_t vo_s = (uint32_t)(mt * 16 + row_l) * 16;
 
     // chunk c's operands for this wave (super-block 2c + sbw, clamped into
     // the tensor: a super-block past the end loads the last one, unused).
-    // Each load is a wave-uniform base plus a 32-bit per-lane offset.
     auto load = [&](int c) -> Pipe {
         Pipe p;
         const int sb = min(c * CHS + sbw, nsb - 1);
-        const char* bw = reinterpret_cast<const char*>(wq4) + (size_t)((nt * nsb + sb) * 64) * 32;
+        const char* bw = reinterpret_cast<const char*>(L.wq4) + (size_t)((nt * nsb + sb) * 64) * 32;
         const char* ba = reinterpret_cast<const char*>(afrag) + (size_t)(((mt * nsb + sb) * 8 + 2 * q4) * 64) * 16;
-        const size_t so_s = (size_t)(sb * NG + 4 * q4) * m_pad * 4;
+        const size_t so_s = (size_t)(sb * (NG / 4) + q4) * m_pad * 16;
         const char* bs = reinterpret_cast<const char*>(ascale) + so_s;
         const char* bg = reinterpret_cast<const char*>(asum) + so_s;
-        const char* bd = reinterpret_cast<const char*>(wdm) + (size_t)((nt * nsb + sb) * 8 + 2 * q4) * 128;
+        const char* bd = reinterpret_cast<const char*>(L.wdm) + (size_t)((nt * nsb + sb) * 8 + 2 * q4) * 128;
         p.wv = *reinterpret_cast<const uint2*>(bw + vo_w);
 #pragma unroll
         for (int h = 0; h < 2; ++h) p.af[h] = *reinterpret_cast<const uint4*>(ba + vo_a + h * 1024);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            p.s[i] = *reinterpret_cast<const float*>(bs + vo_s[i]);
-            p.a[i] = *reinterpret_cast<const float*>(bg + vo_s[i]);
-        }
+        p.s = *reinterpret_cast<const float4*>(bs + vo_s);
+        p.a = *reinterpret_cast<const float4*>(bg + vo_s);
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
@@ -266,26 +273,30 @@ __global__ __launch_bounds__(512) void vk_gemm_q4k(
     // phase 1: the terms of this wave's 4 groups of chunk c into buffer par
     auto terms = [&](const Pipe& p, int c, int par) {
         if (c * CHS + sbw >= nsb) return;  // a chunk with one super-block: waves 4..7 idle
+        const float sv[4] = {p.s.x, p.s.y, p.s.z, p.s.w}, av[4] = {p.a.x, p.a.y, p.a.z, p.a.w};
+        vk_f32x4 isum[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t word = (i < 2) ? p.wv.x : p.wv.y;
             const vk_s16x4 w = q4k_operand(word, 2 * (i & 1));
             const uint4 a4 = p.af[i >> 1];
             const uint2 ap = (i & 1) ? make_uint2(a4.z, a4.w) : make_uint2(a4.x, a4.y);
-            const float c0 = -128.0f * p.a[i];
+            const float c0 = -128.0f * av[i];
             const vk_f32x4 cin = {c0, c0, c0, c0};
             // transposed product: weights as the A operand, so lane l gets
             // activation row l % 16, columns rq..rq+3
-            const vk_f32x4 isum =
-                __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(w, __builtin_bit_cast(vk_s16x4, ap), cin, 0, 0, 0);
+            isum[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(w, __builtin_bit_cast(vk_s16x4, ap), cin, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
             const float4 d01 = p.dm[i >> 1][0], d23 = p.dm[i >> 1][1];  // (d, m) of cols rq .. rq + 3
-            const float s = p.s[i], a = p.a[i];
+            const float s = sv[i], a = av[i];
             float4 t;
-            t.x = s * (d01.x * isum[0] - d01.y * a);
-            t.y = s * (d01.z * isum[1] - d01.w * a);
-            t.z = s * (d23.x * isum[2] - d23.y * a);
-            t.w = s * (d23.z * isum[3] - d23.w * a);
-            *reinterpret_cast<float4*>(&lds_t[par][16 * sbw + 4 * q4 + i][row_l * 16 + rq]) = t;
+            t.x = s * (d01.x * isum[i][0] - d01.y * a);
+            t.y = s * (d01.z * isum[i][1] - d01.w * a);
+            t.z = s * (d23.x * isum[i][2] - d23.y * a);
+            t.w = s * (d23.z * isum[i][3] - d23.w * a);
+            *reinterpret_cast<float4*>(&lds_t[par][16 * sbw + 4 * q4 + i][4 * lane]) = t;
         }
     };
     // phase 2: the ordered adds of chunk c (waves 0..3, one output per thread)
@@ -322,11 +333,11 @@ __global__ __launch_bounds__(512) void vk_gemm_q4k(
         chain(c + 1, 1);
         VK_LDS_BARRIER();
     }
-    if (wave < 4) {
-        const int orow = mt * 16 + (tid >> 4), ocol = nt * 16 + (tid & 15);
-        if (orow < m && ocol < n) {
-            const size_t o = (size_t)orow * n + ocol;
-            out[o] = vk_epi_apply(HAS_BIAS ? acc + bias[ocol] : acc, epi, o);
+    if (owner) {
+        const int r = mt * 16 + orow, col = nt * 16 + ocol;
+        if (r < m && col < L.n) {
+            const size_t o = (size_t)r * L.n + col;
+            L.out[o] = vk_epi_apply(L.bias ? acc + L.bias[col] : acc, L.epi, o);
         }
     }
 }
@@ -363,15 +374,18 @@ hipError_t launch_repack_w_q4k(hipStream_t s, const uint8_t* wq, int n, int n_pa
 }
 
 hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum,
-                           const uint4* wq4, const float2* wdm, const float* bias, float* out, int m, int n, int nsb,
-                           int m_pad, VkEpi epi) {
-    const dim3 grid((n + 15) / 16, (m + 15) / 16);
-    if (bias)
-        hipLaunchKernelGGL(vk_gemm_q4k<true>, grid, dim3(512), 0, s, afrag, ascale, asum, wq4, wdm, bias, epi, out, m,
-                           n, nsb, m_pad);
-    else
-        hipLaunchKernelGGL(vk_gemm_q4k<false>, grid, dim3(512), 0, s, afrag, ascale, asum, wq4, wdm, bias, epi, out, m,
-                           n, nsb, m_pad);
+                           const VkQ4kLin* lins, int n_lin, int m, int nsb, int m_pad) {
+    if (n_lin < 1 || n_lin > 3) return hipErrorInvalidValue;
+    VkQ4kSet set{};
+    int tiles = 0;
+    for (int i = 0; i < n_lin; ++i) {
+        set.l[i] = lins[i];
+        set.tile0[i] = tiles;
+        tiles += (lins[i].n + 15) / 16;
+    }
+    set.count = n_lin;
+    const dim3 grid((unsigned)tiles, (unsigned)((m + 15) / 16));
+    hipLaunchKernelGGL(vk_gemm_q4k, grid, dim3(512), 0, s, afrag, ascale, asum, set, m, nsb, m_pad);
     return hipGetLastError();
 }
 

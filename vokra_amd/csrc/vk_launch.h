@@ -42,6 +42,22 @@ struct VkGemvLin {
     VkEpi epi;
     int n;
 };
+// One linear of a Q4_K matmul launch (repacked weights, optional bias,
+// output [m, n]); up to three linears over the same activations share a grid,
+// tile0[i] being linear i's first column tile.
+struct VkQ4kLin {
+    const uint4* wq4;
+    const float2* wdm;
+    const float* bias;
+    float* out;
+    VkEpi epi;
+    int n;
+};
+struct VkQ4kSet {
+    VkQ4kLin l[3];
+    int tile0[3];
+    int count;
+};
 
 namespace vk {
 constexpr int GEMM_TM = 128;  // block GEMM padding of m (a multiple of its workgroup tile)
@@ -92,8 +108,7 @@ hipError_t launch_quantize_act_g16(hipStream_t s, const float* a, int m, int m_p
 hipError_t launch_repack_w_q4k(hipStream_t s, const uint8_t* wq, int n, int n_pad, int nsb, uint4* wq4,
                                float2* wdm);
 hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum,
-                           const uint4* wq4, const float2* wdm, const float* bias, float* out, int m, int n, int nsb,
-                           int m_pad, VkEpi epi = {nullptr, 0});
+                           const VkQ4kLin* lins, int n_lin, int m, int nsb, int m_pad);
 }  // namespace vk
 
 namespace vk {

@@ -836,9 +836,12 @@ int td_step(vokra_hip_text_decoder* m, size_t n, const int* d_streams, const int
         const TextLayer& L = m->layers[l];
         // pre-norm self-attention (text_decoder.rs:1212-1351)
         SS_TRY(td_rms_quantize(m, m->qa_d, n, m->h.f(), L.attn_g.f()));
-        SS_TRY(L.q.run(c, m->qa_d, m->q.f()));
-        SS_TRY(L.k.run(c, m->qa_d, m->k.f()));
-        SS_TRY(L.v.run(c, m->qa_d, m->v.f()));
+        {  // q, k and v over the same activations: one launch
+            const vokra_hip_qweight_t* qkv[3] = {L.q.w, L.k.w, L.v.w};
+            const float* qkv_b[3] = {L.q.b(), L.k.b(), L.v.b()};
+            float* qkv_o[3] = {m->q.f(), m->k.f(), m->v.f()};
+            SS_TRY(vk::gemm_qact_multi(c, 3, qkv, m->qa_d, qkv_b, qkv_o));
+        }
         SS_HIP(vk::launch_rope_rows(s, m->q.f(), (int)n, (int)m->hq, (int)m->hd, m->theta.f(), d_positions, 0),
                "launch(vk_rope_rows q)");
         SS_HIP(vk::launch_rope_rows(s, m->k.f(), (int)n, (int)m->hkv, (int)m->hd, m->theta.f(), d_positions, 0),
@@ -849,8 +852,12 @@ int td_step(vokra_hip_text_decoder* m, size_t n, const int* d_streams, const int
         SS_TRY(L.o.run(c, m->qa_q, m->h.f(), add_h));
         // pre-norm SwiGLU FFN (text_decoder.rs:1385-1418)
         SS_TRY(td_rms_quantize(m, m->qa_d, n, m->h.f(), L.ffn_g.f()));
-        SS_TRY(L.gate.run(c, m->qa_d, m->g.f()));
-        SS_TRY(L.up.run(c, m->qa_d, m->u.f()));
+        {  // gate and up over the same activations: one launch
+            const vokra_hip_qweight_t* gu[2] = {L.gate.w, L.up.w};
+            const float* gu_b[2] = {L.gate.b(), L.up.b()};
+            float* gu_o[2] = {m->g.f(), m->u.f()};
+            SS_TRY(vk::gemm_qact_multi(c, 2, gu, m->qa_d, gu_b, gu_o));
+        }
         SS_HIP(vk::launch_swiglu_f32(s, m->g.f(), m->u.f(), m->g.f(), n * ff), "launch(vk_swiglu_f32)");
         SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_f, n, m->g.f(), act));
         SS_TRY(L.down.run(c, m->qa_f, m->h.f(), add_h));
