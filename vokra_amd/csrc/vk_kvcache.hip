@@ -780,37 +780,61 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
     for (int et = 0; et < HD / 16; ++et) o[et] = {0.0f, 0.0f, 0.0f, 0.0f};
     const int trow = layer * c.ppl;
     const int va = lane & 7, vc = lane >> 3;  // V staging: keys 4va .. +3, dims 16vc .. +15
+    const int jfirst = k0 + KT * wave;        // this wave's tiles: jfirst + KT * WAVES * t
+    const int ntile =                         // wave-uniform: scalar branches around the loads
+        __builtin_amdgcn_readfirstlane(jfirst < k1 ? (k1 - jfirst + KT * WAVES - 1) / (KT * WAVES) : 0);
 
-    for (int j0 = k0 + KT * wave; j0 < k1; j0 += KT * WAVES) {
-        // slot of key j0 + kk, kk = lane % 32 (lanes 32..63 repeat lanes 0..31)
-        const int jk = j0 + (lane & 31);
-        const int pid = jk < k1 ? c.table[trow + jk / c.bs] : -1;
-        const int slot = pid >= 0 ? (int)kv_hrow(c, pid, jk, s, hk) : 0;  // row 0: in bounds, masked below
-        const int has = pid >= 0 ? 1 : 0;
-
-        // ---- issue every load of the tile
+    // The loads of a tile: its page-table entries one tile ahead, its K / V
+    // rows and block scales one tile ahead of the tile being computed.
+    // Lane l looks up key l % 32 (lanes 32..63 repeat lanes 0..31). Every
+    // load is issued unconditionally (tile indices clamped to the wave's last
+    // tile, keys to the split's last key), so the wait before a tile's
+    // products counts only the younger loads and the prefetch stays in flight.
+    struct Tile {
         uint2 kw[2][NB];  // K operand rows: subtile n, row hh <-> key 8 (hh / 4) + 4 n + hh % 4
+        uint4 vw[4];      // V rows of keys 4va + t, dims 16vc .. +15
+        uint2 kd, vd;     // f16 block scales of key lane % 32
+        int has;          // key lane % 32 is cached
+    };
+    // the raw table entry of key lane % 32 of tile t (the key clamped into
+    // the split); load_tile masks keys past the split, so nothing here waits
+    auto page_of = [&](int t) -> int {
+        const int jk = jfirst + KT * WAVES * t + (lane & 31);
+        return c.table[trow + min(jk, k1 - 1) / c.bs];
+    };
+    auto load_tile = [&](int t, int raw) -> Tile {
+        Tile T;
+        const int jk = jfirst + KT * WAVES * t + (lane & 31);
+        const int pid = jk < k1 ? raw : -1;
+        const int slot_any = (int)kv_hrow(c, max(pid, 0), jk, s, hk);
+        const int slot = pid >= 0 ? slot_any : 0;  // row 0: in bounds, masked
+        T.has = pid >= 0 ? 1 : 0;
 #pragma unroll
         for (int n = 0; n < 2; ++n) {
             const int sl = __shfl(slot, 8 * (hh >> 2) + 4 * n + (hh & 3), VK_WAVE);
             const uint2* kr = reinterpret_cast<const uint2*>(c.kq + (size_t)sl * HD);
 #pragma unroll
-            for (int b = 0; b < NB; ++b) kw[n][b] = kr[4 * b + g];
+            for (int b = 0; b < NB; ++b) T.kw[n][b] = kr[4 * b + g];
         }
-        uint2 kds[8], vds[8];  // f16 block scales of keys 8g + j (j = 4n + r)
+        T.kd = *reinterpret_cast<const uint2*>(c.kd + (size_t)slot * NB);
+        T.vd = *reinterpret_cast<const uint2*>(c.vd + (size_t)slot * NB);
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+            const int sl = __shfl(slot, 4 * va + t4, VK_WAVE);
+            T.vw[t4] = *reinterpret_cast<const uint4*>(c.vq + (size_t)sl * HD + 16 * vc);
+        }
+        return T;
+    };
+    auto compute = [&](const Tile& T) {
+        // scales and presence of keys 8g + j (j = 4n + r) from the lanes that loaded them
+        uint2 kds[8], vds[8];
         int kval[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const int sl = __shfl(slot, 8 * g + j, VK_WAVE);
-            kval[j] = __shfl(has, 8 * g + j, VK_WAVE);
-            kds[j] = *reinterpret_cast<const uint2*>(c.kd + (size_t)sl * NB);
-            vds[j] = *reinterpret_cast<const uint2*>(c.vd + (size_t)sl * NB);
-        }
-        uint4 vw[4];  // V rows of keys 4va + t, dims 16vc .. +15
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int sl = __shfl(slot, 4 * va + t, VK_WAVE);
-            vw[t] = *reinterpret_cast<const uint4*>(c.vq + (size_t)sl * HD + 16 * vc);
+            const int src = 8 * g + j;
+            kds[j] = make_uint2((uint32_t)__shfl((int)T.kd.x, src, VK_WAVE), (uint32_t)__shfl((int)T.kd.y, src, VK_WAVE));
+            vds[j] = make_uint2((uint32_t)__shfl((int)T.vd.x, src, VK_WAVE), (uint32_t)__shfl((int)T.vd.y, src, VK_WAVE));
+            kval[j] = __shfl(T.has, src, VK_WAVE);
         }
 
         // ---- S^T = K . (q hi + lo)^T per key subtile, block scales applied per block
@@ -820,7 +844,7 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
             vk_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                const vk_h16x8_t a = vk_i8x8_f16(kw[n][b]);
+                const vk_h16x8_t a = vk_i8x8_f16(T.kw[n][b]);
                 vk_f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[b], d, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[b], d, 0, 0, 0);
@@ -863,6 +887,7 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
 #pragma unroll
         for (int x = 0; x < 16; ++x) {
             const int cw = x >> 2, sb = x & 3;  // component and byte of dim x in each row's 16 bytes
+            const uint4* vw = T.vw;
             const uint32_t w0 = cw == 0 ? vw[0].x : cw == 1 ? vw[0].y : cw == 2 ? vw[0].z : vw[0].w;
             const uint32_t w1 = cw == 0 ? vw[1].x : cw == 1 ? vw[1].y : cw == 2 ? vw[1].z : vw[1].w;
             const uint32_t w2 = cw == 0 ? vw[2].x : cw == 1 ? vw[2].y : cw == 2 ? vw[2].z : vw[2].w;
@@ -893,6 +918,49 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
                 o[et] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, o[et], 0, 0, 0);
                 o[et] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, o[et], 0, 0, 0);
             }
+        }
+    };
+
+    // Two register sets, alternating (no copies between them); past the
+    // wave's last tile the prefetch reloads that tile, unused. Loads retire
+    // in issue order, so the issue order is page(t + 2), data(t + 1), then
+    // tile t's products: each wait is for the oldest loads in flight only.
+    if (ntile > 0 && ntile <= 4) {
+        // splits of up to 512 keys: straight-line, every load unconditional
+        // (only the products of tiles past the wave's last are skipped)
+        const int last = ntile - 1;
+        const int p0 = page_of(0), p1 = page_of(min(1, last));
+        Tile ta = load_tile(0, p0);
+        const int p2 = page_of(min(2, last));
+        __builtin_amdgcn_sched_barrier(0);  // keep the issue order
+        Tile tb = load_tile(min(1, last), p1);
+        const int p3 = page_of(min(3, last));
+        __builtin_amdgcn_sched_barrier(0);
+        compute(ta);
+        ta = load_tile(min(2, last), p2);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ntile > 1) compute(tb);
+        tb = load_tile(min(3, last), p3);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ntile > 2) compute(ta);
+        if (ntile > 3) compute(tb);
+    } else if (ntile > 4) {
+        const int last = ntile - 1;
+        int pid_a = page_of(0);
+        int pid_b = page_of(min(1, last));
+        Tile ta = load_tile(0, pid_a), tb;
+        for (int t = 0; t < ntile; t += 2) {
+            pid_a = page_of(min(t + 2, last));
+            __builtin_amdgcn_sched_barrier(0);
+            tb = load_tile(min(t + 1, last), pid_b);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(ta);
+            if (t + 1 >= ntile) break;
+            pid_b = page_of(min(t + 3, last));
+            __builtin_amdgcn_sched_barrier(0);
+            ta = load_tile(min(t + 2, last), pid_a);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(tb);
         }
     }
 
