@@ -422,7 +422,8 @@ def bench_decoder(ctx, hip, n_stream=64, n_layer=32, d=1280, H=20, ff=5120, V=51
     # cross o; cross k / v are applied once per utterance) and fc1 / fc2
     w_bytes = n_layer * (6 * d * d + 2 * d * ff) * 18 // 32
     kv_bytes = keys * n_layer * 2 * (d + d // 32 * 2)
-    cross_bytes = n_stream * n_layer * n_audio * d * 4 * 2
+    # cross K and V: fp16 high part + one-byte low part per value
+    cross_bytes = n_stream * n_layer * n_audio * d * 3 * 2
     emb_bytes = V * d * 4
     total = w_bytes + kv_bytes + cross_bytes + emb_bytes
     del dec
@@ -431,7 +432,7 @@ def bench_decoder(ctx, hip, n_stream=64, n_layer=32, d=1280, H=20, ff=5120, V=51
             "last_position": int(lens.max()) + steps,
             "ms_per_step": round(ms, 3), "tokens_per_s": round(n_stream / (ms * 1e-3), 1),
             "cross_f16_mode": {"ms_per_step": round(ms_f16, 3), "tokens_per_s": round(n_stream / (ms_f16 * 1e-3), 1)},
-            "bytes_per_step": {"weights_q4_0": w_bytes, "self_kv_q8_0": kv_bytes, "cross_kv_fp16x2": cross_bytes,
+            "bytes_per_step": {"weights_q4_0": w_bytes, "self_kv_q8_0": kv_bytes, "cross_kv_f16_q7": cross_bytes,
                                "tied_embedding_f32": emb_bytes},
             "gbs": round(total / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(total / (ms * 1e-3) / 1e9 / PEAK["hbm_gbs"], 4)}
 

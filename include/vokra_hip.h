@@ -305,7 +305,11 @@ int vokra_hip_logits_argmax_dev(vokra_hip_ctx_t *ctx, size_t rows, size_t vocab,
  * n_head_q). The projections around it are gemm_q_f32 calls. head_dim is 64
  * or 128 (else UNSUPPORTED_OP); t_kv = 0 gives zeros. Products run as fp16
  * hi/lo split MFMAs (three per product, f32 accumulation): results agree with
- * the f32 reference to about 1e-6 relative. A finite q * scale, k or v element
+ * the f32 reference to about 1e-6 relative. With t_q = 1 (decode) the low
+ * parts of k and v are held in one byte each, an integer times the fp16 high
+ * part's ulp / 128 (relative error at most 2^-18 / (1 - 2^-12), a quarter
+ * fewer bytes for the bandwidth-bound single-query case); the decoder
+ * session's cross-attention uses the same form. A finite q * scale, k or v element
  * of magnitude >= 65520 (beyond fp16) is INVALID_ARGUMENT: here after the
  * launch, for the _dev form at the next vokra_hip_synchronize. */
 int vokra_hip_attn_f32(vokra_hip_ctx_t *ctx, size_t batch, size_t t_q, size_t t_kv, size_t n_head_q,
@@ -530,11 +534,13 @@ int vokra_hip_decoder_set_encoder(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec
 int vokra_hip_decoder_set_encoder_dev(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t stream,
                                       const float *d_enc);
 /* Precision of the cross-attention K/V reads. VOKRA_HIP_CROSS_F32 (default)
- * keeps f32-level products: K and V are held as fp16 hi + lo pairs, the
+ * keeps f32-level products: K and V are held as an fp16 high part plus a
+ * one-byte low part scaled by the high part's ulp (the single-query form of
+ * vokra_hip_attn_f32, relative error at most 2^-18 / (1 - 2^-12)), against the
  * reference's f32 cross_attention (crates/vokra-models/src/whisper/nn.rs:
- * 342-399, decoder.rs:492-510) to f32 rounding. VOKRA_HIP_CROSS_F16 reads the
- * fp16 hi parts only: half the bytes of the step's largest stream, with K and
- * V rounded to fp16 (relative 2^-11). A performance mode with no counterpart in
+ * 342-399, decoder.rs:492-510). VOKRA_HIP_CROSS_F16 reads the fp16 high parts
+ * only: two thirds of the bytes of the step's largest stream, with K and V
+ * rounded to fp16 (relative 2^-11). A performance mode with no counterpart in
  * the reference; it may be switched between steps (both parts stay stored). */
 #define VOKRA_HIP_CROSS_F32 0
 #define VOKRA_HIP_CROSS_F16 1

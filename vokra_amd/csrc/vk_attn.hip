@@ -33,6 +33,9 @@ namespace vk {
 
 typedef _Float16 vk_h16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t vk_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t vk_u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 vk_h16x2a __attribute__((ext_vector_type(2)));
+typedef short vk_i16x2 __attribute__((ext_vector_type(2)));
 
 namespace attn {
 constexpr int QT = 64;   // queries per workgroup
@@ -73,6 +76,40 @@ __device__ __forceinline__ void split8_f16(const float* __restrict__ x, float sc
     }
     hi = make_uint4(h[0], h[1], h[2], h[3]);
     lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+// Compact low part (single-query attention's K / V): x = hi + lo with hi =
+// fp16(x) and lo = q * 2^(e - 32), e = hi's exponent field, q = round((x - hi)
+// * 2^(32 - e)) an integer of magnitude <= 64 stored in one byte (x - hi is
+// exact and at most half an fp16 ulp, 2^(e - 26)). |x - hi - lo| <= 2^(e - 33),
+// relative at most 2^-18 / (1 - 2^-12). Below e = 8 (|x| < 2^-7) lo is zero
+// (absolute error at most 2^-19), as the decoder's fp16 scale 2^(e - 22) is
+// not normal there.
+__device__ __forceinline__ void split_q7(float x, _Float16& hi, int8_t& lo) {
+    hi = (_Float16)x;
+    const int e = (__builtin_bit_cast(uint16_t, hi) >> 10) & 31;
+    lo = (e >= 8 && e < 31) ? (int8_t)(int)rintf(ldexpf(x - (float)hi, 32 - e)) : (int8_t)0;
+}
+// The fp16 low parts of two elements: hpair holds their fp16 high parts,
+// bytes `sel` of qsrc their q. q / 1024 comes exactly from the fp16 bits
+// 0x3C00 | (q + 128) (= 1 + (q + 128) / 1024) minus 1.125; times 2^(e - 22)
+// (fp16 exponent field e - 7, zero below e = 8) it is q * 2^(e - 32), exact.
+__device__ __forceinline__ uint32_t q7pair_f16(uint32_t hpair, uint32_t qsrc, uint32_t sel) {
+    const uint32_t t = __builtin_amdgcn_perm(0u, qsrc, sel) ^ 0x3C803C80u;
+    const vk_h16x2a q = __builtin_bit_cast(vk_h16x2a, t) + (vk_h16x2a){(_Float16)-1.125f, (_Float16)-1.125f};
+    vk_i16x2 e = __builtin_bit_cast(vk_i16x2, hpair & 0x7C007C00u) - (vk_i16x2){0x1C00, 0x1C00};
+    e = e > (vk_i16x2){0, 0} ? e : (vk_i16x2){0, 0};
+    return __builtin_bit_cast(uint32_t, q * __builtin_bit_cast(vk_h16x2a, e));
+}
+// the eight fp16 low parts of the elements whose high parts are h (8 fp16)
+// and whose q are the bytes of ql (8 int8)
+__device__ __forceinline__ vk_u32x4 q7x8_f16(vk_u32x4 h, vk_u32x2 ql) {
+    vk_u32x4 r;
+    r.x = q7pair_f16(h.x, ql.x, 0x0c010c00u);
+    r.y = q7pair_f16(h.y, ql.x, 0x0c030c02u);
+    r.z = q7pair_f16(h.z, ql.y, 0x0c010c00u);
+    r.w = q7pair_f16(h.w, ql.y, 0x0c030c02u);
+    return r;
 }
 
 // ---------------------------------------------------------------------------
@@ -121,8 +158,55 @@ __global__ __launch_bounds__(256) void vk_split_vt(const float* __restrict__ v, 
     }
 }
 
+// The same two pre-passes with the compact low part (one byte per element).
+__global__ void vk_split_rows_q7(const float* __restrict__ x, size_t n4, float scale, uint2* __restrict__ hi,
+                                 uint32_t* __restrict__ lo) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    const float4 v = reinterpret_cast<const float4*>(x)[i];
+    const float a[4] = {v.x * scale, v.y * scale, v.z * scale, v.w * scale};
+    if (vk_f16_overflow(a[0]) || vk_f16_overflow(a[1]) || vk_f16_overflow(a[2]) || vk_f16_overflow(a[3]))
+        attn_range_raise();
+    _Float16 h[4];
+    int8_t l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) split_q7(a[j], h[j], l[j]);
+    hi[i] = make_uint2(__builtin_bit_cast(uint16_t, h[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[1]) << 16),
+                       __builtin_bit_cast(uint16_t, h[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[3]) << 16));
+    lo[i] = (uint32_t)(uint8_t)l[0] | ((uint32_t)(uint8_t)l[1] << 8) | ((uint32_t)(uint8_t)l[2] << 16) |
+            ((uint32_t)(uint8_t)l[3] << 24);
+}
+
+__global__ __launch_bounds__(256) void vk_split_vt_q7(const float* __restrict__ v, int t_kv, int t_pad, int h_kv,
+                                                      int hd, uint16_t* __restrict__ vth, int8_t* __restrict__ vtl) {
+    __shared__ float tile[64][65];
+    const int t0 = blockIdx.x * 64, c0 = (blockIdx.y % (hd / 64)) * 64, h = blockIdx.y / (hd / 64), b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const size_t width = (size_t)h_kv * hd;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = (tid >> 6) + 4 * i, c = tid & 63;
+        const int t = t0 + r;
+        tile[r][c] = t < t_kv ? v[((size_t)b * t_kv + t) * width + (size_t)h * hd + c0 + c] : 0.0f;
+        if (vk_f16_overflow(tile[r][c])) attn_range_raise();
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int c = (tid >> 6) + 4 * i, r = tid & 63;
+        _Float16 hi;
+        int8_t lo;
+        split_q7(tile[r][c], hi, lo);
+        const size_t o = (((size_t)b * h_kv + h) * hd + c0 + c) * t_pad + t0 + r;
+        vth[o] = __builtin_bit_cast(uint16_t, hi);
+        vtl[o] = lo;
+    }
+}
+
 // ---------------------------------------------------------------------------
-template <int HD, bool LO, bool ONEQ>
+// LOM: the K / V low parts in use: 0 none (fp16 high parts only), 1 fp16
+// (kl, vtl as fp16 arrays), 2 compact (one byte per element, split_q7).
+template <int HD, int LOM, bool ONEQ>
 __global__ __launch_bounds__(256) void vk_flash_attn(
     const uint4* __restrict__ qh, const uint4* __restrict__ ql,    // [B][Tq][Hq*HD] fp16, scaled
     const uint4* __restrict__ kh, const uint4* __restrict__ kl,    // [B][Tkv][Hkv*HD] fp16
@@ -138,6 +222,7 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
     constexpr int VROW = KT + VPAD;  // halves per V^T tile row
     constexpr int KU4 = KT * HD / 8 / 256;  // uint4 per thread per K array
     constexpr int VU4 = HD * KT / 8 / 256;  // uint4 per thread per V^T array
+    constexpr bool LO = LOM != 0;
     constexpr int NP = LO ? 2 : 1;                         // fp16 parts of K and V in use
     __shared__ __align__(16) _Float16 lk[NP][KT * KROW];  // K tile, hi (/ lo)
     __shared__ __align__(16) _Float16 lv[NP][HD * VROW];  // V^T tile, hi (/ lo)
@@ -175,11 +260,14 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
     // native vectors (not HIP's uint4 struct) so the stage stays in registers
     struct Stage {
         vk_u32x4 kh[KU4], kl[KU4], vh[VU4], vl[VU4];
+        vk_u32x2 klq[KU4], vlq[VU4];  // LOM == 2
     };
     const vk_u32x4* kh4 = reinterpret_cast<const vk_u32x4*>(kh);
     const vk_u32x4* kl4 = reinterpret_cast<const vk_u32x4*>(kl);
     const vk_u32x4* vh4 = reinterpret_cast<const vk_u32x4*>(vth);
     const vk_u32x4* vl4 = reinterpret_cast<const vk_u32x4*>(vtl);
+    const vk_u32x2* klq2 = reinterpret_cast<const vk_u32x2*>(kl);
+    const vk_u32x2* vlq2 = reinterpret_cast<const vk_u32x2*>(vtl);
     auto load = [&](int kt) __attribute__((always_inline)) -> Stage {
         Stage st;
 #pragma unroll
@@ -189,7 +277,8 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
             const int t = min(kt * KT + r, tkv - 1);
             const size_t o = ((size_t)kb * tkv + t) * kw + (size_t)hk * HD / 8 + c;
             st.kh[i] = kh4[o];
-            if (LO) st.kl[i] = kl4[o];
+            if (LOM == 1) st.kl[i] = kl4[o];
+            if (LOM == 2) st.klq[i] = klq2[o];
         }
 #pragma unroll
         for (int i = 0; i < VU4; ++i) {
@@ -197,7 +286,8 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
             const int r = idx / (KT / 8), c = idx % (KT / 8);
             const size_t o = (((size_t)kb * hkv + hk) * HD + r) * (t_pad / 8) + (size_t)kt * KT / 8 + c;
             st.vh[i] = vh4[o];
-            if (LO) st.vl[i] = vl4[o];
+            if (LOM == 1) st.vl[i] = vl4[o];
+            if (LOM == 2) st.vlq[i] = vlq2[o];
         }
         return st;
     };
@@ -283,14 +373,16 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
             const int idx = tid + 256 * i;
             const int r = idx / (HD / 8), c = idx % (HD / 8);
             *reinterpret_cast<vk_u32x4*>(&lk[0][r * KROW + 8 * c]) = st.kh[i];
-            if (LO) *reinterpret_cast<vk_u32x4*>(&lk[NP - 1][r * KROW + 8 * c]) = st.kl[i];
+            if (LOM == 1) *reinterpret_cast<vk_u32x4*>(&lk[NP - 1][r * KROW + 8 * c]) = st.kl[i];
+            if (LOM == 2) *reinterpret_cast<vk_u32x4*>(&lk[NP - 1][r * KROW + 8 * c]) = q7x8_f16(st.kh[i], st.klq[i]);
         }
 #pragma unroll
         for (int i = 0; i < VU4; ++i) {
             const int idx = tid + 256 * i;
             const int r = idx / (KT / 8), c = idx % (KT / 8);
             *reinterpret_cast<vk_u32x4*>(&lv[0][r * VROW + 8 * c]) = st.vh[i];
-            if (LO) *reinterpret_cast<vk_u32x4*>(&lv[NP - 1][r * VROW + 8 * c]) = st.vl[i];
+            if (LOM == 1) *reinterpret_cast<vk_u32x4*>(&lv[NP - 1][r * VROW + 8 * c]) = st.vl[i];
+            if (LOM == 2) *reinterpret_cast<vk_u32x4*>(&lv[NP - 1][r * VROW + 8 * c]) = q7x8_f16(st.vh[i], st.vlq[i]);
         }
         VK_LDS_BARRIER();
         st = load(min(kt + 1, n_tiles - 1));
@@ -410,6 +502,22 @@ hipError_t launch_split_rows(hipStream_t s, const float* x, size_t n, float scal
     return hipGetLastError();
 }
 
+hipError_t launch_split_rows_q7(hipStream_t s, const float* x, size_t n, float scale, void* hi, void* lo) {
+    const size_t n4 = n / 4;
+    if (n4 == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_split_rows_q7, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, x, n4, scale, (uint2*)hi,
+                       (uint32_t*)lo);
+    return hipGetLastError();
+}
+
+hipError_t launch_split_vt_q7(hipStream_t s, const float* v, int batch, int t_kv, int t_pad, int h_kv, int hd,
+                              void* vth, void* vtl) {
+    if (batch == 0 || t_pad == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_split_vt_q7, dim3(t_pad / 64, h_kv * (hd / 64), batch), dim3(256), 0, s, v, t_kv, t_pad,
+                       h_kv, hd, (uint16_t*)vth, (int8_t*)vtl);
+    return hipGetLastError();
+}
+
 hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, int t_pad, int h_kv, int hd, void* vth,
                            void* vtl) {
     if (batch == 0 || t_pad == 0) return hipSuccess;
@@ -418,48 +526,64 @@ hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, i
     return hipGetLastError();
 }
 
-template <int HD, bool LO>
+template <int HD, int LOM>
 static void go_flash1(hipStream_t s, dim3 grid, const void* qh, const void* ql, const void* kh, const void* kl,
-                     const void* vth, const void* vtl, float* out, int tq, int tkv, int t_pad, int hq, int hkv,
-                     int causal, int q_off, const int* kv_index, const float* qf, float q_scale, const VkQOut& qo) {
+                      const void* vth, const void* vtl, float* out, int tq, int tkv, int t_pad, int hq, int hkv,
+                      int causal, int q_off, const int* kv_index, const float* qf, float q_scale, const VkQOut& qo) {
     if (tq == 1)
-        hipLaunchKernelGGL((vk_flash_attn<HD, LO, true>), grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
+        hipLaunchKernelGGL((vk_flash_attn<HD, LOM, true>), grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
                            (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv,
                            t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
     else
-        hipLaunchKernelGGL((vk_flash_attn<HD, LO, false>), grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
+        hipLaunchKernelGGL((vk_flash_attn<HD, LOM, false>), grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
                            (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv,
                            t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+}
+
+template <int HD>
+static void go_flash_hd(hipStream_t s, dim3 grid, const void* qh, const void* ql, const void* kh, const void* kl,
+                        const void* vth, const void* vtl, float* out, int tq, int tkv, int t_pad, int hq, int hkv,
+                        int causal, int q_off, const int* kv_index, const float* qf, float q_scale, int lo_mode,
+                        const VkQOut& qo) {
+    if (lo_mode == KV_LO_Q7 && tq == 1)  // the compact form exists for single-query launches only
+        go_flash1<HD, 2>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf,
+                         q_scale, qo);
+    else if (lo_mode == KV_LO_F16)
+        go_flash1<HD, 1>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf,
+                         q_scale, qo);
+    else
+        go_flash1<HD, 0>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf,
+                         q_scale, qo);
 }
 
 static hipError_t flash_any(hipStream_t s, int hd, const void* qh, const void* ql, const float* qf, float q_scale,
                             const void* kh, const void* kl, const void* vth, const void* vtl, float* out, int batch,
                             int tq, int tkv, int t_pad, int hq, int hkv, int causal, int q_off, const int* kv_index,
-                            bool kv_lo, const VkQOut& qo) {
+                            int lo_mode, const VkQOut& qo) {
+    if (lo_mode == KV_LO_Q7 && tq != 1) return hipErrorInvalidValue;
     const dim3 grid((tq + attn::QT - 1) / attn::QT, hq, batch);
-    if (hd == 64) {
-        if (kv_lo) go_flash1<64, true>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
-        else go_flash1<64, false>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
-    } else {
-        if (kv_lo) go_flash1<128, true>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
-        else go_flash1<128, false>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
-    }
+    if (hd == 64)
+        go_flash_hd<64>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf,
+                        q_scale, lo_mode, qo);
+    else
+        go_flash_hd<128>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf,
+                         q_scale, lo_mode, qo);
     return hipGetLastError();
 }
 
 hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* ql, const void* kh, const void* kl,
                              const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
-                             int hq, int hkv, int causal, int q_off, const int* kv_index, bool kv_lo) {
+                             int hq, int hkv, int causal, int q_off, const int* kv_index, int lo_mode) {
     return flash_any(s, hd, qh, ql, nullptr, 1.0f, kh, kl, vth, vtl, out, batch, tq, tkv, t_pad, hq, hkv, causal,
-                     q_off, kv_index, kv_lo, VkQOut{});
+                     q_off, kv_index, lo_mode, VkQOut{});
 }
 
 hipError_t launch_flash_attn_f32q(hipStream_t s, int hd, const float* q, float q_scale, const void* kh, const void* kl,
                                   const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
-                                  int hq, int hkv, int causal, int q_off, const int* kv_index, bool kv_lo,
+                                  int hq, int hkv, int causal, int q_off, const int* kv_index, int lo_mode,
                                   const VkQOut* qo) {
     return flash_any(s, hd, nullptr, nullptr, q, q_scale, kh, kl, vth, vtl, out, batch, tq, tkv, t_pad, hq, hkv,
-                     causal, q_off, kv_index, kv_lo, qo ? *qo : VkQOut{});
+                     causal, q_off, kv_index, lo_mode, qo ? *qo : VkQOut{});
 }
 
 // Reads and clears this file's fp16-range flag on the current device; the

@@ -408,27 +408,39 @@ int run_attn(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t hq, s
         VK_TRY(c->at_qh.ensure(nq * 2 + 16), "hipMalloc(attention q)");
         VK_TRY(c->at_ql.ensure(nq * 2 + 16), "hipMalloc(attention q)");
     }
+    // a single query row (decode) reads K / V with one-byte low parts (the
+    // compact form: a quarter fewer bytes; relative error 2^-18), several
+    // rows with fp16 low parts
+    const bool q7 = tq == 1;
+    const int lo_mode = q7 ? vk::KV_LO_Q7 : vk::KV_LO_F16;
     VK_TRY(c->at_kh.ensure(nk * 2 + 16), "hipMalloc(attention k)");
-    VK_TRY(c->at_kl.ensure(nk * 2 + 16), "hipMalloc(attention k)");
+    VK_TRY(c->at_kl.ensure(nk * (q7 ? 1 : 2) + 16), "hipMalloc(attention k)");
     VK_TRY(c->at_vh.ensure(nv * 2 + 16), "hipMalloc(attention v)");
-    VK_TRY(c->at_vl.ensure(nv * 2 + 16), "hipMalloc(attention v)");
+    VK_TRY(c->at_vl.ensure(nv * (q7 ? 1 : 2) + 16), "hipMalloc(attention v)");
     if (!q_in_kernel)
         VK_TRY(vk::launch_split_rows(c->stream, d_q, nq, scale, c->at_qh.p, c->at_ql.p), "launch(vk_split_rows q)");
-    VK_TRY(vk::launch_split_rows(c->stream, d_k, nk, 1.0f, c->at_kh.p, c->at_kl.p), "launch(vk_split_rows k)");
-    VK_TRY(vk::launch_split_vt(c->stream, d_v, (int)batch, (int)tkv, (int)t_pad, (int)hkv, (int)hd, c->at_vh.p,
-                               c->at_vl.p),
-           "launch(vk_split_vt)");
+    if (q7) {
+        VK_TRY(vk::launch_split_rows_q7(c->stream, d_k, nk, 1.0f, c->at_kh.p, c->at_kl.p), "launch(vk_split_rows_q7 k)");
+        VK_TRY(vk::launch_split_vt_q7(c->stream, d_v, (int)batch, (int)tkv, (int)t_pad, (int)hkv, (int)hd, c->at_vh.p,
+                                      c->at_vl.p),
+               "launch(vk_split_vt_q7)");
+    } else {
+        VK_TRY(vk::launch_split_rows(c->stream, d_k, nk, 1.0f, c->at_kh.p, c->at_kl.p), "launch(vk_split_rows k)");
+        VK_TRY(vk::launch_split_vt(c->stream, d_v, (int)batch, (int)tkv, (int)t_pad, (int)hkv, (int)hd, c->at_vh.p,
+                                   c->at_vl.p),
+               "launch(vk_split_vt)");
+    }
     if (q_in_kernel) {
         VK_TRY(vk::launch_flash_attn_f32q(c->stream, (int)hd, d_q, scale, c->at_kh.p, c->at_kl.p, c->at_vh.p,
                                           c->at_vl.p, (qo && !keep_out) ? nullptr : d_out, (int)batch, (int)tq,
                                           (int)tkv, (int)t_pad, (int)hq, (int)hkv, causal ? 1 : 0, (int)q_off,
-                                          nullptr, true, qo),
+                                          nullptr, lo_mode, qo),
                "launch(vk_flash_attn)");
         return VOKRA_HIP_OK;
     }
     VK_TRY(vk::launch_flash_attn(c->stream, (int)hd, c->at_qh.p, c->at_ql.p, c->at_kh.p, c->at_kl.p, c->at_vh.p,
                                  c->at_vl.p, d_out, (int)batch, (int)tq, (int)tkv, (int)t_pad, (int)hq, (int)hkv,
-                                 causal ? 1 : 0, (int)q_off),
+                                 causal ? 1 : 0, (int)q_off, nullptr, lo_mode),
            "launch(vk_flash_attn)");
     if (qo)
         VK_TRY(vk::launch_quantize_act_b32(c->stream, qo->pow2 != 0, d_out, (int)(batch * tq), qo->m_pad, qo->k,

@@ -115,10 +115,18 @@ namespace vk {
 hipError_t launch_split_rows(hipStream_t s, const float* x, size_t n, float scale, void* hi, void* lo);
 hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, int t_pad, int h_kv, int hd, void* vth,
                            void* vtl);
+// The same two splits with one-byte low parts (the compact form, vk_attn.hip
+// split_q7): lo holds n bytes / one byte per V^T element.
+hipError_t launch_split_rows_q7(hipStream_t s, const float* x, size_t n, float scale, void* hi, void* lo);
+hipError_t launch_split_vt_q7(hipStream_t s, const float* v, int batch, int t_kv, int t_pad, int h_kv, int hd,
+                              void* vth, void* vtl);
+// K / V low parts of a flash-attention launch: none (fp16 high parts only;
+// kl, vtl unused), fp16, or the compact one-byte form (single-query launches).
+enum { KV_LO_NONE = 0, KV_LO_F16 = 1, KV_LO_Q7 = 2 };
 hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* ql, const void* kh, const void* kl,
                              const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
                              int hq, int hkv, int causal, int q_off, const int* kv_index = nullptr,
-                             bool kv_lo = true);  // false: K/V fp16 hi parts only (kl, vtl unused)
+                             int lo_mode = KV_LO_F16);
 // The same with q given as f32 [B][Tq][Hq*hd] (16-byte aligned): the kernel
 // splits q * q_scale itself exactly as launch_split_rows would. With qo, the
 // kernel also quantizes O (rows b * tq + i, width hq * hd) into qo's
@@ -126,7 +134,7 @@ hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* 
 hipError_t launch_flash_attn_f32q(hipStream_t s, int hd, const float* q, float q_scale, const void* kh, const void* kl,
                                   const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
                                   int hq, int hkv, int causal, int q_off, const int* kv_index = nullptr,
-                                  bool kv_lo = true, const VkQOut* qo = nullptr);
+                                  int lo_mode = KV_LO_F16, const VkQOut* qo = nullptr);
 }  // namespace vk
 
 namespace vk {

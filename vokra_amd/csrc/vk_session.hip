@@ -163,7 +163,7 @@ struct vokra_hip_decoder {
     std::vector<DecLayer> layers;
     DBuf tok_emb, pos_emb, lnpg, lnpb;
     vokra_hip_kv_t* kv = nullptr;
-    DBuf ckh, ckl, cvh, cvl;  // cross K (fp16 hi/lo) and V^T per (stream, layer)
+    DBuf ckh, ckl, cvh, cvl;  // cross K and V^T per (stream, layer): fp16 high parts, one-byte low parts
     int cross_precision = VOKRA_HIP_CROSS_F32;  // F16: cross-attention reads the hi parts only
     DBuf h, x, q, k, v, attn, f, logits, lpart, lens, kvidx, next, tk, tv, stage;
     vokra_hip_qact_t *qa_d = nullptr, *qa_f = nullptr;
@@ -320,15 +320,17 @@ int dec_setup(vokra_hip_decoder* m, const vokra_hip_decoder_layer_t* layers, con
                                &m->kv));
     const size_t sl = m->n_stream * m->n_layer;
     SS_TRY(m->ckh.alloc(c, sl * m->n_audio * d * 2));
-    SS_TRY(m->ckl.alloc(c, sl * m->n_audio * d * 2));
+    SS_TRY(m->ckl.alloc(c, sl * m->n_audio * d));
     SS_TRY(m->cvh.alloc(c, sl * d * m->t_pad * 2));
-    SS_TRY(m->cvl.alloc(c, sl * d * m->t_pad * 2));
+    SS_TRY(m->cvl.alloc(c, sl * d * m->t_pad));
     // zero cross K/V: a stream stepped through the _dev path before its
     // encoder output is set attends over zeros, never over stale memory
     for (DBuf* b : {&m->ckh, &m->ckl})
-        SS_HIP(hipMemsetAsync(b->p, 0, sl * m->n_audio * d * 2, vk::ctx_stream(c)), "hipMemsetAsync(cross k)");
+        SS_HIP(hipMemsetAsync(b->p, 0, sl * m->n_audio * d * (b == &m->ckh ? 2 : 1), vk::ctx_stream(c)),
+               "hipMemsetAsync(cross k)");
     for (DBuf* b : {&m->cvh, &m->cvl})
-        SS_HIP(hipMemsetAsync(b->p, 0, sl * d * m->t_pad * 2, vk::ctx_stream(c)), "hipMemsetAsync(cross v)");
+        SS_HIP(hipMemsetAsync(b->p, 0, sl * d * m->t_pad * (b == &m->cvh ? 2 : 1), vk::ctx_stream(c)),
+               "hipMemsetAsync(cross v)");
     m->enc_set.assign(m->n_stream, 0);
     m->length.assign(m->n_stream, 0);
     const size_t rows = m->n_stream, rd = rows * d * sizeof(float);
@@ -358,12 +360,12 @@ int dec_set_encoder(vokra_hip_decoder* m, size_t stream, const float* d_enc) {
         SS_TRY(L.cv.run(c, m->qa_d, m->tv.f()));
         const size_t sl = stream * m->n_layer + l;
         uint16_t* kh = (uint16_t*)m->ckh.p + sl * na * d;
-        uint16_t* kl = (uint16_t*)m->ckl.p + sl * na * d;
+        int8_t* kl = (int8_t*)m->ckl.p + sl * na * d;
         uint16_t* vh = (uint16_t*)m->cvh.p + sl * d * m->t_pad;
-        uint16_t* vl = (uint16_t*)m->cvl.p + sl * d * m->t_pad;
-        SS_HIP(vk::launch_split_rows(s, m->tk.f(), na * d, 1.0f, kh, kl), "launch(vk_split_rows cross k)");
-        SS_HIP(vk::launch_split_vt(s, m->tv.f(), 1, (int)na, (int)m->t_pad, (int)m->n_head, (int)m->hd, vh, vl),
-               "launch(vk_split_vt cross v)");
+        int8_t* vl = (int8_t*)m->cvl.p + sl * d * m->t_pad;
+        SS_HIP(vk::launch_split_rows_q7(s, m->tk.f(), na * d, 1.0f, kh, kl), "launch(vk_split_rows_q7 cross k)");
+        SS_HIP(vk::launch_split_vt_q7(s, m->tv.f(), 1, (int)na, (int)m->t_pad, (int)m->n_head, (int)m->hd, vh, vl),
+               "launch(vk_split_vt_q7 cross v)");
     }
     return VOKRA_HIP_OK;
 }
@@ -411,7 +413,8 @@ int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_
         SS_HIP(vk::launch_flash_attn_f32q(s, (int)m->hd, m->q.f(), scale, m->ckh.p, m->ckl.p, m->cvh.p, m->cvl.p,
                                           qo.afrag ? nullptr : m->attn.f(), (int)n, 1, (int)m->n_audio,
                                           (int)m->t_pad, (int)m->n_head, (int)m->n_head, 0, 0, m->kvidx.i() + l * n,
-                                          m->cross_precision == VOKRA_HIP_CROSS_F32, qo.afrag ? &qo : nullptr),
+                                          m->cross_precision == VOKRA_HIP_CROSS_F32 ? vk::KV_LO_Q7 : vk::KV_LO_NONE,
+                                          qo.afrag ? &qo : nullptr),
                "launch(vk_flash_attn cross)");
         if (qo.afrag) vk::qact_outputs_written(m->qa_d, n, act);
         else SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->attn.f(), act));
