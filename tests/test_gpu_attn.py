@@ -157,3 +157,44 @@ def test_attention_rejections(ctx):
     k = np.zeros((2, 2 * 64), np.float32)
     with pytest.raises(hip.InvalidArgument):
         ctx.attn_f32(q, k, k, 3, 2)                    # 3 % 2 != 0
+
+
+def compact_kv(x):
+    """x rounded through the single-query K/V form: fp16 high part plus a
+    one-byte low part q * 2^(e - 32) (e = the high part's exponent field,
+    zero below e = 8), restated in numpy."""
+    x = np.asarray(x, np.float32)
+    hi = x.astype(np.float16)
+    e = ((hi.view(np.uint16) >> 10) & 31).astype(np.int64)
+    r = (x - hi.astype(np.float32)).astype(np.float64)
+    ok = (e >= 8) & (e < 31)
+    q = np.where(ok, np.rint(np.ldexp(r, np.where(ok, 32 - e, 0))), 0)
+    return hi.astype(np.float64) + q * np.ldexp(1.0, np.where(ok, e - 32, 0))
+
+
+def test_single_query_compact_kv_precision(ctx):
+    """t_q = 1 reads K / V as fp16 high parts plus one-byte low parts. Pinned
+    two ways against float64: the format's own rounding is at most
+    2^-18 / (1 - 2^-12) relative (2^-19 absolute below 2^-7), and the kernel
+    agrees with float64 attention over the compact-rounded K / V to 2e-6 of
+    the output scale, while exact-K/V float64 is met to 2e-5 (50x inside the
+    f32 bar)."""
+    print("[case] single-query compact K/V precision", flush=True)
+    g = np.random.default_rng(71)
+    for (tkv, H, hd, kscale) in [(1500, 20, 64, 1.0), (700, 4, 128, 3.0), (37, 2, 64, 0.01)]:
+        q = g.standard_normal((1, H * hd)).astype(np.float32)
+        k = (g.standard_normal((tkv, H * hd)) * kscale).astype(np.float32)
+        v = g.standard_normal((tkv, H * hd)).astype(np.float32)
+        ck, cv = compact_kv(k), compact_kv(v)
+        for x, cx in ((k, ck), (v, cv)):
+            xd = x.astype(np.float64)
+            big = np.abs(xd) >= 2.0 ** -7
+            assert np.all(np.abs(cx - xd)[big] <= 2.0 ** -18 / (1 - 2.0 ** -12) * np.abs(xd)[big])
+            assert np.all(np.abs(cx - xd)[~big] <= 2.0 ** -19)
+        scale = hd ** -0.5
+        got = ctx.attn_f32(q[None], k[None], v[None], H, scale=scale).reshape(1, H * hd).astype(np.float64)
+        scale_out = float(np.abs(v).max())  # |out| <= max |v|
+        want_c = sdpa_f64(q, ck, cv, H, H, scale)
+        want = sdpa_f64(q, k, v, H, H, scale)
+        assert np.abs(got - want_c).max() <= 2e-6 * scale_out, (tkv, np.abs(got - want_c).max())
+        assert np.abs(got - want).max() <= 2e-5 * scale_out, (tkv, np.abs(got - want).max())

@@ -649,6 +649,55 @@ int qact_ln_quantize(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, const float
     return VOKRA_HIP_OK;
 }
 
+// RMSNorm (or SwiGLU) of m rows of width k fused with the K-quant activation
+// pass into qa: one launch, the same bits as the unfused pair.
+static int qact_g16_prepare(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, size_t k, const char* what) {
+    if (!c || !qa || qa->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "%s: bad activation buffer", what);
+    if (m == 0 || m > qa->max_m)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "%s: m=%zu outside 1..%zu", what, m, qa->max_m);
+    if (k == 0 || k % 256 != 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "K-quant INT8 GEMV needs k to be a positive multiple of 256, got %zu", k);
+    if (qa->growable) {
+        int st = qact_reserve(qa, m, k);
+        if (st) return st;
+    } else if (k != qa->k) {
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "%s: width %zu, the activation buffer holds %zu", what, k, qa->k);
+    }
+    VK_TRY(set_dev(c), "hipSetDevice");
+    return VOKRA_HIP_OK;
+}
+
+int qact_rms_quantize_g16(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, size_t k, const float* d_in,
+                          const float* gamma, float eps) {
+    int st = qact_g16_prepare(c, qa, m, k, "rms_quantize");
+    if (st) return st;
+    const size_t m_pad = round_up(m, 16);
+    VK_TRY(vk::launch_rms_quantize_g16(c->stream, d_in, gamma, eps, (int)m, (int)m_pad, (int)k, (uint4*)qa->frag.p,
+                                       (float*)qa->scale.p, (float*)qa->gsum.p),
+           "launch(vk_rms_quantize_g16)");
+    qa->m = m;
+    qa->k = k;
+    qa->m_pad = m_pad;
+    qa->act_quant = VOKRA_HIP_ACT_KQUANT;
+    return VOKRA_HIP_OK;
+}
+
+int qact_swiglu_quantize_g16(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, size_t k, const float* d_g,
+                             const float* d_u) {
+    int st = qact_g16_prepare(c, qa, m, k, "swiglu_quantize");
+    if (st) return st;
+    const size_t m_pad = round_up(m, 16);
+    VK_TRY(vk::launch_swiglu_quantize_g16(c->stream, d_g, d_u, (int)m, (int)m_pad, (int)k, (uint4*)qa->frag.p,
+                                          (float*)qa->scale.p, (float*)qa->gsum.p),
+           "launch(vk_swiglu_quantize_g16)");
+    qa->m = m;
+    qa->k = k;
+    qa->m_pad = m_pad;
+    qa->act_quant = VOKRA_HIP_ACT_KQUANT;
+    return VOKRA_HIP_OK;
+}
+
 // The output side of an activation pass over m rows of qa's width, for a
 // producer kernel that quantizes its own rows; qo->afrag stays NULL for the
 // K-quant convention (its groups of 16 have no fused form). qact_commit then

@@ -74,29 +74,17 @@ __global__ void vk_dequantize_q4k(const uint8_t* __restrict__ bytes, size_t nsb,
 //   ascale / asum: per run of 4 groups (g / 4), per row, the 4 groups' s and
 //          (float) gsum back to back: index ((g / 4) * m_pad + row) * 4 + g % 4.
 // Rows m..m_pad-1 are written as zeros.
-__global__ void vk_quantize_act_g16(const float* __restrict__ a, int m, int m_pad, int k,
-                                    uint2* __restrict__ afrag, float* __restrict__ ascale,
-                                    float* __restrict__ asum) {
-    const int ng = k / 16, nsb = k / kq::QK;
-    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (size_t)ng * m_pad) return;
-    const int g = (int)(gid / m_pad), row = (int)(gid % m_pad);
+// One group's activation pass: the 16 values v of (row, group g) -> its
+// fragment words, s and gsum (zeros when !live: the padding rows).
+__device__ __forceinline__ void vk_q16_store(int row, int g, int m_pad, int nsb, const float (&v)[16], bool live,
+                                             uint2* __restrict__ afrag, float* __restrict__ ascale,
+                                             float* __restrict__ asum) {
     int r[16];
     float s = 0.0f;
     int gsum = 0;
 #pragma unroll
     for (int t = 0; t < 16; ++t) r[t] = 0;
-    if (row < m) {
-        const float4* src = reinterpret_cast<const float4*>(a + (size_t)row * k + 16 * g);
-        float v[16];
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            const float4 x = src[h];
-            v[4 * h] = x.x;
-            v[4 * h + 1] = x.y;
-            v[4 * h + 2] = x.z;
-            v[4 * h + 3] = x.w;
-        }
+    if (live) {
         float amax = 0.0f;
 #pragma unroll
         for (int t = 0; t < 16; ++t) amax = fmaxf(amax, fabsf(v[t]));
@@ -123,6 +111,81 @@ __global__ void vk_quantize_act_g16(const float* __restrict__ a, int m, int m_pa
     const size_t si = ((size_t)(g >> 2) * m_pad + row) * 4 + (g & 3);
     ascale[si] = s;
     asum[si] = (float)gsum;
+}
+
+__global__ void vk_quantize_act_g16(const float* __restrict__ a, int m, int m_pad, int k,
+                                    uint2* __restrict__ afrag, float* __restrict__ ascale,
+                                    float* __restrict__ asum) {
+    const int ng = k / 16, nsb = k / kq::QK;
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (size_t)ng * m_pad) return;
+    const int g = (int)(gid / m_pad), row = (int)(gid % m_pad);
+    float v[16];
+    if (row < m) {
+        const float4* src = reinterpret_cast<const float4*>(a + (size_t)row * k + 16 * g);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const float4 x = src[h];
+            v[4 * h] = x.x;
+            v[4 * h + 1] = x.y;
+            v[4 * h + 2] = x.z;
+            v[4 * h + 3] = x.w;
+        }
+    }
+    vk_q16_store(row, g, m_pad, nsb, v, row < m, afrag, ascale, asum);
+}
+
+// RMSNorm fused with the activation pass, one workgroup per row (rows m ..
+// m_pad-1 write the zero padding): the row's sum of squares exactly as
+// vk_rms_norm_f32 forms it (thread t sums columns t, t + 256, ... in order,
+// then vk_block_sum256), y = x * inv * gamma, then each 16-wide group as
+// vk_quantize_act_g16 would quantize y. Bit-identical to the two launches.
+__global__ __launch_bounds__(256) void vk_rms_quantize_g16(const float* __restrict__ in,
+                                                           const float* __restrict__ gamma, float eps, int m,
+                                                           int m_pad, int k, uint2* __restrict__ afrag,
+                                                           float* __restrict__ ascale, float* __restrict__ asum) {
+    __shared__ float red[4];
+    const int row = blockIdx.x, nsb = k / kq::QK;
+    const bool live = row < m;  // uniform per workgroup
+    float inv = 0.0f;
+    const float* ir = in + (size_t)row * k;
+    if (live) {
+        float s = 0.0f;
+        for (int c = threadIdx.x; c < k; c += 256) s += ir[c] * ir[c];
+        inv = 1.0f / sqrtf(vk_block_sum256(s, red) / (float)k + eps);
+    }
+    for (int g = threadIdx.x; g < k / 16; g += 256) {
+        float v[16];
+        if (live) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) v[t] = ir[16 * g + t] * inv * gamma[16 * g + t];
+        }
+        vk_q16_store(row, g, m_pad, nsb, v, live, afrag, ascale, asum);
+    }
+}
+
+// SwiGLU fused with the activation pass: one thread per (group, row), the
+// 16 values silu(g) * u formed as vk_swiglu_f32 forms them, then quantized as
+// vk_quantize_act_g16 would. Bit-identical to the two launches.
+__global__ void vk_swiglu_quantize_g16(const float* __restrict__ gt, const float* __restrict__ up, int m, int m_pad,
+                                       int k, uint2* __restrict__ afrag, float* __restrict__ ascale,
+                                       float* __restrict__ asum) {
+    const int ng = k / 16, nsb = k / kq::QK;
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (size_t)ng * m_pad) return;
+    const int g = (int)(gid / m_pad), row = (int)(gid % m_pad);
+    float v[16];
+    if (row < m) {
+        const size_t o = (size_t)row * k + 16 * g;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const float x = gt[o + t];
+            const float sg = 1.0f / (1.0f + expf(-x));
+            const float tt = x * sg;
+            v[t] = tt * up[o + t];
+        }
+    }
+    vk_q16_store(row, g, m_pad, nsb, v, row < m, afrag, ascale, asum);
 }
 
 // ---------------------------------------------------------------------------
@@ -361,6 +424,23 @@ hipError_t launch_quantize_act_g16(hipStream_t s, const float* a, int m, int m_p
     if (threads == 0) return hipSuccess;
     hipLaunchKernelGGL(vk_quantize_act_g16, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a, m, m_pad,
                        k, reinterpret_cast<uint2*>(afrag), ascale, asum);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_quantize_g16(hipStream_t s, const float* in, const float* gamma, float eps, int m, int m_pad,
+                                   int k, uint4* afrag, float* ascale, float* asum) {
+    if (m_pad == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_rms_quantize_g16, dim3((unsigned)m_pad), dim3(256), 0, s, in, gamma, eps, m, m_pad, k,
+                       reinterpret_cast<uint2*>(afrag), ascale, asum);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_quantize_g16(hipStream_t s, const float* g, const float* u, int m, int m_pad, int k,
+                                      uint4* afrag, float* ascale, float* asum) {
+    const size_t threads = (size_t)(k / 16) * m_pad;
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_swiglu_quantize_g16, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, g, u, m,
+                       m_pad, k, reinterpret_cast<uint2*>(afrag), ascale, asum);
     return hipGetLastError();
 }
 

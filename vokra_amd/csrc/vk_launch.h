@@ -109,6 +109,13 @@ hipError_t launch_repack_w_q4k(hipStream_t s, const uint8_t* wq, int n, int n_pa
                                float2* wdm);
 hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum,
                            const VkQ4kLin* lins, int n_lin, int m, int nsb, int m_pad);
+// RMSNorm + the K-quant activation pass, and SwiGLU + the activation pass, in
+// one launch each (bit-identical to vk_rms_norm_f32 / vk_swiglu_f32 followed by
+// vk_quantize_act_g16); m_pad = round_up(m, 16), k % 256 == 0.
+hipError_t launch_rms_quantize_g16(hipStream_t s, const float* in, const float* gamma, float eps, int m, int m_pad,
+                                   int k, uint4* afrag, float* ascale, float* asum);
+hipError_t launch_swiglu_quantize_g16(hipStream_t s, const float* g, const float* u, int m, int m_pad, int k,
+                                      uint4* afrag, float* ascale, float* asum);
 }  // namespace vk
 
 namespace vk {
@@ -175,6 +182,10 @@ hipError_t launch_kv_write_allocated(hipStream_t s, const KvView& v, int layer, 
 // pos_offset + r when positions is NULL), theta [hd / 2] from the host.
 hipError_t launch_rope_rows(hipStream_t s, float* x, int rows, int n_head, int hd, const float* theta,
                             const int* positions, int pos_offset);
+// RoPE of q [rows][hq * hd] and k [rows][hkv * hd] at positions[r], one launch
+// (the same values as two launch_rope_rows calls).
+hipError_t launch_rope_rows_qk(hipStream_t s, float* q, float* k, int rows, int hq, int hkv, int hd,
+                               const float* theta, const int* positions);
 // out = silu(g) * u elementwise (out may alias g).
 hipError_t launch_swiglu_f32(hipStream_t s, const float* g, const float* u, float* out, size_t n);
 hipError_t launch_kv_alloc_layers(hipStream_t s, const KvView& v, int layer0, int n_layers, int n, int q_base,
@@ -228,6 +239,13 @@ int gemm_qact_multi(vokra_hip_ctx* c, int n, const vokra_hip_qweight* const* ws,
                     const float* const* biases, float* const* outs);
 int qact_ln_quantize(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, const float* d_in, const float* gamma,
                      const float* beta, float eps, int act_quant, float* d_scratch);
+//   qact_rms_quantize_g16    = RMSNorm (vk_rms_norm_f32) of m rows of width k,
+//                              then vokra_hip_qact_quantize_dev KQUANT
+//   qact_swiglu_quantize_g16 = vk_swiglu_f32 of g, u [m, k], then the same pass
+int qact_rms_quantize_g16(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, size_t k, const float* d_in,
+                          const float* gamma, float eps);
+int qact_swiglu_quantize_g16(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, size_t k, const float* d_g,
+                             const float* d_u);
 //   attn_quantize       = vokra_hip_attn_f32_dev into d_out, then
 //                         vokra_hip_qact_quantize_dev of its batch * t_q rows
 //                         (d_out is then scratch: the fused kernel may skip it)

@@ -39,6 +39,29 @@ __global__ void vk_rope_rows(float* __restrict__ x, int rows, int n_head, int hd
     row[j + half] = as + bc;
 }
 
+// The same rotation over two arrays in one launch: q [rows][hq * hd] and
+// k [rows][hkv * hd] (heads 0 .. hq-1 of the grid are q's, the rest k's).
+__global__ void vk_rope_rows_qk(float* __restrict__ q, float* __restrict__ k, int rows, int hq, int hkv, int hd,
+                                const float* __restrict__ theta, const int* __restrict__ positions) {
+    const int half = hd >> 1;
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t per_row = (size_t)(hq + hkv) * half;
+    if (gid >= (size_t)rows * per_row) return;
+    const int r = (int)(gid / per_row);
+    const int rem = (int)(gid % per_row);
+    const int hh = rem / half, j = rem % half;
+    const bool is_q = hh < hq;
+    const int h = is_q ? hh : hh - hq, nh = is_q ? hq : hkv;
+    const float m = (float)positions[r];
+    const float angle = m * theta[j];
+    const float s = sinf(angle), c = cosf(angle);
+    float* row = (is_q ? q : k) + (size_t)r * nh * hd + (size_t)h * hd;
+    const float a = row[j], b = row[j + half];
+    const float ac = a * c, bs = b * s, as = a * s, bc = b * c;
+    row[j] = ac - bs;
+    row[j + half] = as + bc;
+}
+
 // out[i] = silu(g[i]) * u[i]; out may alias g.
 __global__ void vk_swiglu_f32(const float* g, const float* __restrict__ u, float* out, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
@@ -61,6 +84,15 @@ hipError_t launch_rope_rows(hipStream_t s, float* x, int rows, int n_head, int h
     if (threads == 0) return hipSuccess;
     hipLaunchKernelGGL(vk_rope_rows, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, x, rows, n_head, hd,
                        theta, positions, pos_offset);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_rows_qk(hipStream_t s, float* q, float* k, int rows, int hq, int hkv, int hd,
+                               const float* theta, const int* positions) {
+    const size_t threads = (size_t)rows * (hq + hkv) * (hd / 2);
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_rope_rows_qk, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, q, k, rows, hq, hkv,
+                       hd, theta, positions);
     return hipGetLastError();
 }
 

@@ -813,7 +813,10 @@ int td_setup(vokra_hip_text_decoder* m, const vokra_hip_text_decoder_layer_t* la
 }
 
 // RMSNorm of rows n of in into scratch, then the activation pass into qa.
+// (one fused launch for the K-quant convention)
 int td_rms_quantize(vokra_hip_text_decoder* m, vokra_hip_qact_t* qa, size_t n, const float* in, const float* gamma) {
+    if (act_of(m->wdtype) == VOKRA_HIP_ACT_KQUANT)
+        return vk::qact_rms_quantize_g16(m->ctx, qa, n, m->d, in, gamma, m->eps);
     hipStream_t s = vk::ctx_stream(m->ctx);
     SS_HIP(vk::launch_rms_norm_f32(s, in, m->x.f(), (int)n, (int)m->d, gamma, m->eps), "launch(vk_rms_norm_f32)");
     return vokra_hip_qact_quantize_dev(m->ctx, qa, n, m->x.f(), act_of(m->wdtype));
@@ -845,10 +848,9 @@ int td_step(vokra_hip_text_decoder* m, size_t n, const int* d_streams, const int
             float* qkv_o[3] = {m->q.f(), m->k.f(), m->v.f()};
             SS_TRY(vk::gemm_qact_multi(c, 3, qkv, m->qa_d, qkv_b, qkv_o));
         }
-        SS_HIP(vk::launch_rope_rows(s, m->q.f(), (int)n, (int)m->hq, (int)m->hd, m->theta.f(), d_positions, 0),
-               "launch(vk_rope_rows q)");
-        SS_HIP(vk::launch_rope_rows(s, m->k.f(), (int)n, (int)m->hkv, (int)m->hd, m->theta.f(), d_positions, 0),
-               "launch(vk_rope_rows k)");
+        SS_HIP(vk::launch_rope_rows_qk(s, m->q.f(), m->k.f(), (int)n, (int)m->hq, (int)m->hkv, (int)m->hd,
+                                       m->theta.f(), d_positions),
+               "launch(vk_rope_rows_qk)");
         SS_TRY(vk::kv_write_allocated(c, m->kv, l, n, d_streams, d_positions, m->k.f(), m->v.f()));
         SS_TRY(vk::paged_attn_quantize(c, m->kv, l, n, d_streams, m->lens.i(), m->n_ctx, m->hq, m->q.f(), m->scale,
                                        m->attn.f(), m->qa_q, act));
@@ -861,8 +863,12 @@ int td_step(vokra_hip_text_decoder* m, size_t n, const int* d_streams, const int
             float* gu_o[2] = {m->g.f(), m->u.f()};
             SS_TRY(vk::gemm_qact_multi(c, 2, gu, m->qa_d, gu_b, gu_o));
         }
-        SS_HIP(vk::launch_swiglu_f32(s, m->g.f(), m->u.f(), m->g.f(), n * ff), "launch(vk_swiglu_f32)");
-        SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_f, n, m->g.f(), act));
+        if (act == VOKRA_HIP_ACT_KQUANT) {
+            SS_TRY(vk::qact_swiglu_quantize_g16(c, m->qa_f, n, ff, m->g.f(), m->u.f()));
+        } else {
+            SS_HIP(vk::launch_swiglu_f32(s, m->g.f(), m->u.f(), m->g.f(), n * ff), "launch(vk_swiglu_f32)");
+            SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_f, n, m->g.f(), act));
+        }
         SS_TRY(L.down.run(c, m->qa_f, m->h.f(), add_h));
     }
     // final RMSNorm, LM head, greedy argmax (text_decoder.rs:1423-1451,
