@@ -156,7 +156,18 @@ def test_argmax_rules(ctx, oracle):
     g = np.random.default_rng(5)
     big = g.standard_normal((3, 51866)).astype(np.float32)
     big[1, 777] = big[1, 40000] = 100.0
-    for mat in (rows, big):
+    # ties and NaN at the edges of the 2048-column slices the kernel merges
+    edge = g.standard_normal((6, 6200)).astype(np.float32)
+    edge[0, 2047] = edge[0, 2048] = 50.0
+    edge[1, 4096] = edge[1, 6199] = 50.0
+    edge[2] = 0.0
+    edge[2, :2048] = -0.0
+    edge[3, ::2] = np.nan
+    edge[3, 4095] = 9.0
+    edge[4] = -np.inf
+    edge[4, 6199] = -1e30
+    edge[5] = np.nan
+    for mat in (rows, big, edge):
         d_l = hip.DeviceBuffer.from_array(ctx, mat)
         d_o = hip.DeviceBuffer(ctx, mat.shape[0] * 4)
         ctx.argmax_f32_dev(d_l, mat.shape[0], mat.shape[1], d_o)

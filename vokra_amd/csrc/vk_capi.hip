@@ -1457,6 +1457,13 @@ int vokra_hip_argmax_f32_dev(vokra_hip_ctx_t* c, const float* d_logits, size_t r
     if (rows == 0) return VOKRA_HIP_OK;
     if (!d_logits || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "argmax: NULL buffer");
     VK_TRY(set_dev(c), "hipSetDevice");
+    if (rows <= 65535 && cols > 0) {  // many workgroups per row, then an in-order merge of the slices
+        VK_TRY(c->lg_part.ensure(rows * (size_t)vk::argmax_n_slices((int)cols) * sizeof(float2)),
+               "hipMalloc(argmax partials)");
+        VK_TRY(vk::launch_argmax_sliced(c->stream, d_logits, (int)rows, (int)cols, (float2*)c->lg_part.p, d_out),
+               "launch(vk_argmax_slices)");
+        return VOKRA_HIP_OK;
+    }
     VK_TRY(vk::launch_argmax_f32(c->stream, d_logits, (int)rows, (int)cols, d_out), "launch(vk_argmax_f32)");
     return VOKRA_HIP_OK;
 }

@@ -555,6 +555,42 @@ __global__ __launch_bounds__(256) void vk_argmax_parts(const float2* __restrict_
     }
 }
 
+// argmax over wide rows in two passes: workgroup (slice, row) scans columns
+// [slice * AM_SLICE, +AM_SLICE) with the same strict-greater rule and stores
+// its (max, index) pair; vk_argmax_parts then merges a row's pairs. Each
+// thread visits its columns in increasing order, so "first strict maximum"
+// survives the (value desc, index asc) merges.
+constexpr int AM_SLICE = 2048;
+__global__ __launch_bounds__(256) void vk_argmax_slices(const float* __restrict__ logits, int cols, int n_sl,
+                                                        float2* __restrict__ part) {
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    const float* row = logits + (size_t)blockIdx.y * cols;
+    const int c0 = blockIdx.x * AM_SLICE + threadIdx.x;
+    float v[AM_SLICE / 256];
+#pragma unroll
+    for (int j = 0; j < AM_SLICE / 256; ++j) v[j] = c0 + 256 * j < cols ? row[c0 + 256 * j] : -INFINITY;
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+#pragma unroll
+    for (int j = 0; j < AM_SLICE / 256; ++j)
+        if (v[j] > bv) {
+            bv = v[j];
+            bi = c0 + 256 * j;
+        }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) vk_am_merge(bv, bi, __shfl_xor(bv, o, VK_WAVE), __shfl_xor(bi, o, VK_WAVE));
+    if ((threadIdx.x & 63) == 0) {
+        rv[threadIdx.x >> 6] = bv;
+        ri[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) vk_am_merge(bv, bi, rv[w], ri[w]);
+        part[(size_t)blockIdx.y * n_sl + blockIdx.x] = make_float2(bv, __int_as_float(bi));
+    }
+}
+
 }  // namespace vk
 
 #include "vk_launch.h"
@@ -635,6 +671,20 @@ hipError_t launch_embed_f32(hipStream_t s, const float* tok_emb, const float* po
 hipError_t launch_argmax_f32(hipStream_t s, const float* logits, int rows, int cols, int* out) {
     if (rows == 0) return hipSuccess;
     hipLaunchKernelGGL(vk_argmax_f32, dim3(rows), dim3(256), 0, s, logits, cols, out);
+    return hipGetLastError();
+}
+
+int argmax_n_slices(int cols) { return (cols + AM_SLICE - 1) / AM_SLICE; }
+
+hipError_t launch_argmax_sliced(hipStream_t s, const float* logits, int rows, int cols, float2* part, int* out) {
+    if (rows == 0) return hipSuccess;
+    if (cols < 1 || rows > 65535) return hipErrorInvalidValue;  // grid.y limit
+    const int n_sl = argmax_n_slices(cols);
+    hipLaunchKernelGGL(vk_argmax_slices, dim3((unsigned)n_sl, (unsigned)rows), dim3(256), 0, s, logits, cols, n_sl,
+                       part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(vk_argmax_parts, dim3((unsigned)rows), dim3(256), 0, s, part, n_sl, out);
     return hipGetLastError();
 }
 

@@ -239,35 +239,54 @@ __global__ void vk_repack_w_q4k(const uint8_t* __restrict__ wq, int n, int n_pad
 }
 
 // bf16 operand (4 values, K 4c..4c+3 of one group) from a nibble word:
-// pairs j0 and j0 + 1.
-__device__ __forceinline__ vk_s16x4 q4k_operand(uint32_t w, int j0) {
+// pairs j0 and j0 + 1. mask = 0x000F000F and magic = 0x43004300 come in
+// registers, so each half is one v_and_or_b32 (a three-operand instruction
+// cannot take literals on this architecture).
+__device__ __forceinline__ uint32_t q4k_and_or(uint32_t x, uint32_t mask, uint32_t magic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(mask), "v"(magic));
+    return r;
+}
+__device__ __forceinline__ vk_s16x4 q4k_operand(uint32_t w, int j0, uint32_t mask, uint32_t magic) {
     uint2 r;
-    r.x = ((w >> (4 * j0)) & 0x000F000Fu) | 0x43004300u;
-    r.y = ((w >> (4 * j0 + 4)) & 0x000F000Fu) | 0x43004300u;
+    r.x = q4k_and_or(w >> (4 * j0), mask, magic);
+    r.y = q4k_and_or(w >> (4 * j0 + 4), mask, magic);
     return __builtin_bit_cast(vk_s16x4, r);
 }
 
 // ---------------------------------------------------------------------------
-// Matmul, one workgroup of 8 waves per 16 x 16 output tile (16 activation
+// Matmul, one workgroup of 12 waves per 16 x 16 output tile (16 activation
 // rows, 16 weight rows), K in chunks of two super-blocks (32 groups).
 //
 // The reference combine is, per output, acc += s * (d_eff * isum - m_eff *
 // gsum) over the groups in order. Only the final add is a dependent chain;
 // the term t = s * (d_eff * isum - m_eff * gsum) (four roundings) depends on
 // one group alone. So:
-//   phase 1 (chunk c+1): wave w takes 4 groups of the chunk; per group one
+//   phase 1 (chunk c): wave w takes 4 groups of the chunk; per group one
 //     16x16x16 MFMA with accumulator input -128 * gsum (removing the +128 of
 //     the bf16 nibble trick) gives isum exactly for 4 outputs per lane (the
 //     4 MFMAs are issued before any of their results is used), and the lane
 //     turns them into the 4 terms with the reference's roundings; the terms
-//     go to the LDS buffer of chunk c+1;
-//   phase 2 (chunk c): thread t of waves 0..3 adds the chunk's 32 terms of
-//     its output to acc, in group order;
-//   one barrier per chunk: chunk c+1's terms are complete, chunk c's free.
-// Term buffer layout per group: output (row, col) at (col / 4) * 64 + row * 4
-// + col % 4, so a wave's float4 stores (lane l: row l % 16, cols 4 (l / 16)
-// ..+3) cover 256 consecutive floats and phase 2's thread t reads float t:
-// no bank conflicts on either side.
+//     go to the LDS buffer of chunk c;
+//   phase 2 (chunk c - 1): thread t of waves 8..11 adds the chunk's 32
+//     terms of its output to acc, in group order;
+//   one barrier per chunk: chunk c's terms are complete, chunk c - 1's free.
+// Waves 0..7 only form terms and waves 8..11 only add, so each SIMD runs two
+// term waves and one adding wave: the dependent adds of chunk c - 1 overlap
+// the term arithmetic of chunk c instead of following it.
+// Lane mapping: activations are the MFMA's A operand and weights its B
+// operand, so lane l holds rows 4 (l / 16) .. +3 of weight column l % 16.
+// Each 16-lane DPP row then needs the same 16 activation scales and 16 group
+// sums (4 rows x 4 groups): every lane loads one of each (a wave reads 256
+// contiguous bytes per array) and the values reach their users through
+// row_newbcast DPP operands of the multiplies themselves, and a lane's own
+// column needs only its two (d_eff, m_eff) pairs: 2 + 2 + 8 + 8 bytes per lane
+// of broadcast data instead of 96, which keeps the texture path off the
+// critical path.
+// Term buffer layout per group: the float4 of lane l (its 4 rows) at 4 l, so
+// a wave's stores cover 256 consecutive floats, and phase 2's thread t
+// (t = thread index - 512) reads float t, the output (row 4 (t / 64) + t % 4,
+// column (t / 4) % 16): no bank conflicts on either side.
 // Operands are loaded two chunks ahead into two register sets, each load a
 // wave-uniform base plus a 32-bit lane offset (a chunk past the end loads the
 // last super-block again, unused). Up to three linears over the same
@@ -280,16 +299,21 @@ constexpr int CHS = 2;   // super-blocks per chunk
 struct Pipe {
     uint2 wv;            // nibble words of this wave's 4 groups
     uint4 af[2];         // activation fragments of its 4 groups (2 pairs)
-    float4 s, a;         // s and gsum of this lane's row for its 4 groups
-    float4 dm[2][2];     // [sub-block][half]: (d_eff, m_eff) of cols rq + 2 half, +1
+    float s, a;          // one of the DPP row's 16 scales / group sums
+    float2 dm[2];        // [sub-block]: (d_eff, m_eff) of this lane's column
 };
+// lane J of each 16-lane row, to every lane of that row
+template <int J>
+__device__ __forceinline__ float row_bcast(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x150 + J, 0xf, 0xf, true));
+}
 }  // namespace kq
 
-__global__ __launch_bounds__(512) void vk_gemm_q4k(const uint4* __restrict__ afrag, const float* __restrict__ ascale,
+__global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afrag, const float* __restrict__ ascale,
                                                    const float* __restrict__ asum, VkQ4kSet set, int m, int nsb,
                                                    int m_pad) {
     using namespace kq;
-    __shared__ __align__(16) float lds_t[2][CHG][256];  // terms, [chunk parity][group][(col/4)*64 + row*4 + col%4]
+    __shared__ __align__(16) float lds_t[2][CHG][256];  // terms, [chunk parity][group][4 * lane + r]
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar load bases
@@ -298,110 +322,168 @@ __global__ __launch_bounds__(512) void vk_gemm_q4k(const uint4* __restrict__ afr
     const int li = (set.count > 2 && bx >= set.tile0[2]) ? 2 : (set.count > 1 && bx >= set.tile0[1]) ? 1 : 0;
     const VkQ4kLin L = li == 2 ? set.l[2] : li == 1 ? set.l[1] : set.l[0];
     const int nt = bx - (li == 2 ? set.tile0[2] : li == 1 ? set.tile0[1] : 0);
-    const int row_l = lane & 15, rq = 4 * (lane >> 4);  // MFMA lane: activation row, first weight column
-    const int q4 = wave & 3, sbw = wave >> 2;           // this wave's quarter of a super-block, and which one
+    const int q4 = wave & 3, sbw = (wave >> 2) & 1;  // a term wave's quarter of a super-block, and which one
     const int n_chunk = (nsb + CHS - 1) / CHS;
-    // phase-2 thread: waves 0..3, output (row, col) of the term layout
-    const int orow = (tid >> 2) & 15, ocol = 4 * (tid >> 6) + (tid & 3);
-    const bool owner = wave < 4;
+    // phase-2 thread: waves 8..11, output (row, col) of the term layout
+    const int ot = tid - 512;
+    const int orow = 4 * (ot >> 6) + (ot & 3), ocol = (ot >> 2) & 15;
+    const bool owner = wave >= 8;
 
     // per-lane byte offsets (constant over the K loop)
     const uint32_t vo_w = lane * 32 + 8 * q4;
     const uint32_t vo_a = lane * 16;
-    const uint32_t vo_d = rq * 8;
-    const uint32_t vo_s = (uint32_t)(mt * 16 + row_l) * 16;
+    const uint32_t vo_d = (lane & 15) * 8;
+    const uint32_t vo_s = (uint32_t)(mt * 16) * 16 + lane * 4;
+
+    // Buffer resources over the five operand arrays: every load is a
+    // constant per-lane offset plus a wave-uniform offset computed on the
+    // scalar unit, so no vector instruction forms an address in the K loop.
+    const int n_pad = (L.n + 15) & ~15;
+    const int rsrc_w3 = 0x00020000;  // raw (unswizzled) dword access
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)L.wq4, 0, n_pad * nsb * 128, rsrc_w3);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)L.wdm, 0, n_pad * nsb * 64, rsrc_w3);
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)afrag, 0, m_pad * nsb * 512, rsrc_w3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)ascale, 0, m_pad * nsb * 64, rsrc_w3);
+    const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc((void*)asum, 0, m_pad * nsb * 64, rsrc_w3);
+    typedef unsigned int vk_u32x2 __attribute__((ext_vector_type(2)));
+    typedef unsigned int vk_u32x4 __attribute__((ext_vector_type(4)));
 
     // chunk c's operands for this wave (super-block 2c + sbw, clamped into
     // the tensor: a super-block past the end loads the last one, unused).
     auto load = [&](int c) -> Pipe {
         Pipe p;
         const int sb = min(c * CHS + sbw, nsb - 1);
-        const char* bw = reinterpret_cast<const char*>(L.wq4) + (size_t)((nt * nsb + sb) * 64) * 32;
-        const char* ba = reinterpret_cast<const char*>(afrag) + (size_t)(((mt * nsb + sb) * 8 + 2 * q4) * 64) * 16;
-        const size_t so_s = (size_t)(sb * (NG / 4) + q4) * m_pad * 16;
-        const char* bs = reinterpret_cast<const char*>(ascale) + so_s;
-        const char* bg = reinterpret_cast<const char*>(asum) + so_s;
-        const char* bd = reinterpret_cast<const char*>(L.wdm) + (size_t)((nt * nsb + sb) * 8 + 2 * q4) * 128;
-        p.wv = *reinterpret_cast<const uint2*>(bw + vo_w);
+        const int ow = ((nt * nsb + sb) * 64) * 32;
+        const int oa = (((mt * nsb + sb) * 8 + 2 * q4) * 64) * 16;
+        // scales / sums of groups 4 q4 .. +3 of rows mt*16 .. +15: 256 bytes,
+        // lane 16 k + j holding row 4 k + j / 4, group j % 4
+        const int os = (sb * (NG / 4) + q4) * m_pad * 16;
+        const int od = ((nt * nsb + sb) * 8 + 2 * q4) * 128;
+        const vk_u32x2 w2 = __builtin_amdgcn_raw_buffer_load_b64(rw, vo_w, ow, 0);
+        p.wv = make_uint2(w2.x, w2.y);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) p.af[h] = *reinterpret_cast<const uint4*>(ba + vo_a + h * 1024);
-        p.s = *reinterpret_cast<const float4*>(bs + vo_s);
-        p.a = *reinterpret_cast<const float4*>(bg + vo_s);
+        for (int h = 0; h < 2; ++h) {
+            const vk_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(ra, vo_a + h * 1024, oa, 0);
+            p.af[h] = make_uint4(x.x, x.y, x.z, x.w);
+        }
+        p.s = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vo_s, os, 0));
+        p.a = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, vo_s, os, 0));
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) p.dm[jj][h] = *reinterpret_cast<const float4*>(bd + vo_d + jj * 128 + h * 16);
+        for (int jj = 0; jj < 2; ++jj) {
+            const vk_u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rd, vo_d + jj * 128, od, 0);
+            p.dm[jj] = make_float2(__uint_as_float(x.x), __uint_as_float(x.y));
+        }
         return p;
     };
-    // phase 1: the terms of this wave's 4 groups of chunk c into buffer par
-    auto terms = [&](const Pipe& p, int c, int par) {
-        if (c * CHS + sbw >= nsb) return;  // a chunk with one super-block: waves 4..7 idle
-        const float sv[4] = {p.s.x, p.s.y, p.s.z, p.s.w}, av[4] = {p.a.x, p.a.y, p.a.z, p.a.w};
+    // phase 1: the terms of this wave's 4 groups into buffer par (for a
+    // super-block past the end the terms come from the clamped loads and
+    // phase 2 never reads them)
+    // -128 in a register: a literal operand would keep the multiply that
+    // forms the MFMA's accumulator input from taking its DPP operand
+    float m128;
+    asm volatile("v_mov_b32 %0, 0xc3000000" : "=v"(m128));
+    uint32_t nib_mask, nib_magic;
+    asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(nib_mask));
+    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(nib_magic));
+    auto terms = [&](const Pipe& p, int par) {
         vk_f32x4 isum[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t word = (i < 2) ? p.wv.x : p.wv.y;
-            const vk_s16x4 w = q4k_operand(word, 2 * (i & 1));
-            const uint4 a4 = p.af[i >> 1];
-            const uint2 ap = (i & 1) ? make_uint2(a4.z, a4.w) : make_uint2(a4.x, a4.y);
-            const float c0 = -128.0f * av[i];
-            const vk_f32x4 cin = {c0, c0, c0, c0};
-            // transposed product: weights as the A operand, so lane l gets
-            // activation row l % 16, columns rq..rq+3
-            isum[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(w, __builtin_bit_cast(vk_s16x4, ap), cin, 0, 0, 0);
+        // a second register with the sums, so the accumulator inputs and the
+        // terms read them through separate DPP operands (one shared
+        // broadcast copy would cost a move per use)
+        float ac;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(ac) : "v"(p.a));
+        // group i: the scale and sum of row 4 k + r sit in lane 4 r + i of
+        // DPP row k
+#define VK_Q4K_MFMA(i)                                                                                          \
+        {                                                                                                       \
+            const vk_s16x4 w = q4k_operand((i) < 2 ? p.wv.x : p.wv.y, 2 * ((i) & 1), nib_mask, nib_magic);      \
+            const uint4 a4 = p.af[(i) >> 1];                                                                    \
+            const uint2 ap = ((i) & 1) ? make_uint2(a4.z, a4.w) : make_uint2(a4.x, a4.y);                       \
+            const vk_f32x4 cin = {row_bcast<(i)>(ac) * m128, row_bcast<4 + (i)>(ac) * m128,                      \
+                                  row_bcast<8 + (i)>(ac) * m128, row_bcast<12 + (i)>(ac) * m128};               \
+            isum[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(vk_s16x4, ap), w, cin, 0, 0, 0); \
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 d01 = p.dm[i >> 1][0], d23 = p.dm[i >> 1][1];  // (d, m) of cols rq .. rq + 3
-            const float s = sv[i], a = av[i];
-            float4 t;
-            t.x = s * (d01.x * isum[i][0] - d01.y * a);
-            t.y = s * (d01.z * isum[i][1] - d01.w * a);
-            t.z = s * (d23.x * isum[i][2] - d23.y * a);
-            t.w = s * (d23.z * isum[i][3] - d23.w * a);
-            *reinterpret_cast<float4*>(&lds_t[par][16 * sbw + 4 * q4 + i][4 * lane]) = t;
+        VK_Q4K_MFMA(0) VK_Q4K_MFMA(1) VK_Q4K_MFMA(2) VK_Q4K_MFMA(3)
+#undef VK_Q4K_MFMA
+        // The 16 terms of the wave's 4 groups breadth first, one rounding step
+        // at a time over all of them (the issue order is pinned): each step's
+        // 16 operations are independent, so no multiply waits on the one
+        // before it.
+        float x[4][4], y[4][4];
+#define VK_Q4K_STEP1(i)                                                                                         \
+        {                                                                                                       \
+            const float2 dm = p.dm[(i) >> 1];                                                                   \
+            x[i][0] = dm.x * isum[i][0]; x[i][1] = dm.x * isum[i][1];                                           \
+            x[i][2] = dm.x * isum[i][2]; x[i][3] = dm.x * isum[i][3];                                           \
+            y[i][0] = dm.y * row_bcast<(i)>(p.a); y[i][1] = dm.y * row_bcast<4 + (i)>(p.a);                     \
+            y[i][2] = dm.y * row_bcast<8 + (i)>(p.a); y[i][3] = dm.y * row_bcast<12 + (i)>(p.a);                \
         }
+        VK_Q4K_STEP1(0) VK_Q4K_STEP1(1) VK_Q4K_STEP1(2) VK_Q4K_STEP1(3)
+#undef VK_Q4K_STEP1
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x[i][r] = x[i][r] - y[i][r];
+        __builtin_amdgcn_sched_barrier(0);
+#define VK_Q4K_STEP3(i)                                                                                         \
+        {                                                                                                       \
+            float4 t;                                                                                           \
+            t.x = row_bcast<(i)>(p.s) * x[i][0]; t.y = row_bcast<4 + (i)>(p.s) * x[i][1];                        \
+            t.z = row_bcast<8 + (i)>(p.s) * x[i][2]; t.w = row_bcast<12 + (i)>(p.s) * x[i][3];                  \
+            *reinterpret_cast<float4*>(&lds_t[par][16 * sbw + 4 * q4 + (i)][4 * lane]) = t;                     \
+        }
+        VK_Q4K_STEP3(0) VK_Q4K_STEP3(1) VK_Q4K_STEP3(2) VK_Q4K_STEP3(3)
+#undef VK_Q4K_STEP3
     };
     // phase 2: the ordered adds of chunk c (waves 0..3, one output per thread)
     float acc = 0.0f;
     auto chain = [&](int c, int par) {
-        if (!owner) return;
+        if (c < 0 || c >= n_chunk) return;
         const int ng = min(CHS, nsb - c * CHS) * NG;
         if (ng == CHG) {
 #pragma unroll
-            for (int g = 0; g < CHG; ++g) acc += lds_t[par][g][tid];
+            for (int g = 0; g < CHG; ++g) acc += lds_t[par][g][ot];
         } else {
 #pragma unroll
-            for (int g = 0; g < NG; ++g) acc += lds_t[par][g][tid];
+            for (int g = 0; g < NG; ++g) acc += lds_t[par][g][ot];
         }
     };
 
-    Pipe pa = load(0);
-    Pipe pb = load(n_chunk > 1 ? 1 : 0);
-    terms(pa, 0, 0);
-    if (n_chunk > 2) pa = load(2);
-    VK_LDS_BARRIER();
-    for (int c = 0; c < n_chunk; c += 2) {
-        if (c + 1 < n_chunk) {
-            terms(pb, c + 1, 1);
-            if (c + 3 < n_chunk) pb = load(c + 3);
+    // The term waves issue every load unconditionally (chunks past the end
+    // re-read the last super-block) and from one place, their loop body, so
+    // the two register sets are refilled in the same order from the first
+    // chunk on: loads issued on one side of a branch, or in another order
+    // before the loop, make the compiler wait for all outstanding loads,
+    // which would drain the next chunk's prefetch before each term pass. The
+    // loop starts one step early (c = -2, an opaque value so it is not peeled
+    // off) to issue the first two chunks' loads; each term pass then waits
+    // for its own register set only. Both loops pass the same barriers.
+    int c0;
+    asm volatile("s_mov_b32 %0, -2" : "=s"(c0));
+    if (!owner) {
+        Pipe pa{}, pb{};
+        for (int c = c0; c < n_chunk; c += 2) {
+            if (c >= 0) terms(pa, 0);  // chunk c
+            pa = load(c + 2);
+            VK_LDS_BARRIER();
+            if (c >= 0) terms(pb, 1);  // chunk c + 1
+            pb = load(c + 3);
+            VK_LDS_BARRIER();
         }
+        return;
+    }
+    for (int c = c0; c < n_chunk; c += 2) {
+        chain(c - 1, 1);
+        VK_LDS_BARRIER();
         chain(c, 0);
         VK_LDS_BARRIER();
-        if (c + 1 >= n_chunk) break;
-        if (c + 2 < n_chunk) {
-            terms(pa, c + 2, 0);
-            if (c + 4 < n_chunk) pa = load(c + 4);
-        }
-        chain(c + 1, 1);
-        VK_LDS_BARRIER();
     }
-    if (owner) {
-        const int r = mt * 16 + orow, col = nt * 16 + ocol;
-        if (r < m && col < L.n) {
-            const size_t o = (size_t)r * L.n + col;
-            L.out[o] = vk_epi_apply(L.bias ? acc + L.bias[col] : acc, L.epi, o);
-        }
+    chain(((n_chunk + 1) & ~1) - 1, 1);  // an even count leaves its last chunk
+    const int r = mt * 16 + orow, col = nt * 16 + ocol;
+    if (r < m && col < L.n) {
+        const size_t o = (size_t)r * L.n + col;
+        L.out[o] = vk_epi_apply(L.bias ? acc + L.bias[col] : acc, L.epi, o);
     }
 }
 
@@ -465,7 +547,7 @@ hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascal
     }
     set.count = n_lin;
     const dim3 grid((unsigned)tiles, (unsigned)((m + 15) / 16));
-    hipLaunchKernelGGL(vk_gemm_q4k, grid, dim3(512), 0, s, afrag, ascale, asum, set, m, nsb, m_pad);
+    hipLaunchKernelGGL(vk_gemm_q4k, grid, dim3(768), 0, s, afrag, ascale, asum, set, m, nsb, m_pad);
     return hipGetLastError();
 }
 

@@ -208,6 +208,10 @@ hipError_t launch_add_f32(hipStream_t s, const float* a, const float* b, float* 
 hipError_t launch_embed_f32(hipStream_t s, const float* tok_emb, const float* pos_emb, const int* tokens,
                             const int* positions, int vocab, int n_pos, int d, int rows, float* out);
 hipError_t launch_argmax_f32(hipStream_t s, const float* logits, int rows, int cols, int* out);
+// The same argmax over 2048-column slices (many workgroups per row): part
+// holds rows * argmax_n_slices(cols) pairs; rows at most 65535.
+int argmax_n_slices(int cols);
+hipError_t launch_argmax_sliced(hipStream_t s, const float* logits, int rows, int cols, float2* part, int* out);
 // Fused tied logits + argmax: d a multiple of 128 (an even number of 16-wide
 // k chunks in each of the kernel's four d quarters), rows of x and emb
 // 16-byte aligned; logits may be null. part holds rows * logits_n_vt(vocab)

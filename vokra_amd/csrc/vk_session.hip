@@ -337,7 +337,9 @@ int dec_setup(vokra_hip_decoder* m, const vokra_hip_decoder_layer_t* layers, con
     for (DBuf* b : {&m->h, &m->x, &m->q, &m->k, &m->v, &m->attn}) SS_TRY(b->alloc(c, rd));
     SS_TRY(m->f.alloc(c, rows * ff * sizeof(float)));
     SS_TRY(m->logits.alloc(c, rows * m->vocab * sizeof(float)));
-    SS_TRY(m->lpart.alloc(c, rows * (size_t)vk::logits_n_vt((int)m->vocab) * sizeof(float2)));
+    // (max, index) pairs of the fused logits pass or of the sliced argmax
+    SS_TRY(m->lpart.alloc(c, rows * (size_t)std::max(vk::logits_n_vt((int)m->vocab), vk::argmax_n_slices((int)m->vocab)) *
+                                 sizeof(float2)));
     SS_TRY(m->lens.alloc(c, rows * sizeof(int)));
     SS_TRY(m->kvidx.alloc(c, m->n_layer * rows * sizeof(int)));
     SS_TRY(m->next.alloc(c, rows * sizeof(int)));
@@ -435,7 +437,9 @@ int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_
     }
     float* lg = d_logits ? d_logits : m->logits.f();
     SS_TRY(vokra_hip_gemm_f32_dev(c, n, m->vocab, d, m->x.f(), m->tok_emb.f(), 1, nullptr, lg));
-    return vokra_hip_argmax_f32_dev(c, lg, n, m->vocab, d_next);
+    SS_HIP(vk::launch_argmax_sliced(s, lg, (int)n, (int)m->vocab, (float2*)m->lpart.p, d_next),
+           "launch(vk_argmax_slices)");
+    return VOKRA_HIP_OK;
 }
 
 }  // namespace
@@ -801,7 +805,9 @@ int td_setup(vokra_hip_text_decoder* m, const vokra_hip_text_decoder_layer_t* la
     SS_TRY(m->g.alloc(c, rows * ff * sizeof(float)));
     SS_TRY(m->u.alloc(c, rows * ff * sizeof(float)));
     SS_TRY(m->logits.alloc(c, rows * m->vocab * sizeof(float)));
-    SS_TRY(m->lpart.alloc(c, rows * (size_t)vk::logits_n_vt((int)m->vocab) * sizeof(float2)));
+    // (max, index) pairs of the fused logits pass or of the sliced argmax
+    SS_TRY(m->lpart.alloc(c, rows * (size_t)std::max(vk::logits_n_vt((int)m->vocab), vk::argmax_n_slices((int)m->vocab)) *
+                                 sizeof(float2)));
     SS_TRY(m->lens.alloc(c, rows * sizeof(int)));
     SS_TRY(m->next.alloc(c, rows * sizeof(int)));
     SS_TRY(m->stage.alloc(c, 3 * rows * sizeof(int)));
@@ -879,7 +885,9 @@ int td_step(vokra_hip_text_decoder* m, size_t n, const int* d_streams, const int
         SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->x.f(), act));
         float* lg = d_logits ? d_logits : m->logits.f();
         SS_TRY(m->lm_head.run(c, m->qa_d, lg));
-        return vokra_hip_argmax_f32_dev(c, lg, n, m->vocab, d_next);
+        SS_HIP(vk::launch_argmax_sliced(s, lg, (int)n, (int)m->vocab, (float2*)m->lpart.p, d_next),
+               "launch(vk_argmax_slices)");
+        return VOKRA_HIP_OK;
     }
     if (d % vk::logits_d_multiple() == 0) {
         SS_HIP(vk::launch_logits_argmax(s, m->x.f(), m->tok_emb.f(), d_logits, (float2*)m->lpart.p, d_next, (int)n,
@@ -889,7 +897,9 @@ int td_step(vokra_hip_text_decoder* m, size_t n, const int* d_streams, const int
     }
     float* lg = d_logits ? d_logits : m->logits.f();
     SS_TRY(vokra_hip_gemm_f32_dev(c, n, m->vocab, d, m->x.f(), m->tok_emb.f(), 1, nullptr, lg));
-    return vokra_hip_argmax_f32_dev(c, lg, n, m->vocab, d_next);
+    SS_HIP(vk::launch_argmax_sliced(s, lg, (int)n, (int)m->vocab, (float2*)m->lpart.p, d_next),
+           "launch(vk_argmax_slices)");
+    return VOKRA_HIP_OK;
 }
 
 }  // namespace
