@@ -481,7 +481,7 @@ int kv_append_status(vokra_hip_kv* kv, size_t n, const int* h_streams, const int
 int run_paged_attn(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                    const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
                    const VkQOut* qo = nullptr, const float* d_ak = nullptr, const float* d_av = nullptr,
-                   const int* d_at = nullptr) {
+                   const int* d_at = nullptr, const float2* rope_cs = nullptr) {
     // each item splits its keys by its own length (at most 8 splits of >= 512
     // keys), so its results never depend on the rest of the batch
     const int n_split = vk::paged_attn_grid_splits((int)std::min<size_t>(max_len ? max_len : 1, kv->max_time));
@@ -491,7 +491,7 @@ int run_paged_attn(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, c
     }
     VK_TRY(vk::launch_paged_attn(c->stream, kv->view(), (int)layer, (int)n, d_streams, d_lens, d_q, scale, (int)hq,
                                  (int)kv->d_head, n_split, d_out, (float*)kv->part_ml.p, (float*)kv->part_o.p,
-                                 qo, d_ak, d_av, d_at),
+                                 qo, d_ak, d_av, d_at, rope_cs),
            "launch(vk_paged_attn)");
     return VOKRA_HIP_OK;
 }
@@ -747,9 +747,41 @@ int attn_quantize(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t 
     return VOKRA_HIP_OK;
 }
 
+bool paged_attn_rotates_q(const vokra_hip_kv* kv, size_t n, size_t hq, const float* d_q, const float* d_out) {
+    // part_o is 16-byte aligned whenever it is allocated (hipMalloc)
+    (void)n;
+    return kv && vk::paged_attn_rotates_q(kv->view(), (int)hq, (int)kv->d_head, d_q, d_out, nullptr);
+}
+
 int paged_attn_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                         const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
-                        vokra_hip_qact* qa, int act_quant) {
+                        vokra_hip_qact* qa, int act_quant, const float2* rope_cs) {
+    if (rope_cs && act_quant != VOKRA_HIP_ACT_KQUANT)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn_quantize: the fused rotation needs K-quant activations");
+    if (act_quant == VOKRA_HIP_ACT_KQUANT && kv && kv->ctx == c) {
+        // the K-quant activation pass runs inside the split combine (or as
+        // its own launch when no item splits)
+        const size_t k = hq * kv->d_head;
+        int st = qact_g16_prepare(c, qa, n, k, "paged_attn_quantize");
+        if (st) return st;
+        st = check_paged_attn(kv, layer, n, hq);
+        if (st) return st;
+        if (!d_streams || !d_lens || !d_q || !d_out)
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn: NULL buffer");
+        if (max_len > kv->max_time) max_len = kv->max_time;
+        const size_t m_pad = round_up(n, 16);
+        const VkQOut qo{(uint4*)qa->frag.p, (float*)qa->scale.p, (float*)qa->gsum.p, (int)m_pad, (int)k, 0, 1};
+        if (rope_cs && !paged_attn_rotates_q(kv, n, hq, d_q, d_out))
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn_quantize: no fused rotation for this shape");
+        st = run_paged_attn(c, kv, layer, n, d_streams, d_lens, max_len, hq, d_q, scale, d_out, &qo, nullptr,
+                            nullptr, nullptr, rope_cs);
+        if (st) return st;
+        qa->m = n;
+        qa->k = k;
+        qa->m_pad = m_pad;
+        qa->act_quant = VOKRA_HIP_ACT_KQUANT;
+        return VOKRA_HIP_OK;
+    }
     VkQOut qo;
     int st = qact_bind(c, qa, n, act_quant, &qo);
     if (st) return st;
@@ -814,13 +846,14 @@ int kv_alloc_layers(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t first_layer, size
 }
 
 int kv_write_allocated(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
-                       const int* d_times, const float* d_k, const float* d_v) {
+                       const int* d_times, const float* d_k, const float* d_v, const float2* rope_cs) {
     if (!c || !kv || kv->ctx != c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: bad context or cache");
     if (layer >= kv->n_layer || n > 65535)
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: layer %zu of %zu, %zu items", layer, kv->n_layer, n);
     if (n && (!d_streams || !d_times || !d_k || !d_v)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kv_append: NULL buffer");
     VK_TRY(set_dev(c), "hipSetDevice");
-    VK_TRY(vk::launch_kv_write_allocated(c->stream, kv->view(), (int)layer, (int)n, d_streams, d_times, d_k, d_v),
+    VK_TRY(vk::launch_kv_write_allocated(c->stream, kv->view(), (int)layer, (int)n, d_streams, d_times, d_k, d_v,
+                                         rope_cs, (int)kv->d_head),
            "launch(vk_kv_write_allocated)");
     return VOKRA_HIP_OK;
 }

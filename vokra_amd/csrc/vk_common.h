@@ -85,6 +85,18 @@ __device__ __forceinline__ uint32_t vk_int_to_bf16_bits(int v) {
 // Rust `f32::round` (half away from zero) — roundf is exactly that.
 __device__ __forceinline__ float vk_round_half_away(float x) { return roundf(x); }
 
+// The half-split rotation of one pair (a = x[j], b = x[j + hd / 2]) with
+// cs = (cos, sin) of its angle, as rope_apply forms it: the four products,
+// then x[j] = a c - b s and x[j + hd / 2] = a s + b c.
+__device__ __forceinline__ float vk_rope_lo(float a, float b, float2 cs) {
+    const float ac = a * cs.x, bs = b * cs.y;
+    return ac - bs;
+}
+__device__ __forceinline__ float vk_rope_hi(float a, float b, float2 cs) {
+    const float as = a * cs.y, bc = b * cs.x;
+    return as + bc;
+}
+
 // A finite f32 whose fp16 rounding is infinite (|x| >= 65520): the fp16
 // hi / lo operands of the attention kernels cannot represent it.
 __device__ __forceinline__ bool vk_f16_overflow(float x) {

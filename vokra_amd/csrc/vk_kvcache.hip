@@ -273,9 +273,12 @@ __global__ void vk_kv_write(KvDev c, int layer, int n, const int* __restrict__ s
 // page that an earlier vk_kv_alloc_layers launch gave (layer, times[i] /
 // block_size); items whose entry is empty (allocation failed) or out of range
 // are skipped. Same packing as vk_kv_write. One thread per (item, element).
+// rope_cs (optional): [n][hd / 2] (cos, sin) of each item's position; k is
+// then rotated (head size hd) on the way into the cache, as a RoPE pass over
+// k before the write would leave it.
 __global__ void vk_kv_write_allocated(KvDev c, int layer, int n, const int* __restrict__ streams,
                                       const int* __restrict__ times, const float* __restrict__ k,
-                                      const float* __restrict__ v) {
+                                      const float* __restrict__ v, const float2* __restrict__ rope_cs, int hd) {
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int e = (int)(gid % (size_t)c.width);
     const int item = (int)(gid / (size_t)c.width);
@@ -293,6 +296,12 @@ __global__ void vk_kv_write_allocated(KvDev c, int layer, int n, const int* __re
     if (live) {
         kv = k[(size_t)item * c.width + e];
         vv = v[(size_t)item * c.width + e];
+        if (rope_cs) {
+            const int half = hd >> 1, j = e % hd, jj = j % half;
+            const float2 cs = rope_cs[(size_t)item * half + jj];
+            if (j < half) kv = vk_rope_lo(kv, k[(size_t)item * c.width + e + half], cs);
+            else kv = vk_rope_hi(k[(size_t)item * c.width + e - half], kv, cs);
+        }
     }
     int8_t qk, qv;
     uint16_t dk = 0, dv = 0;
@@ -737,7 +746,8 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
                                                          const int* __restrict__ lens, const float* __restrict__ q,
                                                          float scale, int hq, int n_split,
                                                          float* __restrict__ out, float* __restrict__ part_ml,
-                                                         float* __restrict__ part_o) {
+                                                         float* __restrict__ part_o,
+                                                         const float2* __restrict__ rope_cs) {
     using namespace pg;
     static_assert(G >= 2 && G <= 16, "query heads per kv head");
     __shared__ __align__(16) _Float16 lvt[WAVES][HD][VROW];  // per wave: V^T of its tile (reused by the merge)
@@ -753,21 +763,40 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
     const int k0 = split * kps, k1 = min(len, k0 + kps);
 
     // q * scale of head hh (zero for padding heads) as the S^T B operand:
-    // lane (g, hh) holds dims 32b + 8g .. +7, split into fp16 hi + lo
+    // lane (g, hh) holds dims 32b + 8g .. +7, split into fp16 hi + lo. With
+    // rope_cs, q is first rotated: dims j and j + 64 (blocks b and b + 2) sit
+    // in the same lane.
     vk_h16x8_t qh[NB], ql[NB];
+    float x[NB][8];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        float x[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[b][i] = 0.0f;
         if (hh < G) {
             const float4* qp =
                 reinterpret_cast<const float4*>(q + ((size_t)item * hq + hk * G + hh) * HD + 32 * b + 8 * g);
             const float4 u = qp[0], v = qp[1];
-            x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
-            x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
+            x[b][0] = u.x; x[b][1] = u.y; x[b][2] = u.z; x[b][3] = u.w;
+            x[b][4] = v.x; x[b][5] = v.y; x[b][6] = v.z; x[b][7] = v.w;
         }
+    }
+    if (rope_cs && hh < G) {
+        static_assert(NB == 4, "the rotation pairs blocks b and b + 2");
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float2 cs = rope_cs[(size_t)item * (HD / 2) + 32 * b + 8 * g + i];
+                const float a = x[b][i], bb = x[b + 2][i];
+                x[b][i] = vk_rope_lo(a, bb, cs);
+                x[b + 2][i] = vk_rope_hi(a, bb, cs);
+            }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float xs = x[i] * scale;
+            const float xs = x[b][i] * scale;
             if (vk_f16_overflow(xs)) atomicOr(&vk_kv_range_flag, 1u);
             const _Float16 h = (_Float16)xs;
             qh[b][i] = h;
@@ -1020,25 +1049,63 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
 // Merges split partials: m = max m_s, O = sum O_s e^(m_s - m), l likewise,
 // over the item's own pa_splits(len) splits (partials at stride n_split);
 // items with one split were written whole by the attention kernel.
-template <int HD>
+template <int HD, bool Q16>
 __global__ void vk_paged_attn_combine(int n_split, int hq, const int* __restrict__ lens, int max_time,
                                       const float* __restrict__ part_ml, const float* __restrict__ part_o,
-                                      float* __restrict__ out) {
+                                      float* __restrict__ out, const VkQOut qo) {
     const size_t ih = blockIdx.x;  // (item, head)
     const int e = threadIdx.x;
     const int nsp = pa_splits(min(lens[ih / hq], max_time));
-    if (nsp == 1) return;
-    float m = -INFINITY;
-    for (int sp = 0; sp < nsp; ++sp) m = fmaxf(m, part_ml[2 * (ih * n_split + sp)]);
-    const float m_use = m == -INFINITY ? 0.0f : m;
-    float l = 0.0f, o = 0.0f;
-    for (int sp = 0; sp < nsp; ++sp) {
-        const size_t pi = ih * n_split + sp;
-        const float w = __expf(part_ml[2 * pi] - m_use);
-        l += part_ml[2 * pi + 1] * w;
-        if (e < HD) o += part_o[pi * HD + e] * w;
+    float v;
+    if (nsp == 1) {
+        if (!Q16) return;
+        v = out[ih * HD + e];  // written by the split kernel itself
+    } else {
+        float m = -INFINITY;
+        for (int sp = 0; sp < nsp; ++sp) m = fmaxf(m, part_ml[2 * (ih * n_split + sp)]);
+        const float m_use = m == -INFINITY ? 0.0f : m;
+        float l = 0.0f, o = 0.0f;
+        for (int sp = 0; sp < nsp; ++sp) {
+            const size_t pi = ih * n_split + sp;
+            const float w = __expf(part_ml[2 * pi] - m_use);
+            l += part_ml[2 * pi + 1] * w;
+            o += part_o[pi * HD + e] * w;
+        }
+        v = l > 0.0f ? o / l : 0.0f;
+        out[ih * HD + e] = v;
     }
-    if (e < HD) out[ih * HD + e] = l > 0.0f ? o / l : 0.0f;
+    if constexpr (Q16) {
+        // the K-quant activation pass over this head's slice of the output
+        // row: 16 consecutive threads hold one 16-wide group, quantized as
+        // vk_q16_store quantizes it (amax / 127, round half away, clamp,
+        // integer group sum)
+        const int row = (int)(ih / hq), h = (int)(ih % hq);
+        const int g = h * (HD / 16) + (e >> 4), t = e & 15;
+        float amax = fabsf(v);
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+        amax = fmaxf(0.0f, amax);
+        float sc = 0.0f;
+        int r = 0;
+        if (amax != 0.0f) {
+            sc = amax / 127.0f;
+            const float q = vk_round_half_away(v / sc);
+            r = (q != q) ? 0 : (int)fminf(fmaxf(q, -127.0f), 127.0f);
+        }
+        int gs = r;
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) gs += __shfl_xor(gs, o, 16);
+        const int nsb = qo.k / 256, mt = row >> 4, sb = g >> 4, gi = g & 15;
+        const size_t base = ((((size_t)mt * nsb + sb) * 8 + (gi >> 1)) * 64) * 2 + (gi & 1);
+        const int lane_f = (row & 15) + 16 * (t >> 2);
+        reinterpret_cast<uint16_t*>(qo.afrag)[(base + (size_t)lane_f * 2) * 4 + (t & 3)] =
+            (uint16_t)vk_int_to_bf16_bits(r);
+        if (t == 0) {
+            const size_t si = ((size_t)(g >> 2) * qo.m_pad + row) * 4 + (g & 3);
+            qo.ascale[si] = sc;
+            qo.asum[si] = (float)gs;
+        }
+    }
 }
 
 }  // namespace vk
@@ -1087,12 +1154,14 @@ hipError_t launch_kv_append(hipStream_t s, const KvView& v, int layer, int n, co
 }
 
 hipError_t launch_kv_write_allocated(hipStream_t s, const KvView& v, int layer, int n, const int* streams,
-                                    const int* times, const float* k, const float* vv) {
+                                    const int* times, const float* k, const float* vv, const float2* rope_cs,
+                                    int hd) {
     const KvDev c = kv_view(v);
     const size_t threads = (size_t)n * v.width;
     if (threads == 0) return hipSuccess;
+    if (rope_cs && (hd < 2 || hd % 2 != 0 || v.width % hd != 0)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(vk_kv_write_allocated, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, c, layer, n,
-                       streams, times, k, vv);
+                       streams, times, k, vv, rope_cs, hd);
     return hipGetLastError();
 }
 
@@ -1144,7 +1213,8 @@ hipError_t launch_kv_page_of(hipStream_t s, const KvView& v, int layer, int t, i
 template <int HD, int G>
 static bool go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* streams, const int* lens,
                   const float* q, float scale, int hq, int hkv, int n_split, float* out, float* pml,
-                  float* po, const VkQOut& qo, const float* ak, const float* av, const int* at) {
+                  float* po, const VkQOut& qo, const float* ak, const float* av, const int* at,
+                  const float2* rope_cs) {
     // head_dim 128 with several query heads per kv head: the matrix-core
     // kernel (its slots travel through 32-bit lane shuffles; it moves q and
     // O as float4)
@@ -1154,7 +1224,7 @@ static bool go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* st
     if constexpr (HD == pg::HD && G >= 2) {
         if (small_slots && aligned && !ak) {
             hipLaunchKernelGGL((vk_paged_attn_gqa<G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams,
-                               lens, q, scale, hq, n_split, out, pml, po);
+                               lens, q, scale, hq, n_split, out, pml, po, rope_cs);
             return false;
         }
     }
@@ -1170,18 +1240,29 @@ int paged_attn_grid_splits(int max_len) {
     return k < 1 ? 1 : (k > pa::MAX_SPLIT ? pa::MAX_SPLIT : k);
 }
 
+bool paged_attn_rotates_q(const KvView& v, int hq, int hd, const float* q, const float* out, const float* part_o) {
+    const int hkv = v.width / hd, g = hkv > 0 ? hq / hkv : 0;
+    const bool small_slots = (size_t)v.cap * v.bs * v.n_stream * hkv <= (size_t)INT32_MAX;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
+                           reinterpret_cast<uintptr_t>(part_o)) & 15) == 0;
+    return hd == pg::HD && (g == 2 || g == 4 || g == 8) && small_slots && aligned;
+}
+
 hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, const int* streams, const int* lens,
                              const float* q, float scale, int hq, int hd, int n_split, float* out,
                              float* part_ml, float* part_o, const VkQOut* qo, const float* ak, const float* av,
-                             const int* at) {
+                             const int* at, const float2* rope_cs) {
     const KvDev c = kv_view(v);
     const int hkv = v.width / hd, g = hq / hkv;
+    // the rotation of q rides only on the matrix-core GQA kernel
+    if (rope_cs && (ak || !paged_attn_rotates_q(v, hq, hd, q, out, part_o))) return hipErrorInvalidValue;
     const VkQOut qz = qo ? *qo : VkQOut{};
+    const VkQOut qb = qz.g16 ? VkQOut{} : qz;  // the split kernels' own fused pass is the 32-wide one
     bool fused = false;
 #define VK_PA(HDV, GV)                                                                                          \
     if (hd == HDV && g == GV) {                                                                                 \
         fused = go_pa<HDV, GV>(s, c, layer, n, streams, lens, q, scale, hq, hkv, n_split, out,                  \
-                               part_ml, part_o, qz, ak, av, at);                                                \
+                               part_ml, part_o, qb, ak, av, at, rope_cs);                                       \
     } else
     VK_PA(64, 1) VK_PA(64, 2) VK_PA(64, 4) VK_PA(64, 8) VK_PA(128, 1) VK_PA(128, 2) VK_PA(128, 4) VK_PA(128, 8) {
         return hipErrorInvalidValue;
@@ -1189,17 +1270,25 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
 #undef VK_PA
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // the K-quant activation pass rides on the combine (which then also reads
+    // back the rows of single-split items)
+    const bool g16 = qz.afrag && qz.g16;
     if (n_split > 1) {
-        if (hd == 64)
-            hipLaunchKernelGGL(vk_paged_attn_combine<64>, dim3((unsigned)(n * hq)), dim3(64), 0, s, n_split, hq, lens,
-                               c.max_time, part_ml, part_o, out);
-        else
-            hipLaunchKernelGGL(vk_paged_attn_combine<128>, dim3((unsigned)(n * hq)), dim3(128), 0, s, n_split, hq,
-                               lens, c.max_time, part_ml, part_o, out);
+#define VK_PA_COMBINE(HDV, QV)                                                                                  \
+        hipLaunchKernelGGL((vk_paged_attn_combine<HDV, QV>), dim3((unsigned)(n * hq)), dim3(HDV), 0, s, n_split, hq, \
+                           lens, c.max_time, part_ml, part_o, out, qz)
+        if (hd == 64) {
+            if (g16) VK_PA_COMBINE(64, true); else VK_PA_COMBINE(64, false);
+        } else {
+            if (g16) VK_PA_COMBINE(128, true); else VK_PA_COMBINE(128, false);
+        }
+#undef VK_PA_COMBINE
         e = hipGetLastError();
         if (e != hipSuccess) return e;
+        if (g16) return hipSuccess;
     }
     // kernels without the fused pass: the separate activation pass over out
+    if (g16) return launch_quantize_act_g16(s, out, n, qz.m_pad, qz.k, qz.afrag, qz.ascale, qz.asum);
     if (qz.afrag && !fused)
         return launch_quantize_act_b32(s, qz.pow2 != 0, out, n, qz.m_pad, qz.k, qz.afrag, qz.ascale, qz.asum);
     return hipSuccess;

@@ -22,6 +22,7 @@ struct VkQOut {
     int m_pad;  // the fragments' padded row count
     int k;      // the quantized row width (a multiple of 32)
     int pow2;   // the power-of-two scale convention
+    int g16;    // the K-quant layout instead: 16-wide groups (vk_q16_store), m_pad a multiple of 16
 };
 // One linear of a multi-linear block-GEMM launch: bf16 fragments + scales,
 // optional bias, output [m, n].
@@ -167,7 +168,13 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
                              // fused append: item i's K / V rows (ak, av [n][width]) at time at[i] are
                              // packed into pages allocated beforehand (distinct streams; the generic
                              // kernel runs every head shape then)
-                             const float* ak = nullptr, const float* av = nullptr, const int* at = nullptr);
+                             const float* ak = nullptr, const float* av = nullptr, const int* at = nullptr,
+                             // RoPE of q on load ([n][hd / 2] (cos, sin)): only where
+                             // paged_attn_rotates_q holds, and without a fused append
+                             const float2* rope_cs = nullptr);
+// Whether launch_paged_attn runs the matrix-core GQA kernel for this shape and
+// these buffers (the one that can rotate q on load).
+bool paged_attn_rotates_q(const KvView& v, int hq, int hd, const float* q, const float* out, const float* part_o);
 // The allocation of launch_kv_append for the same items appended to layers
 // layer0 .. layer0 + n_layers - 1 in that order, in one launch (n_layers * n <= 4096).
 // Read and clear the fp16-range flags of the attention kernels (vk_attn.hip)
@@ -176,8 +183,13 @@ hipError_t attn_range_take(hipStream_t s, unsigned* raised);
 hipError_t kv_range_take(hipStream_t s, unsigned* raised);
 // Packs rows into pages given by an earlier launch_kv_alloc_layers (items
 // whose page is missing are skipped).
+// rope_cs (optional, [n][hd / 2] (cos, sin)): k is rotated on the way in.
 hipError_t launch_kv_write_allocated(hipStream_t s, const KvView& v, int layer, int n, const int* streams,
-                                    const int* times, const float* k, const float* vv);
+                                    const int* times, const float* k, const float* vv,
+                                    const float2* rope_cs = nullptr, int hd = 0);
+// cs[r][j] = (cos, sin) of positions[r] * theta[j], j < half: the angles of
+// launch_rope_rows_qk for one step, for the fused rotations.
+hipError_t launch_rope_table(hipStream_t s, const int* positions, const float* theta, int rows, int half, float2* cs);
 // RoPE in place over x [rows][n_head * hd]: row r at positions[r] (or
 // pos_offset + r when positions is NULL), theta [hd / 2] from the host.
 hipError_t launch_rope_rows(hipStream_t s, float* x, int rows, int n_head, int hd, const float* theta,
@@ -265,7 +277,9 @@ int attn_quantize(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t 
                   float* d_out, vokra_hip_qact* qa, int act_quant);
 int paged_attn_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                         const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
-                        vokra_hip_qact* qa, int act_quant);
+                        vokra_hip_qact* qa, int act_quant, const float2* rope_cs = nullptr);
+// Whether paged_attn_quantize can rotate q itself for this cache and buffers.
+bool paged_attn_rotates_q(const vokra_hip_kv* kv, size_t n, size_t hq, const float* d_q, const float* d_out);
 //   kv_alloc_layers + paged_attn_append_quantize (one per layer, in layer
 //   order) = per layer vokra_hip_kv_append_dev of the items' K / V rows at
 //   d_times, then paged_attn_quantize; for distinct streams whose new time
@@ -275,7 +289,7 @@ int kv_alloc_layers(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t first_layer, size
 //   kv_alloc_layers + kv_write_allocated (per layer) = per layer
 //   vokra_hip_kv_append_dev of the items' rows at d_times.
 int kv_write_allocated(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
-                       const int* d_times, const float* d_k, const float* d_v);
+                       const int* d_times, const float* d_k, const float* d_v, const float2* rope_cs = nullptr);
 int paged_attn_append_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                                const int* d_times, const float* d_k, const float* d_v, const int* d_lens,
                                size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,

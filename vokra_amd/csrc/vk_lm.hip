@@ -62,6 +62,19 @@ __global__ void vk_rope_rows_qk(float* __restrict__ q, float* __restrict__ k, in
     row[j + half] = as + bc;
 }
 
+// The rotation's (cos, sin) of every (row, j) of one step: the angles of
+// vk_rope_rows_qk, computed once per step for every layer and head that a
+// fused consumer rotates (the K/V cache write and the GQA kernel's q load
+// apply vk_rope_pair with them: the same products and sums, bit for bit).
+__global__ void vk_rope_table(const int* __restrict__ positions, const float* __restrict__ theta, int rows, int half,
+                              float2* __restrict__ cs) {
+    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= rows * half) return;
+    const int r = gid / half, j = gid % half;
+    const float angle = (float)positions[r] * theta[j];
+    cs[gid] = make_float2(cosf(angle), sinf(angle));
+}
+
 // out[i] = silu(g[i]) * u[i]; out may alias g.
 __global__ void vk_swiglu_f32(const float* g, const float* __restrict__ u, float* out, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
@@ -93,6 +106,14 @@ hipError_t launch_rope_rows_qk(hipStream_t s, float* q, float* k, int rows, int 
     if (threads == 0) return hipSuccess;
     hipLaunchKernelGGL(vk_rope_rows_qk, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, q, k, rows, hq, hkv,
                        hd, theta, positions);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_table(hipStream_t s, const int* positions, const float* theta, int rows, int half, float2* cs) {
+    const int threads = rows * half;
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_rope_table, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, positions, theta, rows,
+                       half, cs);
     return hipGetLastError();
 }
 

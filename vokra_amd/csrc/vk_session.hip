@@ -740,7 +740,7 @@ struct vokra_hip_text_decoder {
     size_t n_layer = 0, d = 0, hq = 0, hkv = 0, hd = 0, ff = 0, vocab = 0, n_ctx = 0, n_stream = 0;
     float rope_base = 0.0f, eps = 0.0f, scale = 0.0f;
     std::vector<TextLayer> layers;
-    DBuf tok_emb, final_g, theta, h, x, q, k, v, attn, g, u, logits, lpart, lens, next, stage;
+    DBuf tok_emb, final_g, theta, h, x, q, k, v, attn, g, u, logits, lpart, lens, next, stage, rope_cs;
     QLin lm_head;
     bool tied = true;
     vokra_hip_kv_t* kv = nullptr;
@@ -752,7 +752,7 @@ struct vokra_hip_text_decoder {
             for (QLin* w : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down}) w->release(ctx);
         }
         for (DBuf* b : {&tok_emb, &final_g, &theta, &h, &x, &q, &k, &v, &attn, &g, &u, &logits, &lpart, &lens, &next,
-                        &stage})
+                        &stage, &rope_cs})
             b->release(ctx);
         lm_head.release(ctx);
         vokra_hip_kv_destroy(kv);
@@ -811,6 +811,7 @@ int td_setup(vokra_hip_text_decoder* m, const vokra_hip_text_decoder_layer_t* la
     SS_TRY(m->lens.alloc(c, rows * sizeof(int)));
     SS_TRY(m->next.alloc(c, rows * sizeof(int)));
     SS_TRY(m->stage.alloc(c, 3 * rows * sizeof(int)));
+    SS_TRY(m->rope_cs.alloc(c, rows * (m->hd / 2) * sizeof(float2)));  // (cos, sin) of one step's positions
     SS_TRY(vokra_hip_qact_create(c, rows, d, &m->qa_d));
     SS_TRY(vokra_hip_qact_create(c, rows, qh, &m->qa_q));
     SS_TRY(vokra_hip_qact_create(c, rows, ff, &m->qa_f));
@@ -844,6 +845,14 @@ int td_step(vokra_hip_text_decoder* m, size_t n, const int* d_streams, const int
     for (size_t l0 = 0, per = std::max<size_t>(1, 4096 / n); l0 < m->n_layer; l0 += per)
         SS_TRY(vk::kv_alloc_layers(c, m->kv, 0, l0, std::min(per, m->n_layer - l0), n, d_streams, d_positions));
     const VkEpi add_h = {m->h.f(), 0};
+    // RoPE fused into the K/V cache write (k) and the GQA kernel's q load: one
+    // (cos, sin) table for the step's positions serves every layer
+    const bool rope_fused =
+        act == VOKRA_HIP_ACT_KQUANT && vk::paged_attn_rotates_q(m->kv, n, m->hq, m->q.f(), m->attn.f());
+    const float2* cs = rope_fused ? (const float2*)m->rope_cs.p : nullptr;
+    if (rope_fused)
+        SS_HIP(vk::launch_rope_table(s, d_positions, m->theta.f(), (int)n, (int)(m->hd / 2), (float2*)m->rope_cs.p),
+               "launch(vk_rope_table)");
     for (size_t l = 0; l < m->n_layer; ++l) {
         const TextLayer& L = m->layers[l];
         // pre-norm self-attention (text_decoder.rs:1212-1351)
@@ -854,12 +863,13 @@ int td_step(vokra_hip_text_decoder* m, size_t n, const int* d_streams, const int
             float* qkv_o[3] = {m->q.f(), m->k.f(), m->v.f()};
             SS_TRY(vk::gemm_qact_multi(c, 3, qkv, m->qa_d, qkv_b, qkv_o));
         }
-        SS_HIP(vk::launch_rope_rows_qk(s, m->q.f(), m->k.f(), (int)n, (int)m->hq, (int)m->hkv, (int)m->hd,
-                                       m->theta.f(), d_positions),
-               "launch(vk_rope_rows_qk)");
-        SS_TRY(vk::kv_write_allocated(c, m->kv, l, n, d_streams, d_positions, m->k.f(), m->v.f()));
+        if (!rope_fused)
+            SS_HIP(vk::launch_rope_rows_qk(s, m->q.f(), m->k.f(), (int)n, (int)m->hq, (int)m->hkv, (int)m->hd,
+                                           m->theta.f(), d_positions),
+                   "launch(vk_rope_rows_qk)");
+        SS_TRY(vk::kv_write_allocated(c, m->kv, l, n, d_streams, d_positions, m->k.f(), m->v.f(), cs));
         SS_TRY(vk::paged_attn_quantize(c, m->kv, l, n, d_streams, m->lens.i(), m->n_ctx, m->hq, m->q.f(), m->scale,
-                                       m->attn.f(), m->qa_q, act));
+                                       m->attn.f(), m->qa_q, act, cs));
         SS_TRY(L.o.run(c, m->qa_q, m->h.f(), add_h));
         // pre-norm SwiGLU FFN (text_decoder.rs:1385-1418)
         SS_TRY(td_rms_quantize(m, m->qa_d, n, m->h.f(), L.ffn_g.f()));
