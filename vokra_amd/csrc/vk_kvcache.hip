@@ -505,12 +505,17 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
         for (int i = 0; i < 4; ++i) o_acc[u][i] = 0.0f;
     __syncthreads();
 
+    // the page-table entry of this thread's key in the next chunk is read
+    // while the current chunk computes (a split of two chunks: three memory
+    // round trips, not four)
+    int pid_next = c.table[layer * c.ppl + min(k0 + tid, k1 - 1) / c.bs];
     for (int j0 = k0; j0 < k1; j0 += pa::CH) {
         // ---- scores: thread = key
         const int j = j0 + tid;
         const bool kv_ok = j < k1;
         const int jt = kv_ok ? j : k0;
-        int pid = c.table[layer * c.ppl + jt / c.bs];
+        int pid = pid_next;
+        pid_next = c.table[layer * c.ppl + min(j0 + pa::CH + tid, k1 - 1) / c.bs];
         const bool has = kv_ok && pid >= 0;
         pid = max(pid, 0);
         const size_t hr = kv_hrow(c, pid, jt, s, hk);
