@@ -200,6 +200,17 @@ __device__ __forceinline__ void vk_row_load256(const float* __restrict__ row, in
         x[j] = c < cols ? row[c] : 0.0f;
     }
 }
+// The same columns, every load issued (columns past the row re-read its last
+// element and are zeroed by a select): no branch around a load, so a wait
+// for one row's loads does not also wait for younger ones.
+__device__ __forceinline__ void vk_row_load256_all(const float* __restrict__ row, int cols, float (&x)[kLnRegJ]) {
+#pragma unroll
+    for (int j = 0; j < kLnRegJ; ++j) {
+        const int c = (int)threadIdx.x + 256 * j;
+        const float v = row[min(c, cols - 1)];
+        x[j] = c < cols ? v : 0.0f;
+    }
+}
 __device__ __forceinline__ float2 vk_ln_stats256(const float (&x)[kLnRegJ], int cols, float eps, float* red) {
     const float inv_cols = 1.0f / (float)cols;
     float s = 0.0f;

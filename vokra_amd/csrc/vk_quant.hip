@@ -263,27 +263,36 @@ __global__ __launch_bounds__(256) void vk_ln_quantize_b32(const float* __restric
     // loop would make its wait (loads retire in order) also wait for the
     // next row's prefetch
     float gv[kLnRegJ], bv[kLnRegJ];
+    vk_row_load256_all(gamma, k, gv);
+    vk_row_load256_all(beta, k, bv);
+    // TILE: rows r+1 .. r+LD are in flight while row r reduces (every row
+    // load issued, rows past the matrix re-reading its last row), so the
+    // workgroup waits one memory latency per LD rows, not per row. The row
+    // loop stays rolled: unrolled over 16 rows the kernel is ~40 KB of code,
+    // and three workgroups per CU at different rows thrash the instruction
+    // cache.
+    constexpr int LD = TILE ? 4 : 1;
+    static_assert(16 % LD == 0, "whole row groups per tile");
+    float xq[LD][kLnRegJ];
+    const int row_first = mt * 16 + (TILE ? 0 : ((int)blockIdx.x & 15));
+    const int row_last = max(m - 1, 0);
+    const float* src = m > 0 ? in : gamma;  // with no rows, reads stay inside gamma (unused)
 #pragma unroll
-    for (int j = 0; j < kLnRegJ; ++j) {
-        const int c = t + 256 * j;
-        gv[j] = c < k ? gamma[c] : 0.0f;
-        bv[j] = c < k ? beta[c] : 0.0f;
-    }
-    // TILE: the rows are unrolled and row r+1 is loaded while row r reduces
-    float xn[kLnRegJ];
-    {
-        const int row0 = mt * 16 + (TILE ? 0 : ((int)blockIdx.x & 15));
-        if (row0 < m) vk_row_load256(in + (size_t)row0 * k, k, xn);
-    }
+    for (int d = 0; d < LD; ++d) vk_row_load256_all(src + (size_t)min(row_first + d, row_last) * k, k, xq[d]);
+    // rows r0 .. r0+LD-1 per pass, row r in slot r % LD (static register
+    // indices: no copies that would wait for the younger rows' loads)
+#pragma unroll 1
+    for (int r0 = 0; r0 < (TILE ? 16 : 1); r0 += LD)
 #pragma unroll
-    for (int r = 0; r < (TILE ? 16 : 1); ++r) {
+    for (int u = 0; u < LD; ++u) {
+        const int r = r0 + u;
         const int mr = TILE ? r : (int)blockIdx.x & 15;
         const int row = mt * 16 + mr;
         const bool live = row < m;  // uniform per workgroup
         float x[kLnRegJ];
 #pragma unroll
-        for (int j = 0; j < kLnRegJ; ++j) x[j] = xn[j];
-        if (TILE && r + 1 < 16 && row + 1 < m) vk_row_load256(in + (size_t)(row + 1) * k, k, xn);
+        for (int j = 0; j < kLnRegJ; ++j) x[j] = xq[u][j];
+        if (TILE) vk_row_load256_all(src + (size_t)min(row + LD, row_last) * k, k, xq[u]);
         float2 st = make_float2(0.0f, 0.0f);
         if (live) st = vk_ln_stats256(x, k, eps, red);
 #pragma unroll
