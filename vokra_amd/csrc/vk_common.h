@@ -104,18 +104,44 @@ __device__ __forceinline__ bool vk_f16_overflow(float x) {
     return a >= 65520.0f && a <= 3.40282347e38f;
 }
 
-// Max-reduce over groups of `G` consecutive lanes (G power of two <= 64).
+// The partner of a lane in a butterfly step over groups of 2 o lanes (lane
+// ^ o), through the cheapest cross-lane path that delivers it: DPP for
+// o <= 8 (a VALU operand modifier, no LDS round trip), ds_swizzle for o = 16,
+// ds_bpermute for o = 32. For o = 4 and 8 the DPP is a mirror (lane i <- the
+// lane 7 - i or 15 - i of its 8 / 16), which is the xor partner's value once
+// the earlier steps have made every lane of a 4- / 8-lane group equal, so the
+// butterfly's reductions (which only ever reach that state) get the same
+// operands.
+template <int O>
+__device__ __forceinline__ int vk_bfly_partner(int v) {
+    if constexpr (O == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xf, 0xf, true);  // quad_perm [1,0,3,2]
+    else if constexpr (O == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xf, 0xf, true);  // quad_perm [2,3,0,1]
+    else if constexpr (O == 4) return __builtin_amdgcn_mov_dpp(v, 0x141, 0xf, 0xf, true);  // row_half_mirror
+    else if constexpr (O == 8) return __builtin_amdgcn_mov_dpp(v, 0x140, 0xf, 0xf, true);  // row_mirror
+    else if constexpr (O == 16) return __builtin_amdgcn_ds_swizzle(v, 0x401F);  // bit mode: lane ^ 16 in 32
+    else return __shfl_xor(v, O, VK_WAVE);
+}
+
+// Max-reduce over groups of `G` consecutive lanes (G power of two <= 64);
+// every lane of a group ends with the group's value. The inputs must be
+// +0 or positive and not NaN (the callers reduce fmaxf(0, |x|), which maps a
+// NaN to 0 as the reference's fold from 0.0 does): on those, the order of
+// the f32 values is the order of their bit patterns, so the reduction runs
+// as an integer max whose DPP operand needs no NaN canonicalization.
 template <int G>
 __device__ __forceinline__ float vk_group_max(float v) {
-#pragma unroll
-    for (int o = 1; o < G; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, VK_WAVE));
-    return v;
+    int b = __float_as_int(v);
+#define VK_GMAX_STEP(O) if constexpr (G > (O)) b = max(b, vk_bfly_partner<(O)>(b));
+    VK_GMAX_STEP(1) VK_GMAX_STEP(2) VK_GMAX_STEP(4) VK_GMAX_STEP(8) VK_GMAX_STEP(16) VK_GMAX_STEP(32)
+#undef VK_GMAX_STEP
+    return __int_as_float(b);
 }
 
 template <int G>
 __device__ __forceinline__ int vk_group_sum_i(int v) {
-#pragma unroll
-    for (int o = 1; o < G; o <<= 1) v += __shfl_xor(v, o, VK_WAVE);
+#define VK_GSUM_STEP(O) if constexpr (G > (O)) v += vk_bfly_partner<(O)>(v);
+    VK_GSUM_STEP(1) VK_GSUM_STEP(2) VK_GSUM_STEP(4) VK_GSUM_STEP(8) VK_GSUM_STEP(16) VK_GSUM_STEP(32)
+#undef VK_GSUM_STEP
     return v;
 }
 
@@ -176,8 +202,14 @@ __device__ __forceinline__ float vk_epi_apply(float v, const VkEpi& e, size_t id
 // for LDS only (not for global loads in flight), so a caller's prefetch of
 // the next row stays in flight across the reduction.
 __device__ __forceinline__ float vk_block_sum256(float v, float* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, VK_WAVE);
+    // the butterfly over the wave in steps 1, 2, .., 32 (the partners of the
+    // first five through DPP / swizzle, see vk_bfly_partner)
+    v += __int_as_float(vk_bfly_partner<1>(__float_as_int(v)));
+    v += __int_as_float(vk_bfly_partner<2>(__float_as_int(v)));
+    v += __int_as_float(vk_bfly_partner<4>(__float_as_int(v)));
+    v += __int_as_float(vk_bfly_partner<8>(__float_as_int(v)));
+    v += __int_as_float(vk_bfly_partner<16>(__float_as_int(v)));
+    v += __shfl_xor(v, 32, VK_WAVE);
     VK_LDS_BARRIER();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     VK_LDS_BARRIER();

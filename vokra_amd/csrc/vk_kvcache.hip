@@ -229,7 +229,7 @@ __global__ __launch_bounds__(1024) void vk_kv_alloc_layers(KvDev c, int layer0, 
 // Same arithmetic as BlockQ8_0::pack: amax = max |x|, d = amax / 127,
 // q = round(clamp(x * (1/d), -127, 127)), scale stored as f16(d).
 __device__ __forceinline__ void q8_0_pack_lane(float v, int lane32, int8_t* q, uint16_t* d) {
-    const float amax = vk_group_max<32>(fabsf(v));
+    const float amax = vk_group_max<32>(fmaxf(0.0f, fabsf(v)));  // NaN -> 0, as the fold from 0.0
     const float dd = amax == 0.0f ? 0.0f : amax / 127.0f;
     const float inv = dd == 0.0f ? 0.0f : 1.0f / dd;
     const float sc = v * inv;

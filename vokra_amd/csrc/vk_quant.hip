@@ -87,7 +87,7 @@ __global__ void vk_pack_q0(int mode, const float* __restrict__ x, size_t n_block
     const int i = (int)(gid & 31);
     const bool live = blk < n_blocks;
     const float v = live ? x[blk * 32 + i] : 0.0f;
-    const float amax = vk_group_max<32>(fabsf(v));
+    const float amax = vk_group_max<32>(fmaxf(0.0f, fabsf(v)));  // NaN -> 0, as the fold from 0.0
     if (!live) return;
     const float div = mode == 3 ? 127.0f : (mode == 1 ? 7.0f : 15.0f);
     const float d = amax == 0.0f ? 0.0f : amax / div;
