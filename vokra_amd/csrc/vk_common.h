@@ -137,6 +137,24 @@ __device__ __forceinline__ float vk_group_max(float v) {
     return __int_as_float(b);
 }
 
+// The same butterflies for any f32 values (fmaxf: NaN ignored unless every
+// value is NaN; sums add the same two partials per step as a shuffle
+// butterfly in ascending steps).
+template <int G>
+__device__ __forceinline__ float vk_group_maxf(float v) {
+#define VK_GMAXF_STEP(O) if constexpr (G > (O)) v = fmaxf(v, __int_as_float(vk_bfly_partner<(O)>(__float_as_int(v))));
+    VK_GMAXF_STEP(1) VK_GMAXF_STEP(2) VK_GMAXF_STEP(4) VK_GMAXF_STEP(8) VK_GMAXF_STEP(16) VK_GMAXF_STEP(32)
+#undef VK_GMAXF_STEP
+    return v;
+}
+template <int G>
+__device__ __forceinline__ float vk_group_sumf(float v) {
+#define VK_GSUMF_STEP(O) if constexpr (G > (O)) v += __int_as_float(vk_bfly_partner<(O)>(__float_as_int(v)));
+    VK_GSUMF_STEP(1) VK_GSUMF_STEP(2) VK_GSUMF_STEP(4) VK_GSUMF_STEP(8) VK_GSUMF_STEP(16) VK_GSUMF_STEP(32)
+#undef VK_GSUMF_STEP
+    return v;
+}
+
 template <int G>
 __device__ __forceinline__ int vk_group_sum_i(int v) {
 #define VK_GSUM_STEP(O) if constexpr (G > (O)) v += vk_bfly_partner<(O)>(v);

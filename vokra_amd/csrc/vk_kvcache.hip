@@ -598,9 +598,7 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             sc[g] = has ? sc[g] : -INFINITY;
-            float mx = sc[g];
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, VK_WAVE));
+            const float mx = vk_group_maxf<64>(sc[g]);
             if (lane == 0) red[g][wave] = mx;
         }
         __syncthreads();
@@ -615,9 +613,7 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
             if (tid == 0) lalpha[g] = alpha[g];
 #pragma unroll
             for (int b = 0; b < NB; ++b) lpd[g][tid][b] = p * dv[b];
-            float ps = p;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) ps += __shfl_xor(ps, o, VK_WAVE);
+            const float ps = vk_group_sumf<64>(p);
             if (lane == 0) red[g][4 + wave] = ps;
             m_run[g] = m_new;
         }
@@ -897,7 +893,7 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
         float mloc = sc[0];
 #pragma unroll
         for (int j = 1; j < 8; ++j) mloc = fmaxf(mloc, sc[j]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, VK_WAVE));
+        mloc = fmaxf(mloc, __int_as_float(vk_bfly_partner<16>(__float_as_int(mloc))));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, VK_WAVE));
         const float m_new = fmaxf(m_run, mloc);
         const float m_use = m_new == -INFINITY ? 0.0f : m_new;
@@ -908,7 +904,7 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
             p[j] = __expf(sc[j] - m_use);
             psum += p[j];
         }
-        psum += __shfl_xor(psum, 16, VK_WAVE);
+        psum += __int_as_float(vk_bfly_partner<16>(__float_as_int(psum)));
         psum += __shfl_xor(psum, 32, VK_WAVE);
         l_run = l_run * alpha + psum;
         m_run = m_new;
@@ -1086,10 +1082,7 @@ __global__ void vk_paged_attn_combine(int n_split, int hq, const int* __restrict
         // integer group sum)
         const int row = (int)(ih / hq), h = (int)(ih % hq);
         const int g = h * (HD / 16) + (e >> 4), t = e & 15;
-        float amax = fabsf(v);
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
-        amax = fmaxf(0.0f, amax);
+        const float amax = vk_group_max<16>(fmaxf(0.0f, fabsf(v)));  // NaN -> 0 first, as the pass does
         float sc = 0.0f;
         int r = 0;
         if (amax != 0.0f) {
@@ -1097,9 +1090,7 @@ __global__ void vk_paged_attn_combine(int n_split, int hq, const int* __restrict
             const float q = vk_round_half_away(v / sc);
             r = (q != q) ? 0 : (int)fminf(fmaxf(q, -127.0f), 127.0f);
         }
-        int gs = r;
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) gs += __shfl_xor(gs, o, 16);
+        const int gs = vk_group_sum_i<16>(r);
         const int nsb = qo.k / 256, mt = row >> 4, sb = g >> 4, gi = g & 15;
         const size_t base = ((((size_t)mt * nsb + sb) * 8 + (gi >> 1)) * 64) * 2 + (gi & 1);
         const int lane_f = (row & 15) + 16 * (t >> 2);

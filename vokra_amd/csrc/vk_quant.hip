@@ -187,8 +187,9 @@ __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pa
     float amax = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
-    amax = fmaxf(amax, __shfl_xor(amax, 16, VK_WAVE));  // the four lanes of a row: l, l^16, l^32, l^48
-    amax = fmaxf(amax, __shfl_xor(amax, 32, VK_WAVE));
+    // the four lanes of a row: l, l^16, l^32, l^48 (non-negative, not NaN: integer max)
+    amax = __int_as_float(max(__float_as_int(amax), vk_bfly_partner<16>(__float_as_int(amax))));
+    amax = __int_as_float(max(__float_as_int(amax), __shfl_xor(__float_as_int(amax), 32, VK_WAVE)));
     float s = 0.0f;
     int q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (amax != 0.0f) {
@@ -209,7 +210,7 @@ __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pa
     int gs = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) gs += q[e];
-    gs += __shfl_xor(gs, 16, VK_WAVE);
+    gs += vk_bfly_partner<16>(gs);
     gs += __shfl_xor(gs, 32, VK_WAVE);
     uint32_t w[4];
 #pragma unroll
