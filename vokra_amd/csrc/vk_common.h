@@ -122,6 +122,12 @@ __device__ __forceinline__ int vk_bfly_partner(int v) {
     else return __shfl_xor(v, O, VK_WAVE);
 }
 
+// Lane J of each 16-lane row, to every lane of that row (DPP row_newbcast).
+template <int J>
+__device__ __forceinline__ int vk_row_bcast_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, 0x150 + J, 0xf, 0xf, true);
+}
+
 // Max-reduce over groups of `G` consecutive lanes (G power of two <= 64);
 // every lane of a group ends with the group's value. The inputs must be
 // +0 or positive and not NaN (the callers reduce fmaxf(0, |x|), which maps a

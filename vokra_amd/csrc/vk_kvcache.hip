@@ -823,8 +823,8 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
     struct Tile {
         uint2 kw[2][NB];  // K operand rows: subtile n, row hh <-> key 8 (hh / 4) + 4 n + hh % 4
         uint4 vw[4];      // V rows of keys 4va + t, dims 16vc .. +15
-        uint2 kd, vd;     // f16 block scales of key lane % 32
-        int has;          // key lane % 32 is cached
+        uint2 kd, vd;     // f16 block scales of key 8 (lane / 16) + lane % 8
+        int has;          // that key is cached
     };
     // the raw table entry of key lane % 32 of tile t (the key clamped into
     // the split); load_tile masks keys past the split, so nothing here waits
@@ -838,7 +838,6 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
         const int pid = jk < k1 ? raw : -1;
         const int slot_any = (int)kv_hrow(c, max(pid, 0), jk, s, hk);
         const int slot = pid >= 0 ? slot_any : 0;  // row 0: in bounds, masked
-        T.has = pid >= 0 ? 1 : 0;
 #pragma unroll
         for (int n = 0; n < 2; ++n) {
             const int sl = __shfl(slot, 8 * (hh >> 2) + 4 * n + (hh & 3), VK_WAVE);
@@ -846,8 +845,14 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
 #pragma unroll
             for (int b = 0; b < NB; ++b) T.kw[n][b] = kr[4 * b + g];
         }
-        T.kd = *reinterpret_cast<const uint2*>(c.kd + (size_t)slot * NB);
-        T.vd = *reinterpret_cast<const uint2*>(c.vd + (size_t)slot * NB);
+        // the scales and presence of key 8 (lane / 16) + lane % 8: lane j < 8
+        // of 16-lane row g then holds key 8 g + j, which the products take
+        // through row_newbcast DPP moves instead of LDS permutes
+        const int src = 8 * (lane >> 4) + (lane & 7);
+        const int slot_s = __shfl(slot, src, VK_WAVE);
+        T.has = __shfl(pid >= 0 ? 1 : 0, src, VK_WAVE);
+        T.kd = *reinterpret_cast<const uint2*>(c.kd + (size_t)slot_s * NB);
+        T.vd = *reinterpret_cast<const uint2*>(c.vd + (size_t)slot_s * NB);
 #pragma unroll
         for (int t4 = 0; t4 < 4; ++t4) {
             const int sl = __shfl(slot, 4 * va + t4, VK_WAVE);
@@ -859,13 +864,12 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
         // scales and presence of keys 8g + j (j = 4n + r) from the lanes that loaded them
         uint2 kds[8], vds[8];
         int kval[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int src = 8 * g + j;
-            kds[j] = make_uint2((uint32_t)__shfl((int)T.kd.x, src, VK_WAVE), (uint32_t)__shfl((int)T.kd.y, src, VK_WAVE));
-            vds[j] = make_uint2((uint32_t)__shfl((int)T.vd.x, src, VK_WAVE), (uint32_t)__shfl((int)T.vd.y, src, VK_WAVE));
-            kval[j] = __shfl(T.has, src, VK_WAVE);
-        }
+#define VK_GQA_BC(J)                                                                                            \
+        kds[J] = make_uint2((uint32_t)vk_row_bcast_i<J>((int)T.kd.x), (uint32_t)vk_row_bcast_i<J>((int)T.kd.y));   \
+        vds[J] = make_uint2((uint32_t)vk_row_bcast_i<J>((int)T.vd.x), (uint32_t)vk_row_bcast_i<J>((int)T.vd.y));   \
+        kval[J] = vk_row_bcast_i<J>(T.has);
+        VK_GQA_BC(0) VK_GQA_BC(1) VK_GQA_BC(2) VK_GQA_BC(3) VK_GQA_BC(4) VK_GQA_BC(5) VK_GQA_BC(6) VK_GQA_BC(7)
+#undef VK_GQA_BC
 
         // ---- S^T = K . (q hi + lo)^T per key subtile, block scales applied per block
         float sc[8];
