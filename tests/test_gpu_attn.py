@@ -111,6 +111,24 @@ def test_batch_equals_separate_calls(ctx):
         assert np.array_equal(one, full[b])
 
 
+def test_unaligned_q_rejected(ctx):
+    """The device entry point takes q, k and out 16-byte aligned (the kernel
+    reads q rows as 16-byte vectors and splits them itself)."""
+    print("[case] unaligned q rejected", flush=True)
+    import ctypes as C
+    from types import SimpleNamespace
+    tq, tkv, H, hd = 4, 8, 1, 64
+    bufs = [hip.DeviceBuffer(ctx, (tq * H * hd + 4) * 4), hip.DeviceBuffer(ctx, tkv * H * hd * 4),
+            hip.DeviceBuffer(ctx, tkv * H * hd * 4), hip.DeviceBuffer(ctx, tq * H * hd * 4)]
+    try:
+        q_off4 = SimpleNamespace(ptr=C.c_void_p(bufs[0].ptr.value + 4))
+        with pytest.raises(hip.InvalidArgument):
+            ctx.attn_f32_dev(1, tq, tkv, H, H, hd, q_off4, bufs[1], bufs[2], 0.125, False, 0, bufs[3])
+    finally:
+        for b in bufs:
+            b.free()
+
+
 def test_uniform_keys_give_mean_of_values(ctx):
     """Identical keys: softmax is uniform, so every output row is mean(v)."""
     print("[case] uniform keys", flush=True)

@@ -10,8 +10,11 @@
 // Precision: every f32 operand x is split into two fp16 values x = hi + lo
 // (hi = fp16(x), lo = fp16(x - hi)) and each product runs as three MFMAs,
 // hi*hi + hi*lo + lo*hi, accumulated in f32: about 22 significant bits per
-// product, i.e. f32-level results, at 3x the fp16 MFMA rate. Inputs must stay
-// within the fp16 range (|x| < 65504 after scaling).
+// product, i.e. f32-level results, at 3x the fp16 MFMA rate. q is split as
+// q * scale * log2(e), so S comes out in base-2 units and P = 2^(S - max)
+// (= e^(s - max) of the natural scores) takes one subtraction and one v_exp
+// per score. Inputs must stay within the fp16 range (|x| < 65504 after that
+// scaling).
 //
 // With LO = false (the decoder's half-precision cross-attention mode) K and V
 // are taken as their fp16 hi parts only: two MFMAs per product (k_hi*q_hi +
@@ -23,7 +26,12 @@
 //   O^T = V^T . P^T (A = V^T tile from LDS, B = P from registers)
 // so every lane holds the scores, softmax statistics and output of one query
 // (lane % 16) and the softmax needs no transposes. K/V tiles of 64 keys are
-// staged through LDS, the next tile's loads in flight during the current one.
+// staged through LDS, the next tile's loads in flight during the current one;
+// the loads are buffer loads whose addresses are a per-lane constant plus a
+// wave-uniform tile offset (no vector address arithmetic in the key loop).
+// The K tile rows are read into S^T in the order that leaves each lane the
+// scores of 8 consecutive keys per 32-key step, which is the P^T operand
+// layout of the second product, so a lane's V^T operand is one 16-byte read.
 #include <hip/hip_fp16.h>
 
 #include "vk_common.h"
@@ -37,12 +45,47 @@ typedef uint32_t vk_u32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 vk_h16x2a __attribute__((ext_vector_type(2)));
 typedef short vk_i16x2 __attribute__((ext_vector_type(2)));
 
+typedef float vk_f32x2 __attribute__((ext_vector_type(2)));
+template <bool B>
+struct AttnMask {
+    static constexpr bool value = B;
+};
+
 namespace attn {
 constexpr int QT = 64;   // queries per workgroup
 constexpr int KT = 64;   // keys per LDS tile
 constexpr int KPAD = 8;  // halves of row padding in the K tile
 constexpr int VPAD = 8;  // halves of row padding in the V^T tile
+constexpr float kLog2e = 1.44269504088896340736f;
+// halves of one K tile (row r at r * (HD + KPAD) + kshift(r), kshift <= 192) and of one V^T tile
+constexpr int k_tile_halves(int hd) { return KT * (hd + KPAD) + 192; }
+constexpr int v_tile_halves(int hd) { return hd * (KT + VPAD); }
+// static LDS bytes of a flash workgroup with np fp16 parts of K / V in use
+constexpr int flash_lds_bytes(int hd, int np) { return np * (k_tile_halves(hd) + v_tile_halves(hd)) * 2; }
+constexpr int kLdsPerCu = 160 * 1024;
+constexpr int kRsrcRaw = 0x00020000;  // buffer resource word 3: raw (unswizzled) dword access
 }  // namespace attn
+
+// max / sum over the four lanes of a query (l, l ^ 16, l ^ 32, l ^ 48): each
+// permlane swap leaves a lane holding its own value and its partner's, in
+// either order (the sum of the two is the same either way)
+__device__ __forceinline__ float attn_fmax_raw(float a, float b) {
+    float r;  // plain v_max_f32: fmaxf would first quiet signalling NaNs, which scores never are
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ float attn_query_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = attn_fmax_raw(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return attn_fmax_raw(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float attn_query_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 // Set (to 1) by any kernel of this file that meets an operand outside the
 // fp16 range; read and cleared by the host (attn_range_take). One per device.
@@ -159,11 +202,7 @@ __global__ __launch_bounds__(256) void vk_split_vt(const float* __restrict__ v, 
 }
 
 // The same two pre-passes with the compact low part (one byte per element).
-__global__ void vk_split_rows_q7(const float* __restrict__ x, size_t n4, float scale, uint2* __restrict__ hi,
-                                 uint32_t* __restrict__ lo) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n4) return;
-    const float4 v = reinterpret_cast<const float4*>(x)[i];
+__device__ __forceinline__ void split4_q7(float4 v, float scale, uint2& hi, uint32_t& lo) {
     const float a[4] = {v.x * scale, v.y * scale, v.z * scale, v.w * scale};
     if (vk_f16_overflow(a[0]) || vk_f16_overflow(a[1]) || vk_f16_overflow(a[2]) || vk_f16_overflow(a[3]))
         attn_range_raise();
@@ -171,14 +210,40 @@ __global__ void vk_split_rows_q7(const float* __restrict__ x, size_t n4, float s
     int8_t l[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) split_q7(a[j], h[j], l[j]);
-    hi[i] = make_uint2(__builtin_bit_cast(uint16_t, h[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[1]) << 16),
-                       __builtin_bit_cast(uint16_t, h[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[3]) << 16));
-    lo[i] = (uint32_t)(uint8_t)l[0] | ((uint32_t)(uint8_t)l[1] << 8) | ((uint32_t)(uint8_t)l[2] << 16) |
-            ((uint32_t)(uint8_t)l[3] << 24);
+    hi = make_uint2(__builtin_bit_cast(uint16_t, h[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[1]) << 16),
+                    __builtin_bit_cast(uint16_t, h[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[3]) << 16));
+    lo = (uint32_t)(uint8_t)l[0] | ((uint32_t)(uint8_t)l[1] << 8) | ((uint32_t)(uint8_t)l[2] << 16) |
+         ((uint32_t)(uint8_t)l[3] << 24);
 }
 
+__global__ void vk_split_rows_q7(const float* __restrict__ x, size_t n4, float scale, uint2* __restrict__ hi,
+                                 uint32_t* __restrict__ lo) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    split4_q7(reinterpret_cast<const float4*>(x)[i], scale, hi[i], lo[i]);
+}
+
+// x [B][T][H*hd] -> hi / lo [B][H][T][hd] (each head's keys contiguous); one
+// thread per 4 output elements.
+__global__ void vk_split_rows_q7_heads(const float* __restrict__ x, size_t n4, int t, int h, int hd4, float scale,
+                                       uint2* __restrict__ hi, uint32_t* __restrict__ lo) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    const int d4 = (int)(i % hd4);
+    const size_t r = i / hd4;  // (b * h + head) * t + key
+    const int key = (int)(r % t);
+    const size_t bh = r / t;
+    const int head = (int)(bh % h);
+    const size_t b = bh / h;
+    const size_t src = ((b * t + key) * h + head) * hd4 + d4;
+    split4_q7(reinterpret_cast<const float4*>(x)[src], scale, hi[i], lo[i]);
+}
+
+// tiled: V^T [B][H][T_pad / 64][hd][64] (each 64-key tile of a head
+// contiguous) instead of [B][H][hd][T_pad]
 __global__ __launch_bounds__(256) void vk_split_vt_q7(const float* __restrict__ v, int t_kv, int t_pad, int h_kv,
-                                                      int hd, uint16_t* __restrict__ vth, int8_t* __restrict__ vtl) {
+                                                      int hd, int tiled, uint16_t* __restrict__ vth,
+                                                      int8_t* __restrict__ vtl) {
     __shared__ float tile[64][65];
     const int t0 = blockIdx.x * 64, c0 = (blockIdx.y % (hd / 64)) * 64, h = blockIdx.y / (hd / 64), b = blockIdx.z;
     const int tid = threadIdx.x;
@@ -197,7 +262,9 @@ __global__ __launch_bounds__(256) void vk_split_vt_q7(const float* __restrict__ 
         _Float16 hi;
         int8_t lo;
         split_q7(tile[r][c], hi, lo);
-        const size_t o = (((size_t)b * h_kv + h) * hd + c0 + c) * t_pad + t0 + r;
+        const size_t slab = ((size_t)b * h_kv + h) * hd * t_pad;
+        const size_t o = tiled ? slab + (size_t)t0 * hd + (size_t)(c0 + c) * 64 + r
+                               : slab + (size_t)(c0 + c) * t_pad + t0 + r;
         vth[o] = __builtin_bit_cast(uint16_t, hi);
         vtl[o] = lo;
     }
@@ -207,14 +274,15 @@ __global__ __launch_bounds__(256) void vk_split_vt_q7(const float* __restrict__ 
 // LOM: the K / V low parts in use: 0 none (fp16 high parts only), 1 fp16
 // (kl, vtl as fp16 arrays), 2 compact (one byte per element, split_q7).
 template <int HD, int LOM, bool ONEQ>
-__global__ __launch_bounds__(256) void vk_flash_attn(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void vk_flash_attn(
     const uint4* __restrict__ qh, const uint4* __restrict__ ql,    // [B][Tq][Hq*HD] fp16, scaled
     const uint4* __restrict__ kh, const uint4* __restrict__ kl,    // [B][Tkv][Hkv*HD] fp16
     const uint4* __restrict__ vth, const uint4* __restrict__ vtl,  // [B][Hkv][HD][Tpad] fp16
     float* __restrict__ out, int tq, int tkv, int t_pad, int hq, int hkv, int causal, int q_off,
     const int* __restrict__ kv_index,
     const float* __restrict__ qf, float q_scale,  // qf != null: f32 q, split here (qh / ql unused)
-    const VkQOut qo) {                            // qo.afrag != null: quantize O (out may be null)
+    const VkQOut qo,                              // qo.afrag != null: quantize O (out may be null)
+    const AttnLayout lay) {                       // K / V element strides
     using namespace attn;
     constexpr int KS = HD / 32;      // 32-wide K steps of S = K . Q^T
     constexpr int OS = HD / 16;      // 16-row output subtiles of O^T
@@ -224,8 +292,9 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
     constexpr int VU4 = HD * KT / 8 / 256;  // uint4 per thread per V^T array
     constexpr bool LO = LOM != 0;
     constexpr int NP = LO ? 2 : 1;                         // fp16 parts of K and V in use
-    __shared__ __align__(16) _Float16 lk[NP][KT * KROW];  // K tile, hi (/ lo)
-    __shared__ __align__(16) _Float16 lv[NP][HD * VROW];  // V^T tile, hi (/ lo)
+    // K tile, hi (/ lo): row r at r * KROW + kshift(r) halves (see krow0)
+    __shared__ __align__(16) _Float16 lk[NP][k_tile_halves(HD)];
+    __shared__ __align__(16) _Float16 lv[NP][v_tile_halves(HD)];  // V^T tile, hi (/ lo)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, lq = lane & 15;
     const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -250,44 +319,69 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
             qa_l[ks] = ql[o];
         }
     }
+    // q is complete before the key loop: the loop's waits then only count
+    // its own K / V loads
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+        asm volatile("" ::"v"(qa_h[ks].x), "v"(qa_h[ks].y), "v"(qa_h[ks].z), "v"(qa_h[ks].w), "v"(qa_l[ks].x),
+                     "v"(qa_l[ks].y), "v"(qa_l[ks].z), "v"(qa_l[ks].w));
 
     // keys this workgroup has to visit
     int kv_end = tkv;
     if (causal) kv_end = min(tkv, q_off + min(qt * QT + QT, tq));
     const int n_tiles = (kv_end + KT - 1) / KT;
 
-    // staged loads of one K / V^T tile (indices clamped into the arrays)
-    // native vectors (not HIP's uint4 struct) so the stage stays in registers
+    // Staged loads of one K / V^T tile. K: the tile's rows start a buffer
+    // resource whose extent ends with row t_kv - 1 of this (batch, kv head)
+    // (a row past it reads as zero; such keys are masked); V^T: one resource
+    // over this (batch, kv head)'s HD x Tpad slab, the tile a scalar offset
+    // into it.
+    // Per-lane byte offsets are loop constants. Native vectors (not HIP's
+    // uint4 struct) keep the stage in registers.
     struct Stage {
         vk_u32x4 kh[KU4], kl[KU4], vh[VU4], vl[VU4];
         vk_u32x2 klq[KU4], vlq[VU4];  // LOM == 2
     };
-    const vk_u32x4* kh4 = reinterpret_cast<const vk_u32x4*>(kh);
-    const vk_u32x4* kl4 = reinterpret_cast<const vk_u32x4*>(kl);
-    const vk_u32x4* vh4 = reinterpret_cast<const vk_u32x4*>(vth);
-    const vk_u32x4* vl4 = reinterpret_cast<const vk_u32x4*>(vtl);
-    const vk_u32x2* klq2 = reinterpret_cast<const vk_u32x2*>(kl);
-    const vk_u32x2* vlq2 = reinterpret_cast<const vk_u32x2*>(vtl);
+    constexpr int KEB = LOM == 2 ? 1 : 2;  // bytes per element of the K / V low parts
+    const size_t kslab = (size_t)kb * lay.kb + (size_t)hk * lay.kh;  // elements: key 0 of this (batch, kv head)
+    const char* kslab_h = reinterpret_cast<const char*>(kh) + kslab * 2;
+    const char* kslab_l = reinterpret_cast<const char*>(kl) + kslab * KEB;
+    const size_t vslab = ((size_t)kb * hkv + hk) * HD * t_pad;  // elements
+    const __amdgpu_buffer_rsrc_t rvh = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<const char*>(vth) + vslab * 2), 0, HD * t_pad * 2, kRsrcRaw);
+    const __amdgpu_buffer_rsrc_t rvl = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<const char*>(vtl) + vslab * KEB), 0, HD * t_pad * KEB, kRsrcRaw);
+    uint32_t ko[KU4], vo[VU4];  // element offsets of this thread's K / V^T chunks within a tile
+#pragma unroll
+    for (int i = 0; i < KU4; ++i) {
+        const int idx = tid + 256 * i, r = idx / (HD / 8), c = idx % (HD / 8);
+        ko[i] = (uint32_t)(r * lay.kt + 8 * c);
+    }
+#pragma unroll
+    for (int i = 0; i < VU4; ++i) {
+        const int idx = tid + 256 * i, r = idx / (KT / 8), c = idx % (KT / 8);
+        vo[i] = (uint32_t)(r * lay.vd + 8 * c);
+    }
     auto load = [&](int kt) __attribute__((always_inline)) -> Stage {
         Stage st;
+        const int rows = min(tkv - kt * KT, KT);  // >= 1: kt < n_tiles
+        const size_t k0 = (size_t)kt * KT * lay.kt;  // elements
+        const int kext = (rows - 1) * lay.kt + HD;   // elements up to the end of row t_kv - 1
+        const __amdgpu_buffer_rsrc_t rkh =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(kslab_h + k0 * 2), 0, kext * 2, kRsrcRaw);
+        const __amdgpu_buffer_rsrc_t rkl =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(kslab_l + k0 * KEB), 0, kext * KEB, kRsrcRaw);
 #pragma unroll
         for (int i = 0; i < KU4; ++i) {
-            const int idx = tid + 256 * i;
-            const int r = idx / (HD / 8), c = idx % (HD / 8);
-            const int t = min(kt * KT + r, tkv - 1);
-            const size_t o = ((size_t)kb * tkv + t) * kw + (size_t)hk * HD / 8 + c;
-            st.kh[i] = kh4[o];
-            if (LOM == 1) st.kl[i] = kl4[o];
-            if (LOM == 2) st.klq[i] = klq2[o];
+            st.kh[i] = __builtin_amdgcn_raw_buffer_load_b128(rkh, ko[i] * 2, 0, 0);
+            if (LOM == 1) st.kl[i] = __builtin_amdgcn_raw_buffer_load_b128(rkl, ko[i] * 2, 0, 0);
+            if (LOM == 2) st.klq[i] = __builtin_amdgcn_raw_buffer_load_b64(rkl, ko[i], 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < VU4; ++i) {
-            const int idx = tid + 256 * i;
-            const int r = idx / (KT / 8), c = idx % (KT / 8);
-            const size_t o = (((size_t)kb * hkv + hk) * HD + r) * (t_pad / 8) + (size_t)kt * KT / 8 + c;
-            st.vh[i] = vh4[o];
-            if (LOM == 1) st.vl[i] = vl4[o];
-            if (LOM == 2) st.vlq[i] = vlq2[o];
+            st.vh[i] = __builtin_amdgcn_raw_buffer_load_b128(rvh, vo[i] * 2, kt * lay.vtile * 2, 0);
+            if (LOM == 1) st.vl[i] = __builtin_amdgcn_raw_buffer_load_b128(rvl, vo[i] * 2, kt * lay.vtile * 2, 0);
+            if (LOM == 2) st.vlq[i] = __builtin_amdgcn_raw_buffer_load_b64(rvl, vo[i], kt * lay.vtile, 0);
         }
         return st;
     };
@@ -363,128 +457,144 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
         return;
     }
     float m_run = -INFINITY, l_run = 0.0f;
+    // S^T subtile n takes K tile row 32 (n / 2) + 4 (n % 2) + 8 (i / 4) + i % 4
+    // as its row i: a lane (g = lane / 16) then holds, for subtile n and
+    // accumulator entry r, key 32 (n / 2) + 8 g + 4 (n % 2) + r. The rows a
+    // 16-lane read phase takes (i = 0..15) are 4 runs of 4 rows 8 apart; row r
+    // starts kshift(r) = 4 (r & 24) + 3 (r & 32) halves past r * KROW, which
+    // puts those 16 reads of 16 bytes on 64 distinct banks (and each 8-lane
+    // half on 32) where the plain row pitch would pair them up; the 3 (r & 32)
+    // term keeps rows 32.. clear of row 31's shifted span. For the rows read
+    // here r & 24 = 8 (lq / 4) and r & 32 = 32 (n / 2).
+    const int krow0 = 8 * (lq >> 2) + (lq & 3);
+    const int kbase = krow0 * KROW + 32 * (lq >> 2) + 8 * g;
 
-    // unconditional (clamped) loads keep the stage in registers
-    Stage st = load(0);
-    for (int kt = 0; kt < n_tiles; ++kt) {
-        // ---- stage the tile into LDS
+    // One tile's two products and softmax step for the active waves; MASK:
+    // the tile holds keys past t_kv or (causal) past some query's position.
+    // The two instantiations keep the whole-tile case free of the masking.
+    auto tile = [&](int kt, auto mask_tag) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        // ---- S^T for 4 key subtiles of 16 (base-2 units)
+        vk_f32x4 s[4];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            s[n] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const int off = kbase + (32 * (n >> 1) + 4 * (n & 1)) * KROW + 96 * (n >> 1) + 32 * ks;
+                const vk_h16x8 ah = *reinterpret_cast<const vk_h16x8*>(&lk[0][off]);
+                const vk_h16x8 bh = __builtin_bit_cast(vk_h16x8, qa_h[ks]);
+                const vk_h16x8 bl = __builtin_bit_cast(vk_h16x8, qa_l[ks]);
+                s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, s[n], 0, 0, 0);
+                s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, s[n], 0, 0, 0);
+                if (LO) {
+                    const vk_h16x8 al = *reinterpret_cast<const vk_h16x8*>(&lk[NP - 1][off]);
+                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, s[n], 0, 0, 0);
+                }
+            }
+        }
+        // ---- mask, online softmax (per query = per lane, across lanes g)
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (MASK) {
+                    const int key = kt * KT + 32 * (n >> 1) + 8 * g + 4 * (n & 1) + r;
+                    const bool ok = key < tkv && (!causal || key <= q_off + q_idx);
+                    s[n][r] = ok ? s[n][r] : -INFINITY;
+                }
+                mloc = fmaxf(mloc, s[n][r]);
+            }
+        mloc = attn_query_max(mloc);
+        const float m_new = fmaxf(m_run, mloc);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        float psum = 0.0f;
+        // P^T operand halves: for 32-key step ks, the lane's keys 32ks + 8g + 4j + r
+        // (subtile n = 2ks + j) are MFMA k-slots 8g + 4j + r
+        vk_u32x4 ph[2], pl[2];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+#pragma unroll
+            for (int r = 0; r < 4; r += 2) {
+                const vk_f32x2 p = {__builtin_amdgcn_exp2f(s[n][r] - m_use),
+                                    __builtin_amdgcn_exp2f(s[n][r + 1] - m_use)};
+                psum += p.x;
+                psum += p.y;
+                const vk_h16x2a hi = __builtin_convertvector(p, vk_h16x2a);
+                const vk_h16x2a lo = __builtin_convertvector(p - __builtin_convertvector(hi, vk_f32x2), vk_h16x2a);
+                ph[n >> 1][2 * (n & 1) + r / 2] = __builtin_bit_cast(uint32_t, hi);
+                pl[n >> 1][2 * (n & 1) + r / 2] = __builtin_bit_cast(uint32_t, lo);
+            }
+        }
+        psum = attn_query_sum(psum);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        // o * 1.0f is o: when no lane's running max moved, the rescale is skipped
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int os = 0; os < OS; ++os)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o_acc[os][r] *= alpha;
+        }
+        // ---- O^T += V^T . P^T over 2 key steps of 32
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const vk_h16x8 bh = __builtin_bit_cast(vk_h16x8, ph[ks]);
+            const vk_h16x8 bl = __builtin_bit_cast(vk_h16x8, pl[ks]);
+#pragma unroll
+            for (int os = 0; os < OS; ++os) {
+                const int off = (16 * os + lq) * VROW + 32 * ks + 8 * g;
+                const vk_h16x8 ah = *reinterpret_cast<const vk_h16x8*>(&lv[0][off]);
+                o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, o_acc[os], 0, 0, 0);
+                o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, o_acc[os], 0, 0, 0);
+                if (LO) {
+                    const vk_h16x8 al = *reinterpret_cast<const vk_h16x8*>(&lv[NP - 1][off]);
+                    o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, o_acc[os], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // Stage a tile's loads (sx) into LDS.
+    auto stage_in = [&](const Stage& sx) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < KU4; ++i) {
             const int idx = tid + 256 * i;
             const int r = idx / (HD / 8), c = idx % (HD / 8);
-            *reinterpret_cast<vk_u32x4*>(&lk[0][r * KROW + 8 * c]) = st.kh[i];
-            if (LOM == 1) *reinterpret_cast<vk_u32x4*>(&lk[NP - 1][r * KROW + 8 * c]) = st.kl[i];
-            if (LOM == 2) *reinterpret_cast<vk_u32x4*>(&lk[NP - 1][r * KROW + 8 * c]) = q7x8_f16(st.kh[i], st.klq[i]);
+            const int at = r * KROW + 4 * (r & 24) + 3 * (r & 32) + 8 * c;
+            *reinterpret_cast<vk_u32x4*>(&lk[0][at]) = sx.kh[i];
+            if (LOM == 1) *reinterpret_cast<vk_u32x4*>(&lk[NP - 1][at]) = sx.kl[i];
+            if (LOM == 2) *reinterpret_cast<vk_u32x4*>(&lk[NP - 1][at]) = q7x8_f16(sx.kh[i], sx.klq[i]);
         }
 #pragma unroll
         for (int i = 0; i < VU4; ++i) {
             const int idx = tid + 256 * i;
             const int r = idx / (KT / 8), c = idx % (KT / 8);
-            *reinterpret_cast<vk_u32x4*>(&lv[0][r * VROW + 8 * c]) = st.vh[i];
-            if (LOM == 1) *reinterpret_cast<vk_u32x4*>(&lv[NP - 1][r * VROW + 8 * c]) = st.vl[i];
-            if (LOM == 2) *reinterpret_cast<vk_u32x4*>(&lv[NP - 1][r * VROW + 8 * c]) = q7x8_f16(st.vh[i], st.vlq[i]);
+            *reinterpret_cast<vk_u32x4*>(&lv[0][r * VROW + 8 * c]) = sx.vh[i];
+            if (LOM == 1) *reinterpret_cast<vk_u32x4*>(&lv[NP - 1][r * VROW + 8 * c]) = sx.vl[i];
+            if (LOM == 2) *reinterpret_cast<vk_u32x4*>(&lv[NP - 1][r * VROW + 8 * c]) = q7x8_f16(sx.vh[i], sx.vlq[i]);
         }
         VK_LDS_BARRIER();
+    };
+    // One tile per step: stage it, start the next tile's loads, run the
+    // products. Tiles that need no masking (all keys below t_kv and,
+    // causal, at or before the workgroup's first query) are a prefix of
+    // the sequence: they run in a loop of their own, so the masked case
+    // costs nothing there.
+    Stage st = load(0);  // unconditional (clamped) loads keep the stage in registers
+    auto step = [&](int kt, auto mask_tag) __attribute__((always_inline)) {
+        stage_in(st);
         st = load(min(kt + 1, n_tiles - 1));
-
-        if (active) {
-            // ---- S^T for 4 key subtiles of 16: lane holds keys 16n + 4g + r
-            vk_f32x4 s[4];
-#pragma unroll
-            for (int n = 0; n < 4; ++n) {
-                s[n] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    const int off = (16 * n + lq) * KROW + 32 * ks + 8 * g;
-                    const vk_h16x8 ah = *reinterpret_cast<const vk_h16x8*>(&lk[0][off]);
-                    const vk_h16x8 bh = __builtin_bit_cast(vk_h16x8, qa_h[ks]);
-                    const vk_h16x8 bl = __builtin_bit_cast(vk_h16x8, qa_l[ks]);
-                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, s[n], 0, 0, 0);
-                    s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, s[n], 0, 0, 0);
-                    if (LO) {
-                        const vk_h16x8 al = *reinterpret_cast<const vk_h16x8*>(&lk[NP - 1][off]);
-                        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, s[n], 0, 0, 0);
-                    }
-                }
-            }
-            // ---- mask, online softmax (per query = per lane, across lanes g)
-            float mloc = -INFINITY;
-            if (!causal && kt * KT + KT <= tkv) {  // a whole tile of live keys: nothing to mask
-#pragma unroll
-                for (int n = 0; n < 4; ++n)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[n][r]);
-            } else {
-#pragma unroll
-                for (int n = 0; n < 4; ++n)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int key = kt * KT + 16 * n + 4 * g + r;
-                        const bool ok = key < tkv && (!causal || key <= q_off + q_idx);
-                        s[n][r] = ok ? s[n][r] : -INFINITY;
-                        mloc = fmaxf(mloc, s[n][r]);
-                    }
-            }
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 16, VK_WAVE));
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, VK_WAVE));
-            const float m_new = fmaxf(m_run, mloc);
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = __expf(m_run - m_use);
-            float psum = 0.0f;
-            uint32_t ph[4][2], pl[4][2];  // P^T operand halves, [key subtile][pair]
-#pragma unroll
-            for (int n = 0; n < 4; ++n) {
-                _Float16 h4[4], l4[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float p = __expf(s[n][r] - m_use);
-                    psum += p;
-                    split_f16(p, h4[r], l4[r]);
-                }
-                ph[n][0] = __builtin_bit_cast(uint16_t, h4[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, h4[1]) << 16);
-                ph[n][1] = __builtin_bit_cast(uint16_t, h4[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, h4[3]) << 16);
-                pl[n][0] = __builtin_bit_cast(uint16_t, l4[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, l4[1]) << 16);
-                pl[n][1] = __builtin_bit_cast(uint16_t, l4[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, l4[3]) << 16);
-            }
-            psum += __shfl_xor(psum, 16, VK_WAVE);
-            psum += __shfl_xor(psum, 32, VK_WAVE);
-            l_run = l_run * alpha + psum;
-            m_run = m_new;
-            // o * 1.0f is o: when no lane's running max moved, the rescale is skipped
-            if (__any(alpha != 1.0f)) {
-#pragma unroll
-                for (int os = 0; os < OS; ++os)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) o_acc[os][r] *= alpha;
-            }
-            // ---- O^T += V^T . P^T over 2 key steps of 32: MFMA k-index 8g + 4j + r
-            //      is key 32ks + 16j + 4g + r (the lane's P values, in order)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const vk_h16x8 bh = __builtin_bit_cast(
-                    vk_h16x8, make_uint4(ph[2 * ks][0], ph[2 * ks][1], ph[2 * ks + 1][0], ph[2 * ks + 1][1]));
-                const vk_h16x8 bl = __builtin_bit_cast(
-                    vk_h16x8, make_uint4(pl[2 * ks][0], pl[2 * ks][1], pl[2 * ks + 1][0], pl[2 * ks + 1][1]));
-#pragma unroll
-                for (int os = 0; os < OS; ++os) {
-                    const int row = (16 * os + lq) * VROW;
-                    const int k0 = 32 * ks + 4 * g;
-                    const uint2 h0 = *reinterpret_cast<const uint2*>(&lv[0][row + k0]);
-                    const uint2 h1 = *reinterpret_cast<const uint2*>(&lv[0][row + k0 + 16]);
-                    const vk_h16x8 ah = __builtin_bit_cast(vk_h16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
-                    o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, o_acc[os], 0, 0, 0);
-                    o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, o_acc[os], 0, 0, 0);
-                    if (LO) {
-                        const uint2 l0 = *reinterpret_cast<const uint2*>(&lv[NP - 1][row + k0]);
-                        const uint2 l1 = *reinterpret_cast<const uint2*>(&lv[NP - 1][row + k0 + 16]);
-                        const vk_h16x8 al = __builtin_bit_cast(vk_h16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
-                        o_acc[os] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, o_acc[os], 0, 0, 0);
-                    }
-                }
-            }
-        }
+        if (active) tile(kt, mask_tag);
         VK_LDS_BARRIER();
-    }
+    };
+    int n_full = min(n_tiles, tkv / KT);
+    if (causal) n_full = min(n_full, (q_off + qt * QT + 1) / KT);
+    int kt = 0;
+    for (; kt < n_full; ++kt) step(kt, AttnMask<false>{});
+    for (; kt < n_tiles; ++kt) step(kt, AttnMask<true>{});
     if (active) finish(o_acc, l_run > 0.0f ? 1.0f / l_run : 0.0f);
 }
 
@@ -493,6 +603,8 @@ __global__ __launch_bounds__(256) void vk_flash_attn(
 #include "vk_launch.h"
 
 namespace vk {
+
+float attn_q_scale(float scale) { return scale * attn::kLog2e; }
 
 hipError_t launch_split_rows(hipStream_t s, const float* x, size_t n, float scale, void* hi, void* lo) {
     const size_t n4 = n / 4;
@@ -511,10 +623,19 @@ hipError_t launch_split_rows_q7(hipStream_t s, const float* x, size_t n, float s
 }
 
 hipError_t launch_split_vt_q7(hipStream_t s, const float* v, int batch, int t_kv, int t_pad, int h_kv, int hd,
-                              void* vth, void* vtl) {
+                              void* vth, void* vtl, bool tiled) {
     if (batch == 0 || t_pad == 0) return hipSuccess;
     hipLaunchKernelGGL(vk_split_vt_q7, dim3(t_pad / 64, h_kv * (hd / 64), batch), dim3(256), 0, s, v, t_kv, t_pad,
-                       h_kv, hd, (uint16_t*)vth, (int8_t*)vtl);
+                       h_kv, hd, tiled ? 1 : 0, (uint16_t*)vth, (int8_t*)vtl);
+    return hipGetLastError();
+}
+
+hipError_t launch_split_rows_q7_heads(hipStream_t s, const float* x, int batch, int t, int h, int hd, float scale,
+                                      void* hi, void* lo) {
+    const size_t n4 = (size_t)batch * t * h * hd / 4;
+    if (n4 == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_split_rows_q7_heads, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, x, n4, t, h,
+                       hd / 4, scale, (uint2*)hi, (uint32_t*)lo);
     return hipGetLastError();
 }
 
@@ -526,64 +647,129 @@ hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, i
     return hipGetLastError();
 }
 
-template <int HD, int LOM>
-static void go_flash1(hipStream_t s, dim3 grid, const void* qh, const void* ql, const void* kh, const void* kl,
-                      const void* vth, const void* vtl, float* out, int tq, int tkv, int t_pad, int hq, int hkv,
-                      int causal, int q_off, const int* kv_index, const float* qf, float q_scale, const VkQOut& qo) {
-    if (tq == 1)
-        hipLaunchKernelGGL((vk_flash_attn<HD, LOM, true>), grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
-                           (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv,
-                           t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
-    else
-        hipLaunchKernelGGL((vk_flash_attn<HD, LOM, false>), grid, dim3(256), 0, s, (const uint4*)qh, (const uint4*)ql,
-                           (const uint4*)kh, (const uint4*)kl, (const uint4*)vth, (const uint4*)vtl, out, tq, tkv,
-                           t_pad, hq, hkv, causal, q_off, kv_index, qf, q_scale, qo);
+AttnLayout attn_layout_rows(int t_kv, int h_kv, int hd, int t_pad) {
+    AttnLayout l;
+    l.kt = h_kv * hd;
+    l.kh = hd;
+    l.kb = (long long)t_kv * h_kv * hd;
+    l.vd = t_pad;
+    l.vtile = attn::KT;
+    return l;
+}
+
+AttnLayout attn_layout_heads(int t_kv, int h_kv, int hd, int t_pad) {
+    AttnLayout l;
+    l.kt = hd;
+    l.kh = (long long)t_kv * hd;
+    l.kb = (long long)t_kv * h_kv * hd;
+    l.vd = attn::KT;
+    l.vtile = attn::KT * hd;
+    (void)t_pad;
+    return l;
+}
+
+namespace {
+// One flash launch's operands (the kernel's arguments).
+struct FlashArgs {
+    const void *qh, *ql, *kh, *kl, *vth, *vtl;
+    float* out;
+    int tq, tkv, t_pad, hq, hkv, causal, q_off;
+    const int* kv_index;
+    const float* qf;
+    float q_scale;
+    VkQOut qo;
+    AttnLayout lay;
+};
+
+// Dynamic LDS that sets a single-query launch's residency. Those launches
+// stream K / V from HBM and finish in rounds of (CUs x workgroups per CU); a
+// last round that holds few workgroups per CU leaves HBM underused while it
+// runs. When the grid needs more than one round at the kernel's full
+// residency r, one fewer per CU is taken if that fills the last round better
+// (decoder step, 64 streams x 20 heads = 1280 workgroups, compact K / V: r = 4
+// gives rounds of 1024 + 256, 3 gives 768 + 512; 7.95 -> 7.43 ms per step;
+// 2 per CU measured 8.17 ms). The padded total sits midway between the two
+// residencies: a total just under a third of the LDS (54272 bytes) ran like
+// 2 per CU.
+int oneq_lds_pad(int r_full, int lds_static, size_t n_wg) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 0;
+    if (r_full <= 1 || n_wg <= (size_t)cus * r_full) return 0;
+    auto fill = [&](int r) {  // share of the last round's slots in use
+        const size_t per = (size_t)cus * r, last = n_wg % per;
+        return last == 0 ? 1.0 : (double)last / (double)per;
+    };
+    if (fill(r_full - 1) <= fill(r_full)) return 0;
+    // a workgroup's LDS total midway between what fits r_full - 1 and r_full
+    // times, clear of the allocation granularity either way
+    const int total = ((attn::kLdsPerCu / r_full + attn::kLdsPerCu / (r_full - 1)) / 2) & ~1023;
+    return total > attn::kLdsPerCu / r_full && total > lds_static ? total - lds_static : 0;
+}
+
+template <int HD, int LOM, bool ONEQ>
+void go_flash(hipStream_t s, dim3 grid, const FlashArgs& a) {
+    int pad = 0;
+    if (ONEQ) {
+        static int r_full = -1;  // workgroups per CU without padding (same for every gfx950 device)
+        if (r_full < 0 &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&r_full, reinterpret_cast<const void*>(&vk_flash_attn<HD, LOM, ONEQ>),
+                                                          256, 0) != hipSuccess)
+            r_full = 0;
+        pad = oneq_lds_pad(r_full, attn::flash_lds_bytes(HD, LOM != 0 ? 2 : 1),
+                           (size_t)grid.x * grid.y * grid.z);
+    }
+    hipLaunchKernelGGL((vk_flash_attn<HD, LOM, ONEQ>), grid, dim3(256), pad, s, (const uint4*)a.qh,
+                       (const uint4*)a.ql, (const uint4*)a.kh, (const uint4*)a.kl, (const uint4*)a.vth,
+                       (const uint4*)a.vtl, a.out, a.tq, a.tkv, a.t_pad, a.hq, a.hkv, a.causal, a.q_off, a.kv_index,
+                       a.qf, a.q_scale, a.qo, a.lay);
 }
 
 template <int HD>
-static void go_flash_hd(hipStream_t s, dim3 grid, const void* qh, const void* ql, const void* kh, const void* kl,
-                        const void* vth, const void* vtl, float* out, int tq, int tkv, int t_pad, int hq, int hkv,
-                        int causal, int q_off, const int* kv_index, const float* qf, float q_scale, int lo_mode,
-                        const VkQOut& qo) {
-    if (lo_mode == KV_LO_Q7 && tq == 1)  // the compact form exists for single-query launches only
-        go_flash1<HD, 2>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf,
-                         q_scale, qo);
+void go_flash_hd(hipStream_t s, dim3 grid, int lo_mode, const FlashArgs& a) {
+    const bool one = a.tq == 1;
+    if (lo_mode == KV_LO_Q7)  // the compact form exists for single-query launches only
+        go_flash<HD, 2, true>(s, grid, a);
     else if (lo_mode == KV_LO_F16)
-        go_flash1<HD, 1>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf,
-                         q_scale, qo);
+        one ? go_flash<HD, 1, true>(s, grid, a) : go_flash<HD, 1, false>(s, grid, a);
     else
-        go_flash1<HD, 0>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf,
-                         q_scale, qo);
+        one ? go_flash<HD, 0, true>(s, grid, a) : go_flash<HD, 0, false>(s, grid, a);
 }
 
-static hipError_t flash_any(hipStream_t s, int hd, const void* qh, const void* ql, const float* qf, float q_scale,
-                            const void* kh, const void* kl, const void* vth, const void* vtl, float* out, int batch,
-                            int tq, int tkv, int t_pad, int hq, int hkv, int causal, int q_off, const int* kv_index,
-                            int lo_mode, const VkQOut& qo) {
-    if (lo_mode == KV_LO_Q7 && tq != 1) return hipErrorInvalidValue;
-    const dim3 grid((tq + attn::QT - 1) / attn::QT, hq, batch);
+hipError_t flash_any(hipStream_t s, int hd, int batch, int lo_mode, const FlashArgs& a) {
+    if (lo_mode == KV_LO_Q7 && a.tq != 1) return hipErrorInvalidValue;
+    // buffer-resource extents (one kv head's V^T slab, 64 K rows) and the
+    // per-lane 32-bit K offsets, in bytes
+    if ((size_t)hd * a.t_pad * 2 > 0x7fffffffu || (size_t)attn::KT * a.lay.kt * 2 > 0x7fffffffu)
+        return hipErrorInvalidValue;
+    const dim3 grid((a.tq + attn::QT - 1) / attn::QT, a.hq, batch);
     if (hd == 64)
-        go_flash_hd<64>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf,
-                        q_scale, lo_mode, qo);
+        go_flash_hd<64>(s, grid, lo_mode, a);
     else
-        go_flash_hd<128>(s, grid, qh, ql, kh, kl, vth, vtl, out, tq, tkv, t_pad, hq, hkv, causal, q_off, kv_index, qf,
-                         q_scale, lo_mode, qo);
+        go_flash_hd<128>(s, grid, lo_mode, a);
     return hipGetLastError();
 }
+}  // namespace
 
 hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* ql, const void* kh, const void* kl,
                              const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
                              int hq, int hkv, int causal, int q_off, const int* kv_index, int lo_mode) {
-    return flash_any(s, hd, qh, ql, nullptr, 1.0f, kh, kl, vth, vtl, out, batch, tq, tkv, t_pad, hq, hkv, causal,
-                     q_off, kv_index, lo_mode, VkQOut{});
+    const FlashArgs a = {qh,     ql,      kh,       kl,       vth,     vtl,  out,       tq,
+                         tkv,    t_pad,   hq,       hkv,      causal,  q_off, kv_index, nullptr,
+                         1.0f,   VkQOut{}, attn_layout_rows(tkv, hkv, hd, t_pad)};
+    return flash_any(s, hd, batch, lo_mode, a);
 }
 
 hipError_t launch_flash_attn_f32q(hipStream_t s, int hd, const float* q, float q_scale, const void* kh, const void* kl,
                                   const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
                                   int hq, int hkv, int causal, int q_off, const int* kv_index, int lo_mode,
-                                  const VkQOut* qo) {
-    return flash_any(s, hd, nullptr, nullptr, q, q_scale, kh, kl, vth, vtl, out, batch, tq, tkv, t_pad, hq, hkv,
-                     causal, q_off, kv_index, lo_mode, qo ? *qo : VkQOut{});
+                                  const VkQOut* qo, const AttnLayout* lay) {
+    const FlashArgs a = {nullptr, nullptr, kh,     kl,    vth,      vtl,
+                         out,     tq,      tkv,    t_pad, hq,       hkv,
+                         causal,  q_off,   kv_index, q,   attn_q_scale(q_scale), qo ? *qo : VkQOut{},
+                         lay ? *lay : attn_layout_rows(tkv, hkv, hd, t_pad)};
+    return flash_any(s, hd, batch, lo_mode, a);
 }
 
 // Reads and clears this file's fp16-range flag on the current device; the

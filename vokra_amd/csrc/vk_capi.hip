@@ -418,7 +418,8 @@ int run_attn(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t hq, s
     VK_TRY(c->at_vh.ensure(nv * 2 + 16), "hipMalloc(attention v)");
     VK_TRY(c->at_vl.ensure(nv * (q7 ? 1 : 2) + 16), "hipMalloc(attention v)");
     if (!q_in_kernel)
-        VK_TRY(vk::launch_split_rows(c->stream, d_q, nq, scale, c->at_qh.p, c->at_ql.p), "launch(vk_split_rows q)");
+        VK_TRY(vk::launch_split_rows(c->stream, d_q, nq, vk::attn_q_scale(scale), c->at_qh.p, c->at_ql.p),
+               "launch(vk_split_rows q)");
     if (q7) {
         VK_TRY(vk::launch_split_rows_q7(c->stream, d_k, nk, 1.0f, c->at_kh.p, c->at_kl.p), "launch(vk_split_rows_q7 k)");
         VK_TRY(vk::launch_split_vt_q7(c->stream, d_v, (int)batch, (int)tkv, (int)t_pad, (int)hkv, (int)hd, c->at_vh.p,

@@ -127,22 +127,45 @@ hipError_t launch_split_vt(hipStream_t s, const float* v, int batch, int t_kv, i
 // split_q7): lo holds n bytes / one byte per V^T element.
 hipError_t launch_split_rows_q7(hipStream_t s, const float* x, size_t n, float scale, void* hi, void* lo);
 hipError_t launch_split_vt_q7(hipStream_t s, const float* v, int batch, int t_kv, int t_pad, int h_kv, int hd,
-                              void* vth, void* vtl);
+                              void* vth, void* vtl, bool tiled = false);
+// x [B][T][H*hd] -> hi / lo [B][H][T][hd] (the attn_layout_heads K form)
+hipError_t launch_split_rows_q7_heads(hipStream_t s, const float* x, int batch, int t, int h, int hd, float scale,
+                                      void* hi, void* lo);
+// Element strides of a flash launch's K / V operands: K element (b, t, h, d)
+// at b * kb + h * kh + t * kt + d; V^T element (b, h, d, t) at
+// (b * h_kv + h) * hd * t_pad + (t / 64) * vtile + d * vd + t % 64.
+struct AttnLayout {
+    long long kb, kh;
+    int kt, vd, vtile;
+};
+// K [B][T][H*hd], V^T [B][H][hd][T_pad] (the split passes' default forms)
+AttnLayout attn_layout_rows(int t_kv, int h_kv, int hd, int t_pad);
+// K [B][H][T][hd], V^T [B][H][T_pad / 64][hd][64]: every 64-key tile of a
+// head is one contiguous block (launch_split_rows_q7_heads, tiled V^T split)
+AttnLayout attn_layout_heads(int t_kv, int h_kv, int hd, int t_pad);
 // K / V low parts of a flash-attention launch: none (fp16 high parts only;
 // kl, vtl unused), fp16, or the compact one-byte form (single-query launches).
 enum { KV_LO_NONE = 0, KV_LO_F16 = 1, KV_LO_Q7 = 2 };
+// The factor the flash kernel takes q in: its scores come out in base-2 units,
+// so q is split (launch_split_rows) as q * attn_q_scale(scale) = q * scale *
+// log2(e).
+float attn_q_scale(float scale);
+// qh / ql: the split of q * attn_q_scale(scale). hd * t_pad * 2 and
+// 64 * hkv * hd * 2 must stay below 2^31 (buffer-resource extents).
 hipError_t launch_flash_attn(hipStream_t s, int hd, const void* qh, const void* ql, const void* kh, const void* kl,
                              const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
                              int hq, int hkv, int causal, int q_off, const int* kv_index = nullptr,
                              int lo_mode = KV_LO_F16);
-// The same with q given as f32 [B][Tq][Hq*hd] (16-byte aligned): the kernel
-// splits q * q_scale itself exactly as launch_split_rows would. With qo, the
+// The same with q given as f32 [B][Tq][Hq*hd] (16-byte aligned) and the
+// softmax scale: the kernel splits q * attn_q_scale(q_scale) itself exactly
+// as launch_split_rows would. With qo, the
 // kernel also quantizes O (rows b * tq + i, width hq * hd) into qo's
 // activation fragments, and out may be null.
 hipError_t launch_flash_attn_f32q(hipStream_t s, int hd, const float* q, float q_scale, const void* kh, const void* kl,
                                   const void* vth, const void* vtl, float* out, int batch, int tq, int tkv, int t_pad,
                                   int hq, int hkv, int causal, int q_off, const int* kv_index = nullptr,
-                                  int lo_mode = KV_LO_F16, const VkQOut* qo = nullptr);
+                                  int lo_mode = KV_LO_F16, const VkQOut* qo = nullptr,
+                                  const AttnLayout* lay = nullptr);  // null: attn_layout_rows
 }  // namespace vk
 
 namespace vk {

@@ -365,8 +365,12 @@ int dec_set_encoder(vokra_hip_decoder* m, size_t stream, const float* d_enc) {
         int8_t* kl = (int8_t*)m->ckl.p + sl * na * d;
         uint16_t* vh = (uint16_t*)m->cvh.p + sl * d * m->t_pad;
         int8_t* vl = (int8_t*)m->cvl.p + sl * d * m->t_pad;
-        SS_HIP(vk::launch_split_rows_q7(s, m->tk.f(), na * d, 1.0f, kh, kl), "launch(vk_split_rows_q7 cross k)");
-        SS_HIP(vk::launch_split_vt_q7(s, m->tv.f(), 1, (int)na, (int)m->t_pad, (int)m->n_head, (int)m->hd, vh, vl),
+        // head-major K and tiled V^T: each 64-frame tile of a head is one
+        // contiguous block for the single-query cross-attention stream
+        SS_HIP(vk::launch_split_rows_q7_heads(s, m->tk.f(), 1, (int)na, (int)m->n_head, (int)m->hd, 1.0f, kh, kl),
+               "launch(vk_split_rows_q7_heads cross k)");
+        SS_HIP(vk::launch_split_vt_q7(s, m->tv.f(), 1, (int)na, (int)m->t_pad, (int)m->n_head, (int)m->hd, vh, vl,
+                                      true),
                "launch(vk_split_vt_q7 cross v)");
     }
     return VOKRA_HIP_OK;
@@ -412,11 +416,12 @@ int dec_step(vokra_hip_decoder* m, size_t n, const int* d_streams, const int* d_
         // fused form)
         VkQOut qo;
         SS_TRY(vk::qact_output(c, m->qa_d, n, act, &qo));
+        const vk::AttnLayout lay = vk::attn_layout_heads((int)m->n_audio, (int)m->n_head, (int)m->hd, (int)m->t_pad);
         SS_HIP(vk::launch_flash_attn_f32q(s, (int)m->hd, m->q.f(), scale, m->ckh.p, m->ckl.p, m->cvh.p, m->cvl.p,
                                           qo.afrag ? nullptr : m->attn.f(), (int)n, 1, (int)m->n_audio,
                                           (int)m->t_pad, (int)m->n_head, (int)m->n_head, 0, 0, m->kvidx.i() + l * n,
                                           m->cross_precision == VOKRA_HIP_CROSS_F32 ? vk::KV_LO_Q7 : vk::KV_LO_NONE,
-                                          qo.afrag ? &qo : nullptr),
+                                          qo.afrag ? &qo : nullptr, &lay),
                "launch(vk_flash_attn cross)");
         if (qo.afrag) vk::qact_outputs_written(m->qa_d, n, act);
         else SS_TRY(vokra_hip_qact_quantize_dev(c, m->qa_d, n, m->attn.f(), act));
