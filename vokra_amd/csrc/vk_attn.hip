@@ -74,6 +74,21 @@ __device__ __forceinline__ float attn_fmax_raw(float a, float b) {
     asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
     return r;
 }
+// x - (float)h for h the low (H = 0) or high (H = 1) fp16 of hpair, in one
+// v_fma_mix_f32 (x + h * -1, one rounding: the exact difference when h is
+// x's own fp16 rounding), instead of a conversion and a subtraction
+template <int H>
+struct AttnHalf {};
+__device__ __forceinline__ float attn_sub_f16(float x, uint32_t hpair, AttnHalf<0>) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(hpair), "v"(x));
+    return r;
+}
+__device__ __forceinline__ float attn_sub_f16(float x, uint32_t hpair, AttnHalf<1>) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(hpair), "v"(x));
+    return r;
+}
 __device__ __forceinline__ float attn_query_max(float v) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     v = attn_fmax_raw(__uint_as_float(a[0]), __uint_as_float(a[1]));
@@ -523,7 +538,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void v
                 psum += p.x;
                 psum += p.y;
                 const vk_h16x2a hi = __builtin_convertvector(p, vk_h16x2a);
-                const vk_h16x2a lo = __builtin_convertvector(p - __builtin_convertvector(hi, vk_f32x2), vk_h16x2a);
+                const uint32_t hb = __builtin_bit_cast(uint32_t, hi);
+                const vk_f32x2 d = {attn_sub_f16(p.x, hb, AttnHalf<0>{}), attn_sub_f16(p.y, hb, AttnHalf<1>{})};
+                const vk_h16x2a lo = __builtin_convertvector(d, vk_h16x2a);
                 ph[n >> 1][2 * (n & 1) + r / 2] = __builtin_bit_cast(uint32_t, hi);
                 pl[n >> 1][2 * (n & 1) + r / 2] = __builtin_bit_cast(uint32_t, lo);
             }
