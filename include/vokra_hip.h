@@ -309,9 +309,10 @@ int vokra_hip_logits_argmax_dev(vokra_hip_ctx_t *ctx, size_t rows, size_t vocab,
  * parts of k and v are held in one byte each, an integer times the fp16 high
  * part's ulp / 128 (relative error at most 2^-18 / (1 - 2^-12), a quarter
  * fewer bytes for the bandwidth-bound single-query case); the decoder
- * session's cross-attention uses the same form. A finite q * scale, k or v element
- * of magnitude >= 65520 (beyond fp16) is INVALID_ARGUMENT: here after the
- * launch, for the _dev form at the next vokra_hip_synchronize. */
+ * session's cross-attention uses the same form. q is split as
+ * q * scale * log2(e) (the softmax runs in base 2); a finite element of that,
+ * of k or of v with magnitude >= 65520 (beyond fp16) is INVALID_ARGUMENT: here
+ * after the launch, for the _dev form at the next vokra_hip_synchronize. */
 int vokra_hip_attn_f32(vokra_hip_ctx_t *ctx, size_t batch, size_t t_q, size_t t_kv, size_t n_head_q,
                        size_t n_head_kv, size_t head_dim, const float *q, const float *k, const float *v,
                        float scale, int causal, size_t q_offset, float *out);
