@@ -709,10 +709,14 @@ struct FlashArgs {
 // residencies: a total just under a third of the LDS (54272 bytes) ran like
 // 2 per CU.
 int oneq_lds_pad(int r_full, int lds_static, size_t n_wg) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        return 0;
+    static int cus = -1;  // CUs per device (the same on every gfx950 device)
+    if (cus < 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 0;
+    }
+    if (cus <= 0) return 0;
     if (r_full <= 1 || n_wg <= (size_t)cus * r_full) return 0;
     auto fill = [&](int r) {  // share of the last round's slots in use
         const size_t per = (size_t)cus * r, last = n_wg % per;
