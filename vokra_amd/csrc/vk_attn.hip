@@ -709,13 +709,13 @@ struct FlashArgs {
 // residencies: a total just under a third of the LDS (54272 bytes) ran like
 // 2 per CU.
 int oneq_lds_pad(int r_full, int lds_static, size_t n_wg) {
-    static int cus = -1;  // CUs per device (the same on every gfx950 device)
-    if (cus < 0) {
-        int dev = 0;
+    static const int cus = [] {  // CUs per device (the same on every gfx950 device)
+        int dev = 0, n = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            cus = 0;
-    }
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        return n;
+    }();
     if (cus <= 0) return 0;
     if (r_full <= 1 || n_wg <= (size_t)cus * r_full) return 0;
     auto fill = [&](int r) {  // share of the last round's slots in use
@@ -733,11 +733,13 @@ template <int HD, int LOM, bool ONEQ>
 void go_flash(hipStream_t s, dim3 grid, const FlashArgs& a) {
     int pad = 0;
     if (ONEQ) {
-        static int r_full = -1;  // workgroups per CU without padding (same for every gfx950 device)
-        if (r_full < 0 &&
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&r_full, reinterpret_cast<const void*>(&vk_flash_attn<HD, LOM, ONEQ>),
-                                                          256, 0) != hipSuccess)
-            r_full = 0;
+        static const int r_full = [] {  // workgroups per CU without padding (same for every gfx950 device)
+            int r = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                    &r, reinterpret_cast<const void*>(&vk_flash_attn<HD, LOM, ONEQ>), 256, 0) != hipSuccess)
+                return 0;
+            return r;
+        }();
         pad = oneq_lds_pad(r_full, attn::flash_lds_bytes(HD, LOM != 0 ? 2 : 1),
                            (size_t)grid.x * grid.y * grid.z);
     }
