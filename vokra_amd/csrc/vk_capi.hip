@@ -521,10 +521,11 @@ hipStream_t ctx_stream(const vokra_hip_ctx* c) { return c->stream; }
 // attention kernels into INVALID_ARGUMENT (the explicit failure of
 // compute.rs:649-696 instead of an inf / NaN result).
 int range_check(vokra_hip_ctx* c) {
-    unsigned a = 0, b = 0;
+    unsigned a = 0, b = 0, g = 0;
     VK_TRY(attn_range_take(c->stream, &a), "attention range flag");
     VK_TRY(kv_range_take(c->stream, &b), "attention range flag");
-    if (a || b)
+    VK_TRY(gemm_range_take(c->stream, &g), "attention range flag");
+    if (a || b || g)
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
                     "attention: an operand is outside the fp16 range of the split products (|x| >= 65520 after "
                     "scaling); the results of the calls since the last check are not valid");
@@ -614,6 +615,32 @@ int gemm_qact_multi(vokra_hip_ctx* c, int n, const vokra_hip_qweight* const* ws,
                                   (const uint4*)qa->frag.p, (const float*)qa->scale.p, (const float*)qa->gsum.p, lins,
                                   n, (int)qa->m, (int)ws[0]->nb, (int)qa->m_pad),
            "launch(vk_gemv_qblock x n)");
+    return VOKRA_HIP_OK;
+}
+
+int gemm_qact_qkv_split(vokra_hip_ctx* c, const vokra_hip_qweight* const* ws, const vokra_hip_qact* qa,
+                        const float* const* biases, float* q_out, const VkSplitOut& ks, float* v_out, bool* fused) {
+    *fused = false;
+    for (int i = 0; i < 3; ++i) {
+        int st = check_gemm_qact(c, ws[i], qa, q_out);
+        if (st) return st;
+    }
+    // the one-grid block-GEMM route with whole 128-column tiles only
+    bool ok = qa->act_quant != VOKRA_HIP_ACT_KQUANT;
+    for (int i = 0; i < 3 && ok; ++i)
+        ok = !ws[i]->kquant && !gemv_route(c, ws[i], qa) && ws[i]->n == ws[0]->n && ws[i]->n_pad == ws[i]->n &&
+             ws[i]->n % 128 == 0;
+    if (!ok) return VOKRA_HIP_OK;
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VkGemmLin lins[3];
+    for (int i = 0; i < 3; ++i)
+        lins[i] = {(const uint4*)ws[i]->frag.p, (const float*)ws[i]->scale.p, biases ? biases[i] : nullptr,
+                   i == 0 ? q_out : i == 2 ? v_out : nullptr, {nullptr, 0}, VkQOut{}, i == 1 ? ks : VkSplitOut{}};
+    VK_TRY(vk::launch_gemm_qblock_multi(c->stream, qa->act_quant == VOKRA_HIP_ACT_POW2, (const uint4*)qa->frag.p,
+                                        (const float*)qa->scale.p, lins, 3, (int)qa->m, (int)qa->m_pad,
+                                        (int)ws[0]->n, (int)ws[0]->n_pad, (int)ws[0]->nb),
+           "launch(vk_gemm_qblock q, split k, v)");
+    *fused = true;
     return VOKRA_HIP_OK;
 }
 
@@ -745,6 +772,23 @@ int attn_quantize(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t 
     st = run_attn(c, batch, tq, tkv, hq, hkv, hd, d_q, d_k, d_v, scale, causal, q_off, d_out, &qo, false);
     if (st) return st;
     qact_commit(qa, batch * tq, act_quant);
+    return VOKRA_HIP_OK;
+}
+
+int attn_quantize_split(vokra_hip_ctx* c, size_t batch, size_t t, size_t h, size_t hd, const float* d_q,
+                        const void* kh, const void* kl, const void* vth, const void* vtl, size_t t_pad, float scale,
+                        float* d_out, vokra_hip_qact* qa, int act_quant) {
+    VkQOut qo;
+    int st = qact_bind(c, qa, batch * t, act_quant, &qo);
+    if (st) return st;
+    if (!qo.afrag || qa->k != h * hd || t < 2 || check_attn(batch, t, t, h, h, hd) ||
+        (reinterpret_cast<uintptr_t>(d_q) & 15))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "attn: split operands need the fused activation pass");
+    VK_TRY(set_dev(c), "hipSetDevice");
+    VK_TRY(vk::launch_flash_attn_f32q(c->stream, (int)hd, d_q, scale, kh, kl, vth, vtl, nullptr, (int)batch, (int)t,
+                                      (int)t, (int)t_pad, (int)h, (int)h, 0, 0, nullptr, vk::KV_LO_F16, &qo),
+           "launch(vk_flash_attn)");
+    qact_commit(qa, batch * t, act_quant);
     return VOKRA_HIP_OK;
 }
 

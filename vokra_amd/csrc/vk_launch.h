@@ -26,13 +26,21 @@ struct VkQOut {
 };
 // One linear of a multi-linear block-GEMM launch: bf16 fragments + scales,
 // optional bias, output [m, n].
+// With hi != null a block-GEMM linear's outputs (bias added) leave as the
+// flash-attention kernel's fp16 operands, hi = fp16(x), lo = fp16(x - hi),
+// row-major [rows][n], in place of f32 (vk_split_rows's arithmetic).
+struct VkSplitOut {
+    uint16_t* hi;
+    uint16_t* lo;
+};
 struct VkGemmLin {
     const uint4* wfrag;
     const float* wscale;
     const float* bias;
-    float* out;  // may be null when qo is set
+    float* out;  // may be null when qo or so is set
     VkEpi epi;
     VkQOut qo;   // qo.afrag != null: the activation pass over the outputs (n % 128 == 0)
+    VkSplitOut so;
 };
 // One linear of a decode-kernel launch: compact weights, optional bias, output [m, n].
 struct VkGemvLin {
@@ -203,6 +211,7 @@ bool paged_attn_rotates_q(const KvView& v, int hq, int hd, const float* q, const
 // Read and clear the fp16-range flags of the attention kernels (vk_attn.hip)
 // and of the GQA decode kernel (vk_kvcache.hip) on the current device.
 hipError_t attn_range_take(hipStream_t s, unsigned* raised);
+hipError_t gemm_range_take(hipStream_t s, unsigned* raised);  // the split outputs' fp16-range flag
 hipError_t kv_range_take(hipStream_t s, unsigned* raised);
 // Packs rows into pages given by an earlier launch_kv_alloc_layers (items
 // whose page is missing are skipped).
@@ -298,6 +307,17 @@ int gemm_qact_quantize(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra
 int attn_quantize(vokra_hip_ctx* c, size_t batch, size_t tq, size_t tkv, size_t hq, size_t hkv, size_t hd,
                   const float* d_q, const float* d_k, const float* d_v, float scale, int causal, size_t q_off,
                   float* d_out, vokra_hip_qact* qa, int act_quant);
+//   gemm_qact_qkv_split + launch_split_vt + attn_quantize_split =
+//   gemm_qact_multi of q, k, v, then attn_quantize (non-causal self-attention),
+//   with k leaving the GEMM already as the attention kernel's fp16 hi / lo
+//   operands (vk_split_rows's values). *fused is false (and nothing ran) when
+//   the three linears do not take the one-grid block-GEMM route; the caller
+//   then runs the pair it replaces.
+int gemm_qact_qkv_split(vokra_hip_ctx* c, const vokra_hip_qweight* const* ws, const vokra_hip_qact* qa,
+                        const float* const* biases, float* q_out, const VkSplitOut& ks, float* v_out, bool* fused);
+int attn_quantize_split(vokra_hip_ctx* c, size_t batch, size_t t, size_t h, size_t hd, const float* d_q,
+                        const void* kh, const void* kl, const void* vth, const void* vtl, size_t t_pad, float scale,
+                        float* d_out, vokra_hip_qact* qa, int act_quant);
 int paged_attn_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                         const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
                         vokra_hip_qact* qa, int act_quant, const float2* rope_cs = nullptr);

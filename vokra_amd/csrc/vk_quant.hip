@@ -385,6 +385,10 @@ __global__ void vk_repack_w_b32(int mode, const uint8_t* __restrict__ wq, int n,
 // The epilogue transposes each wave's 16 x 64 row strips through LDS so rows
 // leave as full 256-byte dwordx4 stores (streaming: the result is not re-read
 // by this kernel).
+// Set (to 1) by a block GEMM whose split outputs (VkSplitOut) meet a value
+// outside the fp16 range; read and cleared by the host (gemm_range_take).
+static __device__ unsigned int vk_gemm_range_flag;
+
 namespace gemm {
 constexpr int WM = 2, WN = 2;                 // waves per workgroup (m x n)
 constexpr int THREADS = 64 * WM * WN;
@@ -453,6 +457,7 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
     float* out = set.lin[li].out;
     const VkEpi epi = set.lin[li].epi;
     const VkQOut qo = set.lin[li].qo;  // used when QOUT (every linear of the launch has it)
+    const VkSplitOut so = set.lin[li].so;
 
     // Per-thread slice of one stage: A fragments wave + q WAVES (q < APT), B
     // fragments likewise, and one scale (threads [0, TM): A rows, [TM, TM+TN):
@@ -617,14 +622,39 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void vk_gemm_qblock(
                         }
                     }
                 }
-                if (row < m && out)
+                if (row < m && so.hi) {  // row-major split (k)
+                    const float e4[4] = {v.x, v.y, v.z, v.w};
+                    uint32_t hw[2], lw[2];
+                    bool bad = false;
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const float x0 = e4[2 * u], x1 = e4[2 * u + 1];
+                        bad |= vk_f16_overflow(x0) | vk_f16_overflow(x1);
+                        const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+                        const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
+                        hw[u] = __builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                        lw[u] = __builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+                    }
+                    if (bad) atomicOr(&vk_gemm_range_flag, 1u);
+                    *reinterpret_cast<uint2*>(so.hi + o) = make_uint2(hw[0], hw[1]);
+                    *reinterpret_cast<uint2*>(so.lo + o) = make_uint2(lw[0], lw[1]);
+                } else if (row < m && out)
                     __builtin_nontemporal_store((vk_f32x4){v.x, v.y, v.z, v.w}, reinterpret_cast<vk_f32x4*>(out + o));
             } else if (row < m) {
                 const float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int col = col0 + c4 + u;
-                    if (col < n) out[o + u] = vk_epi_apply(bias ? e[u] + bias[col] : e[u], epi, o + u);
+                    if (col >= n) continue;
+                    const float y = vk_epi_apply(bias ? e[u] + bias[col] : e[u], epi, o + u);
+                    if (so.hi) {  // row-major split (k)
+                        if (vk_f16_overflow(y)) atomicOr(&vk_gemm_range_flag, 1u);
+                        const _Float16 h = (_Float16)y;
+                        so.hi[o + u] = __builtin_bit_cast(uint16_t, h);
+                        so.lo[o + u] = __builtin_bit_cast(uint16_t, (_Float16)(y - (float)h));
+                    } else {
+                        out[o + u] = y;
+                    }
                 }
             }
         }
@@ -778,6 +808,19 @@ hipError_t launch_gemm_qblock_multi(hipStream_t s, bool pow2, const uint4* afrag
     }
 #undef VK_GQ
     return hipGetLastError();
+}
+
+hipError_t gemm_range_take(hipStream_t s, unsigned* raised) {
+    unsigned v = 0;
+    hipError_t e = hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(vk_gemm_range_flag), sizeof v, 0, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e == hipSuccess && v) {
+        const unsigned z = 0;
+        e = hipMemcpyToSymbolAsync(HIP_SYMBOL(vk_gemm_range_flag), &z, sizeof z, 0, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+    }
+    *raised = v;
+    return e;
 }
 
 hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,

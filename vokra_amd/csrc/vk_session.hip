@@ -142,13 +142,20 @@ struct vokra_hip_encoder {
     // conv stem (optional): weights, positional embedding, im2col / conv1 workspaces
     size_t n_mels = 0, n_frames = 0, n_ctx = 0, stem_batch = 0;
     DBuf c1w, c1b, c2w, c2b, pos, col1, c1, col2;
+    // attention V^T as fp16 hi / lo [batch][d / hd][hd][t_pad] (the v split
+    // pass's output; k's hi / lo, written by the q/k/v GEMM, take k's own
+    // buffer)
+    DBuf vt_hi, vt_lo;
+    size_t vt_cap = 0;
     void release() {
         for (auto& L : layers) {
             for (DBuf* b : {&L.ln1g, &L.ln1b, &L.ln2g, &L.ln2b}) b->release(ctx);
             for (QLin* w : {&L.q, &L.k, &L.v, &L.o, &L.fc1, &L.fc2}) w->release(ctx);
         }
-        for (DBuf* b : {&lnpg, &lnpb, &h, &x, &q, &k, &v, &attn, &f, &c1w, &c1b, &c2w, &c2b, &pos, &col1, &c1, &col2})
+        for (DBuf* b : {&lnpg, &lnpb, &h, &x, &q, &k, &v, &attn, &f, &c1w, &c1b, &c2w, &c2b, &pos, &col1, &c1, &col2,
+                        &vt_hi, &vt_lo})
             b->release(ctx);
+        vt_cap = 0;
         vokra_hip_qact_free(qa_d);
         vokra_hip_qact_free(qa_f);
         qa_d = qa_f = nullptr;
@@ -217,11 +224,25 @@ int enc_setup(vokra_hip_encoder* e, const vokra_hip_prenorm_layer_t* layers, con
     return VOKRA_HIP_OK;
 }
 
+// V^T hi / lo buffers of at least `bytes` each (the split pass writes every
+// element, zeros past each row's frames)
+int enc_vt_ensure(vokra_hip_encoder* e, size_t bytes) {
+    if (bytes <= e->vt_cap) return VOKRA_HIP_OK;
+    e->vt_hi.release(e->ctx);
+    e->vt_lo.release(e->ctx);
+    e->vt_cap = 0;
+    SS_TRY(e->vt_hi.alloc(e->ctx, bytes));
+    SS_TRY(e->vt_lo.alloc(e->ctx, bytes));
+    e->vt_cap = bytes;
+    return VOKRA_HIP_OK;
+}
+
 int enc_forward(vokra_hip_encoder* e, size_t batch, size_t frames, const float* d_x, float* d_out) {
     vokra_hip_ctx_t* c = e->ctx;
     const size_t rows = batch * frames, d = e->d;
     const int act = act_of(e->wdtype);
     const float scale = powf((float)e->hd, -0.5f);  // (hd as f32).powf(-0.5), nn.rs:267
+    const size_t t_pad = (frames + 63) / 64 * 64;
     SS_HIP(hipMemcpyAsync(e->h.p, d_x, rows * d * sizeof(float), hipMemcpyDeviceToDevice, vk::ctx_stream(c)),
            "encoder: hipMemcpyAsync");
     // Per block the entry-point sequence is LN -> quantize -> q/k/v -> attention
@@ -234,10 +255,28 @@ int enc_forward(vokra_hip_encoder* e, size_t batch, size_t frames, const float* 
         SS_TRY(vk::qact_ln_quantize(c, e->qa_d, rows, e->h.f(), L.ln1g.f(), L.ln1b.f(), kLnEps, act, e->x.f()));
         const vokra_hip_qweight_t* qkv[3] = {L.q.w, L.k.w, L.v.w};
         const float* qkv_b[3] = {L.q.b(), L.k.b(), L.v.b()};
-        float* qkv_o[3] = {e->q.f(), e->k.f(), e->v.f()};
-        SS_TRY(vk::gemm_qact_multi(c, 3, qkv, e->qa_d, qkv_b, qkv_o));
-        SS_TRY(vk::attn_quantize(c, batch, frames, frames, e->n_head, e->n_head, e->hd, e->q.f(), e->k.f(), e->v.f(),
-                                 scale, 0, 0, e->attn.f(), e->qa_d, act));
+        // k leaves the GEMM as the attention kernel's fp16 hi / lo operands
+        // (no k split pass); q stays f32 (the kernel splits it), v is split
+        // and transposed by its pass
+        bool fused = false;
+        uint16_t* kh = (uint16_t*)e->k.p;
+        uint16_t* kl = kh + rows * d;
+        if (frames >= 2) {
+            SS_TRY(enc_vt_ensure(e, batch * d * t_pad * sizeof(uint16_t)));
+            SS_TRY(vk::gemm_qact_qkv_split(c, qkv, e->qa_d, qkv_b, e->q.f(), VkSplitOut{kh, kl}, e->v.f(), &fused));
+        }
+        if (fused) {
+            SS_HIP(vk::launch_split_vt(vk::ctx_stream(c), e->v.f(), (int)batch, (int)frames, (int)t_pad,
+                                       (int)e->n_head, (int)e->hd, e->vt_hi.p, e->vt_lo.p),
+                   "launch(vk_split_vt)");
+            SS_TRY(vk::attn_quantize_split(c, batch, frames, e->n_head, e->hd, e->q.f(), kh, kl, e->vt_hi.p,
+                                           e->vt_lo.p, t_pad, scale, e->attn.f(), e->qa_d, act));
+        } else {
+            float* qkv_o[3] = {e->q.f(), e->k.f(), e->v.f()};
+            SS_TRY(vk::gemm_qact_multi(c, 3, qkv, e->qa_d, qkv_b, qkv_o));
+            SS_TRY(vk::attn_quantize(c, batch, frames, frames, e->n_head, e->n_head, e->hd, e->q.f(), e->k.f(),
+                                     e->v.f(), scale, 0, 0, e->attn.f(), e->qa_d, act));
+        }
         SS_TRY(L.o.run(c, e->qa_d, e->h.f(), add_h));
         // MLP block (nn.rs:134-181)
         SS_TRY(vk::qact_ln_quantize(c, e->qa_d, rows, e->h.f(), L.ln2g.f(), L.ln2b.f(), kLnEps, act, e->x.f()));
