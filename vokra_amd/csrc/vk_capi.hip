@@ -859,6 +859,19 @@ int gemm_qact_quantize(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra
                        w->n % 128 == 0 && w->n_pad == w->n && qa_out->k == w->n &&
                        ((reinterpret_cast<uintptr_t>(d_bias) | reinterpret_cast<uintptr_t>(epi.resid)) & 15) == 0;
     VK_TRY(set_dev(c), "hipSetDevice");
+    // the decode route: two 16-column tiles per workgroup hold each 32-column
+    // block, so the pass runs in the GEMV's epilogue
+    const bool fused_gemv = qo.afrag && !w->kquant && qa->act_quant != VOKRA_HIP_ACT_KQUANT && gemv_route(c, w, qa) &&
+                            w->n % 32 == 0 && qa_out->k == w->n && qo.m_pad <= qa->m_pad && qo.m_pad % 16 == 0;
+    if (fused_gemv) {
+        const VkGemvLin lin = {(const uint4*)w->gq.p, (const uint2*)w->gsc.p, d_bias, nullptr, epi, (int)w->n};
+        VK_TRY(vk::launch_gemv_qblock_quant(c->stream, wd_kv_mode(w->wdtype), qa->act_quant == VOKRA_HIP_ACT_POW2,
+                                            (const uint4*)qa->frag.p, (const float*)qa->scale.p,
+                                            (const float*)qa->gsum.p, lin, (int)qa->m, (int)w->nb, (int)qa->m_pad, qo),
+               "launch(vk_gemv_qblock_wq)");
+        qact_commit(qa_out, qa->m, act_quant);
+        return VOKRA_HIP_OK;
+    }
     if (!fused) {
         st = run_gemm_qact(c, w, qa, d_bias, d_out, epi);
         return st ? st : quantize_activations(c, qa_out, d_out, qa->m, w->n, act_quant);

@@ -265,19 +265,18 @@ constexpr int SLOT = 7 * 1024;          // bytes per ring slot: A 4 KiB, W <= 2 
 constexpr int OFF_W = 4096, OFF_WS = 6144, OFF_SA = 6400, OFF_AS = 6656;
 }  // namespace gw
 
-template <int MODE, bool POW2, bool DEV>
-__global__ __launch_bounds__(64) void vk_gemv_qblock_w(
-    const uint4* __restrict__ afrag, const float* __restrict__ ascale, const float* __restrict__ asum,
-    const GemvSet set, const VkGemvLin* __restrict__ dlins, int m, int nb, int m_pad) {
+// One wave's 16 x 16 output tile (weight column tile nt, activation row tile
+// mt) of the wave-per-tile kernel: acc[r] is output (16 mt + 4 (lane / 16) + r,
+// 16 nt + lane % 16). ring: this wave's RING slots of LDS.
+template <int MODE, bool POW2>
+__device__ __forceinline__ void gemv_w_tile(const uint4* __restrict__ afrag, const float* __restrict__ ascale,
+                                            const float* __restrict__ asum, const VkGemvLin& lin, int nt, int mt,
+                                            int nb, int m_pad, uint8_t (&ring)[gw::RING][gw::SLOT], float (&acc)[4]) {
     using namespace gw;
     constexpr int WQ = MODE == 1 ? 1 : 2;           // weight KiB per group
     constexpr int LG = 4 + WQ + 3;                  // direct loads per lane per group
     constexpr float OFFSET = MODE == 1 ? -136.0f : -128.0f;
-    __shared__ __align__(16) uint8_t ring[RING][SLOT];
-    const VkGemvLin lin = DEV ? dlins[blockIdx.z] : set.lin[blockIdx.z];
-    const int nt = blockIdx.x, mt = blockIdx.y;
-    if (nt * 16 >= lin.n) return;  // this linear has fewer column tiles (the whole wave)
-    const int lane = threadIdx.x, rq = 4 * (lane >> 4), col = lane & 15;
+    const int lane = threadIdx.x & 63, col = lane & 15;
     const int G = nb / gemv::GB;
     const uint32_t base = __builtin_amdgcn_readfirstlane(vk_lds_addr(&ring[0][0]));
     // per-lane sources (advanced by group)
@@ -295,7 +294,7 @@ __global__ __launch_bounds__(64) void vk_gemv_qblock_w(
         vk_dma_b32(ascale + (size_t)4 * g * m_pad + s_off, b + OFF_SA);
         vk_dma_b32(asum + (size_t)4 * g * m_pad + s_off, b + OFF_AS);
     };
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    acc[0] = acc[1] = acc[2] = acc[3] = 0.0f;
 #pragma unroll
     for (int p = 0; p < RING - 1; ++p)
         if (p < G) issue(p, p);
@@ -359,6 +358,19 @@ __global__ __launch_bounds__(64) void vk_gemv_qblock_w(
         }
         slot = slot == RING - 1 ? 0 : slot + 1;
     }
+}
+
+template <int MODE, bool POW2, bool DEV>
+__global__ __launch_bounds__(64) void vk_gemv_qblock_w(
+    const uint4* __restrict__ afrag, const float* __restrict__ ascale, const float* __restrict__ asum,
+    const GemvSet set, const VkGemvLin* __restrict__ dlins, int m, int nb, int m_pad) {
+    __shared__ __align__(16) uint8_t ring[gw::RING][gw::SLOT];
+    const VkGemvLin lin = DEV ? dlins[blockIdx.z] : set.lin[blockIdx.z];
+    const int nt = blockIdx.x, mt = blockIdx.y;
+    if (nt * 16 >= lin.n) return;  // this linear has fewer column tiles (the whole wave)
+    const int lane = threadIdx.x, rq = 4 * (lane >> 4), col = lane & 15;
+    float acc[4];
+    gemv_w_tile<MODE, POW2>(afrag, ascale, asum, lin, nt, mt, nb, m_pad, ring, acc);
     const int c = nt * 16 + col;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -366,6 +378,70 @@ __global__ __launch_bounds__(64) void vk_gemv_qblock_w(
         if (row < m && c < lin.n) {
             const size_t o = (size_t)row * lin.n + c;
             lin.out[o] = vk_epi_apply(lin.bias ? acc[r] + lin.bias[c] : acc[r], lin.epi, o);
+        }
+    }
+}
+
+
+// The wave-per-tile kernel for one linear whose outputs go straight into the
+// activation pass of the next linear's input (qo; its f32 outputs are not
+// written): a workgroup of two waves takes the two 16-column tiles of one
+// 32-column block, so the block's absolute maximum and operand sum combine
+// across the waves through LDS. Outputs, scales and sums equal the GEMV
+// followed by vk_quantize_act_b32 (rows past m get zero fragments).
+template <int MODE, bool POW2>
+__global__ __launch_bounds__(128) void vk_gemv_qblock_wq(
+    const uint4* __restrict__ afrag, const float* __restrict__ ascale, const float* __restrict__ asum,
+    const VkGemvLin lin, int m, int nb, int m_pad, const VkQOut qo) {
+    __shared__ __align__(16) uint8_t ring[2][gw::RING][gw::SLOT];
+    __shared__ float xamax[2][16];
+    __shared__ int xsum[2][16];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, rq = 4 * (lane >> 4), col = lane & 15;
+    const int kb = blockIdx.x, nt = 2 * kb + w, mt = blockIdx.y;  // n % 32 == 0: both tiles exist
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (mt * 16 < m)  // row tiles past m only write zero fragments (uniform per workgroup)
+        gemv_w_tile<MODE, POW2>(afrag, ascale, asum, lin, nt, mt, nb, m_pad, ring[w], acc);
+    const int c = nt * 16 + col;
+    float v[4], amax[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = mt * 16 + rq + r;
+        const size_t o = (size_t)row * lin.n + c;
+        v[r] = row < m ? vk_epi_apply(lin.bias ? acc[r] + lin.bias[c] : acc[r], lin.epi, o) : 0.0f;
+        // from 0 and through fmaxf, as the separate pass (NaN ignored)
+        amax[r] = vk_group_max<16>(fmaxf(0.0f, fabsf(v[r])));
+    }
+    if (col == 0)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xamax[w][rq + r] = amax[r];
+    __syncthreads();
+    float sc[4];
+    int q[4], gs[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float a = fmaxf(amax[r], xamax[w ^ 1][rq + r]);
+        sc[r] = 0.0f;
+        q[r] = 0;
+        if (a != 0.0f) {
+            sc[r] = vk_act_scale(a, qo.pow2);
+            q[r] = vk_act_q(v[r], sc[r]);
+        }
+        gs[r] = vk_group_sum_i<16>(q[r]);
+    }
+    if (col == 0)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xsum[w][rq + r] = gs[r];
+    __syncthreads();
+    const int nbo = qo.k >> 5;
+    uint16_t* f16 = reinterpret_cast<uint16_t*>(qo.afrag);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = mt * 16 + rq + r;  // < qo.m_pad
+        f16[vk_afrag_u16((size_t)row, kb, nbo, 16 * w + col)] = (uint16_t)vk_act_bits(q[r], sc[r], qo.pow2);
+        if (w == 0 && col == 0) {
+            const int g = gs[r] + xsum[1][rq + r];  // the block's columns in order: wave 0's, then wave 1's
+            qo.ascale[(size_t)kb * qo.m_pad + row] = sc[r];
+            qo.asum[(size_t)kb * qo.m_pad + row] = qo.pow2 ? (float)g * sc[r] : (float)g;
         }
     }
 }
@@ -418,6 +494,25 @@ hipError_t launch_gemv_qblock(hipStream_t s, int mode, bool pow2, const uint4* a
                     : go<1, false, false>(s, afrag, ascale, asum, set, nullptr, n_lin, n_max, m, nb, m_pad);
     return pow2 ? go<3, true, false>(s, afrag, ascale, asum, set, nullptr, n_lin, n_max, m, nb, m_pad)
                 : go<3, false, false>(s, afrag, ascale, asum, set, nullptr, n_lin, n_max, m, nb, m_pad);
+}
+
+hipError_t launch_gemv_qblock_quant(hipStream_t s, int mode, bool pow2, const uint4* afrag, const float* ascale,
+                                    const float* asum, const VkGemvLin& lin, int m, int nb, int m_pad,
+                                    const VkQOut& qo) {
+    // every padded row of the fragments is written (zero past m), as the
+    // separate pass does; the row tiles read stay inside the input's padding
+    if (m < 1 || lin.n < 32 || lin.n % 32 != 0 || qo.k != lin.n || !qo.afrag || qo.m_pad < m || qo.m_pad % 16 != 0 ||
+        qo.m_pad > m_pad)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(lin.n / 32), (unsigned)(qo.m_pad / 16)), block(128);
+    if (mode == 1) {
+        if (pow2) hipLaunchKernelGGL((vk_gemv_qblock_wq<1, true>), grid, block, 0, s, afrag, ascale, asum, lin, m, nb, m_pad, qo);
+        else hipLaunchKernelGGL((vk_gemv_qblock_wq<1, false>), grid, block, 0, s, afrag, ascale, asum, lin, m, nb, m_pad, qo);
+    } else {
+        if (pow2) hipLaunchKernelGGL((vk_gemv_qblock_wq<3, true>), grid, block, 0, s, afrag, ascale, asum, lin, m, nb, m_pad, qo);
+        else hipLaunchKernelGGL((vk_gemv_qblock_wq<3, false>), grid, block, 0, s, afrag, ascale, asum, lin, m, nb, m_pad, qo);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv_qblock_group(hipStream_t s, int mode, bool pow2, const uint4* afrag, const float* ascale,

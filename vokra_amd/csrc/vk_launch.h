@@ -103,6 +103,12 @@ hipError_t launch_repack_w_gemv(hipStream_t s, int mode, const uint8_t* wq, int 
 // n_lin (1..3) linears over the same activations, one launch.
 hipError_t launch_gemv_qblock(hipStream_t s, int mode, bool pow2, const uint4* afrag, const float* ascale,
                               const float* asum, const VkGemvLin* lins, int n_lin, int m, int nb, int m_pad);
+// One linear whose outputs feed the activation pass of the next input (qo:
+// k == n, n % 32 == 0) instead of f32 out: the same fragments, scales and sums
+// as launch_gemv_qblock followed by vk_quantize_act_b32.
+hipError_t launch_gemv_qblock_quant(hipStream_t s, int mode, bool pow2, const uint4* afrag, const float* ascale,
+                                    const float* asum, const VkGemvLin& lin, int m, int nb, int m_pad,
+                                    const VkQOut& qo);
 // n_lin (1..65535) linears described by a device array d_lins, one launch;
 // n_max is the largest n among them.
 hipError_t launch_gemv_qblock_group(hipStream_t s, int mode, bool pow2, const uint4* afrag, const float* ascale,
