@@ -267,6 +267,21 @@ __device__ __forceinline__ void vk_row_load256_all(const float* __restrict__ row
         x[j] = c < cols ? v : 0.0f;
     }
 }
+// Sum of x[c] * x[c] over this thread's columns c = t, t + 256, t + 512, ...
+// in that order (each a multiply, then an add). The loads are issued eight
+// columns at a time, so a row of up to 2048 columns is one memory round trip.
+__device__ __forceinline__ float vk_sumsq_cols256(const float* __restrict__ row, int cols) {
+    float s = 0.0f;
+    for (int c0 = threadIdx.x; c0 < cols; c0 += 256 * 8) {
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = c0 + 256 * j < cols ? row[c0 + 256 * j] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (c0 + 256 * j < cols) s += x[j] * x[j];
+    }
+    return s;
+}
 __device__ __forceinline__ float2 vk_ln_stats256(const float (&x)[kLnRegJ], int cols, float eps, float* red) {
     const float inv_cols = 1.0f / (float)cols;
     float s = 0.0f;

@@ -298,9 +298,7 @@ __global__ __launch_bounds__(256) void vk_rms_norm_f32(const float* __restrict__
     __shared__ float red[4];
     const float* ir = in + (size_t)blockIdx.x * cols;
     float* orow = out + (size_t)blockIdx.x * cols;
-    float s = 0.0f;
-    for (int c = threadIdx.x; c < cols; c += 256) s += ir[c] * ir[c];
-    const float inv = 1.0f / sqrtf(block_sum(s, red) / (float)cols + eps);
+    const float inv = 1.0f / sqrtf(block_sum(vk_sumsq_cols256(ir, cols), red) / (float)cols + eps);
     for (int c = threadIdx.x; c < cols; c += 256) orow[c] = ir[c] * inv * gamma[c];
 }
 

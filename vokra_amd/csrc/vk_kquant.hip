@@ -150,9 +150,7 @@ __global__ __launch_bounds__(256) void vk_rms_quantize_g16(const float* __restri
     float inv = 0.0f;
     const float* ir = in + (size_t)row * k;
     if (live) {
-        float s = 0.0f;
-        for (int c = threadIdx.x; c < k; c += 256) s += ir[c] * ir[c];
-        inv = 1.0f / sqrtf(vk_block_sum256(s, red) / (float)k + eps);
+        inv = 1.0f / sqrtf(vk_block_sum256(vk_sumsq_cols256(ir, k), red) / (float)k + eps);
     }
     for (int g = threadIdx.x; g < k / 16; g += 256) {
         float v[16];
