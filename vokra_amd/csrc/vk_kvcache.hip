@@ -1066,15 +1066,30 @@ __global__ void vk_paged_attn_combine(int n_split, int hq, const int* __restrict
         if (!Q16) return;
         v = out[ih * HD + e];  // written by the split kernel itself
     } else {
+        // every split's partials are loaded up front (indices clamped to the
+        // item's last split, so all loads stay in bounds and none waits on
+        // another), then merged in split order
+        float pm[pa::MAX_SPLIT], pl[pa::MAX_SPLIT], po[pa::MAX_SPLIT];
+#pragma unroll
+        for (int sp = 0; sp < pa::MAX_SPLIT; ++sp) {
+            const size_t pi = ih * n_split + min(sp, nsp - 1);
+            pm[sp] = part_ml[2 * pi];
+            pl[sp] = part_ml[2 * pi + 1];
+            po[sp] = part_o[pi * HD + e];
+        }
         float m = -INFINITY;
-        for (int sp = 0; sp < nsp; ++sp) m = fmaxf(m, part_ml[2 * (ih * n_split + sp)]);
+#pragma unroll
+        for (int sp = 0; sp < pa::MAX_SPLIT; ++sp)
+            if (sp < nsp) m = fmaxf(m, pm[sp]);
         const float m_use = m == -INFINITY ? 0.0f : m;
         float l = 0.0f, o = 0.0f;
-        for (int sp = 0; sp < nsp; ++sp) {
-            const size_t pi = ih * n_split + sp;
-            const float w = __expf(part_ml[2 * pi] - m_use);
-            l += part_ml[2 * pi + 1] * w;
-            o += part_o[pi * HD + e] * w;
+#pragma unroll
+        for (int sp = 0; sp < pa::MAX_SPLIT; ++sp) {
+            if (sp < nsp) {
+                const float w = __expf(pm[sp] - m_use);
+                l += pl[sp] * w;
+                o += po[sp] * w;
+            }
         }
         v = l > 0.0f ? o / l : 0.0f;
         out[ih * HD + e] = v;
