@@ -140,15 +140,56 @@ __global__ void vk_quantize_act_g16(const float* __restrict__ a, int m, int m_pa
 // vk_rms_norm_f32 forms it (thread t sums columns t, t + 256, ... in order,
 // then vk_block_sum256), y = x * inv * gamma, then each 16-wide group as
 // vk_quantize_act_g16 would quantize y. Bit-identical to the two launches.
+constexpr int kRmsRowLds = 2048;  // rows up to this many columns are read once
 __global__ __launch_bounds__(256) void vk_rms_quantize_g16(const float* __restrict__ in,
                                                            const float* __restrict__ gamma, float eps, int m,
                                                            int m_pad, int k, uint2* __restrict__ afrag,
                                                            float* __restrict__ ascale, float* __restrict__ asum) {
     __shared__ float red[4];
+    __shared__ __align__(16) float xs[kRmsRowLds];
     const int row = blockIdx.x, nsb = k / kq::QK;
     const bool live = row < m;  // uniform per workgroup
     float inv = 0.0f;
     const float* ir = in + (size_t)row * k;
+    if (k <= kRmsRowLds) {
+        // the row is read once: thread t loads columns t, t + 256, ... (its
+        // gamma group is requested first), sums their squares in that order
+        // as vk_sumsq_cols256 does and parks them in LDS for the group pass
+        const int g = threadIdx.x;
+        float gm[16];
+        if (live && g < k / 16) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) gm[t] = gamma[16 * g + t];
+        }
+        if (live) {
+            float x[kRmsRowLds / 256];
+#pragma unroll
+            for (int j = 0; j < kRmsRowLds / 256; ++j) {
+                const int c = (int)threadIdx.x + 256 * j;
+                x[j] = c < k ? ir[c] : 0.0f;
+            }
+            float sq = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kRmsRowLds / 256; ++j) {
+                const int c = (int)threadIdx.x + 256 * j;
+                if (c < k) {
+                    sq += x[j] * x[j];
+                    xs[c] = x[j];
+                }
+            }
+            // the reduction's barriers also order the LDS row
+            inv = 1.0f / sqrtf(vk_block_sum256(sq, red) / (float)k + eps);
+        }
+        if (g < k / 16) {
+            float v[16];
+            if (live) {
+#pragma unroll
+                for (int t = 0; t < 16; ++t) v[t] = xs[16 * g + t] * inv * gm[t];
+            }
+            vk_q16_store(row, g, m_pad, nsb, v, live, afrag, ascale, asum);
+        }
+        return;
+    }
     if (live) {
         inv = 1.0f / sqrtf(vk_block_sum256(vk_sumsq_cols256(ir, k), red) / (float)k + eps);
     }
