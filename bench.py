@@ -383,6 +383,9 @@ def bench_decoder(ctx, hip, n_stream=64, n_layer=32, d=1280, H=20, ff=5120, V=51
     dec = hip.Decoder(ctx, 2, d, H, ff, V, n_text, n_audio, n_stream, layers, tok, pos,
                       np.ones(d, np.float32), np.zeros(d, np.float32), block_size=16)
     del layers, tok
+    # the page table a long-running server ends up with: the self-KV pages
+    # handed out in a seeded random order rather than LIFO from an empty arena
+    dec.set_free_order(rng.permutation(sum(dec.kv_pages())).astype(np.int32))
     d_enc = hip.DeviceBuffer.from_array(ctx, rng.standard_normal((n_audio, d), dtype=np.float32))
     for s in range(n_stream):
         dec.set_encoder_dev(s, d_enc)
@@ -429,6 +432,7 @@ def bench_decoder(ctx, hip, n_stream=64, n_layer=32, d=1280, H=20, ff=5120, V=51
     del dec
     ctx.synchronize()
     return {"streams": n_stream, "layers": n_layer, "vocab": V, "prefix_range": [1, max_prefix],
+            "page_table": "shuffled (seeded free order)",
             "last_position": int(lens.max()) + steps,
             "ms_per_step": round(ms, 3), "tokens_per_s": round(n_stream / (ms * 1e-3), 1),
             "cross_f16_mode": {"ms_per_step": round(ms_f16, 3), "tokens_per_s": round(n_stream / (ms_f16 * 1e-3), 1)},
@@ -467,6 +471,7 @@ def bench_text_decoder(ctx, hip, n_stream=32, n_layer=24, d=2048, hq=16, hkv=2, 
     dec = hip.TextDecoder(ctx, 12, d, hq, hkv, hd, ff, V, n_ctx, n_stream, layers, tok, np.ones(d, np.float32),
                           head, rope_base=1e6, rms_norm_eps=1e-5, block_size=16)
     del layers
+    dec.set_free_order(rng.permutation(sum(dec.kv_pages())).astype(np.int32))   # shuffled page table
     lens = rng.integers(len_lo, len_hi - steps, n_stream)
     kk = rng.standard_normal((n_layer, int(lens.max()), hkv * hd), dtype=np.float32)
     vv = rng.standard_normal((n_layer, int(lens.max()), hkv * hd), dtype=np.float32)
@@ -495,6 +500,7 @@ def bench_text_decoder(ctx, hip, n_stream=32, n_layer=24, d=2048, hq=16, hkv=2, 
     del dec
     ctx.synchronize()
     return {"streams": n_stream, "layers": n_layer, "vocab": V, "context_range": [len_lo, len_hi],
+            "page_table": "shuffled (seeded free order)",
             "mean_context": round(float(lens.mean()), 1), "ms_per_step": round(ms, 3),
             "tokens_per_s": round(n_stream / (ms * 1e-3), 1),
             "bytes_per_step": {"weights_q4_k": w_bytes, "kv_q8_0": kv_bytes},

@@ -307,8 +307,11 @@ int vokra_hip_logits_argmax_dev(vokra_hip_ctx_t *ctx, size_t rows, size_t vocab,
  * hi/lo split MFMAs (three per product, f32 accumulation): results agree with
  * the f32 reference to about 1e-6 relative. With t_q = 1 (decode) the low
  * parts of k and v are held in one byte each, an integer times the fp16 high
- * part's ulp / 128 (relative error at most 2^-18 / (1 - 2^-12), a quarter
- * fewer bytes for the bandwidth-bound single-query case); the decoder
+ * part's ulp / 128 (a quarter fewer bytes for the bandwidth-bound
+ * single-query case). Each k / v element then carries a relative error of at
+ * most 2^-18 / (1 - 2^-12) when |x| >= 2^-7; below that (fp16 exponent field
+ * under 8, subnormals included) the low byte is zero and the element is the
+ * plain fp16 rounding, an absolute error of at most 2^-19. The decoder
  * session's cross-attention uses the same form. q is split as
  * q * scale * log2(e) (the softmax runs in base 2); a finite element of that,
  * of k or of v with magnitude >= 65520 (beyond fp16) is INVALID_ARGUMENT: here
@@ -534,10 +537,11 @@ void vokra_hip_decoder_destroy(vokra_hip_decoder_t *dec);
 int vokra_hip_decoder_set_encoder(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t stream, const float *enc);
 int vokra_hip_decoder_set_encoder_dev(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t stream,
                                       const float *d_enc);
-/* Precision of the cross-attention K/V reads. VOKRA_HIP_CROSS_F32 (default)
- * keeps f32-level products: K and V are held as an fp16 high part plus a
- * one-byte low part scaled by the high part's ulp (the single-query form of
- * vokra_hip_attn_f32, relative error at most 2^-18 / (1 - 2^-12)), against the
+/* Precision of the cross-attention K/V reads. VOKRA_HIP_CROSS_F32 (default):
+ * K and V are held as an fp16 high part plus a one-byte low part scaled by the
+ * high part's ulp (the single-query form of vokra_hip_attn_f32): relative
+ * error at most 2^-18 / (1 - 2^-12) per element of magnitude >= 2^-7, absolute
+ * error at most 2^-19 below it (plain fp16 rounding there), against the
  * reference's f32 cross_attention (crates/vokra-models/src/whisper/nn.rs:
  * 342-399, decoder.rs:492-510). VOKRA_HIP_CROSS_F16 reads the fp16 high parts
  * only: two thirds of the bytes of the step's largest stream, with K and V
@@ -548,6 +552,17 @@ int vokra_hip_decoder_set_encoder_dev(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t 
 int vokra_hip_decoder_set_cross_precision(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, int precision);
 /* Empties the self-KV cache of every stream. */
 int vokra_hip_decoder_reset(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec);
+/* Resets the decoder (every stream back to length 0) with its self-KV cache's
+ * free list set to `order`, a permutation of the cache's page ids (top of the
+ * stack last), as vokra_hip_kv_set_free_order: later steps' pages land at
+ * shuffled addresses, the page-table placement a long-running server ends up
+ * with. Results do not depend on it. No reference counterpart (the reference
+ * cache always starts from [cap-1 .. 0], paged_quant.rs:152-216). */
+int vokra_hip_decoder_set_free_order(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, const int32_t *order, size_t n);
+/* free_pages / pages_in_use of the decoder's self-KV cache (vokra_hip_kv_pages;
+ * their sum is the page count a free order must permute). */
+int vokra_hip_decoder_kv_pages(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t *free_pages,
+                               size_t *pages_in_use);
 /* One decode step of n streams (distinct): stream streams[i] feeds token
  * tokens[i] at position positions[i] (its current length). Per stream this is
  * WhisperDecoder::step_into (crates/vokra-models/src/whisper/decoder.rs:413-567)
@@ -611,7 +626,13 @@ typedef struct vokra_hip_whisper_load_report {
  * messages ("whisper weight `<name>`: missing from GGUF", "... shape [..] !=
  * expected [..]"). A Linear whose ggml type equals wdtype goes to the session
  * from the mapping; an F32/F16 Linear is packed when wdtype is Q8_0, Q4_0 or
- * Q5_0; anything else is UNSUPPORTED_OP naming the tensor. report may be NULL. */
+ * Q5_0; anything else is UNSUPPORTED_OP naming the tensor. report may be NULL.
+ * Divergence: a K-quant Linear whose in_features is not a multiple of 256
+ * (its rows straddle super-blocks: d_model 384 or 640 models, or any FFN width
+ * off the 256 grid) stays on the reference's f32 dequant path and is counted
+ * in report.dequantized_unaligned (weights.rs:471-512); these sessions hold
+ * quantized Linears only, so such a file is UNSUPPORTED_OP ("in_features 384
+ * is not a multiple of 256"), naming the first such tensor. */
 int vokra_hip_whisper_encoder_from_gguf(vokra_hip_ctx_t *ctx, const vokra_hip_gguf_t *f,
                                         const vokra_hip_whisper_config_t *cfg, int wdtype, size_t max_rows,
                                         vokra_hip_whisper_load_report_t *report, vokra_hip_encoder_t **out);
@@ -675,6 +696,12 @@ int vokra_hip_text_decoder_create(vokra_hip_ctx_t *ctx, int wdtype, size_t n_lay
 void vokra_hip_text_decoder_destroy(vokra_hip_text_decoder_t *dec);
 /* TextDecoderSession::reset (text_decoder_session.rs:192): every stream back to position 0. */
 int vokra_hip_text_decoder_reset(vokra_hip_ctx_t *ctx, vokra_hip_text_decoder_t *dec);
+/* As vokra_hip_decoder_set_free_order / _kv_pages, for the text decoder's
+ * cache (every stream back to position 0). No reference counterpart. */
+int vokra_hip_text_decoder_set_free_order(vokra_hip_ctx_t *ctx, vokra_hip_text_decoder_t *dec, const int32_t *order,
+                                          size_t n);
+int vokra_hip_text_decoder_kv_pages(vokra_hip_ctx_t *ctx, vokra_hip_text_decoder_t *dec, size_t *free_pages,
+                                    size_t *pages_in_use);
 /* TextDecoderSession::position (text_decoder_session.rs:187) of one stream. */
 int vokra_hip_text_decoder_position(vokra_hip_ctx_t *ctx, vokra_hip_text_decoder_t *dec, size_t stream,
                                     size_t *position);
@@ -699,6 +726,40 @@ int vokra_hip_text_decoder_step_dev(vokra_hip_ctx_t *ctx, vokra_hip_text_decoder
                                     const int32_t *d_streams, const int32_t *d_tokens, const int32_t *d_positions,
                                     int32_t *d_next_tokens, float *d_logits);
 int vokra_hip_text_decoder_status(vokra_hip_ctx_t *ctx, vokra_hip_text_decoder_t *dec, size_t *n_appended);
+
+/* VoxtralConfig (crates/vokra-models/src/voxtral/config.rs:60-147), the
+ * numeric fields. head_dim is the explicit metadata value (0 when the key is
+ * absent: TextDecoderConfig::head_dim then derives hidden_dim / n_head_q);
+ * rope_base, rms_norm_eps and the optional counts read 0 when absent. */
+typedef struct vokra_hip_voxtral_config {
+    size_t audio_n_layer, audio_n_head, audio_hidden_dim, audio_n_ctx, audio_n_mels, audio_ffn_dim;
+    size_t n_layer, n_head_q, n_head_kv, head_dim, hidden_dim, ffn_dim, vocab_size, n_ctx;
+    float rope_base, rms_norm_eps;
+    size_t cross_attn_hidden_dim;
+} vokra_hip_voxtral_config_t;
+/* VoxtralConfig::from_gguf (config.rs:155-267): the vokra.voxtral.* keys,
+ * required ones (audio_encoder.{n_layer, hidden_dim, n_head, n_mels},
+ * text_decoder.{n_layer, hidden_dim, ffn_dim}) in the reference's order, the
+ * head-split checks, MODEL_LOAD "voxtral config: ..." on failure. The mode
+ * and codec strings are not read (no compute depends on them). */
+int vokra_hip_voxtral_config_from_gguf(const vokra_hip_gguf_t *f, vokra_hip_voxtral_config_t *cfg);
+/* TextDecoder::load (crates/vokra-models/src/voxtral/text_decoder.rs:484-575)
+ * straight into a text-decoder session (vokra_hip_text_decoder_create): the
+ * tensor prefix chosen as pick_prefix (:1456-1471), each layer's
+ * input_layernorm, self_attn.{q,k,v,o}_proj, post_attention_layernorm and
+ * mlp.{gate,up,down}_proj, the final norm and, when present, the untied
+ * lm_head beside the decoder submodule (:763-768), checked in that order with
+ * the reference's messages ("voxtral text_decoder: `<name>` missing from GGUF",
+ * "... shape [..] != expected [..]"). Norms and the embedding widen to f32
+ * (F32, F16 or Q4_K on disk). A Linear already in wdtype is taken from the
+ * mapping (Q4_K: in_features a multiple of 256), an F32/F16 one is packed to
+ * Q8_0 / Q4_0 / Q5_0 at load, anything else is UNSUPPORTED_OP naming it (the
+ * reference widens every Linear to f32 instead). n_ctx = 0 takes the file's
+ * text_decoder.n_ctx. report may be NULL. */
+int vokra_hip_text_decoder_from_gguf(vokra_hip_ctx_t *ctx, const vokra_hip_gguf_t *f,
+                                     const vokra_hip_voxtral_config_t *cfg, int wdtype, size_t n_stream, size_t n_ctx,
+                                     size_t block_size, vokra_hip_whisper_load_report_t *report,
+                                     vokra_hip_text_decoder_t **out);
 
 #ifdef __cplusplus
 }

@@ -88,14 +88,24 @@ class Decoder:
 W_Q4_K = 12
 
 
-def random_text_layer(orc, g, d, hq, hkv, hd, ff, scale=0.05):
-    """One speech-LLM block with Q4_K linears quantized by the oracle's
-    quantize.rs restatement, norms near one."""
+def quantize_weight(orc, wd, w):
+    """Wire bytes of an f32 weight [n, k]: Q4_K through the oracle's
+    quantize.rs restatement, the 32-element block formats through
+    pack_matrix_to_bytes (one row of blocks per output feature)."""
+    n, k = w.shape
+    if wd == W_Q4_K:
+        return orc.kquant_quantize(W_Q4_K, np.ascontiguousarray(w, np.float32).reshape(-1))
+    return orc.pack_matrix_to_bytes(orc.KV_OF_W[wd], np.ascontiguousarray(w, np.float32), n, k // 32)
+
+
+def random_text_layer(orc, g, d, hq, hkv, hd, ff, scale=0.05, wd=W_Q4_K):
+    """One speech-LLM block with linears of weight dtype wd (Q4_K by default)
+    quantized by the oracle, norms near one."""
     L = {"attn_norm_gamma": (1 + 0.1 * g.standard_normal(d)).astype(np.float32),
          "ffn_norm_gamma": (1 + 0.1 * g.standard_normal(d)).astype(np.float32)}
     for name, n, k in (("wq", hq * hd, d), ("wk", hkv * hd, d), ("wv", hkv * hd, d), ("wo", d, hq * hd),
                        ("w_gate", ff, d), ("w_up", ff, d), ("w_down", d, ff)):
-        L[name] = orc.kquant_quantize(W_Q4_K, (g.standard_normal((n, k)) * scale).astype(np.float32).reshape(-1))
+        L[name] = quantize_weight(orc, wd, (g.standard_normal((n, k)) * scale).astype(np.float32))
     return L
 
 
@@ -105,13 +115,15 @@ class TextDecoder:
     RoPE per head at the stream's position, GQA over the cache with the scale
     after the dot, o-proj + residual, RMSNorm, SwiGLU FFN + residual, final
     RMSNorm, LM head), every linear through the oracle's gemm_q_f32 (Q4_K:
-    kquant_gemm_i8) and the K/V through the QuantizedPagedKvCache restatement
-    (Q8_0 rows). lm_head: Q4_K wire bytes [vocab, d], or None for the f32
-    token embedding (tied)."""
+    kquant_gemm_i8; block formats: the block-INT8 GEMM) and the K/V through
+    the QuantizedPagedKvCache restatement (Q8_0 rows). lm_head: wire bytes
+    [vocab, d] of the layers' dtype wd, or None for the f32 token embedding
+    (tied)."""
 
     def __init__(self, orc, layers, tok_emb, final_gamma, lm_head, hq, hkv, hd, ff, n_stream, n_ctx, bs,
-                 rope_base, eps):
+                 rope_base, eps, wd=W_Q4_K):
         self.orc, self.layers, self.tok_emb, self.final_gamma, self.lm_head = orc, layers, tok_emb, final_gamma, lm_head
+        self.wd = wd
         self.d = tok_emb.shape[1]
         self.hq, self.hkv, self.hd, self.ff = hq, hkv, hd, ff
         self.rope_base, self.eps = rope_base, eps
@@ -125,7 +137,7 @@ class TextDecoder:
                 assert self.cache.append_step(li, t, s, k_rows[li, t], v_rows[li, t]) == 0
 
     def lin(self, x, w, n, k):
-        return qlin(self.orc, W_Q4_K, x, w, n, k)
+        return qlin(self.orc, self.wd, x, w, n, k)
 
     def step(self, s, token, pos):
         o, d, hq, hkv, hd, ff = self.orc, self.d, self.hq, self.hkv, self.hd, self.ff

@@ -113,3 +113,95 @@ def test_lookups_and_types(tmp_path):
         f.read_f32("w.q8", 128)
     with pytest.raises(hip.InvalidArgument, match="elements"):
         f.read_f32("ln.gamma", 5)
+
+
+# ---- a GGUF file written by the reference's own converter --------------------
+# tests/golden/silero-vad-v5.gguf is tests/parity/silero_vad/silero-vad-v5.gguf
+# of the reference, copied as data: a v3 file from its converter with 30 F32
+# tensors and 2 string metadata keys. Its layout is read here a second time by
+# a few lines of struct parsing that share nothing with the library's reader.
+SILERO = __import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "silero-vad-v5.gguf")
+
+
+def independent_parse(data):
+    """(version, alignment, metadata {key: (type, value)}, tensors [(name,
+    dims, type, offset)], data_offset): the GGUF v3 layout of
+    crates/vokra-core/src/gguf/mod.rs:1-100, string and scalar values only."""
+    pos = 4
+    version, n_t, n_kv = struct.unpack_from("<IQQ", data, pos)
+    pos += 20
+
+    def rstr(p):
+        n = struct.unpack_from("<Q", data, p)[0]
+        return data[p + 8:p + 8 + n].decode(), p + 8 + n
+
+    scalars = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<B", 10: "<Q", 11: "<q", 12: "<d"}
+    meta = {}
+    for _ in range(n_kv):
+        key, pos = rstr(pos)
+        t = struct.unpack_from("<I", data, pos)[0]
+        pos += 4
+        if t == 8:
+            val, pos = rstr(pos)
+        else:
+            val = struct.unpack_from(scalars[t], data, pos)[0]
+            pos += struct.calcsize(scalars[t])
+        meta[key] = (t, val)
+    tensors = []
+    for _ in range(n_t):
+        name, pos = rstr(pos)
+        nd = struct.unpack_from("<I", data, pos)[0]
+        dims = list(struct.unpack_from(f"<{nd}Q", data, pos + 4))
+        pos += 4 + 8 * nd
+        t, off = struct.unpack_from("<IQ", data, pos)
+        pos += 12
+        tensors.append((name, dims, t, off))
+    align = meta.get("general.alignment", (4, 32))[1]
+    return version, align, meta, tensors, (pos + align - 1) // align * align
+
+
+def test_reference_written_gguf():
+    data = open(SILERO, "rb").read()
+    version, align, meta, tensors, data_off = independent_parse(data)
+    assert data[:4] == b"GGUF" and version == 3 and align == 32
+    assert meta == {"vokra.model.arch": (8, "silero-vad"), "vokra.model.name": (8, "silero-vad-v5")}
+    assert len(tensors) == 30 and all(t[2] == gw.GGML_F32 for t in tensors)
+    f = hip.GgufFile(SILERO)
+    assert len(f) == 30
+    assert f.meta_str("vokra.model.arch") == "silero-vad" and f.meta_str("vokra.model.name") == "silero-vad-v5"
+    spans = []
+    for i, (name, dims, t, off) in enumerate(tensors):
+        n = int(np.prod(dims))
+        start = data_off + off
+        # the reader's checks (reader.rs:333-510): offsets aligned, the payload
+        # (4 bytes per F32 element) inside the file
+        assert off % align == 0 and start + 4 * n <= len(data)
+        got_name, got_type, got_dims, payload = f.tensor(i)
+        assert (got_name, got_type, got_dims) == (name, t, dims) and f.find(name) == i
+        assert payload == data[start:start + 4 * n]
+        assert np.array_equal(f.read_f32(name, n), np.frombuffer(data, np.float32, n, start))
+        spans.append((start, start + 4 * n))
+    spans.sort()
+    assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))   # no two payloads overlap
+    # the converter's shapes for the 16 kHz branch (PyTorch order, as stored)
+    shapes = {name: dims for name, dims, _, _ in tensors}
+    assert shapes["sr16k.stft.forward_basis_buffer"] == [258, 1, 256]
+    assert shapes["sr16k.decoder.rnn.weight_ih"] == [512, 128]
+    assert shapes["sr8k.encoder.0.reparam_conv.weight"] == [128, 65, 3]
+
+
+def test_reference_written_gguf_truncations(tmp_path):
+    """Every cut of the reference-written file inside its header or tensor
+    table is a ModelLoad error, and so is a cut that leaves the last payload
+    short: the reader never reads past what it was given."""
+    data = open(SILERO, "rb").read()
+    _, _, _, tensors, data_off = independent_parse(data)
+    cuts = sorted(set(list(range(0, 64)) + list(range(64, data_off, 97)) + [data_off - 1, len(data) - 4,
+                                                                              len(data) - 1]))
+    for cut in cuts:
+        with pytest.raises(hip.ModelLoad):
+            hip.GgufFile(write(tmp_path, data[:cut], f"cut{cut}.gguf"))
+    bad = bytearray(data)
+    bad[4:8] = struct.pack("<I", 2)
+    with pytest.raises(hip.ModelLoad, match="unsupported version"):
+        hip.GgufFile(write(tmp_path, bytes(bad), "v2.gguf"))

@@ -487,3 +487,62 @@ def test_decoder_config3_prefix_to_447(ctx, oracle):
     with pytest.raises(hip.InvalidArgument, match="n_text_ctx"):
         dec.step([0], [1], [448])
     print("[worst teacher-forced errors]", chk.worst, flush=True)
+
+
+def test_decoder_config3_ragged_prefixes_shuffled_pages(ctx, oracle):
+    """Config 3 as configured: 64 streams whose prefixes are U(1..448)
+    (seeded), reached by decode steps over a shuffled page table, 2 layers.
+    Stream s takes its steps at positions 0 .. P_s - 1 in batches of the
+    streams still short of their prefix, so batch membership is ragged. Bars:
+      * the session with a shuffled free list == a twin with the reference's
+        LIFO order, every step (tokens every step, all logits every 32nd step
+        and at the end): page placement never changes a result;
+      * three tracked streams (the longest, the shortest, one crossing the
+        256-key mark) == the entry-point chain bit for bit at every one of
+        their steps, with the chain's own cache shuffled differently;
+      * their last steps teacher-forced against the oracle (self-attention
+        over P_s dequantized cache rows that sit on shuffled pages)."""
+    print("[case] decoder config 3, prefixes U(1..448), shuffled page table, 64 streams", flush=True)
+    n_stream = 64
+    g = np.random.default_rng(3448)
+    dec, P = make_config3_decoder(ctx, np.random.default_rng(3449), 2, n_stream)
+    twin, _ = make_config3_decoder(ctx, np.random.default_rng(3449), 2, n_stream)
+    free, used = dec.kv_pages()
+    assert used == 0
+    dec.set_free_order(g.permutation(free).astype(np.int32))
+    prefix = g.integers(1, 449, n_stream)
+    prefix[[0, 1, 2]] = [448, 1, 258]
+    g.shuffle(prefix)
+    longest, shortest, mid = int(np.argmax(prefix)), int(np.argmin(prefix)), int(np.argmax(prefix == 258))
+    tracked = [longest, shortest, mid]
+    chain = chain_for(ctx, P, n_stream)
+    chain.kv.set_free_order(g.permutation(sum(chain.kv.pages())).astype(np.int32))
+    chk = Checker(oracle)
+    tok = [int(t) for t in g.integers(0, 51866, n_stream)]
+    n_steps = int(prefix.max())
+    for t in range(n_steps):
+        streams = [int(s) for s in g.permutation(n_stream) if prefix[s] > t]
+        args = ([tok[s] for s in streams], [t] * len(streams))
+        nxt, logits = dec.step(streams, *args, want_logits=True)
+        full = t % 32 == 0 or t == n_steps - 1
+        if full:
+            n_twin, l_twin = twin.step(streams, *args, want_logits=True)
+            assert np.array_equal(logits.view(np.uint32), l_twin.view(np.uint32)), t
+        else:
+            n_twin = twin.step(streams, *args)
+        assert np.array_equal(nxt, n_twin), t
+        # a tracked stream at its last step goes first: the chain's teacher-
+        # forced checks cover the first and last item of its batch
+        rows = sorted((i for i, s in enumerate(streams) if s in tracked), key=lambda i: prefix[streams[i]] != t + 1)
+        if rows:
+            sub = [streams[i] for i in rows]
+            last = [s for s in sub if prefix[s] == t + 1]
+            n2, l2 = chain.step(sub, [tok[s] for s in sub], [t] * len(sub), check=chk if last else None)
+            assert np.array_equal(logits[rows].view(np.uint32), l2.view(np.uint32)), (t, sub)
+            assert np.array_equal(nxt[rows], n2), (t, sub)
+        for i, s in enumerate(streams):
+            tok[s] = int(nxt[i])
+    # a page holds 16 steps of every stream of one layer
+    free_after, used_after = dec.kv_pages()
+    assert free_after + used_after == free and used_after == 2 * ((n_steps + 15) // 16)
+    print("[worst teacher-forced errors]", chk.worst, flush=True)

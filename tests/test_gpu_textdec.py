@@ -25,6 +25,7 @@ from vokra_amd import hip
 pytestmark = pytest.mark.gpu
 
 W_Q4_K = 12
+W_Q8_0 = 8
 U = 2.0 ** -24
 
 
@@ -84,8 +85,8 @@ def test_swiglu_vs_oracle(ctx, oracle):
 
 
 # ---- the session -----------------------------------------------------------
-def make_layers(oracle, g, n_layer, d, hq, hkv, hd, ff, scale=0.03):
-    return [model_oracle.random_text_layer(oracle, g, d, hq, hkv, hd, ff, scale) for _ in range(n_layer)]
+def make_layers(oracle, g, n_layer, d, hq, hkv, hd, ff, scale=0.03, wd=W_Q4_K):
+    return [model_oracle.random_text_layer(oracle, g, d, hq, hkv, hd, ff, scale, wd) for _ in range(n_layer)]
 
 
 class TextDecoderByOps:
@@ -112,11 +113,12 @@ class TextDecoderByOps:
         self.pos[s] = k_rows.shape[1]
 
     def lin(self, x, w, n, k):
-        y = self.ctx.gemm_q_f32(x.shape[0], n, k, x, w, hip.WDtype.Q4_K)
+        wd = self.P.get("wd", W_Q4_K)
+        y = self.ctx.gemm_q_f32(x.shape[0], n, k, x, w, hip.WDtype(wd))
         if self.check is not None:
             rows = min(2, x.shape[0])
-            want = self.check.gemm_q_f32(W_Q4_K, rows, n, k, x[:rows], w)
-            assert np.array_equal(y[:rows].view(np.uint32), want.view(np.uint32)), "Q4_K linear"
+            want = self.check.gemm_q_f32(wd, rows, n, k, x[:rows], w)
+            assert np.array_equal(y[:rows].view(np.uint32), want.view(np.uint32)), f"linear (dtype {wd})"
         return y
 
     def rms(self, h, gamma):
@@ -188,16 +190,16 @@ class TextDecoderByOps:
 
 
 def build(ctx, oracle, seed, n_layer, d, hq, hkv, hd, ff, V, n_ctx, n_stream, bs=16, tied=False, base=1e6,
-          eps=1e-5):
+          eps=1e-5, wd=W_Q4_K):
     g = np.random.default_rng(seed)
-    layers = make_layers(oracle, g, n_layer, d, hq, hkv, hd, ff)
+    layers = make_layers(oracle, g, n_layer, d, hq, hkv, hd, ff, wd=wd)
     tok = (g.standard_normal((V, d)) * 0.5).astype(np.float32)
     fin = (1 + 0.1 * g.standard_normal(d)).astype(np.float32)
-    head = None if tied else oracle.kquant_quantize(W_Q4_K, (g.standard_normal((V, d)) * 0.03).astype(np.float32)
-                                                     .reshape(-1))
+    head = None if tied else model_oracle.quantize_weight(oracle, wd, (g.standard_normal((V, d)) * 0.03)
+                                                          .astype(np.float32))
     P = dict(layers=layers, tok=tok, final=fin, head=head, d=d, hq=hq, hkv=hkv, hd=hd, ff=ff, V=V, n_ctx=n_ctx,
-             bs=bs, base=base, eps=eps)
-    dec = hip.TextDecoder(ctx, W_Q4_K, d, hq, hkv, hd, ff, V, n_ctx, n_stream, layers, tok, fin, head,
+             bs=bs, base=base, eps=eps, wd=wd)
+    dec = hip.TextDecoder(ctx, wd, d, hq, hkv, hd, ff, V, n_ctx, n_stream, layers, tok, fin, head,
                           rope_base=base, rms_norm_eps=eps, block_size=bs)
     return dec, P
 
@@ -208,16 +210,21 @@ def history(g, n_layer, n_pos, w, scale=1.0):
     return k, v
 
 
-@pytest.mark.parametrize("tied", [False, True])
-def test_text_decoder_small_vs_oracle(ctx, oracle, tied):
-    """Toy dims (d=256, 4/2 heads x 64): session == entry points bit for bit,
-    teacher-forced entry points vs the oracle, free-running vs the oracle."""
-    print(f"[case] text decoder small tied={tied}", flush=True)
-    d, hq, hkv, hd, ff, V, n_ctx, n_stream = 256, 4, 2, 64, 512, 96, 64, 3
-    dec, P = build(ctx, oracle, 11, 2, d, hq, hkv, hd, ff, V, n_ctx, n_stream, bs=4, tied=tied)
+@pytest.mark.parametrize("wd,tied,hkv", [(W_Q4_K, False, 2), (W_Q4_K, True, 2), (W_Q4_K, False, 4),
+                                         (W_Q8_0, False, 2), (W_Q8_0, True, 4)])
+def test_text_decoder_small_vs_oracle(ctx, oracle, wd, tied, hkv):
+    """Toy dims (d=256, 4 query heads x 64 over 2 kv heads, or 4 = no
+    grouping): session == entry points bit for bit, teacher-forced entry
+    points vs the oracle, free-running vs the oracle. Q8_0 weights take the
+    block-format route of the step (RMSNorm and the block activation pass as
+    two launches, a separate SwiGLU pass, RoPE as its own launch, paged
+    attention without the rotation table)."""
+    print(f"[case] text decoder small wd={wd} tied={tied} hkv={hkv}", flush=True)
+    d, hq, hd, ff, V, n_ctx, n_stream = 256, 4, 64, 512, 96, 64, 3
+    dec, P = build(ctx, oracle, 11, 2, d, hq, hkv, hd, ff, V, n_ctx, n_stream, bs=4, tied=tied, wd=wd)
     ops = TextDecoderByOps(ctx, P, n_stream, check=oracle)
     ref = model_oracle.TextDecoder(oracle, P["layers"], P["tok"], P["final"], P["head"], hq, hkv, hd, ff, n_stream,
-                                   n_ctx, 4, P["base"], P["eps"])
+                                   n_ctx, 4, P["base"], P["eps"], wd=wd)
     tok = [1, 2, 3]
     schedule = [[0, 1, 2], [0, 1], [2, 0], [1, 2, 0], [0], [2, 1, 0]]
     for step, streams in enumerate(schedule):
@@ -329,3 +336,116 @@ def test_text_decoder_rejections(ctx, oracle):
         hip.TextDecoder(ctx, W_Q4_K, d, 3, 2, hd, ff, V, 8, 1, layers, tok, fin)
     with pytest.raises(hip.UnsupportedOp):
         hip.TextDecoder(ctx, W_Q4_K, d, 4, 2, 96, ff, V, 8, 1, layers, tok, fin)
+
+
+# ---- the text decoder straight from a GGUF file --------------------------------
+def voxtral_gguf(path, P, prefix, n_ctx, tied, f16_norms=False, drop=None, replace=None):
+    """The decoder of P written with TextDecoder::load's tensor names
+    (text_decoder.rs:484-575) under `prefix`, the lm_head beside the decoder
+    submodule, and the vokra.voxtral.* metadata (explicit head_dim)."""
+    from tests import gguf_writer as gw
+    d, hq, hkv, hd, ff, V = P["d"], P["hq"], P["hkv"], P["hd"], P["ff"], P["V"]
+    wd = P.get("wd", W_Q4_K)
+    gt = gw.GGML_Q4_K if wd == W_Q4_K else gw.GGML_Q8_0
+    m = [("vokra.voxtral." + k, t, v) for k, t, v in (
+        ("audio_encoder.n_layer", gw.U32, 2), ("audio_encoder.hidden_dim", gw.U32, 256),
+        ("audio_encoder.n_head", gw.U32, 4), ("audio_encoder.n_mels", gw.U32, 128),
+        ("text_decoder.n_layer", gw.U32, len(P["layers"])), ("text_decoder.hidden_dim", gw.U32, d),
+        ("text_decoder.ffn_dim", gw.U32, ff), ("text_decoder.vocab_size", gw.U32, V),
+        ("text_decoder.n_ctx", gw.U32, n_ctx), ("text_decoder.n_head_q", gw.U32, hq),
+        ("text_decoder.n_head_kv", gw.U32, hkv), ("text_decoder.head_dim", gw.U32, hd),
+        ("text_decoder.rope_base", gw.F32, P["base"]), ("text_decoder.rms_norm_eps", gw.F32, P["eps"]))]
+    t = []
+
+    def norm(name, a):
+        if f16_norms:
+            t.append((name, [a.size], gw.GGML_F16, a.astype(np.float16).tobytes()))
+        else:
+            t.append((name, [a.size], gw.GGML_F32, a.astype(np.float32).tobytes()))
+
+    t.append((prefix + "embed_tokens.weight", [V, d], gw.GGML_F32, P["tok"].tobytes()))
+    for i, L in enumerate(P["layers"]):
+        p = f"{prefix}layers.{i}"
+        norm(p + ".input_layernorm.weight", L["attn_norm_gamma"])
+        for name, key, n, k in (("self_attn.q_proj", "wq", hq * hd, d), ("self_attn.k_proj", "wk", hkv * hd, d),
+                                ("self_attn.v_proj", "wv", hkv * hd, d), ("self_attn.o_proj", "wo", d, hq * hd)):
+            t.append((f"{p}.{name}.weight", [n, k], gt, bytes(np.asarray(L[key], np.uint8))))
+        norm(p + ".post_attention_layernorm.weight", L["ffn_norm_gamma"])
+        for name, key, n, k in (("mlp.gate_proj", "w_gate", ff, d), ("mlp.up_proj", "w_up", ff, d),
+                                ("mlp.down_proj", "w_down", d, ff)):
+            t.append((f"{p}.{name}.weight", [n, k], gt, bytes(np.asarray(L[key], np.uint8))))
+    norm(prefix + "norm.weight", P["final"])
+    if not tied:
+        # lm_head_base (text_decoder.rs:763-768): strip a trailing "model."
+        # only where what is left is empty or ends in a dot
+        base = prefix
+        if prefix.endswith("model.") and (prefix[:-6] == "" or prefix[:-6].endswith(".")):
+            base = prefix[:-6]
+        t.append((base + "lm_head.weight", [V, d], gt, bytes(np.asarray(P["head"], np.uint8))))
+    if drop:
+        t = [x for x in t if x[0] != drop]
+    if replace:
+        t = [replace.get(x[0], x) for x in t]
+    path.write_bytes(gw.build(m, t))
+    return hip.GgufFile(str(path))
+
+
+@pytest.mark.parametrize("prefix,tied,wd", [("language_model.model.", False, W_Q4_K), ("model.", True, W_Q4_K),
+                                            ("language_model.", False, W_Q8_0)])
+def test_text_decoder_from_gguf_equals_direct(ctx, oracle, tmp_path, prefix, tied, wd):
+    """vokra_hip_text_decoder_from_gguf (TextDecoder::load + VoxtralConfig::
+    from_gguf) == the session built from the same arrays, bit for bit, over
+    ragged steps from restored histories; the three tensor prefixes of
+    pick_prefix, the untied head beside the decoder submodule and the tied
+    one; F16 norms widen exactly."""
+    print(f"[case] text decoder from gguf prefix={prefix} tied={tied} wd={wd}", flush=True)
+    d, hq, hkv, hd, ff, V, n_ctx, n_stream = 256, 4, 2, 64, 512, 96, 64, 3
+    dec, P = build(ctx, oracle, 21, 2, d, hq, hkv, hd, ff, V, n_ctx, n_stream, bs=4, tied=tied, wd=wd)
+    f = voxtral_gguf(tmp_path / "td.gguf", P, prefix, n_ctx, tied, f16_norms=True)
+    # the direct session sees the same F16-rounded norms the file holds
+    for L in P["layers"]:
+        for key in ("attn_norm_gamma", "ffn_norm_gamma"):
+            L[key] = L[key].astype(np.float16).astype(np.float32)
+    P["final"] = P["final"].astype(np.float16).astype(np.float32)
+    direct = hip.TextDecoder(ctx, wd, d, hq, hkv, hd, ff, V, n_ctx, n_stream, P["layers"], P["tok"], P["final"],
+                             P["head"], rope_base=P["base"], rms_norm_eps=P["eps"], block_size=4)
+    loaded, rep = hip.TextDecoder.from_gguf(ctx, f, wd, n_stream, block_size=4)
+    assert rep == {"verbatim": 7 * 2 + (0 if tied else 1), "packed": 0}
+    g = np.random.default_rng(22)
+    for s, n_pos in enumerate((5, 0, 17)):
+        k, v = history(g, 2, n_pos, hkv * hd)
+        direct.kv_restore(s, k, v)
+        loaded.kv_restore(s, k, v)
+    tok = [3, 7, 11]
+    for streams in ([0, 1, 2], [2, 0], [1]):
+        args = [tok[s] for s in streams]
+        n1, l1 = direct.step(streams, args, want_logits=True)
+        n2, l2 = loaded.step(streams, args, want_logits=True)
+        assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32)) and np.array_equal(n1, n2), streams
+        for i, s in enumerate(streams):
+            tok[s] = int(n1[i])
+
+
+def test_text_decoder_from_gguf_errors(ctx, oracle, tmp_path):
+    """TextDecoder::load's errors, naming the tensor in the reference's order:
+    a missing layer tensor, a mis-shaped projection, and a present but
+    mis-shaped lm_head (never a silent tie); a Q8_0 file for a Q4_K session."""
+    print("[case] text decoder from gguf errors", flush=True)
+    from tests import gguf_writer as gw
+    d, hq, hkv, hd, ff, V = 256, 4, 2, 64, 512, 96
+    _, P = build(ctx, oracle, 23, 1, d, hq, hkv, hd, ff, V, 16, 1, bs=4)
+    pre = "language_model.model."
+    name = pre + "layers.0.mlp.up_proj.weight"
+    with pytest.raises(hip.ModelLoad, match=rf"voxtral text_decoder: `{name}` missing from GGUF"):
+        hip.TextDecoder.from_gguf(ctx, voxtral_gguf(tmp_path / "a.gguf", P, pre, 16, False, drop=name), W_Q4_K, 1)
+    w = pre + "layers.0.self_attn.k_proj.weight"
+    bad = {w: (w, [d, hkv * hd], gw.GGML_Q4_K, bytes(np.asarray(P["layers"][0]["wk"], np.uint8)))}
+    with pytest.raises(hip.ModelLoad, match=rf"`{w}` shape \[{d}, {hkv * hd}\] != expected \[{hkv * hd}, {d}\]"):
+        hip.TextDecoder.from_gguf(ctx, voxtral_gguf(tmp_path / "b.gguf", P, pre, 16, False, replace=bad), W_Q4_K, 1)
+    h = "language_model.lm_head.weight"
+    bad = {h: (h, [V - 1, d], gw.GGML_F32, bytes((V - 1) * d * 4))}
+    with pytest.raises(hip.ModelLoad, match=rf"`{h}` shape \[{V - 1}, {d}\] != expected \[{V}, {d}\]"):
+        hip.TextDecoder.from_gguf(ctx, voxtral_gguf(tmp_path / "c.gguf", P, pre, 16, False, replace=bad), W_Q4_K, 1)
+    with pytest.raises(hip.UnsupportedOp, match=r"`language_model\.model\.layers\.0\.self_attn\.q_proj\.weight`: "
+                                                r"Q4_K on disk"):
+        hip.TextDecoder.from_gguf(ctx, voxtral_gguf(tmp_path / "d.gguf", P, pre, 16, False), W_Q8_0, 1)

@@ -245,3 +245,17 @@ def test_load_errors_name_the_tensor(ctx, oracle, tmp_path):
     m16 = Model(ctx, oracle, "f16")
     with pytest.raises(hip.UnsupportedOp, match="F16 on disk"):
         hip.Decoder.from_gguf(ctx, m16.write(tmp_path / "d.gguf"), W_Q4_K, 2)
+    # Q4_K Linears whose rows straddle super-blocks (in_features 384, a
+    # d_model-384 model): the reference keeps such a tensor on its f32
+    # dequant path and counts it (weights.rs:471-512,
+    # report.dequantized_unaligned); these sessions hold no f32 Linear, so
+    # the load stops at the first one, naming it
+    cfg384 = dict(CFG, n_audio_state=384, n_text_state=384, n_audio_head=6, n_text_head=6, ffn_dim=768)
+    m384 = Model(ctx, oracle, "q4_k", cfg=cfg384)
+    f384 = m384.write(tmp_path / "e.gguf")
+    for build in (lambda: hip.Encoder.from_gguf(ctx, f384, W_Q4_K, max_rows=64),
+                  lambda: hip.Decoder.from_gguf(ctx, f384, W_Q4_K, 2)):
+        with pytest.raises(hip.UnsupportedOp,
+                           match=r"whisper weight `model\.(en|de)coder\.layers\.0\.[a-z_.]+\.weight`: in_features 384 "
+                                 r"is not a multiple of 256"):
+            build()

@@ -103,7 +103,7 @@ __device__ __forceinline__ float attn_query_sum(float v) {
 }
 
 // Set (to 1) by any kernel of this file that meets an operand outside the
-// fp16 range; read and cleared by the host (attn_range_take). One per device.
+// fp16 range; read and cleared by the host (range_check in vk_capi.hip). One per device.
 static __device__ unsigned int vk_attn_range_flag;
 
 __device__ __forceinline__ void attn_range_raise() { atomicOr(&vk_attn_range_flag, 1u); }
@@ -795,19 +795,8 @@ hipError_t launch_flash_attn_f32q(hipStream_t s, int hd, const float* q, float q
     return flash_any(s, hd, batch, lo_mode, a);
 }
 
-// Reads and clears this file's fp16-range flag on the current device; the
-// copies run on stream s, which is drained first.
-hipError_t attn_range_take(hipStream_t s, unsigned* raised) {
-    unsigned v = 0;
-    hipError_t e = hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(vk_attn_range_flag), sizeof v, 0, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e == hipSuccess && v) {
-        const unsigned z = 0;
-        e = hipMemcpyToSymbolAsync(HIP_SYMBOL(vk_attn_range_flag), &z, sizeof z, 0, hipMemcpyHostToDevice, s);
-        if (e == hipSuccess) e = hipStreamSynchronize(s);
-    }
-    *raised = v;
-    return e;
-}
+// This device's address of this file's fp16-range flag (the host reads and
+// clears it with one small kernel per check).
+hipError_t attn_range_flag_addr(unsigned** p) { return hipGetSymbolAddress((void**)p, HIP_SYMBOL(vk_attn_range_flag)); }
 
 }  // namespace vk

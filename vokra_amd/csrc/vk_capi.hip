@@ -150,6 +150,8 @@ struct vokra_hip_ctx {
     // RoPE frequency table of the last (rope_base, head_dim) the _dev entry saw
     DevBuf rope_theta, rope_pos;
     void* scratch = nullptr;  // this device's address of the no-allocation workspace
+    unsigned *flag_attn = nullptr, *flag_kv = nullptr, *flag_gemm = nullptr;  // this device's range flags
+    unsigned* flags_host = nullptr;  // pinned: the flags' values at the last check
     float rope_base = 0.0f;
     size_t rope_hd = 0;
 };
@@ -520,11 +522,24 @@ hipStream_t ctx_stream(const vokra_hip_ctx* c) { return c->stream; }
 // Drains the context stream and turns a raised fp16-range flag of the
 // attention kernels into INVALID_ARGUMENT (the explicit failure of
 // compute.rs:649-696 instead of an inf / NaN result).
+// Reads and clears the three fp16-range flags in one launch: their values go
+// to the context's pinned host words, so a check is one kernel and one stream
+// drain (it was a copy and a drain per flag).
+__global__ void vk_take_range_flags(unsigned* __restrict__ a, unsigned* __restrict__ b, unsigned* __restrict__ g,
+                                    unsigned* __restrict__ host) {
+    if (threadIdx.x == 0) {
+        host[0] = atomicExch(a, 0u);
+        host[1] = atomicExch(b, 0u);
+        host[2] = atomicExch(g, 0u);
+    }
+}
+
 int range_check(vokra_hip_ctx* c) {
-    unsigned a = 0, b = 0, g = 0;
-    VK_TRY(attn_range_take(c->stream, &a), "attention range flag");
-    VK_TRY(kv_range_take(c->stream, &b), "attention range flag");
-    VK_TRY(gemm_range_take(c->stream, &g), "attention range flag");
+    hipLaunchKernelGGL(vk_take_range_flags, dim3(1), dim3(64), 0, c->stream, c->flag_attn, c->flag_kv, c->flag_gemm,
+                       c->flags_host);
+    VK_TRY(hipGetLastError(), "launch(vk_take_range_flags)");
+    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    const unsigned a = c->flags_host[0], b = c->flags_host[1], g = c->flags_host[2];
     if (a || b || g)
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
                     "attention: an operand is outside the fp16 range of the split products (|x| >= 65520 after "
@@ -1675,9 +1690,16 @@ int vokra_hip_create(int device, vokra_hip_ctx_t** out) {
     c->act.growable = true;
     c->scratch = scr;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = vk::attn_range_flag_addr(&c->flag_attn);
+    if (e == hipSuccess) e = vk::kv_range_flag_addr(&c->flag_kv);
+    if (e == hipSuccess) e = vk::gemm_range_flag_addr(&c->flag_gemm);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&c->flags_host, 4 * sizeof(unsigned), hipHostMallocDefault);
+    if (e == hipSuccess && (!c->flag_attn || !c->flag_kv || !c->flag_gemm)) e = hipErrorInvalidSymbol;
     if (e != hipSuccess) {
+        if (c->stream) (void)hipStreamDestroy(c->stream);
+        if (c->flags_host) (void)hipHostFree(c->flags_host);
         delete c;
-        return hip_fail(e, "hipStreamCreate");
+        return hip_fail(e, "hipStreamCreate / range flags");
     }
     *out = c;
     return VOKRA_HIP_OK;
@@ -1693,14 +1715,14 @@ void vokra_hip_destroy(vokra_hip_ctx_t* c) {
                       &c->rope_theta, &c->rope_pos})
         b->release();
     (void)hipStreamDestroy(c->stream);
+    if (c->flags_host) (void)hipHostFree(c->flags_host);
     delete c;
 }
 
 int vokra_hip_synchronize(vokra_hip_ctx_t* c) {
     if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "synchronize: ctx is NULL");
     VK_TRY(set_dev(c), "hipSetDevice");
-    VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    return vk::range_check(c);
+    return vk::range_check(c);  // drains the stream
 }
 
 int vokra_hip_device_alloc(vokra_hip_ctx_t* c, size_t bytes, void** dptr) {
@@ -2036,9 +2058,13 @@ int vokra_hip_capture_end(vokra_hip_ctx_t* c, vokra_hip_graph_t** out) {
     auto* g = new vokra_hip_graph();
     hipError_t e = hipStreamEndCapture(c->stream, &g->graph);
     if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    // the executable graph goes to the device now, so its first launch costs
+    // what every later one does
+    if (e == hipSuccess) e = hipGraphUpload(g->exec, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
         vokra_hip_graph_destroy(g);
-        return hip_fail(e, "hipStreamEndCapture/hipGraphInstantiate");
+        return hip_fail(e, "hipStreamEndCapture/hipGraphInstantiate/hipGraphUpload");
     }
     *out = g;
     return VOKRA_HIP_OK;

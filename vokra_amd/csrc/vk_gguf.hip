@@ -467,6 +467,38 @@ int opt_pair_array(const vokra_hip_gguf* f, const char* key, size_t n_layer) {
     return VOKRA_HIP_OK;
 }
 
+// ---- VoxtralConfig::from_gguf (crates/vokra-models/src/voxtral/config.rs:
+// 155-267): required keys fail with "missing metadata key", optional ones
+// read as 0 when absent or not of the accessor's type (as_u64 takes the
+// unsigned integers, as_f64 the two float types).
+int vox_bad(const char* fmt, ...) {
+    char buf[400];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    return fail(VOKRA_HIP_ERROR_MODEL_LOAD, "voxtral config: %s", buf);
+}
+
+int vox_req_u32(const vokra_hip_gguf* f, const char* key, size_t* out) {
+    const Meta* m = find_meta(f, key);
+    if (!m) return vox_bad("missing metadata key `%s`", key);
+    if (!unsigned_meta(m->type) || (uint64_t)m->i > UINT32_MAX)
+        return vox_bad("metadata key `%s` is not a u32-range integer", key);
+    *out = (size_t)(uint64_t)m->i;
+    return VOKRA_HIP_OK;
+}
+
+size_t vox_opt_u32(const vokra_hip_gguf* f, const char* key) {
+    const Meta* m = find_meta(f, key);
+    return (m && unsigned_meta(m->type) && (uint64_t)m->i <= UINT32_MAX) ? (size_t)(uint64_t)m->i : 0;
+}
+
+float vox_opt_f32(const vokra_hip_gguf* f, const char* key) {
+    const Meta* m = find_meta(f, key);
+    return (m && (m->type == 6 || m->type == 12)) ? (float)m->f : 0.0f;
+}
+
 std::string dims_str(const uint64_t* d, size_t n) {
     std::string s = "[";
     for (size_t i = 0; i < n; ++i) {
@@ -476,25 +508,20 @@ std::string dims_str(const uint64_t* d, size_t n) {
     return s + "]";
 }
 
-int weight_err(int code, const std::string& name, const char* fmt, ...) {
+// A tensor error in the wording of the loader being mirrored: Whisper
+// (weights.rs: "whisper weight `name`: ...") or the text decoder
+// (text_decoder.rs:1486-1496: "voxtral text_decoder: `name` missing from
+// GGUF", "... `name` shape [..] != expected [..]", other failures
+// "`name`: ...").
+int tensor_err(bool vox, int code, const std::string& name, const char* fmt, ...) {
     char buf[400];
     va_list ap;
     va_start(ap, fmt);
     vsnprintf(buf, sizeof buf, fmt, ap);
     va_end(ap);
-    return fail(code, "whisper weight `%s`: %s", name.c_str(), buf);
-}
-
-// Checks presence and shape as weights.rs:400-410 `tensor` does.
-int shaped(const vokra_hip_gguf* f, const std::string& name, std::initializer_list<uint64_t> want, const Tensor** out) {
-    const Tensor* t = find(f, name.c_str());
-    if (!t) return weight_err(VOKRA_HIP_ERROR_MODEL_LOAD, name, "missing from GGUF");
-    const std::vector<uint64_t> w(want);
-    if (t->dims != w)
-        return weight_err(VOKRA_HIP_ERROR_MODEL_LOAD, name, "shape %s != expected %s",
-                          dims_str(t->dims.data(), t->dims.size()).c_str(), dims_str(w.data(), w.size()).c_str());
-    *out = t;
-    return VOKRA_HIP_OK;
+    if (!vox) return fail(code, "whisper weight `%s`: %s", name.c_str(), buf);
+    const bool bare = !strncmp(buf, "missing", 7) || !strncmp(buf, "shape", 5);
+    return fail(code, "voxtral text_decoder: `%s`%s%s", name.c_str(), bare ? " " : ": ", buf);
 }
 
 // Owns the f32 decodes and packed weights until the session has uploaded them.
@@ -502,16 +529,42 @@ struct Loader {
     vokra_hip_ctx_t* ctx;
     const vokra_hip_gguf* f;
     int wdtype;
+    bool vox = false;  // the text decoder's wording (else Whisper's)
     std::vector<std::vector<float>> floats;
     std::vector<std::vector<uint8_t>> packed;
     size_t verbatim = 0, n_packed = 0;
 
+    // Presence and shape, as weights.rs:400-410 / text_decoder.rs:1486-1493 check them.
+    int shaped(const std::string& name, std::initializer_list<uint64_t> want, const Tensor** out) {
+        const Tensor* t = find(f, name.c_str());
+        if (!t) return tensor_err(vox, VOKRA_HIP_ERROR_MODEL_LOAD, name, "missing from GGUF");
+        const std::vector<uint64_t> w(want);
+        if (t->dims != w)
+            return tensor_err(vox, VOKRA_HIP_ERROR_MODEL_LOAD, name, "shape %s != expected %s",
+                              dims_str(t->dims.data(), t->dims.size()).c_str(), dims_str(w.data(), w.size()).c_str());
+        *out = t;
+        return VOKRA_HIP_OK;
+    }
+
+    // The tensor widened to f32, as GgufFile::tensor_f32 does: F32 as
+    // stored, F16 exactly, Q4_K through the device dequantizer (bit-exact
+    // with gguf/quant/q4_k.rs:34-69).
     int f32(const std::string& name, std::initializer_list<uint64_t> want, const float** out) {
         const Tensor* t;
-        int st = shaped(f, name, want, &t);
+        int st = shaped(name, want, &t);
         if (st) return st;
+        if (t->type == VOKRA_HIP_W_Q4_K) {
+            const size_t n = (size_t)t->nbytes / 144 * 256;
+            floats.emplace_back(n);
+            if ((st = vokra_hip_kquant_dequantize(ctx, VOKRA_HIP_W_Q4_K, f->base + f->data_offset + t->offset,
+                                                  (size_t)t->nbytes, n, floats.back().data())))
+                return st;
+            *out = floats.back().data();
+            return VOKRA_HIP_OK;
+        }
         if (t->type != 0 && t->type != 1)
-            return weight_err(VOKRA_HIP_ERROR_UNSUPPORTED_OP, name, "ggml type %u where F32 or F16 is needed", t->type);
+            return tensor_err(vox, VOKRA_HIP_ERROR_UNSUPPORTED_OP, name, "ggml type %u where F32, F16 or Q4_K is needed",
+                              t->type);
         const size_t n = (size_t)t->nbytes / (t->type == 0 ? 4 : 2);
         floats.emplace_back(n);
         if ((st = vokra_hip_gguf_read_f32(f, name.c_str(), floats.back().data(), n))) return st;
@@ -519,18 +572,19 @@ struct Loader {
         return VOKRA_HIP_OK;
     }
 
-    // linear_with (weights.rs:439-521): bias first, then the [out, in] weight.
+    // linear_with (weights.rs:439-521): bias first, then the [out, in] weight
+    // (the text decoder's projections have no bias, text_decoder.rs:1498-1524).
     int linear(const std::string& prefix, size_t in, size_t outf, bool has_bias, const uint8_t** w, const float** b) {
         int st;
         *b = nullptr;
         if (has_bias && (st = f32(prefix + ".bias", {outf}, b))) return st;
         const std::string wname = prefix + ".weight";
         const Tensor* t;
-        if ((st = shaped(f, wname, {outf, in}, &t))) return st;
+        if ((st = shaped(wname, {outf, in}, &t))) return st;
         if ((int)t->type == wdtype) {
             const size_t be = wdtype == VOKRA_HIP_W_Q4_K ? 256 : 32;
             if (in % be)
-                return weight_err(VOKRA_HIP_ERROR_UNSUPPORTED_OP, wname,
+                return tensor_err(vox, VOKRA_HIP_ERROR_UNSUPPORTED_OP, wname,
                                   "in_features %zu is not a multiple of %zu, so a block would straddle two rows", in, be);
             *w = f->base + f->data_offset + t->offset;
             ++verbatim;
@@ -541,12 +595,12 @@ struct Loader {
                          : wdtype == VOKRA_HIP_W_Q4_0 ? VOKRA_HIP_KV_Q4_0
                          : wdtype == VOKRA_HIP_W_Q5_0 ? VOKRA_HIP_KV_Q5_0 : -1;
         if ((t->type != 0 && t->type != 1) || mode < 0)
-            return weight_err(VOKRA_HIP_ERROR_UNSUPPORTED_OP, wname,
+            return tensor_err(vox, VOKRA_HIP_ERROR_UNSUPPORTED_OP, wname,
                               "%s on disk, and the session's %s weights cannot be made from it (same block dtype, or "
                               "F32/F16 packed to Q8_0 / Q4_0 / Q5_0)",
                               names[t->type], names[wdtype]);
         if (in % 32)
-            return weight_err(VOKRA_HIP_ERROR_UNSUPPORTED_OP, wname,
+            return tensor_err(vox, VOKRA_HIP_ERROR_UNSUPPORTED_OP, wname,
                               "in_features %zu is not a multiple of 32, so its rows cannot be packed to %s blocks", in,
                               names[wdtype]);
         std::vector<float> x(in * outf);
@@ -697,6 +751,146 @@ int vokra_hip_whisper_decoder_from_gguf(vokra_hip_ctx_t* ctx, const vokra_hip_gg
         return st;
     L.report(report);
     *out = dec;
+    return VOKRA_HIP_OK;
+}
+
+}  // extern "C"
+
+// ---- the speech-LLM text decoder straight from a GGUF file -------------------
+//
+// TextDecoder::load (crates/vokra-models/src/voxtral/text_decoder.rs:484-575):
+// the tensor prefix picked by which embedding name exists (:1456-1471), the
+// per-layer names input_layernorm / self_attn.{q,k,v,o}_proj /
+// post_attention_layernorm / mlp.{gate,up,down}_proj with [out, in] shapes,
+// the final norm, and an untied lm_head beside the decoder submodule when
+// present (:763-768), checked in that order with the reference's messages.
+// The reference widens every tensor to f32; these sessions keep the Linears
+// quantized, so a Linear is taken from the mapping when it is already in the
+// session's dtype and packed when it is F32/F16 and the session's dtype is a
+// 32-element block format (anything else is UNSUPPORTED_OP naming it).
+
+namespace {
+
+const char* pick_prefix(const vokra_hip_gguf* f) {
+    if (find(f, "language_model.model.embed_tokens.weight")) return "language_model.model.";
+    if (find(f, "language_model.embed_tokens.weight")) return "language_model.";
+    return "model.";
+}
+
+// "language_model.model." -> "language_model.", "model." -> "", anything else
+// unchanged (text_decoder.rs:763-768)
+std::string lm_head_base(const std::string& prefix) {
+    const std::string suf = "model.";
+    if (prefix.size() >= suf.size() && prefix.compare(prefix.size() - suf.size(), suf.size(), suf) == 0) {
+        const std::string base = prefix.substr(0, prefix.size() - suf.size());
+        if (base.empty() || base.back() == '.') return base;
+    }
+    return prefix;
+}
+
+int td_bad(const char* msg) { return fail(VOKRA_HIP_ERROR_MODEL_LOAD, "voxtral text_decoder: %s", msg); }
+
+}  // namespace
+
+extern "C" {
+
+int vokra_hip_voxtral_config_from_gguf(const vokra_hip_gguf_t* f, vokra_hip_voxtral_config_t* cfg) {
+    if (!f || !cfg) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "voxtral_config_from_gguf: NULL argument");
+    vokra_hip_voxtral_config_t c{};
+    int st;
+    if ((st = vox_req_u32(f, "vokra.voxtral.audio_encoder.n_layer", &c.audio_n_layer)) ||
+        (st = vox_req_u32(f, "vokra.voxtral.audio_encoder.hidden_dim", &c.audio_hidden_dim)) ||
+        (st = vox_req_u32(f, "vokra.voxtral.audio_encoder.n_head", &c.audio_n_head)))
+        return st;
+    c.audio_n_ctx = vox_opt_u32(f, "vokra.voxtral.audio_encoder.n_ctx");
+    if ((st = vox_req_u32(f, "vokra.voxtral.audio_encoder.n_mels", &c.audio_n_mels))) return st;
+    c.audio_ffn_dim = vox_opt_u32(f, "vokra.voxtral.audio_encoder.ffn_dim");
+    if (c.audio_n_head != 0 && c.audio_hidden_dim % c.audio_n_head != 0)
+        return vox_bad("audio_encoder.n_head (%zu) must divide audio_encoder.hidden_dim (%zu)", c.audio_n_head,
+                       c.audio_hidden_dim);
+    if ((st = vox_req_u32(f, "vokra.voxtral.text_decoder.n_layer", &c.n_layer)) ||
+        (st = vox_req_u32(f, "vokra.voxtral.text_decoder.hidden_dim", &c.hidden_dim)) ||
+        (st = vox_req_u32(f, "vokra.voxtral.text_decoder.ffn_dim", &c.ffn_dim)))
+        return st;
+    c.vocab_size = vox_opt_u32(f, "vokra.voxtral.text_decoder.vocab_size");
+    c.n_ctx = vox_opt_u32(f, "vokra.voxtral.text_decoder.n_ctx");
+    c.n_head_q = vox_opt_u32(f, "vokra.voxtral.text_decoder.n_head_q");
+    c.n_head_kv = vox_opt_u32(f, "vokra.voxtral.text_decoder.n_head_kv");
+    c.head_dim = vox_opt_u32(f, "vokra.voxtral.text_decoder.head_dim");
+    c.rope_base = vox_opt_f32(f, "vokra.voxtral.text_decoder.rope_base");
+    c.rms_norm_eps = vox_opt_f32(f, "vokra.voxtral.text_decoder.rms_norm_eps");
+    if (c.head_dim == 0 && c.n_head_q != 0 && c.hidden_dim != 0 && c.hidden_dim % c.n_head_q != 0)
+        return vox_bad("text_decoder.n_head_q (%zu) must divide text_decoder.hidden_dim (%zu) when no explicit "
+                       "text_decoder.head_dim is present - re-convert with a converter that writes "
+                       "vokra.voxtral.text_decoder.head_dim",
+                       c.n_head_q, c.hidden_dim);
+    if (c.n_head_kv != 0 && c.n_head_q != 0 && c.n_head_q % c.n_head_kv != 0)
+        return vox_bad("text_decoder.n_head_kv (%zu) must divide text_decoder.n_head_q (%zu) for GQA", c.n_head_kv,
+                       c.n_head_q);
+    c.cross_attn_hidden_dim = vox_opt_u32(f, "vokra.voxtral.cross_attn.hidden_dim");
+    *cfg = c;
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_text_decoder_from_gguf(vokra_hip_ctx_t* ctx, const vokra_hip_gguf_t* f,
+                                     const vokra_hip_voxtral_config_t* cfg, int wdtype, size_t n_stream, size_t n_ctx,
+                                     size_t block_size, vokra_hip_whisper_load_report_t* report,
+                                     vokra_hip_text_decoder_t** out) {
+    if (!ctx || !f || !cfg || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_from_gguf: NULL argument");
+    *out = nullptr;
+    if (!whisper_wdtype(wdtype))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_from_gguf: unknown weight dtype %d", wdtype);
+    const size_t d = cfg->hidden_dim, ff = cfg->ffn_dim, vocab = cfg->vocab_size;
+    // the converter's shape-only sentinel binds nothing in the reference, and
+    // its session refuses it (TextDecoderSession::new)
+    if (cfg->n_layer == 0 || d == 0)
+        return fail(VOKRA_HIP_ERROR_MODEL_LOAD,
+                    "voxtral::TextDecoderSession: config carries 0-sentinel (n_layer, d, vocab, heads, head_dim)");
+    const std::string prefix = pick_prefix(f);
+    if (vocab == 0) return td_bad("text_decoder.vocab_size must be non-zero");
+    Loader L{ctx, f, wdtype, true};
+    const float *tok, *fin;
+    int st;
+    if ((st = L.f32(prefix + "embed_tokens.weight", {vocab, d}, &tok))) return st;
+    if (cfg->n_head_q == 0 || cfg->n_head_kv == 0)
+        return td_bad("text_decoder.n_head_q and n_head_kv must be non-zero (GQA head split)");
+    // TextDecoderConfig::head_dim (config.rs:108-115): explicit, else derived
+    const size_t hd = cfg->head_dim ? cfg->head_dim : d / cfg->n_head_q;
+    if (hd == 0)
+        return td_bad("text_decoder.head_dim resolves to 0 - re-convert with a converter that writes "
+                      "vokra.voxtral.text_decoder.head_dim");
+    const size_t qh = cfg->n_head_q * hd, kvh = cfg->n_head_kv * hd;
+    std::vector<vokra_hip_text_decoder_layer_t> layers(cfg->n_layer);
+    const float* none = nullptr;
+    for (size_t i = 0; i < cfg->n_layer; ++i) {
+        const std::string p = prefix + "layers." + std::to_string(i);
+        vokra_hip_text_decoder_layer_t& y = layers[i];
+        if ((st = L.f32(p + ".input_layernorm.weight", {d}, &y.attn_norm_gamma)) ||
+            (st = L.linear(p + ".self_attn.q_proj", d, qh, false, &y.wq, &none)) ||
+            (st = L.linear(p + ".self_attn.k_proj", d, kvh, false, &y.wk, &none)) ||
+            (st = L.linear(p + ".self_attn.v_proj", d, kvh, false, &y.wv, &none)) ||
+            (st = L.linear(p + ".self_attn.o_proj", qh, d, false, &y.wo, &none)) ||
+            (st = L.f32(p + ".post_attention_layernorm.weight", {d}, &y.ffn_norm_gamma)) ||
+            (st = L.linear(p + ".mlp.gate_proj", d, ff, false, &y.w_gate, &none)) ||
+            (st = L.linear(p + ".mlp.up_proj", d, ff, false, &y.w_up, &none)) ||
+            (st = L.linear(p + ".mlp.down_proj", ff, d, false, &y.w_down, &none)))
+            return st;
+    }
+    if ((st = L.f32(prefix + "norm.weight", {d}, &fin))) return st;
+    // an untied head is bound when present (a wrong shape is an error, never
+    // a silent tie); absent, the token embedding is the head
+    const uint8_t* head = nullptr;
+    const std::string head_name = lm_head_base(prefix) + "lm_head";
+    if (find(f, (head_name + ".weight").c_str()) && (st = L.linear(head_name, d, vocab, false, &head, &none))) return st;
+    const size_t ctx_len = n_ctx ? n_ctx : cfg->n_ctx;
+    if (ctx_len == 0)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
+                    "text_decoder_from_gguf: n_ctx is 0 and the file has no vokra.voxtral.text_decoder.n_ctx");
+    if ((st = vokra_hip_text_decoder_create(ctx, wdtype, cfg->n_layer, d, cfg->n_head_q, cfg->n_head_kv, hd, ff, vocab,
+                                            ctx_len, n_stream, block_size, cfg->rope_base, cfg->rms_norm_eps,
+                                            layers.data(), tok, fin, head, out)))
+        return st;
+    L.report(report);
     return VOKRA_HIP_OK;
 }
 

@@ -21,7 +21,7 @@
 namespace vk {
 
 // Set (to 1) by the GQA decode kernel when q * scale is outside the fp16
-// range of its operands; read and cleared by the host (kv_range_take).
+// range of its operands; read and cleared by the host (range_check in vk_capi.hip).
 static __device__ unsigned int vk_kv_range_flag;
 
 // Device view of one cache, passed by value to every kernel.
@@ -1309,19 +1309,8 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
     return hipSuccess;
 }
 
-// Reads and clears this file's fp16-range flag on the current device; the
-// copies run on stream s, which is drained first.
-hipError_t kv_range_take(hipStream_t s, unsigned* raised) {
-    unsigned v = 0;
-    hipError_t e = hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(vk_kv_range_flag), sizeof v, 0, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e == hipSuccess && v) {
-        const unsigned z = 0;
-        e = hipMemcpyToSymbolAsync(HIP_SYMBOL(vk_kv_range_flag), &z, sizeof z, 0, hipMemcpyHostToDevice, s);
-        if (e == hipSuccess) e = hipStreamSynchronize(s);
-    }
-    *raised = v;
-    return e;
-}
+// This device's address of this file's fp16-range flag (the host reads and
+// clears it with one small kernel per check).
+hipError_t kv_range_flag_addr(unsigned** p) { return hipGetSymbolAddress((void**)p, HIP_SYMBOL(vk_kv_range_flag)); }
 
 }  // namespace vk

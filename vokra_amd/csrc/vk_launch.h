@@ -216,9 +216,11 @@ bool paged_attn_rotates_q(const KvView& v, int hq, int hd, const float* q, const
 // layer0 .. layer0 + n_layers - 1 in that order, in one launch (n_layers * n <= 4096).
 // Read and clear the fp16-range flags of the attention kernels (vk_attn.hip)
 // and of the GQA decode kernel (vk_kvcache.hip) on the current device.
-hipError_t attn_range_take(hipStream_t s, unsigned* raised);
-hipError_t gemm_range_take(hipStream_t s, unsigned* raised);  // the split outputs' fp16-range flag
-hipError_t kv_range_take(hipStream_t s, unsigned* raised);
+// device addresses (current device) of the fp16-range flags of the attention
+// kernels, the GEMM epilogue's split outputs and the cache's K/V packing
+hipError_t attn_range_flag_addr(unsigned** p);
+hipError_t gemm_range_flag_addr(unsigned** p);
+hipError_t kv_range_flag_addr(unsigned** p);
 // Packs rows into pages given by an earlier launch_kv_alloc_layers (items
 // whose page is missing are skipped).
 // rope_cs (optional, [n][hd / 2] (cos, sin)): k is rotated on the way in.

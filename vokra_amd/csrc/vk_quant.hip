@@ -386,7 +386,7 @@ __global__ void vk_repack_w_b32(int mode, const uint8_t* __restrict__ wq, int n,
 // leave as full 256-byte dwordx4 stores (streaming: the result is not re-read
 // by this kernel).
 // Set (to 1) by a block GEMM whose split outputs (VkSplitOut) meet a value
-// outside the fp16 range; read and cleared by the host (gemm_range_take).
+// outside the fp16 range; read and cleared by the host (range_check in vk_capi.hip).
 static __device__ unsigned int vk_gemm_range_flag;
 
 namespace gemm {
@@ -810,18 +810,9 @@ hipError_t launch_gemm_qblock_multi(hipStream_t s, bool pow2, const uint4* afrag
     return hipGetLastError();
 }
 
-hipError_t gemm_range_take(hipStream_t s, unsigned* raised) {
-    unsigned v = 0;
-    hipError_t e = hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(vk_gemm_range_flag), sizeof v, 0, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e == hipSuccess && v) {
-        const unsigned z = 0;
-        e = hipMemcpyToSymbolAsync(HIP_SYMBOL(vk_gemm_range_flag), &z, sizeof z, 0, hipMemcpyHostToDevice, s);
-        if (e == hipSuccess) e = hipStreamSynchronize(s);
-    }
-    *raised = v;
-    return e;
-}
+// This device's address of this file's fp16-range flag (the host reads and
+// clears it with one small kernel per check).
+hipError_t gemm_range_flag_addr(unsigned** p) { return hipGetSymbolAddress((void**)p, HIP_SYMBOL(vk_gemm_range_flag)); }
 
 hipError_t launch_gemm_qblock(hipStream_t s, bool pow2, const uint4* afrag, const float* ascale,
                               const uint4* wfrag, const float* wscale, const float* bias, float* out,

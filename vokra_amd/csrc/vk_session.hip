@@ -689,6 +689,18 @@ int vokra_hip_decoder_reset(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m) {
     return VOKRA_HIP_OK;
 }
 
+int vokra_hip_decoder_set_free_order(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, const int32_t* order, size_t n) {
+    if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_set_free_order: bad argument");
+    SS_TRY(vokra_hip_kv_set_free_order(c, m->kv, order, n));
+    std::fill(m->length.begin(), m->length.end(), 0);
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_decoder_kv_pages(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t* free_pages, size_t* pages_in_use) {
+    if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_kv_pages: bad argument");
+    return vokra_hip_kv_pages(c, m->kv, free_pages, pages_in_use);
+}
+
 int vokra_hip_decoder_status(vokra_hip_ctx_t* c, vokra_hip_decoder_t* m, size_t* n_appended) {
     if (!c || !m || m->ctx != c) return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "decoder_status: bad argument");
     size_t a = 0;
@@ -1028,6 +1040,22 @@ int vokra_hip_text_decoder_reset(vokra_hip_ctx_t* c, vokra_hip_text_decoder_t* m
     SS_TRY(vokra_hip_kv_reset(c, m->kv));
     std::fill(m->position.begin(), m->position.end(), 0);
     return VOKRA_HIP_OK;
+}
+
+int vokra_hip_text_decoder_set_free_order(vokra_hip_ctx_t* c, vokra_hip_text_decoder_t* m, const int32_t* order,
+                                          size_t n) {
+    if (!c || !m || m->ctx != c)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_set_free_order: bad argument");
+    SS_TRY(vokra_hip_kv_set_free_order(c, m->kv, order, n));
+    std::fill(m->position.begin(), m->position.end(), 0);
+    return VOKRA_HIP_OK;
+}
+
+int vokra_hip_text_decoder_kv_pages(vokra_hip_ctx_t* c, vokra_hip_text_decoder_t* m, size_t* free_pages,
+                                    size_t* pages_in_use) {
+    if (!c || !m || m->ctx != c)
+        return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "text_decoder_kv_pages: bad argument");
+    return vokra_hip_kv_pages(c, m->kv, free_pages, pages_in_use);
 }
 
 int vokra_hip_text_decoder_position(vokra_hip_ctx_t* c, vokra_hip_text_decoder_t* m, size_t stream, size_t* position) {

@@ -111,6 +111,14 @@ class WhisperConfig(C.Structure):
                [("eot", C.c_uint32)]
 
 
+class VoxtralConfig(C.Structure):
+    """vokra_hip_voxtral_config_t (voxtral/config.rs VoxtralConfig, numeric fields)."""
+    _fields_ = [(n, C.c_size_t) for n in ("audio_n_layer", "audio_n_head", "audio_hidden_dim", "audio_n_ctx",
+                                          "audio_n_mels", "audio_ffn_dim", "n_layer", "n_head_q", "n_head_kv",
+                                          "head_dim", "hidden_dim", "ffn_dim", "vocab_size", "n_ctx")] + \
+               [("rope_base", C.c_float), ("rms_norm_eps", C.c_float), ("cross_attn_hidden_dim", C.c_size_t)]
+
+
 class WhisperLoadReport(C.Structure):
     """vokra_hip_whisper_load_report_t: Linear weights taken verbatim / packed at load."""
     _fields_ = [("verbatim", C.c_size_t), ("packed", C.c_size_t)]
@@ -229,6 +237,9 @@ def _declare(L):
     L.vokra_hip_gguf_upload_qweight.argtypes = [P, P, C.c_char_p, C.POINTER(P)]
     L.vokra_hip_gguf_read_f32.argtypes = [P, C.c_char_p, f32p, sz]
     L.vokra_hip_whisper_config_from_gguf.argtypes = [P, C.POINTER(WhisperConfig)]
+    L.vokra_hip_voxtral_config_from_gguf.argtypes = [P, C.POINTER(VoxtralConfig)]
+    L.vokra_hip_text_decoder_from_gguf.argtypes = [P, P, C.POINTER(VoxtralConfig), C.c_int, sz, sz, sz,
+                                                   C.POINTER(WhisperLoadReport), C.POINTER(P)]
     L.vokra_hip_whisper_encoder_from_gguf.argtypes = [P, P, C.POINTER(WhisperConfig), C.c_int, sz,
                                                       C.POINTER(WhisperLoadReport), C.POINTER(P)]
     L.vokra_hip_whisper_decoder_from_gguf.argtypes = [P, P, C.POINTER(WhisperConfig), C.c_int, sz, sz,
@@ -257,6 +268,8 @@ def _declare(L):
     L.vokra_hip_decoder_set_encoder.argtypes = [P, P, sz, f32p]
     L.vokra_hip_decoder_set_encoder_dev.argtypes = [P, P, sz, P]
     L.vokra_hip_decoder_reset.argtypes = [P, P]
+    L.vokra_hip_decoder_set_free_order.argtypes = [P, P, i32p, sz]
+    L.vokra_hip_decoder_kv_pages.argtypes = [P, P, C.POINTER(sz), C.POINTER(sz)]
     L.vokra_hip_decoder_step.argtypes = [P, P, sz, i32p, i32p, i32p, i32p, f32p]
     L.vokra_hip_decoder_step_dev.argtypes = [P, P, sz, P, P, P, P, P]
     L.vokra_hip_decoder_status.argtypes = [P, P, C.POINTER(sz)]
@@ -272,6 +285,8 @@ def _declare(L):
     L.vokra_hip_text_decoder_destroy.argtypes = [P]
     L.vokra_hip_text_decoder_destroy.restype = None
     L.vokra_hip_text_decoder_reset.argtypes = [P, P]
+    L.vokra_hip_text_decoder_set_free_order.argtypes = [P, P, i32p, sz]
+    L.vokra_hip_text_decoder_kv_pages.argtypes = [P, P, C.POINTER(sz), C.POINTER(sz)]
     L.vokra_hip_text_decoder_position.argtypes = [P, P, sz, C.POINTER(sz)]
     L.vokra_hip_text_decoder_kv_restore.argtypes = [P, P, sz, sz, f32p, f32p]
     L.vokra_hip_text_decoder_step.argtypes = [P, P, sz, i32p, i32p, i32p, f32p]
@@ -487,6 +502,14 @@ class GgufFile:
         c = WhisperConfig()
         _check(lib().vokra_hip_whisper_config_from_gguf(self._h, C.byref(c)))
         return {n: getattr(c, n) for n, _ in WhisperConfig._fields_}
+
+    def voxtral_config(self) -> dict:
+        """VoxtralConfig::from_gguf (voxtral/config.rs:155-267); no GPU is touched.
+        head_dim is the explicit key (0 when absent); TextDecoderConfig::head_dim
+        then derives hidden_dim / n_head_q."""
+        c = VoxtralConfig()
+        _check(lib().vokra_hip_voxtral_config_from_gguf(self._h, C.byref(c)))
+        return {n: getattr(c, n) for n, _ in VoxtralConfig._fields_}
 
 
 class Graph:
@@ -749,6 +772,17 @@ class Decoder:
     def reset(self):
         _check(lib().vokra_hip_decoder_reset(self._ctx._h, self._h))
 
+    def kv_pages(self):
+        """(free, in use) pages of the self-KV cache."""
+        fr, used = C.c_size_t(0), C.c_size_t(0)
+        _check(lib().vokra_hip_decoder_kv_pages(self._ctx._h, self._h, C.byref(fr), C.byref(used)))
+        return fr.value, used.value
+
+    def set_free_order(self, order):
+        """Resets every stream and places later pages in `order` (a permutation of the page ids)."""
+        o = np.ascontiguousarray(order, np.int32)
+        _check(lib().vokra_hip_decoder_set_free_order(self._ctx._h, self._h, _ptr(o, C.c_int32), o.size))
+
     def step(self, streams, tokens, positions, want_logits=False):
         st = np.ascontiguousarray(streams, np.int32)
         tk = np.ascontiguousarray(tokens, np.int32)
@@ -807,8 +841,34 @@ class TextDecoder:
                                                    C.byref(h)))
         self._h = h
 
+    @classmethod
+    def from_gguf(cls, ctx, gguf, wdtype, n_stream, n_ctx=0, block_size=16):
+        """vokra_hip_text_decoder_from_gguf: TextDecoder::load
+        (voxtral/text_decoder.rs:484-575) with VoxtralConfig::from_gguf, as a
+        batched session. Returns (decoder, report)."""
+        cfg = VoxtralConfig()
+        _check(lib().vokra_hip_voxtral_config_from_gguf(gguf._h, C.byref(cfg)))
+        rep, h = WhisperLoadReport(), C.c_void_p()
+        _check(lib().vokra_hip_text_decoder_from_gguf(ctx._h, gguf._h, C.byref(cfg), int(wdtype), n_stream, n_ctx,
+                                                      block_size, C.byref(rep), C.byref(h)))
+        dec = cls.__new__(cls)
+        hd = cfg.head_dim or cfg.hidden_dim // cfg.n_head_q
+        dec._ctx, dec.vocab, dec.n_layer, dec.kv_hidden, dec._h = ctx, cfg.vocab_size, cfg.n_layer, cfg.n_head_kv * hd, h
+        return dec, {"verbatim": rep.verbatim, "packed": rep.packed}
+
     def reset(self):
         _check(lib().vokra_hip_text_decoder_reset(self._ctx._h, self._h))
+
+    def kv_pages(self):
+        """(free, in use) pages of the paged cache."""
+        fr, used = C.c_size_t(0), C.c_size_t(0)
+        _check(lib().vokra_hip_text_decoder_kv_pages(self._ctx._h, self._h, C.byref(fr), C.byref(used)))
+        return fr.value, used.value
+
+    def set_free_order(self, order):
+        """Resets every stream and places later pages in `order` (a permutation of the page ids)."""
+        o = np.ascontiguousarray(order, np.int32)
+        _check(lib().vokra_hip_text_decoder_set_free_order(self._ctx._h, self._h, _ptr(o, C.c_int32), o.size))
 
     def position(self, stream) -> int:
         p = C.c_size_t(0)
