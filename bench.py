@@ -557,26 +557,78 @@ def bench_copy(ctx, hip, nbytes=1 << 30, reps=5):
     return {"bytes": nbytes, "ms": round(ms, 4), "gbs": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
 
 
-def cpu_baseline_q8(a, wq, N, K, budget_s=10.0):
-    """Oracle INT8 block GEMM on as many rows as fit the time budget."""
-    from oracle import oracle as orc
-    orc.lib()
-    rows, t_total = 0, 0.0
-    chunk = 8
-    while rows < a.shape[0] and t_total < budget_s:
-        blk = a[rows:rows + chunk]
-        t0 = time.perf_counter()
-        orc.gemm_qblock_i8(orc.W_Q8_0, blk.shape[0], N, K, blk, wq)
-        t_total += time.perf_counter() - t0
-        rows += blk.shape[0]
-    return {"value": 2.0 * rows * N * K / t_total / 1e12, "unit": "TOPS", "cores": 1, "kind": "port",
-            "sample": f"{rows} of 1500 activation rows x full N=5120, K=1280 through the oracle's "
-                      f"INT8 block GEMM (oracle/vokra_oracle.c vo_gemm_qblock_i8_mode), "
-                      f"{t_total:.1f} s on host {platform.processor() or platform.machine()}"}
+def _cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def _host():
-    return f"{platform.processor() or platform.machine()}, {os.cpu_count()} logical cores"
+    return f"{_cpu_model()}, {os.cpu_count()} logical cores"
+
+
+def _threads():
+    """Host threads for the reference's pooled f32 work (VOKRA_CPU_THREADS
+    semantics: every core, pool.rs:340-355)."""
+    return max(1, os.cpu_count() or 1)
+
+
+def _pool_map(fn, items, threads):
+    """Runs fn over items on `threads` host threads (the oracle's ctypes calls
+    release the interpreter lock, so the calls run in parallel)."""
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        return list(ex.map(fn, items))
+
+
+def _sdpa_heads(orc, t_q, t_kv, hd, q, k, v, heads, threads, causal=False, off=0):
+    """attention_from_kv_into's per-head work (whisper/nn.rs:209-325) with the
+    heads spread over the pool, as the reference's per-head GEMMs run on it."""
+    return _pool_map(lambda h: orc.sdpa_whisper(t_q, t_kv, 1, hd, q, k, v, causal=causal, q_pos_offset=off),
+                     range(heads), threads)
+
+
+def cpu_baseline_q8(a, wq, N, K, budget_s=10.0):
+    """The reference CPU's route for a Q8_0 GEMM (vokra-backend-cpu has no
+    fused Q8_0 GEMM): A4 dequantize_bytes of the weight, transposed to [k, n],
+    then gemm_f32 row-parallel on every host thread (kv_quant/mod.rs:307-359,
+    kernels/mod.rs:305-325, scalar.rs:41-72, pool.rs:340-355), on as many
+    activation rows as fit the budget; the weight dequant is inside every
+    timed call. The single-thread route of dequant_gemv_scalar, one call per
+    activation row (dequant_gemm.rs:49-98), is timed beside it."""
+    from oracle import oracle as orc
+    orc.lib()
+    thr = _threads()
+    rows, t_total, chunk = 0, 0.0, 64
+    while rows < a.shape[0] and t_total < budget_s:
+        blk = a[rows:rows + chunk]
+        t0 = time.perf_counter()
+        wt = orc.dequantize_bytes(orc.Q8_0, wq).reshape(N, K).T.copy()
+        orc.gemm_f32(blk.shape[0], N, K, blk, wt, threads=thr)
+        t_total += time.perf_counter() - t0
+        rows += blk.shape[0]
+    pooled = 2.0 * rows * N * K / t_total / 1e12
+    # one thread, one dequant_gemv_scalar call per activation row
+    g_rows, g_total = 0, 0.0
+    while g_rows < 4 or (g_total < budget_s / 3 and g_rows < a.shape[0]):
+        t0 = time.perf_counter()
+        orc.dequant_gemv_scalar(orc.Q8_0, wq, N, K // 32, a[g_rows])
+        g_total += time.perf_counter() - t0
+        g_rows += 1
+    return ({"value": pooled, "unit": "TOPS", "cores": thr, "kind": "port",
+             "sample": f"{rows} of 1500 activation rows x N=5120, K=1280: dequantize_bytes (A4) + gemm_f32 on "
+                       f"{thr} threads (vo_gemm_f32_mt), the weight dequant in every call; {t_total:.1f} s on "
+                       f"{_host()}"},
+            {"dequant_gemv_scalar_per_row": {"value": 2.0 * g_rows * N * K / g_total / 1e12, "unit": "TOPS",
+                                             "cores": 1, "kind": "port",
+                                             "sample": f"{g_rows} activation rows, one dequant_gemv_scalar call each "
+                                                       f"(vo_dequant_gemv_scalar), {g_total:.1f} s on {_host()}"}})
 
 
 def _per_call(fn, budget_s):
@@ -596,27 +648,31 @@ def cpu_baselines(budget_s=3.0):
     """Each leg's CPU column: the oracle's restatement of the reference's CPU
     route (oracle/vokra_oracle.c, the vokra-backend-cpu scalar tier) timed on
     this host on a bounded sample of the leg's workload, with the reference's
-    threading (the INT8 and block routes are single-threaded; f32 GEMMs use
-    the pool, i.e. every core). Values are in the leg's own unit."""
+    threading: the block GEMV (dequant_gemv_scalar) and the K-quant INT8 route
+    single-threaded, every f32 GEMM and the attention heads on the pool (all
+    host threads). Values are in the leg's own unit."""
     from oracle import oracle as orc
     orc.lib()
     rng = np.random.default_rng(5)
     host = _host()
-    ncpu = os.cpu_count() or 1
+    thr = _threads()
     out = {}
 
-    # Q4_0 GEMV (dequant_gemv_scalar, 1 thread): one activation vector
-    n, k = 5120, 1280
-    wq = rng.integers(0, 256, n * (k // 32) * 18, dtype=np.uint8)
-    wq.reshape(-1, 18)[:, 0:2] = np.frombuffer(np.float16(0.002).tobytes(), np.uint8)
-    x = rng.standard_normal(k, dtype=np.float32)
-    sec, reps = _per_call(lambda: orc.dequant_gemv_scalar(1, wq, n, k // 32, x), budget_s)
-    nbytes = n * (k // 32) * 18 + k * 4 + n * 4
-    out["q4_0_gemv_streamed"] = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "us_per_linear": round(sec * 1e6, 1),
-                                 "cores": 1, "kind": "port",
-                                 "sample": f"M=1 N={n} K={k}, dequant_gemv_scalar (vo_dequant_gemv_scalar), "
-                                           f"median of {reps} on {host}"}
-    # Q4_K decode layer (kquant_gemm_i8, 1 thread): the 7 linears at M = 32
+    # Q4_0 GEMV (dequant_gemv_scalar, 1 thread): one activation vector, both config-1 widths
+    gemv = []
+    for n in (5120, 1280):
+        k = 1280
+        wq = rng.integers(0, 256, n * (k // 32) * 18, dtype=np.uint8)
+        wq.reshape(-1, 18)[:, 0:2] = np.frombuffer(np.float16(0.002).tobytes(), np.uint8)
+        x = rng.standard_normal(k, dtype=np.float32)
+        sec, reps = _per_call(lambda: orc.dequant_gemv_scalar(1, wq, n, k // 32, x), budget_s / 2)
+        nbytes = n * (k // 32) * 18 + k * 4 + n * 4
+        gemv.append({"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "us_per_linear": round(sec * 1e6, 1),
+                     "cores": 1, "kind": "port",
+                     "sample": f"M=1 N={n} K={k}, dequant_gemv_scalar (vo_dequant_gemv_scalar), median of {reps} on "
+                               f"{host}"})
+    out["q4_0_gemv_streamed"] = gemv
+    # Q4_K decode layer (kquant_gemm_i8, 1 thread: the reference does not pool it)
     total = 0.0
     for (_, n, k) in Q4K_LAYER:
         w = q4k_random_weight(rng, n, k)
@@ -628,76 +684,99 @@ def cpu_baselines(budget_s=3.0):
                                     "us_per_layer": round(total * 1e6, 1), "cores": 1, "kind": "port",
                                     "sample": f"one config-4 layer (7 linears) at M=32 through kquant_gemm_i8 "
                                               f"(vo_kquant_gemm_i8) on {host}"}
-    # fused SDPA config 1 (attention_from_kv_into per head: f32 GEMMs + softmax, 1 thread)
+    # fused SDPA config 1: the 20 heads of attention_from_kv_into on the pool
     T, hd = 1500, 64
     q, kk, v = (rng.standard_normal((T, hd), dtype=np.float32) for _ in range(3))
-    sec, reps = _per_call(lambda: orc.sdpa_whisper(T, T, 1, hd, q, kk, v), budget_s)
-    flops = 4.0 * T * T * hd
+    sec, reps = _per_call(lambda: _sdpa_heads(orc, T, T, hd, q, kk, v, 20, thr), budget_s)
+    flops = 4.0 * 20 * T * T * hd
     out["sdpa_config1"] = {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s",
-                           "ms_per_op": round(sec * 20 * 1e3, 1), "cores": 1, "kind": "port",
-                           "sample": f"one of the 20 heads (1500 x 1500 x 64, vo_sdpa_whisper), x20 for the op; "
-                                     f"median of {reps} on {host}"}
-    # paged decode attention (config 4: one stream, 16/2 heads x 128, 2300 keys)
+                           "ms_per_op": round(sec * 1e3, 1), "cores": min(thr, 20), "kind": "port",
+                           "sample": f"all 20 heads (1500 x 1500 x 64, vo_sdpa_whisper per head) on {min(thr, 20)} "
+                                     f"threads; median of {reps} on {host}"}
+    # paged decode attention: config 3 (64 streams x 20 heads x 64, 224 keys each, the U(1..448) mean)
+    # and config 4 (one stream, GQA 16/2 x 128, 2300 keys); dequantized rows, heads / streams on the pool
+    t3 = 224
+    K3 = rng.standard_normal((t3, 1280), dtype=np.float32)
+    V3 = rng.standard_normal((t3, 1280), dtype=np.float32)
+    q3 = rng.standard_normal((1, 1280), dtype=np.float32)
+    sec, reps = _per_call(lambda: _pool_map(lambda s: orc.sdpa_whisper(1, t3, 20, 64, q3, K3, V3, causal=True,
+                                                                       q_pos_offset=t3 - 1), range(64), thr),
+                          budget_s / 2)
+    nbytes = 64 * t3 * 2 * (1280 + 80)
+    out["paged_attn_config3"] = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s",
+                                 "us_per_layer": round(sec * 1e6, 1), "cores": thr, "kind": "port",
+                                 "sample": f"64 streams x 224 keys, 20 heads x 64 over dequantized rows "
+                                           f"(vo_sdpa_whisper per stream), streams on {thr} threads; median of "
+                                           f"{reps} on {host}"}
     t_kv = 2300
     Kc = rng.standard_normal((t_kv, 256), dtype=np.float32)
     Vc = rng.standard_normal((t_kv, 256), dtype=np.float32)
     qg = rng.standard_normal((1, 2048), dtype=np.float32)
-    sec, reps = _per_call(lambda: orc.gqa_attention(1, t_kv, 16, 2, 128, qg, Kc, Vc, 0.0884, t_kv - 1), budget_s)
+    sec, reps = _per_call(lambda: orc.gqa_attention(1, t_kv, 16, 2, 128, qg, Kc, Vc, 0.0884, t_kv - 1), budget_s / 2)
     nbytes = t_kv * 2 * (256 + 16)
     out["paged_attn_config4"] = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s",
                                  "us_per_stream": round(sec * 1e6, 1), "cores": 1, "kind": "port",
                                  "sample": f"one stream, 2300 keys, GQA 16/2 x 128 over dequantized rows "
-                                           f"(vo_gqa_attention), median of {reps} on {host}"}
-    # Whisper-large encoder block (config 2): INT8 linears (1 thread) + f32 attention, on 96 query rows
+                                           f"(vo_gqa_attention, text_decoder.rs:1302-1360 is a scalar loop), "
+                                           f"median of {reps} on {host}"}
+    # Whisper-large encoder block (config 2) on 96 of 1500 rows: Q8_0 linears through the
+    # reference route (A4 dequant + gemm_f32 on the pool), attention heads on the pool
     rows, d, ff = 96, 1280, 5120
     a = rng.standard_normal((rows, d), dtype=np.float32)
-    w8 = random_block_weight(rng, 8, d, d, 0.02)
+    wdd = [orc.dequantize_bytes(orc.Q8_0, random_block_weight(rng, 8, d, d, 0.02)).reshape(d, d).T.copy()
+           for _ in range(4)]
     w8f = random_block_weight(rng, 8, ff, d, 0.02)
     w8b = random_block_weight(rng, 8, d, ff, 0.02)
     af = rng.standard_normal((rows, ff), dtype=np.float32)
-    qh, kh, vh = rng.standard_normal((rows, 64), dtype=np.float32), q, v
+    qh = rng.standard_normal((rows, 64), dtype=np.float32)
 
     def enc_sample():
-        for _ in range(4):
-            orc.gemm_q_f32(8, rows, d, d, a, w8)
-        orc.gemm_q_f32(8, rows, ff, d, a, w8f)
-        orc.gemm_q_f32(8, rows, d, ff, af, w8b)
-        for _ in range(20):
-            orc.sdpa_whisper(rows, T, 1, 64, qh, kh, vh)
+        for w in wdd:
+            orc.gemm_f32(rows, d, d, a, w, threads=thr)
+        orc.gemm_f32(rows, ff, d, a, orc.dequantize_bytes(orc.Q8_0, w8f).reshape(ff, d).T.copy(), threads=thr)
+        orc.gemm_f32(rows, d, ff, af, orc.dequantize_bytes(orc.Q8_0, w8b).reshape(d, ff).T.copy(), threads=thr)
+        _sdpa_heads(orc, rows, T, 64, qh, kk, v, 20, thr)
     sec, reps = _per_call(enc_sample, budget_s)
     per_block = sec * (1500 / rows)
     flops_block = 2 * 1500 * (4 * d * d + 2 * d * ff) + 4 * 20 * 1500 * 1500 * 64
-    out["encoder_config2"] = {"value": round(flops_block / per_block / 1e12, 4), "unit": "TFLOP/s",
-                              "ms_per_utterance": round(per_block * 32 * 1e3, 0), "cores": 1, "kind": "port",
-                              "sample": f"one block's linears (gemm_q_f32 Q8_0) and 20 attention heads for {rows} of "
-                                        f"1500 rows, scaled to 1500 rows x 32 blocks; median of {reps} on {host}"}
-    # Whisper decoder step (config 3): one stream, one layer's 8 step linears + self/cross attention + logits
+    enc = {"value": round(flops_block / per_block / 1e12, 4), "unit": "TFLOP/s",
+           "ms_per_utterance": round(per_block * 32 * 1e3, 0), "cores": thr, "kind": "port",
+           "sample": f"one block for {rows} of 1500 rows (Q8_0 linears as dequantize_bytes + gemm_f32 on {thr} "
+                     f"threads, 20 attention heads on the pool), scaled to 1500 rows x 32 blocks; an utterance "
+                     f"batch runs one utterance after another (batch 16 = 16x); median of {reps} on {host}"}
+    out["encoder_config2"] = [enc, dict(enc, sample=enc["sample"] + "; batch 16 line: same per-utterance rate")]
+    # Whisper decoder step (config 3): one stream, one layer's 8 step linears (dequant_gemv_scalar,
+    # 1 thread) + self / cross attention (heads on the pool) + the tied logits (gemm_f32 on the pool)
     Vv = 51866
     a1 = rng.standard_normal((1, d), dtype=np.float32)
-    f1 = rng.standard_normal((1, ff), dtype=np.float32)
+    f1 = rng.standard_normal(ff, dtype=np.float32)
     w4 = random_block_weight(rng, 2, d, d, 0.02)
     w4f = random_block_weight(rng, 2, ff, d, 0.02)
     w4b = random_block_weight(rng, 2, d, ff, 0.02)
     ck = rng.standard_normal((1500, d), dtype=np.float32)
     sk = rng.standard_normal((224, d), dtype=np.float32)
     emb = rng.standard_normal((Vv, d), dtype=np.float32)
+    embt = emb.T.copy()
+    q64, sk64, ck64 = (np.ascontiguousarray(x[:, :64]) for x in (a1, sk, ck))
 
     def dec_layer():
         for _ in range(6):
-            orc.gemm_q_f32(2, 1, d, d, a1, w4)
-        orc.gemm_q_f32(2, 1, ff, d, a1, w4f)
-        orc.gemm_q_f32(2, 1, d, ff, f1, w4b)
-        orc.sdpa_whisper(1, 224, 20, 64, a1, sk, sk, causal=True, q_pos_offset=223)
-        orc.sdpa_whisper(1, 1500, 20, 64, a1, ck, ck)
+            orc.dequant_gemv_scalar(1, w4, d, d // 32, a1[0])
+        orc.dequant_gemv_scalar(1, w4f, ff, d // 32, a1[0])
+        orc.dequant_gemv_scalar(1, w4b, d, ff // 32, f1)
+        _pool_map(lambda h: orc.sdpa_whisper(1, 224, 1, 64, q64, sk64, sk64, causal=True, q_pos_offset=223),
+                  range(20), thr)
+        _pool_map(lambda h: orc.sdpa_whisper(1, 1500, 1, 64, q64, ck64, ck64), range(20), thr)
     sec_l, _ = _per_call(dec_layer, budget_s / 2)
-    sec_g, _ = _per_call(lambda: orc.gemm_f32(1, Vv, d, a1, emb.T.copy(), threads=ncpu), budget_s / 2)
+    sec_g, _ = _per_call(lambda: orc.gemm_f32(1, Vv, d, a1, embt, threads=thr), budget_s / 2)
     step = 32 * sec_l + sec_g
     out["decoder_step_config3"] = {"value": round(1.0 / step, 2), "unit": "tokens/s",
-                                   "ms_per_stream_step": round(step * 1e3, 1), "cores": 1, "kind": "port",
-                                   "sample": f"one stream: one layer (8 Q4_0 step linears, self-attention over 224 "
-                                             f"keys, cross over 1500) x 32, plus the tied logits (gemm_f32 on "
-                                             f"{ncpu} threads); streams run one after another, so 64 streams "
-                                             f"take 64x; on {host}"}
+                                   "ms_per_stream_step": round(step * 1e3, 1), "cores": thr, "kind": "port",
+                                   "sample": f"one stream: one layer (8 Q4_0 step linears through "
+                                             f"dequant_gemv_scalar, 1 thread; self-attention over 224 keys and "
+                                             f"cross over 1500, 20 heads on {thr} threads) x 32, plus the tied "
+                                             f"logits (gemm_f32 on {thr} threads); the reference has no batch "
+                                             f"axis, so 64 streams take 64x; on {host}"}
     # speech-LLM step (config 4): one stream, one layer's 7 Q4_K linears + GQA over 2300 keys
     def td_layer():
         for (_, n, k) in Q4K_LAYER:
@@ -712,19 +791,21 @@ def cpu_baselines(budget_s=3.0):
     out["text_decoder_step_config4"] = {"value": round(1.0 / step, 2), "unit": "tokens/s",
                                         "ms_per_stream_step": round(step * 1e3, 1), "cores": 1, "kind": "port",
                                         "sample": f"one stream: one layer (7 Q4_K linears via kquant_gemm_i8, GQA "
-                                                  f"over 2300 keys) x 24 plus the Q4_K LM head; on {host}"}
-    # log-mel front end (one 30 s clip, 128 mels; the oracle's f64 DFT)
+                                                  f"over 2300 keys; the reference runs both single-threaded) x 24 "
+                                                  f"plus the Q4_K LM head; on {host}"}
+    # log-mel front end (one 30 s clip, 128 mels; the oracle's f64 DFT), clips on the pool
     pcm = rng.standard_normal(480000, dtype=np.float32) * 0.1
-    sec, reps = _per_call(lambda: orc.log_mel(pcm, 128), budget_s)
-    out["frontend_config2_batch16"] = {"value": round(1.0 / sec, 2), "unit": "clips/s", "cores": 1, "kind": "port",
-                                       "sample": f"log-mel of one 30 s clip, 128 mels (vo_log_mel, f64 DFT), median "
-                                                 f"of {reps} on {host}"}
+    sec, reps = _per_call(lambda: _pool_map(lambda i: orc.log_mel(pcm, 128), range(min(thr, 16)), thr), budget_s)
+    out["frontend_config2_batch16"] = {"value": round(min(thr, 16) / sec, 2), "unit": "clips/s",
+                                       "cores": min(thr, 16), "kind": "port",
+                                       "sample": f"log-mel of {min(thr, 16)} 30 s clips, 128 mels (vo_log_mel, f64 "
+                                                 f"DFT), one clip per thread; median of {reps} on {host}"}
     # tied logits + argmax (config 3): gemm_f32 over the embedding on every core
     xs = rng.standard_normal((8, d), dtype=np.float32)
-    sec, reps = _per_call(lambda: orc.gemm_f32(8, Vv, d, xs, emb.T.copy(), threads=ncpu), budget_s)
+    sec, reps = _per_call(lambda: orc.gemm_f32(8, Vv, d, xs, embt, threads=thr), budget_s)
     out["logits_argmax_config3"] = {"value": round(2.0 * 8 * Vv * d / sec / 1e12, 4), "unit": "TFLOP/s",
-                                    "cores": ncpu, "kind": "port",
-                                    "sample": f"8 of 64 stream rows x 51866 x 1280 (vo_gemm_f32_mt, {ncpu} threads), "
+                                    "cores": thr, "kind": "port",
+                                    "sample": f"8 of 64 stream rows x 51866 x 1280 (vo_gemm_f32_mt, {thr} threads), "
                                               f"median of {reps} on {host}"}
     return out
 
@@ -803,10 +884,10 @@ def main():
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK["int8_tops"],
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK["int8_tops"], 4),
                 "traffic": load_traffic("vk_gemm_qblock")}
-    cpu = None
+    cpu, cpu_routes = None, None
     legs_cpu = {}
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline_q8(main_run["a"], main_run["wq"], N, K)
+        cpu, cpu_routes = cpu_baseline_q8(main_run["a"], main_run["wq"], N, K)
         legs_cpu = cpu_baselines()
     line = {
         "metric": METRIC,
@@ -836,6 +917,7 @@ def main():
             "logits_argmax_config3": logits_run,
             "decoder_step_config3": decoder_run,
             "text_decoder_step_config4": textdec_run,
+            "cpu_q8_gemm_other_routes": cpu_routes,
             "gemm_kernel_ms": round(main_run["gemm_ms"], 4),
             "eager_step_ms": round(main_run["eager_ms"], 4),
             "gemm_frac_of_bf16_mfma_peak": round(achieved / PEAK["bf16_tflops"], 4),
@@ -845,15 +927,16 @@ def main():
         },
     }
     for leg, base in legs_cpu.items():
-        key = "paged_attn_config3_config4" if leg == "paged_attn_config4" else leg
+        key = "paged_attn_config3_config4" if leg.startswith("paged_attn_config") else leg
         entry = line["extra"].get(key)
         if isinstance(entry, dict):
             entry["cpu_baseline"] = base
-        elif isinstance(entry, list) and entry and isinstance(entry[-1], dict):
-            # the sampled shape: the first GEMV line (N = 5120) and the batch-1
-            # encoder line; the last paged-attention line (config 4)
-            first = leg in ("q4_0_gemv_streamed", "encoder_config2")
-            entry[0 if first else -1]["cpu_baseline"] = base
+        elif isinstance(entry, list) and entry:
+            if isinstance(base, list):   # one baseline per line (GEMV widths, encoder batches)
+                for e, b in zip(entry, base):
+                    e["cpu_baseline"] = b
+            else:                        # the paged lines: config 3 first, config 4 last
+                entry[0 if leg == "paged_attn_config3" else -1]["cpu_baseline"] = base
     print(json.dumps(line), flush=True)
     ctx.close()
     return 0

@@ -55,7 +55,9 @@ typedef enum vokra_hip_wdtype_t {
     VOKRA_HIP_W_Q4_0 = 2,
     VOKRA_HIP_W_Q5_0 = 6,
     VOKRA_HIP_W_Q8_0 = 8,
-    VOKRA_HIP_W_Q4_K = 12
+    VOKRA_HIP_W_Q4_K = 12,
+    VOKRA_HIP_W_Q5_K = 13,
+    VOKRA_HIP_W_Q6_K = 14
 } vokra_hip_wdtype_t;
 
 /* Activation quantization convention of the INT8 matmul.
@@ -129,11 +131,13 @@ void vokra_hip_graph_destroy(vokra_hip_graph_t *g);
 int vokra_hip_dequantize_bytes(vokra_hip_ctx_t *ctx, int mode, const uint8_t *bytes, size_t n_bytes,
                                float *out, size_t out_len);
 
-/* Q4_K super-blocks -> f32, bit-exact (y = d*sc*q - dmin*m, two roundings).
- * Replaces gguf::quant::dequantize for GgmlType::Q4K
- * (crates/vokra-core/src/gguf/quant/mod.rs:42-63 -> gguf/quant/q4_k.rs:34-69):
- * n_elements must be a multiple of 256 and n_bytes = n_elements/256 * 144
- * (a mismatch is INVALID_ARGUMENT, the reference's TensorSizeMismatch). */
+/* K-quant super-blocks -> f32, bit-exact. Replaces gguf::quant::dequantize
+ * (crates/vokra-core/src/gguf/quant/mod.rs:42-63) for GgmlType::Q4K
+ * (q4_k.rs:34-69: y = d*sc*q - dmin*m, two roundings), Q5K (q5_k.rs:36-80:
+ * the same with a fifth quant bit) and Q6K (q6_k.rs:34-72: y = d*sc*(q - 32)):
+ * n_elements must be a multiple of 256 and n_bytes = n_elements/256 * 144,
+ * 176 or 210 (a mismatch is INVALID_ARGUMENT, the reference's
+ * TensorSizeMismatch). */
 int vokra_hip_kquant_dequantize(vokra_hip_ctx_t *ctx, int wdtype, const uint8_t *bytes, size_t n_bytes,
                                 size_t n_elements, float *out);
 
@@ -162,9 +166,11 @@ int vokra_hip_dequant_gemv_f32(vokra_hip_ctx_t *ctx, int mode, const uint8_t *bl
  * -> kernels::gemm_q_f32 (crates/vokra-backend-cpu/src/kernels/mod.rs:341-364)
  * -> gemm_driver::run_q (gemm_driver.rs:312-332): wq is the untransposed
  * [n, k] payload, a is [m, k], out is [m, n], bias is added after. Block
- * formats use the context's activation convention (default AMAX127); Q4_K
- * runs kquant_gemm_i8 (kquant.rs:845-935): k a multiple of 256, KQUANT
- * activations, bit-identical outputs. */
+ * formats use the context's activation convention (default AMAX127); the
+ * K-quants (Q4_K, Q5_K, Q6_K: the reference's whole KQuantDtype) run
+ * kquant_gemm_i8 (kquant.rs:845-935) over unpack_block_i8's unified
+ * representation (:332-407): k a multiple of 256, KQUANT activations,
+ * bit-identical outputs. */
 int vokra_hip_gemm_q_f32(vokra_hip_ctx_t *ctx, int wdtype, size_t m, size_t n, size_t k, const float *a,
                          size_t a_len, const uint8_t *wq, size_t wq_len, const float *bias, float *out,
                          size_t out_len);

@@ -27,11 +27,11 @@ KV_CACHE_EXHAUSTED = 10
 # KvQuant (kv_quant/mod.rs:81-91)
 FP32, Q4_0, Q5_0, Q8_0 = 0, 1, 2, 3
 # weight dtypes (ggml tags)
-W_Q4_0, W_Q5_0, W_Q8_0, W_Q4_K = 2, 6, 8, 12
+W_Q4_0, W_Q5_0, W_Q8_0, W_Q4_K, W_Q5_K, W_Q6_K = 2, 6, 8, 12, 13, 14
 
 KV_BLOCK_BYTES = {FP32: 128, Q4_0: 18, Q5_0: 22, Q8_0: 34}
-W_BLOCK_BYTES = {W_Q4_0: 18, W_Q5_0: 22, W_Q8_0: 34, W_Q4_K: 144}
-W_BLOCK_ELEMS = {W_Q4_0: 32, W_Q5_0: 32, W_Q8_0: 32, W_Q4_K: 256}
+W_BLOCK_BYTES = {W_Q4_0: 18, W_Q5_0: 22, W_Q8_0: 34, W_Q4_K: 144, W_Q5_K: 176, W_Q6_K: 210}
+W_BLOCK_ELEMS = {W_Q4_0: 32, W_Q5_0: 32, W_Q8_0: 32, W_Q4_K: 256, W_Q5_K: 256, W_Q6_K: 256}
 KV_OF_W = {W_Q4_0: Q4_0, W_Q5_0: Q5_0, W_Q8_0: Q8_0}
 
 

@@ -511,32 +511,96 @@ static void get_scale_min_k4(int j, const uint8_t *s, uint8_t *d, uint8_t *m) {
     }
 }
 
+/* Super-block bytes of a K-quant dtype (gguf/tensor.rs:117-125), 0 if none. */
+static size_t kq_block_bytes(int wd) {
+    return wd == VO_W_Q4_K ? 144 : wd == VO_W_Q5_K ? 176 : wd == VO_W_Q6_K ? 210 : 0;
+}
+
 /* crates/vokra-core/src/gguf/quant/q4_k.rs:34-69 */
+static void dequant_q4k_block(const uint8_t *blk, float *y) {
+    float d = vo_gguf_f16_to_f32(get_u16(blk));
+    float dmin = vo_gguf_f16_to_f32(get_u16(blk + 2));
+    const uint8_t *scales = blk + 4, *qs = blk + 16;
+    int is = 0;
+    size_t q = 0, base = 0;
+    while (base < 256) {
+        uint8_t sc0, m0, sc1, m1s;
+        get_scale_min_k4(is, scales, &sc0, &m0);
+        float d1 = d * (float)sc0, m1 = dmin * (float)m0;
+        get_scale_min_k4(is + 1, scales, &sc1, &m1s);
+        float d2 = d * (float)sc1, m2 = dmin * (float)m1s;
+        for (int l = 0; l < 32; ++l) y[base + l] = d1 * (float)(qs[q + l] & 0xF) - m1;
+        for (int l = 0; l < 32; ++l) y[base + 32 + l] = d2 * (float)(qs[q + l] >> 4) - m2;
+        q += 32;
+        is += 2;
+        base += 64;
+    }
+}
+
+/* crates/vokra-core/src/gguf/quant/q5_k.rs:36-80: Q4_K's sub-scales, each
+ * quant gaining a 5th bit from qh (chunk k: low 32 take bit 2k, high 32 bit
+ * 2k + 1). */
+static void dequant_q5k_block(const uint8_t *blk, float *y) {
+    float d = vo_gguf_f16_to_f32(get_u16(blk));
+    float dmin = vo_gguf_f16_to_f32(get_u16(blk + 2));
+    const uint8_t *scales = blk + 4, *qh = blk + 16, *qs = blk + 48;
+    int is = 0;
+    size_t ql = 0, base = 0;
+    uint8_t u1 = 1, u2 = 2;
+    while (base < 256) {
+        uint8_t sc0, m0, sc1, m1s;
+        get_scale_min_k4(is, scales, &sc0, &m0);
+        float d1 = d * (float)sc0, m1 = dmin * (float)m0;
+        get_scale_min_k4(is + 1, scales, &sc1, &m1s);
+        float d2 = d * (float)sc1, m2 = dmin * (float)m1s;
+        for (int l = 0; l < 32; ++l) {
+            unsigned q = (qs[ql + l] & 0xFu) + ((qh[l] & u1) ? 16u : 0u);
+            y[base + l] = d1 * (float)q - m1;
+        }
+        for (int l = 0; l < 32; ++l) {
+            unsigned q = (unsigned)(qs[ql + l] >> 4) + ((qh[l] & u2) ? 16u : 0u);
+            y[base + 32 + l] = d2 * (float)q - m2;
+        }
+        ql += 32;
+        is += 2;
+        u1 = (uint8_t)(u1 << 2);
+        u2 = (uint8_t)(u2 << 2);
+        base += 64;
+    }
+}
+
+/* crates/vokra-core/src/gguf/quant/q6_k.rs:34-72: y = d * sc (int8) * q with
+ * q = (4 low bits | 2 high bits << 4) - 32, in that association. */
+static void dequant_q6k_block(const uint8_t *blk, float *out) {
+    float d = vo_gguf_f16_to_f32(get_u16(blk + 208));
+    for (int half = 0; half < 2; ++half) {
+        const uint8_t *ql = blk + 64 * half, *qh = blk + 128 + 32 * half, *sc = blk + 192 + 8 * half;
+        float *y = out + 128 * half;
+        for (int l = 0; l < 32; ++l) {
+            int is = l / 16;
+            int q1 = (int)((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32;
+            int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            y[l] = d * (float)(int8_t)sc[is] * (float)q1;
+            y[l + 32] = d * (float)(int8_t)sc[is + 2] * (float)q2;
+            y[l + 64] = d * (float)(int8_t)sc[is + 4] * (float)q3;
+            y[l + 96] = d * (float)(int8_t)sc[is + 6] * (float)q4;
+        }
+    }
+}
+
+/* crates/vokra-core/src/gguf/quant/mod.rs:42-63 dequantize, K-quant arms */
 int vo_kquant_dequantize(int wd, const uint8_t *bytes, size_t n_bytes, size_t n_elements, float *out) {
-    if (wd != VO_W_Q4_K) return VO_UNSUPPORTED_OP;
+    size_t bb = kq_block_bytes(wd);
+    if (!bb) return VO_UNSUPPORTED_OP;
     if (n_elements % 256 != 0) return VO_INVALID_ARGUMENT;
     size_t nb = n_elements / 256;
-    if (n_bytes != nb * 144) return VO_INVALID_ARGUMENT;
+    if (n_bytes != nb * bb) return VO_INVALID_ARGUMENT;
     for (size_t i = 0; i < nb; ++i) {
-        const uint8_t *blk = bytes + i * 144;
-        float d = vo_gguf_f16_to_f32(get_u16(blk));
-        float dmin = vo_gguf_f16_to_f32(get_u16(blk + 2));
-        const uint8_t *scales = blk + 4, *qs = blk + 16;
-        float *y = out + i * 256;
-        int is = 0;
-        size_t q = 0, base = 0;
-        while (base < 256) {
-            uint8_t sc0, m0, sc1, m1s;
-            get_scale_min_k4(is, scales, &sc0, &m0);
-            float d1 = d * (float)sc0, m1 = dmin * (float)m0;
-            get_scale_min_k4(is + 1, scales, &sc1, &m1s);
-            float d2 = d * (float)sc1, m2 = dmin * (float)m1s;
-            for (int l = 0; l < 32; ++l) y[base + l] = d1 * (float)(qs[q + l] & 0xF) - m1;
-            for (int l = 0; l < 32; ++l) y[base + 32 + l] = d2 * (float)(qs[q + l] >> 4) - m2;
-            q += 32;
-            is += 2;
-            base += 64;
-        }
+        if (wd == VO_W_Q4_K) dequant_q4k_block(bytes + i * bb, out + i * 256);
+        else if (wd == VO_W_Q5_K) dequant_q5k_block(bytes + i * bb, out + i * 256);
+        else dequant_q6k_block(bytes + i * bb, out + i * 256);
     }
     return VO_OK;
 }
@@ -580,18 +644,47 @@ int vo_kquant_quantize(int wd, const float *data, size_t n, uint8_t *out) {
     return VO_OK;
 }
 
-/* crates/vokra-backend-cpu/src/kernels/kquant.rs:332-407 (Q4_K arm of
- * unpack_block_i8; sub-scales via q45_sub_scales :290-302). */
+/* crates/vokra-backend-cpu/src/kernels/kquant.rs:332-407 unpack_block_i8: the
+ * format-independent y = d_eff * q - m_eff per 16-element group. Q4_K / Q5_K
+ * take their sub-scales through q45_sub_scales (:290-302; one (d, m) pair per
+ * 32 elements, so two identical groups) and Q5_K adds the qh bit; Q6_K keeps
+ * the biased q6 + 32 in 0..63 with d_eff = d * sc (int8) per 16 elements in
+ * q6_group_scales' order (:306-323) and m_eff = d_eff * 32 (exact). */
 typedef struct {
     uint8_t q[256];
     float d_eff[16];
     float m_eff[16];
 } unpacked_block;
 
-static void unpack_block_i8_q4k(const uint8_t *block, unpacked_block *ub) {
+static void unpack_block_i8(int wd, const uint8_t *block, unpacked_block *ub) {
+    if (wd == VO_W_Q6_K) {
+        float d = vo_gguf_f16_to_f32(get_u16(block + 208));
+        const uint8_t *sc = block + 192;
+        for (int half = 0; half < 2; ++half)
+            for (int quarter = 0; quarter < 4; ++quarter)
+                for (int sub = 0; sub < 2; ++sub) {
+                    int g = (128 * half + 32 * quarter + 16 * sub) / 16;
+                    int idx = 8 * half + sub + 2 * quarter;
+                    ub->d_eff[g] = d * (float)(int8_t)sc[idx];
+                }
+        for (int g = 0; g < 16; ++g) ub->m_eff[g] = ub->d_eff[g] * 32.0f;
+        for (int half = 0; half < 2; ++half) {
+            const uint8_t *ql = block + 64 * half, *qh = block + 128 + 32 * half;
+            uint8_t *y = ub->q + 128 * half;
+            for (int l = 0; l < 32; ++l) {
+                y[l] = (uint8_t)((ql[l] & 0xF) | ((qh[l] & 3) << 4));
+                y[l + 32] = (uint8_t)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4));
+                y[l + 64] = (uint8_t)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4));
+                y[l + 96] = (uint8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4));
+            }
+        }
+        return;
+    }
     float d = vo_gguf_f16_to_f32(get_u16(block));
     float dmin = vo_gguf_f16_to_f32(get_u16(block + 2));
-    const uint8_t *scales = block + 4, *qs = block + 16;
+    const uint8_t *scales = block + 4;
+    const uint8_t *qs = wd == VO_W_Q5_K ? block + 48 : block + 16;
+    const uint8_t *qh = wd == VO_W_Q5_K ? block + 16 : NULL;
     for (int j = 0; j < 8; ++j) {
         uint8_t sc, mn;
         get_scale_min_k4(j, scales, &sc, &mn);
@@ -603,7 +696,9 @@ static void unpack_block_i8_q4k(const uint8_t *block, unpacked_block *ub) {
         int chunk = j / 2, hi = j % 2;
         for (int t = 0; t < 32; ++t) {
             uint8_t byte = qs[32 * chunk + t];
-            ub->q[32 * j + t] = hi ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 0xF);
+            uint8_t q = hi ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 0xF);
+            if (qh && (qh[t] & (1u << j))) q = (uint8_t)(q + 16);
+            ub->q[32 * j + t] = q;
         }
     }
 }
@@ -634,9 +729,10 @@ void vo_kquant_quantize_activations(const float *x, size_t k, int8_t *q, float *
 /* kquant.rs:542-578 validate_gemv_i8 */
 static int validate_gemv_i8(int wd, size_t m, size_t k, size_t w_len, size_t x_len, size_t out_len,
                             size_t n_x) {
-    if (wd != VO_W_Q4_K) return VO_UNSUPPORTED_OP;
+    size_t bb = kq_block_bytes(wd);
+    if (!bb) return VO_UNSUPPORTED_OP;
     if (k == 0 || k % 256 != 0) return VO_INVALID_ARGUMENT;
-    size_t row_bytes = (k / 256) * 144;
+    size_t row_bytes = (k / 256) * bb;
     if (w_len != m * row_bytes) return VO_INVALID_ARGUMENT;
     if (x_len != n_x * k) return VO_INVALID_ARGUMENT;
     if (out_len != n_x * m) return VO_INVALID_ARGUMENT;
@@ -644,18 +740,18 @@ static int validate_gemv_i8(int wd, size_t m, size_t k, size_t w_len, size_t x_l
 }
 
 /* kquant.rs:590-629 kquant_gemv_i8_on (scalar group sums :453-463, combine :447-449) */
-static void kquant_gemv_i8_core(size_t m, size_t k, const uint8_t *w, const float *x, float *out) {
-    size_t nb = k / 256;
+static void kquant_gemv_i8_core(int wd, size_t m, size_t k, const uint8_t *w, const float *x, float *out) {
+    size_t nb = k / 256, bb = kq_block_bytes(wd);
     int8_t *q = (int8_t *)malloc(k);
     float *sc = (float *)malloc((k / 16) * sizeof(float));
     int32_t *gs = (int32_t *)malloc((k / 16) * sizeof(int32_t));
     vo_kquant_quantize_activations(x, k, q, sc, gs);
     unpacked_block ub;
     for (size_t i = 0; i < m; ++i) {
-        const uint8_t *row = w + i * nb * 144;
+        const uint8_t *row = w + i * nb * bb;
         float acc = 0.0f;
         for (size_t blk = 0; blk < nb; ++blk) {
-            unpack_block_i8_q4k(row + blk * 144, &ub);
+            unpack_block_i8(wd, row + blk * bb, &ub);
             for (int g = 0; g < 16; ++g) {
                 int32_t isum = 0;
                 for (int t = 0; t < 16; ++t)
@@ -676,7 +772,7 @@ int vo_kquant_gemv_i8(int wd, size_t m, size_t k, const uint8_t *w, size_t w_len
                       size_t x_len, float *out, size_t out_len) {
     int st = validate_gemv_i8(wd, m, k, w_len, x_len, out_len, 1);
     if (st) return st;
-    kquant_gemv_i8_core(m, k, w, x, out);
+    kquant_gemv_i8_core(wd, m, k, w, x, out);
     return VO_OK;
 }
 
@@ -687,18 +783,18 @@ int vo_kquant_gemm_i8(int wd, size_t m, size_t k, size_t n_act, const uint8_t *w
     if (n_act == 0) return VO_INVALID_ARGUMENT;
     int st = validate_gemv_i8(wd, m, k, w_len, x_len, out_len, n_act);
     if (st) return st;
-    for (size_t c = 0; c < n_act; ++c) kquant_gemv_i8_core(m, k, w, x + c * k, out + c * m);
+    for (size_t c = 0; c < n_act; ++c) kquant_gemv_i8_core(wd, m, k, w, x + c * k, out + c * m);
     return VO_OK;
 }
 
-/* kquant.rs:471-495 int8_error_bound (Q4_K) */
+/* kquant.rs:471-495 int8_error_bound */
 float vo_int8_error_bound(int wd, const uint8_t *w_row, const float *x, size_t k) {
-    (void)wd;
-    size_t nb = k / 256;
+    size_t nb = k / 256, bb = kq_block_bytes(wd);
     unpacked_block ub;
     float bound = 0.0f;
+    if (!bb) return 0.0f;
     for (size_t blk = 0; blk < nb; ++blk) {
-        unpack_block_i8_q4k(w_row + blk * 144, &ub);
+        unpack_block_i8(wd, w_row + blk * bb, &ub);
         for (int g = 0; g < 16; ++g) {
             float s = amax32(x + blk * 256 + 16 * g, 16) / 127.0f;
             float wsum = -0.0f;
@@ -715,7 +811,7 @@ float vo_int8_error_bound(int wd, const uint8_t *w_row, const float *x, size_t k
 int vo_gemm_q_f32(int wd, size_t m, size_t n, size_t k, const float *a, size_t a_len,
                   const uint8_t *wq, size_t wq_len, const float *bias, float *out, size_t out_len) {
     if (a_len != m * k || out_len != m * n) return VO_INVALID_ARGUMENT;
-    if (wd == VO_W_Q4_K) {
+    if (kq_block_bytes(wd)) {
         int st = vo_kquant_gemm_i8(wd, n, k, m, wq, wq_len, a, a_len, out, out_len);
         if (st) return st;
         if (bias)

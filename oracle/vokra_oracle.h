@@ -40,7 +40,7 @@ enum { VO_KV_FP32 = 0, VO_KV_Q4_0 = 1, VO_KV_Q5_0 = 2, VO_KV_Q8_0 = 3 };
 
 /* Weight dtypes for gemm_q_f32, numbered by their ggml type tags
  * (gguf/tensor.rs:57-95 for the K-quants; 2/6/8 are ggml's Q4_0/Q5_0/Q8_0). */
-enum { VO_W_Q4_0 = 2, VO_W_Q5_0 = 6, VO_W_Q8_0 = 8, VO_W_Q4_K = 12 };
+enum { VO_W_Q4_0 = 2, VO_W_Q5_0 = 6, VO_W_Q8_0 = 8, VO_W_Q4_K = 12, VO_W_Q5_K = 13, VO_W_Q6_K = 14 };
 
 /* ---- binary16 (A1) ---------------------------------------------------- */
 float vo_f16_bits_to_f32(uint16_t h);

@@ -8,6 +8,7 @@ U8, I8, U16, I16, U32, I32, F32, BOOL, STRING, ARRAY, U64, I64, F64 = range(13)
 _FMT = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: "<f", BOOL: "<B", U64: "<Q",
         I64: "<q", F64: "<d"}
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q5_0, GGML_Q8_0, GGML_Q4_K = 0, 1, 2, 6, 8, 12
+GGML_Q5_K, GGML_Q6_K, GGML_BF16 = 13, 14, 30
 
 
 def gstr(s) -> bytes:

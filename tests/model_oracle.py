@@ -95,6 +95,9 @@ def quantize_weight(orc, wd, w):
     n, k = w.shape
     if wd == W_Q4_K:
         return orc.kquant_quantize(W_Q4_K, np.ascontiguousarray(w, np.float32).reshape(-1))
+    if wd in (13, 14):   # Q5_K / Q6_K: the tests' quantizer (the reference ships none)
+        from tests.helpers import quantize_kquant_test
+        return quantize_kquant_test(w, wd)
     return orc.pack_matrix_to_bytes(orc.KV_OF_W[wd], np.ascontiguousarray(w, np.float32), n, k // 32)
 
 

@@ -80,7 +80,8 @@ def test_rejections(tmp_path):
     expect(hip.ModelLoad, tmp_path, b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + struct.pack("<Q", 1 << 40) + b"k",
            "truncated")
     q8 = bytes(34)
-    expect(hip.ModelLoad, tmp_path, gw.build([], [("x", [32, 1], 14, bytes(210))]), "unsupported ggml type")
+    expect(hip.ModelLoad, tmp_path, gw.build([], [("x", [32, 1], 7, bytes(24))]), "unsupported ggml type")  # Q5_1
+    expect(hip.ModelLoad, tmp_path, gw.build([], [("x", [32, 1], gw.GGML_Q6_K, bytes(210))]), "whole number")
     expect(hip.ModelLoad, tmp_path, gw.build([], [("x", [32], gw.GGML_Q8_0, q8), ("x", [32], gw.GGML_Q8_0, q8)]),
            "duplicate tensor")
     expect(hip.ModelLoad, tmp_path, gw.build([], [("x", [32], gw.GGML_Q8_0, q8)], offsets=[8]), "not a multiple")
@@ -205,3 +206,23 @@ def test_reference_written_gguf_truncations(tmp_path):
     bad[4:8] = struct.pack("<I", 2)
     with pytest.raises(hip.ModelLoad, match="unsupported version"):
         hip.GgufFile(write(tmp_path, bytes(bad), "v2.gguf"))
+
+
+def test_kquant_and_bf16_tensors(tmp_path):
+    """The reference reader's other tensor types (tensor.rs:85-95): Q5_K (176
+    bytes per 256), Q6_K (210) and BF16 round-trip; BF16 widens to f32
+    exactly (its 16 bits become the high half)."""
+    g = np.random.default_rng(3)
+    q5 = bytes(g.integers(0, 256, 176 * 3, dtype=np.uint8))
+    q6 = bytes(g.integers(0, 256, 210 * 2, dtype=np.uint8))
+    x = g.standard_normal(7).astype(np.float32)
+    bf = (x.view(np.uint32) >> 16).astype(np.uint16)
+    tensors = [("w.q5", [256, 3], gw.GGML_Q5_K, q5), ("w.q6", [512], gw.GGML_Q6_K, q6),
+               ("n.bf", [7], gw.GGML_BF16, bf.tobytes())]
+    f = hip.GgufFile(write(tmp_path, gw.build([], tensors)))
+    for i, (name, dims, gt, payload) in enumerate(tensors):
+        assert f.tensor(i) == (name, gt, dims, payload)
+    want = (bf.astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(f.read_f32("n.bf", 7).view(np.uint32), want.view(np.uint32))
+    with pytest.raises(hip.UnsupportedOp):
+        f.read_f32("w.q5", 768)

@@ -87,6 +87,12 @@ int kv_block_bytes(int mode) {
     }
 }
 
+// Super-block bytes of a K-quant weight dtype (gguf/tensor.rs:117-125), 0 if
+// the dtype is not a K-quant.
+size_t kq_block_bytes(int wd) {
+    return wd == VOKRA_HIP_W_Q4_K ? 144 : wd == VOKRA_HIP_W_Q5_K ? 176 : wd == VOKRA_HIP_W_Q6_K ? 210 : 0;
+}
+
 // Block-format weight dtype -> KvQuant discriminant used by the kernels.
 int wd_kv_mode(int wd) {
     switch (wd) {
@@ -163,7 +169,8 @@ struct vokra_hip_qweight {
     DevBuf frag, scale;  // MFMA-fragment bf16 integers + f32 scales (prefill GEMM)
     bool has_gemv = false;
     DevBuf gq, gsc;      // compact decode layout (Q4_0 / Q8_0, k % 128 == 0); Q4_K: nibble words + (d, m)
-    bool kquant = false; // Q4_K: one matmul kernel for every m
+    bool kquant = false; // K-quants: one matmul kernel for every m
+    int kfmt = 0;        // its weight layout: 0 nibble words (Q4_K), 1 byte words (Q5_K, Q6_K)
 };
 
 // Largest activation count routed to the decode kernel.
@@ -262,17 +269,17 @@ int quantize_activations(vokra_hip_ctx* c, vokra_hip_qact* qa, const float* d_a,
 
 int check_block_shapes(int wdtype, size_t n, size_t k, size_t wq_len) {
     const int mode = wd_kv_mode(wdtype);
-    if (wdtype == VOKRA_HIP_W_Q4_K) {
+    if (const size_t bb = kq_block_bytes(wdtype)) {
         // validate_gemv_i8 (crates/vokra-backend-cpu/src/kernels/kquant.rs:545-578)
         if (k == 0 || k % 256 != 0)
             return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
                         "K-quant INT8 GEMV needs k to be a positive multiple of 256, got %zu", k);
         size_t want;
-        if (!mul_ok(n, (k / 256) * 144, &want))
+        if (!mul_ok(n, (k / 256) * bb, &want))
             return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "K-quant weight byte-length overflow");
         if (wq_len != want)
             return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "K-quant weight payload is %zu bytes, want %zu (m=%zu rows x %zu)",
-                        wq_len, want, n, (k / 256) * 144);
+                        wq_len, want, n, (k / 256) * bb);
         if (n > (size_t)INT32_MAX / 2 || k > (size_t)INT32_MAX)
             return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32: dimension exceeds int32");
         return VOKRA_HIP_OK;
@@ -298,16 +305,26 @@ int upload_weight(vokra_hip_ctx* c, int wdtype, size_t n, size_t k, const uint8_
     w->wdtype = wdtype;
     w->n = n;
     w->k = k;
-    if (wdtype == VOKRA_HIP_W_Q4_K) {
+    if (kq_block_bytes(wdtype)) {
         const size_t nsb = k / 256;
         w->kquant = true;
         w->nb = nsb;
         w->n_pad = round_up(n ? n : 1, 16);
-        VK_TRY(w->gq.ensure(w->n_pad * nsb * 128), "hipMalloc(Q4_K nibble words)");
-        VK_TRY(w->gsc.ensure(w->n_pad * nsb * 8 * sizeof(float) * 2), "hipMalloc(Q4_K scales)");
-        VK_TRY(vk::launch_repack_w_q4k(c->stream, d_wq, (int)n, (int)w->n_pad, (int)nsb, (uint4*)w->gq.p,
-                                       (float2*)w->gsc.p),
-               "launch(vk_repack_w_q4k)");
+        if (wdtype == VOKRA_HIP_W_Q4_K) {
+            w->kfmt = 0;
+            VK_TRY(w->gq.ensure(w->n_pad * nsb * 128), "hipMalloc(Q4_K nibble words)");
+            VK_TRY(w->gsc.ensure(w->n_pad * nsb * 8 * sizeof(float) * 2), "hipMalloc(Q4_K scales)");
+            VK_TRY(vk::launch_repack_w_q4k(c->stream, d_wq, (int)n, (int)w->n_pad, (int)nsb, (uint4*)w->gq.p,
+                                           (float2*)w->gsc.p),
+                   "launch(vk_repack_w_q4k)");
+        } else {
+            w->kfmt = 1;
+            VK_TRY(w->gq.ensure(w->n_pad * nsb * 256), "hipMalloc(K-quant byte words)");
+            VK_TRY(w->gsc.ensure(w->n_pad * nsb * 16 * sizeof(float) * 2), "hipMalloc(K-quant scales)");
+            VK_TRY(vk::launch_repack_w_kq8(c->stream, wdtype, d_wq, (int)n, (int)w->n_pad, (int)nsb, (uint4*)w->gq.p,
+                                           (float2*)w->gsc.p),
+                   "launch(vk_repack_w_kq8)");
+        }
         return VOKRA_HIP_OK;
     }
     w->nb = k / 32;
@@ -346,10 +363,11 @@ int run_gemm_qact(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_
                   float* d_out, VkEpi epi = {nullptr, 0}) {
     if (w->kquant) {
         if (qa->act_quant != VOKRA_HIP_ACT_KQUANT)
-            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: Q4_K weights need KQUANT activations");
+            return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: K-quant weights need KQUANT activations");
         const VkQ4kLin lin = {(const uint4*)w->gq.p, (const float2*)w->gsc.p, d_bias, d_out, epi, (int)w->n};
         VK_TRY(vk::launch_gemm_q4k(c->stream, (const uint4*)qa->frag.p, (const float*)qa->scale.p,
-                                   (const float*)qa->gsum.p, &lin, 1, (int)qa->m, (int)w->nb, (int)qa->m_pad),
+                                   (const float*)qa->gsum.p, &lin, 1, (int)qa->m, (int)w->nb, (int)qa->m_pad,
+                                   w->kfmt),
                "launch(vk_gemm_q4k)");
         return VOKRA_HIP_OK;
     }
@@ -586,7 +604,8 @@ int gemm_qact_multi(vokra_hip_ctx* c, int n, const vokra_hip_qweight* const* ws,
     }
     VK_TRY(set_dev(c), "hipSetDevice");
     bool q4k_all = qa->act_quant == VOKRA_HIP_ACT_KQUANT;
-    for (int i = 0; i < n && q4k_all; ++i) q4k_all = ws[i]->kquant && ws[i]->nb == ws[0]->nb;
+    for (int i = 0; i < n && q4k_all; ++i)
+        q4k_all = ws[i]->kquant && ws[i]->nb == ws[0]->nb && ws[i]->kfmt == ws[0]->kfmt;
     if (q4k_all && n > 1) {
         // K-quant linears over the same activations: one grid
         VkQ4kLin lins[3];
@@ -594,7 +613,8 @@ int gemm_qact_multi(vokra_hip_ctx* c, int n, const vokra_hip_qweight* const* ws,
             lins[i] = {(const uint4*)ws[i]->gq.p, (const float2*)ws[i]->gsc.p, biases ? biases[i] : nullptr, outs[i],
                        {nullptr, 0}, (int)ws[i]->n};
         VK_TRY(vk::launch_gemm_q4k(c->stream, (const uint4*)qa->frag.p, (const float*)qa->scale.p,
-                                   (const float*)qa->gsum.p, lins, n, (int)qa->m, (int)ws[0]->nb, (int)qa->m_pad),
+                                   (const float*)qa->gsum.p, lins, n, (int)qa->m, (int)ws[0]->nb, (int)qa->m_pad,
+                                   ws[0]->kfmt),
                "launch(vk_gemm_q4k x n)");
         return VOKRA_HIP_OK;
     }
@@ -1819,24 +1839,24 @@ int vokra_hip_dequantize_bytes(vokra_hip_ctx_t* c, int mode, const uint8_t* byte
 int vokra_hip_kquant_dequantize(vokra_hip_ctx_t* c, int wdtype, const uint8_t* bytes, size_t n_bytes,
                                 size_t n_elements, float* out) {
     if (!c) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kquant_dequantize: ctx is NULL");
-    if (wdtype != VOKRA_HIP_W_Q4_K)
-        return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "kquant_dequantize: dtype %d is not wired on this arm", wdtype);
+    const size_t bb = kq_block_bytes(wdtype);
+    if (!bb) return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "kquant_dequantize: dtype %d is not wired on this arm", wdtype);
     // GgmlType::payload_size + TensorSizeMismatch (gguf/quant/mod.rs:42-50)
     if (n_elements % 256 != 0)
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
-                    "Q4_K payload needs n_elements a multiple of 256, got %zu", n_elements);
+                    "K-quant payload needs n_elements a multiple of 256, got %zu", n_elements);
     const size_t nsb = n_elements / 256;
-    if (n_bytes != nsb * 144)
-        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "tensor <dequant 12>: expected %zu bytes, got %zu", nsb * 144,
-                    n_bytes);
+    if (n_bytes != nsb * bb)
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "tensor <dequant %d>: expected %zu bytes, got %zu", wdtype,
+                    nsb * bb, n_bytes);
     if (nsb == 0) return VOKRA_HIP_OK;
     if (!bytes || !out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "kquant_dequantize: NULL buffer");
     VK_TRY(set_dev(c), "hipSetDevice");
     VK_TRY(c->in0.ensure(n_bytes), "hipMalloc");
     VK_TRY(c->out0.ensure(n_elements * sizeof(float)), "hipMalloc");
     VK_TRY(hipMemcpyAsync(c->in0.p, bytes, n_bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
-    VK_TRY(vk::launch_dequantize_q4k(c->stream, (const uint8_t*)c->in0.p, nsb, (float*)c->out0.p),
-           "launch(vk_dequantize_q4k)");
+    VK_TRY(vk::launch_dequantize_kq(c->stream, wdtype, (const uint8_t*)c->in0.p, nsb, (float*)c->out0.p),
+           "launch(K-quant dequantize)");
     VK_TRY(hipMemcpyAsync(out, c->out0.p, n_elements * sizeof(float), hipMemcpyDeviceToHost, c->stream),
            "hipMemcpyAsync(D2H)");
     VK_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
@@ -1949,7 +1969,7 @@ int vokra_hip_gemm_q_f32_dev(vokra_hip_ctx_t* c, const vokra_hip_qweight_t* w, s
     if (act_quant != VOKRA_HIP_ACT_AMAX127 && act_quant != VOKRA_HIP_ACT_POW2 && act_quant != VOKRA_HIP_ACT_KQUANT)
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: unknown activation convention %d", act_quant);
     if (act_quant == VOKRA_HIP_ACT_KQUANT && !w->kquant)
-        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: KQUANT activations need Q4_K weights");
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: KQUANT activations need K-quant weights");
     if (!d_a || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev: NULL buffer");
     VK_TRY(set_dev(c), "hipSetDevice");
     return run_gemm(c, w, m, d_a, d_bias, d_out, act_quant);
@@ -1967,7 +1987,7 @@ int vokra_hip_gemm_q_f32_dev_noalloc(vokra_hip_ctx_t* c, const vokra_hip_qweight
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev_noalloc: unknown activation convention %d",
                     act_quant);
     if (act_quant == VOKRA_HIP_ACT_KQUANT && !w->kquant)
-        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev_noalloc: KQUANT activations need Q4_K weights");
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev_noalloc: KQUANT activations need K-quant weights");
     if (!d_a || !d_out) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_q_f32_dev_noalloc: NULL buffer");
     // the workspace regions of qact_reserve(m, k), 256-byte aligned, in the static array
     const size_t k = w->k;

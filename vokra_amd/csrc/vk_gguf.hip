@@ -7,8 +7,9 @@
 // offset), then the data region at the next multiple of general.alignment
 // (default 32); every tensor offset is a multiple of it and its payload lies
 // inside the file. The checks and their order follow the reference reader;
-// the accepted tensor types are the ones this library computes with: F32 (0),
-// F16 (1), Q4_0 (2), Q5_0 (6), Q8_0 (8), Q4_K (12). The reference itself
+// the accepted tensor types are the reference's (F32 0, F16 1, Q4_K 12, Q5_K
+// 13, Q6_K 14, BF16 30; tensor.rs:85-95) and the block formats this library
+// also computes with: Q4_0 (2), Q5_0 (6), Q8_0 (8). The reference itself
 // rejects Q4_0 / Q5_0 / Q8_0 (crates/vokra-core/src/gguf/tensor.rs:85-95);
 // loading them is the block-format route its Whisper loader names
 // (crates/vokra-models/src/whisper/weights.rs:454-509).
@@ -71,6 +72,9 @@ bool type_geometry(uint32_t t, uint64_t* block_elems, uint64_t* block_bytes) {
     case 6: *block_elems = 32; *block_bytes = 22; return true;    // Q5_0
     case 8: *block_elems = 32; *block_bytes = 34; return true;    // Q8_0
     case 12: *block_elems = 256; *block_bytes = 144; return true; // Q4_K
+    case 13: *block_elems = 256; *block_bytes = 176; return true; // Q5_K
+    case 14: *block_elems = 256; *block_bytes = 210; return true; // Q6_K
+    case 30: *block_elems = 1; *block_bytes = 2; return true;     // BF16
     default: return false;
     }
 }
@@ -385,13 +389,21 @@ int vokra_hip_gguf_read_f32(const vokra_hip_gguf_t* f, const char* name, float* 
     if (!f || !name || (!out && out_len)) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gguf_read_f32: NULL argument");
     const Tensor* t = find(f, name);
     if (!t) return fail(VOKRA_HIP_ERROR_MODEL_LOAD, "gguf: missing tensor '%s'", name);
-    if (t->type != 0 && t->type != 1)
-        return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "gguf: tensor '%s' (ggml type %u) is not F32/F16", name, t->type);
+    if (t->type != 0 && t->type != 1 && t->type != 30)
+        return fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "gguf: tensor '%s' (ggml type %u) is not F32/F16/BF16", name, t->type);
     const size_t n = (size_t)t->nbytes / (t->type == 0 ? 4 : 2);
     if (out_len != n) return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gguf: tensor '%s' has %zu elements, not %zu", name, n, out_len);
     const uint8_t* p = f->base + f->data_offset + t->offset;
     if (t->type == 0) {
         memcpy(out, p, n * 4);
+    } else if (t->type == 30) {
+        // bf16 -> f32 is exact: the 16 bits become the high half
+        for (size_t i = 0; i < n; ++i) {
+            uint16_t h;
+            memcpy(&h, p + 2 * i, 2);
+            const uint32_t bits = (uint32_t)h << 16;
+            memcpy(out + i, &bits, 4);
+        }
     } else {
         for (size_t i = 0; i < n; ++i) {
             uint16_t h;
@@ -553,18 +565,19 @@ struct Loader {
         const Tensor* t;
         int st = shaped(name, want, &t);
         if (st) return st;
-        if (t->type == VOKRA_HIP_W_Q4_K) {
-            const size_t n = (size_t)t->nbytes / 144 * 256;
+        if (t->type == VOKRA_HIP_W_Q4_K || t->type == VOKRA_HIP_W_Q5_K || t->type == VOKRA_HIP_W_Q6_K) {
+            const size_t bb = t->type == VOKRA_HIP_W_Q4_K ? 144 : t->type == VOKRA_HIP_W_Q5_K ? 176 : 210;
+            const size_t n = (size_t)t->nbytes / bb * 256;
             floats.emplace_back(n);
-            if ((st = vokra_hip_kquant_dequantize(ctx, VOKRA_HIP_W_Q4_K, f->base + f->data_offset + t->offset,
+            if ((st = vokra_hip_kquant_dequantize(ctx, (int)t->type, f->base + f->data_offset + t->offset,
                                                   (size_t)t->nbytes, n, floats.back().data())))
                 return st;
             *out = floats.back().data();
             return VOKRA_HIP_OK;
         }
-        if (t->type != 0 && t->type != 1)
-            return tensor_err(vox, VOKRA_HIP_ERROR_UNSUPPORTED_OP, name, "ggml type %u where F32, F16 or Q4_K is needed",
-                              t->type);
+        if (t->type != 0 && t->type != 1 && t->type != 30)
+            return tensor_err(vox, VOKRA_HIP_ERROR_UNSUPPORTED_OP, name,
+                              "ggml type %u where F32, F16, BF16 or a K-quant is needed", t->type);
         const size_t n = (size_t)t->nbytes / (t->type == 0 ? 4 : 2);
         floats.emplace_back(n);
         if ((st = vokra_hip_gguf_read_f32(f, name.c_str(), floats.back().data(), n))) return st;
@@ -582,7 +595,8 @@ struct Loader {
         const Tensor* t;
         if ((st = shaped(wname, {outf, in}, &t))) return st;
         if ((int)t->type == wdtype) {
-            const size_t be = wdtype == VOKRA_HIP_W_Q4_K ? 256 : 32;
+            const size_t be = wdtype == VOKRA_HIP_W_Q4_K || wdtype == VOKRA_HIP_W_Q5_K || wdtype == VOKRA_HIP_W_Q6_K
+                                  ? 256 : 32;
             if (in % be)
                 return tensor_err(vox, VOKRA_HIP_ERROR_UNSUPPORTED_OP, wname,
                                   "in_features %zu is not a multiple of %zu, so a block would straddle two rows", in, be);
@@ -590,19 +604,32 @@ struct Loader {
             ++verbatim;
             return VOKRA_HIP_OK;
         }
-        const char* names[] = {"F32", "F16", "Q4_0", "", "", "", "Q5_0", "", "Q8_0", "", "", "", "Q4_K"};
+        auto names = [](uint32_t ty) -> const char* {
+            switch (ty) {
+            case 0: return "F32";
+            case 1: return "F16";
+            case 2: return "Q4_0";
+            case 6: return "Q5_0";
+            case 8: return "Q8_0";
+            case 12: return "Q4_K";
+            case 13: return "Q5_K";
+            case 14: return "Q6_K";
+            case 30: return "BF16";
+            default: return "?";
+            }
+        };
         const int mode = wdtype == VOKRA_HIP_W_Q8_0 ? VOKRA_HIP_KV_Q8_0
                          : wdtype == VOKRA_HIP_W_Q4_0 ? VOKRA_HIP_KV_Q4_0
                          : wdtype == VOKRA_HIP_W_Q5_0 ? VOKRA_HIP_KV_Q5_0 : -1;
-        if ((t->type != 0 && t->type != 1) || mode < 0)
+        if ((t->type != 0 && t->type != 1 && t->type != 30) || mode < 0)
             return tensor_err(vox, VOKRA_HIP_ERROR_UNSUPPORTED_OP, wname,
                               "%s on disk, and the session's %s weights cannot be made from it (same block dtype, or "
-                              "F32/F16 packed to Q8_0 / Q4_0 / Q5_0)",
-                              names[t->type], names[wdtype]);
+                              "F32/F16/BF16 packed to Q8_0 / Q4_0 / Q5_0)",
+                              names(t->type), names((uint32_t)wdtype));
         if (in % 32)
             return tensor_err(vox, VOKRA_HIP_ERROR_UNSUPPORTED_OP, wname,
                               "in_features %zu is not a multiple of 32, so its rows cannot be packed to %s blocks", in,
-                              names[wdtype]);
+                              names((uint32_t)wdtype));
         std::vector<float> x(in * outf);
         if ((st = vokra_hip_gguf_read_f32(f, wname.c_str(), x.data(), x.size()))) return st;
         const size_t bb = wdtype == VOKRA_HIP_W_Q8_0 ? 34 : wdtype == VOKRA_HIP_W_Q4_0 ? 18 : 22;
@@ -638,7 +665,8 @@ struct Loader {
 };
 
 bool whisper_wdtype(int w) {
-    return w == VOKRA_HIP_W_Q8_0 || w == VOKRA_HIP_W_Q4_0 || w == VOKRA_HIP_W_Q5_0 || w == VOKRA_HIP_W_Q4_K;
+    return w == VOKRA_HIP_W_Q8_0 || w == VOKRA_HIP_W_Q4_0 || w == VOKRA_HIP_W_Q5_0 || w == VOKRA_HIP_W_Q4_K ||
+           w == VOKRA_HIP_W_Q5_K || w == VOKRA_HIP_W_Q6_K;
 }
 
 }  // namespace

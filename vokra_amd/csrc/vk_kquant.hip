@@ -18,6 +18,8 @@
 // same roundings, so outputs are bit-identical to the reference.
 #include "vk_common.h"
 
+#include <type_traits>
+
 namespace vk {
 
 namespace kq {
@@ -62,6 +64,59 @@ __global__ void vk_dequantize_q4k(const uint8_t* __restrict__ bytes, size_t nsb,
     y[l + 1] = d1 * (float)(q1 & 15u) - mm1;
     y[32 + l] = d2 * (float)(q0 >> 4) - mm2;
     y[33 + l] = d2 * (float)(q1 >> 4) - mm2;
+}
+
+// Q5_K (crates/vokra-core/src/gguf/quant/q5_k.rs:36-80): Q4_K's layout with
+// 32 bytes of fifth bits before the nibbles (176 bytes); element 64c + l takes
+// qh[l] bit 2c, element 64c + 32 + l bit 2c + 1. One thread per 4 outputs.
+__global__ void vk_dequantize_q5k(const uint8_t* __restrict__ bytes, size_t nsb, float* __restrict__ out) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t sb = gid >> 6;
+    if (sb >= nsb) return;
+    const int t = (int)(gid & 63);
+    const uint8_t* blk = bytes + sb * 176;
+    const float d = vk_f16_to_f32(blk[0] | (blk[1] << 8));
+    const float dmin = vk_f16_to_f32(blk[2] | (blk[3] << 8));
+    const int c = t >> 4, l = (t & 15) * 2;
+    int sc0, m0, sc1, m1;
+    scale_min_k4(2 * c, blk + 4, sc0, m0);
+    scale_min_k4(2 * c + 1, blk + 4, sc1, m1);
+    const float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
+    const float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
+    const uint8_t* qh = blk + 16;
+    const uint32_t q0 = blk[48 + 32 * c + l], q1 = blk[48 + 32 * c + l + 1];
+    const uint32_t lo_bit = 1u << (2 * c), hi_bit = 2u << (2 * c);
+    float* y = out + sb * kq::QK + 64 * c;
+    y[l] = d1 * (float)((q0 & 15u) + ((qh[l] & lo_bit) ? 16u : 0u)) - mm1;
+    y[l + 1] = d1 * (float)((q1 & 15u) + ((qh[l + 1] & lo_bit) ? 16u : 0u)) - mm1;
+    y[32 + l] = d2 * (float)((q0 >> 4) + ((qh[l] & hi_bit) ? 16u : 0u)) - mm2;
+    y[33 + l] = d2 * (float)((q1 >> 4) + ((qh[l + 1] & hi_bit) ? 16u : 0u)) - mm2;
+}
+
+// Q6_K (crates/vokra-core/src/gguf/quant/q6_k.rs:34-72, 210 bytes): per
+// 128-element half, 64 bytes of low nibbles, 32 bytes of 2-bit high parts,
+// 8 int8 scales; y = d * sc * (q - 32) in that association. One thread per
+// (half, l): the four outputs l, l + 32, l + 64, l + 96 of the half.
+__global__ void vk_dequantize_q6k(const uint8_t* __restrict__ bytes, size_t nsb, float* __restrict__ out) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t sb = gid >> 6;
+    if (sb >= nsb) return;
+    const int t = (int)(gid & 63), half = t >> 5, l = t & 31;
+    const uint8_t* blk = bytes + sb * 210;
+    const float d = vk_f16_to_f32(blk[208] | (blk[209] << 8));
+    const uint8_t* ql = blk + 64 * half;
+    const uint8_t* qh = blk + 128 + 32 * half;
+    const int8_t* sc = reinterpret_cast<const int8_t*>(blk + 192 + 8 * half);
+    const int is = l / 16;
+    const int q1 = (int)((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32;
+    const int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+    const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+    const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+    float* y = out + sb * kq::QK + 128 * half;
+    y[l] = d * (float)sc[is] * (float)q1;
+    y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+    y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+    y[l + 96] = d * (float)sc[is + 6] * (float)q4;
 }
 
 // ---------------------------------------------------------------------------
@@ -277,6 +332,83 @@ __global__ void vk_repack_w_q4k(const uint8_t* __restrict__ wq, int n, int n_pad
     }
 }
 
+// Q5_K / Q6_K weights for the matmul (upload time), one thread per (weight
+// row = output column, super-block): the super-block unpacked as
+// unpack_block_i8 does (crates/vokra-backend-cpu/src/kernels/kquant.rs:
+// 332-407) to q in 0..31 (Q5_K) or the biased q6 + 32 in 0..63 (Q6_K), with
+// (d_eff, m_eff) per 16-element group: Q5_K's q45_sub_scales pair (d * sc,
+// dmin * m) repeated over a sub-block's two groups, Q6_K's d * sc (int8) in
+// q6_group_scales order and m_eff = d_eff * 32 (exact). Device layout per
+// (16-column tile nt, super-block sb):
+//   wq:  64 lanes x 64 bytes; lane l = col % 16 + 16 c holds 16 byte words,
+//        word g = K 4c, 4c+2, 4c+1, 4c+3 of group g;
+//   wdm: 16 groups x 16 columns of float2 (d_eff, m_eff).
+// Columns n..n_pad-1 are zero.
+__global__ void vk_repack_w_kq8(int wdtype, const uint8_t* __restrict__ wq, int n, int n_pad, int nsb,
+                                uint4* __restrict__ wq4, float2* __restrict__ wdm) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (size_t)n_pad * nsb) return;
+    const int col = (int)(gid / nsb), sb = (int)(gid % nsb);
+    const int nt = col >> 4, cl = col & 15;
+    const size_t tile = (size_t)nt * nsb + sb;
+    const bool live = col < n;
+    const int bb = wdtype == 13 ? 176 : 210;
+    const uint8_t* blk = wq + ((size_t)(live ? col : 0) * nsb + sb) * bb;
+    uint8_t q[256];
+    float de[16], me[16];
+    if (!live) {
+        for (int e = 0; e < 256; ++e) q[e] = 0;
+        for (int g = 0; g < 16; ++g) de[g] = me[g] = 0.0f;
+    } else if (wdtype == 13) {
+        const float d = vk_f16_to_f32(blk[0] | (blk[1] << 8));
+        const float dmin = vk_f16_to_f32(blk[2] | (blk[3] << 8));
+        const uint8_t *qh = blk + 16, *qs = blk + 48;
+        for (int j = 0; j < 8; ++j) {
+            int sc, mn;
+            scale_min_k4(j, blk + 4, sc, mn);
+            de[2 * j] = de[2 * j + 1] = d * (float)sc;
+            me[2 * j] = me[2 * j + 1] = dmin * (float)mn;
+            const int chunk = j / 2, hi = j % 2;
+            for (int t = 0; t < 32; ++t) {
+                const uint8_t byte = qs[32 * chunk + t];
+                uint8_t v = hi ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 0xF);
+                if (qh[t] & (1u << j)) v = (uint8_t)(v + 16);
+                q[32 * j + t] = v;
+            }
+        }
+    } else {
+        const float d = vk_f16_to_f32(blk[208] | (blk[209] << 8));
+        const int8_t* sc = reinterpret_cast<const int8_t*>(blk + 192);
+        for (int half = 0; half < 2; ++half)
+            for (int quarter = 0; quarter < 4; ++quarter)
+                for (int sub = 0; sub < 2; ++sub) {
+                    const int g = 8 * half + 2 * quarter + sub;  // (128 half + 32 quarter + 16 sub) / 16
+                    de[g] = d * (float)sc[8 * half + sub + 2 * quarter];
+                    me[g] = de[g] * 32.0f;
+                }
+        for (int half = 0; half < 2; ++half) {
+            const uint8_t *ql = blk + 64 * half, *qh = blk + 128 + 32 * half;
+            uint8_t* y = q + 128 * half;
+            for (int l = 0; l < 32; ++l) {
+                y[l] = (uint8_t)((ql[l] & 0xF) | ((qh[l] & 3) << 4));
+                y[l + 32] = (uint8_t)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4));
+                y[l + 64] = (uint8_t)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4));
+                y[l + 96] = (uint8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4));
+            }
+        }
+    }
+    for (int c = 0; c < 4; ++c) {
+        uint32_t w[16];
+        for (int g = 0; g < 16; ++g) {
+            const uint8_t* e = q + 16 * g + 4 * c;
+            w[g] = (uint32_t)e[0] | ((uint32_t)e[2] << 8) | ((uint32_t)e[1] << 16) | ((uint32_t)e[3] << 24);
+        }
+        uint4* dst = wq4 + (tile * 64 + cl + 16 * c) * 4;
+        for (int h = 0; h < 4; ++h) dst[h] = make_uint4(w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]);
+    }
+    for (int g = 0; g < 16; ++g) wdm[(tile * 16 + g) * 16 + cl] = make_float2(de[g], me[g]);
+}
+
 // bf16 operand (4 values, K 4c..4c+3 of one group) from a nibble word:
 // pairs j0 and j0 + 1. mask = 0x000F000F and magic = 0x43004300 come in
 // registers, so each half is one v_and_or_b32 (a three-operand instruction
@@ -291,6 +423,24 @@ __device__ __forceinline__ vk_s16x4 q4k_operand(uint32_t w, int j0, uint32_t mas
     r.x = q4k_and_or(w >> (4 * j0), mask, magic);
     r.y = q4k_and_or(w >> (4 * j0 + 4), mask, magic);
     return __builtin_bit_cast(vk_s16x4, r);
+}
+
+// The B operand of group i (of the wave's 4): Q4_K from the nibble words;
+// Q5_K / Q6_K from a byte word holding K 4c, 4c+2, 4c+1, 4c+3 of the group,
+// so (w & 0x00ff00ff) | magic and ((w >> 8) & 0x00ff00ff) | magic are the
+// bf16 pairs (128 + q) of K 4c, 4c+1 and 4c+2, 4c+3 (q <= 63).
+template <int FMT, class W>
+__device__ __forceinline__ vk_s16x4 kq_operand(const W& wv, int i, uint32_t nib_mask, uint32_t byte_mask,
+                                               uint32_t magic) {
+    if constexpr (FMT == 0) {
+        return q4k_operand(i < 2 ? wv.x : wv.y, 2 * (i & 1), nib_mask, magic);
+    } else {
+        const uint32_t w = i == 0 ? wv.x : i == 1 ? wv.y : i == 2 ? wv.z : wv.w;
+        uint2 r;
+        r.x = q4k_and_or(w, byte_mask, magic);
+        r.y = q4k_and_or(w >> 8, byte_mask, magic);
+        return __builtin_bit_cast(vk_s16x4, r);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -335,11 +485,14 @@ __device__ __forceinline__ vk_s16x4 q4k_operand(uint32_t w, int j0, uint32_t mas
 namespace kq {
 constexpr int CHG = 32;  // groups per chunk (two super-blocks)
 constexpr int CHS = 2;   // super-blocks per chunk
+template <int FMT>
 struct Pipe {
-    uint2 wv;            // nibble words of this wave's 4 groups
+    // FMT 0 (Q4_K): nibble words of this wave's 4 groups; FMT 1 (Q5_K,
+    // Q6_K): one byte word per group
+    typename std::conditional<FMT == 0, uint2, uint4>::type wv;
     uint4 af[2];         // activation fragments of its 4 groups (2 pairs)
     float s, a;          // one of the DPP row's 16 scales / group sums
-    float2 dm[2];        // [sub-block]: (d_eff, m_eff) of this lane's column
+    float2 dm[FMT == 0 ? 2 : 4];  // (d_eff, m_eff) of this lane's column: per sub-block / per group
 };
 // lane J of each 16-lane row, to every lane of that row
 template <int J>
@@ -348,6 +501,7 @@ __device__ __forceinline__ float row_bcast(float x) {
 }
 }  // namespace kq
 
+template <int FMT>
 __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afrag, const float* __restrict__ ascale,
                                                    const float* __restrict__ asum, VkQ4kSet set, int m, int nsb,
                                                    int m_pad) {
@@ -369,7 +523,7 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
     const bool owner = wave >= 8;
 
     // per-lane byte offsets (constant over the K loop)
-    const uint32_t vo_w = lane * 32 + 8 * q4;
+    const uint32_t vo_w = FMT == 0 ? lane * 32 + 8 * q4 : lane * 64 + 16 * q4;
     const uint32_t vo_a = lane * 16;
     const uint32_t vo_d = (lane & 15) * 8;
     const uint32_t vo_s = (uint32_t)(mt * 16) * 16 + lane * 4;
@@ -379,8 +533,10 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
     // scalar unit, so no vector instruction forms an address in the K loop.
     const int n_pad = (L.n + 15) & ~15;
     const int rsrc_w3 = 0x00020000;  // raw (unswizzled) dword access
-    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)L.wq4, 0, n_pad * nsb * 128, rsrc_w3);
-    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)L.wdm, 0, n_pad * nsb * 64, rsrc_w3);
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void*)L.wq4, 0, n_pad * nsb * (FMT == 0 ? 128 : 256), rsrc_w3);
+    const __amdgpu_buffer_rsrc_t rd =
+        __builtin_amdgcn_make_buffer_rsrc((void*)L.wdm, 0, n_pad * nsb * (FMT == 0 ? 64 : 128), rsrc_w3);
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)afrag, 0, m_pad * nsb * 512, rsrc_w3);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)ascale, 0, m_pad * nsb * 64, rsrc_w3);
     const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc((void*)asum, 0, m_pad * nsb * 64, rsrc_w3);
@@ -389,17 +545,22 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
 
     // chunk c's operands for this wave (super-block 2c + sbw, clamped into
     // the tensor: a super-block past the end loads the last one, unused).
-    auto load = [&](int c) -> Pipe {
-        Pipe p;
+    auto load = [&](int c) -> Pipe<FMT> {
+        Pipe<FMT> p;
         const int sb = min(c * CHS + sbw, nsb - 1);
-        const int ow = ((nt * nsb + sb) * 64) * 32;
+        const int ow = ((nt * nsb + sb) * 64) * (FMT == 0 ? 32 : 64);
         const int oa = (((mt * nsb + sb) * 8 + 2 * q4) * 64) * 16;
         // scales / sums of groups 4 q4 .. +3 of rows mt*16 .. +15: 256 bytes,
         // lane 16 k + j holding row 4 k + j / 4, group j % 4
         const int os = (sb * (NG / 4) + q4) * m_pad * 16;
-        const int od = ((nt * nsb + sb) * 8 + 2 * q4) * 128;
-        const vk_u32x2 w2 = __builtin_amdgcn_raw_buffer_load_b64(rw, vo_w, ow, 0);
-        p.wv = make_uint2(w2.x, w2.y);
+        const int od = FMT == 0 ? ((nt * nsb + sb) * 8 + 2 * q4) * 128 : ((nt * nsb + sb) * 16 + 4 * q4) * 128;
+        if constexpr (FMT == 0) {
+            const vk_u32x2 w2 = __builtin_amdgcn_raw_buffer_load_b64(rw, vo_w, ow, 0);
+            p.wv = make_uint2(w2.x, w2.y);
+        } else {
+            const vk_u32x4 w4 = __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, ow, 0);
+            p.wv = make_uint4(w4.x, w4.y, w4.z, w4.w);
+        }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const vk_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(ra, vo_a + h * 1024, oa, 0);
@@ -408,7 +569,7 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
         p.s = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vo_s, os, 0));
         p.a = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, vo_s, os, 0));
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
+        for (int jj = 0; jj < (FMT == 0 ? 2 : 4); ++jj) {
             const vk_u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rd, vo_d + jj * 128, od, 0);
             p.dm[jj] = make_float2(__uint_as_float(x.x), __uint_as_float(x.y));
         }
@@ -421,10 +582,11 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
     // forms the MFMA's accumulator input from taking its DPP operand
     float m128;
     asm volatile("v_mov_b32 %0, 0xc3000000" : "=v"(m128));
-    uint32_t nib_mask, nib_magic;
+    uint32_t nib_mask, byte_mask, nib_magic;
     asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(nib_mask));
+    asm volatile("v_mov_b32 %0, 0x00ff00ff" : "=v"(byte_mask));
     asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(nib_magic));
-    auto terms = [&](const Pipe& p, int par) {
+    auto terms = [&](const Pipe<FMT>& p, int par) {
         vk_f32x4 isum[4];
         // a second register with the sums, so the accumulator inputs and the
         // terms read them through separate DPP operands (one shared
@@ -435,7 +597,7 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
         // DPP row k
 #define VK_Q4K_MFMA(i)                                                                                          \
         {                                                                                                       \
-            const vk_s16x4 w = q4k_operand((i) < 2 ? p.wv.x : p.wv.y, 2 * ((i) & 1), nib_mask, nib_magic);      \
+            const vk_s16x4 w = kq_operand<FMT>(p.wv, i, nib_mask, byte_mask, nib_magic);                      \
             const uint4 a4 = p.af[(i) >> 1];                                                                    \
             const uint2 ap = ((i) & 1) ? make_uint2(a4.z, a4.w) : make_uint2(a4.x, a4.y);                       \
             const vk_f32x4 cin = {row_bcast<(i)>(ac) * m128, row_bcast<4 + (i)>(ac) * m128,                      \
@@ -451,7 +613,7 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
         float x[4][4], y[4][4];
 #define VK_Q4K_STEP1(i)                                                                                         \
         {                                                                                                       \
-            const float2 dm = p.dm[(i) >> 1];                                                                   \
+            const float2 dm = p.dm[FMT == 0 ? (i) >> 1 : (i)];                                                  \
             x[i][0] = dm.x * isum[i][0]; x[i][1] = dm.x * isum[i][1];                                           \
             x[i][2] = dm.x * isum[i][2]; x[i][3] = dm.x * isum[i][3];                                           \
             y[i][0] = dm.y * row_bcast<(i)>(p.a); y[i][1] = dm.y * row_bcast<4 + (i)>(p.a);                     \
@@ -501,7 +663,7 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
     int c0;
     asm volatile("s_mov_b32 %0, -2" : "=s"(c0));
     if (!owner) {
-        Pipe pa{}, pb{};
+        Pipe<FMT> pa{}, pb{};
         for (int c = c0; c < n_chunk; c += 2) {
             if (c >= 0) terms(pa, 0);  // chunk c
             pa = load(c + 2);
@@ -536,6 +698,27 @@ hipError_t launch_dequantize_q4k(hipStream_t s, const uint8_t* bytes, size_t nsb
     if (nsb == 0) return hipSuccess;
     const size_t threads = nsb * 64;
     hipLaunchKernelGGL(vk_dequantize_q4k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, bytes, nsb, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequantize_kq(hipStream_t s, int wdtype, const uint8_t* bytes, size_t nsb, float* out) {
+    if (nsb == 0) return hipSuccess;
+    const size_t threads = nsb * 64;
+    const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+    if (wdtype == 12) hipLaunchKernelGGL(vk_dequantize_q4k, grid, block, 0, s, bytes, nsb, out);
+    else if (wdtype == 13) hipLaunchKernelGGL(vk_dequantize_q5k, grid, block, 0, s, bytes, nsb, out);
+    else if (wdtype == 14) hipLaunchKernelGGL(vk_dequantize_q6k, grid, block, 0, s, bytes, nsb, out);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_repack_w_kq8(hipStream_t s, int wdtype, const uint8_t* wq, int n, int n_pad, int nsb, uint4* wq4,
+                               float2* wdm) {
+    if (wdtype != 13 && wdtype != 14) return hipErrorInvalidValue;
+    const size_t threads = (size_t)n_pad * nsb;
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_repack_w_kq8, dim3((unsigned)((threads + 63) / 64)), dim3(64), 0, s, wdtype, wq, n, n_pad,
+                       nsb, wq4, wdm);
     return hipGetLastError();
 }
 
@@ -575,8 +758,8 @@ hipError_t launch_repack_w_q4k(hipStream_t s, const uint8_t* wq, int n, int n_pa
 }
 
 hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum,
-                           const VkQ4kLin* lins, int n_lin, int m, int nsb, int m_pad) {
-    if (n_lin < 1 || n_lin > 3) return hipErrorInvalidValue;
+                           const VkQ4kLin* lins, int n_lin, int m, int nsb, int m_pad, int fmt) {
+    if (n_lin < 1 || n_lin > 3 || fmt < 0 || fmt > 1) return hipErrorInvalidValue;
     VkQ4kSet set{};
     int tiles = 0;
     for (int i = 0; i < n_lin; ++i) {
@@ -586,7 +769,10 @@ hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascal
     }
     set.count = n_lin;
     const dim3 grid((unsigned)tiles, (unsigned)((m + 15) / 16));
-    hipLaunchKernelGGL(vk_gemm_q4k, grid, dim3(768), 0, s, afrag, ascale, asum, set, m, nsb, m_pad);
+    if (fmt == 0)
+        hipLaunchKernelGGL(vk_gemm_q4k<0>, grid, dim3(768), 0, s, afrag, ascale, asum, set, m, nsb, m_pad);
+    else
+        hipLaunchKernelGGL(vk_gemm_q4k<1>, grid, dim3(768), 0, s, afrag, ascale, asum, set, m, nsb, m_pad);
     return hipGetLastError();
 }
 

@@ -123,7 +123,12 @@ hipError_t launch_quantize_act_g16(hipStream_t s, const float* a, int m, int m_p
 hipError_t launch_repack_w_q4k(hipStream_t s, const uint8_t* wq, int n, int n_pad, int nsb, uint4* wq4,
                                float2* wdm);
 hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum,
-                           const VkQ4kLin* lins, int n_lin, int m, int nsb, int m_pad);
+                           const VkQ4kLin* lins, int n_lin, int m, int nsb, int m_pad, int fmt);
+// Q4_K / Q5_K / Q6_K (ggml tags 12 / 13 / 14) -> f32, bit-exact with gguf/quant.
+hipError_t launch_dequantize_kq(hipStream_t s, int wdtype, const uint8_t* bytes, size_t nsb, float* out);
+// Q5_K / Q6_K weights into the byte-word layout of the matmul's format 1.
+hipError_t launch_repack_w_kq8(hipStream_t s, int wdtype, const uint8_t* wq, int n, int n_pad, int nsb, uint4* wq4,
+                               float2* wdm);
 // RMSNorm + the K-quant activation pass, and SwiGLU + the activation pass, in
 // one launch each (bit-identical to vk_rms_norm_f32 / vk_swiglu_f32 followed by
 // vk_quantize_act_g16); m_pad = round_up(m, 16), k % 256 == 0.

@@ -52,6 +52,8 @@ size_t wire_bytes(int wdtype, size_t n, size_t k) {
     case VOKRA_HIP_W_Q5_0: return n * (k / 32) * 22;
     case VOKRA_HIP_W_Q8_0: return n * (k / 32) * 34;
     case VOKRA_HIP_W_Q4_K: return n * (k / 256) * 144;
+    case VOKRA_HIP_W_Q5_K: return n * (k / 256) * 176;
+    case VOKRA_HIP_W_Q6_K: return n * (k / 256) * 210;
     default: return 0;
     }
 }
@@ -106,7 +108,10 @@ int upload_vec(vokra_hip_ctx_t* c, DBuf& b, const float* h, size_t n, const char
     return b.upload(c, h, n * sizeof(float));
 }
 
-int act_of(int wdtype) { return wdtype == VOKRA_HIP_W_Q4_K ? VOKRA_HIP_ACT_KQUANT : VOKRA_HIP_ACT_AMAX127; }
+bool is_kquant(int wdtype) {
+    return wdtype == VOKRA_HIP_W_Q4_K || wdtype == VOKRA_HIP_W_Q5_K || wdtype == VOKRA_HIP_W_Q6_K;
+}
+int act_of(int wdtype) { return is_kquant(wdtype) ? VOKRA_HIP_ACT_KQUANT : VOKRA_HIP_ACT_AMAX127; }
 
 int check_model_dims(int wdtype, size_t d, size_t n_head, size_t d_ff) {
     if (wire_bytes(wdtype, 1, 256) == 0) return vk::ctx_fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "session: unknown weight dtype");
@@ -114,7 +119,7 @@ int check_model_dims(int wdtype, size_t d, size_t n_head, size_t d_ff) {
         return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "session: d_model must be a multiple of n_head");
     const size_t hd = d / n_head;
     if (hd != 64 && hd != 128) return vk::ctx_fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "session: head_dim must be 64 or 128");
-    const size_t q = wdtype == VOKRA_HIP_W_Q4_K ? 256 : 32;
+    const size_t q = is_kquant(wdtype) ? 256 : 32;
     if (d % q != 0 || d_ff % q != 0 || !d_ff)
         return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "session: d_model and d_ff must be multiples of the quant block");
     return VOKRA_HIP_OK;
@@ -996,7 +1001,7 @@ int vokra_hip_text_decoder_create(vokra_hip_ctx_t* c, int wdtype, size_t n_layer
                             "text_decoder_create: query heads per kv head must be 1, 2, 4 or 8");
     if (wire_bytes(wdtype, 1, 256) == 0)
         return vk::ctx_fail(VOKRA_HIP_ERROR_UNSUPPORTED_OP, "text_decoder_create: unknown weight dtype");
-    const size_t qb = wdtype == VOKRA_HIP_W_Q4_K ? 256 : 32;
+    const size_t qb = is_kquant(wdtype) ? 256 : 32;
     if (d_model % qb || ffn_dim % qb || !ffn_dim || (n_head_q * head_dim) % qb || (n_head_kv * head_dim) % 32)
         return vk::ctx_fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT,
                             "text_decoder_create: d_model, ffn_dim and n_head_q * head_dim must be multiples of the "

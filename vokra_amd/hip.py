@@ -68,6 +68,8 @@ class WDtype(IntEnum):
     Q5_0 = 6
     Q8_0 = 8
     Q4_K = 12
+    Q5_K = 13
+    Q6_K = 14
 
 
 class ActQuant(IntEnum):
