@@ -835,9 +835,12 @@ bool paged_attn_rotates_q(const vokra_hip_kv* kv, size_t n, size_t hq, const flo
 
 int paged_attn_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                         const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
-                        vokra_hip_qact* qa, int act_quant, const float2* rope_cs) {
+                        vokra_hip_qact* qa, int act_quant, const float2* rope_cs, const float* d_ak,
+                        const float* d_av, const int* d_at) {
     if (rope_cs && act_quant != VOKRA_HIP_ACT_KQUANT)
         return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn_quantize: the fused rotation needs K-quant activations");
+    if (d_ak && (!d_av || !d_at || act_quant != VOKRA_HIP_ACT_KQUANT))
+        return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn_quantize: the fused append needs K, V, times and K-quant activations");
     if (act_quant == VOKRA_HIP_ACT_KQUANT && kv && kv->ctx == c) {
         // the K-quant activation pass runs inside the split combine (or as
         // its own launch when no item splits)
@@ -853,8 +856,8 @@ int paged_attn_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t
         const VkQOut qo{(uint4*)qa->frag.p, (float*)qa->scale.p, (float*)qa->gsum.p, (int)m_pad, (int)k, 0, 1};
         if (rope_cs && !paged_attn_rotates_q(kv, n, hq, d_q, d_out))
             return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "paged_attn_quantize: no fused rotation for this shape");
-        st = run_paged_attn(c, kv, layer, n, d_streams, d_lens, max_len, hq, d_q, scale, d_out, &qo, nullptr,
-                            nullptr, nullptr, rope_cs);
+        st = run_paged_attn(c, kv, layer, n, d_streams, d_lens, max_len, hq, d_q, scale, d_out, &qo, d_ak, d_av,
+                            d_at, rope_cs);
         if (st) return st;
         qa->m = n;
         qa->k = k;

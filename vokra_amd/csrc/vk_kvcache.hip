@@ -748,7 +748,9 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
                                                          float scale, int hq, int n_split,
                                                          float* __restrict__ out, float* __restrict__ part_ml,
                                                          float* __restrict__ part_o,
-                                                         const float2* __restrict__ rope_cs) {
+                                                         const float2* __restrict__ rope_cs,
+                                                         const float* __restrict__ ak, const float* __restrict__ av,
+                                                         const int* __restrict__ at) {
     using namespace pg;
     static_assert(G >= 2 && G <= 16, "query heads per kv head");
     __shared__ __align__(16) _Float16 lvt[WAVES][HD][VROW];  // per wave: V^T of its tile (reused by the merge)
@@ -762,6 +764,44 @@ __global__ __launch_bounds__(256, 2) void vk_paged_attn_gqa(KvDev c, int layer, 
     const int kps = pa_kps(len), nsp = pa_splits(len);
     if (split >= nsp) return;  // uniform per workgroup, before any barrier
     const int k0 = split * kps, k1 = min(len, k0 + kps);
+
+    // Fused append (ak != null): the workgroup whose key range holds the
+    // item's new step packs that step's K and V head slices into the cache
+    // (the page comes from an earlier allocation launch), exactly as
+    // vk_kv_write_allocated would: with rope_cs, k is rotated first (lane e
+    // holds the pair e, e + 64 of the head). Wave 0 writes K, wave 1 V; the
+    // tile loads below read the row back.
+    if (ak) {
+        const int t = at[item];
+        if (t >= k0 && t < k1) {  // uniform per workgroup
+            const int pid = c.table[layer * c.ppl + t / c.bs];
+            if (pid >= 0 && wave < 2) {
+                const size_t hr = kv_hrow(c, pid, t, s, hk);
+                const float* src = (wave == 0 ? ak : av) + (size_t)item * c.width + (size_t)hk * HD;
+                float lo = src[lane], hi = src[lane + HD / 2];
+                if (wave == 0 && rope_cs) {
+                    const float2 cs = rope_cs[(size_t)item * (HD / 2) + lane];
+                    const float a = lo, b = hi;
+                    lo = vk_rope_lo(a, b, cs);
+                    hi = vk_rope_hi(a, b, cs);
+                }
+                int8_t* dq = (wave == 0 ? c.kq : c.vq) + hr * HD;
+                uint16_t* dd = (wave == 0 ? c.kd : c.vd) + hr * NB;
+                int8_t qlo, qhi;
+                uint16_t dlo = 0, dhi = 0;
+                q8_0_pack_lane(lo, lane & 31, &qlo, &dlo);
+                q8_0_pack_lane(hi, lane & 31, &qhi, &dhi);
+                dq[lane] = qlo;
+                dq[lane + HD / 2] = qhi;
+                if ((lane & 31) == 0) {
+                    dd[lane >> 5] = dlo;
+                    dd[2 + (lane >> 5)] = dhi;
+                }
+            }
+            __threadfence_block();
+            __syncthreads();
+        }
+    }
 
     // q * scale of head hh (zero for padding heads) as the S^T B operand:
     // lane (g, hh) holds dims 32b + 8g .. +7, split into fp16 hi + lo. With
@@ -1223,8 +1263,8 @@ hipError_t launch_kv_page_of(hipStream_t s, const KvView& v, int layer, int t, i
 }
 
 // Returns whether the kernel that ran also quantized the output (qo). A fused
-// append (ak) runs only in the generic kernel: the caller routes by
-// paged_attn_fuses_append.
+// append (ak) runs in either kernel; the rotation of the appended k (rope_cs)
+// only in the matrix-core one.
 template <int HD, int G>
 static bool go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* streams, const int* lens,
                   const float* q, float scale, int hq, int hkv, int n_split, float* out, float* pml,
@@ -1237,9 +1277,9 @@ static bool go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* st
     const bool aligned = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out) |
                            reinterpret_cast<uintptr_t>(po)) & 15) == 0;
     if constexpr (HD == pg::HD && G >= 2) {
-        if (small_slots && aligned && !ak) {
+        if (small_slots && aligned) {
             hipLaunchKernelGGL((vk_paged_attn_gqa<G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams,
-                               lens, q, scale, hq, n_split, out, pml, po, rope_cs);
+                               lens, q, scale, hq, n_split, out, pml, po, rope_cs, ak, av, at);
             return false;
         }
     }
@@ -1269,8 +1309,8 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
                              const int* at, const float2* rope_cs) {
     const KvDev c = kv_view(v);
     const int hkv = v.width / hd, g = hq / hkv;
-    // the rotation of q rides only on the matrix-core GQA kernel
-    if (rope_cs && (ak || !paged_attn_rotates_q(v, hq, hd, q, out, part_o))) return hipErrorInvalidValue;
+    // the rotation of q (and of an appended k) rides only on the matrix-core GQA kernel
+    if (rope_cs && !paged_attn_rotates_q(v, hq, hd, q, out, part_o)) return hipErrorInvalidValue;
     const VkQOut qz = qo ? *qo : VkQOut{};
     const VkQOut qb = qz.g16 ? VkQOut{} : qz;  // the split kernels' own fused pass is the 32-wide one
     bool fused = false;

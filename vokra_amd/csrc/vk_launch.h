@@ -333,7 +333,12 @@ int attn_quantize_split(vokra_hip_ctx* c, size_t batch, size_t t, size_t h, size
                         float* d_out, vokra_hip_qact* qa, int act_quant);
 int paged_attn_quantize(vokra_hip_ctx* c, vokra_hip_kv* kv, size_t layer, size_t n, const int* d_streams,
                         const int* d_lens, size_t max_len, size_t hq, const float* d_q, float scale, float* d_out,
-                        vokra_hip_qact* qa, int act_quant, const float2* rope_cs = nullptr);
+                        vokra_hip_qact* qa, int act_quant, const float2* rope_cs = nullptr,
+                        const float* d_ak = nullptr, const float* d_av = nullptr, const int* d_at = nullptr);
+// With d_ak / d_av / d_at (K-quant activations only): the items' K / V rows
+// at times d_at are first packed into pages an earlier kv_alloc_layers gave,
+// k rotated by rope_cs when given, inside the attention launch (= a
+// kv_write_allocated before it).
 // Whether paged_attn_quantize can rotate q itself for this cache and buffers.
 bool paged_attn_rotates_q(const vokra_hip_kv* kv, size_t n, size_t hq, const float* d_q, const float* d_out);
 //   kv_alloc_layers + paged_attn_append_quantize (one per layer, in layer

@@ -906,7 +906,7 @@ int td_step(vokra_hip_text_decoder* m, size_t n, const int* d_streams, const int
     for (size_t l0 = 0, per = std::max<size_t>(1, 4096 / n); l0 < m->n_layer; l0 += per)
         SS_TRY(vk::kv_alloc_layers(c, m->kv, 0, l0, std::min(per, m->n_layer - l0), n, d_streams, d_positions));
     const VkEpi add_h = {m->h.f(), 0};
-    // RoPE fused into the K/V cache write (k) and the GQA kernel's q load: one
+    // RoPE fused into the GQA kernel's K/V cache write (k) and q load: one
     // (cos, sin) table for the step's positions serves every layer
     const bool rope_fused =
         act == VOKRA_HIP_ACT_KQUANT && vk::paged_attn_rotates_q(m->kv, n, m->hq, m->q.f(), m->attn.f());
@@ -928,9 +928,13 @@ int td_step(vokra_hip_text_decoder* m, size_t n, const int* d_streams, const int
             SS_HIP(vk::launch_rope_rows_qk(s, m->q.f(), m->k.f(), (int)n, (int)m->hq, (int)m->hkv, (int)m->hd,
                                            m->theta.f(), d_positions),
                    "launch(vk_rope_rows_qk)");
-        SS_TRY(vk::kv_write_allocated(c, m->kv, l, n, d_streams, d_positions, m->k.f(), m->v.f(), cs));
+        // with the fused rotation the attention launch also packs this step's
+        // K / V rows into the cache
+        if (!rope_fused)
+            SS_TRY(vk::kv_write_allocated(c, m->kv, l, n, d_streams, d_positions, m->k.f(), m->v.f(), nullptr));
         SS_TRY(vk::paged_attn_quantize(c, m->kv, l, n, d_streams, m->lens.i(), m->n_ctx, m->hq, m->q.f(), m->scale,
-                                       m->attn.f(), m->qa_q, act, cs));
+                                       m->attn.f(), m->qa_q, act, cs, rope_fused ? m->k.f() : nullptr,
+                                       rope_fused ? m->v.f() : nullptr, rope_fused ? d_positions : nullptr));
         SS_TRY(L.o.run(c, m->qa_q, m->h.f(), add_h));
         // pre-norm SwiGLU FFN (text_decoder.rs:1385-1418)
         SS_TRY(td_rms_quantize(m, m->qa_d, n, m->h.f(), L.ffn_g.f()));
