@@ -832,7 +832,7 @@ def main():
     ap.add_argument("--only", default=None,
                     help="comma list of single legs to run, one JSON line each (for profiling): "
                          "gemm, gemm_pow2, copy, gemv, q4k, sdpa, paged, encoder, decoder, textdec, frontend, "
-                         "logits")
+                         "logits, decoder_l2, textdec_l2 (2-layer steps for counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -855,6 +855,11 @@ def main():
             "encoder": lambda: [bench_encoder(ctx, hip, 1), bench_encoder(ctx, hip, 16)],
             "decoder": lambda: bench_decoder(ctx, hip),
             "textdec": lambda: bench_text_decoder(ctx, hip),
+            # the two steps' per-layer kernels at their full shapes over 2
+            # layers and short prefixes: a fast leg for counter runs (each
+            # kernel's dispatches are those of the full legs)
+            "decoder_l2": lambda: bench_decoder(ctx, hip, n_layer=2, max_prefix=16),
+            "textdec_l2": lambda: bench_text_decoder(ctx, hip, n_layer=2),
             "frontend": lambda: bench_frontend(ctx, hip),
             "logits": lambda: bench_logits(ctx, hip),
         }

@@ -451,10 +451,11 @@ __device__ __forceinline__ vk_s16x4 kq_operand(const W& wv, int i, uint32_t nib_
 // gsum) over the groups in order. Only the final add is a dependent chain;
 // the term t = s * (d_eff * isum - m_eff * gsum) (four roundings) depends on
 // one group alone. So:
-//   phase 1 (chunk c): wave w takes 4 groups of the chunk; per group one
-//     16x16x16 MFMA with accumulator input -128 * gsum (removing the +128 of
-//     the bf16 nibble trick) gives isum exactly for 4 outputs per lane (the
-//     4 MFMAs are issued before any of their results is used), and the lane
+//   phase 1 (chunk c): wave w takes 4 groups of the chunk; per group two
+//     16x16x16 MFMAs, activations times a constant -128 (removing the +128
+//     of the bf16 nibble trick) and then times the (128 + q) weights, give
+//     isum exactly for 4 outputs per lane (the 8 MFMAs are issued before any
+//     of their results is used), and the lane
 //     turns them into the 4 terms with the reference's roundings; the terms
 //     go to the LDS buffer of chunk c;
 //   phase 2 (chunk c - 1): thread t of waves 8..11 adds the chunk's 32
@@ -578,34 +579,34 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
     // phase 1: the terms of this wave's 4 groups into buffer par (for a
     // super-block past the end the terms come from the clamped loads and
     // phase 2 never reads them)
-    // -128 in a register: a literal operand would keep the multiply that
-    // forms the MFMA's accumulator input from taking its DPP operand
-    float m128;
-    asm volatile("v_mov_b32 %0, 0xc3000000" : "=v"(m128));
+    // the bf16 pair (-128, -128)
+    uint32_t neg128_bf16;
+    asm volatile("v_mov_b32 %0, 0xc300c300" : "=v"(neg128_bf16));
     uint32_t nib_mask, byte_mask, nib_magic;
     asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(nib_mask));
     asm volatile("v_mov_b32 %0, 0x00ff00ff" : "=v"(byte_mask));
     asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(nib_magic));
     auto terms = [&](const Pipe<FMT>& p, int par) {
         vk_f32x4 isum[4];
-        // a second register with the sums, so the accumulator inputs and the
-        // terms read them through separate DPP operands (one shared
-        // broadcast copy would cost a move per use)
-        float ac;
-        asm volatile("v_mov_b32 %0, %1" : "=v"(ac) : "v"(p.a));
-        // group i: the scale and sum of row 4 k + r sit in lane 4 r + i of
-        // DPP row k
-#define VK_Q4K_MFMA(i)                                                                                          \
-        {                                                                                                       \
-            const vk_s16x4 w = kq_operand<FMT>(p.wv, i, nib_mask, byte_mask, nib_magic);                      \
-            const uint4 a4 = p.af[(i) >> 1];                                                                    \
-            const uint2 ap = ((i) & 1) ? make_uint2(a4.z, a4.w) : make_uint2(a4.x, a4.y);                       \
-            const vk_f32x4 cin = {row_bcast<(i)>(ac) * m128, row_bcast<4 + (i)>(ac) * m128,                      \
-                                  row_bcast<8 + (i)>(ac) * m128, row_bcast<12 + (i)>(ac) * m128};               \
-            isum[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(vk_s16x4, ap), w, cin, 0, 0, 0); \
+        // The accumulator input -128 * gsum of each output comes from the
+        // matrix core too: the product of the group's activations with a
+        // constant -128 operand (exact: integers below 2^24), so no VALU
+        // instruction forms it; the second product then adds the
+        // (128 + q) weights. Both MFMAs of all 4 groups are issued before
+        // any result is read.
+        const vk_s16x4 neg128 = __builtin_bit_cast(vk_s16x4, make_uint2(neg128_bf16, neg128_bf16));
+        vk_s16x4 aop[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 a4 = p.af[i >> 1];
+            aop[i] = __builtin_bit_cast(vk_s16x4, (i & 1) ? make_uint2(a4.z, a4.w) : make_uint2(a4.x, a4.y));
+            isum[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(aop[i], neg128, (vk_f32x4){0.0f, 0.0f, 0.0f, 0.0f},
+                                                                0, 0, 0);
         }
-        VK_Q4K_MFMA(0) VK_Q4K_MFMA(1) VK_Q4K_MFMA(2) VK_Q4K_MFMA(3)
-#undef VK_Q4K_MFMA
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            isum[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                aop[i], kq_operand<FMT>(p.wv, i, nib_mask, byte_mask, nib_magic), isum[i], 0, 0, 0);
         // The 16 terms of the wave's 4 groups breadth first, one rounding step
         // at a time over all of them (the issue order is pinned): each step's
         // 16 operations are independent, so no multiply waits on the one
