@@ -15,9 +15,10 @@
 //
 // The weight offsets (+128 on every element, and the Q4_0 nibble bias 8) are
 // removed through the MFMA accumulator input: C = -(128 + 8) * sum(A) for
-// Q4_0 and -128 * sum(A) for Q8_0, where sum(A) is the exact operand sum the
-// activation pass writes. Every product and partial sum is an integer (times
-// a power of two for POW2 activations) below 2^24, so D = P_b exactly.
+// Q4_0 and -128 * sum(A) for Q8_0, itself an MFMA of the activations with a
+// constant -136 / -128 operand (no per-row sums are read and no VALU forms
+// it). Every product and partial sum is an integer (times a power of two for
+// POW2 activations) below 2^24, so C and D = P_b are exact.
 #include "vk_common.h"
 
 #include <algorithm>
@@ -136,15 +137,18 @@ __global__ __launch_bounds__(256) void vk_gemv_qblock(
     const GemvSet set, const VkGemvLin* __restrict__ dlins, int m, int nb, int m_pad) {
     using namespace gemv;
     const VkGemvLin lin = DEV ? dlins[blockIdx.z] : set.lin[blockIdx.z];
+    (void)asum;  // the operand sums come from the matrix core (OFFW below)
     const uint4* __restrict__ wq4 = lin.wq4;
     const uint2* __restrict__ wsc = lin.wsc;
     const int n = lin.n;
     if ((int)blockIdx.x * 16 >= n) return;  // this linear has fewer column tiles (whole workgroup)
     constexpr int WQ = MODE == 1 ? 1 : 2;  // weight uint4 per lane per group
-    constexpr float OFFSET = MODE == 1 ? -136.0f : -128.0f;
+    // the weight offsets (-136 for Q4_0: the +128 of the bf16 trick and the
+    // nibble bias 8; -128 for Q8_0) as a bf16 pair: the MFMA of the
+    // activations with it is the accumulator input OFFSET * sum(A), exact
+    constexpr uint32_t OFFW = MODE == 1 ? 0xC308C308u : 0xC300C300u;
     __shared__ float lds_p[CB][256];       // exact block dots, [block][row*16 + col]
     __shared__ float lds_sa[CB][16];       // activation scales, [block][row]
-    __shared__ float lds_as[CB][16];       // activation operand sums, [block][row]
     __shared__ float lds_dw[CB][16];       // weight scales, [block][col]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -160,7 +164,7 @@ __global__ __launch_bounds__(256) void vk_gemv_qblock(
     uint4 wq[GPW][WQ];
     uint2 ws[GPW];
     uint4 af[GPW][GB];
-    float sv[CB * 16 / 256], tv[CB * 16 / 256];
+    float sv[CB * 16 / 256];
     auto load_chunk = [&](int g0) {
         const int gn = min(CB / GB, G - g0);
 #pragma unroll
@@ -180,7 +184,6 @@ __global__ __launch_bounds__(256) void vk_gemv_qblock(
             const int bl = idx >> 4, r = idx & 15;
             const size_t o = (size_t)(g0 * GB + bl) * m_pad + mt * 16 + r;
             sv[h] = ascale[o];
-            tv[h] = asum[o];
         }
     };
     load_chunk(0);
@@ -189,10 +192,7 @@ __global__ __launch_bounds__(256) void vk_gemv_qblock(
 #pragma unroll
         for (int h = 0; h < CB * 16 / 256; ++h) {
             const int idx = tid + 256 * h;
-            if (idx < gn * GB * 16) {
-                lds_sa[idx >> 4][idx & 15] = sv[h];
-                lds_as[idx >> 4][idx & 15] = tv[h];
-            }
+            if (idx < gn * GB * 16) lds_sa[idx >> 4][idx & 15] = sv[h];
         }
         VK_LDS_BARRIER();
         // ---- phase 1 compute: exact P_b for this wave's groups
@@ -213,10 +213,11 @@ __global__ __launch_bounds__(256) void vk_gemv_qblock(
                     bf = (u & 1) ? q8_bytes_to_bf16(q.z, q.w) : q8_bytes_to_bf16(q.x, q.y);
                 }
                 const int bl = gl * GB + u;  // block index within the chunk
-                const float4 t4 = *reinterpret_cast<const float4*>(&lds_as[bl][rq]);
-                const vk_f32x4 cin = {OFFSET * t4.x, OFFSET * t4.y, OFFSET * t4.z, OFFSET * t4.w};
-                const vk_f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    __builtin_bit_cast(vk_bf16x8, af[j][u]), bf, cin, 0, 0, 0);
+                const vk_bf16x8 a8 = __builtin_bit_cast(vk_bf16x8, af[j][u]);
+                const vk_f32x4 cin = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    a8, __builtin_bit_cast(vk_bf16x8, make_uint4(OFFW, OFFW, OFFW, OFFW)),
+                    (vk_f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                const vk_f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a8, bf, cin, 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) lds_p[bl][(rq + r) * 16 + (lane & 15)] = p[r];
                 if (lane < 16) lds_dw[bl][lane] = vk_f16_to_f32_hw(sc_bits[u]);
@@ -262,7 +263,7 @@ namespace gw {
 #endif
 constexpr int RING = VK_GW_RING;        // groups in flight per wave (<= 8: the wait counts stay < 64)
 constexpr int SLOT = 7 * 1024;          // bytes per ring slot: A 4 KiB, W <= 2 KiB, scales 768 B
-constexpr int OFF_W = 4096, OFF_WS = 6144, OFF_SA = 6400, OFF_AS = 6656;
+constexpr int OFF_W = 4096, OFF_WS = 6144, OFF_SA = 6400;
 }  // namespace gw
 
 // One wave's 16 x 16 output tile (weight column tile nt, activation row tile
@@ -274,8 +275,11 @@ __device__ __forceinline__ void gemv_w_tile(const uint4* __restrict__ afrag, con
                                             int nb, int m_pad, uint8_t (&ring)[gw::RING][gw::SLOT], float (&acc)[4]) {
     using namespace gw;
     constexpr int WQ = MODE == 1 ? 1 : 2;           // weight KiB per group
-    constexpr int LG = 4 + WQ + 3;                  // direct loads per lane per group
-    constexpr float OFFSET = MODE == 1 ? -136.0f : -128.0f;
+    constexpr int LG = 4 + WQ + 2;                  // direct loads per lane per group
+    // the weight offsets as a bf16 pair (see vk_gemv_qblock): the accumulator
+    // input OFFSET * sum(A) is an MFMA of the activations with it
+    constexpr uint32_t OFFW = MODE == 1 ? 0xC308C308u : 0xC300C300u;
+    (void)asum;
     const int lane = threadIdx.x & 63, col = lane & 15;
     const int G = nb / gemv::GB;
     const uint32_t base = __builtin_amdgcn_readfirstlane(vk_lds_addr(&ring[0][0]));
@@ -292,7 +296,6 @@ __device__ __forceinline__ void gemv_w_tile(const uint4* __restrict__ afrag, con
         for (int h = 0; h < WQ; ++h) vk_dma_b128(w_src + (size_t)(g * WQ + h) * gemv::FRAG_U4, b + OFF_W + h * 1024);
         vk_dma_b32(ws_src + (size_t)g * 32, b + OFF_WS);
         vk_dma_b32(ascale + (size_t)4 * g * m_pad + s_off, b + OFF_SA);
-        vk_dma_b32(asum + (size_t)4 * g * m_pad + s_off, b + OFF_AS);
     };
     acc[0] = acc[1] = acc[2] = acc[3] = 0.0f;
 #pragma unroll
@@ -330,12 +333,9 @@ __device__ __forceinline__ void gemv_w_tile(const uint4* __restrict__ afrag, con
 #pragma unroll
         for (int h = 0; h < WQ; ++h) wq[h] = reinterpret_cast<const uint4*>(sl + OFF_W + h * 1024)[lane];
         const uint2 ws = reinterpret_cast<const uint2*>(sl + OFF_WS)[col];
-        float4 sa[4], as[4];
+        float4 sa[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            sa[u] = reinterpret_cast<const float4*>(sl + OFF_SA)[u * 4 + (lane >> 4)];
-            as[u] = reinterpret_cast<const float4*>(sl + OFF_AS)[u * 4 + (lane >> 4)];
-        }
+        for (int u = 0; u < 4; ++u) sa[u] = reinterpret_cast<const float4*>(sl + OFF_SA)[u * 4 + (lane >> 4)];
         const uint32_t sc_bits[4] = {ws.x & 0xffffu, ws.x >> 16, ws.y & 0xffffu, ws.y >> 16};
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -348,9 +348,11 @@ __device__ __forceinline__ void gemv_w_tile(const uint4* __restrict__ afrag, con
                 const uint4 q = wq[u >> 1];
                 bf = (u & 1) ? q8_bytes_to_bf16(q.z, q.w) : q8_bytes_to_bf16(q.x, q.y);
             }
-            const vk_f32x4 cin = {OFFSET * as[u].x, OFFSET * as[u].y, OFFSET * as[u].z, OFFSET * as[u].w};
-            const vk_f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(vk_bf16x8, af[u]), bf, cin,
-                                                                       0, 0, 0);
+            const vk_bf16x8 a8 = __builtin_bit_cast(vk_bf16x8, af[u]);
+            const vk_f32x4 cin = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                a8, __builtin_bit_cast(vk_bf16x8, make_uint4(OFFW, OFFW, OFFW, OFFW)),
+                (vk_f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            const vk_f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a8, bf, cin, 0, 0, 0);
             const float dw = vk_f16_to_f32_hw(sc_bits[u]);
             const float sar[4] = {sa[u].x, sa[u].y, sa[u].z, sa[u].w};
 #pragma unroll
