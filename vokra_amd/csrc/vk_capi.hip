@@ -228,7 +228,8 @@ int qact_reserve(vokra_hip_qact* qa, size_t m, size_t k) {
     const size_t m_pad = round_up(m, vk::GEMM_TM);
     const size_t ng = k / 16;
     VK_TRY(qa->frag.ensure(m_pad * k * 2), "hipMalloc(activation fragments)");
-    VK_TRY(qa->scale.ensure(m_pad * ng * sizeof(float)), "hipMalloc(activation scales)");
+    // the K-quant (16-wide) layout keeps (scale, sum) pairs in `scale`
+    VK_TRY(qa->scale.ensure(m_pad * ng * 2 * sizeof(float)), "hipMalloc(activation scales)");
     VK_TRY(qa->gsum.ensure(m_pad * ng * sizeof(float)), "hipMalloc(activation sums)");
     return VOKRA_HIP_OK;
 }
@@ -2016,8 +2017,10 @@ int vokra_hip_gemm_q_f32_dev_noalloc(vokra_hip_ctx_t* c, const vokra_hip_qweight
     unsigned char* base = static_cast<unsigned char*>(c->scratch);
     qa.frag.p = base;
     qa.frag.cap = frag;
+    // block formats use scale and gsum as two arrays; the K-quant layout
+    // keeps (scale, sum) pairs in one array over both regions
     qa.scale.p = base + frag;
-    qa.scale.cap = sc;
+    qa.scale.cap = 2 * sc;
     qa.gsum.p = base + frag + sc;
     qa.gsum.cap = sc;
     int st = quantize_activations(c, &qa, d_a, m, k, w->kquant ? VOKRA_HIP_ACT_KQUANT : act_quant);

@@ -126,8 +126,10 @@ __global__ void vk_dequantize_q6k(const uint8_t* __restrict__ bytes, size_t nsb,
 //          (16-row tile mt, super-block sb, group pair gp) 64 lanes x 16 bytes:
 //          lane l = row % 16 + 16 c holds K 4c..4c+3 of group 2gp (bytes 0..7)
 //          and of group 2gp + 1 (bytes 8..15);
-//   ascale / asum: per run of 4 groups (g / 4), per row, the 4 groups' s and
-//          (float) gsum back to back: index ((g / 4) * m_pad + row) * 4 + g % 4.
+//   ascale: per run of 4 groups (g / 4), per row, the 4 groups' (s, (float)
+//          gsum) pairs back to back: float2 index ((g / 4) * m_pad + row) * 4
+//          + g % 4 (so a matmul lane reads its group's pair with one 8-byte
+//          load); the separate asum array is not used by this layout.
 // Rows m..m_pad-1 are written as zeros.
 // One group's activation pass: the 16 values v of (row, group g) -> its
 // fragment words, s and gsum (zeros when !live: the padding rows).
@@ -164,8 +166,8 @@ __device__ __forceinline__ void vk_q16_store(int row, int g, int m_pad, int nsb,
         afrag[base + (size_t)lane * 2] = w;
     }
     const size_t si = ((size_t)(g >> 2) * m_pad + row) * 4 + (g & 3);
-    ascale[si] = s;
-    asum[si] = (float)gsum;
+    reinterpret_cast<float2*>(ascale)[si] = make_float2(s, (float)gsum);
+    (void)asum;
 }
 
 __global__ void vk_quantize_act_g16(const float* __restrict__ a, int m, int m_pad, int k,
@@ -290,7 +292,8 @@ __global__ void vk_swiglu_quantize_g16(const float* __restrict__ gt, const float
 //        (K_lo, K_hi) = group 2w + j/2, elements 4c + 2(j%2) and +1, with
 //        K_lo at bits 4j..4j+3 and K_hi at bits 16+4j..19+4j, so
 //        ((W >> 4j) & 0x000F000F) | 0x43004300 is the bf16 pair (128 + q).
-//   wdm: 8 sub-blocks x 16 columns of float2 (d * sc, dmin * m).
+//   wdm: 4 sub-block pairs x 16 columns x 2 sub-blocks of float2 (d * sc,
+//        dmin * m): sub-blocks 2p and 2p + 1 of a column side by side.
 // Columns n..n_pad-1 are zero.
 __device__ __forceinline__ uint32_t q4k_nibble(const uint8_t* qs, int e) {
     const int l = e & 63;
@@ -325,10 +328,12 @@ __global__ void vk_repack_w_q4k(const uint8_t* __restrict__ wq, int n, int n_pad
     }
     const float d = live ? vk_f16_to_f32(blk[0] | (blk[1] << 8)) : 0.0f;
     const float dmin = live ? vk_f16_to_f32(blk[2] | (blk[3] << 8)) : 0.0f;
+    // sub-blocks 2p and 2p + 1 of a column side by side (one 16-byte load
+    // per term wave p)
     for (int j = 0; j < 8; ++j) {
         int sc = 0, mn = 0;
         if (live) scale_min_k4(j, blk + 4, sc, mn);
-        wdm[(tile * 8 + j) * 16 + cl] = make_float2(d * (float)sc, dmin * (float)mn);
+        wdm[((tile * 4 + (j >> 1)) * 16 + cl) * 2 + (j & 1)] = make_float2(d * (float)sc, dmin * (float)mn);
     }
 }
 
@@ -342,7 +347,8 @@ __global__ void vk_repack_w_q4k(const uint8_t* __restrict__ wq, int n, int n_pad
 // (16-column tile nt, super-block sb):
 //   wq:  64 lanes x 64 bytes; lane l = col % 16 + 16 c holds 16 byte words,
 //        word g = K 4c, 4c+2, 4c+1, 4c+3 of group g;
-//   wdm: 16 groups x 16 columns of float2 (d_eff, m_eff).
+//   wdm: 8 group pairs x 16 columns x 2 groups of float2 (d_eff, m_eff)
+//        (groups 2p and 2p + 1 of a column side by side: one 16-byte load).
 // Columns n..n_pad-1 are zero.
 __global__ void vk_repack_w_kq8(int wdtype, const uint8_t* __restrict__ wq, int n, int n_pad, int nsb,
                                 uint4* __restrict__ wq4, float2* __restrict__ wdm) {
@@ -406,7 +412,7 @@ __global__ void vk_repack_w_kq8(int wdtype, const uint8_t* __restrict__ wq, int 
         uint4* dst = wq4 + (tile * 64 + cl + 16 * c) * 4;
         for (int h = 0; h < 4; ++h) dst[h] = make_uint4(w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]);
     }
-    for (int g = 0; g < 16; ++g) wdm[(tile * 16 + g) * 16 + cl] = make_float2(de[g], me[g]);
+    for (int g = 0; g < 16; ++g) wdm[((tile * 8 + (g >> 1)) * 16 + cl) * 2 + (g & 1)] = make_float2(de[g], me[g]);
 }
 
 // bf16 operand (4 values, K 4c..4c+3 of one group) from a nibble word:
@@ -467,12 +473,15 @@ __device__ __forceinline__ vk_s16x4 kq_operand(const W& wv, int i, uint32_t nib_
 // Lane mapping: activations are the MFMA's A operand and weights its B
 // operand, so lane l holds rows 4 (l / 16) .. +3 of weight column l % 16.
 // Each 16-lane DPP row then needs the same 16 activation scales and 16 group
-// sums (4 rows x 4 groups): every lane loads one of each (a wave reads 256
-// contiguous bytes per array) and the values reach their users through
+// sums (4 rows x 4 groups): every lane loads one (s, gsum) pair (a wave
+// reads 512 contiguous bytes) and the values reach their users through
 // row_newbcast DPP operands of the multiplies themselves, and a lane's own
-// column needs only its two (d_eff, m_eff) pairs: 2 + 2 + 8 + 8 bytes per lane
-// of broadcast data instead of 96, which keeps the texture path off the
-// critical path.
+// column needs only its two (d_eff, m_eff) pairs, stored side by side: one
+// 8-byte and one 16-byte load per lane (Q5_K / Q6_K: two 16-byte loads for
+// four per-group pairs) instead of 96 bytes of broadcast data, which keeps
+// the texture path off the critical path (each vector-memory instruction of
+// a step costs issue time on the CU's memory pipeline: 5 per step instead of
+// 7 took 57.0 -> 53.8 us per config-4 layer).
 // Term buffer layout per group: the float4 of lane l (its 4 rows) at 4 l, so
 // a wave's stores cover 256 consecutive floats, and phase 2's thread t
 // (t = thread index - 512) reads float t, the output (row 4 (t / 64) + t % 4,
@@ -526,8 +535,8 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
     // per-lane byte offsets (constant over the K loop)
     const uint32_t vo_w = FMT == 0 ? lane * 32 + 8 * q4 : lane * 64 + 16 * q4;
     const uint32_t vo_a = lane * 16;
-    const uint32_t vo_d = (lane & 15) * 8;
-    const uint32_t vo_s = (uint32_t)(mt * 16) * 16 + lane * 4;
+    const uint32_t vo_d = (lane & 15) * 16;
+    const uint32_t vo_s = ((uint32_t)(mt * 16) * 16 + lane * 4) * 2;
 
     // Buffer resources over the five operand arrays: every load is a
     // constant per-lane offset plus a wave-uniform offset computed on the
@@ -539,8 +548,9 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
     const __amdgpu_buffer_rsrc_t rd =
         __builtin_amdgcn_make_buffer_rsrc((void*)L.wdm, 0, n_pad * nsb * (FMT == 0 ? 64 : 128), rsrc_w3);
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)afrag, 0, m_pad * nsb * 512, rsrc_w3);
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)ascale, 0, m_pad * nsb * 64, rsrc_w3);
-    const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc((void*)asum, 0, m_pad * nsb * 64, rsrc_w3);
+    // (s, gsum) pairs of the K-quant activation layout
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)ascale, 0, m_pad * nsb * 128, rsrc_w3);
+    (void)asum;
     typedef unsigned int vk_u32x2 __attribute__((ext_vector_type(2)));
     typedef unsigned int vk_u32x4 __attribute__((ext_vector_type(4)));
 
@@ -553,8 +563,8 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
         const int oa = (((mt * nsb + sb) * 8 + 2 * q4) * 64) * 16;
         // scales / sums of groups 4 q4 .. +3 of rows mt*16 .. +15: 256 bytes,
         // lane 16 k + j holding row 4 k + j / 4, group j % 4
-        const int os = (sb * (NG / 4) + q4) * m_pad * 16;
-        const int od = FMT == 0 ? ((nt * nsb + sb) * 8 + 2 * q4) * 128 : ((nt * nsb + sb) * 16 + 4 * q4) * 128;
+        const int os = (sb * (NG / 4) + q4) * m_pad * 32;
+        const int od = FMT == 0 ? ((nt * nsb + sb) * 4 + q4) * 256 : ((nt * nsb + sb) * 8 + 2 * q4) * 256;
         if constexpr (FMT == 0) {
             const vk_u32x2 w2 = __builtin_amdgcn_raw_buffer_load_b64(rw, vo_w, ow, 0);
             p.wv = make_uint2(w2.x, w2.y);
@@ -567,12 +577,14 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
             const vk_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(ra, vo_a + h * 1024, oa, 0);
             p.af[h] = make_uint4(x.x, x.y, x.z, x.w);
         }
-        p.s = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vo_s, os, 0));
-        p.a = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, vo_s, os, 0));
+        const vk_u32x2 sa = __builtin_amdgcn_raw_buffer_load_b64(rs, vo_s, os, 0);
+        p.s = __uint_as_float(sa.x);
+        p.a = __uint_as_float(sa.y);
 #pragma unroll
-        for (int jj = 0; jj < (FMT == 0 ? 2 : 4); ++jj) {
-            const vk_u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rd, vo_d + jj * 128, od, 0);
+        for (int jj = 0; jj < (FMT == 0 ? 2 : 4); jj += 2) {
+            const vk_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rd, vo_d, od + jj * 128, 0);
             p.dm[jj] = make_float2(__uint_as_float(x.x), __uint_as_float(x.y));
+            p.dm[jj + 1] = make_float2(__uint_as_float(x.z), __uint_as_float(x.w));
         }
         return p;
     };

@@ -1155,10 +1155,9 @@ __global__ void vk_paged_attn_combine(int n_split, int hq, const int* __restrict
         const int lane_f = (row & 15) + 16 * (t >> 2);
         reinterpret_cast<uint16_t*>(qo.afrag)[(base + (size_t)lane_f * 2) * 4 + (t & 3)] =
             (uint16_t)vk_int_to_bf16_bits(r);
-        if (t == 0) {
+        if (t == 0) {  // the K-quant layout's (s, gsum) pair
             const size_t si = ((size_t)(g >> 2) * qo.m_pad + row) * 4 + (g & 3);
-            qo.ascale[si] = sc;
-            qo.asum[si] = (float)gs;
+            reinterpret_cast<float2*>(qo.ascale)[si] = make_float2(sc, (float)gs);
         }
     }
 }
