@@ -249,7 +249,7 @@ int quantize_activations(vokra_hip_ctx* c, vokra_hip_qact* qa, const float* d_a,
             return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "activations must be 16-byte aligned");
         const size_t m_pad = round_up(m, 16);
         VK_TRY(vk::launch_quantize_act_g16(c->stream, d_a, (int)m, (int)m_pad, (int)k, (uint4*)qa->frag.p,
-                                           (float*)qa->scale.p, (float*)qa->gsum.p),
+                                           (float*)qa->scale.p),
                "launch(vk_quantize_act_g16)");
         qa->m = m;
         qa->k = k;
@@ -366,9 +366,8 @@ int run_gemm_qact(vokra_hip_ctx* c, const vokra_hip_qweight* w, const vokra_hip_
         if (qa->act_quant != VOKRA_HIP_ACT_KQUANT)
             return fail(VOKRA_HIP_ERROR_INVALID_ARGUMENT, "gemm_qact: K-quant weights need KQUANT activations");
         const VkQ4kLin lin = {(const uint4*)w->gq.p, (const float2*)w->gsc.p, d_bias, d_out, epi, (int)w->n};
-        VK_TRY(vk::launch_gemm_q4k(c->stream, (const uint4*)qa->frag.p, (const float*)qa->scale.p,
-                                   (const float*)qa->gsum.p, &lin, 1, (int)qa->m, (int)w->nb, (int)qa->m_pad,
-                                   w->kfmt),
+        VK_TRY(vk::launch_gemm_q4k(c->stream, (const uint4*)qa->frag.p, (const float*)qa->scale.p, &lin, 1,
+                                   (int)qa->m, (int)w->nb, (int)qa->m_pad, w->kfmt),
                "launch(vk_gemm_q4k)");
         return VOKRA_HIP_OK;
     }
@@ -613,9 +612,8 @@ int gemm_qact_multi(vokra_hip_ctx* c, int n, const vokra_hip_qweight* const* ws,
         for (int i = 0; i < n; ++i)
             lins[i] = {(const uint4*)ws[i]->gq.p, (const float2*)ws[i]->gsc.p, biases ? biases[i] : nullptr, outs[i],
                        {nullptr, 0}, (int)ws[i]->n};
-        VK_TRY(vk::launch_gemm_q4k(c->stream, (const uint4*)qa->frag.p, (const float*)qa->scale.p,
-                                   (const float*)qa->gsum.p, lins, n, (int)qa->m, (int)ws[0]->nb, (int)qa->m_pad,
-                                   ws[0]->kfmt),
+        VK_TRY(vk::launch_gemm_q4k(c->stream, (const uint4*)qa->frag.p, (const float*)qa->scale.p, lins, n,
+                                   (int)qa->m, (int)ws[0]->nb, (int)qa->m_pad, ws[0]->kfmt),
                "launch(vk_gemm_q4k x n)");
         return VOKRA_HIP_OK;
     }
@@ -738,7 +736,7 @@ int qact_rms_quantize_g16(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, size_t
     if (st) return st;
     const size_t m_pad = round_up(m, 16);
     VK_TRY(vk::launch_rms_quantize_g16(c->stream, d_in, gamma, eps, (int)m, (int)m_pad, (int)k, (uint4*)qa->frag.p,
-                                       (float*)qa->scale.p, (float*)qa->gsum.p),
+                                       (float*)qa->scale.p),
            "launch(vk_rms_quantize_g16)");
     qa->m = m;
     qa->k = k;
@@ -753,7 +751,7 @@ int qact_swiglu_quantize_g16(vokra_hip_ctx* c, vokra_hip_qact* qa, size_t m, siz
     if (st) return st;
     const size_t m_pad = round_up(m, 16);
     VK_TRY(vk::launch_swiglu_quantize_g16(c->stream, d_g, d_u, (int)m, (int)m_pad, (int)k, (uint4*)qa->frag.p,
-                                          (float*)qa->scale.p, (float*)qa->gsum.p),
+                                          (float*)qa->scale.p),
            "launch(vk_swiglu_quantize_g16)");
     qa->m = m;
     qa->k = k;

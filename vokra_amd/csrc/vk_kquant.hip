@@ -129,13 +129,12 @@ __global__ void vk_dequantize_q6k(const uint8_t* __restrict__ bytes, size_t nsb,
 //   ascale: per run of 4 groups (g / 4), per row, the 4 groups' (s, (float)
 //          gsum) pairs back to back: float2 index ((g / 4) * m_pad + row) * 4
 //          + g % 4 (so a matmul lane reads its group's pair with one 8-byte
-//          load); the separate asum array is not used by this layout.
+//          load).
 // Rows m..m_pad-1 are written as zeros.
 // One group's activation pass: the 16 values v of (row, group g) -> its
 // fragment words, s and gsum (zeros when !live: the padding rows).
 __device__ __forceinline__ void vk_q16_store(int row, int g, int m_pad, int nsb, const float (&v)[16], bool live,
-                                             uint2* __restrict__ afrag, float* __restrict__ ascale,
-                                             float* __restrict__ asum) {
+                                             uint2* __restrict__ afrag, float* __restrict__ ascale) {
     int r[16];
     float s = 0.0f;
     int gsum = 0;
@@ -167,12 +166,10 @@ __device__ __forceinline__ void vk_q16_store(int row, int g, int m_pad, int nsb,
     }
     const size_t si = ((size_t)(g >> 2) * m_pad + row) * 4 + (g & 3);
     reinterpret_cast<float2*>(ascale)[si] = make_float2(s, (float)gsum);
-    (void)asum;
 }
 
 __global__ void vk_quantize_act_g16(const float* __restrict__ a, int m, int m_pad, int k,
-                                    uint2* __restrict__ afrag, float* __restrict__ ascale,
-                                    float* __restrict__ asum) {
+                                    uint2* __restrict__ afrag, float* __restrict__ ascale) {
     const int ng = k / 16, nsb = k / kq::QK;
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= (size_t)ng * m_pad) return;
@@ -189,7 +186,7 @@ __global__ void vk_quantize_act_g16(const float* __restrict__ a, int m, int m_pa
             v[4 * h + 3] = x.w;
         }
     }
-    vk_q16_store(row, g, m_pad, nsb, v, row < m, afrag, ascale, asum);
+    vk_q16_store(row, g, m_pad, nsb, v, row < m, afrag, ascale);
 }
 
 // RMSNorm fused with the activation pass, one workgroup per row (rows m ..
@@ -201,7 +198,7 @@ constexpr int kRmsRowLds = 2048;  // rows up to this many columns are read once
 __global__ __launch_bounds__(256) void vk_rms_quantize_g16(const float* __restrict__ in,
                                                            const float* __restrict__ gamma, float eps, int m,
                                                            int m_pad, int k, uint2* __restrict__ afrag,
-                                                           float* __restrict__ ascale, float* __restrict__ asum) {
+                                                           float* __restrict__ ascale) {
     __shared__ float red[4];
     __shared__ __align__(16) float xs[kRmsRowLds];
     const int row = blockIdx.x, nsb = k / kq::QK;
@@ -243,7 +240,7 @@ __global__ __launch_bounds__(256) void vk_rms_quantize_g16(const float* __restri
 #pragma unroll
                 for (int t = 0; t < 16; ++t) v[t] = xs[16 * g + t] * inv * gm[t];
             }
-            vk_q16_store(row, g, m_pad, nsb, v, live, afrag, ascale, asum);
+            vk_q16_store(row, g, m_pad, nsb, v, live, afrag, ascale);
         }
         return;
     }
@@ -256,7 +253,7 @@ __global__ __launch_bounds__(256) void vk_rms_quantize_g16(const float* __restri
 #pragma unroll
             for (int t = 0; t < 16; ++t) v[t] = ir[16 * g + t] * inv * gamma[16 * g + t];
         }
-        vk_q16_store(row, g, m_pad, nsb, v, live, afrag, ascale, asum);
+        vk_q16_store(row, g, m_pad, nsb, v, live, afrag, ascale);
     }
 }
 
@@ -264,8 +261,7 @@ __global__ __launch_bounds__(256) void vk_rms_quantize_g16(const float* __restri
 // 16 values silu(g) * u formed as vk_swiglu_f32 forms them, then quantized as
 // vk_quantize_act_g16 would. Bit-identical to the two launches.
 __global__ void vk_swiglu_quantize_g16(const float* __restrict__ gt, const float* __restrict__ up, int m, int m_pad,
-                                       int k, uint2* __restrict__ afrag, float* __restrict__ ascale,
-                                       float* __restrict__ asum) {
+                                       int k, uint2* __restrict__ afrag, float* __restrict__ ascale) {
     const int ng = k / 16, nsb = k / kq::QK;
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= (size_t)ng * m_pad) return;
@@ -281,7 +277,7 @@ __global__ void vk_swiglu_quantize_g16(const float* __restrict__ gt, const float
             v[t] = tt * up[o + t];
         }
     }
-    vk_q16_store(row, g, m_pad, nsb, v, row < m, afrag, ascale, asum);
+    vk_q16_store(row, g, m_pad, nsb, v, row < m, afrag, ascale);
 }
 
 // ---------------------------------------------------------------------------
@@ -513,8 +509,7 @@ __device__ __forceinline__ float row_bcast(float x) {
 
 template <int FMT>
 __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afrag, const float* __restrict__ ascale,
-                                                   const float* __restrict__ asum, VkQ4kSet set, int m, int nsb,
-                                                   int m_pad) {
+                                                   VkQ4kSet set, int m, int nsb, int m_pad) {
     using namespace kq;
     __shared__ __align__(16) float lds_t[2][CHG][256];  // terms, [chunk parity][group][4 * lane + r]
 
@@ -550,7 +545,6 @@ __global__ __launch_bounds__(768) void vk_gemm_q4k(const uint4* __restrict__ afr
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)afrag, 0, m_pad * nsb * 512, rsrc_w3);
     // (s, gsum) pairs of the K-quant activation layout
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)ascale, 0, m_pad * nsb * 128, rsrc_w3);
-    (void)asum;
     typedef unsigned int vk_u32x2 __attribute__((ext_vector_type(2)));
     typedef unsigned int vk_u32x4 __attribute__((ext_vector_type(4)));
 
@@ -736,28 +730,28 @@ hipError_t launch_repack_w_kq8(hipStream_t s, int wdtype, const uint8_t* wq, int
 }
 
 hipError_t launch_quantize_act_g16(hipStream_t s, const float* a, int m, int m_pad, int k, uint4* afrag,
-                                   float* ascale, float* asum) {
+                                   float* ascale) {
     const size_t threads = (size_t)(k / 16) * m_pad;
     if (threads == 0) return hipSuccess;
     hipLaunchKernelGGL(vk_quantize_act_g16, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a, m, m_pad,
-                       k, reinterpret_cast<uint2*>(afrag), ascale, asum);
+                       k, reinterpret_cast<uint2*>(afrag), ascale);
     return hipGetLastError();
 }
 
 hipError_t launch_rms_quantize_g16(hipStream_t s, const float* in, const float* gamma, float eps, int m, int m_pad,
-                                   int k, uint4* afrag, float* ascale, float* asum) {
+                                   int k, uint4* afrag, float* ascale) {
     if (m_pad == 0) return hipSuccess;
     hipLaunchKernelGGL(vk_rms_quantize_g16, dim3((unsigned)m_pad), dim3(256), 0, s, in, gamma, eps, m, m_pad, k,
-                       reinterpret_cast<uint2*>(afrag), ascale, asum);
+                       reinterpret_cast<uint2*>(afrag), ascale);
     return hipGetLastError();
 }
 
 hipError_t launch_swiglu_quantize_g16(hipStream_t s, const float* g, const float* u, int m, int m_pad, int k,
-                                      uint4* afrag, float* ascale, float* asum) {
+                                      uint4* afrag, float* ascale) {
     const size_t threads = (size_t)(k / 16) * m_pad;
     if (threads == 0) return hipSuccess;
     hipLaunchKernelGGL(vk_swiglu_quantize_g16, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, g, u, m,
-                       m_pad, k, reinterpret_cast<uint2*>(afrag), ascale, asum);
+                       m_pad, k, reinterpret_cast<uint2*>(afrag), ascale);
     return hipGetLastError();
 }
 
@@ -770,8 +764,8 @@ hipError_t launch_repack_w_q4k(hipStream_t s, const uint8_t* wq, int n, int n_pa
     return hipGetLastError();
 }
 
-hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum,
-                           const VkQ4kLin* lins, int n_lin, int m, int nsb, int m_pad, int fmt) {
+hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascale, const VkQ4kLin* lins, int n_lin,
+                           int m, int nsb, int m_pad, int fmt) {
     if (n_lin < 1 || n_lin > 3 || fmt < 0 || fmt > 1) return hipErrorInvalidValue;
     VkQ4kSet set{};
     int tiles = 0;
@@ -783,9 +777,9 @@ hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascal
     set.count = n_lin;
     const dim3 grid((unsigned)tiles, (unsigned)((m + 15) / 16));
     if (fmt == 0)
-        hipLaunchKernelGGL(vk_gemm_q4k<0>, grid, dim3(768), 0, s, afrag, ascale, asum, set, m, nsb, m_pad);
+        hipLaunchKernelGGL(vk_gemm_q4k<0>, grid, dim3(768), 0, s, afrag, ascale, set, m, nsb, m_pad);
     else
-        hipLaunchKernelGGL(vk_gemm_q4k<1>, grid, dim3(768), 0, s, afrag, ascale, asum, set, m, nsb, m_pad);
+        hipLaunchKernelGGL(vk_gemm_q4k<1>, grid, dim3(768), 0, s, afrag, ascale, set, m, nsb, m_pad);
     return hipGetLastError();
 }
 

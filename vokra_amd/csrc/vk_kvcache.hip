@@ -1342,7 +1342,7 @@ hipError_t launch_paged_attn(hipStream_t s, const KvView& v, int layer, int n, c
         if (g16) return hipSuccess;
     }
     // kernels without the fused pass: the separate activation pass over out
-    if (g16) return launch_quantize_act_g16(s, out, n, qz.m_pad, qz.k, qz.afrag, qz.ascale, qz.asum);
+    if (g16) return launch_quantize_act_g16(s, out, n, qz.m_pad, qz.k, qz.afrag, qz.ascale);
     if (qz.afrag && !fused)
         return launch_quantize_act_b32(s, qz.pow2 != 0, out, n, qz.m_pad, qz.k, qz.afrag, qz.ascale, qz.asum);
     return hipSuccess;

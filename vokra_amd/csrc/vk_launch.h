@@ -23,7 +23,7 @@ struct VkQOut {
     int k;      // the quantized row width (a multiple of 32)
     int pow2;   // the power-of-two scale convention
     int g16;    // the K-quant layout instead: 16-wide groups (vk_q16_store), m_pad a multiple of 16,
-                // (scale, sum) pairs in ascale (asum unused)
+                // (scale, sum) pairs in ascale (asum not used by it)
 };
 // One linear of a multi-linear block-GEMM launch: bf16 fragments + scales,
 // optional bias, output [m, n].
@@ -119,12 +119,13 @@ hipError_t launch_gemv_qblock_group(hipStream_t s, int mode, bool pow2, const ui
 
 namespace vk {
 hipError_t launch_dequantize_q4k(hipStream_t s, const uint8_t* bytes, size_t nsb, float* out);
+// K-quant activation pass: fragments, and (scale, sum) pairs in ascale
 hipError_t launch_quantize_act_g16(hipStream_t s, const float* a, int m, int m_pad, int k, uint4* afrag,
-                                   float* ascale, float* asum);
+                                   float* ascale);
 hipError_t launch_repack_w_q4k(hipStream_t s, const uint8_t* wq, int n, int n_pad, int nsb, uint4* wq4,
                                float2* wdm);
-hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum,
-                           const VkQ4kLin* lins, int n_lin, int m, int nsb, int m_pad, int fmt);
+hipError_t launch_gemm_q4k(hipStream_t s, const uint4* afrag, const float* ascale, const VkQ4kLin* lins, int n_lin,
+                           int m, int nsb, int m_pad, int fmt);
 // Q4_K / Q5_K / Q6_K (ggml tags 12 / 13 / 14) -> f32, bit-exact with gguf/quant.
 hipError_t launch_dequantize_kq(hipStream_t s, int wdtype, const uint8_t* bytes, size_t nsb, float* out);
 // Q5_K / Q6_K weights into the byte-word layout of the matmul's format 1.
@@ -134,9 +135,9 @@ hipError_t launch_repack_w_kq8(hipStream_t s, int wdtype, const uint8_t* wq, int
 // one launch each (bit-identical to vk_rms_norm_f32 / vk_swiglu_f32 followed by
 // vk_quantize_act_g16); m_pad = round_up(m, 16), k % 256 == 0.
 hipError_t launch_rms_quantize_g16(hipStream_t s, const float* in, const float* gamma, float eps, int m, int m_pad,
-                                   int k, uint4* afrag, float* ascale, float* asum);
+                                   int k, uint4* afrag, float* ascale);
 hipError_t launch_swiglu_quantize_g16(hipStream_t s, const float* g, const float* u, int m, int m_pad, int k,
-                                      uint4* afrag, float* ascale, float* asum);
+                                      uint4* afrag, float* ascale);
 }  // namespace vk
 
 namespace vk {
