@@ -171,9 +171,10 @@ __device__ __forceinline__ void vk_q16_store(int row, int g, int m_pad, int nsb,
 __global__ void vk_quantize_act_g16(const float* __restrict__ a, int m, int m_pad, int k,
                                     uint2* __restrict__ afrag, float* __restrict__ ascale) {
     const int ng = k / 16, nsb = k / kq::QK;
-    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (size_t)ng * m_pad) return;
-    const int g = (int)(gid / m_pad), row = (int)(gid % m_pad);
+    // (g, row) of this thread in 32-bit arithmetic (ng * m_pad < 2^31)
+    const unsigned gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (unsigned)(ng * m_pad)) return;
+    const int g = (int)(gid / (unsigned)m_pad), row = (int)(gid - (unsigned)g * (unsigned)m_pad);
     float v[16];
     if (row < m) {
         const float4* src = reinterpret_cast<const float4*>(a + (size_t)row * k + 16 * g);
@@ -263,9 +264,10 @@ __global__ __launch_bounds__(256) void vk_rms_quantize_g16(const float* __restri
 __global__ void vk_swiglu_quantize_g16(const float* __restrict__ gt, const float* __restrict__ up, int m, int m_pad,
                                        int k, uint2* __restrict__ afrag, float* __restrict__ ascale) {
     const int ng = k / 16, nsb = k / kq::QK;
-    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (size_t)ng * m_pad) return;
-    const int g = (int)(gid / m_pad), row = (int)(gid % m_pad);
+    // (g, row) of this thread in 32-bit arithmetic (ng * m_pad < 2^31)
+    const unsigned gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (unsigned)(ng * m_pad)) return;
+    const int g = (int)(gid / (unsigned)m_pad), row = (int)(gid - (unsigned)g * (unsigned)m_pad);
     float v[16];
     if (row < m) {
         const size_t o = (size_t)row * k + 16 * g;
@@ -733,6 +735,7 @@ hipError_t launch_quantize_act_g16(hipStream_t s, const float* a, int m, int m_p
                                    float* ascale) {
     const size_t threads = (size_t)(k / 16) * m_pad;
     if (threads == 0) return hipSuccess;
+    if (threads > (size_t)INT32_MAX) return hipErrorInvalidValue;  // the kernel indexes in 32 bits
     hipLaunchKernelGGL(vk_quantize_act_g16, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a, m, m_pad,
                        k, reinterpret_cast<uint2*>(afrag), ascale);
     return hipGetLastError();
@@ -750,6 +753,7 @@ hipError_t launch_swiglu_quantize_g16(hipStream_t s, const float* g, const float
                                       uint4* afrag, float* ascale) {
     const size_t threads = (size_t)(k / 16) * m_pad;
     if (threads == 0) return hipSuccess;
+    if (threads > (size_t)INT32_MAX) return hipErrorInvalidValue;  // the kernel indexes in 32 bits
     hipLaunchKernelGGL(vk_swiglu_quantize_g16, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, g, u, m,
                        m_pad, k, reinterpret_cast<uint2*>(afrag), ascale);
     return hipGetLastError();

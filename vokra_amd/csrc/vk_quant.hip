@@ -167,12 +167,12 @@ __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pa
     // row mr, elements 8c .. 8c+7, and stores its 16 bytes at lane l of the
     // fragment, so every wave writes one contiguous KiB.
     const int nb = k >> 5;
-    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t total = (size_t)m_pad * nb * 4;
-    if (gid >= total) return;  // total is a multiple of 64: whole waves exit together
-    const int lane = (int)(gid & 63), c = lane >> 4, mr = lane & 15;
-    const size_t frag = gid >> 6;  // = mt * nb + b
-    const int mt = (int)(frag / nb), b = (int)(frag % nb);
+    // the fragment index is wave-uniform: its split into (mt, b) runs on the
+    // scalar unit, ahead of the row loads that need it
+    const int frag = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
+    if (frag >= (m_pad >> 4) * nb) return;  // whole waves exit together
+    const int lane = (int)(threadIdx.x & 63), c = lane >> 4, mr = lane & 15;
+    const int mt = frag / nb, b = frag - mt * nb;  // frag = mt * nb + b
     const int row = mt * 16 + mr;
     float v[8];
     if (row < m) {
@@ -225,7 +225,7 @@ __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pa
         }
         w[e] = lo | (hi << 16);
     }
-    afrag[frag * 64 + (size_t)lane] = make_uint4(w[0], w[1], w[2], w[3]);
+    afrag[(size_t)frag * 64 + lane] = make_uint4(w[0], w[1], w[2], w[3]);
     if (c == 0) {  // scales and operand sums are block-major: [nb][m_pad]
         ascale[(size_t)b * m_pad + row] = s;
         // sum of the A operand values of this block (exact: an integer times
@@ -732,6 +732,7 @@ hipError_t launch_quantize_act_b32(hipStream_t s, bool pow2, const float* a, int
     if (m_pad % 16 != 0) return hipErrorInvalidValue;  // whole fragments
     const size_t threads = (size_t)m_pad * (k / 32) * 4;
     if (threads == 0) return hipSuccess;
+    if (threads > (size_t)INT32_MAX) return hipErrorInvalidValue;  // the kernel indexes in 32 bits
     const unsigned grid = (unsigned)((threads + 255) / 256);
     if (pow2)
         hipLaunchKernelGGL(vk_quantize_act_b32<true>, dim3(grid), dim3(256), 0, s, a, m, m_pad, k, afrag,
