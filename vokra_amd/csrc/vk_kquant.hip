@@ -120,8 +120,10 @@ __global__ void vk_dequantize_q6k(const uint8_t* __restrict__ bytes, size_t nsb,
 }
 
 // ---------------------------------------------------------------------------
-// Activation quantization, K-quant convention (kquant.rs:418-441). One thread
-// per (group g, row). Writes
+// Activation quantization, K-quant convention (kquant.rs:418-441): per row and
+// 16-wide group g, amax = max |v| (NaN ignored), s = amax / 127, q =
+// clamp(round_half_away(v / s), -127, 127) with NaN -> 0, gsum = sum q (all
+// zero when amax == 0). Writes
 //   afrag: bf16 integers in the 16x16x16 MFMA A-operand layout, per
 //          (16-row tile mt, super-block sb, group pair gp) 64 lanes x 16 bytes:
 //          lane l = row % 16 + 16 c holds K 4c..4c+3 of group 2gp (bytes 0..7)
@@ -131,155 +133,102 @@ __global__ void vk_dequantize_q6k(const uint8_t* __restrict__ bytes, size_t nsb,
 //          + g % 4 (so a matmul lane reads its group's pair with one 8-byte
 //          load).
 // Rows m..m_pad-1 are written as zeros.
-// One group's activation pass: the 16 values v of (row, group g) -> its
-// fragment words, s and gsum (zeros when !live: the padding rows).
-__device__ __forceinline__ void vk_q16_store(int row, int g, int m_pad, int nsb, const float (&v)[16], bool live,
-                                             uint2* __restrict__ afrag, float* __restrict__ ascale) {
-    int r[16];
+// One element of the pass, formed by the 16 lanes of its group together (an
+// aligned run of 16 lanes, lane t holding element t of the group; v = 0 on
+// the padding rows, which gives their zeros): the group's amax (NaN -> 0,
+// then an integer max of the non-negative values: the same as a fmaxf chain
+// from 0), s, q and integer sum, q's bf16 into its fragment slot, and from
+// lane t = 0 the (s, gsum) pair.
+__device__ __forceinline__ void vk_q16_lane(int row, int g, int t, float v, int m_pad, int nsb,
+                                            uint2* __restrict__ afrag, float* __restrict__ ascale) {
+    const float amax = vk_group_max<16>(fmaxf(0.0f, fabsf(v)));
     float s = 0.0f;
-    int gsum = 0;
-#pragma unroll
-    for (int t = 0; t < 16; ++t) r[t] = 0;
-    if (live) {
-        float amax = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 16; ++t) amax = fmaxf(amax, fabsf(v[t]));
-        if (amax != 0.0f) {
-            s = amax / 127.0f;
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const float q = vk_round_half_away(v[t] / s);
-                // clamp(-127, 127) keeps NaN; `as i32` then maps NaN to 0
-                r[t] = (q != q) ? 0 : (int)fminf(fmaxf(q, -127.0f), 127.0f);
-                gsum += r[t];
-            }
-        }
+    int r = 0;
+    if (amax != 0.0f) {
+        s = amax / 127.0f;
+        const float q = vk_round_half_away(v / s);
+        // clamp(-127, 127) keeps NaN; `as i32` then maps NaN to 0
+        r = (q != q) ? 0 : (int)fminf(fmaxf(q, -127.0f), 127.0f);
     }
+    const int gsum = vk_group_sum_i<16>(r);
     const int mt = row >> 4, sb = g / kq::NG, gi = g % kq::NG;
     const size_t base = ((((size_t)mt * nsb + sb) * 8 + (gi >> 1)) * 64) * 2 + (gi & 1);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int lane = (row & 15) + 16 * c;
-        const uint2 w = make_uint2(vk_int_to_bf16_bits(r[4 * c]) | (vk_int_to_bf16_bits(r[4 * c + 1]) << 16),
-                                   vk_int_to_bf16_bits(r[4 * c + 2]) | (vk_int_to_bf16_bits(r[4 * c + 3]) << 16));
-        afrag[base + (size_t)lane * 2] = w;
+    const int lane = (row & 15) + 16 * (t >> 2);
+    reinterpret_cast<uint16_t*>(afrag)[(base + (size_t)lane * 2) * 4 + (t & 3)] = (uint16_t)vk_int_to_bf16_bits(r);
+    if (t == 0) {
+        const size_t si = ((size_t)(g >> 2) * m_pad + row) * 4 + (g & 3);
+        reinterpret_cast<float2*>(ascale)[si] = make_float2(s, (float)gsum);
     }
-    const size_t si = ((size_t)(g >> 2) * m_pad + row) * 4 + (g & 3);
-    reinterpret_cast<float2*>(ascale)[si] = make_float2(s, (float)gsum);
 }
 
-__global__ void vk_quantize_act_g16(const float* __restrict__ a, int m, int m_pad, int k,
-                                    uint2* __restrict__ afrag, float* __restrict__ ascale) {
-    const int ng = k / 16, nsb = k / kq::QK;
-    // (g, row) of this thread in 32-bit arithmetic (ng * m_pad < 2^31)
-    const unsigned gid = blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (unsigned)(ng * m_pad)) return;
-    const int g = (int)(gid / (unsigned)m_pad), row = (int)(gid - (unsigned)g * (unsigned)m_pad);
-    float v[16];
-    if (row < m) {
-        const float4* src = reinterpret_cast<const float4*>(a + (size_t)row * k + 16 * g);
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            const float4 x = src[h];
-            v[4 * h] = x.x;
-            v[4 * h + 1] = x.y;
-            v[4 * h + 2] = x.z;
-            v[4 * h + 3] = x.w;
-        }
-    }
-    vk_q16_store(row, g, m_pad, nsb, v, row < m, afrag, ascale);
+// The pass over an f32 matrix: one thread per element, grid (k / 256, m_pad).
+__global__ __launch_bounds__(256) void vk_quantize_act_g16(const float* __restrict__ a, int m, int m_pad, int k,
+                                                           uint2* __restrict__ afrag, float* __restrict__ ascale) {
+    const int row = blockIdx.y, col = blockIdx.x * 256 + threadIdx.x;
+    const float v = row < m ? a[(size_t)row * k + col] : 0.0f;
+    vk_q16_lane(row, col >> 4, col & 15, v, m_pad, k / kq::QK, afrag, ascale);
 }
 
-// RMSNorm fused with the activation pass, one workgroup per row (rows m ..
-// m_pad-1 write the zero padding): the row's sum of squares exactly as
-// vk_rms_norm_f32 forms it (thread t sums columns t, t + 256, ... in order,
-// then vk_block_sum256), y = x * inv * gamma, then each 16-wide group as
-// vk_quantize_act_g16 would quantize y. Bit-identical to the two launches.
-constexpr int kRmsRowLds = 2048;  // rows up to this many columns are read once
+// RMSNorm fused with the activation pass, grid (m_pad, k / 256): each
+// workgroup forms its row's sum of squares exactly as vk_rms_norm_f32 forms
+// it (thread t sums columns t, t + 256, ... in order, then vk_block_sum256),
+// y = x * inv * gamma, and quantizes its 256-column slice of y as
+// vk_quantize_act_g16 would, one element per thread (thread t's element,
+// column 256 * slice + t, is one it summed). Rows m .. m_pad-1 write the zero
+// padding. Bit-identical to the two launches.
+constexpr int kRmsRowRegs = 2048;  // rows up to this many columns are read once, into registers
 __global__ __launch_bounds__(256) void vk_rms_quantize_g16(const float* __restrict__ in,
                                                            const float* __restrict__ gamma, float eps, int m,
                                                            int m_pad, int k, uint2* __restrict__ afrag,
                                                            float* __restrict__ ascale) {
     __shared__ float red[4];
-    __shared__ __align__(16) float xs[kRmsRowLds];
-    const int row = blockIdx.x, nsb = k / kq::QK;
+    const int row = blockIdx.x, part = blockIdx.y, col = part * 256 + (int)threadIdx.x;
     const bool live = row < m;  // uniform per workgroup
-    float inv = 0.0f;
     const float* ir = in + (size_t)row * k;
-    if (k <= kRmsRowLds) {
-        // the row is read once: thread t loads columns t, t + 256, ... (its
-        // gamma group is requested first), sums their squares in that order
-        // as vk_sumsq_cols256 does and parks them in LDS for the group pass
-        const int g = threadIdx.x;
-        float gm[16];
-        if (live && g < k / 16) {
+    float v = 0.0f;
+    if (live) {
+        const float gc = gamma[col];  // requested ahead of the reduction
+        float inv, xc = 0.0f;
+        if (k <= kRmsRowRegs) {
+            // the row read once: every column requested together
+            float x[kRmsRowRegs / 256];
 #pragma unroll
-            for (int t = 0; t < 16; ++t) gm[t] = gamma[16 * g + t];
-        }
-        if (live) {
-            float x[kRmsRowLds / 256];
-#pragma unroll
-            for (int j = 0; j < kRmsRowLds / 256; ++j) {
+            for (int j = 0; j < kRmsRowRegs / 256; ++j) {
                 const int c = (int)threadIdx.x + 256 * j;
                 x[j] = c < k ? ir[c] : 0.0f;
             }
             float sq = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kRmsRowLds / 256; ++j) {
-                const int c = (int)threadIdx.x + 256 * j;
-                if (c < k) {
-                    sq += x[j] * x[j];
-                    xs[c] = x[j];
-                }
+            for (int j = 0; j < kRmsRowRegs / 256; ++j) {
+                if ((int)threadIdx.x + 256 * j < k) sq += x[j] * x[j];
+                if (j == part) xc = x[j];
             }
-            // the reduction's barriers also order the LDS row
             inv = 1.0f / sqrtf(vk_block_sum256(sq, red) / (float)k + eps);
+        } else {
+            inv = 1.0f / sqrtf(vk_block_sum256(vk_sumsq_cols256(ir, k), red) / (float)k + eps);
+            xc = ir[col];
         }
-        if (g < k / 16) {
-            float v[16];
-            if (live) {
-#pragma unroll
-                for (int t = 0; t < 16; ++t) v[t] = xs[16 * g + t] * inv * gm[t];
-            }
-            vk_q16_store(row, g, m_pad, nsb, v, live, afrag, ascale);
-        }
-        return;
+        v = xc * inv * gc;
     }
-    if (live) {
-        inv = 1.0f / sqrtf(vk_block_sum256(vk_sumsq_cols256(ir, k), red) / (float)k + eps);
-    }
-    for (int g = threadIdx.x; g < k / 16; g += 256) {
-        float v[16];
-        if (live) {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) v[t] = ir[16 * g + t] * inv * gamma[16 * g + t];
-        }
-        vk_q16_store(row, g, m_pad, nsb, v, live, afrag, ascale);
-    }
+    vk_q16_lane(row, col >> 4, col & 15, v, m_pad, k / kq::QK, afrag, ascale);
 }
 
-// SwiGLU fused with the activation pass: one thread per (group, row), the
-// 16 values silu(g) * u formed as vk_swiglu_f32 forms them, then quantized as
-// vk_quantize_act_g16 would. Bit-identical to the two launches.
-__global__ void vk_swiglu_quantize_g16(const float* __restrict__ gt, const float* __restrict__ up, int m, int m_pad,
-                                       int k, uint2* __restrict__ afrag, float* __restrict__ ascale) {
-    const int ng = k / 16, nsb = k / kq::QK;
-    // (g, row) of this thread in 32-bit arithmetic (ng * m_pad < 2^31)
-    const unsigned gid = blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (unsigned)(ng * m_pad)) return;
-    const int g = (int)(gid / (unsigned)m_pad), row = (int)(gid - (unsigned)g * (unsigned)m_pad);
-    float v[16];
+// SwiGLU fused with the activation pass: one thread per element, grid
+// (k / 256, m_pad), silu(g) * u formed as vk_swiglu_f32 forms it, then
+// quantized as vk_quantize_act_g16 would. Bit-identical to the two launches.
+__global__ __launch_bounds__(256) void vk_swiglu_quantize_g16(const float* __restrict__ gt,
+                                                              const float* __restrict__ up, int m, int m_pad, int k,
+                                                              uint2* __restrict__ afrag, float* __restrict__ ascale) {
+    const int row = blockIdx.y, col = blockIdx.x * 256 + threadIdx.x;
+    float v = 0.0f;
     if (row < m) {
-        const size_t o = (size_t)row * k + 16 * g;
-#pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            const float x = gt[o + t];
-            const float sg = 1.0f / (1.0f + expf(-x));
-            const float tt = x * sg;
-            v[t] = tt * up[o + t];
-        }
+        const size_t o = (size_t)row * k + col;
+        const float x = gt[o];
+        const float sg = 1.0f / (1.0f + expf(-x));
+        const float tt = x * sg;
+        v = tt * up[o];
     }
-    vk_q16_store(row, g, m_pad, nsb, v, row < m, afrag, ascale);
+    vk_q16_lane(row, col >> 4, col & 15, v, m_pad, k / kq::QK, afrag, ascale);
 }
 
 // ---------------------------------------------------------------------------
@@ -733,28 +682,27 @@ hipError_t launch_repack_w_kq8(hipStream_t s, int wdtype, const uint8_t* wq, int
 
 hipError_t launch_quantize_act_g16(hipStream_t s, const float* a, int m, int m_pad, int k, uint4* afrag,
                                    float* ascale) {
-    const size_t threads = (size_t)(k / 16) * m_pad;
-    if (threads == 0) return hipSuccess;
-    if (threads > (size_t)INT32_MAX) return hipErrorInvalidValue;  // the kernel indexes in 32 bits
-    hipLaunchKernelGGL(vk_quantize_act_g16, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a, m, m_pad,
-                       k, reinterpret_cast<uint2*>(afrag), ascale);
+    if (k % kq::QK != 0 || m_pad % 16 != 0 || m_pad > 65535) return hipErrorInvalidValue;
+    if (k == 0 || m_pad == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_quantize_act_g16, dim3((unsigned)(k / 256), (unsigned)m_pad), dim3(256), 0, s, a, m,
+                       m_pad, k, reinterpret_cast<uint2*>(afrag), ascale);
     return hipGetLastError();
 }
 
 hipError_t launch_rms_quantize_g16(hipStream_t s, const float* in, const float* gamma, float eps, int m, int m_pad,
                                    int k, uint4* afrag, float* ascale) {
-    if (m_pad == 0) return hipSuccess;
-    hipLaunchKernelGGL(vk_rms_quantize_g16, dim3((unsigned)m_pad), dim3(256), 0, s, in, gamma, eps, m, m_pad, k,
-                       reinterpret_cast<uint2*>(afrag), ascale);
+    if (k % kq::QK != 0 || m_pad % 16 != 0 || k / 256 > 65535) return hipErrorInvalidValue;
+    if (k == 0 || m_pad == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_rms_quantize_g16, dim3((unsigned)m_pad, (unsigned)(k / 256)), dim3(256), 0, s, in, gamma,
+                       eps, m, m_pad, k, reinterpret_cast<uint2*>(afrag), ascale);
     return hipGetLastError();
 }
 
 hipError_t launch_swiglu_quantize_g16(hipStream_t s, const float* g, const float* u, int m, int m_pad, int k,
                                       uint4* afrag, float* ascale) {
-    const size_t threads = (size_t)(k / 16) * m_pad;
-    if (threads == 0) return hipSuccess;
-    if (threads > (size_t)INT32_MAX) return hipErrorInvalidValue;  // the kernel indexes in 32 bits
-    hipLaunchKernelGGL(vk_swiglu_quantize_g16, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, g, u, m,
+    if (k % kq::QK != 0 || m_pad % 16 != 0 || m_pad > 65535) return hipErrorInvalidValue;
+    if (k == 0 || m_pad == 0) return hipSuccess;
+    hipLaunchKernelGGL(vk_swiglu_quantize_g16, dim3((unsigned)(k / 256), (unsigned)m_pad), dim3(256), 0, s, g, u, m,
                        m_pad, k, reinterpret_cast<uint2*>(afrag), ascale);
     return hipGetLastError();
 }

@@ -1137,7 +1137,7 @@ __global__ void vk_paged_attn_combine(int n_split, int hq, const int* __restrict
     if constexpr (Q16) {
         // the K-quant activation pass over this head's slice of the output
         // row: 16 consecutive threads hold one 16-wide group, quantized as
-        // vk_q16_store quantizes it (amax / 127, round half away, clamp,
+        // vk_q16_lane quantizes it (amax / 127, round half away, clamp,
         // integer group sum)
         const int row = (int)(ih / hq), h = (int)(ih % hq);
         const int g = h * (HD / 16) + (e >> 4), t = e & 15;

@@ -22,7 +22,7 @@ struct VkQOut {
     int m_pad;  // the fragments' padded row count
     int k;      // the quantized row width (a multiple of 32)
     int pow2;   // the power-of-two scale convention
-    int g16;    // the K-quant layout instead: 16-wide groups (vk_q16_store), m_pad a multiple of 16,
+    int g16;    // the K-quant layout instead: 16-wide groups (vk_q16_lane), m_pad a multiple of 16,
                 // (scale, sum) pairs in ascale (asum not used by it)
 };
 // One linear of a multi-linear block-GEMM launch: bf16 fragments + scales,
