@@ -244,10 +244,8 @@ __global__ void vk_quantize_act_b32(const float* __restrict__ a, int m, int m_pa
 //  * TILE: a workgroup takes a 16-row fragment tile, row after row, stages
 //    the bf16 operands in LDS in fragment order ((k / 32) KiB, dynamic) and
 //    stores the tile as contiguous 1 KiB fragments;
-//  * otherwise (a decode-sized batch): grid (m_pad, ceil(k / 256)); each
-//    workgroup forms its row's statistics and quantizes its 256-column slice
-//    (thread t's column t + 256 * slice), operands stored straight to the
-//    fragments.
+//  * otherwise (a decode-sized batch): one row per workgroup, operands stored
+//    straight to the fragments.
 // Rows m .. m_pad-1 are zeros.
 static_assert(kLnQuantMaxK <= kLnRegCols, "the fused pass holds its row in registers");
 template <bool POW2, bool TILE>
@@ -302,7 +300,6 @@ __global__ __launch_bounds__(256) void vk_ln_quantize_b32(const float* __restric
         for (int j = 0; j < kLnRegJ; ++j) {
             const int c = t + 256 * j;
             if (c - (t & 31) >= k) break;  // k is a multiple of 32: whole half-waves
-            if (!TILE && j != (int)blockIdx.y) continue;  // another workgroup's slice (uniform)
             const float v = live ? vk_ln_apply(x[j], st, gv[j], bv[j]) : 0.0f;
             // from 0 and through fmaxf, as the separate pass: NaN elements are ignored
             const float amax = vk_group_max<32>(fmaxf(0.0f, fabsf(v)));
@@ -755,7 +752,7 @@ hipError_t launch_ln_quantize_b32(hipStream_t s, bool pow2, const float* a, int 
     // chip with workgroups that stage whole tiles for contiguous stores
     const bool tile = m_pad / 16 >= 1024;
     const size_t lds = tile ? (size_t)(k / 32) * 1024 : 0;
-    const dim3 grid(tile ? m_pad / 16 : m_pad, tile ? 1 : (k + 255) / 256), block(256);
+    const dim3 grid(tile ? m_pad / 16 : m_pad), block(256);
     if (pow2 && tile)
         hipLaunchKernelGGL((vk_ln_quantize_b32<true, true>), grid, block, lds, s, a, m, m_pad, k, gamma, beta, eps,
                            afrag, ascale, asum);
