@@ -472,12 +472,16 @@ template <int MODE, bool POW2, bool DEV>
 static hipError_t go(hipStream_t s, const uint4* afrag, const float* ascale, const float* asum, const GemvSet& set,
                      const VkGemvLin* dlins, int n_lin, int n_max, int m, int nb, int m_pad) {
     const int n_tiles = (n_max + 15) / 16, m_tiles = (m + 15) / 16;
-    if (DEV || (size_t)n_tiles * m_tiles * n_lin >= (size_t)kWptMinTiles)
-        hipLaunchKernelGGL((vk_gemv_qblock_w<MODE, POW2, DEV>), dim3(n_tiles, m_tiles, n_lin), dim3(64), 0, s, afrag,
-                           ascale, asum, set, dlins, m, nb, m_pad);
-    else
-        hipLaunchKernelGGL((vk_gemv_qblock<MODE, POW2, DEV>), dim3(n_tiles, m_tiles, n_lin), dim3(256), 0, s, afrag,
-                           ascale, asum, set, dlins, m, nb, m_pad);
+    // linears from a device array always run the wave-per-tile kernel
+    if constexpr (!DEV) {
+        if ((size_t)n_tiles * m_tiles * n_lin < (size_t)kWptMinTiles) {
+            hipLaunchKernelGGL((vk_gemv_qblock<MODE, POW2, false>), dim3(n_tiles, m_tiles, n_lin), dim3(256), 0, s,
+                               afrag, ascale, asum, set, dlins, m, nb, m_pad);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((vk_gemv_qblock_w<MODE, POW2, DEV>), dim3(n_tiles, m_tiles, n_lin), dim3(64), 0, s, afrag,
+                       ascale, asum, set, dlins, m, nb, m_pad);
     return hipGetLastError();
 }
 
