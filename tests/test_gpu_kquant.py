@@ -101,6 +101,38 @@ def test_gemm_q4k_bit_exact(ctx, oracle, m, n, k, with_bias):
     assert same_bits(got, want)
 
 
+def test_gemm_q4k_activation_edge_values(ctx, oracle):
+    """The K-quant activation pass (kquant.rs:418-441: amax over the group
+    with NaN ignored, s = amax / 127, q = clamp(round(v / s)) with NaN -> 0,
+    integer group sum) on groups random inputs do not reach, through the
+    matmul, bit-exact: an all-NaN group (amax 0: s = 0, every q 0), one NaN
+    in a normal group, +Inf and -Inf elements (s = inf, every q 0, so the
+    row's outputs are NaN in the same places), exact half ties of v / s
+    (round half away from zero), a subnormal-only group, groups near the
+    largest finite value, and a row count that leaves padding rows."""
+    print("[case] q4k gemm activation edge values", flush=True)
+    m, n, k = 21, 48, 512
+    g = np.random.default_rng(77)
+    a = g.standard_normal((m, k)).astype(np.float32)
+    a[0, :16] = 0.0
+    a[1, 16:32] = np.nan
+    a[1, 40] = np.nan
+    a[2, 48] = np.inf
+    a[3, 64] = -np.inf
+    # amax = 127 / 8, so s = 1/8 exactly and v / s = these values exactly
+    ties = np.array([127, 63.5, -63.5, 0.5, -0.5, 1.5, -2.5, 126.5, -126.5, 3, 0, 7.5, -7.5, 100.5, -0.25, 0.75])
+    a[4, 80:96] = (ties / 8).astype(np.float32)
+    a[5, 96:112] = (np.arange(16) - 8).astype(np.float32) * np.float32(1e-40)
+    a[6, 112:128] = (np.finfo(np.float32).max * (g.random(16) * 2 - 1)).astype(np.float32)
+    a[7, 128:144] = np.float32(np.finfo(np.float32).max)
+    w = q4k_weights(0x77, n, k)
+    got = ctx.gemm_q_f32(m, n, k, a, w, hip.WDtype.Q4_K)
+    want = oracle.gemm_q_f32(W_Q4_K, m, n, k, a, w, None)
+    assert np.isnan(want[2]).all() and np.isnan(want[3]).all()  # the Inf rows
+    assert np.isfinite(want[[0, 1, 4, 5]]).all()
+    assert same_bits(got, want)
+
+
 def test_gemm_q4k_equals_repeated_gemv(ctx):
     """GEMM == n_act independent GEMVs bit for bit (kquant_gemm_parity.rs:129-160)."""
     print("[case] q4k gemm == repeated gemv", flush=True)

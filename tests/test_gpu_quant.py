@@ -158,6 +158,44 @@ def test_gemm_q_block_bit_exact(ctx, oracle, wd, act, m, n, k):
     assert np.array_equal(bits(got), bits(want))
 
 
+@pytest.mark.parametrize("act", [hip.ActQuant.AMAX127, hip.ActQuant.POW2])
+def test_gemm_q_activation_edge_values(ctx, oracle, act):
+    """The 32-wide block activation pass on blocks random inputs do not
+    reach, through the matmul, bit-exact (NaN outputs in the same places):
+    an all-NaN block (amax 0: s = 0, every q 0), one NaN in a normal block
+    (ignored by the maximum, quantized to 0), exact half ties of v / s (round
+    half away from zero), a subnormal-only block, and a row count that leaves
+    padding rows. With AMAX127 (kquant.rs:418-441 at group 32) also +Inf and
+    -Inf elements (s = inf, every q 0, so the row's outputs are NaN); the
+    build-defined POW2 scale of an infinite maximum rests on frexp's
+    unspecified exponent for inf, so that case stays out of its run."""
+    print(f"[case] gemm_q activation edge values act={act.name}", flush=True)
+    m, n, k = 21, 40, 256
+    a, wq, _ = _gemm_case(oracle, hip.WDtype.Q8_0, m, n, k, seed=21, with_bias=False, zero_rows=(0,))
+    a[1, 32:64] = np.nan
+    a[1, 70] = np.nan
+    # amax = 127 / 8, so s = 1/8 exactly (also the POW2 scale) and v / s is exact
+    ties = np.array([127, 63.5, -63.5, 0.5, -0.5, 1.5, -2.5, 126.5, -126.5, 3, 0, 7.5, -7.5, 100.5, -0.25, 0.75] * 2)
+    a[4, 96:128] = (ties / 8).astype(np.float32)
+    a[5, 128:160] = (np.arange(32) - 16).astype(np.float32) * np.float32(1e-40)
+    inf_rows = act == hip.ActQuant.AMAX127
+    if inf_rows:
+        a[2, 160] = np.inf
+        a[3, 200] = -np.inf
+    ctx.set_act_quant(act)
+    try:
+        got = ctx.gemm_q_f32(m, n, k, a, wq, hip.WDtype.Q8_0)
+    finally:
+        ctx.set_act_quant(hip.ActQuant.AMAX127)
+    want = oracle.gemm_qblock_i8(int(hip.WDtype.Q8_0), m, n, k, a, wq, None, pow2=(act == hip.ActQuant.POW2))
+    if inf_rows:
+        assert np.isnan(want[2]).all() and np.isnan(want[3]).all()
+    assert np.isfinite(want[[0, 1, 4, 5]]).all()
+    nw, ng = np.isnan(want), np.isnan(got)
+    assert np.array_equal(nw, ng)
+    assert np.array_equal(bits(got[~ng]), bits(want[~nw]))
+
+
 def test_gemm_q_config1_rows_bit_exact(ctx, oracle):
     """Config-1 shape (M=1500, K=1280, N=5120): every output of 24 sampled
     rows (first, last, interior) bit-exact vs the oracle, and whole-matrix
