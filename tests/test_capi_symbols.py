@@ -34,6 +34,14 @@ def test_library_exports_every_declared_symbol():
     assert not missing, f"declared but not exported: {missing}"
 
 
+def test_integration_ffi_table_binds_every_declared_symbol():
+    """INTEGRATION.md's dlsym table for the reference-side crate (fields named
+    without the vokra_hip_ prefix) has an entry for every declared function."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    missing = [n for n in declared_symbols() if f"pub {n[len('vokra_hip_'):]}:" not in text]
+    assert not missing, f"declared but absent from the FFI table: {missing}"
+
+
 def test_missing_device_is_backend_unavailable():
     """Without a GPU the probe fails loudly (BackendUnavailable), never a CPU path."""
     from vokra_amd import hip
