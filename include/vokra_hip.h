@@ -85,20 +85,26 @@ typedef struct vokra_hip_event vokra_hip_event_t;
 int vokra_hip_probe(int *n_devices);
 
 /* Context on one device with its own default-priority stream. Replaces
- * CudaContext::new (crates/vokra-backend-cuda/src/context.rs:1167). */
+ * CudaContext::new (crates/vokra-backend-cuda/src/context.rs:1167);
+ * destroy replaces its Drop (:4769). */
 int vokra_hip_create(int device, vokra_hip_ctx_t **out);
 void vokra_hip_destroy(vokra_hip_ctx_t *ctx);
 
-/* Message of the last failed call on this thread ("" if none). */
+/* Message of the last failed call on this thread ("" if none). Replaces
+ * vokra_last_error (include/vokra.h:455): per thread, never fails. */
 const char *vokra_hip_last_error(void);
 
-/* Blocks until the context stream drains; reports asynchronous faults, and
+/* Blocks until the context stream drains (the CUDA context's sync_stream,
+ * crates/vokra-backend-cuda/src/context.rs:4711); reports asynchronous faults, and
  * INVALID_ARGUMENT when an attention kernel met an operand outside its fp16
  * range since the last such check (the flag is per device and is cleared by
  * the report). */
 int vokra_hip_synchronize(vokra_hip_ctx_t *ctx);
 
 /* ---- device memory and timing (resident mode plumbing) ------------------ */
+/* Raw-byte forms of CudaContext::alloc_dev / upload / download
+ * (crates/vokra-backend-cuda/src/context.rs:3162-3215), synchronous copies.
+ * The events have no reference counterpart: measurement plumbing. */
 int vokra_hip_device_alloc(vokra_hip_ctx_t *ctx, size_t bytes, void **dptr);
 int vokra_hip_device_free(vokra_hip_ctx_t *ctx, void *dptr);
 int vokra_hip_memcpy_htod(vokra_hip_ctx_t *ctx, void *dst, const void *src, size_t bytes);
@@ -175,10 +181,12 @@ int vokra_hip_gemm_q_f32(vokra_hip_ctx_t *ctx, int wdtype, size_t m, size_t n, s
                          size_t a_len, const uint8_t *wq, size_t wq_len, const float *bias, float *out,
                          size_t out_len);
 
-/* Activation convention for the block-format INT8 path of this context. */
+/* Activation convention for the block-format INT8 path of this context. No
+ * reference counterpart: the reference has no block-format INT8 route (its
+ * one INT8 route is the K-quant one, which always uses KQUANT). */
 int vokra_hip_set_act_quant(vokra_hip_ctx_t *ctx, int act_quant);
 
-/* Kernel routing for m <= 64 (default 1 = the decode kernel that streams the
+/* No reference counterpart. Kernel routing for m <= 64 (default 1 = the decode kernel that streams the
  * compact weights; 0 = the tiled GEMM). Both give bit-identical results; the
  * switch exists so callers and tests can compare them. */
 int vokra_hip_set_decode_kernel(vokra_hip_ctx_t *ctx, int enable);
@@ -357,7 +365,8 @@ int vokra_hip_kv_append(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t layer, 
 /* Same with device arrays, asynchronous; the outcome is read by kv_status. */
 int vokra_hip_kv_append_dev(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t layer, size_t n,
                             const int32_t *d_streams, const int32_t *d_times, const float *d_k, const float *d_v);
-/* Synchronizes and returns the last append's status (n_appended items done). */
+/* Synchronizes and returns the last append's status (n_appended items done):
+ * append_step's result (paged_quant.rs:396-437) for the asynchronous form. */
 int vokra_hip_kv_status(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t *n_appended);
 
 /* read_step (paged_quant.rs:448-480): dequantized rows, *found = 0 for None. */
@@ -366,9 +375,10 @@ int vokra_hip_kv_read(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t layer, si
 /* reset (paged_quant.rs:489-493) and release_layer (:500-515). */
 int vokra_hip_kv_reset(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv);
 int vokra_hip_kv_release_layer(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t layer);
-/* free_pages / pages_in_use (paged_quant.rs:334-343). */
+/* free_pages / pages_in_use (paged_quant.rs:343-353). */
 int vokra_hip_kv_pages(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t *free_pages, size_t *pages_in_use);
-/* The page id of table entry (layer, t / block_size), -1 if none. */
+/* The page id of table entry (layer, t / block_size), -1 if none. No
+ * reference counterpart (inspection of page placement). */
 int vokra_hip_kv_page_of(vokra_hip_ctx_t *ctx, vokra_hip_kv_t *kv, size_t layer, size_t t, long *page);
 /* Resets the cache with the free list set to `order` (a permutation of the
  * page ids, top of the stack last): places pages at shuffled addresses. No
@@ -435,7 +445,8 @@ typedef struct vokra_hip_gguf vokra_hip_gguf_t;
 int vokra_hip_gguf_open(const char *path, vokra_hip_gguf_t **out);
 void vokra_hip_gguf_close(vokra_hip_gguf_t *f);
 int vokra_hip_gguf_tensor_count(const vokra_hip_gguf_t *f, size_t *n);
-/* GgufFile::tensors / tensor_bytes: name, ggml type tag, dims (up to 8, ggml
+/* GgufFile::tensors / tensor_bytes (crates/vokra-core/src/gguf/reader.rs:213,242):
+ * name, ggml type tag, dims (up to 8, ggml
  * order: dims[0] is the contiguous axis) and the payload inside the mapping. */
 int vokra_hip_gguf_tensor_info(const vokra_hip_gguf_t *f, size_t index, const char **name, uint32_t *ggml_type,
                                size_t *n_dims, uint64_t *dims, const void **data, size_t *n_bytes);
@@ -556,7 +567,8 @@ int vokra_hip_decoder_set_encoder_dev(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t 
 #define VOKRA_HIP_CROSS_F32 0
 #define VOKRA_HIP_CROSS_F16 1
 int vokra_hip_decoder_set_cross_precision(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, int precision);
-/* Empties the self-KV cache of every stream. */
+/* Empties the self-KV cache of every stream (DecoderStepSession::reset,
+ * crates/vokra-models/src/compute.rs:3073). */
 int vokra_hip_decoder_reset(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec);
 /* Resets the decoder (every stream back to length 0) with its self-KV cache's
  * free list set to `order`, a permutation of the cache's page ids (top of the
@@ -565,7 +577,7 @@ int vokra_hip_decoder_reset(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec);
  * with. Results do not depend on it. No reference counterpart (the reference
  * cache always starts from [cap-1 .. 0], paged_quant.rs:152-216). */
 int vokra_hip_decoder_set_free_order(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, const int32_t *order, size_t n);
-/* free_pages / pages_in_use of the decoder's self-KV cache (vokra_hip_kv_pages;
+/* free_pages / pages_in_use (paged_quant.rs:343-353) of the decoder's self-KV cache (vokra_hip_kv_pages;
  * their sum is the page count a free order must permute). */
 int vokra_hip_decoder_kv_pages(vokra_hip_ctx_t *ctx, vokra_hip_decoder_t *dec, size_t *free_pages,
                                size_t *pages_in_use);
