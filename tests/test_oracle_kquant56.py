@@ -1,7 +1,7 @@
 """The oracle's Q5_K and Q6_K (the rest of the reference's KQuantDtype,
 crates/vokra-backend-cpu/src/kernels/kquant.rs:56-63), pinned without it:
   * dequantize: the reference's own closed-form block tests
-    (crates/vokra-core/src/gguf/quant/q5_k.rs:84-170, q6_k.rs:76-160) and an
+    (crates/vokra-core/src/gguf/quant/q5_k.rs:84-167, q6_k.rs:76-160) and an
     independent numpy parse of random blocks, bit for bit;
   * the INT8 route (unpack_block_i8, kquant.rs:332-407): GEMM == repeated GEMV
     (kquant_gemm_parity.rs:129-160), == an independent exact-integer route

@@ -1,5 +1,5 @@
 """VoxtralConfig from GGUF metadata (vokra_hip_voxtral_config_from_gguf), the
-cases of crates/vokra-models/src/voxtral/config.rs:269-420: the legacy file
+cases of crates/vokra-models/src/voxtral/config.rs:269-399: the legacy file
 without a head_dim key (derived 3072 / 24 = 128), the shipping mini shape with
 an explicit head_dim that decouples q_hidden from hidden_dim, the
 divisibility rule that applies only to a derived head_dim, a missing required
