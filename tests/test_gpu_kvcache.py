@@ -223,6 +223,36 @@ def test_paged_attention_split_path(ctx, oracle):
         assert ok, (s, err)
 
 
+@pytest.mark.parametrize("H,hd,hq", [(2, 128, 16), (2, 64, 2), (2, 64, 8)])
+def test_paged_attention_contexts_beyond_4096(ctx, oracle, H, hd, hq):
+    """Contexts past 4096 keys, where an item's split grows to 1024 (and 1536)
+    keys: the matrix-core kernel's looped path (8 and 12 tiles per wave), the
+    VALU kernels' 4- to 6-chunk splits, a last split one key short, 5 to 8
+    splits through the combine; against the oracle, and an item alone ==
+    the same item in the batch, bit for bit."""
+    print(f"[case] paged attn beyond 4096 H={H} hd={hd} hq={hq}", flush=True)
+    lens = [4097, 6143, 8192, 8193]
+    n_stream, max_time, bs = len(lens), 8208, 16
+    kv = ctx.kv_cache(1, H, hd, n_stream, max_time, bs)
+    ref = oracle.PagedCache(1, H, hd, n_stream, max_time, bs, Q8_0)
+    rng = np.random.default_rng(4097 + hd + hq)
+    fill_cache(kv, ref, 0, lens, H * hd, rng, n_stream)
+    q = rng.standard_normal((n_stream, hq * hd)).astype(np.float32)
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    got = kv.attn(0, list(range(n_stream)), lens, q, hq, scale)
+    for s in range(n_stream):
+        K, V = cached_kv(ref, 0, s, lens[s])
+        if hq == H:
+            want = oracle.sdpa_whisper(1, lens[s], H, hd, q[s:s + 1], K, V, causal=True,
+                                       q_pos_offset=lens[s] - 1)[0]
+        else:
+            want = oracle.gqa_attention(1, lens[s], hq, H, hd, q[s:s + 1], K, V, scale, lens[s] - 1)[0]
+        ok, err = close(got[s], want.astype(np.float64))
+        assert ok, (s, err)
+        alone = kv.attn(0, [s], [lens[s]], q[s:s + 1], hq, scale)
+        assert np.array_equal(alone[0], got[s]), s
+
+
 def test_config3_self_attention_shape(ctx):
     """Config 3 decoder self-attention: 64 streams, 20 heads x 64, prefix
     lengths U(1..448), 16-token pages at shuffled addresses; checked in float64
