@@ -290,6 +290,36 @@ def test_text_decoder_config4_dims(ctx, oracle):
     print("[worst teacher-forced errors]", ops.worst, flush=True)
 
 
+def test_text_decoder_histories_beyond_4096(ctx, oracle):
+    """Histories past 4096 positions, where the attention splits grow to 1024
+    and 1536 keys: the steps cross 4096 -> 4097 keys (512- to 1024-key
+    splits), 5120 -> 5121 (the new key alone in the last split) and 8192 ->
+    8193 (1024- to 1536-key splits), so the K/V append and RoPE of the step
+    run in each kind of split. Session == entry points bit for bit, every
+    entry point teacher-forced against the oracle."""
+    print("[case] text decoder histories beyond 4096", flush=True)
+    d, hq, hkv, hd, ff, V, n_ctx, n_stream, n_layer = 1024, 8, 2, 128, 512, 96, 8704, 4, 2
+    dec, P = build(ctx, oracle, 31, n_layer, d, hq, hkv, hd, ff, V, n_ctx, n_stream)
+    ops = TextDecoderByOps(ctx, P, n_stream, check=oracle)
+    g = np.random.default_rng(31)
+    lens = [4095, 5119, 8191, 8600]
+    for s, n_pos in enumerate(lens):
+        k, v = history(g, n_layer, n_pos, hkv * hd)
+        dec.kv_restore(s, k, v)
+        ops.restore(s, k, v)
+    streams = list(range(n_stream))
+    tok = [int(t) for t in g.integers(0, V, n_stream)]
+    for step in range(3):
+        args = [tok[s] for s in streams]
+        nxt, logits = dec.step(streams, args, want_logits=True)
+        n2, l2 = ops.step(streams, args)
+        assert np.array_equal(logits, l2) and np.array_equal(nxt, n2), step
+        for i, s in enumerate(streams):
+            tok[s] = int(nxt[i])
+    assert [dec.position(s) for s in streams] == [n + 3 for n in lens]
+    print("[worst teacher-forced errors]", ops.worst, flush=True)
+
+
 def test_text_decoder_full_depth_equals_entry_points(ctx, oracle):
     """All 24 config-4 layers, 32 streams with histories U(512..4096): two
     batched steps are bit-identical to the entry-point chain."""
