@@ -179,7 +179,8 @@ def cached_kv(ref, layer, s, n):
     return np.stack([r[0] for r in rows]), np.stack([r[1] for r in rows])
 
 
-@pytest.mark.parametrize("H,hd,hq", [(4, 64, 4), (2, 128, 16), (2, 64, 8), (3, 128, 6)])
+@pytest.mark.parametrize("H,hd,hq", [(4, 64, 4), (2, 128, 16), (2, 64, 8), (3, 128, 6), (2, 64, 16), (2, 128, 2),
+                                     (2, 128, 8)])
 def test_paged_attention_vs_oracle(ctx, oracle, H, hd, hq):
     print(f"[case] paged attn H={H} hd={hd} hq={hq}", flush=True)
     n_stream, max_time, bs = 5, 300, 16

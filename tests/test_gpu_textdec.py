@@ -290,6 +290,26 @@ def test_text_decoder_config4_dims(ctx, oracle):
     print("[worst teacher-forced errors]", ops.worst, flush=True)
 
 
+def test_text_decoder_rows_wider_than_2048(ctx, oracle):
+    """d = 2304 (9 super-blocks): the RMSNorm + activation pass streams rows
+    wider than the 2048 columns it holds in registers, and the final RMSNorm
+    likewise. Session == entry points bit for bit, every entry point
+    teacher-forced against the oracle."""
+    print("[case] text decoder d=2304", flush=True)
+    d, hq, hkv, hd, ff, V, n_ctx, n_stream, n_layer = 2304, 4, 2, 64, 512, 64, 32, 2, 1
+    dec, P = build(ctx, oracle, 23, n_layer, d, hq, hkv, hd, ff, V, n_ctx, n_stream, bs=4)
+    ops = TextDecoderByOps(ctx, P, n_stream, check=oracle)
+    tok = [3, 7]
+    for step, streams in enumerate([[0, 1], [1], [0, 1], [1, 0]]):
+        args = [tok[s] for s in streams]
+        nxt, logits = dec.step(streams, args, want_logits=True)
+        n2, l2 = ops.step(streams, args)
+        assert np.array_equal(logits, l2) and np.array_equal(nxt, n2), (step, streams)
+        for i, s in enumerate(streams):
+            tok[s] = int(nxt[i])
+    print("[worst teacher-forced errors]", ops.worst, flush=True)
+
+
 def test_text_decoder_histories_beyond_4096(ctx, oracle):
     """Histories past 4096 positions, where the attention splits grow to 1024
     and 1536 keys: the steps cross 4096 -> 4097 keys (512- to 1024-key
