@@ -21,6 +21,7 @@ from vokra_amd import hip
 pytestmark = pytest.mark.gpu
 
 W_Q4_0, W_Q8_0, W_Q4_K = 2, 8, 12
+W_Q5_0, W_Q5_K, W_Q6_K = 6, 13, 14
 
 
 @pytest.fixture(scope="module")
@@ -31,10 +32,13 @@ def ctx():
 
 
 def pack(ctx, wd, w):
-    """f32 [n, k] -> wire bytes of `wd` (device packer; Q4_K via the oracle quantizer)."""
+    """f32 [n, k] -> wire bytes of `wd` (device packer; Q4_K via the oracle
+    quantizer; Q5_0, Q5_K and Q6_K as the oracle composition packs them)."""
+    from oracle import oracle as orc
     if wd == W_Q4_K:
-        from oracle import oracle as orc
         return orc.kquant_quantize(W_Q4_K, w.reshape(-1))
+    if wd in (W_Q5_0, W_Q5_K, W_Q6_K):
+        return model_oracle.quantize_weight(orc, wd, w)
     mode = {W_Q4_0: hip.KvQuant.Q4_0, W_Q8_0: hip.KvQuant.Q8_0}[wd]
     return ctx.quantize_bytes(mode, w)
 
@@ -78,7 +82,8 @@ def encoder_by_ops(ctx, wd, layers, lpg, lpb, x, H, ff):
 
 
 @pytest.mark.parametrize("wd,d,H,ff,T,B", [(W_Q8_0, 128, 2, 256, 70, 2), (W_Q4_0, 128, 2, 256, 64, 1),
-                                           (W_Q4_K, 256, 4, 512, 33, 1)])
+                                           (W_Q4_K, 256, 4, 512, 33, 1), (W_Q5_0, 128, 2, 256, 40, 1),
+                                           (W_Q5_K, 256, 4, 512, 33, 1), (W_Q6_K, 256, 4, 512, 33, 1)])
 def test_encoder_vs_oracle(ctx, oracle, wd, d, H, ff, T, B):
     print(f"[case] encoder wd={wd} d={d} H={H} T={T} B={B}", flush=True)
     g = np.random.default_rng(d + T + wd)
@@ -184,14 +189,17 @@ class DecoderByOps:
         return d_n.download(np.int32, n), d_l.download(np.float32, n * V).reshape(n, V)
 
 
-@pytest.mark.parametrize("wd", [W_Q4_0, W_Q8_0])
+@pytest.mark.parametrize("wd", [W_Q4_0, W_Q8_0, W_Q5_0, W_Q4_K, W_Q5_K, W_Q6_K])
 def test_decoder_step_equals_entry_points(ctx, oracle, wd):
     """A batched decoder step (fused LN + quantize, q split and activation
     pass inside the attention kernels, residual / GELU epilogues, fused
     logits) is bit-identical to the same step issued one entry point at a
-    time, over ragged batches."""
+    time, over ragged batches, for every weight format the session takes
+    (the K-quant ones at d = 256, their group size)."""
     print(f"[case] decoder == entry points wd={wd}", flush=True)
-    gpu, _ = make_decoder(ctx, oracle, np.random.default_rng(5), wd=wd)
+    kq = wd in (W_Q4_K, W_Q5_K, W_Q6_K)
+    gpu, _ = make_decoder(ctx, oracle, np.random.default_rng(5), wd=wd, d=256 if kq else 128, H=4 if kq else 2,
+                          ff=512 if kq else 256)
     ops = DecoderByOps(ctx, gpu.parts, 4)
     pos, tok = [0, 0, 0, 0], [1, 2, 3, 4]
     for streams in ([0, 1, 2, 3], [2, 0], [3, 1, 0, 2], [1]):
