@@ -211,12 +211,13 @@ def history(g, n_layer, n_pos, w, scale=1.0):
 
 
 @pytest.mark.parametrize("wd,tied,hkv", [(W_Q4_K, False, 2), (W_Q4_K, True, 2), (W_Q4_K, False, 4),
-                                         (W_Q8_0, False, 2), (W_Q8_0, True, 4), (13, False, 2), (14, True, 2)])
+                                         (W_Q8_0, False, 2), (W_Q8_0, True, 4), (2, False, 2), (6, True, 4),
+                                         (13, False, 2), (14, True, 2)])
 def test_text_decoder_small_vs_oracle(ctx, oracle, wd, tied, hkv):
     """Toy dims (d=256, 4 query heads x 64 over 2 kv heads, or 4 = no
     grouping): session == entry points bit for bit, teacher-forced entry
-    points vs the oracle, free-running vs the oracle. Q8_0 weights take the
-    block-format route of the step (RMSNorm and the block activation pass as
+    points vs the oracle, free-running vs the oracle. Q8_0 weights (and Q4_0
+    (2), Q5_0 (6)) take the block-format route of the step (RMSNorm and the block activation pass as
     two launches, a separate SwiGLU pass, RoPE as its own launch, paged
     attention without the rotation table); Q5_K (13) and Q6_K (14) the
     K-quant route with the byte-word matmul."""
