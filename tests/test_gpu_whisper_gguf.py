@@ -42,7 +42,8 @@ def metadata(cfg=CFG):
 class Model:
     """Random Whisper weights by reference tensor name (f32 truths) and the
     on-disk tensors: norms / biases / embeddings as F32 or F16, Linears as
-    `lin` ("q8_0": Q8_0 blocks, "f16": F16, packed at load, "q4_k")."""
+    `lin` (a block or K-quant format stored verbatim, or "f16" / "bf16",
+    packed at load into Q8_0)."""
 
     def __init__(self, ctx, oracle, lin, cfg=CFG):
         self.cfg, self.lin, self.t, self.disk = cfg, lin, {}, []
@@ -100,17 +101,28 @@ class Model:
                 self.disk.append((name, [d], gw.GGML_F32, a.tobytes()))
             self.t[name] = a
 
+    BLOCK = {"q8_0": (hip.KvQuant.Q8_0, gw.GGML_Q8_0), "q4_0": (hip.KvQuant.Q4_0, gw.GGML_Q4_0),
+             "q5_0": (hip.KvQuant.Q5_0, gw.GGML_Q5_0)}
+    KQUANT = {"q4_k": (W_Q4_K, gw.GGML_Q4_K), "q5_k": (13, gw.GGML_Q5_K), "q6_k": (14, gw.GGML_Q6_K)}
+    WD = {"q8_0": W_Q8_0, "q4_0": 2, "q5_0": 6, "q4_k": W_Q4_K, "q5_k": 13, "q6_k": 14, "f16": W_Q8_0, "bf16": W_Q8_0}
+
     def linear(self, p, n_in, n_out, bias=True):
         if bias:
             self.dense(f"{p}.bias", (n_out,), 0.05)
         w = (self.rng().standard_normal((n_out, n_in)) * 0.08).astype(np.float32)
         name = f"{p}.weight"
-        if self.lin == "q8_0":
-            wire = self.ctx.quantize_bytes(hip.KvQuant.Q8_0, w)
-            self.disk.append((name, [n_out, n_in], gw.GGML_Q8_0, bytes(wire)))
-        elif self.lin == "q4_k":
-            wire = self.oracle.kquant_quantize(W_Q4_K, w.reshape(-1))
-            self.disk.append((name, [n_out, n_in], gw.GGML_Q4_K, bytes(np.asarray(wire, np.uint8))))
+        if self.lin in self.BLOCK:
+            mode, tag = self.BLOCK[self.lin]
+            wire = self.ctx.quantize_bytes(mode, w)
+            self.disk.append((name, [n_out, n_in], tag, bytes(wire)))
+        elif self.lin in self.KQUANT:
+            wd, tag = self.KQUANT[self.lin]
+            wire = model_oracle.quantize_weight(self.oracle, wd, w)
+            self.disk.append((name, [n_out, n_in], tag, bytes(np.asarray(wire, np.uint8))))
+        elif self.lin == "bf16":  # BF16 on disk (truncated f32 bits); packed at load as F16 is
+            bits = (w.view(np.uint32) >> 16).astype(np.uint16)
+            self.disk.append((name, [n_out, n_in], gw.GGML_BF16, bits.tobytes()))
+            wire = self.ctx.quantize_bytes(hip.KvQuant.Q8_0, (bits.astype(np.uint32) << 16).view(np.float32))
         else:  # F16 on disk; the loader packs what F16 decodes to
             w16 = w.astype(np.float16)
             self.disk.append((name, [n_out, n_in], gw.GGML_F16, w16.tobytes()))
@@ -125,7 +137,7 @@ class Model:
 
     @property
     def wd(self):
-        return W_Q4_K if self.lin == "q4_k" else W_Q8_0
+        return self.WD[self.lin]
 
     def write(self, path, drop=None, replace=None):
         tensors = [t for t in self.disk if t[0] != drop]
@@ -174,7 +186,7 @@ def within(got, want, frac=0.1):
     return err <= frac * rms + 1e-4, err, rms
 
 
-@pytest.mark.parametrize("lin", ["q8_0", "f16", "q4_k"])
+@pytest.mark.parametrize("lin", ["q8_0", "f16", "q4_k", "q4_0", "q5_0", "q5_k", "q6_k", "bf16"])
 def test_sessions_from_gguf_equal_direct_construction(ctx, oracle, tmp_path, lin):
     print(f"[case] whisper gguf sessions, linears {lin}", flush=True)
     cfg = CFG
@@ -185,7 +197,7 @@ def test_sessions_from_gguf_equal_direct_construction(ctx, oracle, tmp_path, lin
     B, n_frames = 2, 2 * cfg["n_audio_ctx"]
 
     enc, rep = hip.Encoder.from_gguf(ctx, f, m.wd, max_rows=B * cfg["n_audio_ctx"])
-    assert rep == ({"verbatim": 0, "packed": n_lin} if lin == "f16" else {"verbatim": n_lin, "packed": 0})
+    assert rep == ({"verbatim": 0, "packed": n_lin} if lin in ("f16", "bf16") else {"verbatim": n_lin, "packed": 0})
     direct = hip.Encoder(ctx, m.wd, d, H, ff, m.enc_layers(), t["model.encoder.layer_norm.weight"],
                          t["model.encoder.layer_norm.bias"], max_rows=B * cfg["n_audio_ctx"])
     direct.set_stem(cfg["n_mels"], n_frames, t["model.encoder.conv1.weight"], t["model.encoder.conv1.bias"],
