@@ -398,7 +398,8 @@ def voxtral_gguf(path, P, prefix, n_ctx, tied, f16_norms=False, drop=None, repla
     from tests import gguf_writer as gw
     d, hq, hkv, hd, ff, V = P["d"], P["hq"], P["hkv"], P["hd"], P["ff"], P["V"]
     wd = P.get("wd", W_Q4_K)
-    gt = gw.GGML_Q4_K if wd == W_Q4_K else gw.GGML_Q8_0
+    gt = {W_Q4_K: gw.GGML_Q4_K, W_Q8_0: gw.GGML_Q8_0, 2: gw.GGML_Q4_0, 6: gw.GGML_Q5_0, 13: gw.GGML_Q5_K,
+          14: gw.GGML_Q6_K}[wd]
     m = [("vokra.voxtral." + k, t, v) for k, t, v in (
         ("audio_encoder.n_layer", gw.U32, 2), ("audio_encoder.hidden_dim", gw.U32, 256),
         ("audio_encoder.n_head", gw.U32, 4), ("audio_encoder.n_mels", gw.U32, 128),
@@ -443,7 +444,8 @@ def voxtral_gguf(path, P, prefix, n_ctx, tied, f16_norms=False, drop=None, repla
 
 
 @pytest.mark.parametrize("prefix,tied,wd", [("language_model.model.", False, W_Q4_K), ("model.", True, W_Q4_K),
-                                            ("language_model.", False, W_Q8_0)])
+                                            ("language_model.", False, W_Q8_0), ("model.", False, 6),
+                                            ("language_model.model.", False, 13), ("model.", True, 14)])
 def test_text_decoder_from_gguf_equals_direct(ctx, oracle, tmp_path, prefix, tied, wd):
     """vokra_hip_text_decoder_from_gguf (TextDecoder::load + VoxtralConfig::
     from_gguf) == the session built from the same arrays, bit for bit, over
