@@ -1,0 +1,111 @@
+"""Resident-mode entry points (device pointers, asynchronous on the context
+stream) against their copy-mode twins: the same kernels behind both, so the
+outputs must agree bit for bit. The copy-mode forms carry the parity tests
+against the oracle; this pins the device-pointer plumbing of each _dev form."""
+import numpy as np
+import pytest
+
+from vokra_amd import hip
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = hip.HipContext(0)
+    yield c
+    c.close()
+
+
+def dev(ctx, a):
+    return hip.DeviceBuffer.from_array(ctx, np.ascontiguousarray(a))
+
+
+def down(ctx, buf, dtype, n):
+    ctx.synchronize()
+    return buf.download(dtype, n)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).reshape(-1).view(np.uint32)
+
+
+def test_gemv_softmax_rms_swiglu_dev_equal_copy_mode(ctx):
+    print("[case] resident f32 kernels", flush=True)
+    g = np.random.default_rng(1)
+    m, k = 37, 300
+    a = g.standard_normal((m, k)).astype(np.float32)
+    x = g.standard_normal(k).astype(np.float32)
+    b = g.standard_normal(m).astype(np.float32)
+    out = hip.DeviceBuffer(ctx, m * 4)
+    ctx.gemv_f32_dev(m, k, dev(ctx, a), dev(ctx, x), out, dev(ctx, b))
+    assert np.array_equal(bits(down(ctx, out, np.float32, m)), bits(ctx.gemv_f32(m, k, a, x, b)))
+
+    rows, cols = 5, 777
+    s = (g.standard_normal((rows, cols)) * 4).astype(np.float32)
+    out = hip.DeviceBuffer(ctx, rows * cols * 4)
+    ctx.softmax_f32_dev(dev(ctx, s), out, rows, cols)
+    assert np.array_equal(bits(down(ctx, out, np.float32, rows * cols)), bits(ctx.softmax_f32(s, rows, cols)))
+
+    for cols in (2048, 2304):   # rows held in registers, and streamed
+        r = g.standard_normal((3, cols)).astype(np.float32)
+        gam = (1 + 0.1 * g.standard_normal(cols)).astype(np.float32)
+        out = hip.DeviceBuffer(ctx, 3 * cols * 4)
+        ctx.rms_norm_f32_dev(dev(ctx, r), out, 3, cols, dev(ctx, gam), 1e-5)
+        assert np.array_equal(bits(down(ctx, out, np.float32, 3 * cols)),
+                              bits(ctx.rms_norm_f32(r, 3, cols, gam, 1e-5)))
+
+    n = 10001
+    gate = (g.standard_normal(n) * 4).astype(np.float32)
+    up = g.standard_normal(n).astype(np.float32)
+    out = hip.DeviceBuffer(ctx, n * 4)
+    ctx.swiglu_f32_dev(dev(ctx, gate), dev(ctx, up), n, out)
+    assert np.array_equal(bits(down(ctx, out, np.float32, n)), bits(ctx.swiglu_f32(gate, up)))
+
+
+def test_conv1d_dev_equals_copy_mode(ctx):
+    print("[case] resident conv1d", flush=True)
+    g = np.random.default_rng(2)
+    in_ch, in_len, out_ch, kernel, stride, padding = 3, 50, 4, 3, 2, 1
+    x = g.standard_normal((in_ch, in_len)).astype(np.float32)
+    w = g.standard_normal((out_ch, in_ch, kernel)).astype(np.float32)
+    bias = g.standard_normal(out_ch).astype(np.float32)
+    want = ctx.conv1d_f32(x, in_ch, in_len, w, out_ch, kernel, bias, stride, padding)
+    out_len = (in_len + 2 * padding - kernel) // stride + 1
+    assert want.shape == (out_ch, out_len)
+    out = hip.DeviceBuffer(ctx, out_ch * out_len * 4)
+    ctx.conv1d_f32_dev(dev(ctx, x), in_ch, in_len, dev(ctx, w), out_ch, kernel, dev(ctx, bias), stride, padding, out)
+    assert np.array_equal(bits(down(ctx, out, np.float32, out_ch * out_len)), bits(want))
+
+
+@pytest.mark.parametrize("mode", [hip.KvQuant.Q4_0, hip.KvQuant.Q5_0, hip.KvQuant.Q8_0])
+def test_quantize_bytes_dev_equals_copy_mode(ctx, mode):
+    print(f"[case] resident quantize_bytes {mode.name}", flush=True)
+    g = np.random.default_rng(int(mode))
+    x = (g.standard_normal(32 * 301) * 3).astype(np.float32)
+    x[:32] = 0.0
+    want = ctx.quantize_bytes(mode, x)
+    out = hip.DeviceBuffer(ctx, want.size)
+    ctx.quantize_bytes_dev(mode, dev(ctx, x), x.size, out)
+    assert np.array_equal(down(ctx, out, np.uint8, want.size), want)
+
+
+def test_kv_append_dev_equals_copy_mode(ctx):
+    """Two caches fed the same batch, one through host arrays and one through
+    device arrays: the same pages, the same rows, the same status."""
+    print("[case] resident kv append", flush=True)
+    H, hd, n_stream, max_time, bs = 2, 64, 3, 24, 4
+    a = ctx.kv_cache(2, H, hd, n_stream, max_time, bs)
+    b = ctx.kv_cache(2, H, hd, n_stream, max_time, bs)
+    g = np.random.default_rng(3)
+    for layer, streams, times in ((1, [0, 2, 1], [0, 5, 9]), (0, [1, 1, 2], [3, 4, 23])):
+        k = g.standard_normal((3, H * hd)).astype(np.float32)
+        v = g.standard_normal((3, H * hd)).astype(np.float32)
+        a.append(layer, streams, times, k, v)
+        b.append_dev(layer, 3, dev(ctx, np.array(streams, np.int32)), dev(ctx, np.array(times, np.int32)),
+                     dev(ctx, k), dev(ctx, v))
+        assert b.status() == 3
+        assert a.pages() == b.pages()
+        for s, t in zip(streams, times):
+            ra, rb = a.read(layer, t, s), b.read(layer, t, s)
+            assert np.array_equal(bits(ra[0]), bits(rb[0])) and np.array_equal(bits(ra[1]), bits(rb[1]))

@@ -1059,6 +1059,13 @@ class HipContext:
                                         _ptr(cv, C.c_float), _ptr(out, C.c_float), m))
         return out[:m]
 
+    def gemv_f32_dev(self, m, k, d_a, d_x, d_out, d_bias=None):
+        _check(lib().vokra_hip_gemv_f32_dev(self._h, m, k, d_a.ptr, d_x.ptr, None if d_bias is None else d_bias.ptr,
+                                            d_out.ptr))
+
+    def softmax_f32_dev(self, d_in, d_out, rows, cols):
+        _check(lib().vokra_hip_softmax_f32_dev(self._h, d_in.ptr, d_out.ptr, rows, cols))
+
     def softmax_f32(self, x, rows, cols):
         xv = _f32(x).reshape(-1)
         out = np.zeros(max(xv.size, 1), np.float32)
@@ -1099,9 +1106,16 @@ class HipContext:
                                         C.c_float(rope_base), position_offset))
         return xv
 
+    def rms_norm_f32_dev(self, d_in, d_out, rows, cols, d_gamma, eps):
+        _check(lib().vokra_hip_rms_norm_f32_dev(self._h, d_in.ptr, d_out.ptr, rows, cols, d_gamma.ptr,
+                                                C.c_float(eps)))
+
     def rope_f32_dev(self, d_x, rows, n_head, head_dim, rope_base, d_positions):
         _check(lib().vokra_hip_rope_f32_dev(self._h, d_x.ptr, rows, n_head, head_dim, C.c_float(rope_base),
                                             d_positions.ptr))
+
+    def swiglu_f32_dev(self, d_gate, d_up, n, d_out):
+        _check(lib().vokra_hip_swiglu_f32_dev(self._h, d_gate.ptr, d_up.ptr, n, d_out.ptr))
 
     def swiglu_f32(self, gate, up):
         """silu(gate) * up (silu_inplace then hadamard_inplace)."""
