@@ -431,6 +431,59 @@ __host__ __device__ __forceinline__ int pa_splits(int len) {
     return len > k ? (len + k - 1) / k : 1;
 }
 
+// Fused append: the workgroup whose key range [k0, k1) holds the item's new
+// time step packs that step's K and V head slices into the cache first,
+// exactly as vk_kv_write would, then reads them back with the other keys. The
+// page comes from an earlier allocation launch. Called by every thread of the
+// workgroup (its barrier is uniform per workgroup).
+template <int HD>
+__device__ __forceinline__ void pa_append_slice(const KvDev& c, int layer, int s, int hk, int item, int k0, int k1,
+                                                const float* __restrict__ ak, const float* __restrict__ av,
+                                                const int* __restrict__ at, int wave, int lane) {
+    constexpr int NB = HD / 32;
+    const int t = at[item];
+    if (t < k0 || t >= k1) return;
+    const int pid = c.table[layer * c.ppl + t / c.bs];
+    if (pid >= 0 && wave < 2) {
+        const size_t hr = kv_hrow(c, pid, t, s, hk);
+        const float* src = (wave == 0 ? ak : av) + (size_t)item * c.width + (size_t)hk * HD;
+        int8_t* dq = (wave == 0 ? c.kq : c.vq) + hr * HD;
+        uint16_t* dd = (wave == 0 ? c.kd : c.vd) + hr * NB;
+#pragma unroll
+        for (int e = lane; e < HD; e += 64) {
+            int8_t qb;
+            uint16_t db = 0;
+            q8_0_pack_lane(src[e], e & 31, &qb, &db);
+            dq[e] = qb;
+            if ((e & 31) == 0) dd[e >> 5] = db;
+        }
+    }
+    __threadfence_block();
+    __syncthreads();
+}
+
+// The activation pass over one output row element (row = item, width hq * HD,
+// column h * HD + e) for the kernels that write the attention output
+// directly: a 32-wide block is one half-wave, so the calling wave's lanes
+// must hold 64 consecutive columns.
+__device__ __forceinline__ void pa_quantize_out(const VkQOut& qo, int item, int col, float val) {
+    const float amax = vk_group_max<32>(fmaxf(0.0f, fabsf(val)));
+    float sc = 0.0f;
+    int qv = 0;
+    if (amax != 0.0f) {
+        sc = vk_act_scale(amax, qo.pow2);
+        qv = vk_act_q(val, sc);
+    }
+    const int gs = vk_group_sum_i<32>(qv);
+    const int kb = col >> 5;
+    reinterpret_cast<uint16_t*>(qo.afrag)[vk_afrag_u16((size_t)item, kb, qo.k >> 5, col & 31)] =
+        (uint16_t)vk_act_bits(qv, sc, qo.pow2);
+    if ((col & 31) == 0) {
+        qo.ascale[(size_t)kb * qo.m_pad + item] = sc;
+        qo.asum[(size_t)kb * qo.m_pad + item] = qo.pow2 ? (float)gs * sc : (float)gs;
+    }
+}
+
 template <int HD, int G>
 __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const int* __restrict__ streams,
                                                      const int* __restrict__ lens, const float* __restrict__ q,
@@ -462,32 +515,7 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
     if (split >= nsp) return;  // uniform per workgroup, before any barrier
     const int k0 = split * kps, k1 = min(len, k0 + kps);
 
-    // Fused append (ak != null): the workgroup whose key range holds the
-    // item's new time step packs that step's K and V head slices into the
-    // cache first, exactly as vk_kv_write would, then reads them back with
-    // the other keys. The page comes from an earlier allocation launch.
-    if (ak) {
-        const int t = at[item];
-        if (t >= k0 && t < k1) {  // uniform per workgroup
-            const int pid = c.table[layer * c.ppl + t / c.bs];
-            if (pid >= 0 && wave < 2) {
-                const size_t hr = kv_hrow(c, pid, t, s, hk);
-                const float* src = (wave == 0 ? ak : av) + (size_t)item * c.width + (size_t)hk * HD;
-                int8_t* dq = (wave == 0 ? c.kq : c.vq) + hr * HD;
-                uint16_t* dd = (wave == 0 ? c.kd : c.vd) + hr * NB;
-#pragma unroll
-                for (int e = lane; e < HD; e += 64) {
-                    int8_t qb;
-                    uint16_t db = 0;
-                    q8_0_pack_lane(src[e], e & 31, &qb, &db);
-                    dq[e] = qb;
-                    if ((e & 31) == 0) dd[e >> 5] = db;
-                }
-            }
-            __threadfence_block();
-            __syncthreads();
-        }
-    }
+    if (ak) pa_append_slice<HD>(c, layer, s, hk, item, k0, k1, ak, av, at, wave, lane);
     for (int x = tid; x < G * HD; x += 256) {
         const int g = x / HD, e = x % HD;
         lq[g][e] = q[((size_t)item * hq + hk * G + g) * HD + e] * scale;
@@ -664,25 +692,7 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
             const float inv = lml[g][1] > 0.0f ? 1.0f / lml[g][1] : 0.0f;
             const float val = a * inv;
             out[((size_t)item * hq + h) * HD + e] = val;
-            if (qo.afrag) {
-                // the activation pass over this row (row = item, width hq * HD);
-                // a 32-wide block is one half-wave (NO is a multiple of 64)
-                const float amax = vk_group_max<32>(fmaxf(0.0f, fabsf(val)));
-                float sc = 0.0f;
-                int qv = 0;
-                if (amax != 0.0f) {
-                    sc = vk_act_scale(amax, qo.pow2);
-                    qv = vk_act_q(val, sc);
-                }
-                const int gs = vk_group_sum_i<32>(qv);
-                const int col = h * HD + e, kb = col >> 5;
-                reinterpret_cast<uint16_t*>(qo.afrag)[vk_afrag_u16((size_t)item, kb, qo.k >> 5, col & 31)] =
-                    (uint16_t)vk_act_bits(qv, sc, qo.pow2);
-                if ((col & 31) == 0) {
-                    qo.ascale[(size_t)kb * qo.m_pad + item] = sc;
-                    qo.asum[(size_t)kb * qo.m_pad + item] = qo.pow2 ? (float)gs * sc : (float)gs;
-                }
-            }
+            if (qo.afrag) pa_quantize_out(qo, item, h * HD + e, val);  // NO is a multiple of 64
         } else {
             const size_t pi = ((size_t)item * hq + h) * n_split + split;
             part_o[pi * HD + e] = a;
@@ -690,6 +700,268 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
                 part_ml[2 * pi] = lml[g][0];
                 part_ml[2 * pi + 1] = lml[g][1];
             }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention with one query head per kv head and head_dim 64 (Whisper's
+// self-attention). Same grid, key splits, outputs, partials and fused passes
+// as vk_paged_attn<64, 1>, but the keys of a split are shared among the four
+// waves rather than the threads of the workgroup: wave w takes the 64-key
+// tiles w, w + 4, ... and keeps its own online softmax, so no barrier runs in
+// the key loop; the four (m, l, O) states merge in wave order at the end.
+// Per tile, in four passes of 16 keys:
+//   scores, a quad of lanes per key (lane 4 k + u holds dims 16 u .. 16 u + 15
+//     of key k of the pass): s = scale * sum_u d_{b(u)} * (sum_{e in quarter
+//     u} q_e k_e), each quarter's dot taken exactly in integers (q as 22-bit
+//     integers in three int8 digits against the int8 quants, v_dot4) and
+//     scaled back in f32, each block's f16 scale applied to its quarter sums
+//     (f32-level numerics, as the matrix-core kernel's); the quad adds its
+//     four terms in a fixed butterfly, so its lanes agree bit for bit;
+//   O += P . V, lane = (dims 4 dq .. 4 dq + 3, keys kg, kg + 4, ..): the V
+//     quants pass through the wave's own LDS copy of the tile, [key][64 B]
+//     (a pass writes 1 KB of consecutive 16-byte chunks, and the 64 lanes of
+//     one read cover four consecutive rows: no bank conflicts), with p * d_v
+//     per key and block beside it.
+namespace pw {
+constexpr int HD = 64, NB = HD / 32, KT = 64, WAVES = 4, DQ = HD / 4, KG = 64 / DQ, KPL = KT / KG;
+constexpr int PASS = 4, KPP = KT / PASS;  // passes per tile, keys per pass (a quad of lanes each)
+}
+// Sum over the 16 quads of a wave whose four lanes hold equal values (xor
+// steps 4 .. 32 only; the mirrors of vk_bfly_partner are exact on such input).
+__device__ __forceinline__ float pw_quad_group_sumf(float v) {
+    v += __int_as_float(vk_bfly_partner<4>(__float_as_int(v)));
+    v += __int_as_float(vk_bfly_partner<8>(__float_as_int(v)));
+    v += __int_as_float(vk_bfly_partner<16>(__float_as_int(v)));
+    v += __int_as_float(vk_bfly_partner<32>(__float_as_int(v)));
+    return v;
+}
+__global__ __launch_bounds__(256, 5) void vk_paged_attn_w64(KvDev c, int layer, const int* __restrict__ streams,
+                                                         const int* __restrict__ lens, const float* __restrict__ q,
+                                                         float scale, int hq, int n_split, float* __restrict__ out,
+                                                         float* __restrict__ part_ml, float* __restrict__ part_o,
+                                                         const VkQOut qo, const float* __restrict__ ak,
+                                                         const float* __restrict__ av, const int* __restrict__ at) {
+    using namespace pw;
+    __shared__ __align__(16) int8_t lv[WAVES][KT][HD];
+    __shared__ __align__(16) float lpd[WAVES][KT][NB];
+    __shared__ __align__(16) float lpo[WAVES][KG][HD];
+    __shared__ float lml[WAVES][2];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int split = blockIdx.x, hk = blockIdx.y, item = blockIdx.z;
+    const int s = streams[item];
+    const int len = min(lens[item], c.max_time);
+    const int kps = pa_kps(len), nsp = pa_splits(len);
+    if (split >= nsp) return;  // uniform per workgroup, before any barrier
+    const int k0 = split * kps, k1 = min(len, k0 + kps);
+    if (ak) pa_append_slice<HD>(c, layer, s, hk, item, k0, k1, ak, av, at, wave, lane);
+
+    const int ku = lane >> 2, u = lane & 3, ub = u >> 1;  // score passes: key of the pass, quarter, block
+    // head rows (kv_hrow) in 32 bits: the launcher checks that every slot
+    // index fits and that the page size is a power of two
+    const int bsh = __builtin_ctz(c.bs), bsm = c.bs - 1;
+    // (through readfirstlane, so that the compiler keeps one 24-bit multiply
+    // per key instead of refactoring it back into kv_hrow's three; the
+    // launcher checks that both factors fit 24 bits)
+    const uint32_t rows_pp = __builtin_amdgcn_readfirstlane((uint32_t)c.n_stream * c.nh * c.bs);
+    const uint32_t row0 = __builtin_amdgcn_readfirstlane(((uint32_t)s * c.nh + hk) * c.bs);
+    const int* tab = c.table + layer * c.ppl;
+    const uint32_t lv_base = vk_lds_addr(&lv[wave][0][0]);
+    const int8_t* kq_l = c.kq + 16 * u;  // the lane's 16-byte chunk of a head row
+    const int8_t* vq_l = c.vq + 16 * u;
+    const uint16_t* kd_l = c.kd + ub;    // and its block's scale
+    const uint16_t* vd_l = c.vd + ub;
+    const int nt = (k1 - k0 + KT - 1) / KT;
+
+    // A tile's loads in two steps: the page entries of its keys, then its rows.
+    int jt[PASS], pid[PASS];
+    bool has[PASS];
+    auto load_table = [&](int t) {
+        const int j0 = k0 + t * KT;
+#pragma unroll
+        for (int p = 0; p < PASS; ++p) {
+            const int j = j0 + KPP * p + ku;
+            has[p] = j < k1;
+            jt[p] = has[p] ? j : k0;
+            pid[p] = tab[jt[p] >> bsh];
+        }
+    };
+    uint4 kw[PASS];
+    uint32_t kd[PASS], vd[PASS];
+    bool hv[PASS];
+    auto load_rows = [&]() {
+#pragma unroll
+        for (int p = 0; p < PASS; ++p) {
+            hv[p] = has[p] && pid[p] >= 0;
+            const uint64_t hr = __umul24((uint32_t)max(pid[p], 0), rows_pp) + row0 + (uint32_t)(jt[p] & bsm);
+            // lane 4 k + u's 16 bytes of V land at row KPP p + k, chunk u, of the wave's copy
+            vk_dma_b128(vq_l + hr * HD, lv_base + p * KPP * HD);
+            kw[p] = *reinterpret_cast<const uint4*>(kq_l + hr * HD);
+            kd[p] = kd_l[hr * NB];
+            vd[p] = vd_l[hr * NB];
+        }
+    };
+
+    float qr[16];
+    {
+        const float4* qs = reinterpret_cast<const float4*>(q + ((size_t)item * hq + hk) * HD + 16 * u);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            const float4 v = qs[x];
+            qr[4 * x] = v.x;
+            qr[4 * x + 1] = v.y;
+            qr[4 * x + 2] = v.z;
+            qr[4 * x + 3] = v.w;
+        }
+    }
+
+    // The lane's 16 q values as integers Q = q * 2^(22 - ex) (|Q| <= 2^22, ex
+    // from the lane's largest |q|, clamped so that 2^(ex - 22) and its inverse
+    // stay normal), split into three signed bytes Q = 2^16 D2 + 2^8 D1 + D0,
+    // four elements to a dword per digit: the block dot then runs as exact
+    // integer dot4 products of the digits with the int8 key quants, and
+    // sum_e q_e k_e = 2^(ex - 22) (2^16 S2 + 2^8 S1 + S0) to f32 rounding.
+    // qbad is 0, or NaN when a q value is not finite (it then reaches the
+    // scores, as the f32 products would carry it).
+    uint32_t qd[3][4];
+    float qsc, qbad = 0.0f;
+    {
+        float m = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            m = fmaxf(m, fabsf(qr[e]));
+            qbad += 0.0f * qr[e];
+        }
+        int ex = -100;
+        if (m > 0.0f && m <= 3.40282347e38f) {
+            frexpf(m, &ex);  // m < 2^ex
+            ex = max(ex, -100);
+        }
+        const float inv = ldexpf(1.0f, 22 - ex);
+        qsc = ldexpf(1.0f, ex - 22);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            uint32_t d0 = 0, d1 = 0, d2 = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float v = qr[4 * x + i] * inv;
+                const int qi = (v == v && fabsf(v) <= 4194304.0f) ? (int)rintf(v) : 0;
+                const int b0 = (int)(int8_t)(qi & 0xff), r1 = (qi - b0) >> 8;
+                const int b1 = (int)(int8_t)(r1 & 0xff), b2 = (r1 - b1) >> 8;
+                d0 |= (uint32_t)(b0 & 0xff) << (8 * i);
+                d1 |= (uint32_t)(b1 & 0xff) << (8 * i);
+                d2 |= (uint32_t)(b2 & 0xff) << (8 * i);
+            }
+            qd[0][x] = d0;
+            qd[1][x] = d1;
+            qd[2][x] = d2;
+        }
+    }
+
+    const int dq = lane % DQ, kg = lane / DQ;
+    float m_run = -INFINITY, l_run = 0.0f;
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = wave; t < nt; t += WAVES) {
+        load_table(t);
+        load_rows();
+        // the products consume the K quants only from here, so every load of
+        // the tile is issued before the first wait
+        asm volatile("" : "+v"(kw[0].x), "+v"(kw[0].y), "+v"(kw[0].z), "+v"(kw[0].w), "+v"(kw[1].x), "+v"(kw[1].y),
+                          "+v"(kw[1].z), "+v"(kw[1].w), "+v"(kw[2].x), "+v"(kw[2].y), "+v"(kw[2].z), "+v"(kw[2].w),
+                          "+v"(kw[3].x), "+v"(kw[3].y), "+v"(kw[3].z), "+v"(kw[3].w));
+        // ---- scores of the tile's four passes
+        float sc[PASS];
+#pragma unroll
+        for (int p = 0; p < PASS; ++p) {
+            const int w[4] = {(int)kw[p].x, (int)kw[p].y, (int)kw[p].z, (int)kw[p].w};
+            int sd[3];
+#pragma unroll
+            for (int g = 0; g < 3; ++g) {
+                int acc = 0;
+#pragma unroll
+                for (int x = 0; x < 4; ++x) acc = __builtin_amdgcn_sdot4((int)qd[g][x], w[x], acc, false);
+                sd[g] = acc;
+            }
+            const float a = fmaf((float)sd[2], 65536.0f, fmaf((float)sd[1], 256.0f, (float)sd[0]));
+            float v = (vk_f16_to_f32_hw(kd[p]) * qsc) * a + qbad;
+            v += __int_as_float(vk_bfly_partner<1>(__float_as_int(v)));
+            v += __int_as_float(vk_bfly_partner<2>(__float_as_int(v)));
+            sc[p] = hv[p] ? v * scale : -INFINITY;
+        }
+        // ---- the wave's online softmax over the tile
+        float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        mx = fmaxf(mx, __int_as_float(vk_bfly_partner<4>(__float_as_int(mx))));
+        mx = fmaxf(mx, __int_as_float(vk_bfly_partner<8>(__float_as_int(mx))));
+        mx = fmaxf(mx, __int_as_float(vk_bfly_partner<16>(__float_as_int(mx))));
+        mx = fmaxf(mx, __int_as_float(vk_bfly_partner<32>(__float_as_int(mx))));
+        const float m_new = fmaxf(m_run, mx);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __expf(m_run - m_use);
+        float ps = 0.0f;
+#pragma unroll
+        for (int p = 0; p < PASS; ++p) {
+            const float e = __expf(sc[p] - m_use);
+            ps += e;
+            // the quad's lanes of one block write the same value
+            lpd[wave][KPP * p + ku][ub] = hv[p] ? e * vk_f16_to_f32_hw(vd[p]) : 0.0f;
+        }
+        l_run = l_run * alpha + pw_quad_group_sumf(ps);
+        m_run = m_new;
+        // ---- O += P . V from the wave's LDS rows: the direct loads of V have
+        // landed once no load of the tile is in flight
+        vk_wait_vm<0>();
+        uint32_t wv[KPL];
+        float pdv[KPL];
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) {  // every read in flight before the first product
+            wv[i] = *reinterpret_cast<const uint32_t*>(&lv[wave][kg + KG * i][4 * dq]);
+            pdv[i] = lpd[wave][kg + KG * i][(4 * dq) / 32];
+        }
+        float a4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < KPL; ++i)
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4)
+                a4[c4] = fmaf(pdv[i], (float)(int8_t)((wv[i] >> (8 * c4)) & 0xffu), a4[c4]);
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) o[c4] = fmaf(o[c4], alpha, a4[c4]);
+        // the rows' reads are done before the next tile's loads overwrite them
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    // ---- merge: key groups, then waves, in order
+    *reinterpret_cast<float4*>(&lpo[wave][kg][4 * dq]) = make_float4(o[0], o[1], o[2], o[3]);
+    if (lane == 0) {
+        lml[wave][0] = m_run;
+        lml[wave][1] = l_run;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    const int e = lane;
+    float m = lml[0][0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) m = fmaxf(m, lml[w][0]);
+    float l = 0.0f, a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+        const float f = lml[w][0] == -INFINITY ? 0.0f : __expf(lml[w][0] - m);
+        float ow = lpo[w][0][e];
+#pragma unroll
+        for (int g = 1; g < KG; ++g) ow += lpo[w][g][e];
+        l = fmaf(f, lml[w][1], l);
+        a = fmaf(f, ow, a);
+    }
+    if (nsp == 1) {
+        const float val = a * (l > 0.0f ? 1.0f / l : 0.0f);
+        out[((size_t)item * hq + hk) * HD + e] = val;
+        if (qo.afrag) pa_quantize_out(qo, item, hk * HD + e, val);
+    } else {
+        const size_t pi = ((size_t)item * hq + hk) * n_split + split;
+        part_o[pi * HD + e] = a;
+        if (e == 0) {
+            part_ml[2 * pi] = m;
+            part_ml[2 * pi + 1] = l;
         }
     }
 }
@@ -1280,6 +1552,17 @@ static bool go_pa(hipStream_t s, const KvDev& c, int layer, int n, const int* st
             hipLaunchKernelGGL((vk_paged_attn_gqa<G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams,
                                lens, q, scale, hq, n_split, out, pml, po, rope_cs, ak, av, at);
             return false;
+        }
+    }
+    // head_dim 64, one query head per kv head: the wave-split kernel (32-bit
+    // head rows from a 24-bit page multiply, page size a power of two, q rows
+    // 16-byte aligned)
+    if constexpr (HD == pw::HD && G == 1) {
+        if (small_slots && (c.bs & (c.bs - 1)) == 0 && (reinterpret_cast<uintptr_t>(q) & 15) == 0 &&
+            c.cap < (1 << 24) && (size_t)c.n_stream * c.nh * c.bs < (1u << 24)) {
+            hipLaunchKernelGGL(vk_paged_attn_w64, dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams, lens,
+                               q, scale, hq, n_split, out, pml, po, n_split == 1 ? qo : VkQOut{}, ak, av, at);
+            return n_split == 1 && qo.afrag;
         }
     }
     hipLaunchKernelGGL((vk_paged_attn<HD, G>), dim3(n_split, hkv, n), dim3(256), 0, s, c, layer, streams, lens, q,
