@@ -748,6 +748,8 @@ __global__ __launch_bounds__(256, 5) void vk_paged_attn_w64(KvDev c, int layer, 
     __shared__ __align__(16) float lpd[WAVES][KT][NB];
     __shared__ __align__(16) float lpo[WAVES][KG][HD];
     __shared__ float lml[WAVES][2];
+    __shared__ __align__(16) int8_t lqd[WAVES][3][HD];  // q's integer digits
+    __shared__ float2 lqs[WAVES][HD / 16];              // per quarter: 2^(ex - 22), qbad
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int split = blockIdx.x, hk = blockIdx.y, item = blockIdx.z;
@@ -804,60 +806,44 @@ __global__ __launch_bounds__(256, 5) void vk_paged_attn_w64(KvDev c, int layer, 
         }
     };
 
-    float qr[16];
-    {
-        const float4* qs = reinterpret_cast<const float4*>(q + ((size_t)item * hq + hk) * HD + 16 * u);
-#pragma unroll
-        for (int x = 0; x < 4; ++x) {
-            const float4 v = qs[x];
-            qr[4 * x] = v.x;
-            qr[4 * x + 1] = v.y;
-            qr[4 * x + 2] = v.z;
-            qr[4 * x + 3] = v.w;
-        }
-    }
-
-    // The lane's 16 q values as integers Q = q * 2^(22 - ex) (|Q| <= 2^22, ex
-    // from the lane's largest |q|, clamped so that 2^(ex - 22) and its inverse
-    // stay normal), split into three signed bytes Q = 2^16 D2 + 2^8 D1 + D0,
-    // four elements to a dword per digit: the block dot then runs as exact
-    // integer dot4 products of the digits with the int8 key quants, and
-    // sum_e q_e k_e = 2^(ex - 22) (2^16 S2 + 2^8 S1 + S0) to f32 rounding.
-    // qbad is 0, or NaN when a q value is not finite (it then reaches the
-    // scores, as the f32 products would carry it).
+    // q as integers Q = q * 2^(22 - ex) per quarter u (|Q| <= 2^22, ex from
+    // the quarter's largest |q|, clamped so that 2^(ex - 22) and its inverse
+    // stay normal), split into three signed bytes Q = 2^16 D2 + 2^8 D1 + D0:
+    // each quarter's block dot then runs as exact integer dot4 products of
+    // the digits with the int8 key quants, and sum_e q_e k_e =
+    // 2^(ex - 22) (2^16 S2 + 2^8 S1 + S0) to f32 rounding. qbad is 0, or NaN
+    // when a q value of the quarter is not finite (it then reaches the
+    // scores, as the f32 products would carry it). Each wave converts one
+    // value per lane and regroups the digits through its own LDS rows.
     uint32_t qd[3][4];
-    float qsc, qbad = 0.0f;
+    float qsc, qbad;
     {
-        float m = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            m = fmaxf(m, fabsf(qr[e]));
-            qbad += 0.0f * qr[e];
-        }
+        const float v = q[((size_t)item * hq + hk) * HD + lane];
+        const float m = vk_group_max<16>(fmaxf(0.0f, fabsf(v)));  // a quarter is 16 lanes
+        const float bad = vk_group_sumf<16>(0.0f * v);
         int ex = -100;
         if (m > 0.0f && m <= 3.40282347e38f) {
             frexpf(m, &ex);  // m < 2^ex
             ex = max(ex, -100);
         }
-        const float inv = ldexpf(1.0f, 22 - ex);
-        qsc = ldexpf(1.0f, ex - 22);
+        const float x = v * ldexpf(1.0f, 22 - ex);
+        const int qi = (x == x && fabsf(x) <= 4194304.0f) ? (int)rintf(x) : 0;
+        const int b0 = (int)(int8_t)(qi & 0xff), r1 = (qi - b0) >> 8;
+        const int b1 = (int)(int8_t)(r1 & 0xff), b2 = (r1 - b1) >> 8;
+        lqd[wave][0][lane] = (int8_t)b0;
+        lqd[wave][1][lane] = (int8_t)b1;
+        lqd[wave][2][lane] = (int8_t)b2;
+        if ((lane & 15) == 0) lqs[wave][lane >> 4] = make_float2(ldexpf(1.0f, ex - 22), bad);
 #pragma unroll
-        for (int x = 0; x < 4; ++x) {
-            uint32_t d0 = 0, d1 = 0, d2 = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float v = qr[4 * x + i] * inv;
-                const int qi = (v == v && fabsf(v) <= 4194304.0f) ? (int)rintf(v) : 0;
-                const int b0 = (int)(int8_t)(qi & 0xff), r1 = (qi - b0) >> 8;
-                const int b1 = (int)(int8_t)(r1 & 0xff), b2 = (r1 - b1) >> 8;
-                d0 |= (uint32_t)(b0 & 0xff) << (8 * i);
-                d1 |= (uint32_t)(b1 & 0xff) << (8 * i);
-                d2 |= (uint32_t)(b2 & 0xff) << (8 * i);
-            }
-            qd[0][x] = d0;
-            qd[1][x] = d1;
-            qd[2][x] = d2;
+        for (int g = 0; g < 3; ++g) {  // the wave's own writes: in order
+            const uint4 w = *reinterpret_cast<const uint4*>(&lqd[wave][g][16 * u]);
+            qd[g][0] = w.x;
+            qd[g][1] = w.y;
+            qd[g][2] = w.z;
+            qd[g][3] = w.w;
         }
+        qsc = lqs[wave][u].x;
+        qbad = lqs[wave][u].y;
     }
 
     const int dq = lane % DQ, kg = lane / DQ;
