@@ -205,6 +205,67 @@ def test_paged_attention_vs_oracle(ctx, oracle, H, hd, hq):
         assert ok, (s, err)
 
 
+@pytest.mark.parametrize("bs", [4, 12, 32])
+def test_paged_attention_page_sizes(ctx, oracle, bs):
+    """Page sizes other than 16 with one q head per kv head at head_dim 64:
+    4 and 32 (powers of two: the wave-split kernel, whose 16-key passes then
+    span four pages or half of one) and 12 (the thread-per-key kernel)."""
+    print(f"[case] paged attn bs={bs}", flush=True)
+    H, hd, n_stream, max_time = 3, 64, 4, 260
+    kv = ctx.kv_cache(1, H, hd, n_stream, max_time, bs)
+    ref = oracle.PagedCache(1, H, hd, n_stream, max_time, bs, Q8_0)
+    rng = np.random.default_rng(bs)
+    lens = [260, 77, 1, 190]
+    fill_cache(kv, ref, 0, lens, H * hd, rng, n_stream)
+    q = rng.standard_normal((n_stream, H * hd)).astype(np.float32)
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    order = [2, 0, 3, 1]
+    got = kv.attn(0, order, [lens[s] for s in order], q, H, scale)
+    for i, s in enumerate(order):
+        K, V = cached_kv(ref, 0, s, lens[s])
+        want = oracle.sdpa_whisper(1, lens[s], H, hd, q[i:i + 1], K, V, causal=True, q_pos_offset=lens[s] - 1)[0]
+        ok, err = close(got[i], want.astype(np.float64))
+        assert ok, (s, err)
+
+
+def test_paged_attention_q_magnitudes_and_non_finite(ctx, oracle):
+    """One q head per kv head at head_dim 64 takes q as 22-bit integers per
+    16-dim quarter, scaled by a power of two from the quarter's largest |q|
+    (clamped for tiny magnitudes): rows of q from 1e-40 (subnormal) to 1e20
+    stay within the f32 tolerance of the oracle, and a NaN or inf q value makes
+    exactly its head's output NaN, as the f32 products do."""
+    print("[case] paged attn q magnitudes", flush=True)
+    H, hd, n_stream, max_time, bs = 4, 64, 6, 200, 16
+    kv = ctx.kv_cache(1, H, hd, n_stream, max_time, bs)
+    ref = oracle.PagedCache(1, H, hd, n_stream, max_time, bs, Q8_0)
+    rng = np.random.default_rng(2024)
+    lens = [200, 131, 64, 97, 1, 150]
+    fill_cache(kv, ref, 0, lens, H * hd, rng, n_stream)
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    q = rng.standard_normal((n_stream, H * hd)).astype(np.float32)
+    mags = [1e-40, 1e-30, 1e-3, 1.0, 1e3, 1e20]
+    q = (q * np.array(mags, np.float32)[:, None]).astype(np.float32)
+    q[2, 16:32] *= np.float32(1e-6)  # quarters of one head with very different ranges
+    got = kv.attn(0, list(range(n_stream)), lens, q, H, scale)
+    for s in range(n_stream):
+        K, V = cached_kv(ref, 0, s, lens[s])
+        want = oracle.sdpa_whisper(1, lens[s], H, hd, q[s:s + 1], K, V, causal=True, q_pos_offset=lens[s] - 1)[0]
+        ok, err = close(got[s], want.astype(np.float64))
+        assert ok, (s, mags[s], err)
+    bad = q.copy()
+    bad[0, 5] = np.nan           # head 0 of stream 0
+    bad[3, hd + 3] = np.inf      # head 1 of stream 3
+    bad[5, 3 * hd + 60] = -np.inf  # head 3 of stream 5
+    got = kv.attn(0, list(range(n_stream)), lens, bad, H, scale).reshape(n_stream, H, hd)
+    nan_heads = {(0, 0), (3, 1), (5, 3)}
+    for s in range(n_stream):
+        for h in range(H):
+            if (s, h) in nan_heads:
+                assert np.isnan(got[s, h]).all(), (s, h)
+            else:
+                assert np.isfinite(got[s, h]).all(), (s, h)
+
+
 def test_paged_attention_split_path(ctx, oracle):
     """Long contexts with few workgroups use the key split + combine kernel."""
     print("[case] paged attn split", flush=True)
