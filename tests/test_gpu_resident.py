@@ -109,3 +109,25 @@ def test_kv_append_dev_equals_copy_mode(ctx):
         for s, t in zip(streams, times):
             ra, rb = a.read(layer, t, s), b.read(layer, t, s)
             assert np.array_equal(bits(ra[0]), bits(rb[0])) and np.array_equal(bits(ra[1]), bits(rb[1]))
+
+
+@pytest.mark.parametrize("H,hd,hq,lens", [(4, 64, 4, [200, 1, 77, 131]),          # one q head per kv head
+                                          (2, 128, 16, [1500, 4097, 33, 600])])  # GQA, key splits + combine
+def test_paged_attn_dev_equals_copy_mode(ctx, H, hd, hq, lens):
+    print(f"[case] resident paged attn H={H} hd={hd} hq={hq}", flush=True)
+    n_stream, max_time, bs = len(lens), max(lens), 16
+    kv = ctx.kv_cache(1, H, hd, n_stream, max_time, bs)
+    g = np.random.default_rng(hd + hq)
+    for t in range(max(lens)):
+        live = [s for s in range(n_stream) if lens[s] > t]
+        rows = g.standard_normal((2, len(live), H * hd)).astype(np.float32)
+        kv.append(0, live, [t] * len(live), rows[0], rows[1])
+    order = [3, 1, 0, 2]
+    ln = [lens[s] for s in order]
+    q = g.standard_normal((n_stream, hq * hd)).astype(np.float32)
+    scale = float(np.float32(hd) ** np.float32(-0.5))
+    want = kv.attn(0, order, ln, q, hq, scale)
+    out = hip.DeviceBuffer(ctx, q.nbytes)
+    kv.attn_dev(0, n_stream, dev(ctx, np.array(order, np.int32)), dev(ctx, np.array(ln, np.int32)), max(ln), hq,
+                dev(ctx, q), scale, out)
+    assert np.array_equal(bits(down(ctx, out, np.float32, q.size)), bits(want))
