@@ -131,3 +131,74 @@ def test_paged_attn_dev_equals_copy_mode(ctx, H, hd, hq, lens):
     kv.attn_dev(0, n_stream, dev(ctx, np.array(order, np.int32)), dev(ctx, np.array(ln, np.int32)), max(ln), hq,
                 dev(ctx, q), scale, out)
     assert np.array_equal(bits(down(ctx, out, np.float32, q.size)), bits(want))
+
+
+def test_decoder_step_dev_equals_step(ctx, oracle):
+    """Two sessions from the same weights, one stepped through host arrays and
+    one through device arrays (the form the bench times and a graph captures):
+    the same next tokens and logits, bit for bit, step after step."""
+    print("[case] resident decoder step", flush=True)
+    from tests.test_gpu_sessions import make_decoder
+    a, _ = make_decoder(ctx, oracle, np.random.default_rng(5))
+    b, _ = make_decoder(ctx, oracle, np.random.default_rng(5))
+    g = np.random.default_rng(6)
+    V = a.parts["V"]
+    streams = np.array([2, 0, 3], np.int32)
+    d_streams = dev(ctx, streams)
+    d_next = hip.DeviceBuffer(ctx, 4 * streams.size)
+    d_logits = hip.DeviceBuffer(ctx, 4 * streams.size * V)
+    for p in range(6):
+        tokens = g.integers(0, V, streams.size).astype(np.int32)
+        pos = np.full(streams.size, p, np.int32)
+        want, lg = a.step(streams, tokens, pos, want_logits=True)
+        b.step_dev(streams.size, d_streams, dev(ctx, tokens), dev(ctx, pos), d_next, d_logits)
+        assert b.status() == len(a.parts["layers"]) * streams.size
+        assert np.array_equal(down(ctx, d_next, np.int32, streams.size), want), p
+        assert np.array_equal(bits(down(ctx, d_logits, np.float32, lg.size)), bits(lg)), p
+
+
+def test_text_decoder_step_dev_equals_step(ctx, oracle):
+    print("[case] resident text decoder step", flush=True)
+    from tests.test_gpu_textdec import build
+    kw = dict(n_layer=2, d=256, hq=4, hkv=2, hd=64, ff=512, V=320, n_ctx=40, n_stream=3)
+    a, P = build(ctx, oracle, 9, **kw)
+    b, _ = build(ctx, oracle, 9, **kw)
+    g = np.random.default_rng(10)
+    streams = np.array([1, 2, 0], np.int32)
+    d_streams = dev(ctx, streams)
+    d_next = hip.DeviceBuffer(ctx, 4 * streams.size)
+    d_logits = hip.DeviceBuffer(ctx, 4 * streams.size * P["V"])
+    for p in range(6):
+        tokens = g.integers(0, P["V"], streams.size).astype(np.int32)
+        want, lg = a.step(streams, tokens, want_logits=True)
+        b.step_dev(streams.size, d_streams, dev(ctx, tokens), dev(ctx, np.full(streams.size, p, np.int32)), d_next,
+                   d_logits)
+        b.status()
+        assert np.array_equal(down(ctx, d_next, np.int32, streams.size), want), p
+        assert np.array_equal(bits(down(ctx, d_logits, np.float32, lg.size)), bits(lg)), p
+
+
+def test_log_mel_dev_equals_copy_mode(ctx):
+    print("[case] resident log-mel", flush=True)
+    g = np.random.default_rng(11)
+    batch, n, n_mels = 2, 40000, 80
+    pcm = (g.standard_normal((batch, n)) * 0.1).astype(np.float32)
+    want = ctx.log_mel(pcm, n_mels)
+    out = hip.DeviceBuffer(ctx, want.nbytes)
+    ctx.log_mel_dev(dev(ctx, pcm), batch, n, n_mels, out)
+    assert np.array_equal(bits(down(ctx, out, np.float32, want.size)), bits(want))
+
+
+def test_events_time_the_library_stream(ctx):
+    """vokra_hip_event_record / _elapsed_ms around work on the library stream."""
+    print("[case] events", flush=True)
+    start, stop = hip.Event(ctx), hip.Event(ctx)
+    x = dev(ctx, np.ones(1 << 20, np.float32))
+    y = hip.DeviceBuffer(ctx, 4 << 20)
+    start.record()
+    for _ in range(4):
+        ctx.gelu_f32_dev(x, y, 1 << 20)
+    stop.record()
+    ctx.synchronize()
+    ms = start.elapsed_ms(stop)
+    assert np.isfinite(ms) and 0.0 <= ms < 1000.0
