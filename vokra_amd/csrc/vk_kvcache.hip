@@ -720,10 +720,10 @@ __global__ __launch_bounds__(256) void vk_paged_attn(KvDev c, int layer, const i
 //     (f32-level numerics, as the matrix-core kernel's); the quad adds its
 //     four terms in a fixed butterfly, so its lanes agree bit for bit;
 //   O += P . V, lane = (dims 4 dq .. 4 dq + 3, keys kg, kg + 4, ..): the V
-//     quants pass through the wave's own LDS copy of the tile, [key][64 B]
-//     (a pass writes 1 KB of consecutive 16-byte chunks, and the 64 lanes of
-//     one read cover four consecutive rows: no bank conflicts), with p * d_v
-//     per key and block beside it.
+//     quants reach the wave's own LDS copy of the tile, [key][64 B], by direct
+//     global-to-LDS loads (one per pass, 1 KB of consecutive 16-byte chunks),
+//     and the 64 lanes of one read cover four consecutive rows (no bank
+//     conflicts), with p * d_v per key and block beside it.
 namespace pw {
 constexpr int HD = 64, NB = HD / 32, KT = 64, WAVES = 4, DQ = HD / 4, KG = 64 / DQ, KPL = KT / KG;
 constexpr int PASS = 4, KPP = KT / PASS;  // passes per tile, keys per pass (a quad of lanes each)
